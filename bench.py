@@ -1,0 +1,327 @@
+"""Benchmark of the MI355X paged-KV data plane (one GPU).
+
+Headline: paged decode attention over 28 layers at batch 256, lognormal contexts (median
+2048, sigma 1.3, clipped to [256, 8192], about 90 GB of K/V resident in HBM).  One step =
+for each of the 28 layers: append the new token's K/V into its slot (kernel 1, decode form)
+and run paged GQA decode attention over the whole context (kernel 3).  ``value`` is the
+algorithmic HBM bandwidth of the whole step: per layer sum(context) x 4096 B of K/V read,
+plus Q read, O written and the appended K/V rows, divided by the timed step time.
+
+Also measured in the same run (reported under ``kernels``): the 28-layer prefill scatter of
+32 prompts U[128, 2048] with churned block tables, and the block-table history gather of
+4 x 16384-token prompts in 2048-token chunks.  The CPU baseline times the reference's torch
+decode chain (the oracle) on the host cores on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only decode]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor datasheet
+METRIC = "paged decode-attn HBM GB/s (% peak) at B=256; e2e output tok/s Qwen3-0.6B"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+class EventTimer:
+    """HIP events on the current stream (the one every data-plane kernel is launched on)."""
+
+    def __init__(self):
+        self.pairs: list[tuple[torch.cuda.Event, torch.cuda.Event]] = []
+
+    def start(self):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append((e, None))
+
+    def stop(self):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs[-1] = (self.pairs[-1][0], e)
+
+    def mean_ms(self) -> float:
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in self.pairs) / max(len(self.pairs), 1)
+
+
+# --------------------------------------------------------------------------- decode (headline)
+def bench_decode(steps: int, warmup: int, device: torch.device):
+    from mini_infra_qwen3_amd import data_plane, workloads as wl
+
+    t0 = time.perf_counter()
+    w = wl.decode_at_scale(seed=0, device=device)
+    torch.cuda.synchronize()
+    log(f"decode workload ready in {time.perf_counter() - t0:.1f}s: batch {len(w.context_lens)}, "
+        f"sum(ctx)={sum(w.context_lens)}, pool {w.num_blocks} blocks x 28 layers "
+        f"({w.pools.numel() * 2 / 1e9:.1f} GB)")
+    batch = len(w.context_lens)
+    block_tables = w.block_tables.to(device)
+    context_lens = torch.tensor(w.context_lens, dtype=torch.long, device=device)
+    slots = w.slot_mapping.to(device)
+    out = torch.empty((batch, wl.NUM_HEADS * wl.HEAD_DIM), dtype=torch.bfloat16, device=device)
+    ws_bytes = data_plane.paged_decode_workspace_bytes(batch, block_tables.shape[1], wl.NUM_HEADS,
+                                                       wl.HEAD_DIM, wl.BLOCK_SIZE)
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    keys = [w.pools[l, 0] for l in range(w.num_layers)]
+    values = [w.pools[l, 1] for l in range(w.num_layers)]
+    new_k = [w.new_key[l].unsqueeze(2) for l in range(w.num_layers)]
+    new_v = [w.new_value[l].unsqueeze(2) for l in range(w.num_layers)]
+    attn_timer = EventTimer()
+
+    def step(timed: bool):
+        for layer in range(w.num_layers):
+            data_plane.reshape_and_cache([new_k[layer]], [new_v[layer]], slots, [keys[layer]], [values[layer]])
+            if timed:
+                attn_timer.start()
+            data_plane.paged_decode_attention(w.query[layer], keys[layer], values[layer], block_tables,
+                                              context_lens, wl.SCALE, out=out, workspace=workspace)
+            if timed:
+                attn_timer.stop()
+
+    for _ in range(warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(steps):
+        step(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ms_per_step = elapsed * 1000.0 / steps
+
+    q_o_bytes = 2 * batch * wl.NUM_HEADS * wl.HEAD_DIM * 2
+    append_bytes = 2 * batch * wl.KV_BYTES_PER_TOKEN_LAYER  # read + write of the new K/V rows
+    attn_bytes_per_launch = w.kv_bytes_per_layer + q_o_bytes
+    step_bytes = w.num_layers * (attn_bytes_per_launch + append_bytes)
+    attn_ms = attn_timer.mean_ms()
+    achieved = attn_bytes_per_launch / (attn_ms * 1e-3) / 1e9
+    result = {
+        "ms_per_step": ms_per_step,
+        "value": step_bytes / (ms_per_step * 1e-3) / 1e9,
+        "attn_launch_ms": attn_ms,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+        },
+        "workload": w,
+    }
+    # Spot-check the timed output of the last layer against its own inputs: finite values.
+    if not torch.isfinite(out.float()).all():
+        raise RuntimeError("decode attention produced non-finite values")
+    return result
+
+
+def cpu_baseline_decode(w, device: torch.device, budget_s: float = 20.0) -> dict:
+    """The reference's torch decode chain (oracle) on the host cores, one layer, bounded sample.
+
+    Sample: the first sequences of the batch (in order) whose contexts sum to about 1/8 of the
+    layer, gathered into a compact CPU pool; timed as gather + bias + repeat_interleave + bf16
+    matmul + fp32 softmax, 1 warmup + repeats (median) within the time budget.
+    """
+    from mini_infra_qwen3_amd import workloads as wl
+    from oracle import torch_ref
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    total = sum(w.context_lens)
+    picked, acc = [], 0
+    for b, n in enumerate(w.context_lens):
+        picked.append(b)
+        acc += n
+        if acc >= total / 8:
+            break
+    blocks = [blk for b in picked for blk in w.tables[b]]
+    index = torch.tensor(blocks, device=device)
+    key_pool = torch.cat([torch.zeros(1, 16, 8, 128, dtype=torch.bfloat16), w.pools[0, 0][index].cpu()])
+    value_pool = torch.cat([torch.zeros(1, 16, 8, 128, dtype=torch.bfloat16), w.pools[0, 1][index].cpu()])
+    tables, k = [], 1
+    for b in picked:
+        tables.append(list(range(k, k + len(w.tables[b]))))
+        k += len(w.tables[b])
+    bt = wl.padded(tables)
+    ctx = torch.tensor([w.context_lens[b] for b in picked])
+    q = w.query[0][picked].cpu()
+    sample_bytes = int(ctx.sum()) * wl.KV_BYTES_PER_TOKEN_LAYER
+    times = []
+    t_budget = time.perf_counter() + budget_s
+    for i in range(6):
+        t0 = time.perf_counter()
+        torch_ref.paged_decode_attention(q, key_pool, value_pool, bt, ctx, wl.SCALE)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_budget and i >= 1:
+            break
+    timed = sorted(times[1:]) if len(times) > 1 else times
+    median = timed[len(timed) // 2]
+    return {
+        "value": sample_bytes / median / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"one layer, {len(picked)} of {len(w.context_lens)} sequences (sum ctx {int(ctx.sum())}), "
+                   f"reference torch chain (gather+bias+repeat_interleave+bf16 matmul+fp32 softmax) on CPU, "
+                   f"median of {len(timed)} after 1 warmup; {cpu_model()}"),
+        "ms_per_layer_sample": median * 1000.0,
+    }
+
+
+# ------------------------------------------------------------------------------- scatter
+def bench_scatter(steps: int, warmup: int, device: torch.device) -> dict:
+    from mini_infra_qwen3_amd import workloads as wl
+    from mini_infra_qwen3_amd.worker import KVCache, PagedKVCachePool
+
+    w = wl.prefill_scatter(seed=0, device=device)
+    pool = PagedKVCachePool(wl.NUM_LAYERS, w.num_blocks, wl.BLOCK_SIZE, wl.NUM_KV_HEADS, wl.HEAD_DIM,
+                            torch.bfloat16, device)
+    cache = KVCache([(w.sources[l, 0], w.sources[l, 1]) for l in range(wl.NUM_LAYERS)])
+    index = torch.from_numpy(w.index).to(device)
+    timer = EventTimer()
+    for _ in range(warmup):
+        pool.write_prefill(cache, index[0], index[1], index[2])
+    for _ in range(steps):
+        timer.start()
+        pool.write_prefill(cache, index[0], index[1], index[2])
+        timer.stop()
+    ms = timer.mean_ms()
+    moved = 2 * w.num_tokens * wl.NUM_LAYERS * wl.KV_BYTES_PER_TOKEN_LAYER  # read + write
+    gbs = moved / (ms * 1e-3) / 1e9
+    del pool, cache
+    return {"workload": f"prefill scatter, 28 layers, 32 prompts U[128,2048] ({w.num_tokens} tokens), churned tables",
+            "ms_per_launch": ms, "bytes_per_launch": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS}
+
+
+# -------------------------------------------------------------------------------- gather
+def bench_gather(steps: int, warmup: int, device: torch.device) -> dict:
+    from mini_infra_qwen3_amd import workloads as wl
+    from mini_infra_qwen3_amd.worker import PagedKVCachePool
+
+    w = wl.chunked_prefill(seed=0)
+    pool = PagedKVCachePool(wl.NUM_LAYERS, w.num_blocks, wl.BLOCK_SIZE, wl.NUM_KV_HEADS, wl.HEAD_DIM,
+                            torch.bfloat16, device)
+    pool.storage.view(torch.int16).random_(generator=torch.Generator(device=device).manual_seed(0))
+    # each chunk c of each prompt gathers its 128 c history blocks, all layers in one launch
+    chunk_tables = []
+    for c in range(1, w.num_chunks):
+        nb = c * w.chunk_len // wl.BLOCK_SIZE
+        chunk_tables.append(torch.tensor([t[:nb] for t in w.tables], dtype=torch.long, device=device))
+    timer = EventTimer()
+
+    def run():
+        for ids in chunk_tables:
+            pool.gather_blocks(ids)
+
+    for _ in range(warmup):
+        run()
+    for _ in range(steps):
+        timer.start()
+        run()
+        timer.stop()
+    ms = timer.mean_ms()
+    moved = 2 * w.history_bytes_per_layer() * wl.NUM_LAYERS  # read history + write the gathered copy
+    gbs = moved / (ms * 1e-3) / 1e9
+    del pool
+    return {"workload": "history gather, 28 layers, 4 prompts x 16384 tokens in 2048-token chunks (7 launches)",
+            "ms_per_prompt_set": ms, "bytes": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--only", choices=["decode", "all"], default="all")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of this path "
+              "is a design note, not a measured configuration.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    device = torch.device("cuda:0")
+    from mini_infra_qwen3_amd import _native
+
+    _native.load()
+    log(f"device {torch.cuda.get_device_name(device)}; library {_native.LIBRARY_PATH}")
+
+    dec = bench_decode(args.steps, args.warmup, device)
+    log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value']:.1f} GB/s; attention launch "
+        f"{dec['attn_launch_ms']:.3f} ms = {dec['roofline']['achieved']:.1f} GB/s "
+        f"({100 * dec['roofline']['frac']:.1f}% of peak)")
+    w = dec.pop("workload")
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_decode(w, device)
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+    ctx_sum = sum(w.context_lens)
+    num_blocks = w.num_blocks
+    del w
+    torch.cuda.empty_cache()
+
+    kernels = {}
+    if args.only == "all":
+        kernels["scatter"] = bench_scatter(max(args.steps // 2, 3), 2, device)
+        log(f"scatter: {kernels['scatter']['achieved_GBps']:.1f} GB/s")
+        torch.cuda.empty_cache()
+        kernels["gather"] = bench_gather(max(args.steps // 4, 3), 1, device)
+        log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s")
+        torch.cuda.empty_cache()
+
+    line = {
+        "metric": METRIC,
+        "value": round(dec["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "paged decode attention step over 28 layers (append + attention per layer), batch 256, "
+                        "contexts lognormal median 2048 sigma 1.3 clipped [256,8192], 16q/8kv heads, head_dim 128, "
+                        "block 16, randomly permuted blocks",
+            "batch": 256,
+            "sum_context_tokens": ctx_sum,
+            "pool_blocks": num_blocks,
+            "kv_bytes_per_step": ctx_sum * 4096 * 28,
+            "pct_hbm_peak": round(100 * dec["value"] / HBM_PEAK_GBS, 2),
+        },
+        "roofline": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec["roofline"].items()},
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

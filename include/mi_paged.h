@@ -1,0 +1,142 @@
+/*
+ * mi_paged.h -- C ABI of the MI355X paged-KV data plane (libmi_paged.so).
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * and a HIP stream handle passed as `void*` (0 = the default stream).  No entry
+ * point allocates or frees device memory: the caller owns pools, metadata,
+ * outputs and workspaces.  Work is enqueued asynchronously on `stream`; nothing
+ * here synchronises the device.
+ *
+ * Return value: MI_OK (0) on success, a negative MI_ERR_* code otherwise.  The
+ * message for the last failure on the calling thread is `mi_last_error()`.
+ *
+ * Pool layout (identical to the reference's PagedKVCachePool tensors, which the
+ * reference's tests index directly): one key pool and one value pool per layer,
+ * each `[num_blocks, block_size, num_kv_heads, head_dim]`, row-major.  A slot is
+ * `block_id * block_size + offset`, i.e. the row number of the pool viewed as
+ * `[num_blocks * block_size, num_kv_heads, head_dim]`.  Block 0 is the null
+ * block used to right-pad block tables.
+ *
+ * Index metadata is int64, as the reference packs it on the host.
+ */
+#ifndef MI_PAGED_H
+#define MI_PAGED_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_PAGED_ABI_VERSION 1
+
+#define MI_OK 0
+#define MI_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, bad stride  */
+#define MI_ERR_UNSUPPORTED (-2)      /* shape or alignment the kernels do not cover */
+#define MI_ERR_WORKSPACE (-3)        /* workspace missing or too small            */
+#define MI_ERR_DEVICE (-4)           /* HIP launch / runtime error                */
+
+/* ABI version of the loaded library (MI_PAGED_ABI_VERSION it was built with). */
+int32_t mi_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mi_last_error(void);
+
+/*
+ * Kernel 1 -- reshape-and-cache scatter of new K/V rows into pool slots.
+ *
+ * Replaces PagedKVCachePool.write_prefill
+ *   (src/mini_infra/worker/paged_kv_cache.py:74-95): per layer
+ *   `pool.view(-1, H, D).index_copy_(0, slot_mapping, src[token_rows, :, token_positions, :])`
+ * and the decode-time append in Qwen3Attention._apply_paged_kv_pool
+ *   (src/mini_infra/model/qwen3.py:282-283): `pool.view(-1, H, D).index_copy_(0, slot_mapping, key.squeeze(2))`.
+ *
+ * For token i and every layer l:
+ *   key_pools[l][slot_mapping[i], h, :] = key_src[l][token_rows[i], h, token_positions[i], :]   (h < num_kv_heads)
+ * and the same for values.  Source element (r, h, p, d) is at
+ *   r * row_stride + h * head_stride + p * pos_stride + d     (element strides, d contiguous).
+ * token_rows == NULL means row i; token_positions == NULL means position 0 (the
+ * decode form, source `[B, H, 1, D]`).  The three index arrays share the
+ * element stride `index_stride` (the reference's decode slot_mapping is a
+ * column of a packed [B, 4 + max_blocks] tensor).
+ *
+ * Slots must be unique (as in the reference).  A token whose slot is outside
+ * [0, num_slots), row outside [0, num_src_rows) or position outside
+ * [0, num_src_positions) is skipped: nothing is read or written for it.  The copy
+ * is bit-exact for any element type of `elem_bytes` bytes (2 for bf16/fp16, 4 for fp32).
+ */
+int32_t mi_reshape_and_cache(const void* const* key_src, const void* const* value_src,
+                             int64_t key_row_stride, int64_t key_head_stride, int64_t key_pos_stride,
+                             int64_t value_row_stride, int64_t value_head_stride, int64_t value_pos_stride,
+                             const int64_t* token_rows, const int64_t* token_positions,
+                             const int64_t* slot_mapping, int64_t index_stride, int64_t num_tokens,
+                             int64_t num_src_rows, int64_t num_src_positions,
+                             void* const* key_pools, void* const* value_pools, int32_t num_layers,
+                             int64_t num_slots, int32_t num_kv_heads, int32_t head_dim, int32_t elem_bytes,
+                             void* stream);
+
+/*
+ * Kernel 2 -- block-table gather of whole physical blocks.
+ *
+ * Replaces PagedKVCachePool.gather_blocks (src/mini_infra/worker/paged_kv_cache.py:54-72),
+ *   `key_pool[block_ids].view(B, nb * block_size, H, D)` per layer (the reference then
+ *   returns `.transpose(1, 2)` views of it),
+ * and the history gather of Qwen3Attention._apply_paged_kv_pool (src/mini_infra/model/qwen3.py:288-291).
+ *
+ * For every layer l, row b < batch and j < num_gathered_blocks:
+ *   key_out[l][b, j, :] = key_pools[l][block_ids[b * block_id_stride + j], :]
+ * where one block is `block_bytes` bytes (block_size * num_kv_heads * head_dim * elem_bytes).
+ * Outputs are contiguous `[batch, num_gathered_blocks, block_bytes]`.  Whole blocks are
+ * copied, including null block 0 and stale tails of recycled blocks, so the result is
+ * bit-identical to the reference's advanced-index gather.  A block id outside
+ * [0, num_blocks) yields a zero-filled block.
+ */
+int32_t mi_gather_blocks(const void* const* key_pools, const void* const* value_pools, int64_t num_blocks,
+                         const int64_t* block_ids, int64_t block_id_stride, int32_t batch,
+                         int32_t num_gathered_blocks, void* const* key_out, void* const* value_out,
+                         int32_t num_layers, int64_t block_bytes, void* stream);
+
+/*
+ * Workspace for mi_paged_decode_attention: bytes of float scratch for the
+ * split-context partial results (0 if no sequence needs more than one partition).
+ */
+int64_t mi_paged_decode_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t num_heads,
+                                        int32_t head_dim, int32_t block_size);
+
+/*
+ * Kernel 3 -- paged GQA decode attention (one query token per sequence).
+ *
+ * Replaces the decode branch of Qwen3Attention: the pool gather of
+ * _apply_paged_kv_pool (src/mini_infra/model/qwen3.py:285-292), the additive
+ * context-length bias of Qwen3Model._build_paged_inputs (:513-528) and
+ * _attend with _repeat_key_value (:219-255, :147-156).
+ *
+ * For sequence b and query head h (kv head g = h / (num_heads / num_kv_heads),
+ * the reference's repeat_interleave mapping), with n = min(context_lens[b], max_blocks * block_size):
+ *   s_t = bf16(bf16(q[b,h,:] . K_t) * scale),  K_t = key_pool[block_tables[b, t / bs], t % bs, g, :]
+ *   out[b, h*D : (h+1)*D] = bf16( sum_{t<n} softmax(s)_t * V_t )
+ * Softmax and accumulation run in fp32.  Positions t >= n are excluded (the
+ * reference adds finfo(bf16).min there, which underflows to exactly zero weight).
+ * n <= 0 writes a zero output row.
+ *
+ * query: `[batch, num_heads, head_dim]` bf16 with row/head element strides, head_dim contiguous.
+ * out:   `[batch, num_heads * head_dim]` bf16 with row element stride.
+ * block_tables: `[batch, max_blocks]` int64 with row element stride; ids outside
+ *   [0, num_blocks) read the null block 0 instead.  context_lens: int64 with element stride.
+ * workspace: at least mi_paged_decode_workspace_bytes(...) bytes of device memory.
+ * Specialised for head_dim 128, block_size 16 and num_heads = 2 * num_kv_heads with
+ * num_kv_heads in {1, 2, 4, 8}; other shapes return MI_ERR_UNSUPPORTED.
+ */
+int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, const void* query,
+                                  int64_t query_row_stride, int64_t query_head_stride,
+                                  const void* key_pool, const void* value_pool, int64_t num_blocks,
+                                  const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,
+                                  const int64_t* context_lens, int64_t context_lens_stride, int32_t batch,
+                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                  float scale, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_PAGED_H */

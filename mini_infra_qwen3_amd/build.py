@@ -1,0 +1,82 @@
+"""Builds libmi_paged.so (the HIP kernels + C ABI) in-tree with hipcc for gfx950.
+
+Usage: ``python -m mini_infra_qwen3_amd.build`` (also called by ``__graft_entry__.build()``).
+Every source is compiled on each call; objects go to ``_build/`` and the library next to
+this file, where ``mini_infra_qwen3_amd._native`` loads it from.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC_DIR = PACKAGE_DIR / "csrc"
+REPO_DIR = PACKAGE_DIR.parent
+BUILD_DIR = REPO_DIR / "_build" / "mi_paged"
+LIBRARY_PATH = PACKAGE_DIR / "libmi_paged.so"
+ARCH = "gfx950"
+
+# -packed-fp32-ops: hipcc must not form v_pk_{add,mul,fma}_f32 on its own.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    f"-I{REPO_DIR / 'include'}",
+]
+
+
+def hipcc() -> str:
+    for candidate in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if candidate and Path(candidate).exists():
+            return candidate
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC_DIR.glob("*.hip"))
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD_DIR / (src.stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stdout}\n{proc.stderr}")
+    return obj
+
+
+def build(verbose: bool = True) -> Path:
+    """Compiles every csrc/*.hip for gfx950 and links libmi_paged.so; returns its path."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+    workers = min(len(srcs), 8)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        objs = list(pool.map(_compile, srcs))
+    tmp = LIBRARY_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link of {LIBRARY_PATH.name} failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, LIBRARY_PATH)
+    if verbose:
+        print(f"built {LIBRARY_PATH} from {len(srcs)} sources", flush=True)
+    return LIBRARY_PATH
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

@@ -1,0 +1,46 @@
+// Shared helpers for the paged-KV data plane kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mi_paged.h"
+
+namespace mi {
+
+// ---------------------------------------------------------------- errors ---
+// Records a printf-style message for mi_last_error() on this thread and
+// returns `code`, so call sites can write `return fail(MI_ERR_..., "...")`.
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears the thread's last error and returns MI_OK.
+int32_t ok();
+// Checks hipGetLastError() after a launch; MI_ERR_DEVICE with the HIP message.
+int32_t check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// At most this many layers go into one launch (pointer tables travel in the
+// kernel argument segment); callers with more layers are split into chunks.
+constexpr int kMaxLayersPerLaunch = 32;
+
+// ---------------------------------------------------------------- bf16 -----
+// bf16 -> fp32 is exact: the bf16 bits are the high half of the fp32 word.
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+// fp32 -> bf16 with round-to-nearest-even (NaN kept quiet): add 0x7fff plus the
+// lowest kept bit, then truncate -- the standard bit-level RNE construction.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+}  // namespace mi

@@ -1,0 +1,163 @@
+// Kernel 1: reshape-and-cache scatter of new K/V rows into pool slots.
+//
+// Behaviour of PagedKVCachePool.write_prefill (src/mini_infra/worker/paged_kv_cache.py:74-95)
+// and of the decode append in Qwen3Attention._apply_paged_kv_pool (src/mini_infra/model/qwen3.py:282-283),
+// as one launch covering every layer instead of an advanced-index gather plus an index_copy_
+// per tensor per layer.
+//
+// Work mapping: one workgroup of 256 lanes owns kTokensPerGroup consecutive tokens of one
+// layer.  A token is one destination K row and one V row of num_kv_heads * head_dim
+// elements (2 KiB each for 8 x 128 bf16), contiguous in the pool, so consecutive lanes
+// write consecutive 16-byte pieces of the same slot row: every wavefront store is a
+// fully coalesced 1 KiB run.  Loads for kUnroll pieces are issued before any store so
+// each lane keeps kUnroll requests in flight.
+#include "mi_common.h"
+
+namespace mi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;
+constexpr int kTokensPerGroup = 8;
+
+struct ScatterArgs {
+  const char* key_src[kMaxLayersPerLaunch];
+  const char* value_src[kMaxLayersPerLaunch];
+  char* key_pool[kMaxLayersPerLaunch];
+  char* value_pool[kMaxLayersPerLaunch];
+  const int64_t* token_rows;       // may be null: row i
+  const int64_t* token_positions;  // may be null: position 0
+  const int64_t* slot_mapping;
+  int64_t index_stride;
+  int64_t num_tokens;
+  int64_t num_slots;
+  int64_t num_rows, num_positions;  // source extents along the row and position axes
+  // Byte strides of the sources.
+  int64_t key_row, key_head, key_pos;
+  int64_t value_row, value_head, value_pos;
+  uint32_t row_bytes;        // bytes of one pool row (num_kv_heads * head_dim * elem)
+  uint32_t head_bytes;       // bytes of one head (head_dim * elem)
+  uint32_t chunks_per_head;  // head_bytes / sizeof(V)
+  uint32_t chunks_per_row;   // num_kv_heads * chunks_per_head
+};
+
+template <typename V>
+__global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(const ScatterArgs a) {
+  const int layer = blockIdx.y;
+  const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * kTokensPerGroup;
+  const int64_t ntok = min(static_cast<int64_t>(kTokensPerGroup), a.num_tokens - tok0);
+  const uint32_t per_token = 2u * a.chunks_per_row;  // K row then V row
+  const uint32_t n_items = static_cast<uint32_t>(ntok) * per_token;
+
+  for (uint32_t base = 0; base < n_items; base += kThreads * kUnroll) {
+    V val[kUnroll];
+    V* dst[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      const uint32_t f = base + k * kThreads + threadIdx.x;
+      dst[k] = nullptr;
+      if (f < n_items) {
+        const uint32_t t = f / per_token;
+        const uint32_t r = f - t * per_token;
+        const int64_t i = tok0 + t;
+        const int64_t slot = a.slot_mapping[i * a.index_stride];
+        const int64_t row = a.token_rows ? a.token_rows[i * a.index_stride] : i;
+        const int64_t pos = a.token_positions ? a.token_positions[i * a.index_stride] : 0;
+        if (slot >= 0 && slot < a.num_slots && row >= 0 && row < a.num_rows && pos >= 0 && pos < a.num_positions) {
+          const bool is_value = r >= a.chunks_per_row;
+          const uint32_t w = is_value ? r - a.chunks_per_row : r;
+          const uint32_t h = w / a.chunks_per_head;
+          const uint32_t j = w - h * a.chunks_per_head;
+          const char* src = is_value ? a.value_src[layer] + row * a.value_row + h * a.value_head + pos * a.value_pos
+                                     : a.key_src[layer] + row * a.key_row + h * a.key_head + pos * a.key_pos;
+          val[k] = *reinterpret_cast<const V*>(src + j * sizeof(V));
+          char* pool = is_value ? a.value_pool[layer] : a.key_pool[layer];
+          dst[k] = reinterpret_cast<V*>(pool + slot * a.row_bytes + w * sizeof(V));
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k)
+      if (dst[k]) *dst[k] = val[k];
+  }
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int32_t mi_reshape_and_cache(const void* const* key_src, const void* const* value_src,
+                                        int64_t key_row_stride, int64_t key_head_stride, int64_t key_pos_stride,
+                                        int64_t value_row_stride, int64_t value_head_stride,
+                                        int64_t value_pos_stride, const int64_t* token_rows,
+                                        const int64_t* token_positions, const int64_t* slot_mapping,
+                                        int64_t index_stride, int64_t num_tokens, int64_t num_src_rows,
+                                        int64_t num_src_positions, void* const* key_pools,
+                                        void* const* value_pools, int32_t num_layers, int64_t num_slots,
+                                        int32_t num_kv_heads, int32_t head_dim, int32_t elem_bytes, void* stream) {
+  using namespace mi;
+  if (num_tokens < 0 || num_layers < 0 || num_slots < 0 || num_src_rows < 0 || num_src_positions < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_reshape_and_cache: negative size");
+  if (num_tokens == 0 || num_layers == 0) return ok();
+  if (!key_src || !value_src || !key_pools || !value_pools || !slot_mapping)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_reshape_and_cache: null pointer argument");
+  if (num_kv_heads <= 0 || head_dim <= 0 || (elem_bytes != 2 && elem_bytes != 4))
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_reshape_and_cache: bad shape (heads=%d head_dim=%d elem=%d)",
+                num_kv_heads, head_dim, elem_bytes);
+  if (index_stride <= 0) return fail(MI_ERR_INVALID_ARGUMENT, "mi_reshape_and_cache: index_stride must be > 0");
+
+  ScatterArgs a{};
+  a.token_rows = token_rows;
+  a.token_positions = token_positions;
+  a.slot_mapping = slot_mapping;
+  a.index_stride = index_stride;
+  a.num_tokens = num_tokens;
+  a.num_slots = num_slots;
+  a.num_rows = num_src_rows;
+  a.num_positions = num_src_positions;
+  a.key_row = key_row_stride * elem_bytes;
+  a.key_head = key_head_stride * elem_bytes;
+  a.key_pos = key_pos_stride * elem_bytes;
+  a.value_row = value_row_stride * elem_bytes;
+  a.value_head = value_head_stride * elem_bytes;
+  a.value_pos = value_pos_stride * elem_bytes;
+  a.head_bytes = static_cast<uint32_t>(head_dim) * elem_bytes;
+  a.row_bytes = a.head_bytes * num_kv_heads;
+
+  // The widest piece every address is a multiple of: 16 B on the usual
+  // contiguous bf16 tensors, else the element size.
+  bool wide = a.head_bytes % 16 == 0;
+  const int64_t strides[6] = {a.key_row, a.key_head, a.key_pos, a.value_row, a.value_head, a.value_pos};
+  for (int64_t s : strides) wide = wide && (s % 16 == 0);
+  for (int l = 0; l < num_layers && wide; ++l)
+    wide = aligned16(key_src[l]) && aligned16(value_src[l]) && aligned16(key_pools[l]) && aligned16(value_pools[l]);
+  const uint32_t piece = wide ? 16u : static_cast<uint32_t>(elem_bytes);
+  a.chunks_per_head = a.head_bytes / piece;
+  a.chunks_per_row = a.chunks_per_head * num_kv_heads;
+  if (2ull * a.chunks_per_row * kTokensPerGroup >= (1ull << 31))
+    return fail(MI_ERR_UNSUPPORTED, "mi_reshape_and_cache: row of %u bytes too large", a.row_bytes);
+
+  const int64_t groups = (num_tokens + kTokensPerGroup - 1) / kTokensPerGroup;
+  if (groups > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "mi_reshape_and_cache: too many tokens");
+  hipStream_t s = as_stream(stream);
+  for (int l0 = 0; l0 < num_layers; l0 += kMaxLayersPerLaunch) {
+    const int nl = num_layers - l0 < kMaxLayersPerLaunch ? num_layers - l0 : kMaxLayersPerLaunch;
+    for (int l = 0; l < nl; ++l) {
+      if (!key_src[l0 + l] || !value_src[l0 + l] || !key_pools[l0 + l] || !value_pools[l0 + l])
+        return fail(MI_ERR_INVALID_ARGUMENT, "mi_reshape_and_cache: null pointer for layer %d", l0 + l);
+      a.key_src[l] = static_cast<const char*>(key_src[l0 + l]);
+      a.value_src[l] = static_cast<const char*>(value_src[l0 + l]);
+      a.key_pool[l] = static_cast<char*>(key_pools[l0 + l]);
+      a.value_pool[l] = static_cast<char*>(value_pools[l0 + l]);
+    }
+    dim3 grid(static_cast<uint32_t>(groups), nl);
+    if (piece == 16)
+      reshape_and_cache_kernel<uint4><<<grid, kThreads, 0, s>>>(a);
+    else if (piece == 4)
+      reshape_and_cache_kernel<uint32_t><<<grid, kThreads, 0, s>>>(a);
+    else
+      reshape_and_cache_kernel<uint16_t><<<grid, kThreads, 0, s>>>(a);
+    int32_t rc = check_launch("mi_reshape_and_cache");
+    if (rc != MI_OK) return rc;
+  }
+  return ok();
+}

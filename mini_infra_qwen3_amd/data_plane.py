@@ -1,0 +1,250 @@
+"""Torch-tensor front end of the C ABI: shape/device checks, strides, stream, error mapping.
+
+Every function here enqueues hand-written HIP kernels from libmi_paged.so on the current
+torch stream of the tensors' device.  They accept only GPU tensors: there is no CPU or
+torch fallback, and a missing library raises ``NativeLibraryError``.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import torch
+
+from mini_infra_qwen3_amd import _native
+
+__all__ = [
+    "chunked_prefill_attention",
+    "gather_blocks",
+    "paged_decode_attention",
+    "paged_decode_workspace_bytes",
+    "reshape_and_cache",
+]
+
+
+def _require_gpu(name: str, tensor: torch.Tensor, device: torch.device | None = None) -> None:
+    if tensor.device.type != "cuda":
+        raise RuntimeError(
+            f"{name} is on {tensor.device}: the paged-KV data plane runs only on the GPU (no CPU fallback)"
+        )
+    if device is not None and tensor.device != device:
+        raise ValueError(f"{name} is on {tensor.device}, expected {device}")
+
+
+def _require_index(name: str, tensor: torch.Tensor, ndim: int) -> None:
+    if tensor.dtype != torch.long or tensor.ndim != ndim:
+        raise ValueError(f"{name} must be an int64 tensor with {ndim} dims, got {tensor.dtype} {tuple(tensor.shape)}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def reshape_and_cache(
+    key_src: Sequence[torch.Tensor],
+    value_src: Sequence[torch.Tensor],
+    slot_mapping: torch.Tensor,
+    key_pools: Sequence[torch.Tensor],
+    value_pools: Sequence[torch.Tensor],
+    token_rows: torch.Tensor | None = None,
+    token_positions: torch.Tensor | None = None,
+) -> None:
+    """Scatters K/V rows of every layer into pool slots (kernel 1), in one launch.
+
+    key_src[l] / value_src[l]: ``[B, H_kv, L, D]`` (any strides with D contiguous), one per layer.
+    slot_mapping / token_rows / token_positions: ``[N]`` int64; token ``i`` copies
+    ``src[token_rows[i], :, token_positions[i], :]`` into ``pool.view(-1, H_kv, D)[slot_mapping[i]]``.
+    ``token_rows=None`` means row ``i`` and ``token_positions=None`` position 0 (decode form).
+    Pools: ``[num_blocks, block_size, H_kv, D]`` contiguous, same dtype as the sources.
+    """
+    num_layers = len(key_pools)
+    if not (len(key_src) == len(value_src) == len(value_pools) == num_layers):
+        raise ValueError("reshape_and_cache: per-layer lists differ in length")
+    if num_layers == 0:
+        return
+    device = key_pools[0].device
+    _require_gpu("slot_mapping", slot_mapping, device)
+    _require_index("slot_mapping", slot_mapping, 1)
+    num_tokens = slot_mapping.shape[0]
+    pool0 = key_pools[0]
+    if pool0.ndim != 4:
+        raise ValueError(f"pools must be [num_blocks, block_size, H_kv, D], got {tuple(pool0.shape)}")
+    num_blocks, block_size, num_kv_heads, head_dim = pool0.shape
+    for name, tensors in (("key_pools", key_pools), ("value_pools", value_pools)):
+        for t in tensors:
+            _require_gpu(name, t, device)
+            if t.shape != pool0.shape or t.dtype != pool0.dtype or not t.is_contiguous():
+                raise ValueError(f"{name}: every pool must be contiguous {tuple(pool0.shape)} {pool0.dtype}")
+    k0, v0 = key_src[0], value_src[0]
+    for name, tensors, ref in (("key_src", key_src, k0), ("value_src", value_src, v0)):
+        for t in tensors:
+            _require_gpu(name, t, device)
+            if t.ndim != 4 or t.shape[1] != num_kv_heads or t.shape[3] != head_dim or t.dtype != pool0.dtype:
+                raise ValueError(f"{name} must be [B, {num_kv_heads}, L, {head_dim}] {pool0.dtype}, got "
+                                 f"{tuple(t.shape)} {t.dtype}")
+            if t.stride() != ref.stride() or t.shape != ref.shape or t.stride(3) != 1:
+                raise ValueError(f"{name}: all layers need the same shape and strides, with D contiguous")
+    if k0.shape[:3] != v0.shape[:3]:
+        raise ValueError("reshape_and_cache: key and value sources differ in shape")
+
+    index_stride = slot_mapping.stride(0) if num_tokens > 1 else 1
+    for name, t in (("token_rows", token_rows), ("token_positions", token_positions)):
+        if t is not None:
+            _require_gpu(name, t, device)
+            _require_index(name, t, 1)
+            if t.shape[0] != num_tokens:
+                raise ValueError(f"{name} has {t.shape[0]} entries, slot_mapping {num_tokens}")
+    strides = {t.stride(0) for t in (slot_mapping, token_rows, token_positions) if t is not None and num_tokens > 1}
+    if len(strides) > 1:
+        slot_mapping = slot_mapping.contiguous()
+        token_rows = token_rows.contiguous() if token_rows is not None else None
+        token_positions = token_positions.contiguous() if token_positions is not None else None
+        index_stride = 1
+    if num_tokens == 0:
+        return
+
+    lib = _native.load()
+    rc = lib.mi_reshape_and_cache(
+        _native.pointer_array([t.data_ptr() for t in key_src]),
+        _native.pointer_array([t.data_ptr() for t in value_src]),
+        k0.stride(0), k0.stride(1), k0.stride(2),
+        v0.stride(0), v0.stride(1), v0.stride(2),
+        token_rows.data_ptr() if token_rows is not None else None,
+        token_positions.data_ptr() if token_positions is not None else None,
+        slot_mapping.data_ptr(),
+        index_stride,
+        num_tokens,
+        k0.shape[0],
+        k0.shape[2],
+        _native.pointer_array([t.data_ptr() for t in key_pools]),
+        _native.pointer_array([t.data_ptr() for t in value_pools]),
+        num_layers,
+        num_blocks * block_size,
+        num_kv_heads,
+        head_dim,
+        pool0.element_size(),
+        _stream(device),
+    )
+    _native.check(rc, "mi_reshape_and_cache")
+
+
+def gather_blocks(
+    key_pools: Sequence[torch.Tensor],
+    value_pools: Sequence[torch.Tensor],
+    block_ids: torch.Tensor,
+    key_out: Sequence[torch.Tensor],
+    value_out: Sequence[torch.Tensor],
+) -> None:
+    """Copies whole pool blocks by block table for every layer (kernel 2), in one launch.
+
+    block_ids: ``[B, nb]`` int64 (rows may be strided); outputs: contiguous ``[B, nb * block_size, H_kv, D]``.
+    """
+    num_layers = len(key_pools)
+    if not (len(value_pools) == len(key_out) == len(value_out) == num_layers):
+        raise ValueError("gather_blocks: per-layer lists differ in length")
+    if num_layers == 0:
+        return
+    pool0 = key_pools[0]
+    device = pool0.device
+    _require_gpu("block_ids", block_ids, device)
+    _require_index("block_ids", block_ids, 2)
+    if block_ids.stride(1) != 1:
+        block_ids = block_ids.contiguous()
+    batch, nb = block_ids.shape
+    num_blocks, block_size, num_kv_heads, head_dim = pool0.shape
+    expect = (batch, nb * block_size, num_kv_heads, head_dim)
+    for name, tensors, shape in (("key_pools", key_pools, pool0.shape), ("value_pools", value_pools, pool0.shape),
+                                 ("key_out", key_out, expect), ("value_out", value_out, expect)):
+        for t in tensors:
+            _require_gpu(name, t, device)
+            if tuple(t.shape) != tuple(shape) or t.dtype != pool0.dtype or not t.is_contiguous():
+                raise ValueError(f"{name}: expected contiguous {tuple(shape)} {pool0.dtype}, got "
+                                 f"{tuple(t.shape)} {t.dtype}")
+    if batch == 0 or nb == 0:
+        return
+    lib = _native.load()
+    rc = lib.mi_gather_blocks(
+        _native.pointer_array([t.data_ptr() for t in key_pools]),
+        _native.pointer_array([t.data_ptr() for t in value_pools]),
+        num_blocks,
+        block_ids.data_ptr(),
+        block_ids.stride(0) if batch > 1 else nb,
+        batch,
+        nb,
+        _native.pointer_array([t.data_ptr() for t in key_out]),
+        _native.pointer_array([t.data_ptr() for t in value_out]),
+        num_layers,
+        block_size * num_kv_heads * head_dim * pool0.element_size(),
+        _stream(device),
+    )
+    _native.check(rc, "mi_gather_blocks")
+
+
+def paged_decode_workspace_bytes(batch: int, max_blocks: int, num_heads: int, head_dim: int, block_size: int) -> int:
+    return int(_native.load().mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size))
+
+
+def paged_decode_attention(
+    query: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Paged GQA decode attention straight from the pool (kernel 3).
+
+    query: ``[B, H, D]`` bf16 (D contiguous); pools ``[num_blocks, 16, H_kv, D]`` bf16 contiguous;
+    block_tables ``[B, max_blocks]`` int64 (null-padded); context_lens ``[B]`` int64 (includes the
+    new token).  Returns ``out`` ``[B, H * D]`` bf16.
+    """
+    device = key_pool.device
+    for name, t in (("query", query), ("key_pool", key_pool), ("value_pool", value_pool),
+                    ("block_tables", block_tables), ("context_lens", context_lens)):
+        _require_gpu(name, t, device)
+    _require_index("block_tables", block_tables, 2)
+    _require_index("context_lens", context_lens, 1)
+    if query.ndim != 3 or query.dtype != torch.bfloat16 or query.stride(2) != 1:
+        raise ValueError(f"query must be [B, H, D] bf16 with D contiguous, got {tuple(query.shape)} {query.dtype}")
+    if key_pool.dtype != torch.bfloat16 or value_pool.shape != key_pool.shape or value_pool.dtype != key_pool.dtype:
+        raise ValueError("pools must be bf16 with identical shapes")
+    if not (key_pool.is_contiguous() and value_pool.is_contiguous()):
+        raise ValueError("pools must be contiguous")
+    batch, num_heads, head_dim = query.shape
+    num_blocks, block_size, num_kv_heads, pool_head_dim = key_pool.shape
+    if pool_head_dim != head_dim:
+        raise ValueError(f"query head_dim {head_dim} != pool head_dim {pool_head_dim}")
+    if block_tables.shape[0] != batch or context_lens.shape[0] != batch:
+        raise ValueError("block_tables / context_lens batch differs from query batch")
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    max_blocks = block_tables.shape[1]
+    if out is None:
+        out = torch.empty((batch, num_heads * head_dim), dtype=torch.bfloat16, device=device)
+    elif out.shape != (batch, num_heads * head_dim) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError(f"out must be [B, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
+    if batch == 0:
+        return out
+    need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size)
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    lib = _native.load()
+    rc = lib.mi_paged_decode_attention(
+        out.data_ptr(), out.stride(0),
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_pool.data_ptr(), value_pool.data_ptr(), num_blocks,
+        block_tables.data_ptr(), block_tables.stride(0) if batch > 1 else max(max_blocks, 1), max_blocks,
+        context_lens.data_ptr(), context_lens.stride(0) if batch > 1 else 1,
+        batch, num_heads, num_kv_heads, head_dim, block_size, float(scale),
+        workspace.data_ptr() if (need > 0 and workspace is not None) else None,
+        (workspace.numel() * workspace.element_size()) if (need > 0 and workspace is not None) else 0,
+        _stream(device),
+    )
+    _native.check(rc, "mi_paged_decode_attention")
+    return out
+
+
+def chunked_prefill_attention(*args, **kwargs):  # pragma: no cover - defined with kernel 4
+    raise NotImplementedError("chunked prefill attention kernel is not built yet")

@@ -1,0 +1,7 @@
+"""GPU data plane of the paged KV cache: block pool, runners, host metadata packing."""
+
+from mini_infra_qwen3_amd.worker.kv_cache import KVCache
+from mini_infra_qwen3_amd.worker.paged_kv_cache import PagedKVCachePool
+from mini_infra_qwen3_amd.worker.sampler import greedy_sample
+
+__all__ = ["KVCache", "PagedKVCachePool", "greedy_sample"]

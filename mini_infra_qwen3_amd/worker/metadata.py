@@ -1,0 +1,107 @@
+"""Host-side packing of paged-attention metadata, vectorised with numpy.
+
+The reference builds these int64 rows with per-token / per-row Python loops
+(src/mini_infra/worker/paged_runner.py:57-72, :118-128, :154-161); the values here are
+identical, computed per block row with array operations so host time stays flat as the
+batch and prompt lengths grow.  Everything returns numpy int64 arrays that the runner
+uploads with a single host-to-device copy.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import numpy as np
+
+from mini_infra_qwen3_amd.core.block_manager import NULL_BLOCK_ID
+
+
+def padded_tables(block_tables: Sequence[Sequence[int]], width: int | None = None) -> np.ndarray:
+    """Ragged block tables -> ``[B, width]`` int64, right-padded with the null block."""
+    lengths = [len(t) for t in block_tables]
+    width = max(lengths, default=0) if width is None else width
+    out = np.full((len(block_tables), width), NULL_BLOCK_ID, dtype=np.int64)
+    for row, (table, n) in enumerate(zip(block_tables, lengths)):
+        n = min(n, width)
+        if n:
+            out[row, :n] = np.asarray(table[:n], dtype=np.int64)
+    return out
+
+
+def pack_decode_rows(block_tables: Sequence[Sequence[int]], last_tokens: Sequence[int],
+                     positions: Sequence[int], block_size: int) -> np.ndarray:
+    """``[B, 4 + max_blocks]``: token, position, slot, context length, null-padded block table.
+
+    Same columns as the reference's decode packing (src/mini_infra/worker/paged_runner.py:154-162).
+    """
+    tables = padded_tables(block_tables)
+    pos = np.asarray(positions, dtype=np.int64)
+    rows = np.arange(len(block_tables))
+    logical = pos // block_size
+    if np.any(logical >= np.array([len(t) for t in block_tables])):
+        raise ValueError("a block table does not cover its decode position")
+    out = np.empty((len(block_tables), 4 + tables.shape[1]), dtype=np.int64)
+    out[:, 0] = np.asarray(last_tokens, dtype=np.int64)
+    out[:, 1] = pos
+    out[:, 2] = tables[rows, logical] * block_size + pos % block_size
+    out[:, 3] = pos + 1
+    out[:, 4:] = tables
+    return out
+
+
+def prefill_scatter_indices(block_tables: Sequence[Sequence[int]], chunk_lens: Sequence[int],
+                            start_positions: Sequence[int], padded_length: int, block_size: int) -> np.ndarray:
+    """``[3, N]`` (token_rows, token_positions, slots) of the valid chunk tokens, row-major.
+
+    Token t of row i sits at padded position ``padded_length - chunk_lens[i] + t`` and goes to
+    logical position ``start_positions[i] + t`` (src/mini_infra/worker/paged_runner.py:118-128).
+    """
+    lens = np.asarray(chunk_lens, dtype=np.int64)
+    starts = np.asarray(start_positions, dtype=np.int64)
+    total = int(lens.sum())
+    out = np.empty((3, total), dtype=np.int64)
+    if total == 0:
+        return out
+    rows = np.repeat(np.arange(len(lens), dtype=np.int64), lens)
+    offsets = np.arange(total, dtype=np.int64) - np.repeat(np.cumsum(lens) - lens, lens)  # t within its row
+    logical = np.repeat(starts, lens) + offsets
+    width = max(int(((starts + lens + block_size - 1) // block_size).max()), 1)
+    tables = padded_tables(block_tables, width)
+    covered = np.array([len(t) for t in block_tables], dtype=np.int64)
+    if np.any(logical // block_size >= covered[rows]):
+        raise ValueError("a block table does not cover its chunk")
+    out[0] = rows
+    out[1] = padded_length - np.repeat(lens, lens) + offsets
+    out[2] = tables[rows, logical // block_size] * block_size + logical % block_size
+    return out
+
+
+def pack_prefill_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions: Sequence[int],
+                      block_tables: Sequence[Sequence[int]], block_size: int, pad_token_id: int) -> np.ndarray:
+    """``[B, 2 L + 2 + max_history_blocks]``: left-padded ids | positions | start, len | history table.
+
+    Same row layout as the reference's chunked-prefill packing
+    (src/mini_infra/worker/paged_runner.py:57-72); history blocks are the first
+    ``ceil(start / block_size)`` entries of each table, null-padded.
+    """
+    lens = [len(ids) for ids in chunk_token_ids]
+    if not lens or min(lens) < 1:
+        raise ValueError("every chunk must hold at least one token")
+    width = max(lens)
+    hist = [-(-s // block_size) for s in start_positions]
+    max_hist = max(hist)
+    out = np.zeros((len(lens), 2 * width + 2 + max_hist), dtype=np.int64)
+    out[:, :width] = pad_token_id
+    for row, (ids, n, start, table, h) in enumerate(zip(chunk_token_ids, lens, start_positions, block_tables, hist)):
+        out[row, width - n:width] = np.asarray(ids, dtype=np.int64)
+        out[row, 2 * width - n:2 * width] = np.arange(start, start + n, dtype=np.int64)
+        out[row, 2 * width] = start
+        out[row, 2 * width + 1] = n
+        if h:
+            if len(table) < h:
+                raise ValueError("a block table does not cover its history")
+            out[row, 2 * width + 2:2 * width + 2 + h] = np.asarray(table[:h], dtype=np.int64)
+    return out
+
+
+__all__ = ["pack_decode_rows", "pack_prefill_rows", "padded_tables", "prefill_scatter_indices"]

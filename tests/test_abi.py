@@ -1,0 +1,99 @@
+"""The C ABI library loads without a GPU, exports every entry point include/*.h declares with
+the signatures the binding expects, and rejects bad arguments on the host (no GPU call)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mini_infra_qwen3_amd import _native
+
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
+DECL = re.compile(r"^\s*(?:const\s+)?[\w\s\*]+?\b(mi_\w+)\s*\(", re.M)
+
+
+def declared_symbols() -> set[str]:
+    names = set()
+    for header in HEADERS:
+        names.update(DECL.findall(header.read_text()))
+    return names
+
+
+def test_headers_declare_the_entry_points():
+    names = declared_symbols()
+    assert {"mi_abi_version", "mi_last_error", "mi_reshape_and_cache", "mi_gather_blocks",
+            "mi_paged_decode_attention", "mi_paged_decode_workspace_bytes"} <= names
+
+
+def test_library_exports_every_declared_symbol(native_lib):
+    for name in sorted(declared_symbols()):
+        assert hasattr(native_lib, name), f"{name} declared in include/ but not exported"
+
+
+def test_binding_covers_every_declared_symbol():
+    assert declared_symbols() == set(_native.SIGNATURES)
+
+
+def test_abi_version(native_lib):
+    assert native_lib.mi_abi_version() == _native.ABI_VERSION
+
+
+def test_decode_workspace_size(native_lib):
+    # one partition (<= 16 blocks) needs no workspace; beyond that batch * parts * heads * (128 + 2) floats
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 16, 16, 128, 16) == 0
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 128, 16) == 256 * 32 * 16 * 130 * 4
+    assert native_lib.mi_paged_decode_workspace_bytes(4, 17, 16, 128, 16) == 4 * 2 * 16 * 130 * 4
+
+
+def _ptrs(n):
+    return (ctypes.c_void_p * n)(*([16] * n))
+
+
+def test_scatter_rejects_bad_arguments_on_host(native_lib):
+    lib = native_lib
+    rc = lib.mi_reshape_and_cache(_ptrs(1), _ptrs(1), 0, 0, 0, 0, 0, 0, None, None, None, 1, -1, 1, 1,
+                                  _ptrs(1), _ptrs(1), 1, 16, 8, 128, 2, None)
+    assert rc == _native.MI_ERR_INVALID_ARGUMENT and b"negative" in lib.mi_last_error()
+    rc = lib.mi_reshape_and_cache(_ptrs(1), _ptrs(1), 0, 0, 0, 0, 0, 0, None, None, None, 1, 4, 1, 1,
+                                  _ptrs(1), _ptrs(1), 1, 16, 8, 128, 2, None)
+    assert rc == _native.MI_ERR_INVALID_ARGUMENT  # null slot_mapping
+    rc = lib.mi_reshape_and_cache(_ptrs(1), _ptrs(1), 0, 0, 0, 0, 0, 0, None, None, 16, 1, 4, 1, 1,
+                                  _ptrs(1), _ptrs(1), 1, 16, 8, 128, 3, None)
+    assert rc == _native.MI_ERR_INVALID_ARGUMENT  # element size 3
+    # nothing to do is success
+    assert lib.mi_reshape_and_cache(None, None, 0, 0, 0, 0, 0, 0, None, None, None, 1, 0, 0, 0,
+                                    None, None, 0, 0, 8, 128, 2, None) == _native.MI_OK
+
+
+def test_gather_rejects_bad_arguments_on_host(native_lib):
+    lib = native_lib
+    rc = lib.mi_gather_blocks(_ptrs(1), _ptrs(1), 8, 16, 1, 2, 4, _ptrs(1), _ptrs(1), 1, 65536, None)
+    assert rc == _native.MI_ERR_INVALID_ARGUMENT and b"stride" in lib.mi_last_error()
+    rc = lib.mi_gather_blocks(_ptrs(1), _ptrs(1), 8, None, 4, 2, 4, _ptrs(1), _ptrs(1), 1, 65536, None)
+    assert rc == _native.MI_ERR_INVALID_ARGUMENT
+
+
+def test_decode_rejects_unsupported_shapes_on_host(native_lib):
+    lib = native_lib
+    args = dict(out=16, q=16, kp=16, vp=16, bt=16, ctx=16)
+
+    def call(heads=16, kv=8, dim=128, bs=16, ws=None, ws_bytes=0, max_blocks=4):
+        return lib.mi_paged_decode_attention(args["out"], heads * dim, args["q"], heads * dim, dim, args["kp"],
+                                             args["vp"], 100, args["bt"], max_blocks, max_blocks, args["ctx"], 1,
+                                             2, heads, kv, dim, bs, 0.1, ws, ws_bytes, None)
+
+    assert call(dim=64) == _native.MI_ERR_UNSUPPORTED
+    assert call(bs=8) == _native.MI_ERR_UNSUPPORTED
+    assert call(heads=24) == _native.MI_ERR_UNSUPPORTED
+    assert call(heads=6, kv=3) == _native.MI_ERR_UNSUPPORTED
+    assert call(max_blocks=40) == _native.MI_ERR_WORKSPACE  # three partitions, no workspace
+    assert b"workspace" in lib.mi_last_error()
+
+
+def test_check_maps_status_to_python_errors(native_lib):
+    native_lib.mi_gather_blocks(_ptrs(1), _ptrs(1), 8, None, 4, 2, 4, _ptrs(1), _ptrs(1), 1, 65536, None)
+    with pytest.raises(ValueError, match="null pointer"):
+        _native.check(_native.MI_ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(RuntimeError):
+        _native.check(_native.MI_ERR_DEVICE, "x")
