@@ -48,33 +48,40 @@ def sources() -> list[Path]:
     return sorted(CSRC_DIR.glob("*.hip"))
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, build_dir: Path, extra: tuple[str, ...]) -> Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stdout}\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compiles every csrc/*.hip for gfx950 and links libmi_paged.so; returns its path."""
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+def build(verbose: bool = True, extra_flags: tuple[str, ...] = (), output: Path | None = None) -> Path:
+    """Compiles every csrc/*.hip for gfx950 and links libmi_paged.so; returns its path.
+
+    ``extra_flags`` (e.g. ``-DMI_DECODE_PART_BLOCKS=32`` to override a kernel tunable) and
+    ``output`` build a variant library elsewhere; the defaults build the in-tree library.
+    """
+    output = LIBRARY_PATH if output is None else Path(output)
+    build_dir = BUILD_DIR if output == LIBRARY_PATH else output.parent / "_obj"
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
     workers = min(len(srcs), 8)
+    extra = tuple(extra_flags)
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objs = list(pool.map(_compile, srcs))
-    tmp = LIBRARY_PATH.with_suffix(".so.tmp")
+        objs = list(pool.map(lambda src: _compile(src, build_dir, extra), srcs))
+    tmp = output.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link of {LIBRARY_PATH.name} failed:\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIBRARY_PATH)
+    os.replace(tmp, output)
     if verbose:
-        print(f"built {LIBRARY_PATH} from {len(srcs)} sources", flush=True)
-    return LIBRARY_PATH
+        print(f"built {output} from {len(srcs)} sources", flush=True)
+    return output
 
 
 if __name__ == "__main__":

@@ -11,8 +11,16 @@
 namespace mi {
 namespace {
 
+#ifndef MI_GATHER_UNROLL
+#define MI_GATHER_UNROLL 8
+#endif
+#ifndef MI_GATHER_NT
+#define MI_GATHER_NT 1
+#endif
+
 constexpr int kThreads = 256;
-constexpr int kUnroll = 8;
+constexpr int kUnroll = MI_GATHER_UNROLL;
+constexpr bool kNt = MI_GATHER_NT != 0;  // non-temporal pool loads and output stores
 
 struct GatherArgs {
   const char* key_pool[kMaxLayersPerLaunch];
@@ -49,7 +57,7 @@ __global__ __launch_bounds__(kThreads) void gather_blocks_kernel(const GatherArg
       const uint32_t p = base + k * kThreads + threadIdx.x;
       if (p < a.pieces) {
         if (valid) {
-          val[k] = src[p];
+          val[k] = load_vec<kNt>(src + p);
         } else {
           val[k] = V{};
         }
@@ -58,7 +66,7 @@ __global__ __launch_bounds__(kThreads) void gather_blocks_kernel(const GatherArg
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < a.pieces) dst[p] = val[k];
+      if (p < a.pieces) store_vec<kNt>(dst + p, val[k]);
     }
   }
 }
@@ -111,7 +119,7 @@ extern "C" int32_t mi_gather_blocks(const void* const* key_pools, const void* co
     }
     dim3 grid(static_cast<uint32_t>(batch) * num_gathered_blocks, nl, 2);
     if (piece == 16)
-      gather_blocks_kernel<uint4><<<grid, kThreads, 0, s>>>(a);
+      gather_blocks_kernel<u32x4><<<grid, kThreads, 0, s>>>(a);
     else if (piece == 4)
       gather_blocks_kernel<uint32_t><<<grid, kThreads, 0, s>>>(a);
     else

@@ -17,6 +17,30 @@ int32_t ok();
 // Checks hipGetLastError() after a launch; MI_ERR_DEVICE with the HIP message.
 int32_t check_launch(const char* what);
 
+// 16-byte vector used by the streaming copies (a native vector type, so the
+// non-temporal builtins accept it).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Loads / stores of data touched once per launch (pool rows, copies), optionally with the
+// non-temporal hint so the stream does not displace reused lines in L2 and the Infinity
+// Cache.  Each kernel picks kNt from its own tunable.
+template <bool kNt, typename T>
+__device__ __forceinline__ T load_vec(const T* p) {
+  if constexpr (kNt) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+template <bool kNt, typename T>
+__device__ __forceinline__ void store_vec(T* p, const T& v) {
+  if constexpr (kNt) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
+}
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

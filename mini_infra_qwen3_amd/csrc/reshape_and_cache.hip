@@ -5,20 +5,37 @@
 // as one launch covering every layer instead of an advanced-index gather plus an index_copy_
 // per tensor per layer.
 //
-// Work mapping: one workgroup of 256 lanes owns kTokensPerGroup consecutive tokens of one
-// layer.  A token is one destination K row and one V row of num_kv_heads * head_dim
-// elements (2 KiB each for 8 x 128 bf16), contiguous in the pool, so consecutive lanes
-// write consecutive 16-byte pieces of the same slot row: every wavefront store is a
-// fully coalesced 1 KiB run.  Loads for kUnroll pieces are issued before any store so
-// each lane keeps kUnroll requests in flight.
+// Work mapping: a token is one destination K row and one V row of num_kv_heads * head_dim
+// elements (2 KiB each for 8 x 128 bf16), contiguous in the pool.  A workgroup of 256 lanes
+// owns kTokensPerGroup consecutive tokens of one layer.
+//  * Row kernel (a token's K+V rows are a multiple of 256 16-byte pieces -- the Qwen3 shape):
+//    every lane owns fixed pieces of the row pair, so consecutive lanes move consecutive
+//    16-byte pieces of one slot row and each wavefront store is a fully coalesced 1 KiB run.
+//    The group's (row, position, slot) triples are staged once through LDS (one coalesced
+//    read), then kUnroll tokens' loads are issued before their stores.
+//  * Generic kernel (any other row size or misaligned strides): flat piece index with
+//    element-size pieces; used by small shapes only.
 #include "mi_common.h"
+
+#ifndef MI_SCATTER_TOKENS_PER_GROUP
+#define MI_SCATTER_TOKENS_PER_GROUP 32
+#endif
+#ifndef MI_SCATTER_UNROLL
+#define MI_SCATTER_UNROLL 8
+#endif
+#ifndef MI_SCATTER_NT
+#define MI_SCATTER_NT 1
+#endif
 
 namespace mi {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 8;
-constexpr int kTokensPerGroup = 8;
+constexpr int kTokensPerGroup = MI_SCATTER_TOKENS_PER_GROUP;
+constexpr int kUnroll = MI_SCATTER_UNROLL;
+constexpr bool kNt = MI_SCATTER_NT != 0;  // non-temporal source loads and pool stores
+constexpr int kGenericUnroll = 8;
+constexpr int kGenericTokensPerGroup = 8;
 
 struct ScatterArgs {
   const char* key_src[kMaxLayersPerLaunch];
@@ -37,47 +54,108 @@ struct ScatterArgs {
   int64_t value_row, value_head, value_pos;
   uint32_t row_bytes;        // bytes of one pool row (num_kv_heads * head_dim * elem)
   uint32_t head_bytes;       // bytes of one head (head_dim * elem)
-  uint32_t chunks_per_head;  // head_bytes / sizeof(V)
+  uint32_t chunks_per_head;  // head_bytes / piece
   uint32_t chunks_per_row;   // num_kv_heads * chunks_per_head
+  int32_t tokens_per_group;  // row kernel: tokens per workgroup (<= kTokensPerGroup)
 };
 
-template <typename V>
-__global__ __launch_bounds__(kThreads) void reshape_and_cache_kernel(const ScatterArgs a) {
+// Source byte offsets of token i for K and V; slot -1 when the token is skipped.
+struct TokenRef {
+  int64_t key_off, value_off, slot;
+};
+
+__device__ __forceinline__ TokenRef token_ref(const ScatterArgs& a, int64_t i) {
+  const int64_t slot = a.slot_mapping[i * a.index_stride];
+  const int64_t row = a.token_rows ? a.token_rows[i * a.index_stride] : i;
+  const int64_t pos = a.token_positions ? a.token_positions[i * a.index_stride] : 0;
+  const bool ok = slot >= 0 && slot < a.num_slots && row >= 0 && row < a.num_rows && pos >= 0 &&
+                  pos < a.num_positions;
+  TokenRef t;
+  t.slot = ok ? slot : -1;
+  t.key_off = row * a.key_row + pos * a.key_pos;
+  t.value_off = row * a.value_row + pos * a.value_pos;
+  return t;
+}
+
+// Row kernel: 2 * chunks_per_row (16-byte pieces per token) is a multiple of kThreads.
+__global__ __launch_bounds__(kThreads) void reshape_and_cache_rows(const ScatterArgs a) {
+  __shared__ int64_t s_key[kTokensPerGroup], s_value[kTokensPerGroup], s_slot[kTokensPerGroup];
   const int layer = blockIdx.y;
-  const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * kTokensPerGroup;
-  const int64_t ntok = min(static_cast<int64_t>(kTokensPerGroup), a.num_tokens - tok0);
+  const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * a.tokens_per_group;
+  const int ntok = static_cast<int>(min(static_cast<int64_t>(a.tokens_per_group), a.num_tokens - tok0));
+  if (static_cast<int>(threadIdx.x) < ntok) {
+    const TokenRef t = token_ref(a, tok0 + threadIdx.x);
+    s_key[threadIdx.x] = t.key_off;
+    s_value[threadIdx.x] = t.value_off;
+    s_slot[threadIdx.x] = t.slot;
+  }
+  __syncthreads();
+
+  const char* key_src = a.key_src[layer];
+  const char* value_src = a.value_src[layer];
+  char* key_pool = a.key_pool[layer];
+  char* value_pool = a.value_pool[layer];
+  const uint32_t per_token = 2u * a.chunks_per_row;
+  for (uint32_t c = threadIdx.x; c < per_token; c += kThreads) {
+    // Fixed piece of this lane: K or V, head h, 16-byte column j.
+    const bool is_value = c >= a.chunks_per_row;
+    const uint32_t w = is_value ? c - a.chunks_per_row : c;
+    const uint32_t h = w / a.chunks_per_head;
+    const uint32_t j = w - h * a.chunks_per_head;
+    const char* src = (is_value ? value_src : key_src) + h * (is_value ? a.value_head : a.key_head) + j * 16u;
+    char* dst = (is_value ? value_pool : key_pool) + w * 16u;
+    const int64_t* s_off = is_value ? s_value : s_key;
+    for (int t0 = 0; t0 < ntok; t0 += kUnroll) {
+      u32x4 val[kUnroll];
+#pragma unroll
+      for (int k = 0; k < kUnroll; ++k) {
+        const int t = t0 + k;
+        if (t < ntok && s_slot[t] >= 0) val[k] = load_vec<kNt>(reinterpret_cast<const u32x4*>(src + s_off[t]));
+      }
+#pragma unroll
+      for (int k = 0; k < kUnroll; ++k) {
+        const int t = t0 + k;
+        if (t < ntok && s_slot[t] >= 0) store_vec<kNt>(reinterpret_cast<u32x4*>(dst + s_slot[t] * a.row_bytes), val[k]);
+      }
+    }
+  }
+}
+
+// Generic kernel: flat piece index, any piece size V.
+template <typename V>
+__global__ __launch_bounds__(kThreads) void reshape_and_cache_generic(const ScatterArgs a) {
+  const int layer = blockIdx.y;
+  const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * kGenericTokensPerGroup;
+  const int64_t ntok = min(static_cast<int64_t>(kGenericTokensPerGroup), a.num_tokens - tok0);
   const uint32_t per_token = 2u * a.chunks_per_row;  // K row then V row
   const uint32_t n_items = static_cast<uint32_t>(ntok) * per_token;
 
-  for (uint32_t base = 0; base < n_items; base += kThreads * kUnroll) {
-    V val[kUnroll];
-    V* dst[kUnroll];
+  for (uint32_t base = 0; base < n_items; base += kThreads * kGenericUnroll) {
+    V val[kGenericUnroll];
+    V* dst[kGenericUnroll];
 #pragma unroll
-    for (int k = 0; k < kUnroll; ++k) {
+    for (int k = 0; k < kGenericUnroll; ++k) {
       const uint32_t f = base + k * kThreads + threadIdx.x;
       dst[k] = nullptr;
       if (f < n_items) {
         const uint32_t t = f / per_token;
         const uint32_t r = f - t * per_token;
-        const int64_t i = tok0 + t;
-        const int64_t slot = a.slot_mapping[i * a.index_stride];
-        const int64_t row = a.token_rows ? a.token_rows[i * a.index_stride] : i;
-        const int64_t pos = a.token_positions ? a.token_positions[i * a.index_stride] : 0;
-        if (slot >= 0 && slot < a.num_slots && row >= 0 && row < a.num_rows && pos >= 0 && pos < a.num_positions) {
+        const TokenRef ref = token_ref(a, tok0 + t);
+        if (ref.slot >= 0) {
           const bool is_value = r >= a.chunks_per_row;
           const uint32_t w = is_value ? r - a.chunks_per_row : r;
           const uint32_t h = w / a.chunks_per_head;
           const uint32_t j = w - h * a.chunks_per_head;
-          const char* src = is_value ? a.value_src[layer] + row * a.value_row + h * a.value_head + pos * a.value_pos
-                                     : a.key_src[layer] + row * a.key_row + h * a.key_head + pos * a.key_pos;
+          const char* src = is_value ? a.value_src[layer] + ref.value_off + h * a.value_head
+                                     : a.key_src[layer] + ref.key_off + h * a.key_head;
           val[k] = *reinterpret_cast<const V*>(src + j * sizeof(V));
           char* pool = is_value ? a.value_pool[layer] : a.key_pool[layer];
-          dst[k] = reinterpret_cast<V*>(pool + slot * a.row_bytes + w * sizeof(V));
+          dst[k] = reinterpret_cast<V*>(pool + ref.slot * a.row_bytes + w * sizeof(V));
         }
       }
     }
 #pragma unroll
-    for (int k = 0; k < kUnroll; ++k)
+    for (int k = 0; k < kGenericUnroll; ++k)
       if (dst[k]) *dst[k] = val[k];
   }
 }
@@ -133,10 +211,19 @@ extern "C" int32_t mi_reshape_and_cache(const void* const* key_src, const void* 
   const uint32_t piece = wide ? 16u : static_cast<uint32_t>(elem_bytes);
   a.chunks_per_head = a.head_bytes / piece;
   a.chunks_per_row = a.chunks_per_head * num_kv_heads;
-  if (2ull * a.chunks_per_row * kTokensPerGroup >= (1ull << 31))
+  if (2ull * a.chunks_per_row * kGenericTokensPerGroup >= (1ull << 31))
     return fail(MI_ERR_UNSUPPORTED, "mi_reshape_and_cache: row of %u bytes too large", a.row_bytes);
+  const bool rows_kernel = wide && (2u * a.chunks_per_row) % kThreads == 0;
+  // Few tokens (a decode append) spread one per workgroup over the CUs; many tokens (a prompt)
+  // go kTokensPerGroup per workgroup so each lane keeps kUnroll loads in flight.
+  int64_t per_group = kGenericTokensPerGroup;
+  if (rows_kernel) {
+    const int64_t spread = (num_tokens * num_layers + 2047) / 2048;
+    per_group = spread < 1 ? 1 : (spread > kTokensPerGroup ? kTokensPerGroup : spread);
+  }
+  a.tokens_per_group = static_cast<int32_t>(per_group);
 
-  const int64_t groups = (num_tokens + kTokensPerGroup - 1) / kTokensPerGroup;
+  const int64_t groups = (num_tokens + per_group - 1) / per_group;
   if (groups > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "mi_reshape_and_cache: too many tokens");
   hipStream_t s = as_stream(stream);
   for (int l0 = 0; l0 < num_layers; l0 += kMaxLayersPerLaunch) {
@@ -150,12 +237,14 @@ extern "C" int32_t mi_reshape_and_cache(const void* const* key_src, const void* 
       a.value_pool[l] = static_cast<char*>(value_pools[l0 + l]);
     }
     dim3 grid(static_cast<uint32_t>(groups), nl);
-    if (piece == 16)
-      reshape_and_cache_kernel<uint4><<<grid, kThreads, 0, s>>>(a);
+    if (rows_kernel)
+      reshape_and_cache_rows<<<grid, kThreads, 0, s>>>(a);
+    else if (piece == 16)
+      reshape_and_cache_generic<u32x4><<<grid, kThreads, 0, s>>>(a);
     else if (piece == 4)
-      reshape_and_cache_kernel<uint32_t><<<grid, kThreads, 0, s>>>(a);
+      reshape_and_cache_generic<uint32_t><<<grid, kThreads, 0, s>>>(a);
     else
-      reshape_and_cache_kernel<uint16_t><<<grid, kThreads, 0, s>>>(a);
+      reshape_and_cache_generic<uint16_t><<<grid, kThreads, 0, s>>>(a);
     int32_t rc = check_launch("mi_reshape_and_cache");
     if (rc != MI_OK) return rc;
   }

@@ -198,7 +198,8 @@ def paged_decode_attention(
 
     query: ``[B, H, D]`` bf16 (D contiguous); pools ``[num_blocks, 16, H_kv, D]`` bf16 contiguous;
     block_tables ``[B, max_blocks]`` int64 (null-padded); context_lens ``[B]`` int64 (includes the
-    new token).  Returns ``out`` ``[B, H * D]`` bf16.
+    new token).  Returns ``out`` ``[B, H * D]`` bf16.  ``workspace`` (optional, uint8, reused across
+    calls) holds the split-context partials; it is allocated here when missing or too small.
     """
     device = key_pool.device
     for name, t in (("query", query), ("key_pool", key_pool), ("value_pool", value_pool),
@@ -227,10 +228,15 @@ def paged_decode_attention(
         raise ValueError(f"out must be [B, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
     if batch == 0:
         return out
-    need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size)
-    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=device)
     lib = _native.load()
+    stream = _stream(device)
+    need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size)
+    ws_ptr, ws_bytes = None, 0
+    if need > 0:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=device)
+        _require_gpu("workspace", workspace, device)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     rc = lib.mi_paged_decode_attention(
         out.data_ptr(), out.stride(0),
         query.data_ptr(), query.stride(0), query.stride(1),
@@ -238,9 +244,7 @@ def paged_decode_attention(
         block_tables.data_ptr(), block_tables.stride(0) if batch > 1 else max(max_blocks, 1), max_blocks,
         context_lens.data_ptr(), context_lens.stride(0) if batch > 1 else 1,
         batch, num_heads, num_kv_heads, head_dim, block_size, float(scale),
-        workspace.data_ptr() if (need > 0 and workspace is not None) else None,
-        (workspace.numel() * workspace.element_size()) if (need > 0 and workspace is not None) else 0,
-        _stream(device),
+        ws_ptr, ws_bytes, stream,
     )
     _native.check(rc, "mi_paged_decode_attention")
     return out

@@ -40,10 +40,11 @@ def test_abi_version(native_lib):
 
 
 def test_decode_workspace_size(native_lib):
-    # one partition (<= 16 blocks) needs no workspace; beyond that batch * parts * heads * (128 + 2) floats
-    assert native_lib.mi_paged_decode_workspace_bytes(256, 16, 16, 128, 16) == 0
-    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 128, 16) == 256 * 32 * 16 * 130 * 4
-    assert native_lib.mi_paged_decode_workspace_bytes(4, 17, 16, 128, 16) == 4 * 2 * 16 * 130 * 4
+    # one 512-token partition (<= 32 blocks) needs no workspace; beyond that
+    # batch * parts * heads * (128 + 2) floats
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 32, 16, 128, 16) == 0
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 128, 16) == 256 * 16 * 16 * 130 * 4
+    assert native_lib.mi_paged_decode_workspace_bytes(4, 33, 16, 128, 16) == 4 * 2 * 16 * 130 * 4
 
 
 def _ptrs(n):
@@ -87,8 +88,10 @@ def test_decode_rejects_unsupported_shapes_on_host(native_lib):
     assert call(bs=8) == _native.MI_ERR_UNSUPPORTED
     assert call(heads=24) == _native.MI_ERR_UNSUPPORTED
     assert call(heads=6, kv=3) == _native.MI_ERR_UNSUPPORTED
-    assert call(max_blocks=40) == _native.MI_ERR_WORKSPACE  # three partitions, no workspace
+    assert call(max_blocks=40) == _native.MI_ERR_WORKSPACE  # two partitions, no workspace
     assert b"workspace" in lib.mi_last_error()
+    need = lib.mi_paged_decode_workspace_bytes(2, 40, 16, 128, 16)
+    assert call(max_blocks=40, ws=256, ws_bytes=need - 4) == _native.MI_ERR_WORKSPACE
 
 
 def test_check_maps_status_to_python_errors(native_lib):

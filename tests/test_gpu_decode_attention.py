@@ -33,7 +33,7 @@ def max_abs(a, b):
 
 
 def test_decode_step_workload_matches_oracle(native_lib, device):
-    """Batch 8, contexts U[64, 512] (1-2 partitions), 4096-block pool, permuted tables."""
+    """Batch 8, contexts U[64, 512] (one partition each), 4096-block pool, permuted tables."""
     w = workloads.decode_step(seed=0)
     q, kp, vp = w.query[0], w.pools[0, 0], w.pools[0, 1]
     got = run_kernel(q, kp, vp, w.block_tables, w.context_lens, device)
@@ -61,8 +61,8 @@ def random_case(seed, ctx, kv_heads=8, spare=8):
     return q, kp, vp, workloads.padded(tables), tables
 
 
-@pytest.mark.parametrize("ctx", [[1], [16], [17], [255, 256, 257], [1, 2, 3, 4, 5, 15, 31, 33],
-                                 [513, 1024, 4099], [8192]])
+@pytest.mark.parametrize("ctx", [[1], [16], [17], [255, 256, 257], [511, 512, 513], [1, 2, 3, 4, 5, 15, 31, 33],
+                                 [1023, 1024, 1025, 4099], [8192]])
 def test_context_edges(native_lib, device, ctx):
     """Single token, exact block / partition multiples and one past them, many partitions."""
     q, kp, vp, bt, _ = random_case(len(ctx) * 7 + ctx[0], ctx)
@@ -146,3 +146,14 @@ def test_decode_at_scale_sampled_sequences(native_lib, device):
     vmax = vp.float().abs().max().item()
     assert got.float().abs().max().item() <= vmax + 1e-3
     assert math.isclose(sum(w.context_lens) * 4096, w.kv_bytes_per_layer)
+
+
+def test_repeated_calls_with_changing_batches(native_lib, device):
+    """Back-to-back calls with different batches and context mixes (multi-partition sequences,
+    shared workspace reuse) all match the oracle."""
+    cases = [[700, 1500, 3], [4099, 257], [700, 1500, 3], [300] * 9, [8000]]
+    for seed, ctx in enumerate(cases):
+        q, kp, vp, bt, _ = random_case(100 + seed, ctx)
+        for _ in range(2):
+            got = run_kernel(q, kp, vp, bt, ctx, device)
+            assert max_abs(got, oracle(q, kp, vp, bt, ctx)) <= TOL, f"case {ctx}"
