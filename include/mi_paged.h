@@ -138,6 +138,43 @@ int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, const void*
                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                   float scale, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * Kernel 4 -- chunked-prefill attention on MFMA with the history read from the pool.
+ *
+ * Replaces, for one layer of PagedRunner.run_prefill_chunk_step
+ * (src/mini_infra/worker/paged_runner.py:130-200): the history gather
+ * PagedKVCachePool.gather_blocks (src/mini_infra/worker/paged_kv_cache.py:54-72), the
+ * history/chunk concat of Qwen3Attention.forward (src/mini_infra/model/qwen3.py:325-330), the
+ * visibility mask (paged_runner.py:179-187 with the causal mask of qwen3.py:477-484) and
+ * Qwen3Attention._attend (qwen3.py:219-255).
+ *
+ * Row b of the batch is a chunk of padded_len positions whose last chunk_lens[b] are real
+ * tokens (left padding).  With pad = padded_len - chunk_lens[b] and
+ * nh = min(start_lens[b], 16 * max_history_blocks), query position i >= pad sees
+ *   - history slot k < nh: key_pool/value_pool row (history_blocks[b, k / 16] * 16 + k % 16, g)
+ *   - chunk position j with pad <= j <= i: key/value[b, g, j, :]
+ * for kv head g = h / 2 of query head h; scores as in kernel 3 (bf16 product, bf16 scale),
+ * fp32 softmax and accumulation, bf16 output.  Rows i < pad get zeros.
+ *
+ * out:   [batch, padded_len, num_heads * head_dim] bf16 (row / token element strides).
+ * query: [batch, num_heads, padded_len, head_dim]; key / value: [batch, num_kv_heads,
+ *   padded_len, head_dim] (row / head / token element strides, head_dim contiguous).
+ * history_blocks: [batch, max_history_blocks] int64, row stride history_stride; ids outside
+ *   [0, num_blocks) read block 0.  start_lens / chunk_lens: int64 with element stride lens_stride.
+ * Specialised for head_dim 128, block_size 16, num_heads = 2 * num_kv_heads, num_kv_heads in
+ * {1, 2, 4, 8}; strides multiples of 8 elements and 16-byte aligned tensors.
+ */
+int32_t mi_chunked_prefill_attention(void* out, int64_t out_row_stride, int64_t out_tok_stride, const void* query,
+                                     int64_t query_row_stride, int64_t query_head_stride, int64_t query_tok_stride,
+                                     const void* key, int64_t key_row_stride, int64_t key_head_stride,
+                                     int64_t key_tok_stride, const void* value, int64_t value_row_stride,
+                                     int64_t value_head_stride, int64_t value_tok_stride, const void* key_pool,
+                                     const void* value_pool, int64_t num_blocks, const int64_t* history_blocks,
+                                     int64_t history_stride, int32_t max_history_blocks, const int64_t* start_lens,
+                                     const int64_t* chunk_lens, int64_t lens_stride, int32_t batch,
+                                     int32_t padded_len, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t block_size, float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

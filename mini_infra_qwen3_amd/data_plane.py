@@ -250,5 +250,67 @@ def paged_decode_attention(
     return out
 
 
-def chunked_prefill_attention(*args, **kwargs):  # pragma: no cover - defined with kernel 4
-    raise NotImplementedError("chunked prefill attention kernel is not built yet")
+def chunked_prefill_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    history_blocks: torch.Tensor,
+    start_lens: torch.Tensor,
+    chunk_lens: torch.Tensor,
+    scale: float,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Chunked-prefill attention with the history read from the pool (kernel 4, MFMA).
+
+    query ``[B, H, L, D]``; key / value ``[B, H_kv, L, D]`` (left-padded chunk, D contiguous, any
+    other strides); pools ``[num_blocks, 16, H_kv, D]``; history_blocks ``[B, nb]`` int64 (may have
+    ``nb = 0``); start_lens / chunk_lens ``[B]`` int64 (views with a common stride are fine).
+    Returns ``out`` ``[B, L, H * D]`` bf16; left-padding rows are zero.
+    """
+    device = query.device
+    for name, t in (("query", query), ("key", key), ("value", value), ("key_pool", key_pool),
+                    ("value_pool", value_pool), ("history_blocks", history_blocks), ("start_lens", start_lens),
+                    ("chunk_lens", chunk_lens)):
+        _require_gpu(name, t, device)
+    _require_index("history_blocks", history_blocks, 2)
+    _require_index("start_lens", start_lens, 1)
+    _require_index("chunk_lens", chunk_lens, 1)
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.ndim != 4 or t.dtype != torch.bfloat16 or t.stride(3) != 1:
+            raise ValueError(f"{name} must be 4-d bf16 with the last dim contiguous, got {tuple(t.shape)} {t.dtype}")
+    batch, num_heads, padded_len, head_dim = query.shape
+    num_blocks, block_size, num_kv_heads, _ = key_pool.shape
+    if key.shape != (batch, num_kv_heads, padded_len, head_dim) or value.shape != key.shape:
+        raise ValueError(f"key/value must be [{batch}, {num_kv_heads}, {padded_len}, {head_dim}]")
+    if key_pool.dtype != torch.bfloat16 or value_pool.shape != key_pool.shape or not key_pool.is_contiguous() \
+            or not value_pool.is_contiguous():
+        raise ValueError("pools must be contiguous bf16 with identical shapes")
+    if history_blocks.shape[0] != batch or start_lens.shape[0] != batch or chunk_lens.shape[0] != batch:
+        raise ValueError("history_blocks / start_lens / chunk_lens batch differs from query batch")
+    if history_blocks.stride(1) != 1:
+        history_blocks = history_blocks.contiguous()
+    if batch > 1 and start_lens.stride(0) != chunk_lens.stride(0):
+        start_lens, chunk_lens = start_lens.contiguous(), chunk_lens.contiguous()
+    lens_stride = start_lens.stride(0) if batch > 1 else 1
+    nb = history_blocks.shape[1]
+    if out is None:
+        out = torch.empty((batch, padded_len, num_heads * head_dim), dtype=torch.bfloat16, device=device)
+    elif out.shape != (batch, padded_len, num_heads * head_dim) or out.dtype != torch.bfloat16 or out.stride(2) != 1:
+        raise ValueError(f"out must be [B, L, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
+    if batch == 0 or padded_len == 0:
+        return out
+    rc = _native.load().mi_chunked_prefill_attention(
+        out.data_ptr(), out.stride(0), out.stride(1),
+        query.data_ptr(), query.stride(0), query.stride(1), query.stride(2),
+        key.data_ptr(), key.stride(0), key.stride(1), key.stride(2),
+        value.data_ptr(), value.stride(0), value.stride(1), value.stride(2),
+        key_pool.data_ptr(), value_pool.data_ptr(), num_blocks,
+        history_blocks.data_ptr() if nb else None, history_blocks.stride(0) if nb else 0, nb,
+        start_lens.data_ptr(), chunk_lens.data_ptr(), lens_stride,
+        batch, padded_len, num_heads, num_kv_heads, head_dim, block_size, float(scale),
+        _stream(device),
+    )
+    _native.check(rc, "mi_chunked_prefill_attention")
+    return out

@@ -23,7 +23,7 @@ def declared_symbols() -> set[str]:
 def test_headers_declare_the_entry_points():
     names = declared_symbols()
     assert {"mi_abi_version", "mi_last_error", "mi_reshape_and_cache", "mi_gather_blocks",
-            "mi_paged_decode_attention", "mi_paged_decode_workspace_bytes"} <= names
+            "mi_paged_decode_attention", "mi_paged_decode_workspace_bytes", "mi_chunked_prefill_attention"} <= names
 
 
 def test_library_exports_every_declared_symbol(native_lib):
@@ -100,3 +100,19 @@ def test_check_maps_status_to_python_errors(native_lib):
         _native.check(_native.MI_ERR_INVALID_ARGUMENT, "x")
     with pytest.raises(RuntimeError):
         _native.check(_native.MI_ERR_DEVICE, "x")
+
+
+def test_prefill_rejects_unsupported_shapes_on_host(native_lib):
+    lib = native_lib
+
+    def call(heads=16, kv=8, dim=128, bs=16, tok=128, nb=2, hist=16, hstride=2):
+        return lib.mi_chunked_prefill_attention(16, 2048 * 4, 2048, 16, 16 * 4 * 128, 4 * 128, tok, 16, 8 * 4 * 128,
+                                                4 * 128, tok, 16, 8 * 4 * 128, 4 * 128, tok, 16, 16, 100,
+                                                hist, hstride, nb, 16, 16, 1, 2, 4, heads, kv, dim, bs, 0.1, None)
+
+    assert call(dim=64) == _native.MI_ERR_UNSUPPORTED
+    assert call(bs=32) == _native.MI_ERR_UNSUPPORTED
+    assert call(heads=8) == _native.MI_ERR_UNSUPPORTED
+    assert call(tok=100) == _native.MI_ERR_UNSUPPORTED  # stride not a multiple of 8 elements
+    assert call(hstride=1) == _native.MI_ERR_INVALID_ARGUMENT
+    assert call(hist=None) == _native.MI_ERR_INVALID_ARGUMENT

@@ -1,0 +1,132 @@
+"""Kernel 4 on the GPU: chunked-prefill attention (history from the pool, causal chunk, MFMA)
+against the oracle (the reference's gather + concat + bias + bf16 matmul / fp32 softmax on CPU),
+max-abs <= 2e-2 on the bf16 outputs of real (non-padding) query rows."""
+
+import numpy as np
+import pytest
+import torch
+
+from mini_infra_qwen3_amd import data_plane, workloads
+from oracle import closed_form, torch_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+SCALE = 128 ** -0.5
+
+
+def make_case(seed, starts, lens, width=None, kv_heads=8, spare=4, value_view=False):
+    gen = torch.Generator().manual_seed(seed)
+    width = width or max(lens)
+    batch = len(lens)
+    totals = [s + n for s, n in zip(starts, lens)]
+    num_blocks = 1 + sum(-(-t // 16) for t in totals) + spare
+    tables = workloads.permuted_tables(totals, num_blocks, gen)
+    kp = torch.randn(num_blocks, 16, kv_heads, 128, generator=gen).to(torch.bfloat16)
+    vp = torch.randn(num_blocks, 16, kv_heads, 128, generator=gen).to(torch.bfloat16)
+    q = torch.randn(batch, 2 * kv_heads, width, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(batch, kv_heads, width, 128, generator=gen).to(torch.bfloat16)
+    if value_view:  # as v_proj(...).view(B, L, H, D).transpose(1, 2) produces it
+        v = torch.randn(batch, width, kv_heads, 128, generator=gen).to(torch.bfloat16).transpose(1, 2)
+    else:
+        v = torch.randn(batch, kv_heads, width, 128, generator=gen).to(torch.bfloat16)
+    nb = max(-(-s // 16) for s in starts)
+    hist = torch.zeros((batch, nb), dtype=torch.long)
+    for b, s in enumerate(starts):
+        h = -(-s // 16)
+        hist[b, :h] = torch.tensor(tables[b][:h], dtype=torch.long)
+    return q, k, v, kp, vp, hist
+
+
+def run_gpu(q, k, v, kp, vp, hist, starts, lens, device):
+    return data_plane.chunked_prefill_attention(
+        q.to(device), k.to(device), v.to(device), kp.to(device), vp.to(device), hist.to(device),
+        torch.tensor(starts, device=device), torch.tensor(lens, device=device), SCALE)
+
+
+def check_against_oracle(got, q, k, v, kp, vp, hist, starts, lens):
+    ref = torch_ref.chunked_prefill_attention(q, k, v, (kp, vp), hist, starts, lens, SCALE)
+    width = q.shape[2]
+    got = got.float().cpu()
+    for b, n in enumerate(lens):
+        real = slice(width - n, width)
+        err = (got[b, real] - ref[b, real].float()).abs().max().item()
+        assert err <= TOL, f"row {b}: max-abs {err}"
+        assert not got[b, :width - n].any(), f"row {b}: padding rows must be zero"
+
+
+@pytest.mark.parametrize("starts,lens,width", [
+    ([0], [37], None),                       # no history, odd length, one partial query tile
+    ([0, 0], [64, 130], None),               # tile edges, left padding of row 0
+    ([40, 200, 3], [57, 100, 1], None),      # history of different lengths, tiny chunk
+    ([16, 64, 65], [70, 5, 128], 130),       # history on block / tile edges, extra padding
+])
+def test_matches_oracle(native_lib, device, starts, lens, width):
+    case = make_case(len(lens) + sum(starts), starts, lens, width=width)
+    got = run_gpu(*case, starts, lens, device)
+    check_against_oracle(got, *case, starts, lens)
+
+
+def test_value_as_transposed_view(native_lib, device):
+    starts, lens = [33, 0], [90, 41]
+    case = make_case(7, starts, lens, value_view=True)
+    got = run_gpu(*case, starts, lens, device)
+    check_against_oracle(got, *case, starts, lens)
+
+
+@pytest.mark.parametrize("kv_heads", [1, 2, 4])
+def test_fewer_kv_heads(native_lib, device, kv_heads):
+    starts, lens = [20, 70], [45, 33]
+    case = make_case(kv_heads, starts, lens, kv_heads=kv_heads)
+    got = run_gpu(*case, starts, lens, device)
+    check_against_oracle(got, *case, starts, lens)
+
+
+def test_matches_fp64_textbook(native_lib, device):
+    starts, lens = [24], [20]
+    q, k, v, kp, vp, hist = make_case(11, starts, lens)
+    got = run_gpu(q, k, v, kp, vp, hist, starts, lens, device).float().cpu()
+    hk = kp[hist[0]].reshape(-1, 8, 128)[:24].transpose(0, 1).float().numpy()
+    hv = vp[hist[0]].reshape(-1, 8, 128)[:24].transpose(0, 1).float().numpy()
+    keys = np.concatenate([hk, k[0].float().numpy()], axis=1)
+    values = np.concatenate([hv, v[0].float().numpy()], axis=1)
+    visible = np.zeros((20, 44), dtype=bool)
+    for i in range(20):
+        visible[i, :24] = True
+        visible[i, 24:25 + i] = True
+    ref = closed_form.prefill_attention_fp64(q[0].float().numpy(), keys, values, visible, SCALE)
+    out = got[0].view(20, 16, 128).transpose(0, 1).numpy()
+    assert np.abs(out - ref).max() <= TOL
+
+
+def test_chunked_equals_one_shot(native_lib, device):
+    """Invariant of the reference suite (tests/unit/test_paged_kv_cache.py:210-246) at the
+    attention level: the rows of chunk [s, e) attended with history s from the pool equal the
+    same rows of the whole-prompt attention."""
+    gen = torch.Generator().manual_seed(3)
+    total, s = 300, 176
+    q = torch.randn(1, 16, total, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(1, 8, total, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(1, 8, total, 128, generator=gen).to(torch.bfloat16)
+    whole = run_gpu(q, k, v, torch.zeros(1, 16, 8, 128, dtype=torch.bfloat16),
+                    torch.zeros(1, 16, 8, 128, dtype=torch.bfloat16), torch.zeros((1, 0), dtype=torch.long),
+                    [0], [total], device)
+    # store the first s tokens into pool blocks 5.. in order
+    nbk = -(-s // 16)
+    kp = torch.zeros(5 + nbk, 16, 8, 128, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    kp.view(-1, 8, 128)[5 * 16:5 * 16 + s] = k[0, :, :s].transpose(0, 1)
+    vp.view(-1, 8, 128)[5 * 16:5 * 16 + s] = v[0, :, :s].transpose(0, 1)
+    hist = torch.arange(5, 5 + nbk).view(1, -1)
+    chunk = run_gpu(q[:, :, s:].contiguous(), k[:, :, s:].contiguous(), v[:, :, s:].contiguous(), kp, vp, hist,
+                    [s], [total - s], device)
+    err = (chunk.float() - whole[:, s:].float()).abs().max().item()
+    assert err <= TOL
+
+
+def test_config_shape_chunk_with_history(native_lib, device):
+    """One 2048-token chunk of a 16384-token prompt at chunk index 1 (2048 history tokens)."""
+    starts, lens = [2048], [2048]
+    case = make_case(99, starts, lens, spare=0)
+    got = run_gpu(*case, starts, lens, device)
+    check_against_oracle(got, *case, starts, lens)
