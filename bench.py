@@ -27,6 +27,7 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor datasheet
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 METRIC = "paged decode-attn HBM GB/s (% peak) at B=256; e2e output tok/s Qwen3-0.6B"
 
 
@@ -248,13 +249,56 @@ def bench_gather(steps: int, warmup: int, device: torch.device) -> dict:
             "ms_per_prompt_set": ms, "bytes": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS}
 
 
+# ------------------------------------------------------------------------- chunked prefill
+def bench_prefill(steps: int, warmup: int, device: torch.device) -> dict:
+    """4 prompts x 16384 tokens, 2048-token chunks, one layer: 8 chunk steps, each one launch over the
+    4 prompts (history 2048 c read from the pool through the block table, causal inside the chunk)."""
+    from mini_infra_qwen3_amd import data_plane, workloads as wl
+
+    w = wl.chunked_prefill(seed=0)
+    gen = torch.Generator(device=device).manual_seed(3)
+    pools = torch.randn((2, w.num_blocks, wl.BLOCK_SIZE, wl.NUM_KV_HEADS, wl.HEAD_DIM), generator=gen,
+                        device=device).to(torch.bfloat16)
+    L = w.chunk_len
+    q = torch.randn((w.num_prompts, wl.NUM_HEADS, L, wl.HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn((w.num_prompts, wl.NUM_KV_HEADS, L, wl.HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn((w.num_prompts, wl.NUM_KV_HEADS, L, wl.HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+    tables = torch.tensor(w.tables, dtype=torch.long, device=device)
+    lens = torch.full((w.num_prompts,), L, dtype=torch.long, device=device)
+    out = torch.empty((w.num_prompts, L, wl.NUM_HEADS * wl.HEAD_DIM), dtype=torch.bfloat16, device=device)
+    steps_c = []
+    for c in range(w.num_chunks):
+        nb = c * L // wl.BLOCK_SIZE
+        steps_c.append((tables[:, :nb], torch.full((w.num_prompts,), c * L, dtype=torch.long, device=device)))
+
+    def layer():
+        for hist, starts in steps_c:
+            data_plane.chunked_prefill_attention(q, k, v, pools[0], pools[1], hist, starts, lens, wl.SCALE, out=out)
+
+    timer = EventTimer()
+    for _ in range(warmup):
+        layer()
+    for _ in range(steps):
+        timer.start()
+        layer()
+        timer.stop()
+    ms = timer.mean_ms()
+    n = w.prompt_len
+    flops = w.num_prompts * 2 * 2 * wl.NUM_HEADS * wl.HEAD_DIM * n * (n + 1) / 2  # QK^T and PV, causal pairs
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "chunked prefill attention, 4 prompts x 16384 tokens, 2048-token chunks, one layer "
+                        "(8 launches, history from the pool)",
+            "ms_per_layer": ms, "tflop_per_layer": flops / 1e12, "achieved_TFLOPs": tflops,
+            "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "frac": tflops / MFMA_BF16_PEAK_TFLOPS}
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["decode", "all"], default="all")
+    parser.add_argument("--only", choices=["decode", "prefill", "copy", "all"], default="all")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of this path "
@@ -269,6 +313,21 @@ def main() -> int:
     _native.load()
     log(f"device {torch.cuda.get_device_name(device)}; library {_native.LIBRARY_PATH}")
 
+    if args.only == "copy":
+        # Calibration for HBM traffic counters: a plain device copy of known size (reads and
+        # writes exactly 1 GiB per launch), profiled with the same counters as the kernels.
+        src = torch.ones(1 << 30, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(max(args.steps, 1)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": src.numel(), "launches": max(args.steps, 1)}), flush=True)
+        return 0
+    if args.only == "prefill":
+        res = bench_prefill(args.steps, args.warmup, device)
+        log(f"chunked prefill: {res['ms_per_layer']:.2f} ms/layer, {res['achieved_TFLOPs']:.1f} TFLOP/s")
+        print(json.dumps(res), flush=True)
+        return 0
     dec = bench_decode(args.steps, args.warmup, device)
     log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value']:.1f} GB/s; attention launch "
         f"{dec['attn_launch_ms']:.3f} ms = {dec['roofline']['achieved']:.1f} GB/s "
@@ -290,6 +349,10 @@ def main() -> int:
         torch.cuda.empty_cache()
         kernels["gather"] = bench_gather(max(args.steps // 4, 3), 1, device)
         log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s")
+        torch.cuda.empty_cache()
+        kernels["chunked_prefill"] = bench_prefill(max(args.steps // 4, 3), 1, device)
+        log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "
+            f"{kernels['chunked_prefill']['achieved_TFLOPs']:.1f} TFLOP/s")
         torch.cuda.empty_cache()
 
     line = {

@@ -26,8 +26,11 @@
 //  * O^T = V^T P^T: the probabilities of a 32-key step are already in the B-operand lanes if
 //    the MFMA's k index is read as key 16 (k' / 4) + 4 (lane / 16) + k' % 4; the A operand
 //    (V^T) is read from LDS with the same permutation (two 8-byte reads).
-//  * Scores keep the reference's bf16 rounding points (bf16 product, bf16 scale); softmax
-//    and accumulation are fp32; lazy rescaling of the running max as in the decode kernel.
+//  * Softmax and accumulation are fp32 with lazy rescaling of the running max as in the decode
+//    kernel.  Scores keep the reference's bf16 rounding points (bf16 product, then bf16 product
+//    with the scale), done on pairs with the packed bf16 convert (~4 VALU ops per score):
+//    for N(0,1) inputs those roundings move logits by ~1e-2, so dropping them
+//    (MI_PREFILL_EXACT_SCORES=0, scale folded into the exp2 FMA) leaves the 2e-2 parity band.
 #include "mi_common.h"
 
 namespace mi {
@@ -41,8 +44,13 @@ constexpr int kKTile = 64;                 // keys per KV tile
 constexpr int kKStride = kHeadDim + 8;     // LDS row of K (elements): 272 B
 constexpr int kVStride = kKTile + 4;       // LDS row of V^T (elements): 136 B
 constexpr int kThreads = 256;
+constexpr int kMaxHistoryBlocks = 16384;   // history table staged in LDS: 64 KiB at most (256k tokens)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;
+#ifndef MI_PREFILL_EXACT_SCORES
+#define MI_PREFILL_EXACT_SCORES 1
+#endif
+constexpr bool kExactScores = MI_PREFILL_EXACT_SCORES != 0;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -71,9 +79,25 @@ struct PrefillArgs {
   float scale;
 };
 
-__device__ __forceinline__ float score_log2(float dot, float scale) {
-  const float s = static_cast<float>(static_cast<__bf16>(static_cast<float>(static_cast<__bf16>(dot)) * scale));
-  return s * kLog2e;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// bf16 rounding of two floats with one packed convert; the results are exact fp32 values.
+__device__ __forceinline__ void round_bf16_pair(float& x, float& y) {
+  const uint32_t pk = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
+  x = __uint_as_float(pk << 16);
+  y = __uint_as_float(pk & 0xffff0000u);
+}
+
+// The reference's scores: bf16(bf16(q . k) * scale) (src/mini_infra/model/qwen3.py:243), in place.
+__device__ __forceinline__ void reference_scores(f32x4& v, float scale) {
+  float a = v[0], b = v[1], c = v[2], d = v[3];
+  round_bf16_pair(a, b);
+  round_bf16_pair(c, d);
+  a *= scale; b *= scale; c *= scale; d *= scale;
+  round_bf16_pair(a, b);
+  round_bf16_pair(c, d);
+  v = f32x4{a, b, c, d};
 }
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
@@ -84,6 +108,7 @@ template <int kKvHeads>
 __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const PrefillArgs a) {
   __shared__ __align__(16) uint16_t sK[2][kKTile * kKStride];
   __shared__ __align__(16) uint16_t sV[2][kHeadDim * kVStride];
+  extern __shared__ int s_hblk[];  // [ceil(nh / 16)] history block ids of this row (dynamic LDS)
 
   const int b = blockIdx.z;
   const int g = blockIdx.y;
@@ -140,66 +165,79 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   const int c_hi = last_q / kKTile;
   const int n_tiles = n_hist_tiles + (c_hi - c_lo + 1);
 
-  // ---- tile loader: thread owns 4 K pieces (key, 8 dims) and 2 V key-pairs (2 keys, 8 dims)
-  uint4 kreg[4], vreg[2][2];
-  auto src_row = [&](int t, int key, bool is_value, bool& ok) -> const uint16_t* {
-    if (t < n_hist_tiles) {
-      const int kpos = t * kKTile + key;
-      ok = kpos < nh;
-      if (!ok) return nullptr;
-      int64_t bid = a.history_blocks[b * a.history_stride + kpos / kBlockSize];
-      if (bid < 0 || bid >= a.num_blocks) bid = 0;
-      const uint16_t* pool = is_value ? a.value_pool : a.key_pool;
-      return pool + ((bid * kBlockSize + kpos % kBlockSize) * kKvHeads + g) * kHeadDim;
-    }
-    const int j = (c_lo + t - n_hist_tiles) * kKTile + key;
-    ok = j < L;
-    if (!ok) return nullptr;
-    return is_value ? a.value + b * a.v_row + g * a.v_head + j * a.v_tok
-                    : a.key + b * a.k_row + g * a.k_head + j * a.k_tok;
-  };
-  auto load_tile = [&](int t) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int c = tid + kThreads * kk;
-      bool ok;
-      const uint16_t* p = src_row(t, c >> 4, false, ok);
-      kreg[kk] = ok ? *reinterpret_cast<const uint4*>(p + (c & 15) * 8) : uint4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int it = tid + kThreads * kk;
-      const int kp = it >> 4, dg = it & 15;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        bool ok;
-        const uint16_t* p = src_row(t, 2 * kp + e, true, ok);
-        vreg[kk][e] = ok ? *reinterpret_cast<const uint4*>(p + dg * 8) : uint4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int c = tid + kThreads * kk;
-      *reinterpret_cast<uint4*>(&sK[buf][(c >> 4) * kKStride + (c & 15) * 8]) = kreg[kk];
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int it = tid + kThreads * kk;
-      const int kp = it >> 4, dg = it & 15;
-      const uint32_t x[4] = {vreg[kk][0].x, vreg[kk][0].y, vreg[kk][0].z, vreg[kk][0].w};
-      const uint32_t y[4] = {vreg[kk][1].x, vreg[kk][1].y, vreg[kk][1].z, vreg[kk][1].w};
-#pragma unroll
-      for (int d2 = 0; d2 < 4; ++d2) {
-        // dims 2 d2 and 2 d2 + 1 of keys (2 kp, 2 kp + 1) -> two V^T words
-        const uint32_t lo = perm(y[d2], x[d2], 0x05040100u);
-        const uint32_t hi = perm(y[d2], x[d2], 0x07060302u);
-        *reinterpret_cast<uint32_t*>(&sV[buf][(dg * 8 + 2 * d2) * kVStride + 2 * kp]) = lo;
-        *reinterpret_cast<uint32_t*>(&sV[buf][(dg * 8 + 2 * d2 + 1) * kVStride + 2 * kp]) = hi;
-      }
-    }
-  };
+  // ---- tile loader.  Thread tid owns K pieces (key 16 kk + tid / 16, dims 8 (tid % 16) .. +8),
+  // kk = 0..3, and V key pairs (keys 32 kk + 2 (tid / 16) + {0, 1}, same dims), kk = 0..1.  In a
+  // history tile K piece kk lies in pool block kk of the tile and V pair kk in block
+  // 2 kk + (tid / 128): block ids are uniform, read from LDS where the workgroup staged its
+  // history table once.  Every load reads valid memory: block indices are clamped to the last
+  // history block and chunk positions to L - 1; keys past the context are masked later.
+  const int tkey = tid >> 4;
+  const int tdim = (tid & 15) * 8;
+  const int vhalf = tid >> 7;
+  const int nhb = (nh + kBlockSize - 1) / kBlockSize;
+  for (int i = tid; i < nhb; i += kThreads) {
+    const int64_t x = a.history_blocks[b * a.history_stride + i];
+    s_hblk[i] = (x < 0 || x >= a.num_blocks) ? 0 : static_cast<int>(x);
+  }
+  constexpr int64_t kBlkElems = static_cast<int64_t>(kBlockSize) * kKvHeads * kHeadDim;
+  const int64_t k_hist_off = static_cast<int64_t>(tkey * kKvHeads + g) * kHeadDim + tdim;
+  const int voff = (2 * tkey) % kBlockSize;
+  const int64_t v_hist_off0 = static_cast<int64_t>(voff * kKvHeads + g) * kHeadDim + tdim;
+  const int64_t v_hist_off1 = v_hist_off0 + kKvHeads * kHeadDim;
+  const uint16_t* k_chunk = a.key + b * a.k_row + g * a.k_head + tdim;
+  const uint16_t* v_chunk = a.value + b * a.v_row + g * a.v_head + tdim;
+
+  u32x4 kreg[4], vreg[2][2];
+#define MI_LOAD_TILE(T)                                                                                         \
+  do {                                                                                                         \
+    const int t_ = (T);                                                                                        \
+    if (t_ < n_hist_tiles) {                                                                                   \
+      int blk[4];                                                                                              \
+      _Pragma("unroll") for (int j = 0; j < 4; ++j)                                                            \
+          blk[j] = __builtin_amdgcn_readfirstlane(s_hblk[min(t_ * (kKTile / kBlockSize) + j, nhb - 1)]);       \
+      _Pragma("unroll") for (int kk = 0; kk < 4; ++kk)                                                         \
+          kreg[kk] = *reinterpret_cast<const u32x4*>(a.key_pool + blk[kk] * kBlkElems + k_hist_off);           \
+      _Pragma("unroll") for (int kk = 0; kk < 2; ++kk) {                                                       \
+        const int64_t vb = static_cast<int64_t>(vhalf ? blk[2 * kk + 1] : blk[2 * kk]) * kBlkElems;            \
+        vreg[kk][0] = *reinterpret_cast<const u32x4*>(a.value_pool + vb + v_hist_off0);                        \
+        vreg[kk][1] = *reinterpret_cast<const u32x4*>(a.value_pool + vb + v_hist_off1);                        \
+      }                                                                                                        \
+    } else {                                                                                                   \
+      const int key0 = (c_lo + t_ - n_hist_tiles) * kKTile;                                                   \
+      if (key0 + kKTile <= L) {                                                                                \
+        _Pragma("unroll") for (int kk = 0; kk < 4; ++kk)                                                       \
+            kreg[kk] = *reinterpret_cast<const u32x4*>(k_chunk + (key0 + 16 * kk + tkey) * a.k_tok);           \
+        _Pragma("unroll") for (int kk = 0; kk < 2; ++kk)                                                       \
+          _Pragma("unroll") for (int e = 0; e < 2; ++e)                                                        \
+            vreg[kk][e] = *reinterpret_cast<const u32x4*>(v_chunk + (key0 + 32 * kk + 2 * tkey + e) * a.v_tok); \
+      } else {                                                                                                 \
+        _Pragma("unroll") for (int kk = 0; kk < 4; ++kk)                                                       \
+            kreg[kk] = *reinterpret_cast<const u32x4*>(k_chunk + min(key0 + 16 * kk + tkey, L - 1) * a.k_tok); \
+        _Pragma("unroll") for (int kk = 0; kk < 2; ++kk)                                                       \
+          _Pragma("unroll") for (int e = 0; e < 2; ++e)                                                        \
+            vreg[kk][e] = *reinterpret_cast<const u32x4*>(                                                     \
+                v_chunk + min(key0 + 32 * kk + 2 * tkey + e, L - 1) * a.v_tok);                                \
+      }                                                                                                        \
+    }                                                                                                          \
+  } while (0)
+
+#define MI_STORE_TILE(BUF)                                                                                     \
+  do {                                                                                                         \
+    const int buf_ = (BUF);                                                                                    \
+    _Pragma("unroll") for (int kk = 0; kk < 4; ++kk)                                                           \
+        *reinterpret_cast<u32x4*>(&sK[buf_][(16 * kk + tkey) * kKStride + tdim]) = kreg[kk];                   \
+    _Pragma("unroll") for (int kk = 0; kk < 2; ++kk) {                                                         \
+      const int key = 32 * kk + 2 * tkey;                                                                      \
+      const uint32_t x[4] = {vreg[kk][0][0], vreg[kk][0][1], vreg[kk][0][2], vreg[kk][0][3]};                  \
+      const uint32_t y[4] = {vreg[kk][1][0], vreg[kk][1][1], vreg[kk][1][2], vreg[kk][1][3]};                  \
+      _Pragma("unroll") for (int d2 = 0; d2 < 4; ++d2) {                                                       \
+        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2) * kVStride + key]) =                            \
+            perm(y[d2], x[d2], 0x05040100u);                                                                   \
+        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2 + 1) * kVStride + key]) =                        \
+            perm(y[d2], x[d2], 0x07060302u);                                                                   \
+      }                                                                                                        \
+    }                                                                                                          \
+  } while (0)
 
   f32x4 oacc[8][2];
 #pragma unroll
@@ -210,15 +248,16 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   float l_part[2] = {0.0f, 0.0f};
   const float scale = a.scale;
 
+  __syncthreads();  // s_hblk ready
   if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
+    MI_LOAD_TILE(0);
+    MI_STORE_TILE(0);
   }
   __syncthreads();
 
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
-    if (t + 1 < n_tiles) load_tile(t + 1);
+    if (t + 1 < n_tiles) MI_LOAD_TILE(t + 1);
 
     // ---- S^T = K Q^T for 64 keys x 32 queries
     f32x4 sacc[4][2];
@@ -246,29 +285,35 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     } else {
       need_mask = key0 + kKTile - 1 > qw0 || key0 < pad || qw0 < pad || qw0 + 31 >= L;
     }
+    // Exact form: scores rounded like the reference, log2(e) applied inside the exp2 FMA below;
+    // fast form: raw dots with scale * log2(e) there (max commutes with a positive factor).
+    if constexpr (kExactScores) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sacc[mt][nt][i] = score_log2(sacc[mt][nt][i], scale);
+        for (int nt = 0; nt < 2; ++nt) reference_scores(sacc[mt][nt], scale);
+    }
     if (need_mask) {
+      // Bitwise (not short-circuit) conditions keep the edge-tile path free of branches.
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const int qi = qw0 + 16 * nt + ql;
-        const bool row_ok = qi >= pad && qi < L;
+        const bool row_ok = (qi >= pad) & (qi < L);
+        const int lo = is_hist ? 0 : pad;        // visible key range [lo, hi] of this query
+        const int hi = is_hist ? nh - 1 : qi;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int kpos = key0 + mt * 16 + 4 * gq + i;
-            const bool vis = row_ok && (is_hist ? kpos < nh : (kpos >= pad && kpos <= qi));
+            const bool vis = row_ok & (kpos >= lo) & (kpos <= hi);
             sacc[mt][nt][i] = vis ? sacc[mt][nt][i] : -INFINITY;
           }
       }
     }
 
     // ---- online softmax per query column (lanes ql, ql+16, ql+32, ql+48 hold its 64 keys)
+    const float to_log2 = kExactScores ? kLog2e : scale * kLog2e;
     float mx[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
@@ -279,7 +324,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
         for (int i = 0; i < 4; ++i) v = fmaxf(v, sacc[mt][nt][i]);
       v = fmaxf(v, __shfl_xor(v, 16));
       v = fmaxf(v, __shfl_xor(v, 32));
-      mx[nt] = v;
+      mx[nt] = v * to_log2;
     }
     const bool grow = mx[0] > m_run[0] + kRescaleSlack || mx[1] > m_run[1] + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
@@ -302,7 +347,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(sacc[mt][nt][i] - ref);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[mt][nt][i], to_log2, -ref));
           sacc[mt][nt][i] = p;
           sum += p;
         }
@@ -331,7 +376,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
       }
     }
 
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
+    if (t + 1 < n_tiles) MI_STORE_TILE(buf ^ 1);
     __syncthreads();
   }
 
@@ -421,13 +466,18 @@ extern "C" int32_t mi_chunked_prefill_attention(
   a.padded_len = padded_len;
   a.scale = scale;
 
+  if (num_blocks > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: pool too large");
+  if (max_history_blocks > kMaxHistoryBlocks)
+    return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: history of %d blocks exceeds %d", max_history_blocks,
+                kMaxHistoryBlocks);
   dim3 grid((padded_len + kQTile - 1) / kQTile, num_kv_heads, batch);
+  const size_t lds = sizeof(int) * static_cast<size_t>(max_history_blocks > 0 ? max_history_blocks : 1);
   hipStream_t s = as_stream(stream);
   switch (num_kv_heads) {
-    case 1: chunked_prefill_kernel<1><<<grid, kThreads, 0, s>>>(a); break;
-    case 2: chunked_prefill_kernel<2><<<grid, kThreads, 0, s>>>(a); break;
-    case 4: chunked_prefill_kernel<4><<<grid, kThreads, 0, s>>>(a); break;
-    default: chunked_prefill_kernel<8><<<grid, kThreads, 0, s>>>(a); break;
+    case 1: chunked_prefill_kernel<1><<<grid, kThreads, lds, s>>>(a); break;
+    case 2: chunked_prefill_kernel<2><<<grid, kThreads, lds, s>>>(a); break;
+    case 4: chunked_prefill_kernel<4><<<grid, kThreads, lds, s>>>(a); break;
+    default: chunked_prefill_kernel<8><<<grid, kThreads, lds, s>>>(a); break;
   }
   return check_launch("mi_chunked_prefill_attention");
 }
