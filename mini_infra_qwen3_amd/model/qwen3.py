@@ -1,0 +1,289 @@
+"""Qwen3 with the paged-KV data plane in its attention.
+
+Parameter names, shapes and the dense numerics (RMSNorm in fp32, bf16 RoPE tables, q/k norm,
+SwiGLU, tied lm_head) follow the reference model (src/mini_infra/model/qwen3.py:55-625), so its
+state_dict loads unchanged.  The attention differs in how it reaches K/V:
+
+* decode (``PagedAttentionMetadata``, one token per sequence): the new K/V rows go into the pool
+  through the reshape-and-cache kernel, then paged GQA decode attention reads the context from
+  the pool (replaces qwen3.py:257-292 + :219-255, no gather, no repeat_interleave);
+* prefill (``PagedPrefillMetadata``, or no metadata for a whole left-padded prompt): the MFMA
+  chunked-prefill kernel attends causally within the chunk and reads the history straight from
+  the pool through the block table (replaces the gather + concat + _attend chain).
+
+Dense GEMMs (projections, MLP, lm_head) stay on PyTorch-ROCm.
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from mini_infra_qwen3_amd import data_plane
+from mini_infra_qwen3_amd.model.config import Qwen3Config
+
+PastKeyValue = tuple[torch.Tensor, torch.Tensor]
+
+
+class PagedAttentionMetadata(NamedTuple):
+    """Paged decode step addressing (reference qwen3.py:27-42).
+
+    slot_mapping ``[B]``, block_tables ``[B, max_blocks]`` (null-padded), context_lens ``[B]`` (new
+    token included) -- int64, possibly column views of one packed tensor; kv_pools per layer.
+    """
+
+    slot_mapping: torch.Tensor
+    block_tables: torch.Tensor
+    context_lens: torch.Tensor
+    kv_pools: tuple[PastKeyValue, ...] = ()
+
+
+class PagedPrefillMetadata(NamedTuple):
+    """Chunked-prefill addressing: row b is a left-padded chunk of ``chunk_lens[b]`` tokens that
+    starts at logical position ``start_lens[b]``; its history is the first ``start_lens[b]`` slots of
+    ``history_block_tables[b]`` (``[B, nb]`` int64, null-padded; ``nb`` may be 0)."""
+
+    history_block_tables: torch.Tensor
+    start_lens: torch.Tensor
+    chunk_lens: torch.Tensor
+    kv_pools: tuple[PastKeyValue, ...] = ()
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) in fp32, cast back, times weight (reference qwen3.py:55-78)."""
+
+    def __init__(self, hidden_size: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        dtype = x.dtype
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return self.weight * xf.to(dtype)
+
+
+class RotaryEmbedding(nn.Module):
+    """cos / sin tables for positions, fp32 angles cast to the model dtype (reference qwen3.py:81-109)."""
+
+    def __init__(self, head_dim: int, rope_theta: float):
+        super().__init__()
+        self.head_dim = head_dim
+        self.rope_theta = rope_theta
+        self.register_buffer("inv_freq", self._frequencies("cpu"), persistent=False)
+
+    def _frequencies(self, device) -> torch.Tensor:
+        exponents = torch.arange(0, self.head_dim, 2, dtype=torch.float32, device=device) / self.head_dim
+        return 1.0 / (self.rope_theta ** exponents)
+
+    def _apply(self, fn, *args, **kwargs):
+        # The frequencies stay fp32 whatever dtype the model is cast to: a bf16 inv_freq moves the
+        # angles of late positions by whole radians (the reference loader restores the fp32 buffer
+        # after model.to(dtype): src/mini_infra/model/loader.py:65-68).
+        super()._apply(fn, *args, **kwargs)
+        self.inv_freq = self._frequencies(self.inv_freq.device)
+        return self
+
+    def forward(self, position_ids: torch.Tensor, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+        freqs = position_ids.float().unsqueeze(-1) * self.inv_freq
+        emb = torch.cat((freqs, freqs), dim=-1)
+        return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+class Qwen3Attention(nn.Module):
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.num_heads = config.num_attention_heads
+        self.num_kv_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim
+        self.scaling = config.head_dim ** -0.5
+        self.q_proj = nn.Linear(config.hidden_size, self.num_heads * self.head_dim, bias=False)
+        self.k_proj = nn.Linear(config.hidden_size, self.num_kv_heads * self.head_dim, bias=False)
+        self.v_proj = nn.Linear(config.hidden_size, self.num_kv_heads * self.head_dim, bias=False)
+        self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, bias=False)
+        self.q_norm = RMSNorm(config.head_dim, config.rms_norm_eps)
+        self.k_norm = RMSNorm(config.head_dim, config.rms_norm_eps)
+
+    def _project(self, hidden: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+        """q ``[B, H, L, D]`` and k ``[B, Hkv, L, D]`` (normed, rotated, contiguous), v ``[B, Hkv, L, D]``
+        (a transpose view), as the reference produces them (qwen3.py:182-217)."""
+        batch, length, _ = hidden.shape
+        q = self.q_norm(self.q_proj(hidden).view(batch, length, self.num_heads, self.head_dim)).transpose(1, 2)
+        k = self.k_norm(self.k_proj(hidden).view(batch, length, self.num_kv_heads, self.head_dim)).transpose(1, 2)
+        v = self.v_proj(hidden).view(batch, length, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+        q = q * cos + _rotate_half(q) * sin
+        k = k * cos + _rotate_half(k) * sin
+        return q, k, v
+
+    def forward(self, hidden, cos, sin, kv_pool: PastKeyValue, metadata, workspace=None):
+        batch, length, _ = hidden.shape
+        q, k, v = self._project(hidden, cos, sin)
+        key_pool, value_pool = kv_pool
+        if isinstance(metadata, PagedAttentionMetadata):
+            data_plane.reshape_and_cache([k], [v], metadata.slot_mapping, [key_pool], [value_pool])
+            out = data_plane.paged_decode_attention(
+                q.view(batch, self.num_heads, self.head_dim), key_pool, value_pool, metadata.block_tables,
+                metadata.context_lens, self.scaling, workspace=workspace,
+            ).view(batch, 1, -1)
+            present = kv_pool
+        else:
+            out = data_plane.chunked_prefill_attention(
+                q, k, v, key_pool, value_pool, metadata.history_block_tables, metadata.start_lens,
+                metadata.chunk_lens, self.scaling,
+            )
+            present = (k, v)
+        return self.o_proj(out), present
+
+
+class Qwen3MLP(nn.Module):
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
+        self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class Qwen3DecoderLayer(nn.Module):
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.self_attn = Qwen3Attention(config)
+        self.mlp = Qwen3MLP(config)
+        self.input_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
+
+    def forward(self, hidden, cos, sin, kv_pool, metadata, workspace=None):
+        attn, present = self.self_attn(self.input_layernorm(hidden), cos, sin, kv_pool, metadata, workspace)
+        hidden = hidden + attn
+        hidden = hidden + self.mlp(self.post_attention_layernorm(hidden))
+        return hidden, present
+
+
+class Qwen3Model(nn.Module):
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        config.validate()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([Qwen3DecoderLayer(config) for _ in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, config.rms_norm_eps)
+        self.rotary_emb = RotaryEmbedding(config.head_dim, config.rope_theta)
+        # Stand-in pool for prefill without history (the kernel reads no pool rows then).
+        self.register_buffer(
+            "_empty_pool", torch.zeros(1, 16, config.num_key_value_heads, config.head_dim), persistent=False
+        )
+
+    def forward(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
+                position_ids: torch.Tensor | None = None,
+                attn_metadata: PagedAttentionMetadata | PagedPrefillMetadata | None = None):
+        """Returns (final hidden states ``[B, L, hidden]``, per-layer present K/V).
+
+        Decode (``PagedAttentionMetadata``): input_ids / position_ids ``[B, 1]``.  Prefill: a
+        left-padded ``[B, L]`` chunk; without metadata, ``attention_mask`` (left padding, True on
+        real tokens) gives the chunk lengths and there is no history.
+        """
+        if input_ids.ndim != 2 or input_ids.shape[1] < 1:
+            raise ValueError("input_ids must be a non-empty [batch, sequence] tensor")
+        batch, length = input_ids.shape
+        device = input_ids.device
+        hidden = self.embed_tokens(input_ids)
+        workspace = None
+        if isinstance(attn_metadata, PagedAttentionMetadata):
+            if length != 1:
+                raise ValueError("paged decode takes input_ids of shape [batch, 1]")
+            if position_ids is None:
+                raise ValueError("paged decode needs position_ids")
+            if len(attn_metadata.kv_pools) != len(self.layers):
+                raise ValueError("kv_pools has a different number of layers than the model")
+            metadata = attn_metadata
+            pools = attn_metadata.kv_pools
+            need = data_plane.paged_decode_workspace_bytes(batch, metadata.block_tables.shape[1],
+                                                          self.config.num_attention_heads, self.config.head_dim,
+                                                          pools[0][0].shape[1])
+            if need:
+                workspace = torch.empty(need, dtype=torch.uint8, device=device)
+        else:
+            if attn_metadata is None:
+                if attention_mask is None:
+                    chunk_lens = torch.full((batch,), length, dtype=torch.long, device=device)
+                else:
+                    chunk_lens = attention_mask.to(device=device).long().sum(dim=-1)
+                pool = self._empty_pool.to(hidden.dtype)
+                metadata = PagedPrefillMetadata(torch.zeros((batch, 0), dtype=torch.long, device=device),
+                                                torch.zeros(batch, dtype=torch.long, device=device), chunk_lens)
+                pools = tuple((pool, pool) for _ in self.layers)
+            elif isinstance(attn_metadata, PagedPrefillMetadata):
+                metadata = attn_metadata
+                pools = attn_metadata.kv_pools
+                if len(pools) != len(self.layers):
+                    raise ValueError("kv_pools has a different number of layers than the model")
+            else:
+                raise NotImplementedError(f"{type(attn_metadata).__name__}: only the paged path is built here")
+            if position_ids is None:  # real tokens count from start, left padding sits at position 0
+                offset = torch.arange(length, device=device).unsqueeze(0) - (length - metadata.chunk_lens).unsqueeze(1)
+                position_ids = torch.where(offset >= 0, offset + metadata.start_lens.unsqueeze(1), 0)
+        cos, sin = self.rotary_emb(position_ids, hidden.dtype)
+        presents: list[PastKeyValue] = []
+        for layer, kv_pool in zip(self.layers, pools):
+            hidden, present = layer(hidden, cos, sin, kv_pool, metadata, workspace)
+            presents.append(present)
+        return self.norm(hidden), presents
+
+
+class Qwen3ForCausalLM(nn.Module):
+    def __init__(self, config: Qwen3Config):
+        super().__init__()
+        self.config = config
+        self.model = Qwen3Model(config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embed_tokens.weight
+
+    def forward(self, input_ids, attention_mask=None, position_ids=None, attn_metadata=None,
+                last_logits_only: bool = False):
+        """(logits, present K/V).  ``last_logits_only`` projects only the last position (``[B, 1, V]``):
+        greedy sampling reads nothing else (reference sampler.py:9-23)."""
+        hidden, presents = self.model(input_ids, attention_mask, position_ids, attn_metadata)
+        if last_logits_only:
+            hidden = hidden[:, -1:, :]
+        return self.lm_head(hidden), presents
+
+
+def init_random_(model: Qwen3ForCausalLM, seed: int, std: float = 0.02, untied_head_seed: int | None = None) -> None:
+    """Random weights: every matrix N(0, std) from one seeded generator, norms at 1.  With
+    ``untied_head_seed`` the lm_head gets its own N(0, 1) draw (a model whose greedy output depends
+    on the context, as the reference's diverse test model: tests/unit/conftest.py:13-25)."""
+    gen = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith("norm.weight") or "layernorm" in name:
+                p.fill_(1.0)
+            else:
+                p.copy_(torch.randn(p.shape, generator=gen) * std)
+        if untied_head_seed is not None:
+            head_gen = torch.Generator().manual_seed(untied_head_seed)
+            model.lm_head.weight = nn.Parameter(
+                torch.randn(model.lm_head.weight.shape, generator=head_gen).to(model.lm_head.weight.device,
+                                                                               model.lm_head.weight.dtype))
+
+
+__all__ = [
+    "PagedAttentionMetadata",
+    "PagedPrefillMetadata",
+    "Qwen3Attention",
+    "Qwen3ForCausalLM",
+    "Qwen3Model",
+    "init_random_",
+]

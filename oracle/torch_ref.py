@@ -17,10 +17,11 @@ NULL_BLOCK_ID = 0
 
 # ----------------------------------------------------------------------------- pool ops
 def make_pools(num_layers: int, num_blocks: int, block_size: int, num_kv_heads: int, head_dim: int,
-               dtype: torch.dtype = torch.bfloat16) -> list[tuple[torch.Tensor, torch.Tensor]]:
+               dtype: torch.dtype = torch.bfloat16, device="cpu") -> list[tuple[torch.Tensor, torch.Tensor]]:
     """Zero-filled per-layer (K, V) pools. src/mini_infra/worker/paged_kv_cache.py:23-41."""
     shape = (num_blocks, block_size, num_kv_heads, head_dim)
-    return [(torch.zeros(shape, dtype=dtype), torch.zeros(shape, dtype=dtype)) for _ in range(num_layers)]
+    return [(torch.zeros(shape, dtype=dtype, device=device), torch.zeros(shape, dtype=dtype, device=device))
+            for _ in range(num_layers)]
 
 
 def write_prefill(kv_pools, prefill_cache, token_rows, token_positions, slot_mapping) -> None:
@@ -99,10 +100,12 @@ def attend(query, key, value, attn_bias, scaling: float) -> torch.Tensor:
     groups = heads // key.shape[1]
     k = repeat_kv(key, groups)
     v = repeat_kv(value, groups)
-    scores = torch.matmul(query, k.transpose(2, 3)) * scaling
+    # Operands made contiguous first (same values; bf16 batched products on a transposed right
+    # operand are avoided on ROCm).
+    scores = torch.matmul(query.contiguous(), k.transpose(2, 3).contiguous()) * scaling
     scores = scores + attn_bias
     probs = F.softmax(scores, dim=-1, dtype=torch.float32).to(query.dtype)
-    out = torch.matmul(probs, v)
+    out = torch.matmul(probs, v.contiguous())
     return out.transpose(1, 2).contiguous().view(batch, q_len, -1)
 
 
@@ -111,9 +114,9 @@ def paged_bias(block_tables: torch.Tensor, context_lens: torch.Tensor, block_siz
     """Additive decode bias ``[B, 1, 1, max_len]``. src/mini_infra/model/qwen3.py:513-528."""
     batch = block_tables.shape[0]
     max_len = block_tables.shape[1] * block_size
-    positions = torch.arange(max_len)
+    positions = torch.arange(max_len, device=block_tables.device)
     allowed = (positions.unsqueeze(0) < context_lens.unsqueeze(1)).view(batch, 1, 1, max_len)
-    bias = torch.zeros(allowed.shape, dtype=dtype)
+    bias = torch.zeros(allowed.shape, dtype=dtype, device=block_tables.device)
     bias.masked_fill_(~allowed, torch.finfo(dtype).min)
     return bias
 

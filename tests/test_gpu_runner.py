@@ -1,0 +1,265 @@
+"""PagedRunner + Qwen3 on the GPU against the oracle's restatement of the reference runner and
+model, same bf16 weights, in the scenarios of the reference suite (tests/unit/test_paged_kv_cache.py)
+at the Qwen3 attention shape (16 / 8 heads of 128, block 16).
+
+The oracle runs twice: on the CPU (greedy tokens must agree) and on cuda:0, where its GEMMs are the
+product's own, so that everything but attention is bit-identical: layer-0 K/V (upstream of any
+attention) must match bit for bit; deeper layers carry only the attention kernels' rounding
+differences (max-abs within ``DEEP_ATOL``: a wrong block, slot or position moves values by O(1))."""
+
+import pytest
+import torch
+
+from mini_infra_qwen3_amd.core import KVCacheManager
+from mini_infra_qwen3_amd.model import Qwen3Config, Qwen3ForCausalLM, init_random_
+from mini_infra_qwen3_amd.worker import PagedKVCachePool, PagedRunner
+from oracle import qwen3_ref, torch_ref
+
+pytestmark = pytest.mark.gpu
+
+BS = 16
+DEEP_ATOL = 5e-2  # K/V of layers after the first attention: a few bf16 ulps at |x| < 8
+LOGIT_RTOL = 2e-2  # logits: fraction of the step's largest |logit|
+
+
+def small_config(layers=2):
+    return Qwen3Config(vocab_size=1000, hidden_size=256, intermediate_size=512, num_hidden_layers=layers,
+                       num_attention_heads=16, num_key_value_heads=8, head_dim=128)
+
+
+@pytest.fixture(scope="module")
+def models():
+    """(product model on cuda:0, oracle on cuda:0, oracle on cpu), identical bf16 weights, untied head."""
+    cfg = small_config()
+    model = Qwen3ForCausalLM(cfg)
+    init_random_(model, seed=0, std=0.05, untied_head_seed=1234)
+    model = model.to(torch.bfloat16)
+    weights = {k: v.clone() for k, v in model.state_dict().items()}
+    return (model.to("cuda:0").eval(), qwen3_ref.ReferenceQwen3(cfg, weights, "cuda:0"),
+            qwen3_ref.ReferenceQwen3(cfg, weights))
+
+
+def assert_kv_close(layer, got, want):
+    got, want = got.float().cpu(), want.float().cpu()
+    if layer == 0:
+        assert torch.equal(got, want)
+    else:
+        assert (got - want).abs().max().item() <= DEEP_ATOL
+
+
+def make_pool(cfg, num_blocks):
+    return PagedKVCachePool(cfg.num_hidden_layers, num_blocks, BS, cfg.num_key_value_heads, cfg.head_dim,
+                            torch.bfloat16, "cuda:0")
+
+
+def request_kv(pool, layer, table, length):
+    key_pool, value_pool = pool.kv_pools[layer]
+    k = torch.cat([key_pool[b] for b in table])[:length].transpose(0, 1)
+    v = torch.cat([value_pool[b] for b in table])[:length].transpose(0, 1)
+    return k, v
+
+
+def prompts_of(lengths, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    return [torch.randint(1, 999, (n,), generator=gen).tolist() for n in lengths]
+
+
+def test_pool_layout_and_byte_accounting(models):
+    model = models[0]
+    cfg = model.config
+    pool = make_pool(cfg, 10)
+    key_pool, value_pool = pool.kv_pools[0]
+    assert len(pool.kv_pools) == cfg.num_hidden_layers
+    assert tuple(key_pool.shape) == (10, BS, 8, 128) == tuple(value_pool.shape)
+    assert not key_pool.any() and not value_pool.any()
+    assert pool.bytes_per_block == 2 * cfg.num_hidden_layers * BS * 8 * 128 * 2
+    assert pool.total_bytes == 10 * pool.bytes_per_block
+
+
+def test_prepare_decode_inputs_packs_reference_metadata(models):
+    model = models[0]
+    runner = PagedRunner(model)
+    ids, pos, meta = runner.prepare_decode_inputs([[9, 4], [7]], last_tokens=[11, 22], positions=[21, 2],
+                                                  block_size=BS)
+    assert ids.tolist() == [[11], [22]] and pos.tolist() == [[21], [2]]
+    assert meta.slot_mapping.tolist() == [4 * BS + 5, 7 * BS + 2]
+    assert meta.context_lens.tolist() == [22, 3]
+    assert meta.block_tables.tolist() == [[9, 4], [7, 0]]
+
+
+def test_store_prefill_matches_oracle_and_isolates_requests(models):
+    """Left-padded batched prefill scattered to each request's blocks (test_paged_kv_cache.py:67-93)."""
+    model, ref, ref_cpu = models
+    prompts = prompts_of([37, 20], seed=1)
+    manager = KVCacheManager(BS, num_blocks=16)
+    manager.allocate_slots(5, 40)  # someone else's blocks first: tables are not 1, 2, ...
+    for i, p in enumerate(prompts):
+        manager.allocate_slots(i, len(p))
+    pool = make_pool(model.config, 16)
+    runner = PagedRunner(model)
+    out = runner.run_prefill_step(prompts)
+    runner.store_prefill(pool, out.prefill_cache, [manager.block_table(i) for i in range(2)], [37, 20], [0, 0])
+    first, presents = qwen3_ref.prefill(ref, prompts)
+    assert out.next_tokens == first == qwen3_ref.prefill(ref_cpu, prompts)[0]
+    for i, p in enumerate(prompts):
+        width = presents[0][0].shape[2]
+        for layer in range(model.config.num_hidden_layers):
+            k, v = request_kv(pool, layer, manager.block_table(i), len(p))
+            assert_kv_close(layer, k, presents[layer][0][i, :, width - len(p):])
+            assert_kv_close(layer, v, presents[layer][1][i, :, width - len(p):])
+    for b in manager.block_table(5):
+        assert not pool.kv_pools[0][0][b].any()
+
+
+def test_paged_decode_matches_oracle_tokens_and_logits(models):
+    """Mixed-length requests decoded step by step (test_paged_kv_cache.py:109-163): same greedy
+    tokens as the oracle's reference path on both devices, logits close."""
+    model, ref, ref_cpu = models
+    cfg = model.config
+    prompts = prompts_of([45, 17, 3], seed=2)
+    steps = 6
+    manager = KVCacheManager(BS, num_blocks=64)
+    pool = make_pool(cfg, 64)
+    ref_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128, device="cuda:0")
+    cpu_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128)
+    runner = PagedRunner(model)
+    for i, p in enumerate(prompts):
+        manager.allocate_slots(i, len(p))
+    tables = [manager.block_table(i) for i in range(3)]
+    out = runner.run_prefill_step(prompts)
+    runner.store_prefill(pool, out.prefill_cache, tables, [len(p) for p in prompts], [0] * 3)
+    first, presents = qwen3_ref.prefill(ref, prompts)
+    qwen3_ref.store_prefill(ref_pools, presents, tables, [len(p) for p in prompts], [0] * 3, BS)
+    _, cpu_presents = qwen3_ref.prefill(ref_cpu, prompts)
+    qwen3_ref.store_prefill(cpu_pools, cpu_presents, tables, [len(p) for p in prompts], [0] * 3, BS)
+    assert out.next_tokens == first
+    tokens = [[t] for t in first]
+    lengths = [len(p) for p in prompts]
+    with torch.inference_mode():
+        for _ in range(steps):
+            for i in range(3):
+                assert manager.allocate_slots(i, 1)
+            tables = [manager.block_table(i) for i in range(3)]
+            ids, pos, meta = runner.prepare_decode_inputs(tables, [t[-1] for t in tokens], lengths, BS)
+            logits = model(ids, position_ids=pos, attn_metadata=meta._replace(kv_pools=tuple(pool.kv_pools)),
+                           last_logits_only=True)[0][:, -1].float()
+            got = runner.run_decode_step(ids, pos, meta, pool)  # rewrites the same rows: same inputs
+            want = qwen3_ref.decode_step(ref, tables, [t[-1] for t in tokens], lengths, ref_pools, BS).float()
+            want_cpu = qwen3_ref.decode_step(ref_cpu, tables, [t[-1] for t in tokens], lengths, cpu_pools, BS)
+            assert got.next_tokens == logits.argmax(-1).tolist() == want.argmax(-1).tolist()
+            assert got.next_tokens == want_cpu.argmax(-1).tolist()
+            assert (logits - want).abs().max().item() <= LOGIT_RTOL * want.abs().max().item()
+            for i in range(3):
+                lengths[i] += 1
+                tokens[i].append(got.next_tokens[i])
+    for i in range(3):  # prefill- and decode-written K/V rows agree with the oracle's pools
+        for layer in range(cfg.num_hidden_layers):
+            for kv in range(2):
+                got = request_kv(pool, layer, manager.block_table(i), lengths[i])[kv]
+                want = torch.cat([ref_pools[layer][kv][b] for b in manager.block_table(i)])[:lengths[i]]
+                assert_kv_close(layer, got, want.transpose(0, 1))
+
+
+def test_stale_data_in_recycled_blocks_is_masked(models):
+    """test_paged_kv_cache.py:166-207: a request reusing freed, unzeroed blocks decodes exactly as
+    one on a fresh pool."""
+    model = models[0]
+    runner = PagedRunner(model)
+
+    def decode_once(manager, pool, idx, prompt):
+        manager.allocate_slots(idx, len(prompt))
+        out = runner.run_prefill_step([prompt])
+        runner.store_prefill(pool, out.prefill_cache, [manager.block_table(idx)], [len(prompt)], [0])
+        manager.allocate_slots(idx, 1)
+        ids, pos, meta = runner.prepare_decode_inputs([manager.block_table(idx)], [7], [len(prompt)], BS)
+        with torch.inference_mode():
+            logits, _ = model(ids, position_ids=pos, attn_metadata=meta._replace(kv_pools=tuple(pool.kv_pools)))
+        return logits
+
+    manager = KVCacheManager(BS, num_blocks=8)
+    pool = make_pool(model.config, 8)
+    decode_once(manager, pool, 0, prompts_of([40], seed=3)[0])  # fills blocks 1-3 with data
+    manager.free(0)
+    recycled = decode_once(manager, pool, 1, [17, 19, 23, 29, 31])
+    fresh = decode_once(KVCacheManager(BS, num_blocks=8), make_pool(model.config, 8), 1, [17, 19, 23, 29, 31])
+    assert torch.equal(recycled, fresh)
+
+
+def test_chunked_prefill_matches_one_shot(models):
+    """test_paged_kv_cache.py:210-246 at block 16: rows with different starts, history of unequal
+    length; pool K/V close to the one-shot prefill, first tokens equal."""
+    model = models[0]
+    cfg = model.config
+    prompts = prompts_of([75, 40], seed=4)
+    rounds = [[(0, 0, 20), (1, 0, 9)], [(0, 20, 52), (1, 9, 33)], [(0, 52, 75), (1, 33, 40)]]
+    manager = KVCacheManager(BS, num_blocks=64)
+    pool = make_pool(cfg, 64)
+    runner = PagedRunner(model)
+    first = {}
+    with torch.inference_mode():
+        for chunks in rounds:
+            for r, s, e in chunks:
+                assert manager.allocate_slots(r, e - s)
+            tables = [manager.block_table(r) for r, _, _ in chunks]
+            starts = [s for _, s, _ in chunks]
+            out = runner.run_prefill_chunk_step([prompts[r][s:e] for r, s, e in chunks], starts, tables, pool)
+            runner.store_prefill(pool, out.prefill_cache, tables, [e - s for _, s, e in chunks], starts)
+            for (r, _, e), t in zip(chunks, out.next_tokens):
+                if e == len(prompts[r]):
+                    first[r] = t
+    for r, p in enumerate(prompts):
+        whole = runner.run_prefill_step([p])
+        assert first[r] == whole.next_tokens[0]
+        for layer in range(cfg.num_hidden_layers):
+            k, v = request_kv(pool, layer, manager.block_table(r), len(p))
+            wk, wv = whole.prefill_cache[layer]  # other GEMM shapes: no bitwise claim even at layer 0
+            assert (k.float() - wk[0].float()).abs().max().item() <= DEEP_ATOL
+            assert (v.float() - wv[0].float()).abs().max().item() <= DEEP_ATOL
+
+
+def test_chunk_without_history_is_bitwise_whole_prompt_prefill(models):
+    """test_paged_kv_cache.py:249-262: start 0 everywhere runs the same path as a whole prefill."""
+    model = models[0]
+    prompts = prompts_of([30, 12], seed=5)
+    runner = PagedRunner(model)
+    pool = make_pool(model.config, 16)
+    chunk = runner.run_prefill_chunk_step(prompts, [0, 0], [[1, 2], [3]], pool)
+    whole = runner.run_prefill_step(prompts)
+    assert chunk.next_tokens == whole.next_tokens
+    for (kc, vc), (kw, vw) in zip(chunk.prefill_cache, whole.prefill_cache):
+        assert torch.equal(kc, kw) and torch.equal(vc, vw)
+
+
+def test_chunked_prefill_matches_oracle_runner(models):
+    """One chunk step with history through both runners: same first tokens, stored K/V close."""
+    model, ref, ref_cpu = models
+    cfg = model.config
+    prompts = prompts_of([50, 33], seed=6)
+    manager = KVCacheManager(BS, num_blocks=32)
+    pool = make_pool(cfg, 32)
+    ref_pools = torch_ref.make_pools(cfg.num_hidden_layers, 32, BS, 8, 128, device="cuda:0")
+    cpu_pools = torch_ref.make_pools(cfg.num_hidden_layers, 32, BS, 8, 128)
+    runner = PagedRunner(model)
+    for r, p in enumerate(prompts):
+        manager.allocate_slots(r, len(p))
+    tables = [manager.block_table(r) for r in range(2)]
+    cut = [21, 16]
+    for chunk_id in range(2):
+        starts = [0, 0] if chunk_id == 0 else cut
+        ends = cut if chunk_id == 0 else [len(p) for p in prompts]
+        chunks = [p[s:e] for p, s, e in zip(prompts, starts, ends)]
+        out = runner.run_prefill_chunk_step(chunks, starts, tables, pool)
+        runner.store_prefill(pool, out.prefill_cache, tables, [e - s for s, e in zip(starts, ends)], starts)
+        lens = [e - s for s, e in zip(starts, ends)]
+        toks, presents = qwen3_ref.prefill_chunk_step(ref, chunks, starts, tables, ref_pools, BS)
+        qwen3_ref.store_prefill(ref_pools, presents, tables, lens, starts, BS)
+        toks_cpu, cpu_presents = qwen3_ref.prefill_chunk_step(ref_cpu, chunks, starts, tables, cpu_pools, BS)
+        qwen3_ref.store_prefill(cpu_pools, cpu_presents, tables, lens, starts, BS)
+        if chunk_id == 1:
+            assert out.next_tokens == toks == toks_cpu
+    for r, p in enumerate(prompts):
+        for layer in range(cfg.num_hidden_layers):
+            for kv in range(2):
+                got = request_kv(pool, layer, tables[r], len(p))[kv]
+                want = torch.cat([ref_pools[layer][kv][b] for b in tables[r]])[:len(p)].transpose(0, 1)
+                assert_kv_close(layer, got, want)

@@ -1,0 +1,124 @@
+"""Pins the oracle's Qwen3 / PagedRunner restatement with the invariants of the reference suite
+(tests/unit/test_paged_kv_cache.py:109-262), run in fp32 on the CPU on a tiny model like the
+reference's own fixture (build_tiny_model + untied head: tests/unit/conftest.py:13-25)."""
+
+from dataclasses import dataclass
+
+import pytest
+import torch
+
+from oracle import qwen3_ref, torch_ref
+
+
+@dataclass
+class TinyConfig:
+    vocab_size: int = 97
+    hidden_size: int = 32
+    intermediate_size: int = 64
+    num_hidden_layers: int = 2
+    num_attention_heads: int = 4
+    num_key_value_heads: int = 2
+    head_dim: int = 4
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 10000.0
+
+
+def tiny_model(seed=0, head_seed=1234) -> qwen3_ref.ReferenceQwen3:
+    c = TinyConfig()
+    gen = torch.Generator().manual_seed(seed)
+    sd = {"model.embed_tokens.weight": torch.randn(c.vocab_size, c.hidden_size, generator=gen) * 0.5,
+          "model.norm.weight": torch.ones(c.hidden_size)}
+    for i in range(c.num_hidden_layers):
+        p = f"model.layers.{i}."
+        qd, kd = c.num_attention_heads * c.head_dim, c.num_key_value_heads * c.head_dim
+        for name, shape in (("self_attn.q_proj", (qd, c.hidden_size)), ("self_attn.k_proj", (kd, c.hidden_size)),
+                            ("self_attn.v_proj", (kd, c.hidden_size)), ("self_attn.o_proj", (c.hidden_size, qd)),
+                            ("mlp.gate_proj", (c.intermediate_size, c.hidden_size)),
+                            ("mlp.up_proj", (c.intermediate_size, c.hidden_size)),
+                            ("mlp.down_proj", (c.hidden_size, c.intermediate_size))):
+            sd[p + name + ".weight"] = torch.randn(shape, generator=gen) * 0.3
+        for name, n in (("self_attn.q_norm", c.head_dim), ("self_attn.k_norm", c.head_dim),
+                        ("input_layernorm", c.hidden_size), ("post_attention_layernorm", c.hidden_size)):
+            sd[p + name + ".weight"] = torch.ones(n)
+    sd["lm_head.weight"] = torch.randn(c.vocab_size, c.hidden_size, generator=torch.Generator().manual_seed(head_seed))
+    return qwen3_ref.ReferenceQwen3(c, sd)
+
+
+def pools_for(model, num_blocks, block_size):
+    c = model.config
+    return torch_ref.make_pools(c.num_hidden_layers, num_blocks, block_size, c.num_key_value_heads, c.head_dim,
+                                dtype=torch.float32)
+
+
+def tables_from(num_tokens, block_size, first_block):
+    nb = -(-num_tokens // block_size)
+    return list(range(first_block, first_block + nb))
+
+
+@pytest.mark.parametrize("block_size", [1, 3, 4, 16])
+def test_paged_decode_equals_dense_decode(block_size):
+    """tests/unit/test_paged_kv_cache.py:109-163 on the oracle: logits within 1e-4, same tokens."""
+    model = tiny_model()
+    prompts = [[3, 5, 7, 9, 11, 13, 15], [17, 19, 23], [29]]
+    steps = 5
+    pools = pools_for(model, 64, block_size)
+    tables, nxt = [], 1
+    for p in prompts:
+        tables.append(tables_from(len(p) + steps, block_size, nxt))
+        nxt += len(tables[-1])
+    _, presents = qwen3_ref.prefill(model, prompts)
+    qwen3_ref.store_prefill(pools, presents, tables, [len(p) for p in prompts], [0] * 3, block_size)
+    dense = [qwen3_ref.prefill(model, [p])[1] for p in prompts]
+    tokens = [[(i * 13 + 2) % 90 + 1] for i in range(3)]
+    lengths = [len(p) for p in prompts]
+    for _ in range(steps):
+        paged = qwen3_ref.decode_step(model, tables, [t[-1] for t in tokens], lengths, pools, block_size)
+        for i in range(3):
+            logits, dense[i] = model.forward(torch.tensor([[tokens[i][-1]]]), position_ids=torch.tensor([[lengths[i]]]),
+                                             past_key_values=dense[i])
+            assert (paged[i] - logits[0, -1]).abs().max().item() <= 1e-4
+            assert int(paged[i].argmax()) == int(logits[0, -1].argmax())
+            lengths[i] += 1
+            tokens[i].append(int(paged[i].argmax()))
+
+
+@pytest.mark.parametrize("block_size", [1, 3, 4, 16])
+def test_chunked_prefill_equals_one_shot(block_size):
+    """tests/unit/test_paged_kv_cache.py:210-246 on the oracle: pool K/V and first tokens."""
+    model = tiny_model()
+    prompts = [[(j * 5 + 3) % 80 + 1 for j in range(11)], [(j * 7 + 2) % 80 + 1 for j in range(6)]]
+    rounds = [[(0, 0, 5), (1, 0, 2)], [(0, 5, 8), (1, 2, 6)], [(0, 8, 11)]]
+    pools = pools_for(model, 64, block_size)
+    tables = [tables_from(11, block_size, 1), tables_from(6, block_size, 1 + len(tables_from(11, block_size, 1)))]
+    first = {}
+    for chunks in rounds:
+        bt = [tables[r] for r, _, _ in chunks]
+        starts = [s for _, s, _ in chunks]
+        toks, presents = qwen3_ref.prefill_chunk_step(model, [prompts[r][s:e] for r, s, e in chunks], starts, bt,
+                                                      pools, block_size)
+        qwen3_ref.store_prefill(pools, presents, bt, [e - s for _, s, e in chunks], starts, block_size)
+        for (r, _, e), t in zip(chunks, toks):
+            if e == len(prompts[r]):
+                first[r] = t
+    for r, p in enumerate(prompts):
+        toks, ref = qwen3_ref.prefill(model, [p])
+        assert first[r] == toks[0]
+        for layer, (k, v) in enumerate(ref):
+            kp, vp = pools[layer]
+            got_k = torch.cat([kp[b] for b in tables[r]])[:len(p)].transpose(0, 1)
+            got_v = torch.cat([vp[b] for b in tables[r]])[:len(p)].transpose(0, 1)
+            torch.testing.assert_close(got_k, k[0], atol=1e-5, rtol=0)
+            torch.testing.assert_close(got_v, v[0], atol=1e-5, rtol=0)
+
+
+def test_chunk_without_history_is_whole_prompt_prefill():
+    """tests/unit/test_paged_kv_cache.py:249-262 on the oracle: bitwise identical."""
+    model = tiny_model()
+    prompts = [[3, 5, 7, 9, 11, 13], [17, 19, 23]]
+    pools = pools_for(model, 16, 4)
+    toks_c, cache_c = qwen3_ref.prefill_chunk_step(model, prompts, [0, 0], [[1, 2], [3]], pools, 4)
+    toks_w, cache_w = qwen3_ref.prefill(model, prompts)
+    assert toks_c == toks_w
+    for (kc, vc), (kw, vw) in zip(cache_c, cache_w):
+        assert torch.equal(kc, kw) and torch.equal(vc, vw)
+
