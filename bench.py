@@ -8,8 +8,10 @@ algorithmic HBM bandwidth of the whole step: per layer sum(context) x 4096 B of 
 plus Q read, O written and the appended K/V rows, divided by the timed step time.
 
 Also measured in the same run (reported under ``kernels``): the 28-layer prefill scatter of
-32 prompts U[128, 2048] with churned block tables, and the block-table history gather of
-4 x 16384-token prompts in 2048-token chunks.  The CPU baseline times the reference's torch
+32 prompts U[128, 2048] with churned block tables, the block-table history gather and the MFMA
+chunked-prefill attention of 4 x 16384-token prompts in 2048-token chunks; and (under ``e2e``)
+the continuous-batching run of a random-init Qwen3-0.6B: 128 requests at 20 req/s, prompts
+U[32, 1024], 128 output tokens, chunked prefill with a 2048-token budget.  The CPU baseline times the reference's torch
 decode chain (the oracle) on the host cores on a bounded sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only decode]
@@ -292,13 +294,62 @@ def bench_prefill(steps: int, warmup: int, device: torch.device) -> dict:
             "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "frac": tflops / MFMA_BF16_PEAK_TFLOPS}
 
 
+# ------------------------------------------------------------------------ e2e continuous batching
+def bench_e2e(device: torch.device, seed: int = 0) -> dict:
+    """Continuous batching with chunked prefill (token budget 2048, block 16, batch slots = number of
+    requests) of a random-init Qwen3-0.6B (bf16, N(0, 0.02), tied embeddings): 128 requests, Poisson
+    arrivals at 20 req/s, prompts U[32, 1024], 128 greedy tokens each, EOS disabled.  Output tok/s =
+    output tokens x 1000 / busy_ms, busy_ms = sum over steps of (device-timed forward + host-timed
+    cache management), on the logical clock the measured step times advance."""
+    from mini_infra_qwen3_amd.core.scheduler import SchedulePhase
+    from mini_infra_qwen3_amd.engine import PagedScheduleBackend, run_scheduler
+    from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
+    from mini_infra_qwen3_amd.workloads import serving_requests
+
+    model = Qwen3ForCausalLM(qwen3_0_6b())
+    init_random_(model, seed=seed, std=0.02)
+    model = model.to(device=device, dtype=torch.bfloat16).eval()
+
+    def run(requests):
+        backend = PagedScheduleBackend(model, requests, len(requests))
+        return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False)
+
+    run(serving_requests(seed=seed + 1, num_requests=8, max_new_tokens=8))  # warm-up: kernels, GEMM choices
+    requests = serving_requests(seed=seed)
+    res = run(requests)
+    decode = [e for e in res.events if e.phase is SchedulePhase.DECODE]
+    prefill = [e for e in res.events if e.phase is SchedulePhase.PREFILL]
+    out = {
+        "metric": "e2e output tok/s Qwen3-0.6B (continuous batching, chunked prefill 2048, paged KV)",
+        "output_tok_s": round(res.throughput_tok_s, 1),
+        "wall_tok_s": round(res.wall_tok_s, 1),
+        "busy_ms": round(res.busy_ms, 1),
+        "model_ms": round(res.model_ms, 1),
+        "cache_ms": round(res.cache_ms, 1),
+        "wall_ms": round(res.wall_ms, 1),
+        "makespan_ms": round(res.makespan_ms, 1),
+        "output_tokens": res.num_output_tokens,
+        "prompt_tokens": sum(r.prompt_len for r in requests),
+        "decode_steps": len(decode),
+        "prefill_steps": len(prefill),
+        "decode_step_ms_mean": round(sum(e.step_ms for e in decode) / max(len(decode), 1), 3),
+        "decode_batch_mean": round(sum(len(e.request_ids) for e in decode) / max(len(decode), 1), 2),
+        "prefill_step_ms_mean": round(sum(e.step_ms for e in prefill) / max(len(prefill), 1), 3),
+        "requests": len(requests),
+        "arrival_rate_req_s": 20.0,
+    }
+    del model, res
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["decode", "prefill", "copy", "all"], default="all")
+    parser.add_argument("--only", choices=["decode", "prefill", "copy", "e2e", "all"], default="all")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of this path "
@@ -328,6 +379,11 @@ def main() -> int:
         log(f"chunked prefill: {res['ms_per_layer']:.2f} ms/layer, {res['achieved_TFLOPs']:.1f} TFLOP/s")
         print(json.dumps(res), flush=True)
         return 0
+    if args.only == "e2e":
+        res = bench_e2e(device)
+        log(f"e2e: {res['output_tok_s']:.1f} output tok/s (busy), {res['wall_tok_s']:.1f} tok/s (wall)")
+        print(json.dumps(res), flush=True)
+        return 0
     dec = bench_decode(args.steps, args.warmup, device)
     log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value']:.1f} GB/s; attention launch "
         f"{dec['attn_launch_ms']:.3f} ms = {dec['roofline']['achieved']:.1f} GB/s "
@@ -354,6 +410,10 @@ def main() -> int:
         log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "
             f"{kernels['chunked_prefill']['achieved_TFLOPs']:.1f} TFLOP/s")
         torch.cuda.empty_cache()
+    e2e = None
+    if args.only == "all":
+        e2e = bench_e2e(device)
+        log(f"e2e: {e2e['output_tok_s']:.1f} output tok/s (busy), {e2e['wall_tok_s']:.1f} tok/s (wall)")
 
     line = {
         "metric": METRIC,
@@ -381,6 +441,7 @@ def main() -> int:
         "roofline": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec["roofline"].items()},
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "e2e": e2e,
     }
     print(json.dumps(line), flush=True)
     return 0

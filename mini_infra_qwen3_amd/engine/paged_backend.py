@@ -1,0 +1,89 @@
+"""Step execution of the paged continuous-batching run on the HIP data plane.
+
+Same contract and timing as the reference's PagedScheduleBackend
+(src/mini_infra/engine/paged_schedule_backend.py:25-128):
+
+* ``model_ms``: the runner's device-timed forward + greedy sample (StepTimer);
+* ``cache_ms``: host-timed, between device syncs: ``store_prefill`` after a prefill step, and
+  ``prepare_decode_inputs`` (pack + upload) before a decode step.
+"""
+
+from __future__ import annotations
+
+import time
+from collections.abc import Sequence
+from dataclasses import dataclass
+
+import torch
+
+from mini_infra_qwen3_amd.core import KVCacheManager, PagedCacheConfig, num_blocks_for_tokens, required_pool_blocks
+from mini_infra_qwen3_amd.core.scheduler import PrefillChunk, RequestState
+from mini_infra_qwen3_amd.core.types import Request
+from mini_infra_qwen3_amd.device import synchronize
+from mini_infra_qwen3_amd.worker import PagedKVCachePool, PagedRunner
+
+
+@dataclass(frozen=True)
+class ScheduleStepOutput:
+    """What one executed step hands back to the loop (reference schedule_backend.py:26-37)."""
+
+    next_tokens: list[int]
+    model_ms: float
+    cache_ms: float
+    physical_batch_size: int
+    live_kv_cache_bytes: int
+    accessed_kv_cache_tokens: int = 0
+
+
+class PagedScheduleBackend:
+    """Owns the pool and the block allocator; runs prefill chunks and decode steps through PagedRunner."""
+
+    def __init__(self, model: torch.nn.Module, requests: Sequence[Request], max_running_requests: int,
+                 paged_cache_config: PagedCacheConfig = PagedCacheConfig(), pad_token_id: int = 0):
+        self.model = model
+        self.device = next(model.parameters()).device
+        self.block_size = paged_cache_config.block_size
+        num_blocks = paged_cache_config.num_blocks or required_pool_blocks(requests, max_running_requests,
+                                                                          self.block_size)
+        largest = max(num_blocks_for_tokens(r.prompt_len + r.max_new_tokens - 1, self.block_size) for r in requests)
+        if largest > num_blocks - 1:
+            raise ValueError(f"num_blocks={num_blocks} cannot hold one request of {largest} blocks "
+                             "(plus the null block)")
+        config = model.config
+        self.runner = PagedRunner(model, pad_token_id)
+        self.pool = PagedKVCachePool(config.num_hidden_layers, num_blocks, self.block_size,
+                                     config.num_key_value_heads, config.head_dim,
+                                     next(model.parameters()).dtype, self.device)
+        self.kv_cache_manager = KVCacheManager(self.block_size, num_blocks)
+
+    def _live_bytes(self) -> int:
+        return self.kv_cache_manager.num_used_blocks * self.pool.bytes_per_block
+
+    def execute_prefill(self, chunks: Sequence[PrefillChunk]) -> ScheduleStepOutput:
+        tables = [self.kv_cache_manager.block_table(c.state.request.request_idx) for c in chunks]
+        starts = [c.start for c in chunks]
+        out = self.runner.run_prefill_chunk_step([c.state.request.token_ids[c.start:c.end] for c in chunks], starts,
+                                                 tables, self.pool)
+        synchronize(self.device)
+        t0 = time.perf_counter()
+        self.runner.store_prefill(self.pool, out.prefill_cache, tables, [c.num_tokens for c in chunks], starts)
+        synchronize(self.device)
+        cache_ms = (time.perf_counter() - t0) * 1000.0
+        return ScheduleStepOutput([t for t, c in zip(out.next_tokens, chunks) if c.is_last], out.model_ms, cache_ms,
+                                  len(chunks), self._live_bytes(), sum(c.start for c in chunks))
+
+    def execute_decode(self, states: Sequence[RequestState]) -> ScheduleStepOutput:
+        synchronize(self.device)
+        t0 = time.perf_counter()
+        ids, pos, meta = self.runner.prepare_decode_inputs(
+            [self.kv_cache_manager.block_table(s.request.request_idx) for s in states],
+            last_tokens=[s.generated[-1] for s in states], positions=[s.cache_length for s in states],
+            block_size=self.block_size)
+        synchronize(self.device)
+        cache_ms = (time.perf_counter() - t0) * 1000.0
+        out = self.runner.run_decode_step(ids, pos, meta, self.pool)
+        return ScheduleStepOutput(out.next_tokens, out.model_ms, cache_ms, len(states), self._live_bytes(),
+                                  sum(s.cache_length + 1 for s in states))
+
+
+__all__ = ["PagedScheduleBackend", "ScheduleStepOutput"]

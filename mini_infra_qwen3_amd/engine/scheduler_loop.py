@@ -1,0 +1,140 @@
+"""The continuous-batching loop and its summary metrics.
+
+Loop semantics of the reference's ``_run_schedule_loop`` (src/mini_infra/engine/scheduler_loop.py:47-134):
+a logical clock starts at the first arrival; each iteration moves arrived requests into the waiting
+queue, asks the scheduler for a step, executes it and advances the clock by the step's
+``model_ms + cache_ms``; an idle scheduler jumps the clock to the next arrival.  Summary metrics
+follow ``summarize_schedule`` (src/mini_infra/engine/metrics.py:330-430): ``busy_ms`` is the sum of
+step times and ``throughput_tok_s = output tokens * 1000 / busy_ms``.
+
+``step_clock`` (not in the reference) replaces the measured step time on the logical clock by a
+function of the plan, which makes the schedule independent of timing: two backends given the same
+``step_clock`` execute identical step sequences.
+"""
+
+from __future__ import annotations
+
+import time
+from collections.abc import Callable, Sequence
+from dataclasses import dataclass
+
+import torch
+
+from mini_infra_qwen3_amd.core.scheduler import (
+    ArrivalQueue,
+    IterationScheduler,
+    RequestState,
+    SchedulePhase,
+    SchedulerOutput,
+)
+from mini_infra_qwen3_amd.core.types import Request
+from mini_infra_qwen3_amd.device import synchronize
+
+
+@dataclass(frozen=True)
+class ScheduleEvent:
+    """One executed step (reference metrics.py:269-289, the fields this path reports)."""
+
+    phase: SchedulePhase
+    request_ids: tuple[int, ...]
+    admitted_request_ids: tuple[int, ...]
+    finished_request_ids: tuple[int, ...]
+    chunk_spans: tuple[tuple[int, int], ...]
+    num_scheduled_tokens: int
+    num_generated_tokens: int
+    step_ms: float
+    model_ms: float
+    cache_ms: float
+    live_kv_cache_bytes: int
+
+
+@dataclass(frozen=True)
+class ScheduleResult:
+    """Generated tokens per request (request_idx order), the step events and the summary."""
+
+    tokens: dict[int, list[int]]
+    events: list[ScheduleEvent]
+    busy_ms: float
+    model_ms: float
+    cache_ms: float
+    wall_ms: float
+    makespan_ms: float
+    num_output_tokens: int
+
+    @property
+    def throughput_tok_s(self) -> float:
+        return self.num_output_tokens * 1000.0 / self.busy_ms if self.busy_ms else 0.0
+
+    @property
+    def wall_tok_s(self) -> float:
+        return self.num_output_tokens * 1000.0 / self.wall_ms if self.wall_ms else 0.0
+
+    def phase_ms(self, phase: SchedulePhase) -> float:
+        return sum(e.step_ms for e in self.events if e.phase is phase)
+
+    def num_steps(self, phase: SchedulePhase) -> int:
+        return sum(1 for e in self.events if e.phase is phase)
+
+
+@torch.inference_mode()
+def run_scheduler(backend, requests: Sequence[Request], token_budget: int = 2048,
+                  max_running_requests: int | None = None, eos_token_id: int | None = None,
+                  stop_on_eos: bool = True,
+                  step_clock: Callable[[SchedulerOutput], float] | None = None) -> ScheduleResult:
+    """Runs ``requests`` to completion on ``backend`` (``execute_prefill`` / ``execute_decode`` and a
+    ``kv_cache_manager``) with continuous batching and chunked prefill under ``token_budget``.
+
+    ``max_running_requests`` defaults to the number of requests (reference scheduler_loop.py:162-163).
+    """
+    if not requests:
+        raise ValueError("requests must not be empty")
+    if len({r.request_idx for r in requests}) != len(requests):
+        raise ValueError("request_idx must be unique")
+    mrr = max_running_requests if max_running_requests is not None else len(requests)
+    states = [RequestState(r) for r in requests]
+    arrivals = ArrivalQueue(states)
+    clock_ms = min(r.arrival_ms for r in requests)
+    scheduler = IterationScheduler(token_budget, mrr, backend.kv_cache_manager)
+    events: list[ScheduleEvent] = []
+    device = getattr(backend, "device", torch.device("cpu"))
+    synchronize(device)
+    wall_start = time.perf_counter()
+    while len(arrivals) or scheduler.has_unfinished_requests:
+        scheduler.add_requests(arrivals.pop_arrived(clock_ms))
+        output = scheduler.schedule(clock_ms)
+        if output is None:
+            clock_ms = arrivals.next_arrival_ms()
+            continue
+        if output.phase is SchedulePhase.PREFILL:
+            step = backend.execute_prefill(output.prefill_chunks)
+        else:
+            step = backend.execute_decode(output.scheduled_requests)
+        step_ms = step.model_ms + step.cache_ms
+        clock_ms += step_ms if step_clock is None else step_clock(output)
+        finished = scheduler.update_from_output(output, step.next_tokens, clock_ms, eos_token_id, stop_on_eos)
+        events.append(ScheduleEvent(
+            phase=output.phase,
+            request_ids=tuple(s.request.request_idx for s in output.scheduled_requests),
+            admitted_request_ids=tuple(c.state.request.request_idx for c in output.prefill_chunks if c.start == 0),
+            finished_request_ids=tuple(s.request.request_idx for s in finished),
+            chunk_spans=tuple((c.start, c.end) for c in output.prefill_chunks),
+            num_scheduled_tokens=output.num_scheduled_tokens,
+            num_generated_tokens=len(step.next_tokens),
+            step_ms=step_ms, model_ms=step.model_ms, cache_ms=step.cache_ms,
+            live_kv_cache_bytes=step.live_kv_cache_bytes,
+        ))
+    synchronize(device)
+    wall_ms = (time.perf_counter() - wall_start) * 1000.0
+    return ScheduleResult(
+        tokens={s.request.request_idx: list(s.generated) for s in sorted(states, key=lambda s: s.request.request_idx)},
+        events=events,
+        busy_ms=sum(e.step_ms for e in events),
+        model_ms=sum(e.model_ms for e in events),
+        cache_ms=sum(e.cache_ms for e in events),
+        wall_ms=wall_ms,
+        makespan_ms=max(s.completion_ms for s in states) - min(r.arrival_ms for r in requests),
+        num_output_tokens=sum(len(s.generated) for s in states),
+    )
+
+
+__all__ = ["ScheduleEvent", "ScheduleResult", "run_scheduler"]

@@ -11,6 +11,9 @@ GPU path and the CPU checker see identical inputs:
 * ``decode_at_scale`` -- 28 layers: batch 256, contexts lognormal (median 2048, sigma 1.3,
   clipped to [256, 8192]; about 90 GB of K/V), randomly permuted blocks.
 * ``chunked_prefill`` -- 4 prompts of 16384 tokens in 2048-token chunks with history.
+* ``serving_requests`` -- the continuous-batching run: 128 requests, Poisson arrivals at 20 req/s
+  (exponential gaps, mean 50 ms, first arrival at 0), prompt lengths uniform in [32, 1024] with
+  token ids uniform in [1000, 100000), 128 output tokens each.
 
 Small values (context counts, tables) are drawn on the CPU with ``torch.Generator``; bulk
 values are drawn with ``randn`` in fp32 and cast to bf16, on the CPU for the small workloads
@@ -214,9 +217,27 @@ def chunked_prefill(seed: int = 0, num_prompts: int = 4, prompt_len: int = 16384
     return ChunkedPrefillWorkload(prompt_len, chunk_len, num_prompts, tables, num_blocks)
 
 
+def serving_requests(seed: int = 0, num_requests: int = 128, rate_per_s: float = 20.0, min_prompt: int = 32,
+                     max_prompt: int = 1024, max_new_tokens: int = 128, vocab_size: int = 151936):
+    """Requests of the continuous-batching run (pure Poisson arrivals: no initial burst, no clamping
+    of the gaps).  Token ids span [1000, min(vocab, 100000)) as the reference's synthetic prompts do
+    (src/mini_infra/bench/synthetic.py:29-31)."""
+    from mini_infra_qwen3_amd.core.types import Request
+
+    rng = np.random.default_rng(seed)
+    gaps = rng.exponential(1000.0 / rate_per_s, num_requests)
+    gaps[0] = 0.0
+    arrivals = np.round(np.cumsum(gaps), 3)
+    lengths = rng.integers(min_prompt, max_prompt + 1, num_requests)
+    low = 1000 if vocab_size > 1000 else 1
+    high = min(vocab_size, 100000)
+    return [Request(i, tuple(int(t) for t in rng.integers(low, high, int(n))), max_new_tokens, float(a))
+            for i, (n, a) in enumerate(zip(lengths, arrivals))]
+
+
 __all__ = [
     "BLOCK_SIZE", "HEAD_DIM", "KV_BYTES_PER_TOKEN_LAYER", "NUM_HEADS", "NUM_KV_HEADS", "NUM_LAYERS", "SCALE",
     "ChunkedPrefillWorkload", "DecodeWorkload", "PrefillScatterWorkload", "chunked_prefill", "churned_tables",
     "decode_at_scale", "decode_step", "lognormal_lengths", "padded", "permuted_tables", "prefill_scatter",
-    "slots_of", "uniform_lengths",
+    "serving_requests", "slots_of", "uniform_lengths",
 ]

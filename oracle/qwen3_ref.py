@@ -128,9 +128,10 @@ def prefill(model: ReferenceQwen3, prompts, pad_token_id: int = 0):
     return logits[:, -1].argmax(-1).tolist(), presents
 
 
-def prefill_chunk_step(model: ReferenceQwen3, chunk_token_ids, start_positions, block_tables, pools, block_size,
-                       pad_token_id: int = 0):
-    """``run_prefill_chunk_step`` (paged_runner.py:32-102): gather history, mask, dense forward."""
+def prefill_chunk_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, block_tables, pools, block_size,
+                         pad_token_id: int = 0):
+    """``run_prefill_chunk_step`` (paged_runner.py:32-102): gather history, mask, dense forward.
+    Returns (last-position logits ``[B, V]``, per-layer K/V of history + chunk)."""
     lens = [len(c) for c in chunk_token_ids]
     width = max(lens)
     hist = [-(-s // block_size) for s in start_positions]
@@ -148,7 +149,15 @@ def prefill_chunk_step(model: ReferenceQwen3, chunk_token_ids, start_positions, 
         mask = torch.cat((hpos < starts, mask), dim=1)
         past = torch_ref.gather_blocks(pools, packed[:, 2 * width + 2:])
     logits, presents = model.forward(input_ids, attention_mask=mask, position_ids=position_ids, past_key_values=past)
-    return logits[:, -1].argmax(-1).tolist(), presents
+    return logits[:, -1], presents
+
+
+def prefill_chunk_step(model: ReferenceQwen3, chunk_token_ids, start_positions, block_tables, pools, block_size,
+                       pad_token_id: int = 0):
+    """``run_prefill_chunk_step``: (greedy tokens after each row's last position, per-layer K/V)."""
+    logits, presents = prefill_chunk_logits(model, chunk_token_ids, start_positions, block_tables, pools, block_size,
+                                            pad_token_id)
+    return logits.argmax(-1).tolist(), presents
 
 
 def store_prefill(pools, presents, block_tables, chunk_lens, start_positions, block_size):
@@ -167,3 +176,64 @@ def decode_step(model: ReferenceQwen3, block_tables, last_tokens, positions, poo
              "kv_pools": pools}
     logits, _ = model.forward(packed[:, 0:1], position_ids=packed[:, 1:2], paged=paged)
     return logits[:, -1]
+
+
+class ReferenceScheduleBackend:
+    """The reference's PagedScheduleBackend over this restatement
+    (src/mini_infra/engine/paged_schedule_backend.py:70-128), for the continuous-batching loop.
+
+    Pools live on ``model.device``.  With ``forced_tokens`` (request_idx -> token list) every step
+    returns those tokens instead of its own greedy choice -- the run follows another backend's
+    sequences -- and records, per produced token, ``(request_idx, forced, own argmax, logit gap,
+    row std)`` where the gap is ``max logit - logit[forced]`` (0 when they agree) and the row std
+    is the standard deviation of the row's logits (the scale of the gap).
+    """
+
+    def __init__(self, model: ReferenceQwen3, requests, max_running_requests: int, block_size: int = 16,
+                 num_blocks: int | None = None, forced_tokens: dict | None = None):
+        from mini_infra_qwen3_amd.core import KVCacheManager, required_pool_blocks
+
+        c = model.config
+        self.model = model
+        self.device = model.device
+        self.block_size = block_size
+        num_blocks = num_blocks or required_pool_blocks(requests, max_running_requests, block_size)
+        self.pools = torch_ref.make_pools(c.num_hidden_layers, num_blocks, block_size, c.num_key_value_heads,
+                                          c.head_dim, dtype=model.dtype, device=model.device)
+        self.kv_cache_manager = KVCacheManager(block_size, num_blocks)
+        self.forced = forced_tokens
+        self.records: list[tuple[int, int, int, float, float]] = []
+
+    def _choose(self, request_ids, produced_index, logits):
+        own = logits.argmax(-1).tolist()
+        if self.forced is None:
+            return own
+        out = []
+        for r, k, row, mine in zip(request_ids, produced_index, logits, own):
+            token = self.forced[r][k]
+            self.records.append((r, token, mine, float(row.max() - row[token]), float(row.std())))
+            out.append(token)
+        return out
+
+    def execute_prefill(self, chunks):
+        from mini_infra_qwen3_amd.engine import ScheduleStepOutput
+
+        tables = [self.kv_cache_manager.block_table(ch.state.request.request_idx) for ch in chunks]
+        starts = [ch.start for ch in chunks]
+        lens = [ch.num_tokens for ch in chunks]
+        logits, presents = prefill_chunk_logits(self.model, [ch.state.request.token_ids[ch.start:ch.end] for ch in chunks],
+                                                starts, tables, self.pools, self.block_size)
+        store_prefill(self.pools, presents, tables, lens, starts, self.block_size)
+        last = [i for i, ch in enumerate(chunks) if ch.is_last]
+        tokens = self._choose([chunks[i].state.request.request_idx for i in last], [0] * len(last),
+                              logits[last].float()) if last else []
+        return ScheduleStepOutput(tokens, 0.0, 0.0, len(chunks), 0)
+
+    def execute_decode(self, states):
+        from mini_infra_qwen3_amd.engine import ScheduleStepOutput
+
+        tables = [self.kv_cache_manager.block_table(s.request.request_idx) for s in states]
+        logits = decode_step(self.model, tables, [s.generated[-1] for s in states],
+                             [s.cache_length for s in states], self.pools, self.block_size).float()
+        tokens = self._choose([s.request.request_idx for s in states], [len(s.generated) for s in states], logits)
+        return ScheduleStepOutput(tokens, 0.0, 0.0, len(states), 0)

@@ -1,0 +1,73 @@
+"""Continuous batching with chunked prefill on Qwen3-0.6B (28 layers, hidden 1024, vocab 151936,
+bf16, random init): the HIP path against the oracle's restatement of the reference torch path
+(run on cuda:0 with the same weights and GEMMs), both driven through the same scheduler loop with
+a fixed logical step clock, so that they execute the identical step sequence.
+
+The two paths round attention differently (the oracle rounds bf16 scores, normalised bf16
+probabilities and a bf16 PV product; the kernels keep fp32 online-softmax state), so a greedy
+choice between two logits closer than that rounding can go either way, after which the two
+sequences are different texts.  The oracle therefore follows the HIP path's tokens (teacher
+forcing) and checks each one: it must be the oracle's own argmax, or a near tie -- its logit within
+``TIE`` row standard deviations of the oracle's maximum -- and near ties must stay rare.  Both the
+benchmark's model (tied embeddings, N(0, 0.02)) and an untied model with an N(0, 1) head (output
+that depends on the whole context, as the reference's diverse test model:
+tests/unit/conftest.py:13-25) are checked.
+"""
+
+import pytest
+import torch
+
+from mini_infra_qwen3_amd.core.scheduler import SchedulePhase
+from mini_infra_qwen3_amd.engine import PagedScheduleBackend, run_scheduler
+from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
+from mini_infra_qwen3_amd.workloads import serving_requests
+from oracle import qwen3_ref
+
+pytestmark = pytest.mark.gpu
+
+# bf16 logits of a 151936-token vocabulary are coarse: the top logit sits near 4-5 row standard
+# deviations, where one bf16 ulp is about 0.02-0.03 of a deviation, and the top two logits of so
+# many are that close (or exactly equal) a few percent of the time.  Observed disagreements are
+# exact bf16 ties or 1-3 ulps apart; a wrong block, slot or position moves logits by deviations.
+TIE = 0.1  # logit gap, in row standard deviations, below which a greedy choice is a near tie
+MAX_TIE_FRACTION = 0.1
+
+
+def step_clock(out):
+    return 10.0 if out.phase is SchedulePhase.PREFILL else 5.0
+
+
+def build(untied_head_seed=None):
+    cfg = qwen3_0_6b()
+    model = Qwen3ForCausalLM(cfg)
+    init_random_(model, seed=0, std=0.02, untied_head_seed=untied_head_seed)
+    model = model.to(torch.bfloat16)
+    weights = {k: v.clone() for k, v in model.state_dict().items()}
+    return model.to("cuda:0").eval(), qwen3_ref.ReferenceQwen3(cfg, weights, "cuda:0")
+
+
+@pytest.fixture(scope="module")
+def requests():
+    # 12 requests at 20 req/s, prompts up to 700 tokens, 24 outputs: a 256-token budget chunks them
+    return serving_requests(seed=1, num_requests=12, min_prompt=32, max_prompt=700, max_new_tokens=24)
+
+
+@pytest.mark.parametrize("untied_head_seed", [None, 1234], ids=["benchmark_model", "context_dependent_model"])
+def test_tokens_are_oracle_greedy_choices(requests, untied_head_seed):
+    model, ref = build(untied_head_seed)
+    mrr, budget = 8, 256
+    product = run_scheduler(PagedScheduleBackend(model, requests, mrr), requests, token_budget=budget,
+                            max_running_requests=mrr, eos_token_id=-1, stop_on_eos=False, step_clock=step_clock)
+    assert product.num_steps(SchedulePhase.PREFILL) > len(requests)  # prompts were chunked
+    backend = qwen3_ref.ReferenceScheduleBackend(ref, requests, mrr, forced_tokens=product.tokens)
+    oracle = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
+                           stop_on_eos=False, step_clock=step_clock)
+    assert [(e.phase, e.request_ids, e.chunk_spans) for e in product.events] == \
+        [(e.phase, e.request_ids, e.chunk_spans) for e in oracle.events]
+    records = backend.records
+    assert len(records) == sum(len(t) for t in product.tokens.values()) == 12 * 24
+    flips = [(r, tok, own, round(gap / std, 4)) for r, tok, own, gap, std in records if tok != own]
+    print(f"\n{len(records)} tokens, {len({t for _, t, _, _, _ in records})} distinct, {len(flips)} differ from "
+          f"the oracle's argmax (request, token, oracle argmax, gap / row std): {flips}")
+    assert all(gap <= TIE for _, _, _, gap in flips), flips
+    assert len(flips) <= MAX_TIE_FRACTION * len(records), flips

@@ -122,3 +122,33 @@ def test_chunk_without_history_is_whole_prompt_prefill():
     for (kc, vc), (kw, vw) in zip(cache_c, cache_w):
         assert torch.equal(kc, kw) and torch.equal(vc, vw)
 
+
+
+def serial_generate(model, prompt, max_new):
+    """One request alone: whole-prompt prefill, then dense-cache decode (reference serial baseline,
+    tests/unit/test_paged_scheduler.py:30-45)."""
+    toks, cache = qwen3_ref.prefill(model, [prompt])
+    out = [toks[0]]
+    for k in range(max_new - 1):
+        logits, cache = model.forward(torch.tensor([[out[-1]]]), position_ids=torch.tensor([[len(prompt) + k]]),
+                                      past_key_values=cache)
+        out.append(int(logits[0, -1].argmax()))
+    return out
+
+
+@pytest.mark.parametrize("budget,capacity,block_size", [(8, 2, 4), (5, 3, 1), (64, 4, 16)])
+def test_scheduled_paged_run_matches_serial_generation(budget, capacity, block_size):
+    """tests/unit/test_paged_scheduler.py:368-390 on the oracle backend: continuous batching with
+    chunked prefill produces each request's serial greedy sequence."""
+    from mini_infra_qwen3_amd.core import Request
+    from mini_infra_qwen3_amd.engine import run_scheduler
+
+    model = tiny_model()
+    prompts = [[(j * 7 + i * 3) % 90 + 1 for j in range(n)] for i, n in enumerate([13, 4, 9, 2, 16])]
+    budgets = [5, 7, 3, 6, 4]
+    requests = [Request(i, tuple(p), m, a) for i, (p, m, a) in enumerate(zip(prompts, budgets, [0, 0, 0, 1, 2]))]
+    backend = qwen3_ref.ReferenceScheduleBackend(model, requests, capacity, block_size=block_size)
+    result = run_scheduler(backend, requests, token_budget=budget, max_running_requests=capacity,
+                           step_clock=lambda out: 1.0)
+    for i, (p, m) in enumerate(zip(prompts, budgets)):
+        assert result.tokens[i] == serial_generate(model, p, m)
