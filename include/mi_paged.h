@@ -142,10 +142,10 @@ int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, const void*
  * Kernel 4 -- chunked-prefill attention on MFMA with the history read from the pool.
  *
  * Replaces, for one layer of PagedRunner.run_prefill_chunk_step
- * (src/mini_infra/worker/paged_runner.py:130-200): the history gather
+ * (src/mini_infra/worker/paged_runner.py:32-102): the history gather
  * PagedKVCachePool.gather_blocks (src/mini_infra/worker/paged_kv_cache.py:54-72), the
  * history/chunk concat of Qwen3Attention.forward (src/mini_infra/model/qwen3.py:325-330), the
- * visibility mask (paged_runner.py:179-187 with the causal mask of qwen3.py:477-484) and
+ * visibility mask (paged_runner.py:83-89 with the causal mask of qwen3.py:477-484) and
  * Qwen3Attention._attend (qwen3.py:219-255).
  *
  * Row b of the batch is a chunk of padded_len positions whose last chunk_lens[b] are real

@@ -3,7 +3,7 @@
 // Behaviour of a chunked-prefill layer of the reference: the history gather of
 // PagedKVCachePool.gather_blocks (src/mini_infra/worker/paged_kv_cache.py:54-72), the concat of
 // history and chunk in Qwen3Attention.forward (src/mini_infra/model/qwen3.py:325-330), the visibility
-// mask of PagedRunner.run_prefill_chunk_step (src/mini_infra/worker/paged_runner.py:179-187) with the
+// mask of PagedRunner.run_prefill_chunk_step (src/mini_infra/worker/paged_runner.py:83-89) with the
 // causal mask of Qwen3Model._prepare_position_ids_and_allowed_mask (qwen3.py:477-484), and
 // Qwen3Attention._attend (qwen3.py:219-255) -- as one flash-style kernel.
 //

@@ -164,7 +164,7 @@ def chunk_allowed_mask(start_lens: Sequence[int], chunk_lens: Sequence[int], num
                        block_size: int, padded_chunk_len: int) -> torch.Tensor:
     """``[B, 1, L, hist + L]`` visibility of a chunked-prefill step.
 
-    History slot k is visible iff k < start (src/mini_infra/worker/paged_runner.py:179-187); chunk
+    History slot k is visible iff k < start (src/mini_infra/worker/paged_runner.py:83-89); chunk
     key j is visible to chunk query i iff j <= i (causal, src/mini_infra/model/qwen3.py:477-484) and
     j is not left padding.
     """
