@@ -48,6 +48,24 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def profiled_traffic(kernel: str) -> int | None:
+    """HBM bytes per launch of ``kernel`` from the committed counter summary (profiles/hbm_traffic.md,
+    lines ``traffic <kernel> <bytes>``: rocprofv3 FETCH_SIZE and WRITE_SIZE per dispatch, scaled by
+    the same counters' reading for a copy of known size); None if absent."""
+    try:
+        with open(os.path.join(PROFILES, "hbm_traffic.md")) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 class EventTimer:
     """HIP events on the current stream (the one every data-plane kernel is launched on)."""
 
@@ -129,7 +147,8 @@ def bench_decode(steps: int, warmup: int, device: torch.device):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": profiled_traffic("paged_decode_attention"),
+            "algorithmic_bytes_per_launch": attn_bytes_per_launch,
         },
         "workload": w,
     }
@@ -214,7 +233,8 @@ def bench_scatter(steps: int, warmup: int, device: torch.device) -> dict:
     gbs = moved / (ms * 1e-3) / 1e9
     del pool, cache
     return {"workload": f"prefill scatter, 28 layers, 32 prompts U[128,2048] ({w.num_tokens} tokens), churned tables",
-            "ms_per_launch": ms, "bytes_per_launch": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS}
+            "ms_per_launch": ms, "bytes_per_launch": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
+            "traffic": profiled_traffic("reshape_and_cache")}
 
 
 # -------------------------------------------------------------------------------- gather
@@ -248,7 +268,28 @@ def bench_gather(steps: int, warmup: int, device: torch.device) -> dict:
     gbs = moved / (ms * 1e-3) / 1e9
     del pool
     return {"workload": "history gather, 28 layers, 4 prompts x 16384 tokens in 2048-token chunks (7 launches)",
-            "ms_per_prompt_set": ms, "bytes": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS}
+            "ms_per_prompt_set": ms, "bytes": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
+            "traffic_per_prompt_set": profiled_traffic("gather_blocks")}
+
+
+# ------------------------------------------------------------------------------ device copy
+def bench_copy(steps: int, device: torch.device, nbytes: int = 1 << 30) -> dict:
+    """torch's device-to-device copy of a 1 GiB buffer (reads and writes exactly ``nbytes`` per
+    launch): the reference point for read+write kernels, and the calibration workload of the HBM
+    traffic counters."""
+    src = torch.ones(nbytes, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    timer = EventTimer()
+    for _ in range(max(steps, 1)):
+        timer.start()
+        dst.copy_(src)
+        timer.stop()
+    ms = timer.mean_ms()
+    gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+    del src, dst
+    return {"workload": "torch device copy, 1 GiB", "bytes_per_launch": 2 * nbytes, "ms_per_launch": ms,
+            "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS}
 
 
 # ------------------------------------------------------------------------- chunked prefill
@@ -349,7 +390,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["decode", "prefill", "copy", "e2e", "all"], default="all")
+    parser.add_argument("--only", choices=["decode", "scatter", "gather", "prefill", "copy", "e2e", "all"],
+                        default="all")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of this path "
@@ -364,19 +406,15 @@ def main() -> int:
     _native.load()
     log(f"device {torch.cuda.get_device_name(device)}; library {_native.LIBRARY_PATH}")
 
-    if args.only == "copy":
-        # Calibration for HBM traffic counters: a plain device copy of known size (reads and
-        # writes exactly 1 GiB per launch), profiled with the same counters as the kernels.
-        src = torch.ones(1 << 30, dtype=torch.uint8, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(max(args.steps, 1)):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes_per_launch": src.numel(), "launches": max(args.steps, 1)}), flush=True)
-        return 0
-    if args.only == "prefill":
-        res = bench_prefill(args.steps, args.warmup, device)
-        log(f"chunked prefill: {res['ms_per_layer']:.2f} ms/layer, {res['achieved_TFLOPs']:.1f} TFLOP/s")
+    single = {
+        "copy": lambda: bench_copy(args.steps, device),
+        "scatter": lambda: bench_scatter(args.steps, args.warmup, device),
+        "gather": lambda: bench_gather(args.steps, args.warmup, device),
+        "prefill": lambda: bench_prefill(args.steps, args.warmup, device),
+    }
+    if args.only in single:  # one kernel alone (for counter runs)
+        res = single[args.only]()
+        log(f"{args.only}: {json.dumps(res)}")
         print(json.dumps(res), flush=True)
         return 0
     if args.only == "e2e":
@@ -410,6 +448,8 @@ def main() -> int:
         log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "
             f"{kernels['chunked_prefill']['achieved_TFLOPs']:.1f} TFLOP/s")
         torch.cuda.empty_cache()
+        kernels["device_copy"] = bench_copy(5, device)
+        log(f"device copy: {kernels['device_copy']['achieved_GBps']:.1f} GB/s")
     e2e = None
     if args.only == "all":
         e2e = bench_e2e(device)
