@@ -175,6 +175,48 @@ int32_t mi_chunked_prefill_attention(void* out, int64_t out_row_stride, int64_t 
                                      int32_t padded_len, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                      int32_t block_size, float scale, void* stream);
 
+/*
+ * Fused layer ops: the elementwise chains around attention in a Qwen3 decoder layer, one
+ * launch each, with the reference's bf16 rounding points.  All tensors are bf16, rows of
+ * contiguous elements, 16-byte aligned.
+ *
+ * mi_rms_norm -- RMSNorm (src/mini_infra/model/qwen3.py:55-78), optionally after the residual
+ * add of Qwen3DecoderLayer.forward (:368-400):
+ *   h = residual ? bf16(x + residual) : x;  residual_out = h (when residual is given)
+ *   out = bf16(weight * bf16(h * rsqrt(sum(h^2) / hidden + eps)))      (fp32 inside)
+ * x / residual / residual_out / out: [rows, hidden] contiguous; hidden a multiple of 8, <= 4096.
+ */
+int32_t mi_rms_norm(void* out, const void* x, const void* residual, void* residual_out, const void* weight,
+                    int64_t rows, int32_t hidden, float eps, void* stream);
+
+/*
+ * mi_qk_norm_rope -- per-head q/k RMSNorm and RoPE of Qwen3Attention._project_qkv
+ * (src/mini_infra/model/qwen3.py:182-217, 111-145):
+ *   q_out[t, h] = rope(bf16(q_weight * bf16(norm(q[t, h]))), cos[t], sin[t])
+ *   rope(x) = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)),  rotate_half(x) = cat(-x[64:], x[:64])
+ * and the same for k with k_weight; v is copied unchanged.
+ * Prefill form (slot_mapping == NULL): k and v go to k_out / v_out [T, Hkv, 128].
+ * Decode form: they go straight to pool slot slot_mapping[t * slot_stride] of key_pool /
+ * value_pool ([num_slots, Hkv, 128]) -- the reshape-and-cache append of
+ * _apply_paged_kv_pool (:282-283) fused in; out-of-range slots are skipped.
+ * q / k / v: token rows with element strides q_stride / k_stride / v_stride; cos / sin: [T, 128].
+ * q_out: [T, Hq, 128].  head_dim must be 128.
+ */
+int32_t mi_qk_norm_rope(void* q_out, void* k_out, void* v_out, const void* q, int64_t q_stride, const void* k,
+                        int64_t k_stride, const void* v, int64_t v_stride, const void* q_weight,
+                        const void* k_weight, const void* cos, const void* sin, int64_t num_tokens,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float eps,
+                        const int64_t* slot_mapping, int64_t slot_stride, void* key_pool, void* value_pool,
+                        int64_t num_slots, void* stream);
+
+/*
+ * mi_silu_mul -- the SwiGLU product of Qwen3MLP.forward (src/mini_infra/model/qwen3.py:347-355):
+ *   out = bf16(bf16(silu(gate)) * up),  silu(g) = g / (1 + exp(-g)) in fp32.
+ * gate / up / out: [rows, cols] with row element strides; cols and strides multiples of 8.
+ */
+int32_t mi_silu_mul(void* out, int64_t out_stride, const void* gate, int64_t gate_stride, const void* up,
+                    int64_t up_stride, int64_t rows, int32_t cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

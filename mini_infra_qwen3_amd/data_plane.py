@@ -18,7 +18,10 @@ __all__ = [
     "gather_blocks",
     "paged_decode_attention",
     "paged_decode_workspace_bytes",
+    "qk_norm_rope",
     "reshape_and_cache",
+    "rms_norm",
+    "silu_mul",
 ]
 
 
@@ -313,4 +316,115 @@ def chunked_prefill_attention(
         _stream(device),
     )
     _native.check(rc, "mi_chunked_prefill_attention")
+    return out
+
+
+# ----------------------------------------------------------------------------- fused layer ops
+def _require_bf16_rows(name: str, tensor: torch.Tensor, device: torch.device) -> None:
+    _require_gpu(name, tensor, device)
+    if tensor.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {tensor.dtype}")
+    if tensor.stride(-1) != 1:
+        raise ValueError(f"{name} must have a contiguous last dimension")
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+             residual: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """RMSNorm over the last dim, optionally of ``x + residual`` (one launch).
+
+    Returns ``(normed, h)`` with ``h = x + residual`` (or ``x`` itself without a residual): the
+    next residual of a decoder layer.  bf16, contiguous rows.
+    """
+    device = x.device
+    _require_bf16_rows("x", x, device)
+    _require_bf16_rows("weight", weight, device)
+    x = x.contiguous()
+    hidden = x.shape[-1]
+    if weight.shape != (hidden,):
+        raise ValueError(f"weight {tuple(weight.shape)} does not match hidden size {hidden}")
+    out = torch.empty_like(x)
+    res_out = x
+    res_ptr = None
+    if residual is not None:
+        _require_bf16_rows("residual", residual, device)
+        if residual.shape != x.shape:
+            raise ValueError(f"residual {tuple(residual.shape)} differs from x {tuple(x.shape)}")
+        residual = residual.contiguous()
+        res_out = torch.empty_like(x)
+        res_ptr = residual.data_ptr()
+    lib = _native.load()
+    rc = lib.mi_rms_norm(out.data_ptr(), x.data_ptr(), res_ptr, res_out.data_ptr() if res_ptr else None,
+                         weight.contiguous().data_ptr(), x.numel() // hidden, hidden, float(eps), _stream(device))
+    _native.check(rc, "mi_rms_norm")
+    return out, res_out
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: torch.Tensor,
+                 k_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float,
+                 slot_mapping: torch.Tensor | None = None, key_pool: torch.Tensor | None = None,
+                 value_pool: torch.Tensor | None = None):
+    """Per-head RMSNorm + RoPE of q and k, v passed through (one launch).
+
+    q ``[..., Hq * 128]``, k / v ``[..., Hkv * 128]`` over the same T tokens (row views of a
+    projection are fine); cos / sin ``[T, 128]`` (any leading shape with T tokens).
+    Returns ``q_out [T, Hq, 128]`` and, in the prefill form, ``k_out`` / ``v_out [T, Hkv, 128]``;
+    with ``slot_mapping`` (decode form) k and v are written into ``key_pool`` / ``value_pool``
+    ``[num_blocks, block_size, Hkv, 128]`` at those slots and ``(q_out, None, None)`` is returned.
+    """
+    device = q.device
+    for name, t in (("q", q), ("k", k), ("v", v), ("q_weight", q_weight), ("k_weight", k_weight),
+                    ("cos", cos), ("sin", sin)):
+        _require_bf16_rows(name, t, device)
+    head_dim = q_weight.shape[-1]
+    tokens = q.numel() // q.shape[-1]
+    num_heads, num_kv_heads = q.shape[-1] // head_dim, k.shape[-1] // head_dim
+    q2, k2, v2 = q.reshape(tokens, -1), k.reshape(tokens, -1), v.reshape(tokens, -1)
+    cos2, sin2 = cos.reshape(tokens, head_dim).contiguous(), sin.reshape(tokens, head_dim).contiguous()
+    if v.shape[-1] != k.shape[-1] or k_weight.shape != q_weight.shape:
+        raise ValueError("k / v / weights have inconsistent head sizes")
+    q_out = torch.empty((tokens, num_heads, head_dim), dtype=q.dtype, device=device)
+    k_out = v_out = None
+    lib = _native.load()
+    if slot_mapping is None:
+        k_out = torch.empty((tokens, num_kv_heads, head_dim), dtype=q.dtype, device=device)
+        v_out = torch.empty_like(k_out)
+        rc = lib.mi_qk_norm_rope(q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), q2.data_ptr(), q2.stride(0),
+                                 k2.data_ptr(), k2.stride(0), v2.data_ptr(), v2.stride(0), q_weight.data_ptr(),
+                                 k_weight.data_ptr(), cos2.data_ptr(), sin2.data_ptr(), tokens, num_heads,
+                                 num_kv_heads, head_dim, float(eps), None, 1, None, None, 0, _stream(device))
+    else:
+        _require_gpu("slot_mapping", slot_mapping, device)
+        _require_index("slot_mapping", slot_mapping, 1)
+        if slot_mapping.shape[0] != tokens:
+            raise ValueError(f"slot_mapping has {slot_mapping.shape[0]} entries for {tokens} tokens")
+        for name, pool in (("key_pool", key_pool), ("value_pool", value_pool)):
+            if pool is None:
+                raise ValueError(f"{name} is required with slot_mapping")
+            _require_bf16_rows(name, pool, device)
+            if not pool.is_contiguous() or pool.shape[-2:] != (num_kv_heads, head_dim):
+                raise ValueError(f"{name} must be contiguous [num_blocks, block_size, {num_kv_heads}, {head_dim}]")
+        num_slots = key_pool.numel() // (num_kv_heads * head_dim)
+        rc = lib.mi_qk_norm_rope(q_out.data_ptr(), None, None, q2.data_ptr(), q2.stride(0), k2.data_ptr(),
+                                 k2.stride(0), v2.data_ptr(), v2.stride(0), q_weight.data_ptr(), k_weight.data_ptr(),
+                                 cos2.data_ptr(), sin2.data_ptr(), tokens, num_heads, num_kv_heads, head_dim,
+                                 float(eps), slot_mapping.data_ptr(), slot_mapping.stride(0), key_pool.data_ptr(),
+                                 value_pool.data_ptr(), num_slots, _stream(device))
+    _native.check(rc, "mi_qk_norm_rope")
+    return q_out, k_out, v_out
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``bf16(bf16(silu(gate)) * up)`` elementwise (one launch); gate / up ``[..., I]`` row views."""
+    device = gate.device
+    _require_bf16_rows("gate", gate, device)
+    _require_bf16_rows("up", up, device)
+    if gate.shape != up.shape:
+        raise ValueError(f"gate {tuple(gate.shape)} and up {tuple(up.shape)} differ")
+    cols = gate.shape[-1]
+    rows = gate.numel() // cols
+    g2, u2 = gate.reshape(rows, cols), up.reshape(rows, cols)
+    out = torch.empty(gate.shape, dtype=gate.dtype, device=device)
+    rc = _native.load().mi_silu_mul(out.data_ptr(), cols, g2.data_ptr(), g2.stride(0), u2.data_ptr(), u2.stride(0),
+                                    rows, cols, _stream(device))
+    _native.check(rc, "mi_silu_mul")
     return out

@@ -5,13 +5,15 @@ SwiGLU, tied lm_head) follow the reference model (src/mini_infra/model/qwen3.py:
 state_dict loads unchanged.  The attention differs in how it reaches K/V:
 
 * decode (``PagedAttentionMetadata``, one token per sequence): the new K/V rows go into the pool
-  through the reshape-and-cache kernel, then paged GQA decode attention reads the context from
-  the pool (replaces qwen3.py:257-292 + :219-255, no gather, no repeat_interleave);
+  slots straight from the fused q/k-norm + RoPE launch, then paged GQA decode attention reads the
+  context from the pool (replaces qwen3.py:257-292 + :219-255, no gather, no repeat_interleave);
 * prefill (``PagedPrefillMetadata``, or no metadata for a whole left-padded prompt): the MFMA
   chunked-prefill kernel attends causally within the chunk and reads the history straight from
   the pool through the block table (replaces the gather + concat + _attend chain).
 
-Dense GEMMs (projections, MLP, lm_head) stay on PyTorch-ROCm.
+Dense GEMMs (projections, MLP, lm_head) stay on PyTorch-ROCm; the elementwise chains around them
+run as fused launches of the same library (``data_plane.rms_norm`` with the residual add,
+``qk_norm_rope`` with the decode append, ``silu_mul``), keeping the reference's bf16 rounding points.
 """
 
 from __future__ import annotations
@@ -19,7 +21,6 @@ from __future__ import annotations
 from typing import NamedTuple
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from mini_infra_qwen3_amd import data_plane
@@ -53,18 +54,17 @@ class PagedPrefillMetadata(NamedTuple):
 
 
 class RMSNorm(nn.Module):
-    """x * rsqrt(mean(x^2) + eps) in fp32, cast back, times weight (reference qwen3.py:55-78)."""
+    """RMSNorm weight holder (reference qwen3.py:55-78).  The norm itself runs fused with the
+    preceding residual add in ``data_plane.rms_norm`` (fp32 inside, reference rounding points)."""
 
     def __init__(self, hidden_size: int, eps: float):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(hidden_size))
         self.eps = eps
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        dtype = x.dtype
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
-        return self.weight * xf.to(dtype)
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """(normed, x + residual): the normalised input of the next block and the new residual."""
+        return data_plane.rms_norm(x, self.weight, self.eps, residual)
 
 
 class RotaryEmbedding(nn.Module):
@@ -94,11 +94,6 @@ class RotaryEmbedding(nn.Module):
         return emb.cos().to(dtype), emb.sin().to(dtype)
 
 
-def _rotate_half(x: torch.Tensor) -> torch.Tensor:
-    half = x.shape[-1] // 2
-    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
-
-
 class Qwen3Attention(nn.Module):
     def __init__(self, config: Qwen3Config):
         super().__init__()
@@ -113,35 +108,34 @@ class Qwen3Attention(nn.Module):
         self.q_norm = RMSNorm(config.head_dim, config.rms_norm_eps)
         self.k_norm = RMSNorm(config.head_dim, config.rms_norm_eps)
 
-    def _project(self, hidden: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
-        """q ``[B, H, L, D]`` and k ``[B, Hkv, L, D]`` (normed, rotated, contiguous), v ``[B, Hkv, L, D]``
-        (a transpose view), as the reference produces them (qwen3.py:182-217)."""
-        batch, length, _ = hidden.shape
-        q = self.q_norm(self.q_proj(hidden).view(batch, length, self.num_heads, self.head_dim)).transpose(1, 2)
-        k = self.k_norm(self.k_proj(hidden).view(batch, length, self.num_kv_heads, self.head_dim)).transpose(1, 2)
-        v = self.v_proj(hidden).view(batch, length, self.num_kv_heads, self.head_dim).transpose(1, 2)
-        cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
-        q = q * cos + _rotate_half(q) * sin
-        k = k * cos + _rotate_half(k) * sin
-        return q, k, v
-
     def forward(self, hidden, cos, sin, kv_pool: PastKeyValue, metadata, workspace=None):
+        """q/k/v projections (PyTorch GEMMs), then one fused launch for q/k RMSNorm + RoPE (plus,
+        when decoding, the K/V append into the pool), then paged attention."""
         batch, length, _ = hidden.shape
-        q, k, v = self._project(hidden, cos, sin)
+        q, k, v = self.q_proj(hidden), self.k_proj(hidden), self.v_proj(hidden)
         key_pool, value_pool = kv_pool
+        eps = self.q_norm.eps
         if isinstance(metadata, PagedAttentionMetadata):
-            data_plane.reshape_and_cache([k], [v], metadata.slot_mapping, [key_pool], [value_pool])
+            q_rot, _, _ = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin, eps,
+                                                  slot_mapping=metadata.slot_mapping, key_pool=key_pool,
+                                                  value_pool=value_pool)
             out = data_plane.paged_decode_attention(
-                q.view(batch, self.num_heads, self.head_dim), key_pool, value_pool, metadata.block_tables,
-                metadata.context_lens, self.scaling, workspace=workspace,
+                q_rot, key_pool, value_pool, metadata.block_tables, metadata.context_lens, self.scaling,
+                workspace=workspace,
             ).view(batch, 1, -1)
             present = kv_pool
         else:
+            q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin,
+                                                           eps)
+            # token-major [B, L, H, D] buffers seen as [B, H, L, D] (strided views, no copies)
+            q_rot = q_rot.view(batch, length, self.num_heads, self.head_dim).transpose(1, 2)
+            k_rot = k_rot.view(batch, length, self.num_kv_heads, self.head_dim).transpose(1, 2)
+            v_rows = v_rows.view(batch, length, self.num_kv_heads, self.head_dim).transpose(1, 2)
             out = data_plane.chunked_prefill_attention(
-                q, k, v, key_pool, value_pool, metadata.history_block_tables, metadata.start_lens,
+                q_rot, k_rot, v_rows, key_pool, value_pool, metadata.history_block_tables, metadata.start_lens,
                 metadata.chunk_lens, self.scaling,
             )
-            present = (k, v)
+            present = (k_rot, v_rows)
         return self.o_proj(out), present
 
 
@@ -153,7 +147,7 @@ class Qwen3MLP(nn.Module):
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        return self.down_proj(data_plane.silu_mul(self.gate_proj(x), self.up_proj(x)))
 
 
 class Qwen3DecoderLayer(nn.Module):
@@ -164,11 +158,14 @@ class Qwen3DecoderLayer(nn.Module):
         self.input_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
 
-    def forward(self, hidden, cos, sin, kv_pool, metadata, workspace=None):
-        attn, present = self.self_attn(self.input_layernorm(hidden), cos, sin, kv_pool, metadata, workspace)
-        hidden = hidden + attn
-        hidden = hidden + self.mlp(self.post_attention_layernorm(hidden))
-        return hidden, present
+    def forward(self, hidden, residual, cos, sin, kv_pool, metadata, workspace=None):
+        """Pre-norm block in residual-stream form: takes the previous block's output and the
+        residual before it (None for the first layer), returns the MLP output and the residual
+        (the reference's hidden state is their sum, formed by the next norm's fused add)."""
+        x, residual = self.input_layernorm(hidden, residual)
+        attn, present = self.self_attn(x, cos, sin, kv_pool, metadata, workspace)
+        x, residual = self.post_attention_layernorm(attn, residual)
+        return self.mlp(x), residual, present
 
 
 class Qwen3Model(nn.Module):
@@ -187,8 +184,10 @@ class Qwen3Model(nn.Module):
 
     def forward(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
                 position_ids: torch.Tensor | None = None,
-                attn_metadata: PagedAttentionMetadata | PagedPrefillMetadata | None = None):
-        """Returns (final hidden states ``[B, L, hidden]``, per-layer present K/V).
+                attn_metadata: PagedAttentionMetadata | PagedPrefillMetadata | None = None,
+                last_only: bool = False):
+        """Returns (final hidden states ``[B, L, hidden]``, or ``[B, 1, hidden]`` of the last position
+        with ``last_only``, and the per-layer present K/V).
 
         Decode (``PagedAttentionMetadata``): input_ids / position_ids ``[B, 1]``.  Prefill: a
         left-padded ``[B, L]`` chunk; without metadata, ``attention_mask`` (left padding, True on
@@ -236,10 +235,13 @@ class Qwen3Model(nn.Module):
                 position_ids = torch.where(offset >= 0, offset + metadata.start_lens.unsqueeze(1), 0)
         cos, sin = self.rotary_emb(position_ids, hidden.dtype)
         presents: list[PastKeyValue] = []
+        residual = None
         for layer, kv_pool in zip(self.layers, pools):
-            hidden, present = layer(hidden, cos, sin, kv_pool, metadata, workspace)
+            hidden, residual, present = layer(hidden, residual, cos, sin, kv_pool, metadata, workspace)
             presents.append(present)
-        return self.norm(hidden), presents
+        if last_only:  # the norm is row-wise: only the position the sampler reads
+            hidden, residual = hidden[:, -1:, :], residual[:, -1:, :]
+        return self.norm(hidden, residual)[0], presents
 
 
 class Qwen3ForCausalLM(nn.Module):
@@ -255,9 +257,7 @@ class Qwen3ForCausalLM(nn.Module):
                 last_logits_only: bool = False):
         """(logits, present K/V).  ``last_logits_only`` projects only the last position (``[B, 1, V]``):
         greedy sampling reads nothing else (reference sampler.py:9-23)."""
-        hidden, presents = self.model(input_ids, attention_mask, position_ids, attn_metadata)
-        if last_logits_only:
-            hidden = hidden[:, -1:, :]
+        hidden, presents = self.model(input_ids, attention_mask, position_ids, attn_metadata, last_logits_only)
         return self.lm_head(hidden), presents
 
 

@@ -3,9 +3,10 @@ model, same bf16 weights, in the scenarios of the reference suite (tests/unit/te
 at the Qwen3 attention shape (16 / 8 heads of 128, block 16).
 
 The oracle runs twice: on the CPU (greedy tokens must agree) and on cuda:0, where its GEMMs are the
-product's own, so that everything but attention is bit-identical: layer-0 K/V (upstream of any
-attention) must match bit for bit; deeper layers carry only the attention kernels' rounding
-differences (max-abs within ``DEEP_ATOL``: a wrong block, slot or position moves values by O(1))."""
+product's own, so that only the fused elementwise launches and attention differ: layer-0 K/V
+(upstream of any attention) must match within one bf16 ulp (the fused RMSNorm sums squares in
+another order); deeper layers carry the attention kernels' rounding differences (max-abs within
+``DEEP_ATOL``: a wrong block, slot or position moves values by O(1))."""
 
 import pytest
 import torch
@@ -42,7 +43,7 @@ def models():
 def assert_kv_close(layer, got, want):
     got, want = got.float().cpu(), want.float().cpu()
     if layer == 0:
-        assert torch.equal(got, want)
+        assert ((got - want).abs() <= want.abs() * 2.0 ** -7).all()
     else:
         assert (got - want).abs().max().item() <= DEEP_ATOL
 
