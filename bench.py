@@ -341,7 +341,9 @@ def bench_e2e(device: torch.device, seed: int = 0) -> dict:
     requests) of a random-init Qwen3-0.6B (bf16, N(0, 0.02), tied embeddings): 128 requests, Poisson
     arrivals at 20 req/s, prompts U[32, 1024], 128 greedy tokens each, EOS disabled.  Output tok/s =
     output tokens x 1000 / busy_ms, busy_ms = sum over steps of (device-timed forward + host-timed
-    cache management), on the logical clock the measured step times advance."""
+    cache management), on the logical clock the measured step times advance.  The decode forward
+    is replayed from HIP graphs captured per padded (batch, blocks) bucket when the backend is set
+    up (``setup_s``, outside the timed run)."""
     from mini_infra_qwen3_amd.core.scheduler import SchedulePhase
     from mini_infra_qwen3_amd.engine import PagedScheduleBackend, run_scheduler
     from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
@@ -352,12 +354,14 @@ def bench_e2e(device: torch.device, seed: int = 0) -> dict:
     model = model.to(device=device, dtype=torch.bfloat16).eval()
 
     def run(requests):
-        backend = PagedScheduleBackend(model, requests, len(requests))
-        return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False)
+        t0 = time.perf_counter()
+        backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True)
+        setup_s = time.perf_counter() - t0
+        return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False), setup_s
 
     run(serving_requests(seed=seed + 1, num_requests=8, max_new_tokens=8))  # warm-up: kernels, GEMM choices
     requests = serving_requests(seed=seed)
-    res = run(requests)
+    res, setup_s = run(requests)
     decode = [e for e in res.events if e.phase is SchedulePhase.DECODE]
     prefill = [e for e in res.events if e.phase is SchedulePhase.PREFILL]
     out = {
@@ -378,6 +382,8 @@ def bench_e2e(device: torch.device, seed: int = 0) -> dict:
         "prefill_step_ms_mean": round(sum(e.step_ms for e in prefill) / max(len(prefill), 1), 3),
         "requests": len(requests),
         "arrival_rate_req_s": 20.0,
+        "decode_graphs": True,
+        "setup_s": round(setup_s, 2),
     }
     del model, res
     torch.cuda.empty_cache()

@@ -39,7 +39,10 @@ class PagedScheduleBackend:
     """Owns the pool and the block allocator; runs prefill chunks and decode steps through PagedRunner."""
 
     def __init__(self, model: torch.nn.Module, requests: Sequence[Request], max_running_requests: int,
-                 paged_cache_config: PagedCacheConfig = PagedCacheConfig(), pad_token_id: int = 0):
+                 paged_cache_config: PagedCacheConfig = PagedCacheConfig(), pad_token_id: int = 0,
+                 decode_graphs: bool = False):
+        """``decode_graphs``: capture the decode forward in HIP graphs for every padded (batch, blocks)
+        bucket this run can reach, before the run (as serving engines do at start-up)."""
         self.model = model
         self.device = next(model.parameters()).device
         self.block_size = paged_cache_config.block_size
@@ -55,6 +58,9 @@ class PagedScheduleBackend:
                                      config.num_key_value_heads, config.head_dim,
                                      next(model.parameters()).dtype, self.device)
         self.kv_cache_manager = KVCacheManager(self.block_size, num_blocks)
+        if decode_graphs:
+            self.runner.enable_decode_graphs(self.pool, max_batch=min(max_running_requests, len(requests)),
+                                             max_blocks=largest)
 
     def _live_bytes(self) -> int:
         return self.kv_cache_manager.num_used_blocks * self.pool.bytes_per_block

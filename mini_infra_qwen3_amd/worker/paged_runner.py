@@ -9,7 +9,11 @@ Same entry points, arguments and return types as the reference's PagedRunner
   (``[B, H_kv, padded_chunk_len, D]`` per layer; the reference returns history + chunk, of which
   ``store_prefill`` only ever reads the chunk's tail);
 * ``store_prefill`` is one scatter launch for all layers;
-* ``run_decode_step`` appends and attends through the pool (see ``model.qwen3``).
+* ``run_decode_step`` appends and attends through the pool (see ``model.qwen3``).  With
+  ``enable_decode_graphs`` the whole decode forward is captured once per padded (batch, blocks)
+  bucket in a HIP graph: ``prepare_decode_inputs`` then packs the step (pad rows: slot -1 = no
+  append, context 0 = zero output) straight into the bucket's static metadata buffer with one
+  upload, and ``run_decode_step`` replays the graph -- one launch instead of ~300.
 """
 
 from __future__ import annotations
@@ -17,6 +21,7 @@ from __future__ import annotations
 from collections.abc import Sequence
 from typing import NamedTuple
 
+import numpy as np
 import torch
 
 from mini_infra_qwen3_amd.device import StepTimer
@@ -30,6 +35,42 @@ from mini_infra_qwen3_amd.worker.sampler import greedy_sample
 _NULL_BLOCK_ID = 0
 
 
+class _DecodeGraph:
+    """The decode forward of one padded bucket, captured over a static packed-metadata buffer
+    ``[batch, 4 + blocks]`` (token, position, slot, context length, block table)."""
+
+    def __init__(self, model: torch.nn.Module, pool: PagedKVCachePool, batch: int, blocks: int,
+                 device: torch.device):
+        self.batch, self.blocks = batch, blocks
+        self.static = torch.zeros((batch, 4 + blocks), dtype=torch.long, device=device)
+        self.static[:, 2] = -1  # every row is padding until a step is loaded
+        ids, pos, meta = self.views(batch)
+        meta = meta._replace(kv_pools=tuple(pool.kv_pools))
+        side = torch.cuda.Stream(device)  # default priority
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side), torch.inference_mode():
+            for _ in range(2):  # warm-up outside the capture: GEMM choices, library state
+                model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
+        torch.cuda.current_stream(device).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph), torch.inference_mode():
+            logits, _ = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
+        self.logits = logits[:, -1]
+
+    def views(self, rows: int):
+        s = self.static[:rows]
+        return s[:, 0:1], s[:, 1:2], PagedAttentionMetadata(slot_mapping=s[:, 2], block_tables=s[:, 4:],
+                                                            context_lens=s[:, 3])
+
+    def load(self, packed: np.ndarray) -> None:
+        """Copies a host-packed ``[rows, 4 + nb]`` step in, padding rows and block columns."""
+        rows, cols = packed.shape
+        full = np.zeros((self.batch, 4 + self.blocks), dtype=np.int64)
+        full[:, 2] = -1
+        full[:rows, :cols] = packed
+        self.static.copy_(torch.from_numpy(full))
+
+
 class PagedDecodeOutput(NamedTuple):
     """Next token per row (input order) and the model time in ms."""
 
@@ -38,7 +79,41 @@ class PagedDecodeOutput(NamedTuple):
 
 
 class PagedRunner(BaseModelRunner):
-    """Stateless runner driving a PagedKVCachePool (reference paged_runner.py:29)."""
+    """Runner driving a PagedKVCachePool (reference paged_runner.py:29); stateless unless decode
+    graphs are enabled."""
+
+    def __init__(self, model: torch.nn.Module, pad_token_id: int = 0):
+        super().__init__(model, pad_token_id)
+        self._graphs: dict[tuple[int, int], _DecodeGraph] = {}
+        self._graph_pool: PagedKVCachePool | None = None
+        self._batch_buckets: list[int] = []
+        self._block_buckets: list[int] = []
+        self._loaded: tuple[_DecodeGraph, int] | None = None
+
+    def enable_decode_graphs(self, pool: PagedKVCachePool, max_batch: int, max_blocks: int,
+                             batch_buckets: Sequence[int] | None = None, block_quantum: int = 16) -> None:
+        """Captures the decode forward for every (batch bucket, block bucket) up to ``max_batch``
+        rows and ``max_blocks`` blocks per row, over ``pool``.  Steps outside the buckets, or on
+        another pool, run without a graph."""
+        if self.device.type != "cuda":
+            raise RuntimeError("decode graphs need the GPU")
+        if batch_buckets is None:
+            batch_buckets = [b for b in (1, 2, 4, 8, 12, 16, 24, 32, 48, 64, 80, 96, 112, 128, 160, 192, 224, 256)
+                             if b < max_batch] + [max_batch]
+        self._batch_buckets = sorted(set(int(b) for b in batch_buckets if 0 < b <= max_batch))
+        top = -(-max_blocks // block_quantum) * block_quantum
+        self._block_buckets = list(range(block_quantum, top + 1, block_quantum))
+        self._graph_pool = pool
+        self._graphs = {}
+        for b in self._batch_buckets:
+            for nb in self._block_buckets:
+                self._graphs[(b, nb)] = _DecodeGraph(self.model, pool, b, nb, self.device)
+        torch.cuda.synchronize(self.device)
+
+    def _bucket(self, rows: int, blocks: int) -> _DecodeGraph | None:
+        b = next((x for x in self._batch_buckets if x >= rows), None)
+        nb = next((x for x in self._block_buckets if x >= blocks), None)
+        return None if b is None or nb is None else self._graphs[(b, nb)]
 
     def run_prefill_chunk_step(
         self,
@@ -98,7 +173,14 @@ class PagedRunner(BaseModelRunner):
         """Packs one decode step as ``[B, 4 + max_blocks]`` and uploads it once (reference
         paged_runner.py:138-166).  Returns column views: input_ids / position_ids ``[B, 1]`` and the
         metadata's slot_mapping, block_tables and context_lens."""
-        packed = torch.from_numpy(pack_decode_rows(block_tables, last_tokens, positions, block_size)).to(self.device)
+        rows = pack_decode_rows(block_tables, last_tokens, positions, block_size)
+        graph = self._bucket(*rows.shape) if self._graphs and block_size == self._graph_pool.block_size else None
+        self._loaded = None
+        if graph is not None:
+            graph.load(rows)
+            self._loaded = (graph, rows.shape[0])
+            return graph.views(rows.shape[0])
+        packed = torch.from_numpy(rows).to(self.device)
         metadata = PagedAttentionMetadata(slot_mapping=packed[:, 2], block_tables=packed[:, 4:],
                                           context_lens=packed[:, 3])
         return packed[:, 0:1], packed[:, 1:2], metadata
@@ -111,6 +193,14 @@ class PagedRunner(BaseModelRunner):
         pool: PagedKVCachePool,
     ) -> PagedDecodeOutput:
         """One decode step: append the new K/V into the pool and attend (reference paged_runner.py:168-189)."""
+        loaded = self._loaded
+        if (loaded is not None and pool is self._graph_pool and input_ids.shape[0] == loaded[1]
+                and metadata.slot_mapping.data_ptr() == loaded[0].static[:, 2].data_ptr()):
+            graph, rows = loaded
+            with StepTimer(self.device) as timer:
+                graph.graph.replay()
+                next_token = torch.argmax(graph.logits[:rows], dim=-1)
+            return PagedDecodeOutput(next_token.tolist(), timer.elapsed_ms)
         with StepTimer(self.device) as timer:
             logits, _ = self.model(input_ids, position_ids=position_ids,
                                    attn_metadata=metadata._replace(kv_pools=tuple(pool.kv_pools)))

@@ -52,12 +52,14 @@ def requests():
     return serving_requests(seed=1, num_requests=12, min_prompt=32, max_prompt=700, max_new_tokens=24)
 
 
-@pytest.mark.parametrize("untied_head_seed", [None, 1234], ids=["benchmark_model", "context_dependent_model"])
-def test_tokens_are_oracle_greedy_choices(requests, untied_head_seed):
+@pytest.mark.parametrize("untied_head_seed,graphs", [(None, True), (1234, False)],
+                         ids=["benchmark_model_decode_graphs", "context_dependent_model"])
+def test_tokens_are_oracle_greedy_choices(requests, untied_head_seed, graphs):
     model, ref = build(untied_head_seed)
     mrr, budget = 8, 256
-    product = run_scheduler(PagedScheduleBackend(model, requests, mrr), requests, token_budget=budget,
-                            max_running_requests=mrr, eos_token_id=-1, stop_on_eos=False, step_clock=step_clock)
+    backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=graphs)
+    product = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
+                            stop_on_eos=False, step_clock=step_clock)
     assert product.num_steps(SchedulePhase.PREFILL) > len(requests)  # prompts were chunked
     backend = qwen3_ref.ReferenceScheduleBackend(ref, requests, mrr, forced_tokens=product.tokens)
     oracle = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,

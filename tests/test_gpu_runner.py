@@ -264,3 +264,53 @@ def test_chunked_prefill_matches_oracle_runner(models):
                 got = request_kv(pool, layer, tables[r], len(p))[kv]
                 want = torch.cat([ref_pools[layer][kv][b] for b in tables[r]])[:len(p)].transpose(0, 1)
                 assert_kv_close(layer, got, want)
+
+
+def test_decode_graph_replays_match_eager_forward_and_touch_only_live_slots(models):
+    """Decode graphs: each replay equals an eager forward of the same padded inputs, bit for bit,
+    with eager work and syncs between replays; pad rows write nothing; batches shrink and grow
+    across buckets and contexts cross block boundaries."""
+    model = models[0]
+    cfg = model.config
+    prompts = prompts_of([30, 17, 5, 44], seed=7)
+    manager = KVCacheManager(BS, num_blocks=40)
+    pool = make_pool(cfg, 40)
+    runner = PagedRunner(model)
+    runner.enable_decode_graphs(pool, max_batch=4, max_blocks=8, batch_buckets=[1, 2, 4])
+    for i, p in enumerate(prompts):
+        manager.allocate_slots(i, len(p))
+    out = runner.run_prefill_step(prompts)
+    runner.store_prefill(pool, out.prefill_cache, [manager.block_table(i) for i in range(4)],
+                         [len(p) for p in prompts], [0] * 4)
+    tokens = {i: [t] for i, t in enumerate(out.next_tokens)}
+    lengths = {i: len(p) for i, p in enumerate(prompts)}
+    schedule = [[0, 1, 2, 3], [0, 1, 2], [0, 2], [2], [1, 3], [0, 1, 2, 3], [3, 1]]
+    replays = 0
+    with torch.inference_mode():
+        for active in schedule:
+            for i in active:
+                assert manager.allocate_slots(i, 1)
+            tables = [manager.block_table(i) for i in active]
+            ids, pos, meta = runner.prepare_decode_inputs(tables, [tokens[i][-1] for i in active],
+                                                          [lengths[i] for i in active], BS)
+            graph = runner._loaded[0]
+            assert graph.batch >= len(active) and meta.slot_mapping.data_ptr() == graph.static[:, 2].data_ptr()
+            full_ids, full_pos, full_meta = graph.views(graph.batch)
+            before = [t.clone() for kv in pool.kv_pools for t in kv]
+            eager = model(full_ids, position_ids=full_pos,
+                          attn_metadata=full_meta._replace(kv_pools=tuple(pool.kv_pools)),
+                          last_logits_only=True)[0][:, -1]
+            torch.cuda.synchronize()
+            got = runner.run_decode_step(ids, pos, meta, pool)
+            replays += 1
+            assert torch.equal(graph.logits, eager), f"replay {replays} differs from the eager forward"
+            assert got.next_tokens == eager[:len(active)].argmax(-1).tolist()
+            live = set(meta.slot_mapping.tolist())
+            after = [t for kv in pool.kv_pools for t in kv]
+            for b, a in zip(before, after):
+                changed = (b.view(-1, 8 * 128) != a.view(-1, 8 * 128)).any(dim=1).nonzero().flatten().tolist()
+                assert set(changed) <= live
+            for i, t in zip(active, got.next_tokens):
+                tokens[i].append(t)
+                lengths[i] += 1
+    assert replays == len(schedule)
