@@ -97,9 +97,11 @@ int32_t mi_gather_blocks(const void* const* key_pools, const void* const* value_
                          int32_t num_layers, int64_t block_bytes, void* stream);
 
 /*
- * Workspace for mi_paged_decode_attention: bytes of float scratch for the
- * split-context partial results (0 if no sequence can need more than one
- * 512-token partition, i.e. max_blocks <= 32).  No initialisation needed.
+ * Workspace for mi_paged_decode_attention: bytes of float scratch for the partial
+ * results of sequences cut between two of the launch's equal block ranges -- two slots
+ * per range per query head, (128 + 2) floats each.  It depends on the device's CU count and,
+ * for small launches, on batch * max_blocks; never on the context lengths.  0 when
+ * batch or max_blocks is 0.  No initialisation needed.
  */
 int64_t mi_paged_decode_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t num_heads,
                                         int32_t head_dim, int32_t block_size);
@@ -125,8 +127,9 @@ int64_t mi_paged_decode_workspace_bytes(int32_t batch, int32_t max_blocks, int32
  * block_tables: `[batch, max_blocks]` int64 with row element stride; ids outside
  *   [0, num_blocks) read the null block 0 instead.  context_lens: int64 with element stride.
  * workspace: at least mi_paged_decode_workspace_bytes(...) bytes (may be null when
- *   max_blocks <= 32).  Contexts longer than 512 tokens are split into 512-token
- *   partitions whose partial results a second launch merges.
+ *   max_blocks is 0).  The launch's blocks are cut into equal ranges, one per workgroup
+ *   (and head group); sequences cut between ranges leave partials that a second, small
+ *   launch merges (it also writes the zero rows).
  * Specialised for head_dim 128, block_size 16 and num_heads = 2 * num_kv_heads with
  * num_kv_heads in {1, 2, 4, 8}; other shapes return MI_ERR_UNSUPPORTED.
  */

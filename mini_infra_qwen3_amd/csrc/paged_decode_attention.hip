@@ -6,14 +6,19 @@
 // _repeat_key_value (:219-255, :147-156) -- computed straight from the pool, without
 // materialising the padded history or the repeated K/V.
 //
-// Work decomposition (MI355X: 256 CUs, 64-lane wavefronts, bandwidth-bound):
-//  * A work unit is (sequence b, partition of kPartBlocks pool blocks of its context,
-//    group of kWaves KV heads).  Wavefront w of the group serves KV head g and both query
-//    heads 2g, 2g+1 that share it (GQA group 2), so every K/V byte is loaded exactly once.
-//  * Persistent workgroups (a few per CU, MI_DECODE_PERSISTENT=1): each workgroup first turns
-//    the context lengths into a prefix sum of partitions per sequence in LDS, then walks the
-//    compact unit list with a grid stride -- no empty workgroups for short sequences.  With
-//    MI_DECODE_PERSISTENT=0 the grid is (partitions x head groups, batch), one unit each.
+// Work decomposition (MI355X: 256 CUs in 8 XCDs, 64-lane wavefronts, bandwidth-bound):
+//  * The work of one launch is the list of (sequence, pool block) pairs, sequences in order,
+//    N blocks in all.  It is cut into `streams` contiguous ranges of N / streams blocks (+-1),
+//    and workgroup (stream s, head group hg) streams range s for the kWaves KV heads of hg.
+//    Every workgroup gets the same number of blocks whatever the context lengths, and the
+//    head groups of one range run side by side (adjacent workgroup ids), so the 2 KiB pool
+//    rows of a block are read by concurrent workgroups.  Wavefront w of a group serves KV
+//    head g and both query heads 2g, 2g+1 that share it (GQA group 2): every K/V byte is
+//    loaded exactly once.
+//  * Each workgroup first turns the context lengths into a prefix sum of blocks per sequence
+//    in LDS (so a block index maps to its sequence by binary search); block ids of the next
+//    64 blocks of the range are fetched one per lane, a window ahead, and broadcast with
+//    readlane.
 //  * Inside a wavefront, lane = 16 * row + dl.  Lane dl holds dims [8 dl, 8 dl + 8) of the
 //    two query rows; row r owns tokens 4 i + r (i = 0..3) of every 16-token block.  One
 //    16-byte load per lane per i brings four 256-byte (token, head) rows per instruction.
@@ -26,12 +31,17 @@
 //  * PV: probabilities of token pairs are packed to bf16 and v_perm regroups V so that one
 //    v_dot2 covers two tokens of one dim.
 //  * K/V of the next kDepth-1 blocks are in flight in registers while the current block
-//    is computed (a register ring: the VGPR file is 512 KiB per CU, LDS is 160 KiB).
-//  * Rows merge at the end of the partition (log-sum-exp).  A sequence with one partition
-//    writes bf16 output directly.  Otherwise the partition's (m, l, acc) go to the caller's
-//    workspace and a second, small kernel merges the partitions.  (Merging inside the first
-//    kernel needs device-scope release/acquire fences per partition, and on this GPU each
-//    such fence writes back and invalidates a whole XCD L2: far more costly than a launch.)
+//    is computed (a register ring: the VGPR file is 512 KiB per CU, LDS is 160 KiB).  The
+//    ring runs straight across sequence boundaries, so the memory pipeline never drains
+//    inside a range.
+//  * At the end of a sequence's segment the four rows merge (log-sum-exp).  A sequence whose
+//    blocks all lie in one range writes its bf16 output directly.  A sequence cut by a range
+//    boundary leaves (m, l, acc) partials: a range holds at most two cut sequences (its first
+//    and its last), so the caller's workspace is 2 slots per range per head, whatever the
+//    batch and context lengths.  A second, small kernel merges the cut sequences and writes
+//    zero rows for empty contexts.  (Merging inside the first kernel needs device-scope
+//    release/acquire fences, and on this GPU each such fence writes back and invalidates a
+//    whole XCD L2: far more costly than a launch.)
 #include "mi_common.h"
 
 namespace mi {
@@ -40,9 +50,6 @@ namespace {
 constexpr int kHeadDim = 128;
 constexpr int kBlockSize = 16;
 constexpr int kGroup = 2;          // query heads per KV head
-#ifndef MI_DECODE_PART_BLOCKS
-#define MI_DECODE_PART_BLOCKS 32
-#endif
 #ifndef MI_DECODE_DEPTH
 #define MI_DECODE_DEPTH 2
 #endif
@@ -55,21 +62,17 @@ constexpr int kGroup = 2;          // query heads per KV head
 #ifndef MI_DECODE_GROUPS_PER_CU
 #define MI_DECODE_GROUPS_PER_CU 4
 #endif
-#ifndef MI_DECODE_PERSISTENT
-#define MI_DECODE_PERSISTENT 1
-#endif
-constexpr int kPartBlocks = MI_DECODE_PART_BLOCKS;  // pool blocks per partition (512 tokens)
-constexpr int kPartTokens = kPartBlocks * kBlockSize;
 constexpr int kDepth = MI_DECODE_DEPTH;            // register ring depth (blocks in flight incl. current)
 constexpr int kMaxWaves = MI_DECODE_MAX_WAVES;     // wavefronts (KV heads) per workgroup
 constexpr bool kNtLoads = MI_DECODE_NT_LOADS != 0; // K/V stream with the non-temporal hint
 constexpr int kGroupsPerCu = MI_DECODE_GROUPS_PER_CU;
-constexpr bool kPersistent = MI_DECODE_PERSISTENT != 0;
 constexpr int kMaxBatchPerLaunch = 4096;           // sequences whose prefix sum one workgroup holds in LDS
+constexpr int kMinBlocksPerStream = 8;             // small launches use fewer, longer ranges
+constexpr int kWindow = 64;                        // block ids fetched per window, one per lane
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;
 
-static_assert(kPartBlocks <= 64, "one block id per lane");
+static_assert(kDepth >= 2 && kDepth - 1 < kWindow, "the ring looks ahead less than one id window");
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -88,10 +91,10 @@ struct DecodeArgs {
   int64_t ctx_stride;
   int32_t batch;                   // sequences of this launch
   int32_t max_blocks;
-  int32_t max_parts;               // partitions per sequence the workspace is sized for
+  int32_t streams;                 // block ranges; grid = streams x head groups
   float scale;                     // softmax scale (natural units)
-  float* ws_acc;                   // [batch, max_parts, heads, 128]
-  float* ws_ml;                    // [batch, max_parts, heads, 2] = (m, l) in log2 units
+  float* ws_acc;                   // [streams, 2, heads, 128]: slot 0 = range's first (cut) sequence, 1 = last
+  float* ws_ml;                    // [streams, 2, heads, 2] = (m, l) in log2 units
 };
 
 __device__ __forceinline__ float dpp_sum16(float x) {
@@ -134,9 +137,14 @@ __device__ __forceinline__ int64_t context_of(const DecodeArgs& a, int b) {
   return min(n, static_cast<int64_t>(a.max_blocks) * kBlockSize);
 }
 
-// Partitions of a context of n tokens; an empty context still owns one unit (zero output).
-__device__ __forceinline__ int parts_of(int64_t n) {
-  return n <= 0 ? 1 : static_cast<int>((n + kPartTokens - 1) / kPartTokens);
+// Pool blocks of a context of n tokens (0 for an empty context).
+__device__ __forceinline__ int blocks_of(int64_t n) {
+  return n <= 0 ? 0 : static_cast<int>((n + kBlockSize - 1) / kBlockSize);
+}
+
+// Range holding block x of N: the last s with floor(s N / streams) <= x.
+__device__ __forceinline__ int stream_of(int64_t x, int64_t total, int streams) {
+  return static_cast<int>(((x + 1) * streams - 1) / total);
 }
 
 __device__ __forceinline__ void store_bf16x8(uint16_t* dst, const float* o, float inv) {
@@ -148,15 +156,16 @@ __device__ __forceinline__ void store_bf16x8(uint16_t* dst, const float* o, floa
   *reinterpret_cast<uint4*>(dst) = v;
 }
 
-// Exclusive prefix sums of the partitions per sequence into s_off[0..batch]; returns the total.
+// Exclusive prefix sums of the blocks per sequence into s_off[0..batch]; returns the total.
 template <int kThreads>
-__device__ int scan_partitions(const DecodeArgs& a, int* s_off, int* s_wave) {
+__device__ int scan_blocks(const DecodeArgs& a, int* s_off, int* s_wave) {
   constexpr int kWavesPerGroup = kThreads / 64;
+  static_assert(kThreads % 64 == 0, "whole wavefronts");
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int carry = 0;
   for (int base = 0; base < a.batch; base += kThreads) {
     const int i = base + threadIdx.x;
-    int v = i < a.batch ? parts_of(context_of(a, i)) : 0;
+    int v = i < a.batch ? blocks_of(context_of(a, i)) : 0;
     for (int d = 1; d < 64; d <<= 1) {
       const int y = __shfl_up(v, d);
       if (lane >= d) v += y;
@@ -179,9 +188,19 @@ __device__ int scan_partitions(const DecodeArgs& a, int* s_off, int* s_wave) {
   return carry;
 }
 
+// Sequence of block x (x < total): the last b with s_off[b] <= x (empty sequences are skipped).
+__device__ __forceinline__ int row_of(const int* s_off, int batch, int64_t x) {
+  int lo = 0, hi = batch;  // s_off[lo] <= x < s_off[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (s_off[mid] <= x) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
 template <int kKvHeads, int kWaves>
 // Second bound: minimum wavefronts per SIMD, so that kGroupsPerCu workgroups fit on a CU
-// (4 SIMDs per CU) and the persistent grid is fully resident.
+// (4 SIMDs per CU) and the whole grid is resident.
 __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void paged_decode_kernel(const DecodeArgs a) {
   constexpr int kThreads = 64 * kWaves;
   constexpr int kRowElems = kKvHeads * kHeadDim;     // elements of one pool row (token)
@@ -189,116 +208,94 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
   constexpr int kHeadGroups = kKvHeads / kWaves;
   constexpr int kHeads = kKvHeads * kGroup;
 
-  extern __shared__ int s_off[];                     // [batch + 1] partition prefix sums
+  extern __shared__ int s_off[];                     // [batch + 1] block prefix sums
   __shared__ int s_wave[kWaves];
-
-  int total_units, first_unit, unit_stride;
-  if constexpr (kPersistent) {
-    total_units = scan_partitions<kThreads>(a, s_off, s_wave) * kHeadGroups;
-    first_unit = blockIdx.x;
-    unit_stride = gridDim.x;
-  } else {
-    total_units = 1;
-    first_unit = 0;
-    unit_stride = 1;
-  }
+  const int total = scan_blocks<kThreads>(a, s_off, s_wave);
+  const int stream = blockIdx.x / kHeadGroups;
+  const int hg = blockIdx.x - stream * kHeadGroups;
+  const int64_t lo = static_cast<int64_t>(stream) * total / a.streams;
+  const int64_t hi = static_cast<int64_t>(stream + 1) * total / a.streams;
+  if (lo >= hi) return;
 
   const int lane = threadIdx.x & 63;
   const int dl = lane & 15;
   const int r = lane >> 4;
+  const int g = hg * kWaves + (threadIdx.x >> 6);
   const float scale = a.scale;
+  // Lane offset (elements) of its piece of token 4 i + r inside a block.
+  const int lane_off = r * kRowElems + g * kHeadDim + 8 * dl;
 
-  for (int unit = first_unit; unit < total_units; unit += unit_stride) {
-    int b, part, hg;
-    if constexpr (kPersistent) {
-      hg = unit % kHeadGroups;
-      const int pu = unit / kHeadGroups;
-      int lo = 0, hi = a.batch;  // s_off[lo] <= pu < s_off[hi]
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (s_off[mid] <= pu) lo = mid; else hi = mid;
-      }
-      b = lo;
-      part = pu - s_off[b];
-    } else {
-      b = blockIdx.y;
-      part = blockIdx.x / kHeadGroups;
-      hg = blockIdx.x - part * kHeadGroups;
+  // Block ids of window [base, base + 64), one per lane (indices past the range repeat its
+  // last block; ids outside the pool read block 0).
+  auto fetch_ids = [&](int64_t base, uint32_t& id_lo, uint32_t& id_hi) {
+    const int64_t x = min(base + lane, hi - 1);
+    const int b = row_of(s_off, a.batch, x);
+    int64_t id = a.block_tables[b * a.bt_stride + (x - s_off[b])];
+    if (id < 0 || id >= a.num_blocks) id = 0;
+    id_lo = static_cast<uint32_t>(id);
+    id_hi = static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32);
+  };
+  int64_t wbase = lo;
+  uint32_t cur_lo, cur_hi, nxt_lo, nxt_hi;
+  fetch_ids(wbase, cur_lo, cur_hi);
+  fetch_ids(wbase + kWindow, nxt_lo, nxt_hi);
+
+  u32x4 kbuf[kDepth][4], vbuf[kDepth][4];
+  // Loads block y (clamped to the range) into ring slot `slot`; y never passes the next window.
+  auto issue = [&](int slot, int64_t y) {
+    y = min(y, hi - 1);
+    if (y >= wbase + kWindow) {  // wave-uniform: slide the window, fetch the one after
+      wbase += kWindow;
+      cur_lo = nxt_lo;
+      cur_hi = nxt_hi;
+      fetch_ids(wbase + kWindow, nxt_lo, nxt_hi);
     }
-    const int g = hg * kWaves + (threadIdx.x >> 6);
-    const int64_t n = context_of(a, b);
-    const int nparts = parts_of(n);
-    if (part >= nparts) continue;  // grid form: partition past this sequence's context
+    const int j = static_cast<int>(y - wbase);
+    const uint32_t blo = __builtin_amdgcn_readlane(cur_lo, j);
+    const uint32_t bhi = __builtin_amdgcn_readlane(cur_hi, j);
+    const int64_t base = static_cast<int64_t>((static_cast<uint64_t>(bhi) << 32) | blo) * kBlockElems;
+    const uint16_t* kp = a.key_pool + base + lane_off;
+    const uint16_t* vp = a.value_pool + base + lane_off;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kbuf[slot][i] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(kp + i * 4 * kRowElems));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vbuf[slot][i] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(vp + i * 4 * kRowElems));
+  };
+#pragma unroll
+  for (int s = 0; s < kDepth - 1; ++s) issue(s, lo + s);  // ring slot of block x: (x - lo) % kDepth
 
-    if (n <= 0) {  // empty context: zero output row for this group's heads
-      if (r < kGroup) {
-        uint16_t* o = a.out + b * a.out_row + (g * kGroup + r) * kHeadDim + 8 * dl;
-        *reinterpret_cast<uint4*>(o) = uint4{0, 0, 0, 0};
-      }
-      continue;
-    }
-    const int64_t t_begin = static_cast<int64_t>(part) * kPartTokens;
-    const int n32 = static_cast<int>(n);  // contexts are bounded by max_blocks * 16 < 2^31
-    const int blk0 = part * kPartBlocks;
-    const int nblk = static_cast<int>(min(static_cast<int64_t>(kPartBlocks), (n - t_begin + kBlockSize - 1) / kBlockSize));
-
-    // Block ids of this partition, one per lane; ids out of range read block 0.
-    int64_t my_bid = 0;
-    if (lane < nblk) {
-      my_bid = a.block_tables[b * a.bt_stride + blk0 + lane];
-      if (my_bid < 0 || my_bid >= a.num_blocks) my_bid = 0;
-    }
-    const uint32_t bid_lo = static_cast<uint32_t>(my_bid);
-    const uint32_t bid_hi = static_cast<uint32_t>(static_cast<uint64_t>(my_bid) >> 32);
-
+  int b = row_of(s_off, a.batch, lo);
+  int64_t x = lo;
+  while (x < hi) {
+    const int64_t row_lo = s_off[b], row_hi = s_off[b + 1];
+    const int64_t seg_end = min(hi, row_hi);
+    const int n32 = static_cast<int>(context_of(a, b));  // contexts are bounded by max_blocks * 16 < 2^31
     const uint16_t* qp = a.query + b * a.q_row + (g * kGroup) * a.q_head + 8 * dl;
     const uint4 q0 = *reinterpret_cast<const uint4*>(qp);
     const uint4 q1 = *reinterpret_cast<const uint4*>(qp + a.q_head);
-
-    // Lane offset (elements) of its piece of token 4 i + r inside a block.
-    const int lane_off = r * kRowElems + g * kHeadDim + 8 * dl;
-
-    auto block_base = [&](int j) -> int64_t {
-      const uint32_t blo = __builtin_amdgcn_readlane(bid_lo, j);
-      const uint32_t bhi = __builtin_amdgcn_readlane(bid_hi, j);
-      return static_cast<int64_t>((static_cast<uint64_t>(bhi) << 32) | blo) * kBlockElems;
-    };
-
-    u32x4 kbuf[kDepth][4], vbuf[kDepth][4];
-    auto issue = [&](int slot, int j) {
-      const int64_t base = block_base(min(j, nblk - 1));
-      const uint16_t* kp = a.key_pool + base + lane_off;
-      const uint16_t* vp = a.value_pool + base + lane_off;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) kbuf[slot][i] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(kp + i * 4 * kRowElems));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vbuf[slot][i] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(vp + i * 4 * kRowElems));
-    };
 
     float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
     float acc0[8], acc1[8];
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc0[d] = acc1[d] = 0.0f;
 
-#pragma unroll
-    for (int s = 0; s < kDepth - 1; ++s) issue(s, s);
-
-    for (int j0 = 0; j0 < nblk; j0 += kDepth) {
+    const int64_t seg_begin = x;
+    for (int64_t x0 = x - (x - lo) % kDepth; x0 < seg_end; x0 += kDepth) {
 #pragma unroll
       for (int s = 0; s < kDepth; ++s) {
-        const int j = j0 + s;
-        if (j >= nblk) break;
-        issue((s + kDepth - 1) % kDepth, j + kDepth - 1);
+        const int64_t xb = x0 + s;
+        if (xb < seg_begin || xb >= seg_end) continue;  // wave-uniform
+        issue((s + kDepth - 1) % kDepth, xb + kDepth - 1);
 
-        // ---- scores of tokens 4 i + r of block j, both query heads.  Only a partition's
-        // last block can reach past the context; full blocks skip the masking (uniform branch).
+        // ---- scores of tokens 4 i + r of block xb, both query heads.  Only a sequence's
+        // last block can reach past its context; full blocks skip the masking (uniform branch).
         float s0[4], s1[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           s0[i] = score_log2(dpp_sum16(dot8(q0, kbuf[s][i])), scale);
           s1[i] = score_log2(dpp_sum16(dot8(q1, kbuf[s][i])), scale);
         }
-        const int tok_base = static_cast<int>(t_begin) + j * kBlockSize;
+        const int tok_base = static_cast<int>(xb - row_lo) * kBlockSize;
         if (tok_base + kBlockSize > n32) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -360,6 +357,7 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
         }
       }
     }
+    x = seg_end;
 
     // ---- merge the four rows (log-sum-exp)
     float M0 = fmaxf(m0, __shfl_xor(m0, 16));
@@ -389,74 +387,74 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
     float o[8];
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[d] = (r & 1) == 0 ? acc0[d] : acc1[d];
-    if (nparts == 1) {
-      if (r < kGroup) store_bf16x8(a.out + b * a.out_row + h * kHeadDim + 8 * dl, o, 1.0f / ((r & 1) == 0 ? l0 : l1));
-      continue;
-    }
     if (r < kGroup) {
-      const int64_t slot = (static_cast<int64_t>(b) * a.max_parts + part) * kHeads + h;
-      float4* dst = reinterpret_cast<float4*>(a.ws_acc + slot * kHeadDim + 8 * dl);
-      dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-      dst[1] = make_float4(o[4], o[5], o[6], o[7]);
-      if (dl == 0) {
-        a.ws_ml[slot * 2 + 0] = (r & 1) == 0 ? M0 : M1;
-        a.ws_ml[slot * 2 + 1] = (r & 1) == 0 ? l0 : l1;
+      if (row_lo >= lo && row_hi <= hi) {  // the whole sequence is in this range
+        store_bf16x8(a.out + b * a.out_row + h * kHeadDim + 8 * dl, o, 1.0f / ((r & 1) == 0 ? l0 : l1));
+      } else {  // cut sequence: slot 0 if it began before this range (its first), else 1 (its last)
+        const int64_t slot = (static_cast<int64_t>(stream) * 2 + (row_lo < lo ? 0 : 1)) * kHeads + h;
+        float4* dst = reinterpret_cast<float4*>(a.ws_acc + slot * kHeadDim + 8 * dl);
+        dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+        dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+        if (dl == 0) {
+          a.ws_ml[slot * 2 + 0] = (r & 1) == 0 ? M0 : M1;
+          a.ws_ml[slot * 2 + 1] = (r & 1) == 0 ? l0 : l1;
+        }
       }
+    }
+    if (x < hi) {  // next non-empty sequence (uniform)
+      while (s_off[b + 1] <= x) ++b;
     }
   }
 }
 
-// Merge the partitions of sequences longer than one partition.
-// grid: batch; block: heads * 16 lanes, lane (h, dm) owns dims [8 dm, 8 dm + 8) of head h.
-// Partials of one sequence are contiguous; kMergeUnroll partitions are loaded per step.
+// Finishes what the stream kernel left: sequences cut by a range boundary (merge of their
+// partials: the cut range's last-sequence slot, then the first-sequence slot of every later
+// range up to the one holding the sequence's last block) and empty contexts (zero rows).
+// grid: batch; block: max(64, heads * 16) lanes, lane (h, dm) < heads * 16 owns dims
+// [8 dm, 8 dm + 8) of head h.
 template <int kHeads>
-__global__ __launch_bounds__(kHeads * 16) void paged_decode_merge_kernel(const DecodeArgs a) {
-  constexpr int kMergeUnroll = 8;
+__global__ __launch_bounds__(kHeads * 16 < 64 ? 64 : kHeads * 16) void paged_decode_merge_kernel(const DecodeArgs a) {
+  constexpr int kThreads = kHeads * 16 < 64 ? 64 : kHeads * 16;
+  extern __shared__ int s_off[];
+  __shared__ int s_wave[kThreads / 64];
+  const int total = scan_blocks<kThreads>(a, s_off, s_wave);
   const int b = blockIdx.x;
+  if (threadIdx.x >= kHeads * 16) return;
   const int h = threadIdx.x >> 4;
   const int dm = threadIdx.x & 15;
-  const int nparts = parts_of(context_of(a, b));
-  if (context_of(a, b) <= 0 || nparts <= 1) return;
-  const int64_t base = static_cast<int64_t>(b) * a.max_parts * kHeads + h;
-  float M = -INFINITY;
-  for (int p0 = 0; p0 < nparts; p0 += kMergeUnroll) {
-    float m[kMergeUnroll];
-#pragma unroll
-    for (int k = 0; k < kMergeUnroll; ++k)
-      m[k] = p0 + k < nparts ? a.ws_ml[(base + (p0 + k) * kHeads) * 2] : -INFINITY;
-#pragma unroll
-    for (int k = 0; k < kMergeUnroll; ++k) M = fmaxf(M, m[k]);
+  uint16_t* dst = a.out + b * a.out_row + h * kHeadDim + 8 * dm;
+  const int nblk = s_off[b + 1] - s_off[b];
+  if (nblk == 0) {
+    *reinterpret_cast<uint4*>(dst) = uint4{0, 0, 0, 0};
+    return;
   }
+  const int first = stream_of(s_off[b], total, a.streams);
+  const int last = stream_of(s_off[b + 1] - 1, total, a.streams);
+  if (first == last) return;  // written by the stream kernel
+  // Partials: the first range's last-sequence slot (1), then the first-sequence slot (0) of each
+  // later non-empty range up to `last` (empty ranges -- fewer blocks than ranges -- wrote nothing).
+  auto slot_of = [&](int k) -> int64_t { return (static_cast<int64_t>(k) * 2 + (k == first ? 1 : 0)) * kHeads + h; };
+  auto empty = [&](int k) {
+    return static_cast<int64_t>(k) * total / a.streams >= static_cast<int64_t>(k + 1) * total / a.streams;
+  };
+  float M = -INFINITY;
+  for (int k = first; k <= last; ++k)
+    if (!empty(k)) M = fmaxf(M, a.ws_ml[slot_of(k) * 2]);
   float L = 0.0f, acc[8];
 #pragma unroll
   for (int d = 0; d < 8; ++d) acc[d] = 0.0f;
-  for (int p0 = 0; p0 < nparts; p0 += kMergeUnroll) {
-    float4 x[kMergeUnroll], y[kMergeUnroll];
-    float m[kMergeUnroll], l[kMergeUnroll];
-#pragma unroll
-    for (int k = 0; k < kMergeUnroll; ++k) {
-      if (p0 + k < nparts) {
-        const int64_t slot = base + (p0 + k) * kHeads;
-        m[k] = a.ws_ml[slot * 2];
-        l[k] = a.ws_ml[slot * 2 + 1];
-        const float4* src = reinterpret_cast<const float4*>(a.ws_acc + slot * kHeadDim + 8 * dm);
-        x[k] = src[0];
-        y[k] = src[1];
-      } else {
-        m[k] = -INFINITY;
-        l[k] = 0.0f;
-        x[k] = y[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < kMergeUnroll; ++k) {
-      const float w = m[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[k] - M);
-      L += w * l[k];
-      acc[0] += w * x[k].x; acc[1] += w * x[k].y; acc[2] += w * x[k].z; acc[3] += w * x[k].w;
-      acc[4] += w * y[k].x; acc[5] += w * y[k].y; acc[6] += w * y[k].z; acc[7] += w * y[k].w;
-    }
+  for (int k = first; k <= last; ++k) {
+    if (empty(k)) continue;
+    const int64_t slot = slot_of(k);
+    const float m = a.ws_ml[slot * 2];
+    const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+    L += w * a.ws_ml[slot * 2 + 1];
+    const float4* src = reinterpret_cast<const float4*>(a.ws_acc + slot * kHeadDim + 8 * dm);
+    const float4 xv = src[0], yv = src[1];
+    acc[0] += w * xv.x; acc[1] += w * xv.y; acc[2] += w * xv.z; acc[3] += w * xv.w;
+    acc[4] += w * yv.x; acc[5] += w * yv.y; acc[6] += w * yv.z; acc[7] += w * yv.w;
   }
-  store_bf16x8(a.out + b * a.out_row + h * kHeadDim + 8 * dm, acc, 1.0f / L);
+  store_bf16x8(dst, acc, 1.0f / L);
 }
 
 int device_cus() {
@@ -471,31 +469,36 @@ int device_cus() {
   return cached[dev];
 }
 
+int head_groups_for(int32_t num_kv_heads) {
+  const int waves = num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves;
+  return num_kv_heads / waves;
+}
+
+// Ranges of one launch of `batch` sequences: enough to fill the device (kGroupsPerCu resident
+// workgroups per CU), fewer when the launch cannot hold kMinBlocksPerStream blocks per range.
+int streams_for(int32_t batch, int32_t max_blocks, int32_t num_kv_heads) {
+  const int64_t groups = head_groups_for(num_kv_heads);
+  const int64_t resident = static_cast<int64_t>(device_cus()) * kGroupsPerCu / groups;
+  const int64_t rows = batch < kMaxBatchPerLaunch ? batch : kMaxBatchPerLaunch;
+  const int64_t by_work = (rows * max_blocks + kMinBlocksPerStream - 1) / kMinBlocksPerStream;
+  const int64_t s = by_work < resident ? by_work : resident;
+  return static_cast<int>(s < 1 ? 1 : s);
+}
+
 template <int kKvHeads>
 int32_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   constexpr int kWaves = kKvHeads < kMaxWaves ? kKvHeads : kMaxWaves;
   constexpr int kHeadGroups = kKvHeads / kWaves;
-  if constexpr (kPersistent) {
-    const int64_t units_bound = static_cast<int64_t>(a.batch) * a.max_parts * kHeadGroups;
-    const int64_t resident = static_cast<int64_t>(device_cus()) * kGroupsPerCu;
-    const uint32_t grid = static_cast<uint32_t>(units_bound < resident ? units_bound : resident);
-    const size_t lds = sizeof(int) * (static_cast<size_t>(a.batch) + 1);
-    paged_decode_kernel<kKvHeads, kWaves><<<grid, 64 * kWaves, lds, s>>>(a);
-  } else {
-    dim3 grid(static_cast<uint32_t>(a.max_parts * kHeadGroups), static_cast<uint32_t>(a.batch));
-    paged_decode_kernel<kKvHeads, kWaves><<<grid, 64 * kWaves, 0, s>>>(a);
+  constexpr int kHeads = kKvHeads * kGroup;
+  constexpr int kMergeThreads = kHeads * 16 < 64 ? 64 : kHeads * 16;
+  const size_t lds = sizeof(int) * (static_cast<size_t>(a.batch) + 1);
+  if (a.max_blocks > 0) {
+    paged_decode_kernel<kKvHeads, kWaves><<<static_cast<uint32_t>(a.streams) * kHeadGroups, 64 * kWaves, lds, s>>>(a);
+    int32_t rc = check_launch("mi_paged_decode_attention");
+    if (rc != MI_OK) return rc;
   }
-  int32_t rc = check_launch("mi_paged_decode_attention");
-  if (rc != MI_OK || a.max_parts <= 1) return rc;
-  paged_decode_merge_kernel<kKvHeads * kGroup><<<a.batch, kKvHeads * kGroup * 16, 0, s>>>(a);
+  paged_decode_merge_kernel<kHeads><<<a.batch, kMergeThreads, lds, s>>>(a);
   return check_launch("mi_paged_decode_attention(merge)");
-}
-
-int64_t parts_for(int32_t max_blocks) { return (static_cast<int64_t>(max_blocks) + kPartBlocks - 1) / kPartBlocks; }
-
-int head_groups_for(int32_t num_kv_heads) {
-  const int waves = num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves;
-  return num_kv_heads / waves;
 }
 
 }  // namespace
@@ -503,10 +506,12 @@ int head_groups_for(int32_t num_kv_heads) {
 
 extern "C" int64_t mi_paged_decode_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t num_heads,
                                                    int32_t head_dim, int32_t block_size) {
-  if (batch <= 0 || max_blocks <= 0 || num_heads <= 0 || head_dim <= 0 || block_size != mi::kBlockSize) return 0;
-  const int64_t parts = mi::parts_for(max_blocks);
-  if (parts <= 1) return 0;
-  return static_cast<int64_t>(batch) * parts * num_heads * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
+  using namespace mi;
+  if (batch <= 0 || max_blocks <= 0 || num_heads <= 0 || head_dim <= 0 || block_size != kBlockSize ||
+      num_heads % kGroup != 0)
+    return 0;
+  const int64_t streams = streams_for(batch, max_blocks, num_heads / kGroup);
+  return streams * 2 * num_heads * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
 }
 
 extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, const void* query,
@@ -537,26 +542,22 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention: block_table_stride < max_blocks");
   if (context_lens_stride <= 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention: context_lens_stride must be > 0");
+  if (static_cast<int64_t>(kMaxBatchPerLaunch) * max_blocks >= (1ll << 31))
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: max_blocks %d too large", max_blocks);
 
-  const int64_t parts = max_blocks > 0 ? parts_for(max_blocks) : 1;
-  float* ws_acc = nullptr;
-  float* ws_ml = nullptr;
-  if (parts > 1) {
-    const int64_t need = mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size);
-    if (!workspace || workspace_bytes < need)
-      return fail(MI_ERR_WORKSPACE, "mi_paged_decode_attention: workspace of %lld bytes needed, got %lld",
-                  static_cast<long long>(need), static_cast<long long>(workspace_bytes));
-    if (!aligned16(workspace))
-      return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: workspace must be 16-byte aligned");
-    ws_acc = static_cast<float*>(workspace);
-    ws_ml = ws_acc + static_cast<int64_t>(batch) * parts * num_heads * kHeadDim;
-  }
-  if (static_cast<int64_t>(batch) * parts * head_groups_for(num_kv_heads) > 0x7fffffff ||
-      (!kPersistent && batch > 65535))
-    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: too many work units");
+  const int32_t streams = streams_for(batch, max_blocks, num_kv_heads);
+  const int64_t need = mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size);
+  if (max_blocks > 0 && (!workspace || workspace_bytes < need))
+    return fail(MI_ERR_WORKSPACE, "mi_paged_decode_attention: workspace of %lld bytes needed, got %lld",
+                static_cast<long long>(need), static_cast<long long>(workspace_bytes));
+  if (max_blocks > 0 && !aligned16(workspace))
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: workspace must be 16-byte aligned");
+  float* ws_acc = static_cast<float*>(workspace);
+  float* ws_ml = ws_acc ? ws_acc + static_cast<int64_t>(streams) * 2 * num_heads * kHeadDim : nullptr;
 
   hipStream_t s = as_stream(stream);
-  // Sequences go in slices of at most kMaxBatchPerLaunch (the per-workgroup prefix sum lives in LDS).
+  // Sequences go in slices of at most kMaxBatchPerLaunch (the per-workgroup prefix sum lives in
+  // LDS); the slices reuse the workspace one after the other on the stream.
   for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
     const int32_t nb = batch - b0 < kMaxBatchPerLaunch ? batch - b0 : kMaxBatchPerLaunch;
     DecodeArgs a{};
@@ -574,12 +575,10 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
     a.ctx_stride = context_lens_stride;
     a.batch = nb;
     a.max_blocks = max_blocks;
-    a.max_parts = static_cast<int32_t>(parts);
+    a.streams = streams;
     a.scale = scale;
-    if (parts > 1) {
-      a.ws_acc = ws_acc + static_cast<int64_t>(b0) * parts * num_heads * kHeadDim;
-      a.ws_ml = ws_ml + static_cast<int64_t>(b0) * parts * num_heads * 2;
-    }
+    a.ws_acc = ws_acc;
+    a.ws_ml = ws_ml;
     int32_t rc;
     switch (num_kv_heads) {
       case 1: rc = launch_decode<1>(a, s); break;

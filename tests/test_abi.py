@@ -40,11 +40,18 @@ def test_abi_version(native_lib):
 
 
 def test_decode_workspace_size(native_lib):
-    # one 512-token partition (<= 32 blocks) needs no workspace; beyond that
-    # batch * parts * heads * (128 + 2) floats
-    assert native_lib.mi_paged_decode_workspace_bytes(256, 32, 16, 128, 16) == 0
-    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 128, 16) == 256 * 16 * 16 * 130 * 4
-    assert native_lib.mi_paged_decode_workspace_bytes(4, 33, 16, 128, 16) == 4 * 2 * 16 * 130 * 4
+    # two slots per block range per head, (128 + 2) floats each; ranges = resident workgroups
+    # (256 CUs x 4, over 4 head groups at 8 KV heads; 256 CUs assumed without a device), fewer
+    # for launches under 8 blocks per range
+    slot = 2 * 16 * 130 * 4
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 128, 16) == 256 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 32, 16, 128, 16) == 256 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(4, 33, 16, 128, 16) == 17 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(1, 1, 16, 128, 16) == 1 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(0, 512, 16, 128, 16) == 0
+    assert native_lib.mi_paged_decode_workspace_bytes(8, 0, 16, 128, 16) == 0
+    # 2 KV heads: one head group, so ranges = 256 x 4
+    assert native_lib.mi_paged_decode_workspace_bytes(512, 512, 4, 128, 16) == 1024 * 2 * 4 * 130 * 4
 
 
 def _ptrs(n):
@@ -88,7 +95,7 @@ def test_decode_rejects_unsupported_shapes_on_host(native_lib):
     assert call(bs=8) == _native.MI_ERR_UNSUPPORTED
     assert call(heads=24) == _native.MI_ERR_UNSUPPORTED
     assert call(heads=6, kv=3) == _native.MI_ERR_UNSUPPORTED
-    assert call(max_blocks=40) == _native.MI_ERR_WORKSPACE  # two partitions, no workspace
+    assert call(max_blocks=40) == _native.MI_ERR_WORKSPACE  # no workspace
     assert b"workspace" in lib.mi_last_error()
     need = lib.mi_paged_decode_workspace_bytes(2, 40, 16, 128, 16)
     assert call(max_blocks=40, ws=256, ws_bytes=need - 4) == _native.MI_ERR_WORKSPACE

@@ -157,3 +157,32 @@ def test_repeated_calls_with_changing_batches(native_lib, device):
         for _ in range(2):
             got = run_kernel(q, kp, vp, bt, ctx, device)
             assert max_abs(got, oracle(q, kp, vp, bt, ctx)) <= TOL, f"case {ctx}"
+
+
+@pytest.mark.parametrize("kv_heads", [8, 1])
+def test_more_ranges_than_blocks_and_cut_sequences(native_lib, device, kv_heads):
+    """The launch's blocks are cut into equal ranges sized from batch x max_blocks: tiny
+    contexts under a wide table leave empty ranges and cut two-block sequences in two;
+    empty contexts sit between them (zero rows)."""
+    ctx = [0, 17, 1, 0, 32, 20, 5, 0, 31, 33] * 6
+    q, kp, vp, bt, tables = random_case(41 + kv_heads, ctx, kv_heads=kv_heads)
+    wide = torch.zeros(len(ctx), 64, dtype=torch.long)  # max_blocks 64: many more ranges than blocks
+    wide[:, :bt.shape[1]] = bt
+    got = run_kernel(q, kp, vp, wide, ctx, device).view(len(ctx), -1)
+    ref = oracle(q, kp, vp, wide, ctx).view(len(ctx), -1)
+    live = [i for i, n in enumerate(ctx) if n > 0]
+    zero = [i for i, n in enumerate(ctx) if n == 0]  # kernel contract: zero row (the reference never decodes one)
+    assert max_abs(got[live], ref[live]) <= TOL
+    assert not got[zero].float().abs().any()
+
+
+def test_one_long_sequence_across_many_ranges(native_lib, device):
+    """An 8192-token sequence among short ones spans a couple of hundred ranges; their
+    partials all merge into its row."""
+    ctx = [8192, 3, 0, 700, 16, 4099]
+    q, kp, vp, bt, _ = random_case(77, ctx)
+    got = run_kernel(q, kp, vp, bt, ctx, device).view(len(ctx), -1)
+    ref = oracle(q, kp, vp, bt, ctx).view(len(ctx), -1)
+    live = [0, 1, 3, 4, 5]
+    assert max_abs(got[live], ref[live]) <= TOL
+    assert not got[2].float().abs().any()
