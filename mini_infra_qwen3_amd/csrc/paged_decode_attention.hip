@@ -67,7 +67,7 @@ constexpr int kMaxWaves = MI_DECODE_MAX_WAVES;     // wavefronts (KV heads) per 
 constexpr bool kNtLoads = MI_DECODE_NT_LOADS != 0; // K/V stream with the non-temporal hint
 constexpr int kGroupsPerCu = MI_DECODE_GROUPS_PER_CU;
 constexpr int kMaxBatchPerLaunch = 4096;           // sequences whose prefix sum one workgroup holds in LDS
-constexpr int kMinBlocksPerStream = 8;             // small launches use fewer, longer ranges
+constexpr int kMinBlocksPerStream = 32;            // small launches use fewer, longer ranges
 constexpr int kWindow = 64;                        // block ids fetched per window, one per lane
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;
@@ -437,22 +437,49 @@ __global__ __launch_bounds__(kHeads * 16 < 64 ? 64 : kHeads * 16) void paged_dec
   auto empty = [&](int k) {
     return static_cast<int64_t>(k) * total / a.streams >= static_cast<int64_t>(k + 1) * total / a.streams;
   };
+  // kMergeUnroll partials per step with independent loads (a serial chain of dependent loads
+  // would make a launch of many cut sequences latency-bound).
+  constexpr int kMergeUnroll = 4;
   float M = -INFINITY;
-  for (int k = first; k <= last; ++k)
-    if (!empty(k)) M = fmaxf(M, a.ws_ml[slot_of(k) * 2]);
+  for (int k0 = first; k0 <= last; k0 += kMergeUnroll) {
+    float m[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const int k = k0 + u;
+      m[u] = (k <= last && !empty(k)) ? a.ws_ml[slot_of(k) * 2] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) M = fmaxf(M, m[u]);
+  }
   float L = 0.0f, acc[8];
 #pragma unroll
   for (int d = 0; d < 8; ++d) acc[d] = 0.0f;
-  for (int k = first; k <= last; ++k) {
-    if (empty(k)) continue;
-    const int64_t slot = slot_of(k);
-    const float m = a.ws_ml[slot * 2];
-    const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
-    L += w * a.ws_ml[slot * 2 + 1];
-    const float4* src = reinterpret_cast<const float4*>(a.ws_acc + slot * kHeadDim + 8 * dm);
-    const float4 xv = src[0], yv = src[1];
-    acc[0] += w * xv.x; acc[1] += w * xv.y; acc[2] += w * xv.z; acc[3] += w * xv.w;
-    acc[4] += w * yv.x; acc[5] += w * yv.y; acc[6] += w * yv.z; acc[7] += w * yv.w;
+  for (int k0 = first; k0 <= last; k0 += kMergeUnroll) {
+    float m[kMergeUnroll], l[kMergeUnroll];
+    float4 xv[kMergeUnroll], yv[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const int k = k0 + u;
+      if (k <= last && !empty(k)) {
+        const int64_t slot = slot_of(k);
+        m[u] = a.ws_ml[slot * 2];
+        l[u] = a.ws_ml[slot * 2 + 1];
+        const float4* src = reinterpret_cast<const float4*>(a.ws_acc + slot * kHeadDim + 8 * dm);
+        xv[u] = src[0];
+        yv[u] = src[1];
+      } else {
+        m[u] = -INFINITY;
+        l[u] = 0.0f;
+        xv[u] = yv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const float w = m[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[u] - M);
+      L += w * l[u];
+      acc[0] += w * xv[u].x; acc[1] += w * xv[u].y; acc[2] += w * xv[u].z; acc[3] += w * xv[u].w;
+      acc[4] += w * yv[u].x; acc[5] += w * yv[u].y; acc[6] += w * yv[u].z; acc[7] += w * yv[u].w;
+    }
   }
   store_bf16x8(dst, acc, 1.0f / L);
 }
