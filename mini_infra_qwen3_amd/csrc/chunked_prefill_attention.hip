@@ -89,15 +89,16 @@ __device__ __forceinline__ void round_bf16_pair(float& x, float& y) {
   y = __uint_as_float(pk & 0xffff0000u);
 }
 
+// bf16 rounding of one float as an fp32 value in one instruction: the packed convert with a zero
+// low half leaves bf16(x) in the high half and zeros below, which is exactly bf16(x) as fp32.
+__device__ __forceinline__ float round_bf16_hi(float x) {
+  return __builtin_bit_cast(float, __builtin_convertvector((f32x2){0.0f, x}, bf16x2));
+}
+
 // The reference's scores: bf16(bf16(q . k) * scale) (src/mini_infra/model/qwen3.py:243), in place.
 __device__ __forceinline__ void reference_scores(f32x4& v, float scale) {
-  float a = v[0], b = v[1], c = v[2], d = v[3];
-  round_bf16_pair(a, b);
-  round_bf16_pair(c, d);
-  a *= scale; b *= scale; c *= scale; d *= scale;
-  round_bf16_pair(a, b);
-  round_bf16_pair(c, d);
-  v = f32x4{a, b, c, d};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = round_bf16_hi(round_bf16_hi(v[i]) * scale);
 }
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
