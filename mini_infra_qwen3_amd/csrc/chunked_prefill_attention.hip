@@ -101,6 +101,12 @@ __device__ __forceinline__ void reference_scores(f32x4& v, float scale) {
   for (int i = 0; i < 4; ++i) v[i] = round_bf16_hi(round_bf16_hi(v[i]) * scale);
 }
 
+// Column (element) of key `key` in V^T row `dim`: rows of 32 dims are rotated by 8 keys (4 dwords)
+// per group, so that the transposing stores -- each thread writes dims 8 x .. 8 x + 7 of two keys,
+// x = lane % 16 -- spread over all banks (32 or 64 banks of 4 bytes) instead of 8 of them, while
+// the PV operand reads (8 consecutive keys of one dim) stay contiguous and conflict-free.
+__device__ __forceinline__ int vcol(int dim, int key) { return (key + 8 * (dim >> 5)) & (kKTile - 1); }
+
 __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
@@ -232,9 +238,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
       const uint32_t x[4] = {vreg[kk][0][0], vreg[kk][0][1], vreg[kk][0][2], vreg[kk][0][3]};                  \
       const uint32_t y[4] = {vreg[kk][1][0], vreg[kk][1][1], vreg[kk][1][2], vreg[kk][1][3]};                  \
       _Pragma("unroll") for (int d2 = 0; d2 < 4; ++d2) {                                                       \
-        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2) * kVStride + key]) =                            \
+        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2) * kVStride + vcol(tdim, key)]) =                \
             perm(y[d2], x[d2], 0x05040100u);                                                                   \
-        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2 + 1) * kVStride + key]) =                        \
+        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2 + 1) * kVStride + vcol(tdim, key)]) =            \
             perm(y[d2], x[d2], 0x07060302u);                                                                   \
       }                                                                                                        \
     }                                                                                                          \
@@ -367,9 +373,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     for (int ks2 = 0; ks2 < 2; ++ks2) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* vrow = &sV[buf][(dt * 16 + ql) * kVStride + 32 * ks2 + 4 * gq];
-        const bf16x4 v0 = *reinterpret_cast<const bf16x4*>(vrow);
-        const bf16x4 v1 = *reinterpret_cast<const bf16x4*>(vrow + 16);
+        const uint16_t* vrow = &sV[buf][(dt * 16 + ql) * kVStride];
+        const bf16x4 v0 = *reinterpret_cast<const bf16x4*>(vrow + vcol(dt * 16, 32 * ks2 + 4 * gq));
+        const bf16x4 v1 = *reinterpret_cast<const bf16x4*>(vrow + vcol(dt * 16, 32 * ks2 + 4 * gq + 16));
         const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
