@@ -246,13 +246,19 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     }                                                                                                          \
   } while (0)
 
-  f32x4 oacc[8][2];
+  // oacc[0..7]: O^T dims 16 dt + 4 gq + i; oacc[8]: the softmax row sums.  Tile 8 multiplies P^T by
+  // a constant A with ones in rows 0, 4, 8, 12: its rows 0, 4, 8, 12 -- element 0 of every lane group
+  // -- accumulate sum_k bf16(p_k) on the matrix cores instead of 32 VALU adds per tile, and the
+  // lazy rescale of oacc covers them.
+  f32x4 oacc[9][2];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < 9; ++dt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const __bf16 one_or_zero = (ql & 3) == 0 ? static_cast<__bf16>(1.0f) : static_cast<__bf16>(0.0f);
+  const bf16x8 ones_frag = {one_or_zero, one_or_zero, one_or_zero, one_or_zero,
+                            one_or_zero, one_or_zero, one_or_zero, one_or_zero};
   float m_run[2] = {-INFINITY, -INFINITY};
-  float l_part[2] = {0.0f, 0.0f};
   const float scale = a.scale;
 
   __syncthreads();  // s_hblk ready
@@ -340,25 +346,18 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
         const float mn = fmaxf(m_run[nt], mx[nt]);
         const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[nt] - mn);
         m_run[nt] = mn;
-        l_part[nt] *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) oacc[dt][nt] *= alpha;
+        for (int dt = 0; dt < 9; ++dt) oacc[dt][nt] *= alpha;
       }
     }
     bf16x8 pf[2][2];  // [nt][ks2]
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const float ref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
-      float sum = 0.0f;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[mt][nt][i], to_log2, -ref));
-          sacc[mt][nt][i] = p;
-          sum += p;
-        }
-      l_part[nt] += sum;
+        for (int i = 0; i < 4; ++i) sacc[mt][nt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[mt][nt][i], to_log2, -ref));
 #pragma unroll
       for (int ks2 = 0; ks2 < 2; ++ks2) {
         const f32x8 pv = {sacc[2 * ks2][nt][0], sacc[2 * ks2][nt][1], sacc[2 * ks2][nt][2], sacc[2 * ks2][nt][3],
@@ -381,6 +380,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
         for (int nt = 0; nt < 2; ++nt)
           oacc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[nt][ks2], oacc[dt][nt], 0, 0, 0);
       }
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        oacc[8][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_frag, pf[nt][ks2], oacc[8][nt], 0, 0, 0);
     }
 
     if (t + 1 < n_tiles) MI_STORE_TILE(buf ^ 1);
@@ -390,9 +392,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   // ---- normalise and write: lane holds query qw0 + 16 nt + ql, dims 16 dt + 4 gq + i
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    float lt = l_part[nt];
-    lt += __shfl_xor(lt, 16);
-    lt += __shfl_xor(lt, 32);
+    const float lt = oacc[8][nt][0];
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int qi = qw0 + 16 * nt + ql;
     if (qi >= L) continue;
