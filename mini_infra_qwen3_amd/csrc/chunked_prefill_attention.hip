@@ -117,9 +117,29 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   __shared__ __align__(16) uint16_t sV[2][kHeadDim * kVStride];
   extern __shared__ int s_hblk[];  // [ceil(nh / 16)] history block ids of this row (dynamic LDS)
 
-  const int b = blockIdx.z;
-  const int g = blockIdx.y;
-  const int qt = gridDim.x - 1 - blockIdx.x;  // heaviest (latest) query tiles start first
+  // Workgroup -> (row b, KV head g, query tile qt).  Consecutive workgroup ids go round-robin to
+  // the 8 XCDs, each with its own L2; so that the query tiles of one (row, head) -- which stream
+  // the same K/V tiles -- share an L2, id L runs on XCD L % 8 and takes the (L / 8)-th tile of that
+  // XCD's (row, head) pairs in order.  Shapes whose pair count is not a multiple of 8 keep the
+  // plain mapping.  Within a pair the heaviest (latest) query tiles start first.
+  int b, g, qt;
+  {
+    const int tiles = gridDim.x;
+    const int pairs = gridDim.y * gridDim.z;
+    const int lin = blockIdx.x + tiles * (blockIdx.y + gridDim.y * blockIdx.z);
+    int pair, rank;
+    if (pairs % 8 == 0) {
+      const int slot = lin >> 3;
+      pair = (slot / tiles) * 8 + (lin & 7);
+      rank = slot % tiles;
+    } else {
+      pair = lin / tiles;
+      rank = lin % tiles;
+    }
+    g = pair % gridDim.y;
+    b = pair / gridDim.y;
+    qt = tiles - 1 - rank;
+  }
   const int q0 = qt * kQTile;
   const int L = a.padded_len;
   int64_t len64 = a.chunk_lens[b * a.lens_stride];
