@@ -41,8 +41,14 @@ constexpr int kBlockSize = 16;
 constexpr int kGroup = 2;
 constexpr int kQTile = 64;                 // queries per head per workgroup
 constexpr int kKTile = 64;                 // keys per KV tile
-constexpr int kKStride = kHeadDim + 8;     // LDS row of K (elements): 272 B
-constexpr int kVStride = kKTile + 4;       // LDS row of V^T (elements): 136 B
+#ifndef MI_PREFILL_K_PAD
+#define MI_PREFILL_K_PAD 8
+#endif
+#ifndef MI_PREFILL_V_PAD
+#define MI_PREFILL_V_PAD 4
+#endif
+constexpr int kKStride = kHeadDim + MI_PREFILL_K_PAD;  // LDS row of K (elements): 272 B
+constexpr int kVStride = kKTile + MI_PREFILL_V_PAD;    // LDS row of V^T (elements): 136 B
 constexpr int kThreads = 256;
 constexpr int kMaxHistoryBlocks = 16384;   // history table staged in LDS: 64 KiB at most (256k tokens)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -346,6 +352,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     }
 
     // ---- online softmax per query column (lanes ql, ql+16, ql+32, ql+48 hold its 64 keys)
+    // Lazy rescale: m_run (shared by the four lanes of a query column) only has to bound every
+    // score to within kRescaleSlack, so each lane tests its own 16 scores and the cross-lane
+    // column max is taken only on the rare tiles that raise m_run.
     const float to_log2 = kExactScores ? kLog2e : scale * kLog2e;
     float mx[2];
 #pragma unroll
@@ -355,14 +364,14 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) v = fmaxf(v, sacc[mt][nt][i]);
-      v = fmaxf(v, __shfl_xor(v, 16));
-      v = fmaxf(v, __shfl_xor(v, 32));
       mx[nt] = v * to_log2;
     }
     const bool grow = mx[0] > m_run[0] + kRescaleSlack || mx[1] > m_run[1] + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
+        mx[nt] = fmaxf(mx[nt], __shfl_xor(mx[nt], 16));
+        mx[nt] = fmaxf(mx[nt], __shfl_xor(mx[nt], 32));
         const float mn = fmaxf(m_run[nt], mx[nt]);
         const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[nt] - mn);
         m_run[nt] = mn;
