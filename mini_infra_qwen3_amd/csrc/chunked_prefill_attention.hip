@@ -39,17 +39,25 @@ namespace {
 constexpr int kHeadDim = 128;
 constexpr int kBlockSize = 16;
 constexpr int kGroup = 2;
-constexpr int kQTile = 64;                 // queries per head per workgroup
+#ifndef MI_PREFILL_WAVES_PER_HEAD
+#define MI_PREFILL_WAVES_PER_HEAD 4
+#endif
+constexpr int kWavesPerHead = MI_PREFILL_WAVES_PER_HEAD;  // 32 queries per wave
+constexpr int kQTile = 32 * kWavesPerHead;                // queries per head per workgroup
 constexpr int kKTile = 64;                 // keys per KV tile
 #ifndef MI_PREFILL_K_PAD
-#define MI_PREFILL_K_PAD 8
+#define MI_PREFILL_K_PAD 16
 #endif
 #ifndef MI_PREFILL_V_PAD
 #define MI_PREFILL_V_PAD 4
 #endif
-constexpr int kKStride = kHeadDim + MI_PREFILL_K_PAD;  // LDS row of K (elements): 272 B
+constexpr int kKStride = kHeadDim + MI_PREFILL_K_PAD;  // LDS row of K (elements): 288 B
 constexpr int kVStride = kKTile + MI_PREFILL_V_PAD;    // LDS row of V^T (elements): 136 B
-constexpr int kThreads = 256;
+constexpr int kThreads = 64 * kGroup * kWavesPerHead;    // one workgroup per CU at 4 waves per head
+constexpr int kKeysPerPass = kThreads / 16;               // K rows one pass of 16-byte pieces covers
+constexpr int kKPieces = kKTile / kKeysPerPass;           // K pieces per thread and tile
+constexpr int kVPieces = kKTile / (2 * kKeysPerPass);     // V key pairs per thread and tile
+static_assert(kKPieces * kKeysPerPass == kKTile && kVPieces * 2 * kKeysPerPass == kKTile, "tile cover");
 constexpr int kMaxHistoryBlocks = 16384;   // history table staged in LDS: 64 KiB at most (256k tokens)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;
@@ -159,8 +167,8 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
-  const int hh = w >> 1;
-  const int qs = w & 1;
+  const int hh = w / kWavesPerHead;
+  const int qs = w % kWavesPerHead;
   const int h = g * kGroup + hh;
   const int ql = lane & 15;
   const int gq = lane >> 4;
@@ -198,71 +206,73 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   const int c_hi = last_q / kKTile;
   const int n_tiles = n_hist_tiles + (c_hi - c_lo + 1);
 
-  // ---- tile loader.  Thread tid owns K pieces (key 16 kk + tid / 16, dims 8 (tid % 16) .. +8),
-  // kk = 0..3, and V key pairs (keys 32 kk + 2 (tid / 16) + {0, 1}, same dims), kk = 0..1.  In a
-  // history tile K piece kk lies in pool block kk of the tile and V pair kk in block
-  // 2 kk + (tid / 128): block ids are uniform, read from LDS where the workgroup staged its
-  // history table once.  Every load reads valid memory: block indices are clamped to the last
-  // history block and chunk positions to L - 1; keys past the context are masked later.
+  // ---- tile loader.  Thread tid owns K pieces (key kKeysPerPass kk + tid / 16, dims 8 (tid % 16)
+  // .. +8), kk < kKPieces, and V key pairs (keys 2 kKeysPerPass kk + 2 (tid / 16) + {0, 1}, same
+  // dims), kk < kVPieces.  In a history tile each piece lies in pool block (its first key) / 16 of
+  // the tile -- uniform across a wavefront, whose 64 lanes span 4 consecutive keys (or pairs) of
+  // one block -- read from LDS where the workgroup staged its history table once.  Every load
+  // reads valid memory: block indices are clamped to the last history block and chunk positions
+  // to L - 1; keys past the context are masked later.
   const int tkey = tid >> 4;
   const int tdim = (tid & 15) * 8;
-  const int vhalf = tid >> 7;
   const int nhb = (nh + kBlockSize - 1) / kBlockSize;
   for (int i = tid; i < nhb; i += kThreads) {
     const int64_t x = a.history_blocks[b * a.history_stride + i];
     s_hblk[i] = (x < 0 || x >= a.num_blocks) ? 0 : static_cast<int>(x);
   }
   constexpr int64_t kBlkElems = static_cast<int64_t>(kBlockSize) * kKvHeads * kHeadDim;
-  const int64_t k_hist_off = static_cast<int64_t>(tkey * kKvHeads + g) * kHeadDim + tdim;
+  const int64_t k_hist_off = static_cast<int64_t>((tkey % kBlockSize) * kKvHeads + g) * kHeadDim + tdim;
   const int voff = (2 * tkey) % kBlockSize;
   const int64_t v_hist_off0 = static_cast<int64_t>(voff * kKvHeads + g) * kHeadDim + tdim;
   const int64_t v_hist_off1 = v_hist_off0 + kKvHeads * kHeadDim;
   const uint16_t* k_chunk = a.key + b * a.k_row + g * a.k_head + tdim;
   const uint16_t* v_chunk = a.value + b * a.v_row + g * a.v_head + tdim;
 
-  u32x4 kreg[4], vreg[2][2];
-#define MI_LOAD_TILE(T)                                                                                         \
+#define MI_HIST_BLOCK(T, KEY) \
+  __builtin_amdgcn_readfirstlane(s_hblk[min((T) * (kKTile / kBlockSize) + (KEY) / kBlockSize, nhb - 1)])
+#define MI_LOAD_TILE(T, KR, VR)                                                                                      \
   do {                                                                                                         \
     const int t_ = (T);                                                                                        \
     if (t_ < n_hist_tiles) {                                                                                   \
-      int blk[4];                                                                                              \
-      _Pragma("unroll") for (int j = 0; j < 4; ++j)                                                            \
-          blk[j] = __builtin_amdgcn_readfirstlane(s_hblk[min(t_ * (kKTile / kBlockSize) + j, nhb - 1)]);       \
-      _Pragma("unroll") for (int kk = 0; kk < 4; ++kk)                                                         \
-          kreg[kk] = *reinterpret_cast<const u32x4*>(a.key_pool + blk[kk] * kBlkElems + k_hist_off);           \
-      _Pragma("unroll") for (int kk = 0; kk < 2; ++kk) {                                                       \
-        const int64_t vb = static_cast<int64_t>(vhalf ? blk[2 * kk + 1] : blk[2 * kk]) * kBlkElems;            \
-        vreg[kk][0] = *reinterpret_cast<const u32x4*>(a.value_pool + vb + v_hist_off0);                        \
-        vreg[kk][1] = *reinterpret_cast<const u32x4*>(a.value_pool + vb + v_hist_off1);                        \
+      _Pragma("unroll") for (int kk = 0; kk < kKPieces; ++kk) {                                                \
+        const int64_t kb = static_cast<int64_t>(MI_HIST_BLOCK(t_, kKeysPerPass * kk + tkey)) * kBlkElems;      \
+        KR[kk] = *reinterpret_cast<const u32x4*>(a.key_pool + kb + k_hist_off);                              \
+      }                                                                                                        \
+      _Pragma("unroll") for (int kk = 0; kk < kVPieces; ++kk) {                                                \
+        const int64_t vb = static_cast<int64_t>(MI_HIST_BLOCK(t_, 2 * kKeysPerPass * kk + 2 * tkey)) * kBlkElems; \
+        VR[kk][0] = *reinterpret_cast<const u32x4*>(a.value_pool + vb + v_hist_off0);                        \
+        VR[kk][1] = *reinterpret_cast<const u32x4*>(a.value_pool + vb + v_hist_off1);                        \
       }                                                                                                        \
     } else {                                                                                                   \
       const int key0 = (c_lo + t_ - n_hist_tiles) * kKTile;                                                   \
       if (key0 + kKTile <= L) {                                                                                \
-        _Pragma("unroll") for (int kk = 0; kk < 4; ++kk)                                                       \
-            kreg[kk] = *reinterpret_cast<const u32x4*>(k_chunk + (key0 + 16 * kk + tkey) * a.k_tok);           \
-        _Pragma("unroll") for (int kk = 0; kk < 2; ++kk)                                                       \
+        _Pragma("unroll") for (int kk = 0; kk < kKPieces; ++kk)                                                \
+            KR[kk] = *reinterpret_cast<const u32x4*>(k_chunk + (key0 + kKeysPerPass * kk + tkey) * a.k_tok); \
+        _Pragma("unroll") for (int kk = 0; kk < kVPieces; ++kk)                                                \
           _Pragma("unroll") for (int e = 0; e < 2; ++e)                                                        \
-            vreg[kk][e] = *reinterpret_cast<const u32x4*>(v_chunk + (key0 + 32 * kk + 2 * tkey + e) * a.v_tok); \
+            VR[kk][e] = *reinterpret_cast<const u32x4*>(                                                     \
+                v_chunk + (key0 + 2 * kKeysPerPass * kk + 2 * tkey + e) * a.v_tok);                            \
       } else {                                                                                                 \
-        _Pragma("unroll") for (int kk = 0; kk < 4; ++kk)                                                       \
-            kreg[kk] = *reinterpret_cast<const u32x4*>(k_chunk + min(key0 + 16 * kk + tkey, L - 1) * a.k_tok); \
-        _Pragma("unroll") for (int kk = 0; kk < 2; ++kk)                                                       \
+        _Pragma("unroll") for (int kk = 0; kk < kKPieces; ++kk)                                                \
+            KR[kk] = *reinterpret_cast<const u32x4*>(                                                        \
+                k_chunk + min(key0 + kKeysPerPass * kk + tkey, L - 1) * a.k_tok);                              \
+        _Pragma("unroll") for (int kk = 0; kk < kVPieces; ++kk)                                                \
           _Pragma("unroll") for (int e = 0; e < 2; ++e)                                                        \
-            vreg[kk][e] = *reinterpret_cast<const u32x4*>(                                                     \
-                v_chunk + min(key0 + 32 * kk + 2 * tkey + e, L - 1) * a.v_tok);                                \
+            VR[kk][e] = *reinterpret_cast<const u32x4*>(                                                     \
+                v_chunk + min(key0 + 2 * kKeysPerPass * kk + 2 * tkey + e, L - 1) * a.v_tok);                  \
       }                                                                                                        \
     }                                                                                                          \
   } while (0)
 
-#define MI_STORE_TILE(BUF)                                                                                     \
+#define MI_STORE_TILE(BUF, KR, VR)                                                                                 \
   do {                                                                                                         \
     const int buf_ = (BUF);                                                                                    \
-    _Pragma("unroll") for (int kk = 0; kk < 4; ++kk)                                                           \
-        *reinterpret_cast<u32x4*>(&sK[buf_][(16 * kk + tkey) * kKStride + tdim]) = kreg[kk];                   \
-    _Pragma("unroll") for (int kk = 0; kk < 2; ++kk) {                                                         \
-      const int key = 32 * kk + 2 * tkey;                                                                      \
-      const uint32_t x[4] = {vreg[kk][0][0], vreg[kk][0][1], vreg[kk][0][2], vreg[kk][0][3]};                  \
-      const uint32_t y[4] = {vreg[kk][1][0], vreg[kk][1][1], vreg[kk][1][2], vreg[kk][1][3]};                  \
+    _Pragma("unroll") for (int kk = 0; kk < kKPieces; ++kk)                                                    \
+        *reinterpret_cast<u32x4*>(&sK[buf_][(kKeysPerPass * kk + tkey) * kKStride + tdim]) = KR[kk];         \
+    _Pragma("unroll") for (int kk = 0; kk < kVPieces; ++kk) {                                                  \
+      const int key = 2 * kKeysPerPass * kk + 2 * tkey;                                                        \
+      const uint32_t x[4] = {VR[kk][0][0], VR[kk][0][1], VR[kk][0][2], VR[kk][0][3]};                  \
+      const uint32_t y[4] = {VR[kk][1][0], VR[kk][1][1], VR[kk][1][2], VR[kk][1][3]};                  \
       _Pragma("unroll") for (int d2 = 0; d2 < 4; ++d2) {                                                       \
         *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2) * kVStride + vcol(tdim, key)]) =                \
             perm(y[d2], x[d2], 0x05040100u);                                                                   \
@@ -287,16 +297,22 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   float m_run[2] = {-INFINITY, -INFINITY};
   const float scale = a.scale;
 
+  // Two register sets carry the K/V pieces of the next two tiles: tile t + 2 is fetched while
+  // tile t is computed, and tile t + 1 (fetched one iteration earlier) goes to LDS at its end.
+  u32x4 kregA[kKPieces], vregA[kVPieces][2], kregB[kKPieces], vregB[kVPieces][2];
   __syncthreads();  // s_hblk ready
   if (n_tiles > 0) {
-    MI_LOAD_TILE(0);
-    MI_STORE_TILE(0);
+    MI_LOAD_TILE(0, kregA, vregA);
+    MI_STORE_TILE(0, kregA, vregA);
   }
+  if (n_tiles > 1) MI_LOAD_TILE(1, kregA, vregA);
   __syncthreads();
 
-  for (int t = 0; t < n_tiles; ++t) {
+  // kl / vl: registers tile t + 2 is fetched into; ks / vs: registers holding tile t + 1.
+  auto tile_step = [&](const int t, u32x4 (&kl)[kKPieces], u32x4 (&vl)[kVPieces][2], u32x4 (&ks_)[kKPieces],
+                       u32x4 (&vs_)[kVPieces][2]) {
     const int buf = t & 1;
-    if (t + 1 < n_tiles) MI_LOAD_TILE(t + 1);
+    if (t + 2 < n_tiles) MI_LOAD_TILE(t + 2, kl, vl);
 
     // ---- S^T = K Q^T for 64 keys x 32 queries
     f32x4 sacc[4][2];
@@ -414,8 +430,12 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
         oacc[8][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_frag, pf[nt][ks2], oacc[8][nt], 0, 0, 0);
     }
 
-    if (t + 1 < n_tiles) MI_STORE_TILE(buf ^ 1);
+    if (t + 1 < n_tiles) MI_STORE_TILE(buf ^ 1, ks_, vs_);
     __syncthreads();
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(t, kregB, vregB, kregA, vregA);
+    if (t + 1 < n_tiles) tile_step(t + 1, kregA, vregA, kregB, vregB);
   }
 
   // ---- normalise and write: lane holds query qw0 + 16 nt + ql, dims 16 dt + 4 gq + i
