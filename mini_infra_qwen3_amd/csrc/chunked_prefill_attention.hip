@@ -221,48 +221,50 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     s_hblk[i] = (x < 0 || x >= a.num_blocks) ? 0 : static_cast<int>(x);
   }
   constexpr int64_t kBlkElems = static_cast<int64_t>(kBlockSize) * kKvHeads * kHeadDim;
-  const int64_t k_hist_off = static_cast<int64_t>((tkey % kBlockSize) * kKvHeads + g) * kHeadDim + tdim;
+  // Per-lane parts of the load addresses (elements, 32-bit): the uniform parts -- the pool block
+  // of a history piece, the first chunk row of a pass -- are added as one scalar base per load.
+  const uint32_t k_hist_off = static_cast<uint32_t>(((tkey % kBlockSize) * kKvHeads + g) * kHeadDim + tdim);
   const int voff = (2 * tkey) % kBlockSize;
-  const int64_t v_hist_off0 = static_cast<int64_t>(voff * kKvHeads + g) * kHeadDim + tdim;
-  const int64_t v_hist_off1 = v_hist_off0 + kKvHeads * kHeadDim;
-  const uint16_t* k_chunk = a.key + b * a.k_row + g * a.k_head + tdim;
-  const uint16_t* v_chunk = a.value + b * a.v_row + g * a.v_head + tdim;
+  const uint32_t v_hist_off0 = static_cast<uint32_t>((voff * kKvHeads + g) * kHeadDim + tdim);
+  const uint32_t v_hist_off1 = v_hist_off0 + kKvHeads * kHeadDim;
+  const uint16_t* k_rows = a.key + b * a.k_row + g * a.k_head;
+  const uint16_t* v_rows = a.value + b * a.v_row + g * a.v_head;
+  const uint32_t k_tok = static_cast<uint32_t>(a.k_tok);  // < 2^24, checked by the entry point
+  const uint32_t v_tok = static_cast<uint32_t>(a.v_tok);
 
 #define MI_HIST_BLOCK(T, KEY) \
-  __builtin_amdgcn_readfirstlane(s_hblk[min((T) * (kKTile / kBlockSize) + (KEY) / kBlockSize, nhb - 1)])
-#define MI_LOAD_TILE(T, KR, VR)                                                                                      \
-  do {                                                                                                         \
-    const int t_ = (T);                                                                                        \
-    if (t_ < n_hist_tiles) {                                                                                   \
-      _Pragma("unroll") for (int kk = 0; kk < kKPieces; ++kk) {                                                \
-        const int64_t kb = static_cast<int64_t>(MI_HIST_BLOCK(t_, kKeysPerPass * kk + tkey)) * kBlkElems;      \
-        KR[kk] = *reinterpret_cast<const u32x4*>(a.key_pool + kb + k_hist_off);                              \
-      }                                                                                                        \
-      _Pragma("unroll") for (int kk = 0; kk < kVPieces; ++kk) {                                                \
-        const int64_t vb = static_cast<int64_t>(MI_HIST_BLOCK(t_, 2 * kKeysPerPass * kk + 2 * tkey)) * kBlkElems; \
-        VR[kk][0] = *reinterpret_cast<const u32x4*>(a.value_pool + vb + v_hist_off0);                        \
-        VR[kk][1] = *reinterpret_cast<const u32x4*>(a.value_pool + vb + v_hist_off1);                        \
-      }                                                                                                        \
-    } else {                                                                                                   \
-      const int key0 = (c_lo + t_ - n_hist_tiles) * kKTile;                                                   \
-      if (key0 + kKTile <= L) {                                                                                \
-        _Pragma("unroll") for (int kk = 0; kk < kKPieces; ++kk)                                                \
-            KR[kk] = *reinterpret_cast<const u32x4*>(k_chunk + (key0 + kKeysPerPass * kk + tkey) * a.k_tok); \
-        _Pragma("unroll") for (int kk = 0; kk < kVPieces; ++kk)                                                \
-          _Pragma("unroll") for (int e = 0; e < 2; ++e)                                                        \
-            VR[kk][e] = *reinterpret_cast<const u32x4*>(                                                     \
-                v_chunk + (key0 + 2 * kKeysPerPass * kk + 2 * tkey + e) * a.v_tok);                            \
-      } else {                                                                                                 \
-        _Pragma("unroll") for (int kk = 0; kk < kKPieces; ++kk)                                                \
-            KR[kk] = *reinterpret_cast<const u32x4*>(                                                        \
-                k_chunk + min(key0 + kKeysPerPass * kk + tkey, L - 1) * a.k_tok);                              \
-        _Pragma("unroll") for (int kk = 0; kk < kVPieces; ++kk)                                                \
-          _Pragma("unroll") for (int e = 0; e < 2; ++e)                                                        \
-            VR[kk][e] = *reinterpret_cast<const u32x4*>(                                                     \
-                v_chunk + min(key0 + 2 * kKeysPerPass * kk + 2 * tkey + e, L - 1) * a.v_tok);                  \
-      }                                                                                                        \
-    }                                                                                                          \
-  } while (0)
+  __builtin_amdgcn_readfirstlane(s_hblk[min((T) * (kKTile / kBlockSize) + (KEY) / kBlockSize, max(nhb - 1, 0))])
+  // Loads of tile t, branch-free: each piece is a scalar base (pool block, or the chunk row of the
+  // pass clamped to L - 1) plus a 32-bit lane offset, selected on the uniform history/chunk test,
+  // so the compiler can count them and wait for exactly the pieces a store needs.  Chunk rows past
+  // L - 1 read row L - 1 (their keys are masked).
+  auto load_tile = [&](const int t, u32x4 (&kr)[kKPieces], u32x4 (&vr)[kVPieces][2]) {
+    const bool hist = t < n_hist_tiles;
+    const int key0 = (c_lo + t - n_hist_tiles) * kKTile;
+#pragma unroll
+    for (int kk = 0; kk < kKPieces; ++kk) {
+      const int row = kKeysPerPass * kk;
+      const int kc = min(key0 + row, L - 1);
+      const uint32_t chunk_off = __umul24(static_cast<uint32_t>(min(tkey, L - 1 - kc)), k_tok) + tdim;
+      const uint16_t* base = hist ? a.key_pool + static_cast<int64_t>(MI_HIST_BLOCK(t, row + tkey)) * kBlkElems
+                                  : k_rows + static_cast<int64_t>(kc) * a.k_tok;
+      const uint32_t off = hist ? k_hist_off : chunk_off;
+      kr[kk] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + 2u * off);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kVPieces; ++kk) {
+      const int row = 2 * kKeysPerPass * kk;
+      const int vc = min(key0 + row, L - 1);
+      const uint16_t* base = hist ? a.value_pool + static_cast<int64_t>(MI_HIST_BLOCK(t, row + 2 * tkey)) * kBlkElems
+                                  : v_rows + static_cast<int64_t>(vc) * a.v_tok;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t chunk_off = __umul24(static_cast<uint32_t>(min(2 * tkey + e, L - 1 - vc)), v_tok) + tdim;
+        const uint32_t off = hist ? (e ? v_hist_off1 : v_hist_off0) : chunk_off;
+        vr[kk][e] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + 2u * off);
+      }
+    }
+  };
 
 #define MI_STORE_TILE(BUF, KR, VR)                                                                                 \
   do {                                                                                                         \
@@ -301,18 +303,16 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   // tile t is computed, and tile t + 1 (fetched one iteration earlier) goes to LDS at its end.
   u32x4 kregA[kKPieces], vregA[kVPieces][2], kregB[kKPieces], vregB[kVPieces][2];
   __syncthreads();  // s_hblk ready
-  if (n_tiles > 0) {
-    MI_LOAD_TILE(0, kregA, vregA);
-    MI_STORE_TILE(0, kregA, vregA);
-  }
-  if (n_tiles > 1) MI_LOAD_TILE(1, kregA, vregA);
+  load_tile(0, kregA, vregA);
+  MI_STORE_TILE(0, kregA, vregA);
+  load_tile(min(1, n_tiles - 1), kregA, vregA);
   __syncthreads();
 
   // kl / vl: registers tile t + 2 is fetched into; ks / vs: registers holding tile t + 1.
   auto tile_step = [&](const int t, u32x4 (&kl)[kKPieces], u32x4 (&vl)[kVPieces][2], u32x4 (&ks_)[kKPieces],
                        u32x4 (&vs_)[kVPieces][2]) {
     const int buf = t & 1;
-    if (t + 2 < n_tiles) MI_LOAD_TILE(t + 2, kl, vl);
+    load_tile(min(t + 2, n_tiles - 1), kl, vl);  // past the end: re-reads the last tile
 
     // ---- S^T = K Q^T for 64 keys x 32 queries
     f32x4 sacc[4][2];
@@ -430,7 +430,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
         oacc[8][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_frag, pf[nt][ks2], oacc[8][nt], 0, 0, 0);
     }
 
-    if (t + 1 < n_tiles) MI_STORE_TILE(buf ^ 1, ks_, vs_);
+    MI_STORE_TILE(buf ^ 1, ks_, vs_);  // past the end: a buffer no later tile reads
     __syncthreads();
   };
   for (int t = 0; t < n_tiles; t += 2) {
@@ -492,6 +492,8 @@ extern "C" int32_t mi_chunked_prefill_attention(
   if (max_history_blocks > 0 && history_stride < max_history_blocks)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_chunked_prefill_attention: history_stride < max_history_blocks");
   if (lens_stride <= 0) return fail(MI_ERR_INVALID_ARGUMENT, "mi_chunked_prefill_attention: lens_stride must be > 0");
+  if (key_tok_stride < 0 || key_tok_stride >= (1 << 24) || value_tok_stride < 0 || value_tok_stride >= (1 << 24))
+    return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: key/value token strides must be in [0, 2^24)");
   if (batch > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: batch > 65535");
 
   PrefillArgs a{};
