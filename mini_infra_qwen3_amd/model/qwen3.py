@@ -11,7 +11,8 @@ state_dict loads unchanged.  The attention differs in how it reaches K/V:
   chunked-prefill kernel attends causally within the chunk and reads the history straight from
   the pool through the block table (replaces the gather + concat + _attend chain).
 
-Dense GEMMs (projections, MLP, lm_head) stay on PyTorch-ROCm; the elementwise chains around them
+Dense GEMMs (projections, MLP, lm_head) stay on PyTorch-ROCm -- q/k/v, and gate/up, each as one
+GEMM over the row-concatenated weights, the outputs split as column views; the elementwise chains around them
 run as fused launches of the same library (``data_plane.rms_norm`` with the residual add,
 ``qk_norm_rope`` with the decode append, ``silu_mul``), keeping the reference's bf16 rounding points.
 """
@@ -21,6 +22,7 @@ from __future__ import annotations
 from typing import NamedTuple
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from mini_infra_qwen3_amd import data_plane
@@ -94,6 +96,20 @@ class RotaryEmbedding(nn.Module):
         return emb.cos().to(dtype), emb.sin().to(dtype)
 
 
+def _concat_weight(owner: nn.Module, linears: tuple[nn.Linear, ...]) -> torch.Tensor:
+    """Row-concatenated weights of bias-free linears that read the same input, so their
+    projections run as one GEMM (one launch) whose output columns are views of each.  Cached on
+    the owner and rebuilt when any weight moves or is modified in place (storage or version)."""
+    key = tuple((l.weight.data_ptr(), l.weight._version, l.weight.dtype) for l in linears)
+    cached = owner.__dict__.get("_concat_cache")
+    if cached is None or cached[0] != key:
+        with torch.no_grad():
+            fused = torch.cat([l.weight for l in linears], dim=0)
+        owner.__dict__["_concat_cache"] = (key, fused)
+        return fused
+    return cached[1]
+
+
 class Qwen3Attention(nn.Module):
     def __init__(self, config: Qwen3Config):
         super().__init__()
@@ -109,10 +125,12 @@ class Qwen3Attention(nn.Module):
         self.k_norm = RMSNorm(config.head_dim, config.rms_norm_eps)
 
     def forward(self, hidden, cos, sin, kv_pool: PastKeyValue, metadata, workspace=None):
-        """q/k/v projections (PyTorch GEMMs), then one fused launch for q/k RMSNorm + RoPE (plus,
+        """q/k/v projections (one PyTorch GEMM over the concatenated weights), then one fused launch for q/k RMSNorm + RoPE (plus,
         when decoding, the K/V append into the pool), then paged attention."""
         batch, length, _ = hidden.shape
-        q, k, v = self.q_proj(hidden), self.k_proj(hidden), self.v_proj(hidden)
+        nq, nkv = self.num_heads * self.head_dim, self.num_kv_heads * self.head_dim
+        qkv = F.linear(hidden, _concat_weight(self, (self.q_proj, self.k_proj, self.v_proj)))
+        q, k, v = qkv[..., :nq], qkv[..., nq:nq + nkv], qkv[..., nq + nkv:]
         key_pool, value_pool = kv_pool
         eps = self.q_norm.eps
         if isinstance(metadata, PagedAttentionMetadata):
@@ -147,7 +165,9 @@ class Qwen3MLP(nn.Module):
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(data_plane.silu_mul(self.gate_proj(x), self.up_proj(x)))
+        inter = self.gate_proj.out_features
+        gate_up = F.linear(x, _concat_weight(self, (self.gate_proj, self.up_proj)))
+        return self.down_proj(data_plane.silu_mul(gate_up[..., :inter], gate_up[..., inter:]))
 
 
 class Qwen3DecoderLayer(nn.Module):
