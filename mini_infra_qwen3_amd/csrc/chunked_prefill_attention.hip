@@ -13,24 +13,27 @@
 // chunk keys j with L - len_b <= j <= i.  Rows i < L - len_b (padding) get a zero output.
 //
 // Tiling for gfx950 (v_mfma_f32_16x16x32_bf16, 64-lane wavefronts):
-//  * workgroup = (row b, KV head g, 64-query tile), 4 wavefronts: wave w serves query head
-//    2 g + (w >> 1) and queries [32 (w & 1), +32) of the tile, so the two GQA heads share
-//    every K/V tile staged in LDS.
+//  * workgroup = (row b, KV head g, 128-query tile), 8 wavefronts (one workgroup per CU at two
+//    waves per SIMD): wave w serves query head 2 g + (w >> 2) and queries [32 (w & 3), +32) of
+//    the tile, so the two GQA heads share every K/V tile staged in LDS.
 //  * KV tiles of 64 keys: history tiles first (pool blocks through the block table -- the
 //    gather is fused, nothing is materialised), then chunk tiles up to the causal limit.
-//    K is staged row-major, V transposed (V^T) in double-buffered LDS; the next tile's global
-//    loads are in flight while the current one is multiplied.
+//    K is staged row-major (288-byte rows), V transposed (V^T) in double-buffered LDS; the loads
+//    of the next two tiles are in flight in registers while the current one is multiplied.
 //  * S^T = K Q^T: A = K rows from LDS, B = Q^T from registers (loaded once), C lane layout =
 //    (query = lane % 16, keys 4 (lane / 16) + i).  Each query's softmax state lives in the
 //    lanes of its column; the row max needs two cross-lane steps, the row sum is deferred.
 //  * O^T = V^T P^T: the probabilities of a 32-key step are already in the B-operand lanes if
-//    the MFMA's k index is read as key 16 (k' / 4) + 4 (lane / 16) + k' % 4; the A operand
-//    (V^T) is read from LDS with the same permutation (two 8-byte reads).
+//    the MFMA's k index is read as key 16 (k' / 4) + 4 (lane / 16) + k' % 4; V^T rows in LDS
+//    hold the keys in that order, so the A operand is one 16-byte read.
 //  * Softmax and accumulation are fp32 with lazy rescaling of the running max as in the decode
 //    kernel.  Scores keep the reference's bf16 rounding points (bf16 product, then bf16 product
-//    with the scale), done on pairs with the packed bf16 convert (~4 VALU ops per score):
-//    for N(0,1) inputs those roundings move logits by ~1e-2, so dropping them
-//    (MI_PREFILL_EXACT_SCORES=0, scale folded into the exp2 FMA) leaves the 2e-2 parity band.
+//    with the scale), one packed bf16 convert per rounding: for N(0,1) inputs those roundings
+//    move logits by ~1e-2, so dropping them (MI_PREFILL_EXACT_SCORES=0, scale folded into the
+//    exp2 FMA) leaves the 2e-2 parity band.
+//  * Measured on MI355X, MFMA and VALU work of the same SIMD mostly add up rather than overlap,
+//    so the time per tile is about MFMA + VALU: the score roundings, exponentials and converts
+//    are the VALU share.
 #include "mi_common.h"
 
 namespace mi {
@@ -49,10 +52,10 @@ constexpr int kKTile = 64;                 // keys per KV tile
 #define MI_PREFILL_K_PAD 16
 #endif
 #ifndef MI_PREFILL_V_PAD
-#define MI_PREFILL_V_PAD 4
+#define MI_PREFILL_V_PAD 8
 #endif
 constexpr int kKStride = kHeadDim + MI_PREFILL_K_PAD;  // LDS row of K (elements): 288 B
-constexpr int kVStride = kKTile + MI_PREFILL_V_PAD;    // LDS row of V^T (elements): 136 B
+constexpr int kVStride = kKTile + MI_PREFILL_V_PAD;    // LDS row of V^T (elements): 144 B, 16-byte aligned
 constexpr int kThreads = 64 * kGroup * kWavesPerHead;    // one workgroup per CU at 4 waves per head
 constexpr int kKeysPerPass = kThreads / 16;               // K rows one pass of 16-byte pieces covers
 constexpr int kKPieces = kKTile / kKeysPerPass;           // K pieces per thread and tile
@@ -120,6 +123,13 @@ __device__ __forceinline__ void reference_scores(f32x4& v, float scale) {
 // x = lane % 16 -- spread over all banks (32 or 64 banks of 4 bytes) instead of 8 of them, while
 // the PV operand reads (8 consecutive keys of one dim) stay contiguous and conflict-free.
 __device__ __forceinline__ int vcol(int dim, int key) { return (key + 8 * (dim >> 5)) & (kKTile - 1); }
+// Position of key k of a tile in its V^T row (before the vcol rotation): the 8 keys one lane group
+// feeds to a PV MFMA (16 (k' / 4) + 4 (lane / 16) + k' % 4 within each 32-key half) sit next to
+// each other, so the A operand is one 16-byte read; key pairs (2 j, 2 j + 1) stay adjacent.
+__device__ __forceinline__ int vpos(int key) {
+  const int k = key & 31;
+  return (key & 32) + 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3);
+}
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
@@ -276,9 +286,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
       const uint32_t x[4] = {VR[kk][0][0], VR[kk][0][1], VR[kk][0][2], VR[kk][0][3]};                  \
       const uint32_t y[4] = {VR[kk][1][0], VR[kk][1][1], VR[kk][1][2], VR[kk][1][3]};                  \
       _Pragma("unroll") for (int d2 = 0; d2 < 4; ++d2) {                                                       \
-        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2) * kVStride + vcol(tdim, key)]) =                \
+        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2) * kVStride + vcol(tdim, vpos(key))]) =          \
             perm(y[d2], x[d2], 0x05040100u);                                                                   \
-        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2 + 1) * kVStride + vcol(tdim, key)]) =            \
+        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2 + 1) * kVStride + vcol(tdim, vpos(key))]) =      \
             perm(y[d2], x[d2], 0x07060302u);                                                                   \
       }                                                                                                        \
     }                                                                                                          \
@@ -418,9 +428,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const uint16_t* vrow = &sV[buf][(dt * 16 + ql) * kVStride];
-        const bf16x4 v0 = *reinterpret_cast<const bf16x4*>(vrow + vcol(dt * 16, 32 * ks2 + 4 * gq));
-        const bf16x4 v1 = *reinterpret_cast<const bf16x4*>(vrow + vcol(dt * 16, 32 * ks2 + 4 * gq + 16));
-        const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vrow + vcol(dt * 16, 32 * ks2 + 8 * gq));
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
           oacc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[nt][ks2], oacc[dt][nt], 0, 0, 0);
