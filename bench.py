@@ -450,7 +450,7 @@ def main() -> int:
         kernels["gather"] = bench_gather(max(args.steps // 4, 3), 1, device)
         log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s")
         torch.cuda.empty_cache()
-        kernels["chunked_prefill"] = bench_prefill(max(args.steps // 4, 3), 1, device)
+        kernels["chunked_prefill"] = bench_prefill(max(args.steps // 4, 3), 3, device)
         log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "
             f"{kernels['chunked_prefill']['achieved_TFLOPs']:.1f} TFLOP/s")
         torch.cuda.empty_cache()
