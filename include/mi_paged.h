@@ -165,7 +165,8 @@ int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, const void*
  * history_blocks: [batch, max_history_blocks] int64, row stride history_stride; ids outside
  *   [0, num_blocks) read block 0.  start_lens / chunk_lens: int64 with element stride lens_stride.
  * Specialised for head_dim 128, block_size 16, num_heads = 2 * num_kv_heads, num_kv_heads in
- * {1, 2, 4, 8}; strides multiples of 8 elements and 16-byte aligned tensors.
+ * {1, 2, 4, 8}; strides multiples of 8 elements, key / value token strides below 2^24 elements,
+ * and 16-byte aligned tensors.
  */
 int32_t mi_chunked_prefill_attention(void* out, int64_t out_row_stride, int64_t out_tok_stride, const void* query,
                                      int64_t query_row_stride, int64_t query_head_stride, int64_t query_tok_stride,

@@ -122,5 +122,6 @@ def test_prefill_rejects_unsupported_shapes_on_host(native_lib):
     assert call(bs=32) == _native.MI_ERR_UNSUPPORTED
     assert call(heads=8) == _native.MI_ERR_UNSUPPORTED
     assert call(tok=100) == _native.MI_ERR_UNSUPPORTED  # stride not a multiple of 8 elements
+    assert call(tok=1 << 24) == _native.MI_ERR_UNSUPPORTED  # key / value token stride >= 2^24 elements
     assert call(hstride=1) == _native.MI_ERR_INVALID_ARGUMENT
     assert call(hist=None) == _native.MI_ERR_INVALID_ARGUMENT
