@@ -67,7 +67,7 @@ constexpr int kMaxWaves = MI_DECODE_MAX_WAVES;     // wavefronts (KV heads) per 
 constexpr bool kNtLoads = MI_DECODE_NT_LOADS != 0; // K/V stream with the non-temporal hint
 constexpr int kGroupsPerCu = MI_DECODE_GROUPS_PER_CU;
 constexpr int kMaxBatchPerLaunch = 4096;           // sequences whose prefix sum one workgroup holds in LDS
-constexpr int kMinBlocksPerStream = 32;            // small launches use fewer, longer ranges
+constexpr int kMinBlocksPerStream = 16;            // small launches use fewer, longer ranges
 constexpr int kWindow = 64;                        // block ids fetched per window, one per lane
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;

@@ -42,12 +42,12 @@ def test_abi_version(native_lib):
 def test_decode_workspace_size(native_lib):
     # two slots per block range per head, (128 + 2) floats each; ranges = resident workgroups
     # (256 CUs x 4, over 4 head groups at 8 KV heads; 256 CUs assumed without a device), fewer
-    # for launches under 32 blocks per range
+    # for launches under 16 blocks per range
     slot = 2 * 16 * 130 * 4
     assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 128, 16) == 256 * slot
     assert native_lib.mi_paged_decode_workspace_bytes(256, 32, 16, 128, 16) == 256 * slot
-    assert native_lib.mi_paged_decode_workspace_bytes(4, 33, 16, 128, 16) == 5 * slot
-    assert native_lib.mi_paged_decode_workspace_bytes(16, 80, 16, 128, 16) == 40 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(4, 33, 16, 128, 16) == 9 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(16, 80, 16, 128, 16) == 80 * slot
     assert native_lib.mi_paged_decode_workspace_bytes(1, 1, 16, 128, 16) == 1 * slot
     assert native_lib.mi_paged_decode_workspace_bytes(0, 512, 16, 128, 16) == 0
     assert native_lib.mi_paged_decode_workspace_bytes(8, 0, 16, 128, 16) == 0
