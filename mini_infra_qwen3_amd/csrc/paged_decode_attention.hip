@@ -42,6 +42,9 @@
 //    zero rows for empty contexts.  (Merging inside the first kernel needs device-scope
 //    release/acquire fences, and on this GPU each such fence writes back and invalidates a
 //    whole XCD L2: far more costly than a launch.)
+#include <cstdlib>
+#include <cstring>
+
 #include "mi_common.h"
 
 namespace mi {
@@ -407,6 +410,201 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
   }
 }
 
+// ---- Small launches: one workgroup per (sequence, KV head).  Its kSeqWaves wavefronts take
+// blocks w, w + kSeqWaves, ... of the sequence with the stream kernel's per-block arithmetic
+// (same lane layout, rounding points and lazy rescale), merge their four rows, then merge the
+// wavefronts' softmax states through LDS and write the bf16 rows: one launch, nothing in the
+// workspace.  A few sequences then spread over many wavefronts instead of a few block ranges
+// that a second launch has to merge.
+#ifndef MI_DECODE_SEQ_WAVES
+#define MI_DECODE_SEQ_WAVES 8
+#endif
+#ifndef MI_DECODE_SEQ_DEPTH
+#define MI_DECODE_SEQ_DEPTH 2
+#endif
+constexpr int kSeqWaves = MI_DECODE_SEQ_WAVES;
+constexpr int kSeqMaxBlocks = 64 * kSeqWaves;  // a lane holds one block id of its wavefront
+
+template <int kKvHeads>
+__global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const DecodeArgs a) {
+  constexpr int kRowElems = kKvHeads * kHeadDim;
+  constexpr int kBlockElems = kBlockSize * kRowElems;
+  constexpr int kSeqDepth = MI_DECODE_SEQ_DEPTH;  // ring: the next kSeqDepth - 1 blocks of the wavefront in flight
+  __shared__ float s_acc[kSeqWaves][kGroup][kHeadDim];
+  __shared__ float s_ml[kSeqWaves][kGroup][2];
+  const int b = blockIdx.x;
+  const int g = blockIdx.y;
+  const int w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int dl = lane & 15;
+  const int r = lane >> 4;
+  const int n = static_cast<int>(context_of(a, b));
+  const int nblk = blocks_of(n);
+  uint16_t* out_b = a.out + b * a.out_row + (g * kGroup) * kHeadDim;  // query heads 2 g, 2 g + 1
+  if (nblk == 0) {  // empty context: zero rows (uniform over the workgroup)
+    if (threadIdx.x < kGroup * 16) *reinterpret_cast<uint4*>(out_b + 8 * threadIdx.x) = uint4{0, 0, 0, 0};
+    return;
+  }
+  const float scale = a.scale;
+  const int lane_off = r * kRowElems + g * kHeadDim + 8 * dl;
+  const int cnt = nblk > w ? (nblk - 1 - w) / kSeqWaves + 1 : 0;  // blocks w + kSeqWaves i, i < cnt <= 64
+
+  // Lane i holds the id of block w + kSeqWaves i (ids outside the pool read block 0).
+  uint32_t id_lo = 0, id_hi = 0;
+  if (lane < cnt) {
+    int64_t id = a.block_tables[b * a.bt_stride + w + kSeqWaves * lane];
+    if (id < 0 || id >= a.num_blocks) id = 0;
+    id_lo = static_cast<uint32_t>(id);
+    id_hi = static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32);
+  }
+  const uint16_t* qp = a.query + b * a.q_row + (g * kGroup) * a.q_head + 8 * dl;
+  const uint4 q0 = *reinterpret_cast<const uint4*>(qp);
+  const uint4 q1 = *reinterpret_cast<const uint4*>(qp + a.q_head);
+
+  float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
+  float acc0[8], acc1[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) acc0[d] = acc1[d] = 0.0f;
+
+  u32x4 kbuf[kSeqDepth][4], vbuf[kSeqDepth][4];
+  auto issue = [&](int slot, int i) {  // block w + kSeqWaves i, clamped to the wavefront's last
+    i = min(i, cnt - 1);
+    const uint32_t blo = __builtin_amdgcn_readlane(id_lo, i);
+    const uint32_t bhi = __builtin_amdgcn_readlane(id_hi, i);
+    const int64_t base = static_cast<int64_t>((static_cast<uint64_t>(bhi) << 32) | blo) * kBlockElems;
+    const uint16_t* kp = a.key_pool + base + lane_off;
+    const uint16_t* vp = a.value_pool + base + lane_off;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) kbuf[slot][t] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(kp + t * 4 * kRowElems));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) vbuf[slot][t] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(vp + t * 4 * kRowElems));
+  };
+  if (cnt > 0) {  // wave-uniform
+#pragma unroll
+    for (int s = 0; s < kSeqDepth - 1; ++s) issue(s, s);  // ring slot of block i: i % kSeqDepth
+    if (kSeqDepth == 1) issue(0, 0);
+    for (int i0 = 0; i0 < cnt; i0 += kSeqDepth) {
+#pragma unroll
+      for (int s = 0; s < kSeqDepth; ++s) {
+        const int i = i0 + s;
+        if (i >= cnt) break;  // wave-uniform
+        if (kSeqDepth > 1) issue((s + kSeqDepth - 1) % kSeqDepth, i + kSeqDepth - 1);
+        else if (i > 0) issue(0, i);
+
+        float s0[4], s1[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          s0[t] = score_log2(dpp_sum16(dot8(q0, kbuf[s][t])), scale);
+          s1[t] = score_log2(dpp_sum16(dot8(q1, kbuf[s][t])), scale);
+        }
+        const int tok_base = (w + kSeqWaves * i) * kBlockSize;
+        if (tok_base + kBlockSize > n) {  // the sequence's last block (uniform branch)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const bool valid = tok_base + 4 * t + r < n;
+            s0[t] = valid ? s0[t] : -INFINITY;
+            s1[t] = valid ? s1[t] : -INFINITY;
+          }
+        }
+        const float mb0 = fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3]));
+        const float mb1 = fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]));
+        const bool grow = (mb0 > m0 + kRescaleSlack) || (mb1 > m1 + kRescaleSlack);
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float n0 = fmaxf(m0, mb0), n1 = fmaxf(m1, mb1);
+          const float a0 = (n0 == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m0 - n0);
+          const float a1 = (n1 == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m1 - n1);
+          m0 = n0;
+          m1 = n1;
+          l0 *= a0;
+          l1 *= a1;
+#pragma unroll
+          for (int d = 0; d < 8; ++d) {
+            acc0[d] *= a0;
+            acc1[d] *= a1;
+          }
+        }
+        const float r0 = m0 == -INFINITY ? 0.0f : m0;
+        const float r1 = m1 == -INFINITY ? 0.0f : m1;
+        float p0[4], p1[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          p0[t] = __builtin_amdgcn_exp2f(s0[t] - r0);
+          p1[t] = __builtin_amdgcn_exp2f(s1[t] - r1);
+        }
+        l0 += (p0[0] + p0[1]) + (p0[2] + p0[3]);
+        l1 += (p1[0] + p1[1]) + (p1[2] + p1[3]);
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          const uint32_t ph0 = pack_p(p0[2 * pr], p0[2 * pr + 1]);
+          const uint32_t ph1 = pack_p(p1[2 * pr], p1[2 * pr + 1]);
+          const u32x4 va = vbuf[s][2 * pr];
+          const u32x4 vc = vbuf[s][2 * pr + 1];
+          const uint32_t aw[4] = {va[0], va[1], va[2], va[3]};
+          const uint32_t cw[4] = {vc[0], vc[1], vc[2], vc[3]};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t plo = __builtin_amdgcn_perm(cw[q], aw[q], 0x05040100u);
+            const uint32_t phi = __builtin_amdgcn_perm(cw[q], aw[q], 0x07060302u);
+            acc0[2 * q] = fdot2(ph0, plo, acc0[2 * q]);
+            acc0[2 * q + 1] = fdot2(ph0, phi, acc0[2 * q + 1]);
+            acc1[2 * q] = fdot2(ph1, plo, acc1[2 * q]);
+            acc1[2 * q + 1] = fdot2(ph1, phi, acc1[2 * q + 1]);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- merge the four rows of the wavefront (log-sum-exp), then the wavefronts through LDS
+  float M0 = fmaxf(m0, __shfl_xor(m0, 16));
+  M0 = fmaxf(M0, __shfl_xor(M0, 32));
+  float M1 = fmaxf(m1, __shfl_xor(m1, 16));
+  M1 = fmaxf(M1, __shfl_xor(M1, 32));
+  const float w0 = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M0);
+  const float w1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - M1);
+  l0 *= w0;
+  l1 *= w1;
+  l0 += __shfl_xor(l0, 16);
+  l0 += __shfl_xor(l0, 32);
+  l1 += __shfl_xor(l1, 16);
+  l1 += __shfl_xor(l1, 32);
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    acc0[d] *= w0;
+    acc1[d] *= w1;
+    acc0[d] += __shfl_xor(acc0[d], 16);
+    acc0[d] += __shfl_xor(acc0[d], 32);
+    acc1[d] += __shfl_xor(acc1[d], 16);
+    acc1[d] += __shfl_xor(acc1[d], 32);
+  }
+  if (r < kGroup) {  // row 0: query head 2 g, row 1: 2 g + 1 (every row holds both after the merge)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) s_acc[w][r][8 * dl + d] = r == 0 ? acc0[d] : acc1[d];
+    if (dl == 0) {
+      s_ml[w][r][0] = r == 0 ? M0 : M1;
+      s_ml[w][r][1] = r == 0 ? l0 : l1;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < kGroup * 16) {
+    const int h = threadIdx.x >> 4;
+    const int dm = threadIdx.x & 15;
+    float M = -INFINITY;
+    for (int v = 0; v < kSeqWaves; ++v) M = fmaxf(M, s_ml[v][h][0]);
+    float L = 0.0f, o[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[d] = 0.0f;
+    for (int v = 0; v < kSeqWaves; ++v) {
+      const float mv = s_ml[v][h][0];
+      const float e = mv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv - M);
+      L += e * s_ml[v][h][1];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) o[d] += e * s_acc[v][h][8 * dm + d];
+    }
+    store_bf16x8(out_b + h * kHeadDim + 8 * dm, o, 1.0f / L);
+  }
+}
+
 // Finishes what the stream kernel left: sequences cut by a range boundary (merge of their
 // partials: the cut range's last-sequence slot, then the first-sequence slot of every later
 // range up to the one holding the sequence's last block) and empty contexts (zero rows).
@@ -512,13 +710,28 @@ int streams_for(int32_t batch, int32_t max_blocks, int32_t num_kv_heads) {
   return static_cast<int>(s < 1 ? 1 : s);
 }
 
+// The per-sequence kernel serves launches of at most one workgroup per CU with tables it can
+// hold; MI_DECODE_PATH=stream or =seq (environment) forces one kernel where both apply.
+bool use_seq_path(int32_t batch, int32_t max_blocks, int32_t num_kv_heads) {
+  if (max_blocks <= 0 || max_blocks > kSeqMaxBlocks) return false;
+  const char* forced = getenv("MI_DECODE_PATH");
+  if (forced && strcmp(forced, "stream") == 0) return false;
+  if (forced && strcmp(forced, "seq") == 0) return true;
+  return static_cast<int64_t>(batch) * num_kv_heads <= device_cus();
+}
+
 template <int kKvHeads>
-int32_t launch_decode(const DecodeArgs& a, hipStream_t s) {
+int32_t launch_decode(const DecodeArgs& a, bool seq_path, hipStream_t s) {
   constexpr int kWaves = kKvHeads < kMaxWaves ? kKvHeads : kMaxWaves;
   constexpr int kHeadGroups = kKvHeads / kWaves;
   constexpr int kHeads = kKvHeads * kGroup;
   constexpr int kMergeThreads = kHeads * 16 < 64 ? 64 : kHeads * 16;
   const size_t lds = sizeof(int) * (static_cast<size_t>(a.batch) + 1);
+  if (seq_path) {
+    if (a.max_blocks > kSeqMaxBlocks) return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: table too long");
+    paged_decode_seq_kernel<kKvHeads><<<dim3(a.batch, kKvHeads), 64 * kSeqWaves, 0, s>>>(a);
+    return check_launch("mi_paged_decode_attention(seq)");
+  }
   if (a.max_blocks > 0) {
     paged_decode_kernel<kKvHeads, kWaves><<<static_cast<uint32_t>(a.streams) * kHeadGroups, 64 * kWaves, lds, s>>>(a);
     int32_t rc = check_launch("mi_paged_decode_attention");
@@ -583,6 +796,7 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
   float* ws_ml = ws_acc ? ws_acc + static_cast<int64_t>(streams) * 2 * num_heads * kHeadDim : nullptr;
 
   hipStream_t s = as_stream(stream);
+  const bool seq_path = use_seq_path(batch, max_blocks, num_kv_heads);
   // Sequences go in slices of at most kMaxBatchPerLaunch (the per-workgroup prefix sum lives in
   // LDS); the slices reuse the workspace one after the other on the stream.
   for (int32_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
@@ -608,10 +822,10 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
     a.ws_ml = ws_ml;
     int32_t rc;
     switch (num_kv_heads) {
-      case 1: rc = launch_decode<1>(a, s); break;
-      case 2: rc = launch_decode<2>(a, s); break;
-      case 4: rc = launch_decode<4>(a, s); break;
-      default: rc = launch_decode<8>(a, s); break;
+      case 1: rc = launch_decode<1>(a, seq_path, s); break;
+      case 2: rc = launch_decode<2>(a, seq_path, s); break;
+      case 4: rc = launch_decode<4>(a, seq_path, s); break;
+      default: rc = launch_decode<8>(a, seq_path, s); break;
     }
     if (rc != MI_OK) return rc;
   }

@@ -17,6 +17,18 @@ TOL = 2e-2  # max-abs on bf16 outputs
 SCALE = 128 ** -0.5
 
 
+@pytest.fixture(autouse=True, params=["auto", "stream", "seq"])
+def decode_path(request, monkeypatch):
+    """Every case runs through both kernels of the entry point: the block-range stream kernel with
+    its merge launch, and the per-sequence kernel small launches use (the library picks one per
+    call; MI_DECODE_PATH forces it where the table fits the per-sequence kernel)."""
+    if request.param == "auto":
+        monkeypatch.delenv("MI_DECODE_PATH", raising=False)
+    else:
+        monkeypatch.setenv("MI_DECODE_PATH", request.param)
+    return request.param
+
+
 def run_kernel(query, key_pool, value_pool, tables, ctx, device):
     return data_plane.paged_decode_attention(
         query.to(device), key_pool.to(device), value_pool.to(device), tables.to(device),
