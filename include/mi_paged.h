@@ -129,7 +129,10 @@ int64_t mi_paged_decode_workspace_bytes(int32_t batch, int32_t max_blocks, int32
  * workspace: at least mi_paged_decode_workspace_bytes(...) bytes (may be null when
  *   max_blocks is 0).  The launch's blocks are cut into equal ranges, one per workgroup
  *   (and head group); sequences cut between ranges leave partials that a second, small
- *   launch merges (it also writes the zero rows).
+ *   launch merges (it also writes the zero rows).  Launches of at most one (sequence, KV
+ *   head) per CU with max_blocks <= 512 run a single per-sequence kernel instead, which
+ *   leaves the workspace untouched; the environment variable MI_DECODE_PATH=stream or =seq
+ *   forces either kernel where both apply.
  * Specialised for head_dim 128, block_size 16 and num_heads = 2 * num_kv_heads with
  * num_kv_heads in {1, 2, 4, 8}; other shapes return MI_ERR_UNSUPPORTED.
  */
