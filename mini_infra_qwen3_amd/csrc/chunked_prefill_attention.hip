@@ -29,8 +29,7 @@
 //  * Softmax and accumulation are fp32 with lazy rescaling of the running max as in the decode
 //    kernel.  Scores keep the reference's bf16 rounding points (bf16 product, then bf16 product
 //    with the scale), one packed bf16 convert per rounding: for N(0,1) inputs those roundings
-//    move logits by ~1e-2, so dropping them (MI_PREFILL_EXACT_SCORES=0, scale folded into the
-//    exp2 FMA) leaves the 2e-2 parity band.
+//    move logits by ~1e-2, so dropping them would leave the 2e-2 parity band.
 //  * Measured on MI355X, MFMA and VALU work of the same SIMD mostly add up rather than overlap,
 //    so the time per tile is about MFMA + VALU: the score roundings, exponentials and converts
 //    are the VALU share.
@@ -64,10 +63,6 @@ static_assert(kKPieces * kKeysPerPass == kKTile && kVPieces * 2 * kKeysPerPass =
 constexpr int kMaxHistoryBlocks = 16384;   // history table staged in LDS: 64 KiB at most (256k tokens)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;
-#ifndef MI_PREFILL_EXACT_SCORES
-#define MI_PREFILL_EXACT_SCORES 1
-#endif
-constexpr bool kExactScores = MI_PREFILL_EXACT_SCORES != 0;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -350,14 +345,11 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     } else {
       need_mask = key0 + kKTile - 1 > qw0 || key0 < pad || qw0 < pad || qw0 + 31 >= L;
     }
-    // Exact form: scores rounded like the reference, log2(e) applied inside the exp2 FMA below;
-    // fast form: raw dots with scale * log2(e) there (max commutes with a positive factor).
-    if constexpr (kExactScores) {
+    // Scores rounded like the reference; log2(e) is applied inside the exp2 FMA below.
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) reference_scores(sacc[mt][nt], scale);
-    }
+      for (int nt = 0; nt < 2; ++nt) reference_scores(sacc[mt][nt], scale);
     if (need_mask) {
       // Bitwise (not short-circuit) conditions keep the edge-tile path free of branches.
 #pragma unroll
@@ -381,7 +373,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     // Lazy rescale: m_run (shared by the four lanes of a query column) only has to bound every
     // score to within kRescaleSlack, so each lane tests its own 16 scores and the cross-lane
     // column max is taken only on the rare tiles that raise m_run.
-    const float to_log2 = kExactScores ? kLog2e : scale * kLog2e;
+    constexpr float to_log2 = kLog2e;
     float mx[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
