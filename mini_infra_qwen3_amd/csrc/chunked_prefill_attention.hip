@@ -94,13 +94,6 @@ struct PrefillArgs {
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// bf16 rounding of two floats with one packed convert; the results are exact fp32 values.
-__device__ __forceinline__ void round_bf16_pair(float& x, float& y) {
-  const uint32_t pk = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, y}, bf16x2));
-  x = __uint_as_float(pk << 16);
-  y = __uint_as_float(pk & 0xffff0000u);
-}
-
 // bf16 rounding of one float as an fp32 value in one instruction: the packed convert with a zero
 // low half leaves bf16(x) in the high half and zeros below, which is exactly bf16(x) as fp32.
 __device__ __forceinline__ float round_bf16_hi(float x) {
