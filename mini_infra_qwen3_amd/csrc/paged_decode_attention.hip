@@ -483,11 +483,13 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
 #pragma unroll
     for (int s = 0; s < kSeqDepth - 1; ++s) issue(s, s);  // ring slot of block i: i % kSeqDepth
     if (kSeqDepth == 1) issue(0, 0);
+    // Whole rounds of kSeqDepth blocks, so that the loads stay in straight-line code the compiler
+    // can count: indices past cnt re-read the last block and mask all its tokens (block
+    // w + kSeqWaves i >= nblk starts at or past the context end).
     for (int i0 = 0; i0 < cnt; i0 += kSeqDepth) {
 #pragma unroll
       for (int s = 0; s < kSeqDepth; ++s) {
         const int i = i0 + s;
-        if (i >= cnt) break;  // wave-uniform
         if (kSeqDepth > 1) issue((s + kSeqDepth - 1) % kSeqDepth, i + kSeqDepth - 1);
         else if (i > 0) issue(0, i);
 
