@@ -384,6 +384,7 @@ def bench_e2e(device: torch.device, seed: int = 0) -> dict:
         "arrival_rate_req_s": 20.0,
         "decode_graphs": True,
         "setup_s": round(setup_s, 2),
+        "latency_ms": {k: round(v, 2) for k, v in res.latency_summary().items()},
     }
     del model, res
     torch.cuda.empty_cache()

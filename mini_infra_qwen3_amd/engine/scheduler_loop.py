@@ -14,6 +14,7 @@ function of the plan, which makes the schedule independent of timing: two backen
 
 from __future__ import annotations
 
+import math
 import time
 from collections.abc import Callable, Sequence
 from dataclasses import dataclass
@@ -48,6 +49,44 @@ class ScheduleEvent:
     live_kv_cache_bytes: int
 
 
+def percentile(values: Sequence[float], percent: float) -> float:
+    """Nearest-rank percentile, 0.0 for no values (reference src/mini_infra/utils.py:7-13): the
+    ceil(n * percent / 100)-th smallest value, at least the first."""
+    if not values:
+        return 0.0
+    ordered = sorted(values)
+    rank = max(1, math.ceil(len(ordered) * percent / 100))
+    return ordered[min(rank, len(ordered)) - 1]
+
+
+@dataclass(frozen=True)
+class RequestLatency:
+    """Logical-clock timeline of one request (reference core/types.py:278-304), in ms."""
+
+    request_idx: int
+    arrival_ms: float
+    admitted_ms: float
+    first_token_ms: float
+    completion_ms: float
+    token_times_ms: tuple[float, ...]
+
+    @property
+    def queue_ms(self) -> float:
+        return self.admitted_ms - self.arrival_ms
+
+    @property
+    def ttft_ms(self) -> float:
+        return self.first_token_ms - self.arrival_ms
+
+    @property
+    def end_to_end_ms(self) -> float:
+        return self.completion_ms - self.arrival_ms
+
+    @property
+    def inter_token_latencies_ms(self) -> list[float]:
+        return [b - a for a, b in zip(self.token_times_ms, self.token_times_ms[1:])]
+
+
 @dataclass(frozen=True)
 class ScheduleResult:
     """Generated tokens per request (request_idx order), the step events and the summary."""
@@ -60,6 +99,23 @@ class ScheduleResult:
     wall_ms: float
     makespan_ms: float
     num_output_tokens: int
+    requests: tuple[RequestLatency, ...] = ()
+
+    def latency_summary(self) -> dict[str, float]:
+        """Queue, TTFT, end-to-end and inter-token latency percentiles over the requests, as the
+        reference's schedule metrics report them (src/mini_infra/engine/metrics.py:370,426-434)."""
+        itls = [x for r in self.requests for x in r.inter_token_latencies_ms]
+        return {
+            "queue_ms_p50": percentile([r.queue_ms for r in self.requests], 50),
+            "queue_ms_p95": percentile([r.queue_ms for r in self.requests], 95),
+            "ttft_ms_p50": percentile([r.ttft_ms for r in self.requests], 50),
+            "ttft_ms_p95": percentile([r.ttft_ms for r in self.requests], 95),
+            "end_to_end_ms_p50": percentile([r.end_to_end_ms for r in self.requests], 50),
+            "end_to_end_ms_p95": percentile([r.end_to_end_ms for r in self.requests], 95),
+            "itl_ms_p50": percentile(itls, 50),
+            "itl_ms_p95": percentile(itls, 95),
+            "itl_ms_max": max(itls, default=0.0),
+        }
 
     @property
     def throughput_tok_s(self) -> float:
@@ -134,7 +190,10 @@ def run_scheduler(backend, requests: Sequence[Request], token_budget: int = 2048
         wall_ms=wall_ms,
         makespan_ms=max(s.completion_ms for s in states) - min(r.arrival_ms for r in requests),
         num_output_tokens=sum(len(s.generated) for s in states),
+        requests=tuple(RequestLatency(s.request.request_idx, s.request.arrival_ms, s.admitted_ms, s.first_token_ms,
+                                      s.completion_ms, tuple(s.token_times_ms))
+                       for s in sorted(states, key=lambda s: s.request.request_idx)),
     )
 
 
-__all__ = ["ScheduleEvent", "ScheduleResult", "run_scheduler"]
+__all__ = ["RequestLatency", "ScheduleEvent", "ScheduleResult", "percentile", "run_scheduler"]

@@ -8,7 +8,7 @@ import pytest
 
 from mini_infra_qwen3_amd.core import KVCacheManager, Request
 from mini_infra_qwen3_amd.core.scheduler import IterationScheduler, RequestState, SchedulePhase
-from mini_infra_qwen3_amd.engine import ScheduleStepOutput, run_scheduler
+from mini_infra_qwen3_amd.engine import ScheduleStepOutput, percentile, run_scheduler
 
 DECODE, PREFILL = SchedulePhase.DECODE, SchedulePhase.PREFILL
 
@@ -178,3 +178,29 @@ def test_step_clock_makes_the_schedule_timing_independent():
     run_scheduler(a, requests, token_budget=8, max_running_requests=3, step_clock=lambda out: 5.0)
     run_scheduler(b, requests, token_budget=8, max_running_requests=3, step_clock=lambda out: 5.0)
     assert a.executed == b.executed
+
+
+def test_percentile_is_nearest_rank():
+    # reference src/mini_infra/utils.py:7-13: the ceil(n p / 100)-th smallest, at least the first
+    assert percentile([], 50) == 0.0
+    assert percentile([7.0], 95) == 7.0
+    assert percentile(list(range(1, 11)), 50) == 5
+    assert percentile(list(range(1, 11)), 95) == 10
+    assert percentile(list(range(1, 11)), 1) == 1
+    assert percentile([4.0, 1.0, 3.0, 2.0], 75) == 3.0
+
+
+def test_latency_summary_from_the_logical_clock():
+    """Fixed step costs make every timestamp known: one request arriving at 0 with a 6-token
+    prompt (budget 8: one prefill step of 2.5 ms) and 3 output tokens (two decode steps of
+    1.25 ms); a second request arriving at 100 ms, after the first finished."""
+    requests = [Request(0, tuple(range(1, 7)), 3, 0.0), Request(1, tuple(range(1, 5)), 2, 100.0)]
+    result = run_scheduler(FakeBackend(), requests, token_budget=8, max_running_requests=2)
+    r0, r1 = result.requests
+    assert (r0.queue_ms, r0.ttft_ms, r0.end_to_end_ms) == (0.0, 2.5, 5.0)
+    assert r0.inter_token_latencies_ms == [1.25, 1.25]
+    assert (r1.arrival_ms, r1.ttft_ms, r1.end_to_end_ms) == (100.0, 2.5, 3.75)
+    summary = result.latency_summary()
+    assert summary["ttft_ms_p50"] == 2.5 and summary["end_to_end_ms_p95"] == 5.0
+    assert summary["itl_ms_p50"] == 1.25 and summary["itl_ms_max"] == 1.25
+    assert result.busy_ms == 2.5 + 2 * 1.25 + 2.5 + 1.25
