@@ -14,6 +14,7 @@ import torch
 from mini_infra_qwen3_amd import _native
 
 __all__ = [
+    "KERNEL_BLOCK_SIZE",
     "chunked_prefill_attention",
     "gather_blocks",
     "paged_decode_attention",
@@ -183,7 +184,30 @@ def gather_blocks(
     _native.check(rc, "mi_gather_blocks")
 
 
+KERNEL_BLOCK_SIZE = 16  # token rows per block the attention kernels are specialised for
+
+
+def _as_kernel_blocks(key_pool: torch.Tensor, value_pool: torch.Tensor, tables: torch.Tensor):
+    """A pool of block_size 16 k is the same memory as a pool of 16-token blocks, block i holding
+    sub-blocks k i .. k i + k - 1.  Returns the pools viewed that way and the table of sub-block
+    ids (entry j of a row -> table[j // k] * k + j % k; ids outside the pool stay outside, so they
+    still read the null block).  Other block sizes pass through (the kernels reject them)."""
+    block_size = key_pool.shape[1]
+    if block_size == KERNEL_BLOCK_SIZE or block_size % KERNEL_BLOCK_SIZE != 0:
+        return key_pool, value_pool, tables
+    k = block_size // KERNEL_BLOCK_SIZE
+    n = key_pool.shape[0]
+    kp = key_pool.view(n * k, KERNEL_BLOCK_SIZE, *key_pool.shape[2:])
+    vp = value_pool.view(n * k, KERNEL_BLOCK_SIZE, *value_pool.shape[2:])
+    sub = torch.arange(k, dtype=tables.dtype, device=tables.device)
+    return kp, vp, (tables.unsqueeze(-1) * k + sub).reshape(tables.shape[0], tables.shape[1] * k)
+
+
 def paged_decode_workspace_bytes(batch: int, max_blocks: int, num_heads: int, head_dim: int, block_size: int) -> int:
+    """Workspace for ``paged_decode_attention`` on ``[batch, max_blocks]`` tables of a pool with
+    ``block_size``-token blocks (multiples of 16 count as 16-token sub-blocks)."""
+    if block_size > KERNEL_BLOCK_SIZE and block_size % KERNEL_BLOCK_SIZE == 0:
+        max_blocks, block_size = max_blocks * (block_size // KERNEL_BLOCK_SIZE), KERNEL_BLOCK_SIZE
     return int(_native.load().mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size))
 
 
@@ -199,10 +223,11 @@ def paged_decode_attention(
 ) -> torch.Tensor:
     """Paged GQA decode attention straight from the pool (kernel 3).
 
-    query: ``[B, H, D]`` bf16 (D contiguous); pools ``[num_blocks, 16, H_kv, D]`` bf16 contiguous;
-    block_tables ``[B, max_blocks]`` int64 (null-padded); context_lens ``[B]`` int64 (includes the
-    new token).  Returns ``out`` ``[B, H * D]`` bf16.  ``workspace`` (optional, uint8, reused across
-    calls) holds the split-context partials; it is allocated here when missing or too small.
+    query: ``[B, H, D]`` bf16 (D contiguous); pools ``[num_blocks, block_size, H_kv, D]`` bf16
+    contiguous, block_size 16 or a multiple of it; block_tables ``[B, max_blocks]`` int64
+    (null-padded); context_lens ``[B]`` int64 (includes the new token).  Returns ``out``
+    ``[B, H * D]`` bf16.  ``workspace`` (optional, uint8, reused across calls) holds the
+    split-context partials; it is allocated here when missing or too small.
     """
     device = key_pool.device
     for name, t in (("query", query), ("key_pool", key_pool), ("value_pool", value_pool),
@@ -222,6 +247,8 @@ def paged_decode_attention(
         raise ValueError(f"query head_dim {head_dim} != pool head_dim {pool_head_dim}")
     if block_tables.shape[0] != batch or context_lens.shape[0] != batch:
         raise ValueError("block_tables / context_lens batch differs from query batch")
+    key_pool, value_pool, block_tables = _as_kernel_blocks(key_pool, value_pool, block_tables)
+    num_blocks, block_size = key_pool.shape[:2]
     if block_tables.stride(1) != 1:
         block_tables = block_tables.contiguous()
     max_blocks = block_tables.shape[1]
@@ -268,8 +295,9 @@ def chunked_prefill_attention(
     """Chunked-prefill attention with the history read from the pool (kernel 4, MFMA).
 
     query ``[B, H, L, D]``; key / value ``[B, H_kv, L, D]`` (left-padded chunk, D contiguous, any
-    other strides); pools ``[num_blocks, 16, H_kv, D]``; history_blocks ``[B, nb]`` int64 (may have
-    ``nb = 0``); start_lens / chunk_lens ``[B]`` int64 (views with a common stride are fine).
+    other strides); pools ``[num_blocks, block_size, H_kv, D]``, block_size 16 or a multiple of it;
+    history_blocks ``[B, nb]`` int64 (may have ``nb = 0``); start_lens / chunk_lens ``[B]`` int64
+    (views with a common stride are fine).
     Returns ``out`` ``[B, L, H * D]`` bf16; left-padding rows are zero.
     """
     device = query.device
@@ -292,6 +320,8 @@ def chunked_prefill_attention(
         raise ValueError("pools must be contiguous bf16 with identical shapes")
     if history_blocks.shape[0] != batch or start_lens.shape[0] != batch or chunk_lens.shape[0] != batch:
         raise ValueError("history_blocks / start_lens / chunk_lens batch differs from query batch")
+    key_pool, value_pool, history_blocks = _as_kernel_blocks(key_pool, value_pool, history_blocks)
+    num_blocks, block_size = key_pool.shape[:2]
     if history_blocks.stride(1) != 1:
         history_blocks = history_blocks.contiguous()
     if batch > 1 and start_lens.stride(0) != chunk_lens.stride(0):

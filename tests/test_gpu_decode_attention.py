@@ -198,3 +198,19 @@ def test_one_long_sequence_across_many_ranges(native_lib, device):
     live = [0, 1, 3, 4, 5]
     assert max_abs(got[live], ref[live]) <= TOL
     assert not got[2].float().abs().any()
+
+
+@pytest.mark.parametrize("block_size", [32, 64])
+def test_pool_blocks_of_multiples_of_16_tokens(native_lib, device, block_size):
+    """A pool of 16 k-token blocks runs as 16-token sub-blocks (same memory): results match the
+    oracle gathering whole blocks."""
+    ctx = [1, 31, 32, 33, 100, 700, 64]
+    gen = torch.Generator().manual_seed(block_size)
+    num_blocks = 1 + sum(-(-n // block_size) for n in ctx) + 3
+    tables = workloads.permuted_tables(ctx, num_blocks, gen, block_size=block_size)
+    kp = torch.randn(num_blocks, block_size, 8, 128, generator=gen).to(torch.bfloat16)
+    vp = torch.randn(num_blocks, block_size, 8, 128, generator=gen).to(torch.bfloat16)
+    q = torch.randn(len(ctx), 16, 128, generator=gen).to(torch.bfloat16)
+    bt = workloads.padded(tables)
+    got = run_kernel(q, kp, vp, bt, ctx, device)
+    assert max_abs(got, oracle(q, kp, vp, bt, ctx)) <= TOL

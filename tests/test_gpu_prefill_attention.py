@@ -130,3 +130,26 @@ def test_config_shape_chunk_with_history(native_lib, device):
     case = make_case(99, starts, lens, spare=0)
     got = run_gpu(*case, starts, lens, device)
     check_against_oracle(got, *case, starts, lens)
+
+
+@pytest.mark.parametrize("block_size", [32, 64])
+def test_pool_blocks_of_multiples_of_16_tokens(native_lib, device, block_size):
+    """History in a pool of 16 k-token blocks, read as 16-token sub-blocks."""
+    starts, lens = [40, 200, 0], [57, 100, 30]
+    gen = torch.Generator().manual_seed(block_size)
+    width = max(lens)
+    totals = [s + n for s, n in zip(starts, lens)]
+    num_blocks = 1 + sum(-(-t // block_size) for t in totals) + 2
+    tables = workloads.permuted_tables(totals, num_blocks, gen, block_size=block_size)
+    kp = torch.randn(num_blocks, block_size, 8, 128, generator=gen).to(torch.bfloat16)
+    vp = torch.randn(num_blocks, block_size, 8, 128, generator=gen).to(torch.bfloat16)
+    q = torch.randn(3, 16, width, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(3, 8, width, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(3, 8, width, 128, generator=gen).to(torch.bfloat16)
+    nb = max(-(-s // block_size) for s in starts)
+    hist = torch.zeros((3, nb), dtype=torch.long)
+    for b, s in enumerate(starts):
+        h = -(-s // block_size)
+        hist[b, :h] = torch.tensor(tables[b][:h], dtype=torch.long)
+    got = run_gpu(q, k, v, kp, vp, hist, starts, lens, device)
+    check_against_oracle(got, q, k, v, kp, vp, hist, starts, lens)

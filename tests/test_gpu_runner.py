@@ -48,8 +48,8 @@ def assert_kv_close(layer, got, want):
         assert (got - want).abs().max().item() <= DEEP_ATOL
 
 
-def make_pool(cfg, num_blocks):
-    return PagedKVCachePool(cfg.num_hidden_layers, num_blocks, BS, cfg.num_key_value_heads, cfg.head_dim,
+def make_pool(cfg, num_blocks, block_size=BS):
+    return PagedKVCachePool(cfg.num_hidden_layers, num_blocks, block_size, cfg.num_key_value_heads, cfg.head_dim,
                             torch.bfloat16, "cuda:0")
 
 
@@ -112,17 +112,19 @@ def test_store_prefill_matches_oracle_and_isolates_requests(models):
         assert not pool.kv_pools[0][0][b].any()
 
 
-def test_paged_decode_matches_oracle_tokens_and_logits(models):
+@pytest.mark.parametrize("bs", [BS, 2 * BS], ids=["block16", "block32"])
+def test_paged_decode_matches_oracle_tokens_and_logits(models, bs):
     """Mixed-length requests decoded step by step (test_paged_kv_cache.py:109-163): same greedy
-    tokens as the oracle's reference path on both devices, logits close."""
+    tokens as the oracle's reference path on both devices, logits close.  A 32-token block pool
+    runs the kernels on 16-token sub-blocks."""
     model, ref, ref_cpu = models
     cfg = model.config
     prompts = prompts_of([45, 17, 3], seed=2)
     steps = 6
-    manager = KVCacheManager(BS, num_blocks=64)
-    pool = make_pool(cfg, 64)
-    ref_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128, device="cuda:0")
-    cpu_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128)
+    manager = KVCacheManager(bs, num_blocks=64)
+    pool = make_pool(cfg, 64, bs)
+    ref_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, bs, 8, 128, device="cuda:0")
+    cpu_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, bs, 8, 128)
     runner = PagedRunner(model)
     for i, p in enumerate(prompts):
         manager.allocate_slots(i, len(p))
@@ -130,9 +132,9 @@ def test_paged_decode_matches_oracle_tokens_and_logits(models):
     out = runner.run_prefill_step(prompts)
     runner.store_prefill(pool, out.prefill_cache, tables, [len(p) for p in prompts], [0] * 3)
     first, presents = qwen3_ref.prefill(ref, prompts)
-    qwen3_ref.store_prefill(ref_pools, presents, tables, [len(p) for p in prompts], [0] * 3, BS)
+    qwen3_ref.store_prefill(ref_pools, presents, tables, [len(p) for p in prompts], [0] * 3, bs)
     _, cpu_presents = qwen3_ref.prefill(ref_cpu, prompts)
-    qwen3_ref.store_prefill(cpu_pools, cpu_presents, tables, [len(p) for p in prompts], [0] * 3, BS)
+    qwen3_ref.store_prefill(cpu_pools, cpu_presents, tables, [len(p) for p in prompts], [0] * 3, bs)
     assert out.next_tokens == first
     tokens = [[t] for t in first]
     lengths = [len(p) for p in prompts]
@@ -141,12 +143,12 @@ def test_paged_decode_matches_oracle_tokens_and_logits(models):
             for i in range(3):
                 assert manager.allocate_slots(i, 1)
             tables = [manager.block_table(i) for i in range(3)]
-            ids, pos, meta = runner.prepare_decode_inputs(tables, [t[-1] for t in tokens], lengths, BS)
+            ids, pos, meta = runner.prepare_decode_inputs(tables, [t[-1] for t in tokens], lengths, bs)
             logits = model(ids, position_ids=pos, attn_metadata=meta._replace(kv_pools=tuple(pool.kv_pools)),
                            last_logits_only=True)[0][:, -1].float()
             got = runner.run_decode_step(ids, pos, meta, pool)  # rewrites the same rows: same inputs
-            want = qwen3_ref.decode_step(ref, tables, [t[-1] for t in tokens], lengths, ref_pools, BS).float()
-            want_cpu = qwen3_ref.decode_step(ref_cpu, tables, [t[-1] for t in tokens], lengths, cpu_pools, BS)
+            want = qwen3_ref.decode_step(ref, tables, [t[-1] for t in tokens], lengths, ref_pools, bs).float()
+            want_cpu = qwen3_ref.decode_step(ref_cpu, tables, [t[-1] for t in tokens], lengths, cpu_pools, bs)
             assert got.next_tokens == logits.argmax(-1).tolist() == want.argmax(-1).tolist()
             assert got.next_tokens == want_cpu.argmax(-1).tolist()
             assert (logits - want).abs().max().item() <= LOGIT_RTOL * want.abs().max().item()
