@@ -125,3 +125,4 @@ def test_prefill_rejects_unsupported_shapes_on_host(native_lib):
     assert call(tok=1 << 24) == _native.MI_ERR_UNSUPPORTED  # key / value token stride >= 2^24 elements
     assert call(hstride=1) == _native.MI_ERR_INVALID_ARGUMENT
     assert call(hist=None) == _native.MI_ERR_INVALID_ARGUMENT
+    assert call(nb=16385, hstride=16385) == _native.MI_ERR_UNSUPPORTED  # history table beyond 64 KiB of LDS

@@ -214,3 +214,12 @@ def test_pool_blocks_of_multiples_of_16_tokens(native_lib, device, block_size):
     bt = workloads.padded(tables)
     got = run_kernel(q, kp, vp, bt, ctx, device)
     assert max_abs(got, oracle(q, kp, vp, bt, ctx)) <= TOL
+
+
+def test_context_of_forty_thousand_tokens(native_lib, device):
+    """A 40k-token context (2500 blocks, beyond the per-sequence kernel's table) next to short
+    ones, in every decode kernel."""
+    ctx = [40000, 17, 1500]
+    q, kp, vp, bt, _ = random_case(91, ctx, spare=2)
+    got = run_kernel(q, kp, vp, bt, ctx, device)
+    assert max_abs(got, oracle(q, kp, vp, bt, ctx)) <= TOL

@@ -153,3 +153,12 @@ def test_pool_blocks_of_multiples_of_16_tokens(native_lib, device, block_size):
         hist[b, :h] = torch.tensor(tables[b][:h], dtype=torch.long)
     got = run_gpu(q, k, v, kp, vp, hist, starts, lens, device)
     check_against_oracle(got, q, k, v, kp, vp, hist, starts, lens)
+
+
+def test_history_of_a_hundred_thousand_tokens(native_lib, device):
+    """A 40-token chunk over 100k tokens of history (6250 pool blocks staged in LDS) and a
+    short row beside it."""
+    starts, lens = [100000, 30], [40, 7]
+    q, k, v, kp, vp, hist = make_case(5, starts, lens, spare=2)
+    got = run_gpu(q, k, v, kp, vp, hist, starts, lens, device)
+    check_against_oracle(got, q, k, v, kp, vp, hist, starts, lens)
