@@ -224,6 +224,16 @@ int32_t mi_qk_norm_rope(void* q_out, void* k_out, void* v_out, const void* q, in
 int32_t mi_silu_mul(void* out, int64_t out_stride, const void* gate, int64_t gate_stride, const void* up,
                     int64_t up_stride, int64_t rows, int32_t cols, void* stream);
 
+/*
+ * mi_argmax_rows -- greedy sampling, the torch.argmax of greedy_sample
+ * (src/mini_infra/worker/sampler.py:9-23): out[r] = index of the largest of logits[r, 0:cols].
+ * logits: bf16 rows with element stride row_stride >= cols; out: int64 [rows].
+ * Ties go to the smallest index, -0 equals +0, a NaN is larger than every number (the first NaN
+ * wins), as torch.argmax.  One workgroup per row; no workspace.
+ */
+int32_t mi_argmax_rows(int64_t* out, const void* logits, int64_t rows, int32_t cols, int64_t row_stride,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

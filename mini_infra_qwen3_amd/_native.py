@@ -59,6 +59,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          ctypes.c_float, _ptr, _i64, _ptr, _ptr, _i64, _ptr],
     ),
     "mi_silu_mul": (_i32, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i32, _ptr]),
+    "mi_argmax_rows": (_i32, [_ptr, _ptr, _i64, _i32, _i64, _ptr]),
 }
 
 

@@ -15,6 +15,7 @@ from mini_infra_qwen3_amd import _native
 
 __all__ = [
     "KERNEL_BLOCK_SIZE",
+    "argmax_rows",
     "chunked_prefill_attention",
     "gather_blocks",
     "paged_decode_attention",
@@ -457,4 +458,24 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     rc = _native.load().mi_silu_mul(out.data_ptr(), cols, g2.data_ptr(), g2.stride(0), u2.data_ptr(), u2.stride(0),
                                     rows, cols, _stream(device))
     _native.check(rc, "mi_silu_mul")
+    return out
+
+
+def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
+    """Greedy token of each row of bf16 ``logits [rows, vocab]`` (any row stride): int64 ``[rows]``.
+
+    Same answer as ``torch.argmax(logits, dim=-1)`` -- first index on ties, NaN above every number --
+    in one launch (the sampler of reference src/mini_infra/worker/sampler.py:9-23).
+    """
+    device = logits.device
+    _require_bf16_rows("logits", logits, device)
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [rows, vocab], got {tuple(logits.shape)}")
+    rows, cols = logits.shape
+    out = torch.empty(rows, dtype=torch.int64, device=device)
+    if rows == 0:
+        return out
+    row_stride = logits.stride(0) if rows > 1 else cols
+    rc = _native.load().mi_argmax_rows(out.data_ptr(), logits.data_ptr(), rows, cols, row_stride, _stream(device))
+    _native.check(rc, "mi_argmax_rows")
     return out

@@ -24,6 +24,7 @@ from typing import NamedTuple
 import numpy as np
 import torch
 
+from mini_infra_qwen3_amd.data_plane import argmax_rows
 from mini_infra_qwen3_amd.device import StepTimer
 from mini_infra_qwen3_amd.model.qwen3 import PagedAttentionMetadata, PagedPrefillMetadata
 from mini_infra_qwen3_amd.worker.base_runner import BaseModelRunner, PrefillOutput
@@ -199,7 +200,7 @@ class PagedRunner(BaseModelRunner):
             graph, rows = loaded
             with StepTimer(self.device) as timer:
                 graph.graph.replay()
-                next_token = torch.argmax(graph.logits[:rows], dim=-1)
+                next_token = argmax_rows(graph.logits[:rows])
             return PagedDecodeOutput(next_token.tolist(), timer.elapsed_ms)
         with StepTimer(self.device) as timer:
             logits, _ = self.model(input_ids, position_ids=position_ids,

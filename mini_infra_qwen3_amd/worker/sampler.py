@@ -4,11 +4,16 @@ from __future__ import annotations
 
 import torch
 
+from mini_infra_qwen3_amd.data_plane import argmax_rows
+
 
 def greedy_sample(logits: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """logits ``[B, L, V]`` -> (next_token ``[B, 1]`` int64, last_logits ``[B, V]``)."""
+    """bf16 logits ``[B, L, V]`` on the GPU -> (next_token ``[B, 1]`` int64, last_logits ``[B, V]``).
+
+    The argmax is the HIP kernel behind ``argmax_rows`` (torch.argmax's answer: first index on ties).
+    """
     last_logits = logits[:, -1, :]
-    return torch.argmax(last_logits, dim=-1, keepdim=True), last_logits
+    return argmax_rows(last_logits).unsqueeze(-1), last_logits
 
 
 __all__ = ["greedy_sample"]

@@ -126,3 +126,13 @@ def test_prefill_rejects_unsupported_shapes_on_host(native_lib):
     assert call(hstride=1) == _native.MI_ERR_INVALID_ARGUMENT
     assert call(hist=None) == _native.MI_ERR_INVALID_ARGUMENT
     assert call(nb=16385, hstride=16385) == _native.MI_ERR_UNSUPPORTED  # history table beyond 64 KiB of LDS
+
+
+def test_argmax_rejects_bad_arguments_on_host(native_lib):
+    lib = native_lib
+    assert lib.mi_argmax_rows(16, 16, 4, 0, 16, None) == _native.MI_ERR_INVALID_ARGUMENT
+    assert lib.mi_argmax_rows(16, 16, -1, 8, 8, None) == _native.MI_ERR_INVALID_ARGUMENT
+    assert lib.mi_argmax_rows(16, 16, 2, 100, 99, None) == _native.MI_ERR_INVALID_ARGUMENT
+    assert lib.mi_argmax_rows(None, 16, 2, 8, 8, None) == _native.MI_ERR_INVALID_ARGUMENT
+    assert lib.mi_argmax_rows(None, None, 0, 8, 8, None) == _native.MI_OK
+    assert lib.mi_argmax_rows(16, 16, 1 << 31, 8, 8, None) == _native.MI_ERR_UNSUPPORTED
