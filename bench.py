@@ -8,8 +8,9 @@ algorithmic HBM bandwidth of the whole step: per layer sum(context) x 4096 B of 
 plus Q read, O written and the appended K/V rows, divided by the timed step time.
 
 Also measured in the same run (reported under ``kernels``): the 28-layer prefill scatter of
-32 prompts U[128, 2048] with churned block tables, the block-table history gather and the MFMA
-chunked-prefill attention of 4 x 16384-token prompts in 2048-token chunks; and (under ``e2e``)
+32 prompts U[128, 2048] with churned block tables, the block-table history gather, the MFMA
+chunked-prefill attention of 4 x 16384-token prompts in 2048-token chunks, and the KV block
+records of 2048 blocks (pack / unpack in HBM, swap to pinned host memory and back); and (under ``e2e``)
 the continuous-batching run of a random-init Qwen3-0.6B: 128 requests at 20 req/s, prompts
 U[32, 1024], 128 output tokens, chunked prefill with a 2048-token budget.  The CPU baseline times the reference's torch
 decode chain (the oracle) on the host cores on a bounded sample of the same workload.
@@ -30,6 +31,7 @@ import torch
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor datasheet
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
+PCIE_PEAK_GBS = 64.0  # MI355X host link, PCIe 5.0 x16, one direction
 METRIC = "paged decode-attn HBM GB/s (% peak) at B=256; e2e output tok/s Qwen3-0.6B"
 
 
@@ -292,6 +294,61 @@ def bench_copy(steps: int, device: torch.device, nbytes: int = 1 << 30) -> dict:
             "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS}
 
 
+# ------------------------------------------------------------------------ KV block swap
+def bench_swap(steps: int, warmup: int, device: torch.device, num_records: int = 2048) -> dict:
+    """KV block records of the Qwen3-0.6B pool (28 layers, 1.75 MiB per block): pack 2048 randomly
+    placed blocks into records and unpack them into other blocks (HBM: each moves 2 x 3.76 GB per
+    launch), and the whole swap to pinned host memory and back (pack + DMA, DMA + unpack: PCIe)."""
+    from mini_infra_qwen3_amd import workloads as wl
+    from mini_infra_qwen3_amd.worker import HostSwapPool, PagedKVCachePool
+
+    pool = PagedKVCachePool(wl.NUM_LAYERS, 2 * num_records + 1, wl.BLOCK_SIZE, wl.NUM_KV_HEADS, wl.HEAD_DIM,
+                            torch.bfloat16, device)
+    pool.storage.view(torch.int16).random_(generator=torch.Generator(device=device).manual_seed(0))
+    perm = (torch.randperm(2 * num_records, generator=torch.Generator().manual_seed(1)) + 1).tolist()
+    src, dst = perm[:num_records], perm[num_records:]
+    src_t = torch.tensor(src, dtype=torch.long, device=device)
+    dst_t = torch.tensor(dst, dtype=torch.long, device=device)
+    record_bytes = pool.bytes_per_block
+    records = pool.pack_blocks(src_t)
+    res = {"workload": f"{num_records} blocks of a 28-layer Qwen3-0.6B pool ({record_bytes} B per block record), "
+                       "random block ids"}
+    for name, fn in (("pack", lambda: pool.pack_blocks(src_t)), ("unpack", lambda: pool.unpack_blocks(records, dst_t))):
+        timer = EventTimer()
+        for _ in range(warmup):
+            fn()
+        for _ in range(steps):
+            timer.start()
+            fn()
+            timer.stop()
+        ms = timer.mean_ms()
+        gbs = 2 * num_records * record_bytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms_per_launch": ms, "bytes_per_launch": 2 * num_records * record_bytes, "achieved_GBps": gbs,
+                     "frac": gbs / HBM_PEAK_GBS}
+    del records
+    swap = HostSwapPool(num_records, pool)
+    for name in ("swap_out", "swap_in"):
+        timer = EventTimer()
+        for i in range(warmup + max(steps // 4, 2)):
+            if i >= warmup:
+                timer.start()
+            if name == "swap_out":
+                slots = swap.swap_out(pool, src)
+            else:
+                slots = swap.allocate(num_records)
+                swap.swap_in(pool, slots, dst)
+            if i >= warmup:
+                timer.stop()
+            if name == "swap_out":
+                swap.free(slots)
+        ms = timer.mean_ms()
+        gbs = num_records * record_bytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": ms, "bytes": num_records * record_bytes, "achieved_GBps": gbs,
+                     "frac_of_pcie": gbs / PCIE_PEAK_GBS}
+    del swap, pool
+    return res
+
+
 # ------------------------------------------------------------------------- chunked prefill
 def bench_prefill(steps: int, warmup: int, device: torch.device) -> dict:
     """4 prompts x 16384 tokens, 2048-token chunks, one layer: 8 chunk steps, each one launch over the
@@ -397,7 +454,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["decode", "scatter", "gather", "prefill", "copy", "e2e", "all"],
+    parser.add_argument("--only", choices=["decode", "scatter", "gather", "prefill", "copy", "swap", "e2e", "all"],
                         default="all")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -418,6 +475,7 @@ def main() -> int:
         "scatter": lambda: bench_scatter(args.steps, args.warmup, device),
         "gather": lambda: bench_gather(args.steps, args.warmup, device),
         "prefill": lambda: bench_prefill(args.steps, args.warmup, device),
+        "swap": lambda: bench_swap(args.steps, args.warmup, device),
     }
     if args.only in single:  # one kernel alone (for counter runs)
         res = single[args.only]()
@@ -457,6 +515,13 @@ def main() -> int:
         torch.cuda.empty_cache()
         kernels["device_copy"] = bench_copy(5, device)
         log(f"device copy: {kernels['device_copy']['achieved_GBps']:.1f} GB/s")
+        torch.cuda.empty_cache()
+        kernels["kv_block_swap"] = bench_swap(max(args.steps // 4, 3), 1, device)
+        sw = kernels["kv_block_swap"]
+        log(f"kv block records: pack {sw['pack']['achieved_GBps']:.1f} GB/s, unpack "
+            f"{sw['unpack']['achieved_GBps']:.1f} GB/s; swap out {sw['swap_out']['achieved_GBps']:.1f} GB/s, "
+            f"swap in {sw['swap_in']['achieved_GBps']:.1f} GB/s")
+        torch.cuda.empty_cache()
     e2e = None
     if args.only == "all":
         e2e = bench_e2e(device)

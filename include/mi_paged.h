@@ -234,6 +234,29 @@ int32_t mi_silu_mul(void* out, int64_t out_stride, const void* gate, int64_t gat
 int32_t mi_argmax_rows(int64_t* out, const void* logits, int64_t rows, int32_t cols, int64_t row_stride,
                        void* stream);
 
+/*
+ * KV block records -- the wire / swap format of whole physical blocks, for the "swap" preemption
+ * mode the reference plans (src/mini_infra/core/types.py:110-114, core/scheduler.py:312-313:
+ * a victim's physical KV blocks go to a CPU host swap pool over PCIe and come back on resume).
+ * One record is one block of every layer, contiguous:
+ *   record[layer][0 = K, 1 = V][block_size * H * D elements]   record_bytes = 2 * num_layers * block_bytes
+ * where block_bytes is one layer's K (or V) block, as laid out in the pool of
+ * src/mini_infra/worker/paged_kv_cache.py:23-52.  Records of one call are contiguous.
+ *
+ * mi_pack_blocks:   records[i] = block block_ids[i] of every layer (ids out of [0, num_blocks)
+ *                   give a zero record).
+ * mi_unpack_blocks: block block_ids[i] of every layer = records[i] (out-of-range ids skipped;
+ *                   ids must be unique).
+ * key_pools / value_pools: num_layers device pointers, each num_blocks * block_bytes.
+ * block_ids: device int64 [num_records].  Bit-exact copies; no workspace.
+ */
+int32_t mi_pack_blocks(void* records, const void* const* key_pools, const void* const* value_pools,
+                       int64_t num_blocks, const int64_t* block_ids, int64_t num_records, int32_t num_layers,
+                       int64_t block_bytes, void* stream);
+int32_t mi_unpack_blocks(void* const* key_pools, void* const* value_pools, int64_t num_blocks,
+                         const void* records, const int64_t* block_ids, int64_t num_records, int32_t num_layers,
+                         int64_t block_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "mi_silu_mul": (_i32, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _i64, _i32, _ptr]),
     "mi_argmax_rows": (_i32, [_ptr, _ptr, _i64, _i32, _i64, _ptr]),
+    "mi_pack_blocks": (_i32, [_ptr, _c_void_p_p, _c_void_p_p, _i64, _ptr, _i64, _i32, _i64, _ptr]),
+    "mi_unpack_blocks": (_i32, [_c_void_p_p, _c_void_p_p, _i64, _ptr, _ptr, _i64, _i32, _i64, _ptr]),
 }
 
 

@@ -1,0 +1,131 @@
+// KV block records: the wire / swap format of whole physical blocks.
+//
+// The reference plans a "swap" preemption mode that moves a victim's physical KV blocks to a CPU
+// host swap pool over PCIe and back on resume (src/mini_infra/core/types.py:110-114,
+// src/mini_infra/core/scheduler.py:312-313); its pool keeps each layer's K and V as
+// [num_blocks, block_size, H, D] (src/mini_infra/worker/paged_kv_cache.py:23-52), so one block's
+// data is 2 x num_layers pieces scattered over the pool.
+//
+// A record is one physical block, every layer, contiguous:
+//   record[layer][0 = K, 1 = V][block_size][H][D]      (record_bytes = 2 * num_layers * block_bytes)
+// n records are n * record_bytes contiguous bytes, so a swap is one DMA copy and a file is a
+// header plus the records.  mi_pack_blocks gathers blocks into records and mi_unpack_blocks
+// scatters records into (other) blocks; both are bit-exact copies.
+//
+// grid: x = record, y = layer of this launch, z = K / V.  Each workgroup moves one block_bytes
+// piece (32 KiB for 16 x 8 x 128 bf16) with 16-byte loads, all issued before the stores.
+#include "mi_common.h"
+
+namespace mi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;
+
+struct RecordArgs {
+  char* pool[2][kMaxLayersPerLaunch];  // [0] = key pools, [1] = value pools of this launch's layers
+  char* records;
+  const int64_t* block_ids;
+  int64_t num_blocks;
+  int64_t block_bytes;
+  int64_t record_bytes;
+  int32_t layer0;   // first layer of this launch
+  uint32_t pieces;  // block_bytes / sizeof(V)
+};
+
+// kPack: block -> record (an out-of-range block id writes a zero piece: nothing is read).
+// !kPack: record -> block (an out-of-range block id is skipped).
+template <typename V, bool kPack>
+__global__ __launch_bounds__(kThreads) void kv_records_kernel(const RecordArgs a) {
+  const int64_t i = blockIdx.x;
+  const int layer = blockIdx.y;
+  const int kv = blockIdx.z;
+  const int64_t bid = a.block_ids[i];
+  const bool valid = bid >= 0 && bid < a.num_blocks;
+  if (!kPack && !valid) return;
+  V* block = reinterpret_cast<V*>(a.pool[kv][layer] + (valid ? bid : 0) * a.block_bytes);
+  V* rec = reinterpret_cast<V*>(a.records + i * a.record_bytes + (2 * (a.layer0 + layer) + kv) * a.block_bytes);
+  const V* src = kPack ? block : rec;
+  V* dst = kPack ? rec : block;
+  for (uint32_t base = 0; base < a.pieces; base += kThreads * kUnroll) {
+    V val[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      const uint32_t p = base + k * kThreads + threadIdx.x;
+      if (p < a.pieces) val[k] = (!kPack || valid) ? load_vec<true>(src + p) : V{};
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      const uint32_t p = base + k * kThreads + threadIdx.x;
+      if (p < a.pieces) store_vec<true>(dst + p, val[k]);
+    }
+  }
+}
+
+template <bool kPack>
+int32_t launch_records(const char* what, void* records, const void* const* key_pools,
+                       const void* const* value_pools, int64_t num_blocks, const int64_t* block_ids,
+                       int64_t num_records, int32_t num_layers, int64_t block_bytes, void* stream) {
+  if (num_records < 0 || num_layers < 0 || num_blocks < 0 || block_bytes < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
+  if (num_records == 0 || num_layers == 0 || block_bytes == 0) return ok();
+  if (!records || !key_pools || !value_pools || !block_ids)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
+  if (num_records > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "%s: too many records in one call", what);
+  const int64_t record_bytes = 2 * static_cast<int64_t>(num_layers) * block_bytes;
+
+  bool wide = block_bytes % 16 == 0 && aligned16(records);
+  for (int l = 0; l < num_layers && wide; ++l) wide = aligned16(key_pools[l]) && aligned16(value_pools[l]);
+  const int64_t piece = wide ? 16 : (block_bytes % 4 == 0 ? 4 : 2);
+  if (block_bytes % piece != 0 || block_bytes / piece > 0x7fffffff)
+    return fail(MI_ERR_UNSUPPORTED, "%s: block of %lld bytes not supported", what,
+                static_cast<long long>(block_bytes));
+
+  RecordArgs a{};
+  a.records = static_cast<char*>(records);
+  a.block_ids = block_ids;
+  a.num_blocks = num_blocks;
+  a.block_bytes = block_bytes;
+  a.record_bytes = record_bytes;
+  a.pieces = static_cast<uint32_t>(block_bytes / piece);
+  hipStream_t s = as_stream(stream);
+  for (int l0 = 0; l0 < num_layers; l0 += kMaxLayersPerLaunch) {
+    const int nl = num_layers - l0 < kMaxLayersPerLaunch ? num_layers - l0 : kMaxLayersPerLaunch;
+    for (int l = 0; l < nl; ++l) {
+      if (!key_pools[l0 + l] || !value_pools[l0 + l])
+        return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer for layer %d", what, l0 + l);
+      a.pool[0][l] = const_cast<char*>(static_cast<const char*>(key_pools[l0 + l]));
+      a.pool[1][l] = const_cast<char*>(static_cast<const char*>(value_pools[l0 + l]));
+    }
+    a.layer0 = l0;
+    const dim3 grid(static_cast<uint32_t>(num_records), nl, 2);
+    if (piece == 16)
+      kv_records_kernel<u32x4, kPack><<<grid, kThreads, 0, s>>>(a);
+    else if (piece == 4)
+      kv_records_kernel<uint32_t, kPack><<<grid, kThreads, 0, s>>>(a);
+    else
+      kv_records_kernel<uint16_t, kPack><<<grid, kThreads, 0, s>>>(a);
+    const int32_t rc = check_launch(what);
+    if (rc != MI_OK) return rc;
+  }
+  return ok();
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int32_t mi_pack_blocks(void* records, const void* const* key_pools, const void* const* value_pools,
+                                  int64_t num_blocks, const int64_t* block_ids, int64_t num_records,
+                                  int32_t num_layers, int64_t block_bytes, void* stream) {
+  return mi::launch_records<true>("mi_pack_blocks", records, key_pools, value_pools, num_blocks, block_ids,
+                                  num_records, num_layers, block_bytes, stream);
+}
+
+extern "C" int32_t mi_unpack_blocks(void* const* key_pools, void* const* value_pools, int64_t num_blocks,
+                                    const void* records, const int64_t* block_ids, int64_t num_records,
+                                    int32_t num_layers, int64_t block_bytes, void* stream) {
+  return mi::launch_records<false>("mi_unpack_blocks", const_cast<void*>(records),
+                                   const_cast<const void* const*>(key_pools),
+                                   const_cast<const void* const*>(value_pools), num_blocks, block_ids, num_records,
+                                   num_layers, block_bytes, stream);
+}

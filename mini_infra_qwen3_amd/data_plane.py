@@ -18,12 +18,14 @@ __all__ = [
     "argmax_rows",
     "chunked_prefill_attention",
     "gather_blocks",
+    "pack_blocks",
     "paged_decode_attention",
     "paged_decode_workspace_bytes",
     "qk_norm_rope",
     "reshape_and_cache",
     "rms_norm",
     "silu_mul",
+    "unpack_blocks",
 ]
 
 
@@ -479,3 +481,70 @@ def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     rc = _native.load().mi_argmax_rows(out.data_ptr(), logits.data_ptr(), rows, cols, row_stride, _stream(device))
     _native.check(rc, "mi_argmax_rows")
     return out
+
+
+def _record_pools(key_pools: Sequence[torch.Tensor], value_pools: Sequence[torch.Tensor]):
+    """Validates per-layer pools ``[num_blocks, bs, H, D]`` (one shape and dtype, contiguous)."""
+    if len(key_pools) != len(value_pools) or not key_pools:
+        raise ValueError("key_pools and value_pools must be equal-length, non-empty per-layer lists")
+    pool0 = key_pools[0]
+    device = pool0.device
+    for name, tensors in (("key_pools", key_pools), ("value_pools", value_pools)):
+        for t in tensors:
+            _require_gpu(name, t, device)
+            if t.shape != pool0.shape or t.dtype != pool0.dtype or not t.is_contiguous() or t.dim() != 4:
+                raise ValueError(f"{name}: expected contiguous {tuple(pool0.shape)} {pool0.dtype}, got "
+                                 f"{tuple(t.shape)} {t.dtype}")
+    block_bytes = pool0[0].numel() * pool0.element_size()
+    return pool0, device, block_bytes
+
+
+def pack_blocks(key_pools: Sequence[torch.Tensor], value_pools: Sequence[torch.Tensor], block_ids: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Packs whole physical blocks of every layer into contiguous records (one launch).
+
+    Returns ``records [n, num_layers, 2, bs, H, D]`` with ``records[i, l, 0] = key_pools[l][block_ids[i]]``
+    and ``records[i, l, 1] = value_pools[l][block_ids[i]]``: the wire / swap format.  block_ids:
+    ``[n]`` int64 on the pools' device; ids outside ``[0, num_blocks)`` give zero records.
+    """
+    pool0, device, block_bytes = _record_pools(key_pools, value_pools)
+    _require_gpu("block_ids", block_ids, device)
+    _require_index("block_ids", block_ids, 1)
+    block_ids = block_ids.contiguous()
+    shape = (block_ids.shape[0], len(key_pools), 2, *pool0.shape[1:])
+    if out is None:
+        out = torch.empty(shape, dtype=pool0.dtype, device=device)
+    else:
+        _require_gpu("out", out, device)
+        if tuple(out.shape) != shape or out.dtype != pool0.dtype or not out.is_contiguous():
+            raise ValueError(f"out: expected contiguous {shape} {pool0.dtype}, got {tuple(out.shape)} {out.dtype}")
+    if block_ids.shape[0] == 0:
+        return out
+    rc = _native.load().mi_pack_blocks(
+        out.data_ptr(), _native.pointer_array([t.data_ptr() for t in key_pools]),
+        _native.pointer_array([t.data_ptr() for t in value_pools]), pool0.shape[0], block_ids.data_ptr(),
+        block_ids.shape[0], len(key_pools), block_bytes, _stream(device))
+    _native.check(rc, "mi_pack_blocks")
+    return out
+
+
+def unpack_blocks(records: torch.Tensor, key_pools: Sequence[torch.Tensor], value_pools: Sequence[torch.Tensor],
+                  block_ids: torch.Tensor) -> None:
+    """Writes records (the layout ``pack_blocks`` returns) into physical blocks ``block_ids`` of every
+    layer (one launch).  block_ids: ``[n]`` int64, unique; ids outside ``[0, num_blocks)`` are skipped."""
+    pool0, device, block_bytes = _record_pools(key_pools, value_pools)
+    _require_gpu("records", records, device)
+    _require_gpu("block_ids", block_ids, device)
+    _require_index("block_ids", block_ids, 1)
+    block_ids = block_ids.contiguous()
+    shape = (block_ids.shape[0], len(key_pools), 2, *pool0.shape[1:])
+    if tuple(records.shape) != shape or records.dtype != pool0.dtype or not records.is_contiguous():
+        raise ValueError(f"records: expected contiguous {shape} {pool0.dtype}, got {tuple(records.shape)} "
+                         f"{records.dtype}")
+    if block_ids.shape[0] == 0:
+        return
+    rc = _native.load().mi_unpack_blocks(
+        _native.pointer_array([t.data_ptr() for t in key_pools]),
+        _native.pointer_array([t.data_ptr() for t in value_pools]), pool0.shape[0], records.data_ptr(),
+        block_ids.data_ptr(), block_ids.shape[0], len(key_pools), block_bytes, _stream(device))
+    _native.check(rc, "mi_unpack_blocks")

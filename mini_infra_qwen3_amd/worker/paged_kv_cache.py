@@ -89,6 +89,27 @@ class PagedKVCachePool:
         )
         return tuple((k.transpose(1, 2), v.transpose(1, 2)) for k, v in zip(keys, values))
 
+    def _block_id_tensor(self, block_ids, unique: bool) -> torch.Tensor:
+        if isinstance(block_ids, torch.Tensor):
+            return block_ids.to(device=self.device, dtype=torch.long).reshape(-1)
+        ids = [int(b) for b in block_ids]
+        if any(not 0 <= b < self.num_blocks for b in ids):
+            raise ValueError(f"block ids must lie in [0, {self.num_blocks})")
+        if unique and len(set(ids)) != len(ids):
+            raise ValueError("block ids written by one call must be unique")
+        return torch.tensor(ids, dtype=torch.long).to(self.device, non_blocking=True)
+
+    def pack_blocks(self, block_ids) -> torch.Tensor:
+        """Blocks ``block_ids`` of every layer as contiguous KV block records
+        ``[n, num_layers, 2, bs, H, D]`` (the swap / wire format), one kernel launch."""
+        return data_plane.pack_blocks([k for k, _ in self.kv_pools], [v for _, v in self.kv_pools],
+                                      self._block_id_tensor(block_ids, unique=False))
+
+    def unpack_blocks(self, records: torch.Tensor, block_ids) -> None:
+        """Writes KV block records into blocks ``block_ids`` (unique) of every layer, one kernel launch."""
+        data_plane.unpack_blocks(records, [k for k, _ in self.kv_pools], [v for _, v in self.kv_pools],
+                                 self._block_id_tensor(block_ids, unique=True))
+
     def write_prefill(
         self,
         prefill_cache: KVCache,

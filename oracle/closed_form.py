@@ -40,6 +40,44 @@ def gather_rows(pool_bits: np.ndarray, block_ids: np.ndarray) -> np.ndarray:
     return out
 
 
+def pack_records(key_bits, value_bits, block_ids) -> np.ndarray:
+    """Closed form of the KV block record format (the swap / wire format of whole physical blocks
+    for the "swap" preemption mode the reference plans, src/mini_infra/core/types.py:110-114,
+    over the pool layout of src/mini_infra/worker/paged_kv_cache.py:23-52).
+
+    key_bits / value_bits: per-layer ``[num_blocks, bs, H, D]`` arrays.  Record i is block
+    ``block_ids[i]`` of every layer: ``rec[i, l, 0] = key[l][id]``, ``rec[i, l, 1] = value[l][id]``;
+    an id outside ``[0, num_blocks)`` gives a zero record.  Explicit loops, one block at a time.
+    """
+    layers = len(key_bits)
+    nb = key_bits[0].shape[0]
+    out = np.zeros((len(block_ids), layers, 2, *key_bits[0].shape[1:]), dtype=key_bits[0].dtype)
+    for i, bid in enumerate(block_ids):
+        bid = int(bid)
+        if not 0 <= bid < nb:
+            continue
+        for layer in range(layers):
+            out[i, layer, 0] = key_bits[layer][bid]
+            out[i, layer, 1] = value_bits[layer][bid]
+    return out
+
+
+def unpack_records(key_bits, value_bits, records: np.ndarray, block_ids):
+    """Inverse of ``pack_records``: new per-layer pools with block ``block_ids[i]`` of every layer
+    set from record i (ids outside ``[0, num_blocks)`` skipped), every other block unchanged."""
+    keys = [k.copy() for k in key_bits]
+    values = [v.copy() for v in value_bits]
+    nb = keys[0].shape[0]
+    for i, bid in enumerate(block_ids):
+        bid = int(bid)
+        if not 0 <= bid < nb:
+            continue
+        for layer in range(len(keys)):
+            keys[layer][bid] = records[i, layer, 0]
+            values[layer][bid] = records[i, layer, 1]
+    return keys, values
+
+
 def slot_of(table, position: int, block_size: int) -> int:
     """Physical slot of a logical position (src/mini_infra/worker/paged_kv_cache.py:19)."""
     return int(table[position // block_size]) * block_size + position % block_size
