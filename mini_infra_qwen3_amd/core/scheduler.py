@@ -12,6 +12,12 @@ src/mini_infra/core/request.py:52-110):
   prefills) share the token budget: each gets ``token_budget // n`` prompt tokens at most;
 * with nothing to prefill, decode every request whose prompt is fully cached; else idle.
 
+``mixed=True`` is the mixed chunk + decode batching the reference lists as its next step
+(src/mini_infra/core/scheduler.py:310-311, src/mini_infra/core/types.py:108): every step decodes
+all requests whose prompt is cached and spends what is left of the token budget (one token per
+decoding request) on prefill chunks, split as above, in one MIXED step; a step with only one kind
+of work is a plain DECODE or PREFILL step.  There is no decode protection: decoding never waits.
+
 Pure CPU logic: no tensors, no device.
 """
 
@@ -36,6 +42,7 @@ class RequestStatus(str, Enum):
 class SchedulePhase(str, Enum):
     PREFILL = "prefill"
     DECODE = "decode"
+    MIXED = "mixed"
 
 
 @dataclass
@@ -115,12 +122,18 @@ class PrefillChunk:
 @dataclass(frozen=True)
 class SchedulerOutput:
     """One step's plan.  ``num_scheduled_tokens``: padded chunk tokens (rows x longest chunk) for
-    PREFILL, the number of rows for DECODE (reference scheduler.py:249-264)."""
+    PREFILL, the number of rows for DECODE (reference scheduler.py:249-264), their sum for MIXED.
+    ``scheduled_requests`` lists a MIXED step's decoding requests first, then its chunks' requests."""
 
     phase: SchedulePhase
     scheduled_requests: tuple[RequestState, ...]
     num_scheduled_tokens: int
     prefill_chunks: tuple[PrefillChunk, ...] = ()
+
+    @property
+    def decode_requests(self) -> tuple[RequestState, ...]:
+        """The requests that decode one token in this step (all of them for DECODE, none for PREFILL)."""
+        return self.scheduled_requests[:len(self.scheduled_requests) - len(self.prefill_chunks)]
 
 
 class IterationScheduler:
@@ -130,13 +143,15 @@ class IterationScheduler:
     batch slots; ``kv_cache_manager``: the block allocator this scheduler allocates and frees with.
     """
 
-    def __init__(self, token_budget: int, max_running_requests: int, kv_cache_manager: KVCacheManager):
+    def __init__(self, token_budget: int, max_running_requests: int, kv_cache_manager: KVCacheManager,
+                 mixed: bool = False):
         if max_running_requests < 1:
             raise ValueError("max_running_requests must be positive")
         if token_budget < max_running_requests:
             raise ValueError("token_budget must be at least max_running_requests (every running prefill "
                              "advances by at least one token per step)")
         self.token_budget = token_budget
+        self.mixed = mixed
         self.max_running_requests = max_running_requests
         self.kv_cache_manager = kv_cache_manager
         self.waiting: deque[RequestState] = deque()
@@ -173,19 +188,27 @@ class IterationScheduler:
                                                     self._reserved_blocks())
         return candidates[:fits]
 
-    def _plan_chunks(self) -> tuple[PrefillChunk, ...]:
+    def _plan_chunks(self, budget: int) -> tuple[PrefillChunk, ...]:
         candidates = self._prefilling() + self._admission_candidates()
         if not candidates:
             return ()
-        cap = self.token_budget // len(candidates)
+        cap = budget // len(candidates)
         return tuple(PrefillChunk(s, s.cache_length, s.cache_length + min(s.request.prompt_len - s.cache_length, cap))
                      for s in candidates)
 
     def _decide(self) -> SchedulerOutput | None:
         decoding = self._decoding()
-        if decoding and self._last_phase is SchedulePhase.PREFILL:
+        if self.mixed:
+            # token_budget >= max_running_requests, so every chunk still gets at least one token
+            chunks = self._plan_chunks(self.token_budget - len(decoding))
+            if chunks and decoding:
+                padded = len(chunks) * max(c.num_tokens for c in chunks)
+                return SchedulerOutput(SchedulePhase.MIXED, decoding + tuple(c.state for c in chunks),
+                                       len(decoding) + padded, chunks)
+        elif decoding and self._last_phase is SchedulePhase.PREFILL:
             return SchedulerOutput(SchedulePhase.DECODE, decoding, len(decoding))
-        chunks = self._plan_chunks()
+        else:
+            chunks = self._plan_chunks(self.token_budget)
         if chunks:
             return SchedulerOutput(SchedulePhase.PREFILL, tuple(c.state for c in chunks),
                                    len(chunks) * max(c.num_tokens for c in chunks), chunks)
@@ -203,7 +226,7 @@ class IterationScheduler:
         output = self._decide()
         if output is None:
             return None
-        if output.phase is SchedulePhase.PREFILL:
+        if output.phase is not SchedulePhase.DECODE:
             admitted = sum(1 for c in output.prefill_chunks if c.state.status is RequestStatus.WAITING)
             for _ in range(admitted):
                 state = self.waiting.popleft()
@@ -213,24 +236,20 @@ class IterationScheduler:
                 self.running.append(state)
             for chunk in output.prefill_chunks:
                 self._allocate(chunk.state, chunk.num_tokens)
-        else:
-            for state in output.scheduled_requests:
-                self._allocate(state, 1)
+        for state in output.decode_requests:
+            self._allocate(state, 1)
         self._last_phase = output.phase
         return output
 
     def update_from_output(self, output: SchedulerOutput, token_ids: Sequence[int], clock_ms: float,
                            eos_token_id: int | None = None, stop_on_eos: bool = True) -> list[RequestState]:
         """Advances the requests of a finished step; ``token_ids`` are the new tokens of every decode
-        row, or of the prefill rows whose chunk completed the prompt.  Frees finished requests."""
-        if output.phase is SchedulePhase.DECODE:
-            for state in output.scheduled_requests:
-                state.cache_length += 1
-            producers = output.scheduled_requests
-        else:
-            for chunk in output.prefill_chunks:
-                chunk.state.cache_length = chunk.end
-            producers = tuple(c.state for c in output.prefill_chunks if c.is_last)
+        row, then of the prefill rows whose chunk completed the prompt.  Frees finished requests."""
+        for state in output.decode_requests:
+            state.cache_length += 1
+        for chunk in output.prefill_chunks:
+            chunk.state.cache_length = chunk.end
+        producers = output.decode_requests + tuple(c.state for c in output.prefill_chunks if c.is_last)
         if len(token_ids) != len(producers):
             raise ValueError(f"{len(token_ids)} tokens for {len(producers)} producing requests")
         finished = [s for s, t in zip(producers, token_ids) if s.append_token(int(t), clock_ms, eos_token_id,

@@ -5,7 +5,8 @@ Same contract and timing as the reference's PagedScheduleBackend
 
 * ``model_ms``: the runner's device-timed forward + greedy sample (StepTimer);
 * ``cache_ms``: host-timed, between device syncs: ``store_prefill`` after a prefill step, and
-  ``prepare_decode_inputs`` (pack + upload) before a decode step.
+  ``prepare_decode_inputs`` (pack + upload) before a decode step; a mixed step (decode rows and
+  prefill chunks in one forward, not in the reference) counts both its packing and its store.
 """
 
 from __future__ import annotations
@@ -90,6 +91,30 @@ class PagedScheduleBackend:
         out = self.runner.run_decode_step(ids, pos, meta, self.pool)
         return ScheduleStepOutput(out.next_tokens, out.model_ms, cache_ms, len(states), self._live_bytes(),
                                   sum(s.cache_length + 1 for s in states))
+
+    def execute_mixed(self, states: Sequence[RequestState], chunks: Sequence[PrefillChunk]) -> ScheduleStepOutput:
+        """Decode rows ``states`` and prefill ``chunks`` in one forward; tokens: the decode rows', then
+        those of the chunks that complete their prompt."""
+        manager = self.kv_cache_manager
+        tables = [manager.block_table(c.state.request.request_idx) for c in chunks]
+        starts = [c.start for c in chunks]
+        synchronize(self.device)
+        t0 = time.perf_counter()
+        ids, pos, meta = self.runner.prepare_mixed_inputs(
+            [c.state.request.token_ids[c.start:c.end] for c in chunks], starts, tables,
+            [s.generated[-1] for s in states], [s.cache_length for s in states],
+            [manager.block_table(s.request.request_idx) for s in states], self.pool)
+        synchronize(self.device)
+        cache_ms = (time.perf_counter() - t0) * 1000.0
+        out = self.runner.run_mixed_step(ids, pos, meta)
+        synchronize(self.device)
+        t0 = time.perf_counter()
+        self.runner.store_prefill(self.pool, out.prefill_cache, tables, [c.num_tokens for c in chunks], starts)
+        synchronize(self.device)
+        cache_ms += (time.perf_counter() - t0) * 1000.0
+        tokens = out.decode_next_tokens + [t for t, c in zip(out.prefill_next_tokens, chunks) if c.is_last]
+        return ScheduleStepOutput(tokens, out.model_ms, cache_ms, len(states) + len(chunks), self._live_bytes(),
+                                  sum(s.cache_length + 1 for s in states) + sum(c.start for c in chunks))
 
 
 __all__ = ["PagedScheduleBackend", "ScheduleStepOutput"]

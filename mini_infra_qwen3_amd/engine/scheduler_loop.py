@@ -136,11 +136,13 @@ class ScheduleResult:
 def run_scheduler(backend, requests: Sequence[Request], token_budget: int = 2048,
                   max_running_requests: int | None = None, eos_token_id: int | None = None,
                   stop_on_eos: bool = True,
-                  step_clock: Callable[[SchedulerOutput], float] | None = None) -> ScheduleResult:
+                  step_clock: Callable[[SchedulerOutput], float] | None = None,
+                  mixed_batching: bool = False) -> ScheduleResult:
     """Runs ``requests`` to completion on ``backend`` (``execute_prefill`` / ``execute_decode`` and a
     ``kv_cache_manager``) with continuous batching and chunked prefill under ``token_budget``.
 
     ``max_running_requests`` defaults to the number of requests (reference scheduler_loop.py:162-163).
+    ``mixed_batching`` runs decode rows and prefill chunks in the same step (``execute_mixed``).
     """
     if not requests:
         raise ValueError("requests must not be empty")
@@ -150,7 +152,7 @@ def run_scheduler(backend, requests: Sequence[Request], token_budget: int = 2048
     states = [RequestState(r) for r in requests]
     arrivals = ArrivalQueue(states)
     clock_ms = min(r.arrival_ms for r in requests)
-    scheduler = IterationScheduler(token_budget, mrr, backend.kv_cache_manager)
+    scheduler = IterationScheduler(token_budget, mrr, backend.kv_cache_manager, mixed=mixed_batching)
     events: list[ScheduleEvent] = []
     device = getattr(backend, "device", torch.device("cpu"))
     synchronize(device)
@@ -163,6 +165,8 @@ def run_scheduler(backend, requests: Sequence[Request], token_budget: int = 2048
             continue
         if output.phase is SchedulePhase.PREFILL:
             step = backend.execute_prefill(output.prefill_chunks)
+        elif output.phase is SchedulePhase.MIXED:
+            step = backend.execute_mixed(output.decode_requests, output.prefill_chunks)
         else:
             step = backend.execute_decode(output.scheduled_requests)
         step_ms = step.model_ms + step.cache_ms

@@ -3,6 +3,7 @@
 from mini_infra_qwen3_amd.model.config import Qwen3Config, qwen3_0_6b
 from mini_infra_qwen3_amd.model.qwen3 import (
     PagedAttentionMetadata,
+    PagedMixedMetadata,
     PagedPrefillMetadata,
     Qwen3ForCausalLM,
     Qwen3Model,
@@ -11,6 +12,7 @@ from mini_infra_qwen3_amd.model.qwen3 import (
 
 __all__ = [
     "PagedAttentionMetadata",
+    "PagedMixedMetadata",
     "PagedPrefillMetadata",
     "Qwen3Config",
     "Qwen3ForCausalLM",

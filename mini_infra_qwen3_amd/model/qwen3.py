@@ -9,7 +9,11 @@ state_dict loads unchanged.  The attention differs in how it reaches K/V:
   context from the pool (replaces qwen3.py:257-292 + :219-255, no gather, no repeat_interleave);
 * prefill (``PagedPrefillMetadata``, or no metadata for a whole left-padded prompt): the MFMA
   chunked-prefill kernel attends causally within the chunk and reads the history straight from
-  the pool through the block table (replaces the gather + concat + _attend chain).
+  the pool through the block table (replaces the gather + concat + _attend chain);
+* mixed (``PagedMixedMetadata``): prefill chunks and decode tokens in one forward, the batching
+  the reference plans next (src/mini_infra/core/scheduler.py:310-311).  The GEMMs, norms and MLP
+  run once over all tokens; q/k norm + RoPE and attention run in their prefill and decode forms
+  on the two token ranges, writing one output buffer.
 
 Dense GEMMs (projections, MLP, lm_head) stay on PyTorch-ROCm -- q/k/v, and gate/up, each as one
 GEMM over the row-concatenated weights, the outputs split as column views; the elementwise chains around them
@@ -52,6 +56,18 @@ class PagedPrefillMetadata(NamedTuple):
     history_block_tables: torch.Tensor
     start_lens: torch.Tensor
     chunk_lens: torch.Tensor
+    kv_pools: tuple[PastKeyValue, ...] = ()
+
+
+class PagedMixedMetadata(NamedTuple):
+    """A mixed chunk + decode step over a flattened ``[1, T]`` batch: tokens ``[0, P L)`` are
+    ``prefill_rows`` (P) left-padded chunks of ``prefill_width`` (L) tokens addressed by ``prefill``;
+    the last ``T - P L`` tokens are one new token per decoding sequence, addressed by ``decode``."""
+
+    prefill: PagedPrefillMetadata
+    decode: PagedAttentionMetadata
+    prefill_rows: int
+    prefill_width: int
     kv_pools: tuple[PastKeyValue, ...] = ()
 
 
@@ -133,6 +149,8 @@ class Qwen3Attention(nn.Module):
         q, k, v = qkv[..., :nq], qkv[..., nq:nq + nkv], qkv[..., nq + nkv:]
         key_pool, value_pool = kv_pool
         eps = self.q_norm.eps
+        if isinstance(metadata, PagedMixedMetadata):
+            return self._mixed(q[0], k[0], v[0], cos[0], sin[0], kv_pool, metadata, workspace)
         if isinstance(metadata, PagedAttentionMetadata):
             q_rot, _, _ = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin, eps,
                                                   slot_mapping=metadata.slot_mapping, key_pool=key_pool,
@@ -155,6 +173,32 @@ class Qwen3Attention(nn.Module):
             )
             present = (k_rot, v_rows)
         return self.o_proj(out), present
+
+    def _mixed(self, q, k, v, cos, sin, kv_pool: PastKeyValue, metadata: PagedMixedMetadata, workspace):
+        """Token rows ``[0, P L)`` take the prefill path, the rest the decode path (its K/V append
+        first, so decode attention sees the new token); both attentions write one ``[T, H D]`` buffer."""
+        key_pool, value_pool = kv_pool
+        rows, width = metadata.prefill_rows, metadata.prefill_width
+        n = rows * width
+        tokens = q.shape[0]
+        eps = self.q_norm.eps
+        q_dec, _, _ = data_plane.qk_norm_rope(q[n:], k[n:], v[n:], self.q_norm.weight, self.k_norm.weight, cos[n:],
+                                              sin[n:], eps, slot_mapping=metadata.decode.slot_mapping,
+                                              key_pool=key_pool, value_pool=value_pool)
+        q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q[:n], k[:n], v[:n], self.q_norm.weight, self.k_norm.weight,
+                                                       cos[:n], sin[:n], eps)
+        q_rot = q_rot.view(rows, width, self.num_heads, self.head_dim).transpose(1, 2)
+        k_rot = k_rot.view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        v_rows = v_rows.view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        out = torch.empty((tokens, self.num_heads * self.head_dim), dtype=q.dtype, device=q.device)
+        prefill = metadata.prefill
+        data_plane.chunked_prefill_attention(q_rot, k_rot, v_rows, key_pool, value_pool, prefill.history_block_tables,
+                                             prefill.start_lens, prefill.chunk_lens, self.scaling,
+                                             out=out[:n].view(rows, width, -1))
+        decode = metadata.decode
+        data_plane.paged_decode_attention(q_dec, key_pool, value_pool, decode.block_tables, decode.context_lens,
+                                          self.scaling, out=out[n:], workspace=workspace)
+        return self.o_proj(out.unsqueeze(0)), (k_rot, v_rows)
 
 
 class Qwen3MLP(nn.Module):
@@ -204,14 +248,16 @@ class Qwen3Model(nn.Module):
 
     def forward(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None,
                 position_ids: torch.Tensor | None = None,
-                attn_metadata: PagedAttentionMetadata | PagedPrefillMetadata | None = None,
+                attn_metadata: PagedAttentionMetadata | PagedPrefillMetadata | PagedMixedMetadata | None = None,
                 last_only: bool = False):
         """Returns (final hidden states ``[B, L, hidden]``, or ``[B, 1, hidden]`` of the last position
         with ``last_only``, and the per-layer present K/V).
 
         Decode (``PagedAttentionMetadata``): input_ids / position_ids ``[B, 1]``.  Prefill: a
         left-padded ``[B, L]`` chunk; without metadata, ``attention_mask`` (left padding, True on
-        real tokens) gives the chunk lengths and there is no history.
+        real tokens) gives the chunk lengths and there is no history.  Mixed (``PagedMixedMetadata``):
+        ``[1, P L + D]``; with ``last_only`` the rows are the P chunks' last positions, then the D
+        decode tokens (``[P + D, 1, hidden]``), and the present K/V are the chunks'.
         """
         if input_ids.ndim != 2 or input_ids.shape[1] < 1:
             raise ValueError("input_ids must be a non-empty [batch, sequence] tensor")
@@ -219,7 +265,23 @@ class Qwen3Model(nn.Module):
         device = input_ids.device
         hidden = self.embed_tokens(input_ids)
         workspace = None
-        if isinstance(attn_metadata, PagedAttentionMetadata):
+        if isinstance(attn_metadata, PagedMixedMetadata):
+            metadata = attn_metadata
+            pools = metadata.kv_pools
+            rows, width = metadata.prefill_rows, metadata.prefill_width
+            decode_rows = metadata.decode.slot_mapping.shape[0]
+            if batch != 1 or length != rows * width + decode_rows or rows < 1 or decode_rows < 1:
+                raise ValueError(f"mixed step takes input_ids [1, P * L + D] with P, D >= 1, got {tuple(input_ids.shape)}")
+            if position_ids is None:
+                raise ValueError("a mixed step needs position_ids")
+            if len(pools) != len(self.layers):
+                raise ValueError("kv_pools has a different number of layers than the model")
+            need = data_plane.paged_decode_workspace_bytes(decode_rows, metadata.decode.block_tables.shape[1],
+                                                          self.config.num_attention_heads, self.config.head_dim,
+                                                          pools[0][0].shape[1])
+            if need:
+                workspace = torch.empty(need, dtype=torch.uint8, device=device)
+        elif isinstance(attn_metadata, PagedAttentionMetadata):
             if length != 1:
                 raise ValueError("paged decode takes input_ids of shape [batch, 1]")
             if position_ids is None:
@@ -259,7 +321,11 @@ class Qwen3Model(nn.Module):
         for layer, kv_pool in zip(self.layers, pools):
             hidden, residual, present = layer(hidden, residual, cos, sin, kv_pool, metadata, workspace)
             presents.append(present)
-        if last_only:  # the norm is row-wise: only the position the sampler reads
+        if last_only and isinstance(metadata, PagedMixedMetadata):
+            width, n = metadata.prefill_width, metadata.prefill_rows * metadata.prefill_width
+            hidden = torch.cat((hidden[0, width - 1:n:width], hidden[0, n:])).unsqueeze(1)
+            residual = torch.cat((residual[0, width - 1:n:width], residual[0, n:])).unsqueeze(1)
+        elif last_only:  # the norm is row-wise: only the position the sampler reads
             hidden, residual = hidden[:, -1:, :], residual[:, -1:, :]
         return self.norm(hidden, residual)[0], presents
 
@@ -301,6 +367,7 @@ def init_random_(model: Qwen3ForCausalLM, seed: int, std: float = 0.02, untied_h
 
 __all__ = [
     "PagedAttentionMetadata",
+    "PagedMixedMetadata",
     "PagedPrefillMetadata",
     "Qwen3Attention",
     "Qwen3ForCausalLM",

@@ -4,7 +4,7 @@ from mini_infra_qwen3_amd.worker.base_runner import BaseModelRunner, PrefillOutp
 from mini_infra_qwen3_amd.worker.kv_cache import KVCache
 from mini_infra_qwen3_amd.worker.kv_swap import HostSwapPool, KVBlockHeader, load_kv_blocks, save_kv_blocks
 from mini_infra_qwen3_amd.worker.paged_kv_cache import PagedKVCachePool
-from mini_infra_qwen3_amd.worker.paged_runner import PagedDecodeOutput, PagedRunner
+from mini_infra_qwen3_amd.worker.paged_runner import MixedStepOutput, PagedDecodeOutput, PagedRunner
 from mini_infra_qwen3_amd.worker.sampler import greedy_sample
 
 __all__ = [
@@ -12,6 +12,7 @@ __all__ = [
     "HostSwapPool",
     "KVBlockHeader",
     "KVCache",
+    "MixedStepOutput",
     "PagedDecodeOutput",
     "PagedKVCachePool",
     "PagedRunner",

@@ -104,4 +104,25 @@ def pack_prefill_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions:
     return out
 
 
-__all__ = ["pack_decode_rows", "pack_prefill_rows", "padded_tables", "prefill_scatter_indices"]
+def pack_mixed_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions: Sequence[int],
+                    prefill_tables: Sequence[Sequence[int]], last_tokens: Sequence[int], positions: Sequence[int],
+                    decode_tables: Sequence[Sequence[int]], block_size: int,
+                    pad_token_id: int) -> tuple[np.ndarray, tuple[int, int, int, int, int]]:
+    """One int64 buffer for a mixed chunk + decode step, uploaded at once.
+
+    Layout (T = P L + D): tokens ``[T]`` | positions ``[T]`` | per chunk row (start, length,
+    history table) ``[P, 2 + nb]`` | per decode row (slot, context length, block table)
+    ``[D, 2 + mb]``.  The first P L tokens / positions are the chunks left-padded to L, row-major,
+    as ``pack_prefill_rows`` lays them out; the last D are the decode tokens of ``pack_decode_rows``.
+    Returns the buffer and (P, L, nb, D, mb).
+    """
+    prefill = pack_prefill_rows(chunk_token_ids, start_positions, prefill_tables, block_size, pad_token_id)
+    decode = pack_decode_rows(decode_tables, last_tokens, positions, block_size)
+    rows, width = prefill.shape[0], max(len(ids) for ids in chunk_token_ids)
+    nb = prefill.shape[1] - 2 * width - 2
+    flat = np.concatenate([prefill[:, :width].ravel(), decode[:, 0], prefill[:, width:2 * width].ravel(), decode[:, 1],
+                           prefill[:, 2 * width:].ravel(), decode[:, 2:].ravel()])
+    return flat, (rows, width, nb, decode.shape[0], decode.shape[1] - 4)
+
+
+__all__ = ["pack_decode_rows", "pack_mixed_rows", "pack_prefill_rows", "padded_tables", "prefill_scatter_indices"]

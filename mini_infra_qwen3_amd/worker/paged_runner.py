@@ -13,7 +13,9 @@ Same entry points, arguments and return types as the reference's PagedRunner
   ``enable_decode_graphs`` the whole decode forward is captured once per padded (batch, blocks)
   bucket in a HIP graph: ``prepare_decode_inputs`` then packs the step (pad rows: slot -1 = no
   append, context 0 = zero output) straight into the bucket's static metadata buffer with one
-  upload, and ``run_decode_step`` replays the graph -- one launch instead of ~300.
+  upload, and ``run_decode_step`` replays the graph -- one launch instead of ~300;
+* ``prepare_mixed_inputs`` / ``run_mixed_step`` run prefill chunks and decode tokens in one forward
+  (the mixed batching the reference plans next: src/mini_infra/core/scheduler.py:310-311).
 """
 
 from __future__ import annotations
@@ -26,10 +28,11 @@ import torch
 
 from mini_infra_qwen3_amd.data_plane import argmax_rows
 from mini_infra_qwen3_amd.device import StepTimer
-from mini_infra_qwen3_amd.model.qwen3 import PagedAttentionMetadata, PagedPrefillMetadata
+from mini_infra_qwen3_amd.model.qwen3 import PagedAttentionMetadata, PagedMixedMetadata, PagedPrefillMetadata
 from mini_infra_qwen3_amd.worker.base_runner import BaseModelRunner, PrefillOutput
 from mini_infra_qwen3_amd.worker.kv_cache import KVCache
-from mini_infra_qwen3_amd.worker.metadata import pack_decode_rows, pack_prefill_rows, prefill_scatter_indices
+from mini_infra_qwen3_amd.worker.metadata import (pack_decode_rows, pack_mixed_rows, pack_prefill_rows,
+                                                  prefill_scatter_indices)
 from mini_infra_qwen3_amd.worker.paged_kv_cache import PagedKVCachePool
 from mini_infra_qwen3_amd.worker.sampler import greedy_sample
 
@@ -76,6 +79,16 @@ class PagedDecodeOutput(NamedTuple):
     """Next token per row (input order) and the model time in ms."""
 
     next_tokens: list[int]
+    model_ms: float
+
+
+class MixedStepOutput(NamedTuple):
+    """A mixed step: the greedy token after each chunk row (meaningful where the chunk completes its
+    prompt) and after each decode row, the chunks' K/V (for ``store_prefill``) and the model time."""
+
+    prefill_next_tokens: list[int]
+    decode_next_tokens: list[int]
+    prefill_cache: KVCache
     model_ms: float
 
 
@@ -208,5 +221,48 @@ class PagedRunner(BaseModelRunner):
             next_token, _ = greedy_sample(logits)
         return PagedDecodeOutput(next_token.squeeze(-1).tolist(), timer.elapsed_ms)
 
+    def prepare_mixed_inputs(
+        self,
+        chunk_token_ids: Sequence[Sequence[int]],
+        start_positions: Sequence[int],
+        prefill_block_tables: Sequence[Sequence[int]],
+        last_tokens: Sequence[int],
+        positions: Sequence[int],
+        decode_block_tables: Sequence[Sequence[int]],
+        pool: PagedKVCachePool,
+    ) -> tuple[torch.Tensor, torch.Tensor, PagedMixedMetadata]:
+        """Packs a mixed step -- chunk rows as ``run_prefill_chunk_step`` takes them, decode rows as
+        ``prepare_decode_inputs`` does -- into one int64 buffer with one upload.  Returns input_ids /
+        position_ids ``[1, P L + D]`` and the metadata, all views of that buffer."""
+        flat, (rows, width, nb, decode_rows, mb) = pack_mixed_rows(
+            chunk_token_ids, start_positions, prefill_block_tables, last_tokens, positions, decode_block_tables,
+            pool.block_size, self.pad_token_id)
+        packed = torch.from_numpy(flat).to(self.device)
+        tokens = rows * width + decode_rows
+        at = 2 * tokens
+        chunk = packed[at:at + rows * (2 + nb)].view(rows, 2 + nb)
+        at += rows * (2 + nb)
+        dec = packed[at:].view(decode_rows, 2 + mb)
+        pools = tuple(pool.kv_pools)
+        metadata = PagedMixedMetadata(
+            prefill=PagedPrefillMetadata(history_block_tables=chunk[:, 2:], start_lens=chunk[:, 0],
+                                         chunk_lens=chunk[:, 1], kv_pools=pools),
+            decode=PagedAttentionMetadata(slot_mapping=dec[:, 0], block_tables=dec[:, 2:], context_lens=dec[:, 1],
+                                          kv_pools=pools),
+            prefill_rows=rows, prefill_width=width, kv_pools=pools)
+        return packed[:tokens].view(1, tokens), packed[tokens:2 * tokens].view(1, tokens), metadata
 
-__all__ = ["PagedDecodeOutput", "PagedRunner"]
+    def run_mixed_step(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
+                       metadata: PagedMixedMetadata) -> MixedStepOutput:
+        """One forward over the chunks and the decode tokens: the decode rows' K/V go into the pool,
+        the chunks' K/V come back as ``prefill_cache``; greedy tokens of both."""
+        with StepTimer(self.device) as timer:
+            logits, present = self.model(input_ids, position_ids=position_ids, attn_metadata=metadata,
+                                         last_logits_only=True)
+            next_token, _ = greedy_sample(logits)
+        tokens = next_token.squeeze(-1).tolist()
+        rows = metadata.prefill_rows
+        return MixedStepOutput(tokens[:rows], tokens[rows:], KVCache(present), timer.elapsed_ms)
+
+
+__all__ = ["MixedStepOutput", "PagedDecodeOutput", "PagedRunner"]

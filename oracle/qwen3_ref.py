@@ -237,3 +237,13 @@ class ReferenceScheduleBackend:
                              [s.cache_length for s in states], self.pools, self.block_size).float()
         tokens = self._choose([s.request.request_idx for s in states], [len(s.generated) for s in states], logits)
         return ScheduleStepOutput(tokens, 0.0, 0.0, len(states), 0)
+
+    def execute_mixed(self, states, chunks):
+        """A mixed step is, by definition, the decode step of ``states`` and the chunk step of
+        ``chunks``: disjoint requests with disjoint blocks, so neither reads what the other writes.
+        Runs both; tokens of the decode rows first, as the mixed step returns them."""
+        from mini_infra_qwen3_amd.engine import ScheduleStepOutput
+
+        decode = self.execute_decode(states)
+        prefill = self.execute_prefill(chunks)
+        return ScheduleStepOutput(decode.next_tokens + prefill.next_tokens, 0.0, 0.0, len(states) + len(chunks), 0)

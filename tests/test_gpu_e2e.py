@@ -34,7 +34,7 @@ MAX_TIE_FRACTION = 0.1
 
 
 def step_clock(out):
-    return 10.0 if out.phase is SchedulePhase.PREFILL else 5.0
+    return {SchedulePhase.PREFILL: 10.0, SchedulePhase.MIXED: 12.0}.get(out.phase, 5.0)
 
 
 def build(untied_head_seed=None):
@@ -52,18 +52,23 @@ def requests():
     return serving_requests(seed=1, num_requests=12, min_prompt=32, max_prompt=700, max_new_tokens=24)
 
 
-@pytest.mark.parametrize("untied_head_seed,graphs", [(None, True), (1234, False)],
-                         ids=["benchmark_model_decode_graphs", "context_dependent_model"])
-def test_tokens_are_oracle_greedy_choices(requests, untied_head_seed, graphs):
+@pytest.mark.parametrize("untied_head_seed,graphs,mixed", [(None, True, False), (1234, False, False),
+                                                           (None, True, True)],
+                         ids=["benchmark_model_decode_graphs", "context_dependent_model", "mixed_batching"])
+def test_tokens_are_oracle_greedy_choices(requests, untied_head_seed, graphs, mixed):
+    """``mixed_batching``: decode rows and prefill chunks share steps (the oracle runs a mixed step
+    as the decode step and the chunk step it consists of)."""
     model, ref = build(untied_head_seed)
     mrr, budget = 8, 256
     backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=graphs)
     product = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
-                            stop_on_eos=False, step_clock=step_clock)
-    assert product.num_steps(SchedulePhase.PREFILL) > len(requests)  # prompts were chunked
+                            stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed)
+    chunk_steps = product.num_steps(SchedulePhase.PREFILL) + product.num_steps(SchedulePhase.MIXED)
+    assert chunk_steps > len(requests)  # prompts were chunked
+    assert (product.num_steps(SchedulePhase.MIXED) > 0) == mixed
     backend = qwen3_ref.ReferenceScheduleBackend(ref, requests, mrr, forced_tokens=product.tokens)
     oracle = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
-                           stop_on_eos=False, step_clock=step_clock)
+                           stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed)
     assert [(e.phase, e.request_ids, e.chunk_spans) for e in product.events] == \
         [(e.phase, e.request_ids, e.chunk_spans) for e in oracle.events]
     records = backend.records

@@ -268,6 +268,70 @@ def test_chunked_prefill_matches_oracle_runner(models):
                 assert_kv_close(layer, got, want)
 
 
+def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
+    """One forward over two prompt chunks (one with history, one completing its prompt) and three
+    decoding requests equals the chunk step and the decode step run apart: same greedy tokens as
+    those and as the CPU oracle, logits close, every stored K/V row close."""
+    model, _, ref_cpu = models
+    cfg = model.config
+    runner = PagedRunner(model)
+    decoders = prompts_of([45, 17, 3], seed=8)
+    chunked = prompts_of([70, 20], seed=9)
+    pools = [make_pool(cfg, 64), make_pool(cfg, 64)]
+    cpu_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128)
+    manager = KVCacheManager(BS, num_blocks=64)
+    for i, p in enumerate(decoders + chunked):
+        manager.allocate_slots(i, len(p))
+    tables = [manager.block_table(i) for i in range(5)]
+    # set-up, identical on both pools: decoders prefilled, request 3 has its first 30 tokens cached
+    first = None
+    for pool in pools:
+        out = runner.run_prefill_step(decoders)
+        runner.store_prefill(pool, out.prefill_cache, tables[:3], [len(p) for p in decoders], [0] * 3)
+        part = runner.run_prefill_chunk_step([chunked[0][:30]], [0], [tables[3]], pool)
+        runner.store_prefill(pool, part.prefill_cache, [tables[3]], [30], [0])
+        first = out.next_tokens
+    _, presents = qwen3_ref.prefill(ref_cpu, decoders)
+    qwen3_ref.store_prefill(cpu_pools, presents, tables[:3], [len(p) for p in decoders], [0] * 3, BS)
+    _, presents = qwen3_ref.prefill_chunk_step(ref_cpu, [chunked[0][:30]], [0], [tables[3]], cpu_pools, BS)
+    qwen3_ref.store_prefill(cpu_pools, presents, [tables[3]], [30], [0], BS)
+    chunks, starts = [chunked[0][30:], chunked[1]], [30, 0]
+    lens = [len(c) for c in chunks]
+    positions = [len(p) for p in decoders]
+    for i in range(3):
+        assert manager.allocate_slots(i, 1)
+    dec_tables = [manager.block_table(i) for i in range(3)]
+    pf_tables = [tables[3], tables[4]]
+    with torch.inference_mode():
+        # apart: chunk step + store, then decode step (pool 0)
+        apart = runner.run_prefill_chunk_step(chunks, starts, pf_tables, pools[0])
+        runner.store_prefill(pools[0], apart.prefill_cache, pf_tables, lens, starts)
+        ids, pos, meta = runner.prepare_decode_inputs(dec_tables, first, positions, BS)
+        dec_logits = model(ids, position_ids=pos, attn_metadata=meta._replace(kv_pools=tuple(pools[0].kv_pools)),
+                           last_logits_only=True)[0][:, -1].float()
+        # mixed (pool 1)
+        ids, pos, meta = runner.prepare_mixed_inputs(chunks, starts, pf_tables, first, positions, dec_tables,
+                                                     pools[1])
+        assert ids.shape == (1, 2 * max(lens) + 3)
+        # the decode rows' append rewrites the same values when the step runs again
+        mixed_logits = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)[0][:, -1].float()
+        got = runner.run_mixed_step(ids, pos, meta)
+        runner.store_prefill(pools[1], got.prefill_cache, pf_tables, lens, starts)
+    want_dec = qwen3_ref.decode_step(ref_cpu, dec_tables, first, positions, cpu_pools, BS)
+    want_pf, _ = qwen3_ref.prefill_chunk_step(ref_cpu, chunks, starts, pf_tables, cpu_pools, BS)
+    assert got.decode_next_tokens == dec_logits.argmax(-1).tolist() == want_dec.argmax(-1).tolist()
+    assert got.prefill_next_tokens == apart.next_tokens == want_pf
+    assert (mixed_logits[2:] - dec_logits).abs().max().item() <= LOGIT_RTOL * dec_logits.abs().max().item()
+    for r in range(5):
+        length = positions[r] + 1 if r < 3 else len(chunked[r - 3])
+        table = manager.block_table(r)
+        for layer in range(cfg.num_hidden_layers):
+            for kv in range(2):
+                a = request_kv(pools[0], layer, table, length)[kv]
+                b = request_kv(pools[1], layer, table, length)[kv]
+                assert_kv_close(layer, b, a)
+
+
 def test_decode_graph_replays_match_eager_forward_and_touch_only_live_slots(models):
     """Decode graphs: each replay equals an eager forward of the same padded inputs, bit for bit,
     with eager work and syncs between replays; pad rows write nothing; batches shrink and grow

@@ -10,15 +10,15 @@ from mini_infra_qwen3_amd.core import KVCacheManager, Request
 from mini_infra_qwen3_amd.core.scheduler import IterationScheduler, RequestState, SchedulePhase
 from mini_infra_qwen3_amd.engine import ScheduleStepOutput, percentile, run_scheduler
 
-DECODE, PREFILL = SchedulePhase.DECODE, SchedulePhase.PREFILL
+DECODE, PREFILL, MIXED = SchedulePhase.DECODE, SchedulePhase.PREFILL, SchedulePhase.MIXED
 
 
 def states_with(prompt_lens, max_new=4):
     return [RequestState(Request(i, tuple(range(1, n + 1)), max_new)) for i, n in enumerate(prompt_lens)]
 
 
-def scheduler(token_budget, capacity, manager=None):
-    return IterationScheduler(token_budget, capacity, manager or KVCacheManager(4, 1000))
+def scheduler(token_budget, capacity, manager=None, mixed=False):
+    return IterationScheduler(token_budget, capacity, manager or KVCacheManager(4, 1000), mixed=mixed)
 
 
 def ranges(out):
@@ -28,7 +28,7 @@ def ranges(out):
 def step(sched, clock):
     out = sched.schedule(clock)
     assert out is not None
-    n = sum(c.is_last for c in out.prefill_chunks) if out.phase is PREFILL else len(out.scheduled_requests)
+    n = sum(c.is_last for c in out.prefill_chunks) + len(out.decode_requests)
     sched.update_from_output(out, [7] * n, clock, stop_on_eos=False)
     return out
 
@@ -147,6 +147,13 @@ class FakeBackend:
         toks = [(s.request.request_idx * 31 + s.cache_length + 1) % 97 + 1 for s in states]
         return ScheduleStepOutput(toks, 1.0, 0.25, len(states), 0)
 
+    def execute_mixed(self, states, chunks):
+        self.executed.append(("mixed", [s.request.request_idx for s in states],
+                              [(c.state.request.request_idx, c.start, c.end) for c in chunks]))
+        toks = [(s.request.request_idx * 31 + s.cache_length + 1) % 97 + 1 for s in states]
+        toks += [(c.state.request.request_idx * 31 + c.end) % 97 + 1 for c in chunks if c.is_last]
+        return ScheduleStepOutput(toks, 2.2, 0.6, len(states) + len(chunks), 0)
+
 
 @pytest.mark.parametrize("budget,capacity", [(8, 2), (16, 4), (64, 8)])
 def test_loop_invariants_and_metric(budget, capacity):
@@ -178,6 +185,68 @@ def test_step_clock_makes_the_schedule_timing_independent():
     run_scheduler(a, requests, token_budget=8, max_running_requests=3, step_clock=lambda out: 5.0)
     run_scheduler(b, requests, token_budget=8, max_running_requests=3, step_clock=lambda out: 5.0)
     assert a.executed == b.executed
+
+
+def test_mixed_steps_decode_while_prefilling():
+    """Mixed batching (the reference's planned policy, core/scheduler.py:310-311): decoding requests
+    take one token of the budget each, chunks share the rest, in one MIXED step."""
+    s = scheduler(8, 4, mixed=True)
+    s.add_requests(states_with([2, 20], max_new=10))
+    first = step(s, 0.0)
+    assert first.phase is PREFILL and ranges(first) == [(0, 0, 2), (1, 0, 4)]
+    for clock, want in ((1.0, (1, 4, 11)), (2.0, (1, 11, 18)), (3.0, (1, 18, 20))):
+        out = step(s, clock)
+        assert out.phase is MIXED and ranges(out) == [want]
+        assert [st.request.request_idx for st in out.decode_requests] == [0]
+        assert out.num_scheduled_tokens == 1 + want[2] - want[1] <= 8
+    last = step(s, 4.0)
+    assert last.phase is DECODE and [st.request.request_idx for st in last.decode_requests] == [0, 1]
+    assert last.prefill_chunks == ()
+
+
+def test_mixed_update_takes_decode_tokens_first():
+    s = scheduler(8, 4, mixed=True)
+    a, b = states_with([2, 3], max_new=5)
+    s.add_requests([a])
+    step(s, 0.0)
+    s.add_requests([b])
+    out = s.schedule(1.0)
+    assert out.phase is MIXED and out.decode_requests == (a,) and ranges(out) == [(1, 0, 3)]
+    s.update_from_output(out, [11, 22], 1.0, stop_on_eos=False)
+    assert a.generated == [7, 11] and b.generated == [22] and a.cache_length == 3 and b.cache_length == 3
+    with pytest.raises(ValueError):
+        s.update_from_output(s.schedule(2.0), [1], 2.0)
+
+
+@pytest.mark.parametrize("budget,capacity", [(8, 2), (16, 4), (64, 8)])
+def test_mixed_loop_generates_the_same_tokens(budget, capacity):
+    lens, outs = [13, 4, 9, 2, 16, 30, 7], [5, 7, 3, 6, 4, 2, 9]
+    arrivals = [0.0, 0.0, 3.0, 3.5, 20.0, 21.0, 200.0]
+    requests = [Request(i, tuple(range(1, n + 1)), m, a) for i, (n, m, a) in enumerate(zip(lens, outs, arrivals))]
+    plain = run_scheduler(FakeBackend(), requests, token_budget=budget, max_running_requests=capacity)
+    backend = FakeBackend()
+    mixed = run_scheduler(backend, requests, token_budget=budget, max_running_requests=capacity,
+                          mixed_batching=True)
+    assert mixed.tokens == plain.tokens
+    assert any(e.phase is MIXED for e in mixed.events)
+    assert all(e.num_scheduled_tokens <= budget for e in mixed.events if e.phase is not DECODE)
+    # replay the executed steps: every request that has its first token and is not finished
+    # decodes in every step (no decoder waits behind a prefill)
+    decoding, made = set(), {}
+    for kind, *rest in backend.executed:
+        rows = rest[0] if kind != "prefill" else []
+        chunks = rest[-1] if kind != "decode" else []
+        assert set(rows) == decoding
+        for i in rows:
+            made[i] += 1
+        for i, _, end in chunks:
+            if end == lens[i]:
+                made[i] = 1
+                decoding.add(i)
+        decoding -= {i for i in decoding if made[i] == outs[i]}
+    assert max(len(e.request_ids) for e in mixed.events) <= capacity
+    assert backend.kv_cache_manager.num_used_blocks == 0
+    assert sorted(i for e in mixed.events for i in e.finished_request_ids) == list(range(7))
 
 
 def test_percentile_is_nearest_rank():
