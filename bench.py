@@ -393,14 +393,16 @@ def bench_prefill(steps: int, warmup: int, device: torch.device) -> dict:
 
 
 # ------------------------------------------------------------------------ e2e continuous batching
-def bench_e2e(device: torch.device, seed: int = 0) -> dict:
+def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False) -> dict:
     """Continuous batching with chunked prefill (token budget 2048, block 16, batch slots = number of
     requests) of a random-init Qwen3-0.6B (bf16, N(0, 0.02), tied embeddings): 128 requests, Poisson
     arrivals at 20 req/s, prompts U[32, 1024], 128 greedy tokens each, EOS disabled.  Output tok/s =
     output tokens x 1000 / busy_ms, busy_ms = sum over steps of (device-timed forward + host-timed
     cache management), on the logical clock the measured step times advance.  The decode forward
-    is replayed from HIP graphs captured per padded (batch, blocks) bucket when the backend is set
-    up (``setup_s``, outside the timed run)."""
+    is replayed from HIP graphs captured per padded (batch, blocks) bucket, and the prefill forward
+    of one or two chunks per padded (rows, width, history) bucket, when the backend is set up
+    (``setup_s``, outside the timed run).  ``mixed``: decode rows ride in the prefill steps (the
+    mixed batching the reference plans) instead of the reference's alternating prefill / decode."""
     from mini_infra_qwen3_amd.core.scheduler import SchedulePhase
     from mini_infra_qwen3_amd.engine import PagedScheduleBackend, run_scheduler
     from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
@@ -412,17 +414,20 @@ def bench_e2e(device: torch.device, seed: int = 0) -> dict:
 
     def run(requests):
         t0 = time.perf_counter()
-        backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True)
+        backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True, prefill_graphs=True)
         setup_s = time.perf_counter() - t0
-        return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False), setup_s
+        return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False,
+                             mixed_batching=mixed), setup_s
 
     run(serving_requests(seed=seed + 1, num_requests=8, max_new_tokens=8))  # warm-up: kernels, GEMM choices
     requests = serving_requests(seed=seed)
     res, setup_s = run(requests)
     decode = [e for e in res.events if e.phase is SchedulePhase.DECODE]
     prefill = [e for e in res.events if e.phase is SchedulePhase.PREFILL]
+    mixed_steps = [e for e in res.events if e.phase is SchedulePhase.MIXED]
     out = {
         "metric": "e2e output tok/s Qwen3-0.6B (continuous batching, chunked prefill 2048, paged KV)",
+        "mixed_batching": mixed,
         "output_tok_s": round(res.throughput_tok_s, 1),
         "wall_tok_s": round(res.wall_tok_s, 1),
         "busy_ms": round(res.busy_ms, 1),
@@ -437,9 +442,12 @@ def bench_e2e(device: torch.device, seed: int = 0) -> dict:
         "decode_step_ms_mean": round(sum(e.step_ms for e in decode) / max(len(decode), 1), 3),
         "decode_batch_mean": round(sum(len(e.request_ids) for e in decode) / max(len(decode), 1), 2),
         "prefill_step_ms_mean": round(sum(e.step_ms for e in prefill) / max(len(prefill), 1), 3),
+        "mixed_steps": len(mixed_steps),
+        "mixed_step_ms_mean": round(sum(e.step_ms for e in mixed_steps) / max(len(mixed_steps), 1), 3),
         "requests": len(requests),
         "arrival_rate_req_s": 20.0,
         "decode_graphs": True,
+        "prefill_graphs": True,
         "setup_s": round(setup_s, 2),
         "latency_ms": {k: round(v, 2) for k, v in res.latency_summary().items()},
     }
@@ -454,7 +462,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["decode", "scatter", "gather", "prefill", "copy", "swap", "e2e", "all"],
+    parser.add_argument("--only", choices=["decode", "scatter", "gather", "prefill", "copy", "swap", "e2e", "e2e-mixed", "all"],
                         default="all")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -482,8 +490,8 @@ def main() -> int:
         log(f"{args.only}: {json.dumps(res)}")
         print(json.dumps(res), flush=True)
         return 0
-    if args.only == "e2e":
-        res = bench_e2e(device)
+    if args.only in ("e2e", "e2e-mixed"):
+        res = bench_e2e(device, mixed=args.only == "e2e-mixed")
         log(f"e2e: {res['output_tok_s']:.1f} output tok/s (busy), {res['wall_tok_s']:.1f} tok/s (wall)")
         print(json.dumps(res), flush=True)
         return 0
@@ -522,10 +530,13 @@ def main() -> int:
             f"{sw['unpack']['achieved_GBps']:.1f} GB/s; swap out {sw['swap_out']['achieved_GBps']:.1f} GB/s, "
             f"swap in {sw['swap_in']['achieved_GBps']:.1f} GB/s")
         torch.cuda.empty_cache()
-    e2e = None
+    e2e = e2e_mixed = None
     if args.only == "all":
         e2e = bench_e2e(device)
         log(f"e2e: {e2e['output_tok_s']:.1f} output tok/s (busy), {e2e['wall_tok_s']:.1f} tok/s (wall)")
+        e2e_mixed = bench_e2e(device, mixed=True)
+        log(f"e2e mixed batching: {e2e_mixed['output_tok_s']:.1f} output tok/s (busy), ITL max "
+            f"{e2e_mixed['latency_ms']['itl_ms_max']:.2f} ms (alternating: {e2e['latency_ms']['itl_ms_max']:.2f} ms)")
 
     line = {
         "metric": METRIC,
@@ -554,6 +565,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "kernels": kernels,
         "e2e": e2e,
+        "e2e_mixed_batching": e2e_mixed,
     }
     print(json.dumps(line), flush=True)
     return 0

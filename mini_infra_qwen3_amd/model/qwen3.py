@@ -57,6 +57,9 @@ class PagedPrefillMetadata(NamedTuple):
     start_lens: torch.Tensor
     chunk_lens: torch.Tensor
     kv_pools: tuple[PastKeyValue, ...] = ()
+    # optional per-layer (K, V) buffers, contiguous [B * L, H_kv, D], that receive the chunk's K/V
+    # (the present) instead of new allocations
+    kv_out: tuple[PastKeyValue, ...] = ()
 
 
 class PagedMixedMetadata(NamedTuple):
@@ -140,7 +143,7 @@ class Qwen3Attention(nn.Module):
         self.q_norm = RMSNorm(config.head_dim, config.rms_norm_eps)
         self.k_norm = RMSNorm(config.head_dim, config.rms_norm_eps)
 
-    def forward(self, hidden, cos, sin, kv_pool: PastKeyValue, metadata, workspace=None):
+    def forward(self, hidden, cos, sin, kv_pool: PastKeyValue, metadata, workspace=None, kv_out=None):
         """q/k/v projections (one PyTorch GEMM over the concatenated weights), then one fused launch for q/k RMSNorm + RoPE (plus,
         when decoding, the K/V append into the pool), then paged attention."""
         batch, length, _ = hidden.shape
@@ -161,8 +164,9 @@ class Qwen3Attention(nn.Module):
             ).view(batch, 1, -1)
             present = kv_pool
         else:
+            k_buf, v_buf = kv_out if kv_out is not None else (None, None)
             q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin,
-                                                           eps)
+                                                           eps, k_out=k_buf, v_out=v_buf)
             # token-major [B, L, H, D] buffers seen as [B, H, L, D] (strided views, no copies)
             q_rot = q_rot.view(batch, length, self.num_heads, self.head_dim).transpose(1, 2)
             k_rot = k_rot.view(batch, length, self.num_kv_heads, self.head_dim).transpose(1, 2)
@@ -222,12 +226,12 @@ class Qwen3DecoderLayer(nn.Module):
         self.input_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
 
-    def forward(self, hidden, residual, cos, sin, kv_pool, metadata, workspace=None):
+    def forward(self, hidden, residual, cos, sin, kv_pool, metadata, workspace=None, kv_out=None):
         """Pre-norm block in residual-stream form: takes the previous block's output and the
         residual before it (None for the first layer), returns the MLP output and the residual
         (the reference's hidden state is their sum, formed by the next norm's fused add)."""
         x, residual = self.input_layernorm(hidden, residual)
-        attn, present = self.self_attn(x, cos, sin, kv_pool, metadata, workspace)
+        attn, present = self.self_attn(x, cos, sin, kv_pool, metadata, workspace, kv_out)
         x, residual = self.post_attention_layernorm(attn, residual)
         return self.mlp(x), residual, present
 
@@ -318,8 +322,9 @@ class Qwen3Model(nn.Module):
         cos, sin = self.rotary_emb(position_ids, hidden.dtype)
         presents: list[PastKeyValue] = []
         residual = None
-        for layer, kv_pool in zip(self.layers, pools):
-            hidden, residual, present = layer(hidden, residual, cos, sin, kv_pool, metadata, workspace)
+        kv_outs = getattr(metadata, "kv_out", ()) or (None,) * len(self.layers)
+        for layer, kv_pool, kv_out in zip(self.layers, pools, kv_outs):
+            hidden, residual, present = layer(hidden, residual, cos, sin, kv_pool, metadata, workspace, kv_out)
             presents.append(present)
         if last_only and isinstance(metadata, PagedMixedMetadata):
             width, n = metadata.prefill_width, metadata.prefill_rows * metadata.prefill_width

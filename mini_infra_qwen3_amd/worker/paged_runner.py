@@ -75,6 +75,55 @@ class _DecodeGraph:
         self.static.copy_(torch.from_numpy(full))
 
 
+class _PrefillGraph:
+    """The chunked-prefill forward of one (rows, padded width W) bucket with history tables NB blocks
+    wide, captured over a static packed buffer ``[rows, 2 W + 2 + NB]`` in the ``pack_prefill_rows``
+    layout.  The
+    chunk K/V (the present) go to the runner's staging buffers, which every prefill graph shares, so
+    captured graphs hold no per-graph outputs beyond their logits."""
+
+    def __init__(self, model: torch.nn.Module, pool: PagedKVCachePool, rows: int, width: int, hist_blocks: int,
+                 staging: torch.Tensor, mempool, pad_token_id: int, device: torch.device):
+        self.rows, self.width, self.hist_blocks = rows, width, hist_blocks
+        self.pad_token_id = pad_token_id
+        self.static = torch.zeros((rows, 2 * width + 2 + hist_blocks), dtype=torch.long, device=device)
+        self.static[:, :width] = pad_token_id  # every row is an empty chunk until a step is loaded
+        ids, pos, meta = self.views()
+        tokens = rows * width
+        meta = meta._replace(kv_pools=tuple(pool.kv_pools),
+                             kv_out=tuple((staging[l, 0, :tokens], staging[l, 1, :tokens])
+                                          for l in range(staging.shape[0])))
+        side = torch.cuda.Stream(device)  # default priority
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side), torch.inference_mode():
+            for _ in range(2):  # warm-up outside the capture: GEMM choices, library state
+                model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
+        torch.cuda.current_stream(device).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, pool=mempool), torch.inference_mode():
+            logits, presents = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
+        self.logits = logits[:, -1]
+        self.presents = presents
+
+    def views(self):
+        s, w = self.static, self.width
+        return s[:, :w], s[:, w:2 * w], PagedPrefillMetadata(history_block_tables=s[:, 2 * w + 2:],
+                                                             start_lens=s[:, 2 * w], chunk_lens=s[:, 2 * w + 1])
+
+    def load(self, packed: np.ndarray, chunk_width: int) -> None:
+        """Copies a host-packed ``[rows, 2 L + 2 + nb]`` step in (L <= W, nb <= NB), widening the left
+        padding to W and null-padding the history tables."""
+        w, length = self.width, chunk_width
+        nb = packed.shape[1] - 2 * length - 2
+        full = np.zeros((self.rows, 2 * w + 2 + self.hist_blocks), dtype=np.int64)
+        full[:, :w - length] = self.pad_token_id
+        full[:, w - length:w] = packed[:, :length]
+        full[:, 2 * w - length:2 * w] = packed[:, length:2 * length]
+        full[:, 2 * w:2 * w + 2] = packed[:, 2 * length:2 * length + 2]
+        full[:, 2 * w + 2:2 * w + 2 + nb] = packed[:, 2 * length + 2:]
+        self.static.copy_(torch.from_numpy(full))
+
+
 class PagedDecodeOutput(NamedTuple):
     """Next token per row (input order) and the model time in ms."""
 
@@ -103,6 +152,9 @@ class PagedRunner(BaseModelRunner):
         self._batch_buckets: list[int] = []
         self._block_buckets: list[int] = []
         self._loaded: tuple[_DecodeGraph, int] | None = None
+        self._prefill_graphs: dict[tuple[int, int], _PrefillGraph] = {}
+        self._prefill_pool: PagedKVCachePool | None = None
+        self._width_quantum, self._hist_blocks = 1, 0
 
     def enable_decode_graphs(self, pool: PagedKVCachePool, max_batch: int, max_blocks: int,
                              batch_buckets: Sequence[int] | None = None, block_quantum: int = 16) -> None:
@@ -124,6 +176,37 @@ class PagedRunner(BaseModelRunner):
                 self._graphs[(b, nb)] = _DecodeGraph(self.model, pool, b, nb, self.device)
         torch.cuda.synchronize(self.device)
 
+    def enable_prefill_graphs(self, pool: PagedKVCachePool, max_rows: int, max_width: int, max_history_blocks: int,
+                              width_quantum: int = 128) -> None:
+        """Captures the chunked-prefill forward for 1..``max_rows`` rows and padded chunk widths in
+        multiples of ``width_quantum`` up to ``max_width``, over ``pool``.  Every graph takes history
+        tables ``max_history_blocks`` wide (null-padded; the kernel reads only the entries a row's
+        start covers, so the width costs nothing).  Steps outside the buckets, or on another pool,
+        run without a graph.  With graphs, a step's ``prefill_cache`` lives in buffers the next
+        graphed prefill step overwrites: store it first (as ``store_prefill`` right after the step
+        does)."""
+        if self.device.type != "cuda":
+            raise RuntimeError("prefill graphs need the GPU")
+        cfg = self.model.config
+        top_w = -(-max_width // width_quantum) * width_quantum
+        self._prefill_staging = torch.empty((cfg.num_hidden_layers, 2, max_rows * top_w, cfg.num_key_value_heads,
+                                             cfg.head_dim), dtype=pool.storage.dtype, device=self.device)
+        mempool = torch.cuda.graph_pool_handle()
+        self._prefill_pool = pool
+        self._width_quantum, self._hist_blocks = width_quantum, max(int(max_history_blocks), 0)
+        self._prefill_graphs = {}
+        for rows in range(1, max_rows + 1):
+            for width in range(width_quantum, top_w + 1, width_quantum):
+                self._prefill_graphs[(rows, width)] = _PrefillGraph(
+                    self.model, pool, rows, width, self._hist_blocks, self._prefill_staging, mempool,
+                    self.pad_token_id, self.device)
+        torch.cuda.synchronize(self.device)
+
+    def _prefill_bucket(self, rows: int, width: int, blocks: int) -> _PrefillGraph | None:
+        if blocks > self._hist_blocks:
+            return None
+        return self._prefill_graphs.get((rows, -(-width // self._width_quantum) * self._width_quantum))
+
     def _bucket(self, rows: int, blocks: int) -> _DecodeGraph | None:
         b = next((x for x in self._batch_buckets if x >= rows), None)
         nb = next((x for x in self._block_buckets if x >= blocks), None)
@@ -143,9 +226,18 @@ class PagedRunner(BaseModelRunner):
         first ``start`` slots are visible (reference paged_runner.py:32-102).  next_tokens holds the greedy
         token after each row's last position (meaningful where the chunk completes the prompt).
         """
-        packed = torch.from_numpy(pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size,
-                                                    self.pad_token_id)).to(self.device)
+        rows = pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size, self.pad_token_id)
         width = max(len(c) for c in chunk_token_ids)
+        graph = None
+        if self._prefill_graphs and pool is self._prefill_pool:
+            graph = self._prefill_bucket(rows.shape[0], width, rows.shape[1] - 2 * width - 2)
+        if graph is not None:
+            graph.load(rows, width)
+            with StepTimer(self.device) as timer:
+                graph.graph.replay()
+                next_token = argmax_rows(graph.logits)
+            return PrefillOutput(next_token.tolist(), KVCache(graph.presents), timer.elapsed_ms)
+        packed = torch.from_numpy(rows).to(self.device)
         input_ids = packed[:, :width]
         position_ids = packed[:, width:2 * width]
         metadata = PagedPrefillMetadata(

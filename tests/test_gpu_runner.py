@@ -380,3 +380,57 @@ def test_decode_graph_replays_match_eager_forward_and_touch_only_live_slots(mode
                 tokens[i].append(t)
                 lengths[i] += 1
     assert replays == len(schedule)
+
+
+def test_prefill_graph_replays_match_eager_forward(models):
+    """Prefill graphs: each replay equals an eager forward of the same padded inputs, bit for bit
+    (logits and the chunk K/V), with eager work and syncs between replays, across row counts, widths
+    and history buckets; the tokens and stored K/V equal the eager runner's (which pads the chunk to
+    its own width, so values agree to rounding) and the CPU oracle's tokens."""
+    model, _, ref_cpu = models
+    cfg = model.config
+    prompts = prompts_of([150, 90, 60, 200, 300], seed=12)
+    manager = KVCacheManager(BS, num_blocks=64)
+    pools = [make_pool(cfg, 64), make_pool(cfg, 64)]  # graphed, eager
+    cpu_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128)
+    graphed, eager_runner = PagedRunner(model), PagedRunner(model)
+    graphed.enable_prefill_graphs(pools[0], max_rows=2, max_width=256, max_history_blocks=16)
+    assert len(graphed._prefill_graphs) == 2 * 2
+    for i, p in enumerate(prompts):
+        manager.allocate_slots(i, len(p))
+    tables = [manager.block_table(i) for i in range(5)]
+    # (requests, chunk starts, chunk ends): no history, two rows, two rows with history, the first
+    # bucket again, a history of 100 tokens (7 blocks), and a chunk too wide for the buckets (eager)
+    steps = [([0], [0], [70]), ([1, 2], [0, 0], [40, 60]), ([0, 1], [70, 40], [150, 90]), ([3], [0], [100]),
+             ([3], [100], [200]), ([4], [0], [300])]
+    replays = 0
+    with torch.inference_mode():
+        for reqs, starts, ends in steps:
+            chunks = [prompts[r][s:e] for r, s, e in zip(reqs, starts, ends)]
+            tabs = [tables[r] for r in reqs]
+            lens = [e - s for s, e in zip(starts, ends)]
+            got = graphed.run_prefill_chunk_step(chunks, starts, tabs, pools[0])
+            graph = graphed._prefill_bucket(len(reqs), max(lens), -(-max(starts) // BS))
+            if graph is not None:
+                replays += 1
+                ids, pos, meta = graph.views()
+                logits = graph.logits.clone()
+                present = [(k.clone(), v.clone()) for k, v in got.prefill_cache]
+                eager, eager_present = model(ids, position_ids=pos, last_logits_only=True,
+                                             attn_metadata=meta._replace(kv_pools=tuple(pools[0].kv_pools)))
+                torch.cuda.synchronize()
+                assert torch.equal(logits, eager[:, -1]), f"replay {replays} differs from the eager forward"
+                for (k, v), (ek, ev) in zip(present, eager_present):
+                    assert torch.equal(k, ek) and torch.equal(v, ev)
+            want = eager_runner.run_prefill_chunk_step(chunks, starts, tabs, pools[1])
+            graphed.store_prefill(pools[0], got.prefill_cache, tabs, lens, starts)
+            eager_runner.store_prefill(pools[1], want.prefill_cache, tabs, lens, starts)
+            toks, presents = qwen3_ref.prefill_chunk_step(ref_cpu, chunks, starts, tabs, cpu_pools, BS)
+            qwen3_ref.store_prefill(cpu_pools, presents, tabs, lens, starts, BS)
+            assert got.next_tokens == want.next_tokens == toks
+    assert replays == 5
+    for r, p in enumerate(prompts):
+        for layer in range(cfg.num_hidden_layers):
+            for kv in range(2):
+                assert_kv_close(layer, request_kv(pools[0], layer, tables[r], len(p))[kv],
+                                request_kv(pools[1], layer, tables[r], len(p))[kv])
