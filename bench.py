@@ -402,7 +402,8 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False) -> dict:
     is replayed from HIP graphs captured per padded (batch, blocks) bucket, and the prefill forward
     of one or two chunks per padded (rows, width, history) bucket, when the backend is set up
     (``setup_s``, outside the timed run).  ``mixed``: decode rows ride in the prefill steps (the
-    mixed batching the reference plans) instead of the reference's alternating prefill / decode."""
+    mixed batching the reference plans) instead of the reference's alternating prefill / decode,
+    with mixed steps of one or two chunks and up to 32 decode rows replayed from graphs too."""
     from mini_infra_qwen3_amd.core.scheduler import SchedulePhase
     from mini_infra_qwen3_amd.engine import PagedScheduleBackend, run_scheduler
     from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
@@ -414,7 +415,8 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False) -> dict:
 
     def run(requests):
         t0 = time.perf_counter()
-        backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True, prefill_graphs=True)
+        backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True, prefill_graphs=True,
+                                       mixed_graphs=mixed)
         setup_s = time.perf_counter() - t0
         return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False,
                              mixed_batching=mixed), setup_s

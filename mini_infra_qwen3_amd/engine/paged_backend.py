@@ -41,11 +41,14 @@ class PagedScheduleBackend:
 
     def __init__(self, model: torch.nn.Module, requests: Sequence[Request], max_running_requests: int,
                  paged_cache_config: PagedCacheConfig = PagedCacheConfig(), pad_token_id: int = 0,
-                 decode_graphs: bool = False, prefill_graphs: bool = False, prefill_graph_rows: int = 4):
+                 decode_graphs: bool = False, prefill_graphs: bool = False, prefill_graph_rows: int = 4,
+                 mixed_graphs: bool = False, mixed_graph_rows: int = 2, mixed_graph_decode_rows: int = 32):
         """``decode_graphs``: capture the decode forward in HIP graphs for every padded (batch, blocks)
         bucket this run can reach, before the run (as serving engines do at start-up).
         ``prefill_graphs``: likewise the chunked-prefill forward of up to ``prefill_graph_rows`` chunks,
-        for widths up to the longest prompt and histories up to its blocks."""
+        for widths up to the longest prompt and histories up to its blocks.  ``mixed_graphs``: the
+        mixed-step forward of up to ``mixed_graph_rows`` chunks with up to ``mixed_graph_decode_rows``
+        decode rows."""
         self.model = model
         self.device = next(model.parameters()).device
         self.block_size = paged_cache_config.block_size
@@ -64,8 +67,13 @@ class PagedScheduleBackend:
         if decode_graphs:
             self.runner.enable_decode_graphs(self.pool, max_batch=min(max_running_requests, len(requests)),
                                              max_blocks=largest)
+        longest = max(r.prompt_len for r in requests)
+        if mixed_graphs:
+            self.runner.enable_mixed_graphs(
+                self.pool, max_rows=min(mixed_graph_rows, max_running_requests), max_width=longest,
+                max_decode_rows=min(mixed_graph_decode_rows, max_running_requests, len(requests)),
+                max_history_blocks=num_blocks_for_tokens(longest, self.block_size), max_decode_blocks=largest)
         if prefill_graphs:
-            longest = max(r.prompt_len for r in requests)
             self.runner.enable_prefill_graphs(self.pool, max_rows=min(prefill_graph_rows, max_running_requests),
                                               max_width=longest,
                                               max_history_blocks=num_blocks_for_tokens(longest, self.block_size))

@@ -153,7 +153,7 @@ class Qwen3Attention(nn.Module):
         key_pool, value_pool = kv_pool
         eps = self.q_norm.eps
         if isinstance(metadata, PagedMixedMetadata):
-            return self._mixed(q[0], k[0], v[0], cos[0], sin[0], kv_pool, metadata, workspace)
+            return self._mixed(q[0], k[0], v[0], cos[0], sin[0], kv_pool, metadata, workspace, kv_out)
         if isinstance(metadata, PagedAttentionMetadata):
             q_rot, _, _ = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin, eps,
                                                   slot_mapping=metadata.slot_mapping, key_pool=key_pool,
@@ -178,7 +178,7 @@ class Qwen3Attention(nn.Module):
             present = (k_rot, v_rows)
         return self.o_proj(out), present
 
-    def _mixed(self, q, k, v, cos, sin, kv_pool: PastKeyValue, metadata: PagedMixedMetadata, workspace):
+    def _mixed(self, q, k, v, cos, sin, kv_pool: PastKeyValue, metadata: PagedMixedMetadata, workspace, kv_out=None):
         """Token rows ``[0, P L)`` take the prefill path, the rest the decode path (its K/V append
         first, so decode attention sees the new token); both attentions write one ``[T, H D]`` buffer."""
         key_pool, value_pool = kv_pool
@@ -189,8 +189,9 @@ class Qwen3Attention(nn.Module):
         q_dec, _, _ = data_plane.qk_norm_rope(q[n:], k[n:], v[n:], self.q_norm.weight, self.k_norm.weight, cos[n:],
                                               sin[n:], eps, slot_mapping=metadata.decode.slot_mapping,
                                               key_pool=key_pool, value_pool=value_pool)
+        k_buf, v_buf = kv_out if kv_out is not None else (None, None)
         q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q[:n], k[:n], v[:n], self.q_norm.weight, self.k_norm.weight,
-                                                       cos[:n], sin[:n], eps)
+                                                       cos[:n], sin[:n], eps, k_out=k_buf, v_out=v_buf)
         q_rot = q_rot.view(rows, width, self.num_heads, self.head_dim).transpose(1, 2)
         k_rot = k_rot.view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
         v_rows = v_rows.view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
@@ -322,7 +323,8 @@ class Qwen3Model(nn.Module):
         cos, sin = self.rotary_emb(position_ids, hidden.dtype)
         presents: list[PastKeyValue] = []
         residual = None
-        kv_outs = getattr(metadata, "kv_out", ()) or (None,) * len(self.layers)
+        holder = metadata.prefill if isinstance(metadata, PagedMixedMetadata) else metadata
+        kv_outs = getattr(holder, "kv_out", ()) or (None,) * len(self.layers)
         for layer, kv_pool, kv_out in zip(self.layers, pools, kv_outs):
             hidden, residual, present = layer(hidden, residual, cos, sin, kv_pool, metadata, workspace, kv_out)
             presents.append(present)

@@ -124,6 +124,83 @@ class _PrefillGraph:
         self.static.copy_(torch.from_numpy(full))
 
 
+class _MixedGraph:
+    """A mixed step's forward for one (chunk rows P, padded width W, decode rows D) bucket, with
+    history tables NB and decode tables MB blocks wide, captured over a static buffer in the
+    ``pack_mixed_rows`` layout; chunk K/V go to the shared staging buffers.  Pad decode rows carry
+    slot -1 (no append) and context 0 (zero output)."""
+
+    def __init__(self, model: torch.nn.Module, pool: PagedKVCachePool, rows: int, width: int, decode_rows: int,
+                 hist_blocks: int, decode_blocks: int, staging: torch.Tensor, mempool, pad_token_id: int,
+                 device: torch.device):
+        self.rows, self.width, self.decode_rows = rows, width, decode_rows
+        self.hist_blocks, self.decode_blocks = hist_blocks, decode_blocks
+        self.pad_token_id = pad_token_id
+        self.tokens = rows * width + decode_rows
+        self.static = torch.from_numpy(self._empty()).to(device)
+        ids, pos, meta = self.views()
+        n = rows * width
+        meta = meta._replace(kv_pools=tuple(pool.kv_pools),
+                             prefill=meta.prefill._replace(kv_out=tuple((staging[l, 0, :n], staging[l, 1, :n])
+                                                                        for l in range(staging.shape[0]))))
+        side = torch.cuda.Stream(device)  # default priority
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side), torch.inference_mode():
+            for _ in range(2):  # warm-up outside the capture: GEMM choices, library state
+                model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
+        torch.cuda.current_stream(device).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, pool=mempool), torch.inference_mode():
+            logits, presents = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
+        self.logits = logits[:, -1]
+        self.presents = presents
+        self.static_slots_ptr = self.views()[2].decode.slot_mapping.data_ptr()
+
+    def _empty(self) -> np.ndarray:
+        t, n = self.tokens, self.rows * self.width
+        full = np.zeros(2 * t + self.rows * (2 + self.hist_blocks) + self.decode_rows * (2 + self.decode_blocks),
+                        dtype=np.int64)
+        full[:n] = self.pad_token_id
+        full[n:t] = self.pad_token_id
+        dec = full[2 * t + self.rows * (2 + self.hist_blocks):].reshape(self.decode_rows, 2 + self.decode_blocks)
+        dec[:, 0] = -1
+        return full
+
+    def views(self):
+        s, t = self.static, self.tokens
+        at = 2 * t + self.rows * (2 + self.hist_blocks)
+        chunk = s[2 * t:at].view(self.rows, 2 + self.hist_blocks)
+        dec = s[at:].view(self.decode_rows, 2 + self.decode_blocks)
+        meta = PagedMixedMetadata(
+            prefill=PagedPrefillMetadata(history_block_tables=chunk[:, 2:], start_lens=chunk[:, 0],
+                                         chunk_lens=chunk[:, 1]),
+            decode=PagedAttentionMetadata(slot_mapping=dec[:, 0], block_tables=dec[:, 2:], context_lens=dec[:, 1]),
+            prefill_rows=self.rows, prefill_width=self.width)
+        return s[:t].view(1, t), s[t:2 * t].view(1, t), meta
+
+    def load(self, prefill: np.ndarray, chunk_width: int, decode: np.ndarray) -> None:
+        """Copies host-packed chunk rows (``pack_prefill_rows``, width L <= W, nb <= NB) and decode rows
+        (``pack_decode_rows``, d <= D rows, mb <= MB blocks) into the bucket's layout."""
+        full = self._empty()
+        t, w, length = self.tokens, self.width, chunk_width
+        n = self.rows * w
+        ids, pos = full[:n].reshape(self.rows, w), full[t:t + n].reshape(self.rows, w)
+        ids[:, w - length:] = prefill[:, :length]
+        pos[:, w - length:] = prefill[:, length:2 * length]
+        d = decode.shape[0]
+        full[n:n + d] = decode[:, 0]
+        full[t + n:t + n + d] = decode[:, 1]
+        at = 2 * t + self.rows * (2 + self.hist_blocks)
+        chunk = full[2 * t:at].reshape(self.rows, 2 + self.hist_blocks)
+        nb = prefill.shape[1] - 2 * length - 2
+        chunk[:, :2] = prefill[:, 2 * length:2 * length + 2]
+        chunk[:, 2:2 + nb] = prefill[:, 2 * length + 2:]
+        dec = full[at:].reshape(self.decode_rows, 2 + self.decode_blocks)
+        dec[:d, :2] = decode[:, 2:4]
+        dec[:d, 2:2 + decode.shape[1] - 4] = decode[:, 4:]
+        self.static.copy_(torch.from_numpy(full))
+
+
 class PagedDecodeOutput(NamedTuple):
     """Next token per row (input order) and the model time in ms."""
 
@@ -155,6 +232,23 @@ class PagedRunner(BaseModelRunner):
         self._prefill_graphs: dict[tuple[int, int], _PrefillGraph] = {}
         self._prefill_pool: PagedKVCachePool | None = None
         self._width_quantum, self._hist_blocks = 1, 0
+        self._mixed_graphs: dict[tuple[int, int, int], _MixedGraph] = {}
+        self._mixed_pool: PagedKVCachePool | None = None
+        self._mixed_loaded: tuple[_MixedGraph, int] | None = None
+        self._decode_row_buckets: list[int] = []
+        self._staging: torch.Tensor | None = None
+        self._mempool = None
+
+    def _shared_staging(self, tokens: int, pool: PagedKVCachePool) -> torch.Tensor:
+        """Chunk K/V staging ``[layers, 2, tokens, H_kv, D]`` shared by the prefill and mixed graphs
+        (a larger request allocates a new one; graphs captured earlier keep theirs alive)."""
+        if self._staging is None or self._staging.shape[2] < tokens:
+            cfg = self.model.config
+            self._staging = torch.empty((cfg.num_hidden_layers, 2, tokens, cfg.num_key_value_heads, cfg.head_dim),
+                                        dtype=pool.storage.dtype, device=self.device)
+        if self._mempool is None:
+            self._mempool = torch.cuda.graph_pool_handle()
+        return self._staging
 
     def enable_decode_graphs(self, pool: PagedKVCachePool, max_batch: int, max_blocks: int,
                              batch_buckets: Sequence[int] | None = None, block_quantum: int = 16) -> None:
@@ -187,20 +281,53 @@ class PagedRunner(BaseModelRunner):
         does)."""
         if self.device.type != "cuda":
             raise RuntimeError("prefill graphs need the GPU")
-        cfg = self.model.config
         top_w = -(-max_width // width_quantum) * width_quantum
-        self._prefill_staging = torch.empty((cfg.num_hidden_layers, 2, max_rows * top_w, cfg.num_key_value_heads,
-                                             cfg.head_dim), dtype=pool.storage.dtype, device=self.device)
-        mempool = torch.cuda.graph_pool_handle()
+        staging = self._shared_staging(max_rows * top_w, pool)
         self._prefill_pool = pool
         self._width_quantum, self._hist_blocks = width_quantum, max(int(max_history_blocks), 0)
         self._prefill_graphs = {}
         for rows in range(1, max_rows + 1):
             for width in range(width_quantum, top_w + 1, width_quantum):
                 self._prefill_graphs[(rows, width)] = _PrefillGraph(
-                    self.model, pool, rows, width, self._hist_blocks, self._prefill_staging, mempool,
-                    self.pad_token_id, self.device)
+                    self.model, pool, rows, width, self._hist_blocks, staging, self._mempool, self.pad_token_id,
+                    self.device)
         torch.cuda.synchronize(self.device)
+
+    def enable_mixed_graphs(self, pool: PagedKVCachePool, max_rows: int, max_width: int, max_decode_rows: int,
+                            max_history_blocks: int, max_decode_blocks: int, width_quantum: int = 128,
+                            decode_row_buckets: Sequence[int] | None = None) -> None:
+        """Captures the mixed-step forward for 1..``max_rows`` chunk rows, padded widths in multiples of
+        ``width_quantum`` up to ``max_width`` and decode-row buckets up to ``max_decode_rows`` (pad
+        rows append nothing), with history / decode tables ``max_history_blocks`` /
+        ``max_decode_blocks`` wide, over ``pool``.  Other steps run without a graph; as with prefill
+        graphs, store a step's ``prefill_cache`` before the next graphed step."""
+        if self.device.type != "cuda":
+            raise RuntimeError("mixed graphs need the GPU")
+        if decode_row_buckets is None:
+            decode_row_buckets = [b for b in (1, 2, 4, 8, 16, 32, 64, 128, 256) if b < max_decode_rows]
+            decode_row_buckets.append(max_decode_rows)
+        self._decode_row_buckets = sorted(set(int(b) for b in decode_row_buckets if 0 < b <= max_decode_rows))
+        top_w = -(-max_width // width_quantum) * width_quantum
+        staging = self._shared_staging(max_rows * top_w, pool)
+        self._mixed_pool = pool
+        self._mixed_quantum = width_quantum
+        self._mixed_tables = (max(int(max_history_blocks), 0), max(int(max_decode_blocks), 1))
+        self._mixed_graphs = {}
+        for rows in range(1, max_rows + 1):
+            for width in range(width_quantum, top_w + 1, width_quantum):
+                for d in self._decode_row_buckets:
+                    self._mixed_graphs[(rows, width, d)] = _MixedGraph(
+                        self.model, pool, rows, width, d, *self._mixed_tables, staging, self._mempool,
+                        self.pad_token_id, self.device)
+        torch.cuda.synchronize(self.device)
+
+    def _mixed_bucket(self, rows: int, width: int, hist_blocks: int, decode_rows: int,
+                      decode_blocks: int) -> _MixedGraph | None:
+        if not self._mixed_graphs or hist_blocks > self._mixed_tables[0] or decode_blocks > self._mixed_tables[1]:
+            return None
+        d = next((b for b in self._decode_row_buckets if b >= decode_rows), None)
+        w = -(-width // self._mixed_quantum) * self._mixed_quantum
+        return None if d is None else self._mixed_graphs.get((rows, w, d))
 
     def _prefill_bucket(self, rows: int, width: int, blocks: int) -> _PrefillGraph | None:
         if blocks > self._hist_blocks:
@@ -326,6 +453,19 @@ class PagedRunner(BaseModelRunner):
         """Packs a mixed step -- chunk rows as ``run_prefill_chunk_step`` takes them, decode rows as
         ``prepare_decode_inputs`` does -- into one int64 buffer with one upload.  Returns input_ids /
         position_ids ``[1, P L + D]`` and the metadata, all views of that buffer."""
+        self._mixed_loaded = None
+        if self._mixed_graphs and pool is self._mixed_pool:
+            prefill = pack_prefill_rows(chunk_token_ids, start_positions, prefill_block_tables, pool.block_size,
+                                        self.pad_token_id)
+            decode = pack_decode_rows(decode_block_tables, last_tokens, positions, pool.block_size)
+            width = max(len(c) for c in chunk_token_ids)
+            graph = self._mixed_bucket(prefill.shape[0], width, prefill.shape[1] - 2 * width - 2, decode.shape[0],
+                                       decode.shape[1] - 4)
+            if graph is not None:
+                graph.load(prefill, width, decode)
+                self._mixed_loaded = (graph, decode.shape[0])
+                ids, pos, meta = graph.views()
+                return ids, pos, meta._replace(kv_pools=tuple(pool.kv_pools))
         flat, (rows, width, nb, decode_rows, mb) = pack_mixed_rows(
             chunk_token_ids, start_positions, prefill_block_tables, last_tokens, positions, decode_block_tables,
             pool.block_size, self.pad_token_id)
@@ -347,7 +487,17 @@ class PagedRunner(BaseModelRunner):
     def run_mixed_step(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
                        metadata: PagedMixedMetadata) -> MixedStepOutput:
         """One forward over the chunks and the decode tokens: the decode rows' K/V go into the pool,
-        the chunks' K/V come back as ``prefill_cache``; greedy tokens of both."""
+        the chunks' K/V come back as ``prefill_cache``; greedy tokens of both.  Inputs that
+        ``prepare_mixed_inputs`` loaded into a captured bucket replay its graph."""
+        loaded = self._mixed_loaded
+        if loaded is not None and metadata.decode.slot_mapping.data_ptr() == loaded[0].static_slots_ptr:
+            graph, live = loaded
+            with StepTimer(self.device) as timer:
+                graph.graph.replay()
+                next_token = argmax_rows(graph.logits)
+            tokens = next_token.tolist()
+            return MixedStepOutput(tokens[:graph.rows], tokens[graph.rows:graph.rows + live], KVCache(graph.presents),
+                                   timer.elapsed_ms)
         with StepTimer(self.device) as timer:
             logits, present = self.model(input_ids, position_ids=position_ids, attn_metadata=metadata,
                                          last_logits_only=True)

@@ -56,12 +56,13 @@ def requests():
                                                            (None, True, True)],
                          ids=["benchmark_model_graphs", "context_dependent_model", "mixed_batching"])
 def test_tokens_are_oracle_greedy_choices(requests, untied_head_seed, graphs, mixed):
-    """``graphs``: decode and prefill steps replay HIP graphs.  ``mixed_batching``: decode rows and
+    """``graphs``: decode, prefill (and mixed) steps replay HIP graphs.  ``mixed_batching``: decode rows and
     prefill chunks share steps (the oracle runs a mixed step as the decode step and the chunk step
     it consists of)."""
     model, ref = build(untied_head_seed)
     mrr, budget = 8, 256
-    backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=graphs, prefill_graphs=graphs)
+    backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=graphs, prefill_graphs=graphs,
+                                   mixed_graphs=graphs and mixed)
     product = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
                             stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed)
     chunk_steps = product.num_steps(SchedulePhase.PREFILL) + product.num_steps(SchedulePhase.MIXED)

@@ -434,3 +434,72 @@ def test_prefill_graph_replays_match_eager_forward(models):
             for kv in range(2):
                 assert_kv_close(layer, request_kv(pools[0], layer, tables[r], len(p))[kv],
                                 request_kv(pools[1], layer, tables[r], len(p))[kv])
+
+
+def test_mixed_graph_replays_match_eager_forward(models):
+    """Mixed graphs: each replay equals an eager forward of the same padded inputs, bit for bit
+    (logits and chunk K/V), across chunk-row and decode-row buckets (pad decode rows write nothing);
+    tokens equal the eager runner's unpadded mixed step and the CPU oracle's, stored K/V agree."""
+    model, _, ref_cpu = models
+    cfg = model.config
+    decoders = prompts_of([45, 17, 3], seed=8)
+    chunked = prompts_of([70, 20, 50], seed=9)
+    pools = [make_pool(cfg, 64), make_pool(cfg, 64)]  # graphed, eager
+    cpu_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128)
+    manager = KVCacheManager(BS, num_blocks=64)
+    graphed, eager_runner = PagedRunner(model), PagedRunner(model)
+    graphed.enable_mixed_graphs(pools[0], max_rows=2, max_width=128, max_decode_rows=4, max_history_blocks=8,
+                                max_decode_blocks=8, decode_row_buckets=[2, 4])
+    assert len(graphed._mixed_graphs) == 2 * 1 * 2
+    for i, p in enumerate(decoders + chunked):
+        manager.allocate_slots(i, len(p))
+    tables = [manager.block_table(i) for i in range(6)]
+    with torch.inference_mode():
+        for pool, runner in zip(pools, (graphed, eager_runner)):
+            out = runner.run_prefill_step(decoders)
+            runner.store_prefill(pool, out.prefill_cache, tables[:3], [len(p) for p in decoders], [0] * 3)
+    _, presents = qwen3_ref.prefill(ref_cpu, decoders)
+    qwen3_ref.store_prefill(cpu_pools, presents, tables[:3], [len(p) for p in decoders], [0] * 3, BS)
+    last, positions = list(out.next_tokens), [len(p) for p in decoders]
+    # (chunks as (chunked request, start, end), decoding requests)
+    steps = [([(0, 0, 30)], [0, 1, 2]), ([(0, 30, 70), (1, 0, 20)], [0, 1, 2]), ([(2, 0, 50)], [0, 2])]
+    with torch.inference_mode():
+        for chunks, dec in steps:
+            for i in dec:
+                assert manager.allocate_slots(i, 1)
+            dec_tables = [manager.block_table(i) for i in dec]
+            chunk_ids = [chunked[c][a:b] for c, a, b in chunks]
+            starts, lens = [a for _, a, _ in chunks], [b - a for _, a, b in chunks]
+            pf_tables = [tables[3 + c] for c, _, _ in chunks]
+            results = []
+            for pool, runner in zip(pools, (graphed, eager_runner)):
+                ids, pos, meta = runner.prepare_mixed_inputs(chunk_ids, starts, pf_tables, [last[i] for i in dec],
+                                                             [positions[i] for i in dec], dec_tables, pool)
+                if runner is graphed:
+                    graph = runner._mixed_loaded[0]
+                    assert graph.rows == len(chunks) and graph.decode_rows >= len(dec)
+                    eager, eager_present = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
+                    torch.cuda.synchronize()
+                got = runner.run_mixed_step(ids, pos, meta)
+                if runner is graphed:
+                    assert torch.equal(graph.logits, eager[:, -1])
+                    for (k, v), (ek, ev) in zip(got.prefill_cache, eager_present):
+                        assert torch.equal(k, ek) and torch.equal(v, ev)
+                runner.store_prefill(pool, got.prefill_cache, pf_tables, lens, starts)
+                results.append(got)
+            want_dec = qwen3_ref.decode_step(ref_cpu, dec_tables, [last[i] for i in dec], [positions[i] for i in dec],
+                                             cpu_pools, BS)
+            want_pf, presents = qwen3_ref.prefill_chunk_step(ref_cpu, chunk_ids, starts, pf_tables, cpu_pools, BS)
+            qwen3_ref.store_prefill(cpu_pools, presents, pf_tables, lens, starts, BS)
+            assert results[0].decode_next_tokens == results[1].decode_next_tokens == want_dec.argmax(-1).tolist()
+            done = [k for k, (c, _, b) in enumerate(chunks) if b == len(chunked[c])]
+            assert [results[0].prefill_next_tokens[k] for k in done] == \
+                [results[1].prefill_next_tokens[k] for k in done] == [want_pf[k] for k in done]
+            for i, t in zip(dec, results[0].decode_next_tokens):
+                last[i], positions[i] = t, positions[i] + 1
+    for r in range(6):
+        length = positions[r] if r < 3 else len(chunked[r - 3])
+        for layer in range(cfg.num_hidden_layers):
+            for kv in range(2):
+                assert_kv_close(layer, request_kv(pools[0], layer, tables[r], length)[kv],
+                                request_kv(pools[1], layer, tables[r], length)[kv])
