@@ -145,6 +145,28 @@ int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, const void*
                                   float scale, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * mi_paged_decode_attention_fused -- mi_qk_norm_rope's decode form (q/k RMSNorm + RoPE of the new
+ * tokens, K/V rows into their slots: qwen3.py:182-217 with _apply_paged_kv_pool's append :282-283)
+ * followed by mi_paged_decode_attention (qwen3.py:219-292), with the same results bit for bit.
+ * Where the per-sequence kernel serves the launch (batch * num_kv_heads <= CUs, max_blocks <= 512)
+ * it is one launch whose workgroups rotate their own q heads and append their own K/V head;
+ * otherwise it runs the two entry points, rotating q into q_scratch.
+ * q: [batch] rows of num_heads * 128 (q_row_stride), k / v: rows of num_kv_heads * 128;
+ * cos / sin: [batch, 128]; q_scratch: [batch, num_heads, 128] bf16 (always required).
+ * The remaining arguments are those of mi_qk_norm_rope and mi_paged_decode_attention.
+ */
+int32_t mi_paged_decode_attention_fused(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
+                                        const void* k, int64_t k_row_stride, const void* v, int64_t v_row_stride,
+                                        const void* q_weight, const void* k_weight, const void* cos,
+                                        const void* sin, float eps, const int64_t* slot_mapping,
+                                        int64_t slot_stride, void* key_pool, void* value_pool, int64_t num_blocks,
+                                        const int64_t* block_tables, int64_t block_table_stride,
+                                        int32_t max_blocks, const int64_t* context_lens,
+                                        int64_t context_lens_stride, int32_t batch, int32_t num_heads,
+                                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                                        void* q_scratch, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Kernel 4 -- chunked-prefill attention on MFMA with the history read from the pool.
  *
  * Replaces, for one layer of PagedRunner.run_prefill_chunk_step

@@ -137,16 +137,8 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(const QkArgs a) 
     if (slot < 0 || slot >= a.num_slots) slot = -1;
   }
   const uint16_t* src = is_q ? a.q + t * a.q_stride + h * 128 : a.k + t * a.k_stride + h * 128;
-  const uint16_t* w = is_q ? a.q_weight : a.k_weight;
-  const float x0 = bf16_to_f32(src[lane]), x1 = bf16_to_f32(src[lane + 64]);
-  const float r = rsqrtf(wave_sum(x0 * x0 + x1 * x1) * (1.0f / 128.0f) + a.eps);
-  const float y0 = round_bf16(bf16_to_f32(w[lane]) * round_bf16(x0 * r));
-  const float y1 = round_bf16(bf16_to_f32(w[lane + 64]) * round_bf16(x1 * r));
-  const uint16_t* c = a.cos + t * 128;
-  const uint16_t* s = a.sin + t * 128;
-  // element l:      x*cos - x[l+64]*sin ; element l+64: x*cos + x[l]*sin  (rotate_half = cat(-x2, x1))
-  const float o0 = round_bf16(y0 * bf16_to_f32(c[lane])) + round_bf16(-y1 * bf16_to_f32(s[lane]));
-  const float o1 = round_bf16(y1 * bf16_to_f32(c[lane + 64])) + round_bf16(y0 * bf16_to_f32(s[lane + 64]));
+  float o0, o1;
+  norm_rope_head(src, is_q ? a.q_weight : a.k_weight, a.cos + t * 128, a.sin + t * 128, a.eps, lane, o0, o1);
   uint16_t* dst;
   if (is_q) {
     dst = a.q_out + (t * a.q_heads + h) * 128;

@@ -66,5 +66,30 @@ __device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(f3
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
+
+// ------------------------------------------------------- q/k norm + RoPE ---
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Per-head RMSNorm + RoPE of one 128-wide q or k head by one wavefront, with the reference's bf16
+// rounding points (src/mini_infra/model/qwen3.py:67-78 on the head, then _apply_rotary_embedding
+// :111-145): n = bf16(x * rsqrt(mean(x^2) + eps)), y = bf16(w * n),
+// out = bf16(bf16(y * cos) + bf16(rotate_half(y) * sin)).  Lane l owns elements l and l + 64, the
+// pair rotate_half couples, so the rotation is lane-local; o0 / o1 are elements l / l + 64 (exact
+// bf16 values held in fp32).
+__device__ __forceinline__ void norm_rope_head(const uint16_t* src, const uint16_t* weight, const uint16_t* cos,
+                                               const uint16_t* sin, float eps, int lane, float& o0, float& o1) {
+  const float x0 = bf16_bits_to_f32(src[lane]), x1 = bf16_bits_to_f32(src[lane + 64]);
+  const float r = rsqrtf(wave_sum64(x0 * x0 + x1 * x1) * (1.0f / 128.0f) + eps);
+  const float y0 = round_bf16(bf16_bits_to_f32(weight[lane]) * round_bf16(x0 * r));
+  const float y1 = round_bf16(bf16_bits_to_f32(weight[lane + 64]) * round_bf16(x1 * r));
+  // element l:      y*cos - y[l+64]*sin ; element l+64: y*cos + y[l]*sin  (rotate_half = cat(-y2, y1))
+  o0 = round_bf16(round_bf16(y0 * bf16_bits_to_f32(cos[lane])) + round_bf16(-y1 * bf16_bits_to_f32(sin[lane])));
+  o1 = round_bf16(round_bf16(y1 * bf16_bits_to_f32(cos[lane + 64])) + round_bf16(y0 * bf16_bits_to_f32(sin[lane + 64])));
+}
 
 }  // namespace mi

@@ -98,6 +98,20 @@ struct DecodeArgs {
   float scale;                     // softmax scale (natural units)
   float* ws_acc;                   // [streams, 2, heads, 128]: slot 0 = range's first (cut) sequence, 1 = last
   float* ws_ml;                    // [streams, 2, heads, 2] = (m, l) in log2 units
+  // Fused form of the per-sequence kernel: raw q / k / v projection rows of the new tokens, the
+  // q/k norm weights, cos / sin rows [batch, 128] and the slots of the new K/V rows.
+  const uint16_t* q_raw;
+  const uint16_t* k_raw;
+  const uint16_t* v_raw;
+  int64_t q_raw_row, k_raw_row, v_raw_row;  // elements
+  const uint16_t* q_weight;
+  const uint16_t* k_weight;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  const int64_t* slot_mapping;
+  int64_t slot_stride;
+  int64_t num_slots;
+  float eps;
 };
 
 __device__ __forceinline__ float dpp_sum16(float x) {
@@ -425,19 +439,53 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
 constexpr int kSeqWaves = MI_DECODE_SEQ_WAVES;
 constexpr int kSeqMaxBlocks = 64 * kSeqWaves;  // a lane holds one block id of its wavefront
 
-template <int kKvHeads>
+// kFused: the workgroup first does what mi_qk_norm_rope's decode form does for its heads --
+// wavefronts 0 and 1 normalise and rotate query heads 2 g and 2 g + 1 into LDS, wavefront 2 key
+// head g, which it writes with value head g into the sequence's new slot -- then attends.  The
+// barrier after the pool stores makes them visible to the workgroup's own loads of that block
+// (the slot's lines are not in the CU cache before: no other workgroup reads head g of this
+// sequence, and the cache starts every launch clean).
+template <int kKvHeads, bool kFused>
 __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const DecodeArgs a) {
   constexpr int kRowElems = kKvHeads * kHeadDim;
   constexpr int kBlockElems = kBlockSize * kRowElems;
   constexpr int kSeqDepth = MI_DECODE_SEQ_DEPTH;  // ring: the next kSeqDepth - 1 blocks of the wavefront in flight
   __shared__ float s_acc[kSeqWaves][kGroup][kHeadDim];
   __shared__ float s_ml[kSeqWaves][kGroup][2];
+  __shared__ __align__(16) uint16_t s_q[kFused ? kGroup : 1][kHeadDim];
   const int b = blockIdx.x;
   const int g = blockIdx.y;
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int dl = lane & 15;
   const int r = lane >> 4;
+  if constexpr (kFused) {
+    static_assert(kSeqWaves > kGroup, "the fused prologue needs kGroup + 1 wavefronts");
+    if (w <= kGroup) {  // wave-uniform
+      const bool is_q = w < kGroup;
+      const uint16_t* src = is_q ? a.q_raw + b * a.q_raw_row + (g * kGroup + w) * kHeadDim
+                                 : a.k_raw + b * a.k_raw_row + g * kHeadDim;
+      float o0, o1;
+      norm_rope_head(src, is_q ? a.q_weight : a.k_weight, a.cos + b * kHeadDim, a.sin + b * kHeadDim, a.eps, lane,
+                     o0, o1);
+      if (is_q) {
+        s_q[w][lane] = static_cast<uint16_t>(f32_to_bf16_bits(o0));
+        s_q[w][lane + 64] = static_cast<uint16_t>(f32_to_bf16_bits(o1));
+      } else {
+        const int64_t slot = a.slot_mapping[b * a.slot_stride];
+        if (slot >= 0 && slot < a.num_slots) {
+          uint16_t* kd = const_cast<uint16_t*>(a.key_pool) + (slot * kKvHeads + g) * kHeadDim;
+          uint16_t* vd = const_cast<uint16_t*>(a.value_pool) + (slot * kKvHeads + g) * kHeadDim;
+          const uint16_t* vs = a.v_raw + b * a.v_raw_row + g * kHeadDim;
+          kd[lane] = static_cast<uint16_t>(f32_to_bf16_bits(o0));
+          kd[lane + 64] = static_cast<uint16_t>(f32_to_bf16_bits(o1));
+          vd[lane] = vs[lane];
+          vd[lane + 64] = vs[lane + 64];
+        }
+      }
+    }
+    __syncthreads();
+  }
   const int n = static_cast<int>(context_of(a, b));
   const int nblk = blocks_of(n);
   uint16_t* out_b = a.out + b * a.out_row + (g * kGroup) * kHeadDim;  // query heads 2 g, 2 g + 1
@@ -457,9 +505,15 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
     id_lo = static_cast<uint32_t>(id);
     id_hi = static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32);
   }
-  const uint16_t* qp = a.query + b * a.q_row + (g * kGroup) * a.q_head + 8 * dl;
-  const uint4 q0 = *reinterpret_cast<const uint4*>(qp);
-  const uint4 q1 = *reinterpret_cast<const uint4*>(qp + a.q_head);
+  uint4 q0, q1;
+  if constexpr (kFused) {
+    q0 = *reinterpret_cast<const uint4*>(&s_q[0][8 * dl]);
+    q1 = *reinterpret_cast<const uint4*>(&s_q[1][8 * dl]);
+  } else {
+    const uint16_t* qp = a.query + b * a.q_row + (g * kGroup) * a.q_head + 8 * dl;
+    q0 = *reinterpret_cast<const uint4*>(qp);
+    q1 = *reinterpret_cast<const uint4*>(qp + a.q_head);
+  }
 
   float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
   float acc0[8], acc1[8];
@@ -722,7 +776,7 @@ bool use_seq_path(int32_t batch, int32_t max_blocks, int32_t num_kv_heads) {
   return static_cast<int64_t>(batch) * num_kv_heads <= device_cus();
 }
 
-template <int kKvHeads>
+template <int kKvHeads, bool kFused = false>
 int32_t launch_decode(const DecodeArgs& a, bool seq_path, hipStream_t s) {
   constexpr int kWaves = kKvHeads < kMaxWaves ? kKvHeads : kMaxWaves;
   constexpr int kHeadGroups = kKvHeads / kWaves;
@@ -731,9 +785,10 @@ int32_t launch_decode(const DecodeArgs& a, bool seq_path, hipStream_t s) {
   const size_t lds = sizeof(int) * (static_cast<size_t>(a.batch) + 1);
   if (seq_path) {
     if (a.max_blocks > kSeqMaxBlocks) return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: table too long");
-    paged_decode_seq_kernel<kKvHeads><<<dim3(a.batch, kKvHeads), 64 * kSeqWaves, 0, s>>>(a);
+    paged_decode_seq_kernel<kKvHeads, kFused><<<dim3(a.batch, kKvHeads), 64 * kSeqWaves, 0, s>>>(a);
     return check_launch("mi_paged_decode_attention(seq)");
   }
+  if constexpr (kFused) return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: fused form needs the per-sequence kernel");
   if (a.max_blocks > 0) {
     paged_decode_kernel<kKvHeads, kWaves><<<static_cast<uint32_t>(a.streams) * kHeadGroups, 64 * kWaves, lds, s>>>(a);
     int32_t rc = check_launch("mi_paged_decode_attention");
@@ -832,4 +887,80 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
     if (rc != MI_OK) return rc;
   }
   return ok();
+}
+
+extern "C" int32_t mi_paged_decode_attention_fused(
+    void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride, const void* k, int64_t k_row_stride,
+    const void* v, int64_t v_row_stride, const void* q_weight, const void* k_weight, const void* cos, const void* sin,
+    float eps, const int64_t* slot_mapping, int64_t slot_stride, void* key_pool, void* value_pool, int64_t num_blocks,
+    const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks, const int64_t* context_lens,
+    int64_t context_lens_stride, int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, float scale, void* q_scratch, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace mi;
+  if (batch < 0 || max_blocks < 0 || num_blocks < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: negative size");
+  if (batch == 0) return ok();
+  if (!q || !k || !v || !q_weight || !k_weight || !cos || !sin || !slot_mapping || !q_scratch)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: null pointer argument");
+  if (num_blocks > INT64_MAX / kBlockSize)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: pool too large");
+  if (!use_seq_path(batch, max_blocks, num_kv_heads) || max_blocks == 0 || num_heads != kGroup * num_kv_heads) {
+    // Large launches: the two-launch form (the append and q rotation, then the stream kernel).
+    int32_t rc = mi_qk_norm_rope(q_scratch, nullptr, nullptr, q, q_row_stride, k, k_row_stride, v, v_row_stride,
+                                 q_weight, k_weight, cos, sin, batch, num_heads, num_kv_heads, head_dim, eps,
+                                 slot_mapping, slot_stride, key_pool, value_pool, num_blocks * block_size, stream);
+    if (rc != MI_OK) return rc;
+    return mi_paged_decode_attention(out, out_row_stride, q_scratch, static_cast<int64_t>(num_heads) * head_dim,
+                                     head_dim, key_pool, value_pool, num_blocks, block_tables, block_table_stride,
+                                     max_blocks, context_lens, context_lens_stride, batch, num_heads, num_kv_heads,
+                                     head_dim, block_size, scale, workspace, workspace_bytes, stream);
+  }
+  // One launch: the per-sequence kernel with the prologue.  Shape checks as in the two entry points.
+  if (!out || !key_pool || !value_pool || !context_lens || !block_tables)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: null pointer argument");
+  if (head_dim != kHeadDim || block_size != kBlockSize)
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention_fused: needs head_dim %d, block_size %d", kHeadDim,
+                kBlockSize);
+  if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention_fused: num_kv_heads %d not in {1,2,4,8}", num_kv_heads);
+  if (!aligned16(out) || !aligned16(key_pool) || !aligned16(value_pool) || out_row_stride % 8 != 0)
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention_fused: out/pools must be 16-byte aligned");
+  if (block_table_stride < max_blocks || context_lens_stride <= 0 || q_row_stride < num_heads * head_dim ||
+      k_row_stride < num_kv_heads * head_dim || v_row_stride < num_kv_heads * head_dim)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: bad stride");
+  DecodeArgs a{};
+  a.out = static_cast<uint16_t*>(out);
+  a.out_row = out_row_stride;
+  a.key_pool = static_cast<const uint16_t*>(key_pool);
+  a.value_pool = static_cast<const uint16_t*>(value_pool);
+  a.num_blocks = num_blocks;
+  a.block_tables = block_tables;
+  a.bt_stride = block_table_stride;
+  a.context_lens = context_lens;
+  a.ctx_stride = context_lens_stride;
+  a.batch = batch;
+  a.max_blocks = max_blocks;
+  a.streams = 1;
+  a.scale = scale;
+  a.q_raw = static_cast<const uint16_t*>(q);
+  a.k_raw = static_cast<const uint16_t*>(k);
+  a.v_raw = static_cast<const uint16_t*>(v);
+  a.q_raw_row = q_row_stride;
+  a.k_raw_row = k_row_stride;
+  a.v_raw_row = v_row_stride;
+  a.q_weight = static_cast<const uint16_t*>(q_weight);
+  a.k_weight = static_cast<const uint16_t*>(k_weight);
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.slot_mapping = slot_mapping;
+  a.slot_stride = slot_stride;
+  a.num_slots = num_blocks * kBlockSize;
+  a.eps = eps;
+  hipStream_t s = as_stream(stream);
+  switch (num_kv_heads) {
+    case 1: return launch_decode<1, true>(a, true, s);
+    case 2: return launch_decode<2, true>(a, true, s);
+    case 4: return launch_decode<4, true>(a, true, s);
+    default: return launch_decode<8, true>(a, true, s);
+  }
 }

@@ -20,6 +20,7 @@ __all__ = [
     "gather_blocks",
     "pack_blocks",
     "paged_decode_attention",
+    "paged_decode_attention_fused",
     "paged_decode_workspace_bytes",
     "qk_norm_rope",
     "reshape_and_cache",
@@ -280,6 +281,83 @@ def paged_decode_attention(
         ws_ptr, ws_bytes, stream,
     )
     _native.check(rc, "mi_paged_decode_attention")
+    return out
+
+
+def paged_decode_attention_fused(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float,
+    slot_mapping: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``qk_norm_rope`` (decode form: the new K/V rows go to ``slot_mapping``) followed by
+    ``paged_decode_attention``, in one launch where the per-sequence kernel serves the batch.
+
+    q ``[B, Hq * 128]``, k / v ``[B, Hkv * 128]``: the new tokens' projection rows (row views are
+    fine); cos / sin ``[B, 128]``; the rest as in the two functions.  Same results, bit for bit.
+    Returns ``out`` ``[B, Hq * 128]``.
+    """
+    device = key_pool.device
+    for name, t in (("q", q), ("k", k), ("v", v), ("q_weight", q_weight), ("k_weight", k_weight), ("cos", cos),
+                    ("sin", sin)):
+        _require_bf16_rows(name, t, device)
+    for name, t in (("key_pool", key_pool), ("value_pool", value_pool), ("block_tables", block_tables),
+                    ("context_lens", context_lens), ("slot_mapping", slot_mapping)):
+        _require_gpu(name, t, device)
+    _require_index("block_tables", block_tables, 2)
+    _require_index("context_lens", context_lens, 1)
+    _require_index("slot_mapping", slot_mapping, 1)
+    if key_pool.dtype != torch.bfloat16 or value_pool.shape != key_pool.shape or value_pool.dtype != key_pool.dtype \
+            or not key_pool.is_contiguous() or not value_pool.is_contiguous():
+        raise ValueError("pools must be contiguous bf16 with identical shapes")
+    head_dim = q_weight.shape[-1]
+    batch = q.numel() // q.shape[-1]
+    q2, k2, v2 = q.reshape(batch, -1), k.reshape(batch, -1), v.reshape(batch, -1)
+    num_heads, num_kv_heads = q2.shape[1] // head_dim, k2.shape[1] // head_dim
+    cos2, sin2 = cos.reshape(batch, head_dim).contiguous(), sin.reshape(batch, head_dim).contiguous()
+    if v2.shape != k2.shape or k_weight.shape != q_weight.shape or key_pool.shape[2:] != (num_kv_heads, head_dim):
+        raise ValueError("q / k / v / weights / pools have inconsistent head sizes")
+    if block_tables.shape[0] != batch or context_lens.shape[0] != batch or slot_mapping.shape[0] != batch:
+        raise ValueError("block_tables / context_lens / slot_mapping batch differs from the tokens'")
+    key_pool, value_pool, block_tables = _as_kernel_blocks(key_pool, value_pool, block_tables)
+    num_blocks, block_size = key_pool.shape[:2]
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    max_blocks = block_tables.shape[1]
+    if out is None:
+        out = torch.empty((batch, num_heads * head_dim), dtype=torch.bfloat16, device=device)
+    elif out.shape != (batch, num_heads * head_dim) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError(f"out must be [B, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
+    if batch == 0:
+        return out
+    q_scratch = torch.empty((batch, num_heads, head_dim), dtype=torch.bfloat16, device=device)
+    need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size)
+    ws_ptr, ws_bytes = None, 0
+    if need > 0:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=device)
+        _require_gpu("workspace", workspace, device)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    rc = _native.load().mi_paged_decode_attention_fused(
+        out.data_ptr(), out.stride(0), q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0), v2.data_ptr(),
+        v2.stride(0), q_weight.data_ptr(), k_weight.data_ptr(), cos2.data_ptr(), sin2.data_ptr(), float(eps),
+        slot_mapping.data_ptr(), slot_mapping.stride(0) if batch > 1 else 1, key_pool.data_ptr(), value_pool.data_ptr(),
+        num_blocks, block_tables.data_ptr(), block_tables.stride(0) if batch > 1 else max(max_blocks, 1), max_blocks,
+        context_lens.data_ptr(), context_lens.stride(0) if batch > 1 else 1, batch, num_heads, num_kv_heads,
+        head_dim, block_size, float(scale), q_scratch.data_ptr(), ws_ptr, ws_bytes, _stream(device))
+    _native.check(rc, "mi_paged_decode_attention_fused")
     return out
 
 

@@ -4,9 +4,10 @@ Parameter names, shapes and the dense numerics (RMSNorm in fp32, bf16 RoPE table
 SwiGLU, tied lm_head) follow the reference model (src/mini_infra/model/qwen3.py:55-625), so its
 state_dict loads unchanged.  The attention differs in how it reaches K/V:
 
-* decode (``PagedAttentionMetadata``, one token per sequence): the new K/V rows go into the pool
-  slots straight from the fused q/k-norm + RoPE launch, then paged GQA decode attention reads the
-  context from the pool (replaces qwen3.py:257-292 + :219-255, no gather, no repeat_interleave);
+* decode (``PagedAttentionMetadata``, one token per sequence): q/k norm + RoPE, the append of the
+  new K/V rows into their pool slots and paged GQA decode attention over the context in the pool
+  -- one launch for small batches (the per-sequence kernel does the first two in its prologue),
+  two for large ones (replaces qwen3.py:257-292 + :219-255, no gather, no repeat_interleave);
 * prefill (``PagedPrefillMetadata``, or no metadata for a whole left-padded prompt): the MFMA
   chunked-prefill kernel attends causally within the chunk and reads the history straight from
   the pool through the block table (replaces the gather + concat + _attend chain);
@@ -155,12 +156,9 @@ class Qwen3Attention(nn.Module):
         if isinstance(metadata, PagedMixedMetadata):
             return self._mixed(q[0], k[0], v[0], cos[0], sin[0], kv_pool, metadata, workspace, kv_out)
         if isinstance(metadata, PagedAttentionMetadata):
-            q_rot, _, _ = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin, eps,
-                                                  slot_mapping=metadata.slot_mapping, key_pool=key_pool,
-                                                  value_pool=value_pool)
-            out = data_plane.paged_decode_attention(
-                q_rot, key_pool, value_pool, metadata.block_tables, metadata.context_lens, self.scaling,
-                workspace=workspace,
+            out = data_plane.paged_decode_attention_fused(
+                q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin, eps, metadata.slot_mapping, key_pool,
+                value_pool, metadata.block_tables, metadata.context_lens, self.scaling, workspace=workspace,
             ).view(batch, 1, -1)
             present = kv_pool
         else:
@@ -186,23 +184,22 @@ class Qwen3Attention(nn.Module):
         n = rows * width
         tokens = q.shape[0]
         eps = self.q_norm.eps
-        q_dec, _, _ = data_plane.qk_norm_rope(q[n:], k[n:], v[n:], self.q_norm.weight, self.k_norm.weight, cos[n:],
-                                              sin[n:], eps, slot_mapping=metadata.decode.slot_mapping,
-                                              key_pool=key_pool, value_pool=value_pool)
+        out = torch.empty((tokens, self.num_heads * self.head_dim), dtype=q.dtype, device=q.device)
+        decode = metadata.decode
+        data_plane.paged_decode_attention_fused(q[n:], k[n:], v[n:], self.q_norm.weight, self.k_norm.weight, cos[n:],
+                                                sin[n:], eps, decode.slot_mapping, key_pool, value_pool,
+                                                decode.block_tables, decode.context_lens, self.scaling,
+                                                out=out[n:], workspace=workspace)
         k_buf, v_buf = kv_out if kv_out is not None else (None, None)
         q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q[:n], k[:n], v[:n], self.q_norm.weight, self.k_norm.weight,
                                                        cos[:n], sin[:n], eps, k_out=k_buf, v_out=v_buf)
         q_rot = q_rot.view(rows, width, self.num_heads, self.head_dim).transpose(1, 2)
         k_rot = k_rot.view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
         v_rows = v_rows.view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
-        out = torch.empty((tokens, self.num_heads * self.head_dim), dtype=q.dtype, device=q.device)
         prefill = metadata.prefill
         data_plane.chunked_prefill_attention(q_rot, k_rot, v_rows, key_pool, value_pool, prefill.history_block_tables,
                                              prefill.start_lens, prefill.chunk_lens, self.scaling,
                                              out=out[:n].view(rows, width, -1))
-        decode = metadata.decode
-        data_plane.paged_decode_attention(q_dec, key_pool, value_pool, decode.block_tables, decode.context_lens,
-                                          self.scaling, out=out[n:], workspace=workspace)
         return self.o_proj(out.unsqueeze(0)), (k_rot, v_rows)
 
 

@@ -223,3 +223,46 @@ def test_context_of_forty_thousand_tokens(native_lib, device):
     q, kp, vp, bt, _ = random_case(91, ctx, spare=2)
     got = run_kernel(q, kp, vp, bt, ctx, device)
     assert max_abs(got, oracle(q, kp, vp, bt, ctx)) <= TOL
+
+
+def two_launches(q, k, v, qw, kw, cos, sin, slots, kp, vp, tables, ctx):
+    q_rot, _, _ = data_plane.qk_norm_rope(q, k, v, qw, kw, cos, sin, 1e-6, slot_mapping=slots, key_pool=kp,
+                                          value_pool=vp)
+    return data_plane.paged_decode_attention(q_rot, kp, vp, tables, ctx, SCALE)
+
+
+@pytest.mark.parametrize("batch,kv_heads,block_size", [(6, 8, 16), (1, 8, 16), (32, 8, 16), (40, 8, 16),
+                                                       (5, 2, 16), (7, 8, 32)])
+def test_fused_form_equals_norm_rope_then_attention(native_lib, device, batch, kv_heads, block_size):
+    """mi_paged_decode_attention_fused (q/k norm + RoPE + append in the per-sequence kernel's
+    prologue, or the two launches for batches past one workgroup per CU) against qk_norm_rope then
+    paged_decode_attention: output and pool bit for bit, including a pad row (slot -1, context 0)
+    and a context of one token (only the new one)."""
+    g = torch.Generator().manual_seed(batch * 10 + kv_heads)
+    heads = 2 * kv_heads
+    blocks_per = 40 * 16 // block_size
+    nb = batch * blocks_per + 8
+    bf = torch.bfloat16
+    q = torch.randn(batch, heads * 128 + 64, generator=g).to(bf)[:, :heads * 128]  # a row view
+    k = torch.randn(batch, kv_heads * 128, generator=g).to(bf)
+    v = torch.randn(batch, kv_heads * 128, generator=g).to(bf)
+    qw, kw = (torch.rand(128, generator=g) + 0.5).to(bf), (torch.rand(128, generator=g) + 0.5).to(bf)
+    ang = torch.rand(batch, 128, generator=g) * 6.28
+    cos, sin = ang.cos().to(bf), ang.sin().to(bf)
+    pool = torch.randn(2, nb, block_size, kv_heads, 128, generator=g).to(bf)
+    perm = torch.randperm(nb - 1, generator=g)[:batch * blocks_per] + 1
+    tables = perm.view(batch, blocks_per)
+    ctx = torch.randint(1, blocks_per * block_size + 1, (batch,), generator=g)
+    ctx[0] = 1
+    slots = tables.gather(1, ((ctx - 1) // block_size).unsqueeze(1)).squeeze(1) * block_size + (ctx - 1) % block_size
+    if batch > 1:
+        slots[-1], ctx[-1] = -1, 0
+    dev = [t.to(device) for t in (q, k, v, qw, kw, cos, sin, slots)]
+    pools = [pool.clone().to(device), pool.clone().to(device)]
+    want = two_launches(*dev, pools[0][0], pools[0][1], tables.to(device), ctx.to(device))
+    got = data_plane.paged_decode_attention_fused(*dev[:7], 1e-6, dev[7], pools[1][0], pools[1][1],
+                                                  tables.to(device), ctx.to(device), SCALE)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(pools[1].view(torch.int16), pools[0].view(torch.int16))
+    if batch > 1:
+        assert not got[-1].any()
