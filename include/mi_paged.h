@@ -153,7 +153,9 @@ int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, const void*
  * otherwise it runs the two entry points, rotating q into q_scratch.
  * q: [batch] rows of num_heads * 128 (q_row_stride), k / v: rows of num_kv_heads * 128;
  * cos / sin: [batch, 128]; q_scratch: [batch, num_heads, 128] bf16 (always required).
- * The remaining arguments are those of mi_qk_norm_rope and mi_paged_decode_attention.
+ * The remaining arguments are those of mi_qk_norm_rope and mi_paged_decode_attention.  Each row's
+ * slot must lie in one of its own blocks (decode packing puts it at position context - 1): in the
+ * one-launch form only the row's own workgroups are ordered after its append.
  */
 int32_t mi_paged_decode_attention_fused(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
                                         const void* k, int64_t k_row_stride, const void* v, int64_t v_row_stride,
