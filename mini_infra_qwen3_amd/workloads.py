@@ -2,7 +2,7 @@
 
 Shapes: 16 query heads, 8 KV heads, head_dim 128, bf16, block_size 16, 28 layers.
 Context lengths, block tables and values are all drawn from seeded generators, so the
-GPU path and the CPU checker see identical inputs:
+GPU path and the CPU oracle see identical inputs:
 
 * ``decode_step`` -- one layer: batch 8, contexts uniform in [64, 512], pool 4096 blocks,
   block tables from one random permutation of blocks 1..4095.

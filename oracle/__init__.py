@@ -2,7 +2,7 @@
 
 A CPU restatement of the reference's torch path for the paged-KV hot path
 (src/mini_infra/worker/paged_kv_cache.py, src/mini_infra/worker/paged_runner.py,
-src/mini_infra/model/qwen3.py), used only as the checker:
+src/mini_infra/model/qwen3.py), used only as the reference the tests compare against:
 
 * ``oracle.torch_ref`` -- the reference's op chains (advanced-index gather, index_copy_,
   repeat_interleave, bf16 matmul, fp32 softmax) in the same order with the same bf16

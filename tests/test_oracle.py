@@ -1,5 +1,5 @@
-"""Pins the oracle (CPU restatement of the reference torch path) before it is trusted as the
-checker: against the reference suite's known-answer tests, the closed forms of
+"""Pins the oracle (CPU restatement of the reference torch path) before the GPU tests compare
+against it: against the reference suite's known-answer tests, the closed forms of
 ``oracle.closed_form`` (numpy indexing, fp64 loops) and the reference's own invariants."""
 
 import numpy as np
