@@ -44,17 +44,28 @@ constexpr int kGroup = 2;
 #ifndef MI_PREFILL_WAVES_PER_HEAD
 #define MI_PREFILL_WAVES_PER_HEAD 4
 #endif
-constexpr int kWavesPerHead = MI_PREFILL_WAVES_PER_HEAD;  // 32 queries per wave
-constexpr int kQTile = 32 * kWavesPerHead;                // queries per head per workgroup
+constexpr int kWavesPerHead = MI_PREFILL_WAVES_PER_HEAD;
+#ifndef MI_PREFILL_NT
+#define MI_PREFILL_NT 2
+#endif
+constexpr int kNt = MI_PREFILL_NT;                        // 16-query MFMA column tiles per wave
+constexpr int kQPerWave = 16 * kNt;
+constexpr int kQTile = kQPerWave * kWavesPerHead;         // queries per head per workgroup
+constexpr int kWavesPerSimd = kNt == 1 ? 4 : 2;           // occupancy the register budget is set for
+#ifndef MI_PREFILL_AHEAD
+#define MI_PREFILL_AHEAD 2
+#endif
+constexpr int kAhead = MI_PREFILL_AHEAD;                  // K/V tiles in flight in registers (1 or 2)
+static_assert(kAhead == 1 || kAhead == 2, "one or two tiles ahead");
 constexpr int kKTile = 64;                 // keys per KV tile
 #ifndef MI_PREFILL_K_PAD
 #define MI_PREFILL_K_PAD 16
 #endif
 #ifndef MI_PREFILL_V_PAD
-#define MI_PREFILL_V_PAD 8
+#define MI_PREFILL_V_PAD 16
 #endif
 constexpr int kKStride = kHeadDim + MI_PREFILL_K_PAD;  // LDS row of K (elements): 288 B
-constexpr int kVStride = kKTile + MI_PREFILL_V_PAD;    // LDS row of V^T (elements): 144 B, 16-byte aligned
+constexpr int kVStride = kKTile + MI_PREFILL_V_PAD;    // LDS row of V^T (elements): 160 B, 16-byte aligned
 constexpr int kThreads = 64 * kGroup * kWavesPerHead;    // one workgroup per CU at 4 waves per head
 constexpr int kKeysPerPass = kThreads / 16;               // K rows one pass of 16-byte pieces covers
 constexpr int kKPieces = kKTile / kKeysPerPass;           // K pieces per thread and tile
@@ -124,7 +135,7 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint3
 }
 
 template <int kKvHeads>
-__global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kernel(const PrefillArgs a) {
   __shared__ __align__(16) uint16_t sK[2][kKTile * kKStride];
   __shared__ __align__(16) uint16_t sV[2][kHeadDim * kVStride];
   extern __shared__ int s_hblk[];  // [ceil(nh / 16)] history block ids of this row (dynamic LDS)
@@ -164,7 +175,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform: keeps edge-tile branches real
   const int hh = w / kWavesPerHead;
   const int qs = w % kWavesPerHead;
   const int h = g * kGroup + hh;
@@ -185,10 +196,10 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   }
 
   // ---- Q^T fragments (B operand): query column n = ql of n-tile nt, dims 32 ks + 8 gq .. +8
-  bf16x8 qf[2][4];
-  const int qw0 = q0 + 32 * qs;  // first query of this wave
+  bf16x8 qf[kNt][4];
+  const int qw0 = q0 + kQPerWave * qs;  // first query of this wave
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < kNt; ++nt) {
     const int qi = qw0 + 16 * nt + ql;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -286,45 +297,48 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
   // a constant A with ones in rows 0, 4, 8, 12: its rows 0, 4, 8, 12 -- element 0 of every lane group
   // -- accumulate sum_k bf16(p_k) on the matrix cores instead of 32 VALU adds per tile, and the
   // lazy rescale of oacc covers them.
-  f32x4 oacc[9][2];
+  f32x4 oacc[9][kNt];
 #pragma unroll
   for (int dt = 0; dt < 9; ++dt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) oacc[dt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nt = 0; nt < kNt; ++nt) oacc[dt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const __bf16 one_or_zero = (ql & 3) == 0 ? static_cast<__bf16>(1.0f) : static_cast<__bf16>(0.0f);
   const bf16x8 ones_frag = {one_or_zero, one_or_zero, one_or_zero, one_or_zero,
                             one_or_zero, one_or_zero, one_or_zero, one_or_zero};
-  float m_run[2] = {-INFINITY, -INFINITY};
+  float m_run[kNt];
+#pragma unroll
+  for (int nt = 0; nt < kNt; ++nt) m_run[nt] = -INFINITY;
   const float scale = a.scale;
 
-  // Two register sets carry the K/V pieces of the next two tiles: tile t + 2 is fetched while
-  // tile t is computed, and tile t + 1 (fetched one iteration earlier) goes to LDS at its end.
+  // With kAhead = 2, two register sets carry the K/V pieces of the next two tiles: tile t + 2 is
+  // fetched while tile t is computed, and tile t + 1 (fetched one iteration earlier) goes to LDS
+  // at its end.  With kAhead = 1 one set fetches tile t + 1 and stores it at the end of tile t.
   u32x4 kregA[kKPieces], vregA[kVPieces][2], kregB[kKPieces], vregB[kVPieces][2];
   __syncthreads();  // s_hblk ready
   load_tile(0, kregA, vregA);
   MI_STORE_TILE(0, kregA, vregA);
-  load_tile(min(1, n_tiles - 1), kregA, vregA);
+  if constexpr (kAhead == 2) load_tile(min(1, n_tiles - 1), kregA, vregA);
   __syncthreads();
 
   // kl / vl: registers tile t + 2 is fetched into; ks / vs: registers holding tile t + 1.
   auto tile_step = [&](const int t, u32x4 (&kl)[kKPieces], u32x4 (&vl)[kVPieces][2], u32x4 (&ks_)[kKPieces],
                        u32x4 (&vs_)[kVPieces][2]) {
     const int buf = t & 1;
-    load_tile(min(t + 2, n_tiles - 1), kl, vl);  // past the end: re-reads the last tile
+    load_tile(min(t + kAhead, n_tiles - 1), kl, vl);  // past the end: re-reads the last tile
 
     // ---- S^T = K Q^T for 64 keys x 32 queries
-    f32x4 sacc[4][2];
+    f32x4 sacc[4][kNt];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) sacc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int nt = 0; nt < kNt; ++nt) sacc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[buf][(mt * 16 + ql) * kKStride + ks * 32 + gq * 8]);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < kNt; ++nt)
           sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[nt][ks], sacc[mt][nt], 0, 0, 0);
       }
     }
@@ -334,19 +348,19 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     const int key0 = is_hist ? t * kKTile : (c_lo + t - n_hist_tiles) * kKTile;
     bool need_mask;
     if (is_hist) {
-      need_mask = key0 + kKTile > nh || qw0 < pad || qw0 + 31 >= L;
+      need_mask = key0 + kKTile > nh || qw0 < pad || qw0 + kQPerWave - 1 >= L;
     } else {
-      need_mask = key0 + kKTile - 1 > qw0 || key0 < pad || qw0 < pad || qw0 + 31 >= L;
+      need_mask = key0 + kKTile - 1 > qw0 || key0 < pad || qw0 < pad || qw0 + kQPerWave - 1 >= L;
     }
     // Scores rounded like the reference; log2(e) is applied inside the exp2 FMA below.
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) reference_scores(sacc[mt][nt], scale);
-    if (need_mask) {
+      for (int nt = 0; nt < kNt; ++nt) reference_scores(sacc[mt][nt], scale);
+    if (__builtin_expect(__builtin_amdgcn_readfirstlane(static_cast<int>(need_mask)) != 0, 0)) {
       // Bitwise (not short-circuit) conditions keep the edge-tile path free of branches.
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < kNt; ++nt) {
         const int qi = qw0 + 16 * nt + ql;
         const bool row_ok = (qi >= pad) & (qi < L);
         const int lo = is_hist ? 0 : pad;        // visible key range [lo, hi] of this query
@@ -367,9 +381,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
     // score to within kRescaleSlack, so each lane tests its own 16 scores and the cross-lane
     // column max is taken only on the rare tiles that raise m_run.
     constexpr float to_log2 = kLog2e;
-    float mx[2];
+    float mx[kNt];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < kNt; ++nt) {
       float v = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
@@ -377,10 +391,12 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
         for (int i = 0; i < 4; ++i) v = fmaxf(v, sacc[mt][nt][i]);
       mx[nt] = v * to_log2;
     }
-    const bool grow = mx[0] > m_run[0] + kRescaleSlack || mx[1] > m_run[1] + kRescaleSlack;
+    bool grow = false;
+#pragma unroll
+    for (int nt = 0; nt < kNt; ++nt) grow = grow || mx[nt] > m_run[nt] + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < kNt; ++nt) {
         mx[nt] = fmaxf(mx[nt], __shfl_xor(mx[nt], 16));
         mx[nt] = fmaxf(mx[nt], __shfl_xor(mx[nt], 32));
         const float mn = fmaxf(m_run[nt], mx[nt]);
@@ -390,9 +406,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
         for (int dt = 0; dt < 9; ++dt) oacc[dt][nt] *= alpha;
       }
     }
-    bf16x8 pf[2][2];  // [nt][ks2]
+    bf16x8 pf[kNt][2];  // [nt][ks2]
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < kNt; ++nt) {
       const float ref = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
@@ -415,25 +431,29 @@ __global__ __launch_bounds__(kThreads, 2) void chunked_prefill_kernel(const Pref
         const uint16_t* vrow = &sV[buf][(dt * 16 + ql) * kVStride];
         const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vrow + vcol(dt * 16, 32 * ks2 + 8 * gq));
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < kNt; ++nt)
           oacc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[nt][ks2], oacc[dt][nt], 0, 0, 0);
       }
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
+      for (int nt = 0; nt < kNt; ++nt)
         oacc[8][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_frag, pf[nt][ks2], oacc[8][nt], 0, 0, 0);
     }
 
     MI_STORE_TILE(buf ^ 1, ks_, vs_);  // past the end: a buffer no later tile reads
     __syncthreads();
   };
-  for (int t = 0; t < n_tiles; t += 2) {
-    tile_step(t, kregB, vregB, kregA, vregA);
-    if (t + 1 < n_tiles) tile_step(t + 1, kregA, vregA, kregB, vregB);
+  if constexpr (kAhead == 2) {
+    for (int t = 0; t < n_tiles; t += 2) {
+      tile_step(t, kregB, vregB, kregA, vregA);
+      if (t + 1 < n_tiles) tile_step(t + 1, kregA, vregA, kregB, vregB);
+    }
+  } else {
+    for (int t = 0; t < n_tiles; ++t) tile_step(t, kregA, vregA, kregA, vregA);
   }
 
   // ---- normalise and write: lane holds query qw0 + 16 nt + ql, dims 16 dt + 4 gq + i
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < kNt; ++nt) {
     const float lt = oacc[8][nt][0];
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int qi = qw0 + 16 * nt + ql;
