@@ -29,23 +29,33 @@ def padded_tables(block_tables: Sequence[Sequence[int]], width: int | None = Non
 
 
 def pack_decode_rows(block_tables: Sequence[Sequence[int]], last_tokens: Sequence[int],
-                     positions: Sequence[int], block_size: int) -> np.ndarray:
+                     positions: Sequence[int], block_size: int, rows: int | None = None,
+                     blocks: int | None = None) -> np.ndarray:
     """``[B, 4 + max_blocks]``: token, position, slot, context length, null-padded block table.
 
     Same columns as the reference's decode packing (src/mini_infra/worker/paged_runner.py:154-162).
+    ``rows`` / ``blocks`` (at least B / the longest table) fix the shape of a padded bucket: pad
+    rows are token 0, position 0, slot -1 (no append) and context 0 (zero output).
     """
-    tables = padded_tables(block_tables)
+    n = len(block_tables)
+    width = max((len(t) for t in block_tables), default=0) if blocks is None else blocks
+    total = n if rows is None else rows
+    if total < n:
+        raise ValueError(f"{n} decode rows do not fit {total}")
+    tables = padded_tables(block_tables, width)
+    if blocks is not None and any(len(t) > blocks for t in block_tables):
+        raise ValueError(f"a block table is longer than {blocks}")
     pos = np.asarray(positions, dtype=np.int64)
-    rows = np.arange(len(block_tables))
     logical = pos // block_size
-    if np.any(logical >= np.array([len(t) for t in block_tables])):
+    if np.any(logical >= np.array([len(t) for t in block_tables], dtype=np.int64)):
         raise ValueError("a block table does not cover its decode position")
-    out = np.empty((len(block_tables), 4 + tables.shape[1]), dtype=np.int64)
-    out[:, 0] = np.asarray(last_tokens, dtype=np.int64)
-    out[:, 1] = pos
-    out[:, 2] = tables[rows, logical] * block_size + pos % block_size
-    out[:, 3] = pos + 1
-    out[:, 4:] = tables
+    out = np.zeros((total, 4 + width), dtype=np.int64)
+    out[n:, 2] = -1
+    out[:n, 0] = np.asarray(last_tokens, dtype=np.int64)
+    out[:n, 1] = pos
+    out[:n, 2] = tables[np.arange(n), logical] * block_size + pos % block_size
+    out[:n, 3] = pos + 1
+    out[:n, 4:] = tables
     return out
 
 
@@ -77,19 +87,28 @@ def prefill_scatter_indices(block_tables: Sequence[Sequence[int]], chunk_lens: S
 
 
 def pack_prefill_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions: Sequence[int],
-                      block_tables: Sequence[Sequence[int]], block_size: int, pad_token_id: int) -> np.ndarray:
+                      block_tables: Sequence[Sequence[int]], block_size: int, pad_token_id: int,
+                      width: int | None = None, history_blocks: int | None = None) -> np.ndarray:
     """``[B, 2 L + 2 + max_history_blocks]``: left-padded ids | positions | start, len | history table.
 
     Same row layout as the reference's chunked-prefill packing
     (src/mini_infra/worker/paged_runner.py:57-72); history blocks are the first
-    ``ceil(start / block_size)`` entries of each table, null-padded.
+    ``ceil(start / block_size)`` entries of each table, null-padded.  ``width`` / ``history_blocks``
+    (at least the longest chunk / history) fix the shape of a padded bucket: wider left padding
+    (pad tokens at position 0) and null-padded tables.
     """
     lens = [len(ids) for ids in chunk_token_ids]
     if not lens or min(lens) < 1:
         raise ValueError("every chunk must hold at least one token")
-    width = max(lens)
     hist = [-(-s // block_size) for s in start_positions]
-    max_hist = max(hist)
+    if width is None:
+        width = max(lens)
+    if history_blocks is None:
+        history_blocks = max(hist)
+    if width < max(lens) or history_blocks < max(hist):
+        raise ValueError(f"chunks of {max(lens)} tokens / {max(hist)} history blocks do not fit "
+                         f"width {width} / {history_blocks} blocks")
+    max_hist = history_blocks
     out = np.zeros((len(lens), 2 * width + 2 + max_hist), dtype=np.int64)
     out[:, :width] = pad_token_id
     for row, (ids, n, start, table, h) in enumerate(zip(chunk_token_ids, lens, start_positions, block_tables, hist)):
@@ -106,19 +125,24 @@ def pack_prefill_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions:
 
 def pack_mixed_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions: Sequence[int],
                     prefill_tables: Sequence[Sequence[int]], last_tokens: Sequence[int], positions: Sequence[int],
-                    decode_tables: Sequence[Sequence[int]], block_size: int,
-                    pad_token_id: int) -> tuple[np.ndarray, tuple[int, int, int, int, int]]:
+                    decode_tables: Sequence[Sequence[int]], block_size: int, pad_token_id: int,
+                    width: int | None = None, history_blocks: int | None = None, decode_rows: int | None = None,
+                    decode_blocks: int | None = None) -> tuple[np.ndarray, tuple[int, int, int, int, int]]:
     """One int64 buffer for a mixed chunk + decode step, uploaded at once.
 
     Layout (T = P L + D): tokens ``[T]`` | positions ``[T]`` | per chunk row (start, length,
     history table) ``[P, 2 + nb]`` | per decode row (slot, context length, block table)
     ``[D, 2 + mb]``.  The first P L tokens / positions are the chunks left-padded to L, row-major,
     as ``pack_prefill_rows`` lays them out; the last D are the decode tokens of ``pack_decode_rows``.
+    The optional sizes fix L, nb, D and mb for a padded bucket (see the two packers).
     Returns the buffer and (P, L, nb, D, mb).
     """
-    prefill = pack_prefill_rows(chunk_token_ids, start_positions, prefill_tables, block_size, pad_token_id)
-    decode = pack_decode_rows(decode_tables, last_tokens, positions, block_size)
-    rows, width = prefill.shape[0], max(len(ids) for ids in chunk_token_ids)
+    prefill = pack_prefill_rows(chunk_token_ids, start_positions, prefill_tables, block_size, pad_token_id,
+                                width=width, history_blocks=history_blocks)
+    decode = pack_decode_rows(decode_tables, last_tokens, positions, block_size, rows=decode_rows,
+                              blocks=decode_blocks)
+    rows = prefill.shape[0]
+    width = max(len(ids) for ids in chunk_token_ids) if width is None else width
     nb = prefill.shape[1] - 2 * width - 2
     flat = np.concatenate([prefill[:, :width].ravel(), decode[:, 0], prefill[:, width:2 * width].ravel(), decode[:, 1],
                            prefill[:, 2 * width:].ravel(), decode[:, 2:].ravel()])

@@ -67,12 +67,8 @@ class _DecodeGraph:
                                                             context_lens=s[:, 3])
 
     def load(self, packed: np.ndarray) -> None:
-        """Copies a host-packed ``[rows, 4 + nb]`` step in, padding rows and block columns."""
-        rows, cols = packed.shape
-        full = np.zeros((self.batch, 4 + self.blocks), dtype=np.int64)
-        full[:, 2] = -1
-        full[:rows, :cols] = packed
-        self.static.copy_(torch.from_numpy(full))
+        """Copies a step packed at the bucket's shape (``pack_decode_rows(..., rows, blocks)``)."""
+        self.static.copy_(torch.from_numpy(packed))
 
 
 class _PrefillGraph:
@@ -110,18 +106,9 @@ class _PrefillGraph:
         return s[:, :w], s[:, w:2 * w], PagedPrefillMetadata(history_block_tables=s[:, 2 * w + 2:],
                                                              start_lens=s[:, 2 * w], chunk_lens=s[:, 2 * w + 1])
 
-    def load(self, packed: np.ndarray, chunk_width: int) -> None:
-        """Copies a host-packed ``[rows, 2 L + 2 + nb]`` step in (L <= W, nb <= NB), widening the left
-        padding to W and null-padding the history tables."""
-        w, length = self.width, chunk_width
-        nb = packed.shape[1] - 2 * length - 2
-        full = np.zeros((self.rows, 2 * w + 2 + self.hist_blocks), dtype=np.int64)
-        full[:, :w - length] = self.pad_token_id
-        full[:, w - length:w] = packed[:, :length]
-        full[:, 2 * w - length:2 * w] = packed[:, length:2 * length]
-        full[:, 2 * w:2 * w + 2] = packed[:, 2 * length:2 * length + 2]
-        full[:, 2 * w + 2:2 * w + 2 + nb] = packed[:, 2 * length + 2:]
-        self.static.copy_(torch.from_numpy(full))
+    def load(self, packed: np.ndarray) -> None:
+        """Copies a step packed at the bucket's shape (``pack_prefill_rows(..., width, history_blocks)``)."""
+        self.static.copy_(torch.from_numpy(packed))
 
 
 class _MixedGraph:
@@ -178,27 +165,9 @@ class _MixedGraph:
             prefill_rows=self.rows, prefill_width=self.width)
         return s[:t].view(1, t), s[t:2 * t].view(1, t), meta
 
-    def load(self, prefill: np.ndarray, chunk_width: int, decode: np.ndarray) -> None:
-        """Copies host-packed chunk rows (``pack_prefill_rows``, width L <= W, nb <= NB) and decode rows
-        (``pack_decode_rows``, d <= D rows, mb <= MB blocks) into the bucket's layout."""
-        full = self._empty()
-        t, w, length = self.tokens, self.width, chunk_width
-        n = self.rows * w
-        ids, pos = full[:n].reshape(self.rows, w), full[t:t + n].reshape(self.rows, w)
-        ids[:, w - length:] = prefill[:, :length]
-        pos[:, w - length:] = prefill[:, length:2 * length]
-        d = decode.shape[0]
-        full[n:n + d] = decode[:, 0]
-        full[t + n:t + n + d] = decode[:, 1]
-        at = 2 * t + self.rows * (2 + self.hist_blocks)
-        chunk = full[2 * t:at].reshape(self.rows, 2 + self.hist_blocks)
-        nb = prefill.shape[1] - 2 * length - 2
-        chunk[:, :2] = prefill[:, 2 * length:2 * length + 2]
-        chunk[:, 2:2 + nb] = prefill[:, 2 * length + 2:]
-        dec = full[at:].reshape(self.decode_rows, 2 + self.decode_blocks)
-        dec[:d, :2] = decode[:, 2:4]
-        dec[:d, 2:2 + decode.shape[1] - 4] = decode[:, 4:]
-        self.static.copy_(torch.from_numpy(full))
+    def load(self, flat: np.ndarray) -> None:
+        """Copies a step packed at the bucket's shape (``pack_mixed_rows`` with its four sizes)."""
+        self.static.copy_(torch.from_numpy(flat))
 
 
 class PagedDecodeOutput(NamedTuple):
@@ -353,18 +322,20 @@ class PagedRunner(BaseModelRunner):
         first ``start`` slots are visible (reference paged_runner.py:32-102).  next_tokens holds the greedy
         token after each row's last position (meaningful where the chunk completes the prompt).
         """
-        rows = pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size, self.pad_token_id)
         width = max(len(c) for c in chunk_token_ids)
         graph = None
         if self._prefill_graphs and pool is self._prefill_pool:
-            graph = self._prefill_bucket(rows.shape[0], width, rows.shape[1] - 2 * width - 2)
+            hist = max(-(-st // pool.block_size) for st in start_positions)
+            graph = self._prefill_bucket(len(chunk_token_ids), width, hist)
         if graph is not None:
-            graph.load(rows, width)
+            graph.load(pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size,
+                                         self.pad_token_id, width=graph.width, history_blocks=graph.hist_blocks))
             with StepTimer(self.device) as timer:
                 graph.graph.replay()
                 next_token = argmax_rows(graph.logits)
             return PrefillOutput(next_token.tolist(), KVCache(graph.presents), timer.elapsed_ms)
-        packed = torch.from_numpy(rows).to(self.device)
+        packed = torch.from_numpy(pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size,
+                                                    self.pad_token_id)).to(self.device)
         input_ids = packed[:, :width]
         position_ids = packed[:, width:2 * width]
         metadata = PagedPrefillMetadata(
@@ -406,13 +377,16 @@ class PagedRunner(BaseModelRunner):
         """Packs one decode step as ``[B, 4 + max_blocks]`` and uploads it once (reference
         paged_runner.py:138-166).  Returns column views: input_ids / position_ids ``[B, 1]`` and the
         metadata's slot_mapping, block_tables and context_lens."""
-        rows = pack_decode_rows(block_tables, last_tokens, positions, block_size)
-        graph = self._bucket(*rows.shape) if self._graphs and block_size == self._graph_pool.block_size else None
+        graph = None
+        if self._graphs and block_size == self._graph_pool.block_size:
+            graph = self._bucket(len(block_tables), max((len(t) for t in block_tables), default=0))
         self._loaded = None
         if graph is not None:
-            graph.load(rows)
-            self._loaded = (graph, rows.shape[0])
-            return graph.views(rows.shape[0])
+            graph.load(pack_decode_rows(block_tables, last_tokens, positions, block_size, rows=graph.batch,
+                                        blocks=graph.blocks))
+            self._loaded = (graph, len(block_tables))
+            return graph.views(len(block_tables))
+        rows = pack_decode_rows(block_tables, last_tokens, positions, block_size)
         packed = torch.from_numpy(rows).to(self.device)
         metadata = PagedAttentionMetadata(slot_mapping=packed[:, 2], block_tables=packed[:, 4:],
                                           context_lens=packed[:, 3])
@@ -455,15 +429,17 @@ class PagedRunner(BaseModelRunner):
         position_ids ``[1, P L + D]`` and the metadata, all views of that buffer."""
         self._mixed_loaded = None
         if self._mixed_graphs and pool is self._mixed_pool:
-            prefill = pack_prefill_rows(chunk_token_ids, start_positions, prefill_block_tables, pool.block_size,
-                                        self.pad_token_id)
-            decode = pack_decode_rows(decode_block_tables, last_tokens, positions, pool.block_size)
             width = max(len(c) for c in chunk_token_ids)
-            graph = self._mixed_bucket(prefill.shape[0], width, prefill.shape[1] - 2 * width - 2, decode.shape[0],
-                                       decode.shape[1] - 4)
+            hist = max(-(-st // pool.block_size) for st in start_positions)
+            graph = self._mixed_bucket(len(chunk_token_ids), width, hist, len(decode_block_tables),
+                                       max((len(t) for t in decode_block_tables), default=0))
             if graph is not None:
-                graph.load(prefill, width, decode)
-                self._mixed_loaded = (graph, decode.shape[0])
+                flat, _ = pack_mixed_rows(chunk_token_ids, start_positions, prefill_block_tables, last_tokens, positions,
+                                          decode_block_tables, pool.block_size, self.pad_token_id, width=graph.width,
+                                          history_blocks=graph.hist_blocks, decode_rows=graph.decode_rows,
+                                          decode_blocks=graph.decode_blocks)
+                graph.load(flat)
+                self._mixed_loaded = (graph, len(decode_block_tables))
                 ids, pos, meta = graph.views()
                 return ids, pos, meta._replace(kv_pools=tuple(pool.kv_pools))
         flat, (rows, width, nb, decode_rows, mb) = pack_mixed_rows(

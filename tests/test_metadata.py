@@ -9,6 +9,7 @@ import pytest
 from mini_infra_qwen3_amd.core import KVCacheManager
 from mini_infra_qwen3_amd.worker.metadata import (
     pack_decode_rows,
+    pack_mixed_rows,
     pack_prefill_rows,
     padded_tables,
     prefill_scatter_indices,
@@ -92,3 +93,58 @@ def test_tables_cover_positions():
     with pytest.raises(ValueError):
         prefill_scatter_indices([[1]], [2], [3], 2, 4)
     assert padded_tables([[1, 2], []]).tolist() == [[1, 2], [0, 0]]
+
+
+# ------------------------------------------------------------------ padded graph buckets
+def test_decode_rows_padded_to_a_bucket():
+    """Pad rows append nothing (slot -1) and attend to nothing (context 0); live rows are the
+    unpadded packing with null-padded tables."""
+    tables, toks, pos = [[9, 4], [7]], [11, 22], [5, 2]
+    plain = pack_decode_rows(tables, toks, pos, block_size=4)
+    padded = pack_decode_rows(tables, toks, pos, block_size=4, rows=4, blocks=5)
+    assert padded.shape == (4, 9)
+    assert (padded[:2, :4] == plain[:, :4]).all()
+    assert padded[:2, 4:].tolist() == [[9, 4, 0, 0, 0], [7, 0, 0, 0, 0]]
+    assert padded[2:].tolist() == [[0, 0, -1, 0] + [0] * 5] * 2
+    with pytest.raises(ValueError):
+        pack_decode_rows(tables, toks, pos, block_size=4, rows=1)
+    with pytest.raises(ValueError):
+        pack_decode_rows(tables, toks, pos, block_size=4, blocks=1)
+
+
+def test_prefill_rows_widened_to_a_bucket():
+    """A chunk widened to a bucket: more left padding (pad id, position 0), the same start / length,
+    history tables null-padded."""
+    chunks, starts, tables = [[5, 6, 7], [8]], [4, 0], [[3, 9, 2], [1]]
+    plain = pack_prefill_rows(chunks, starts, tables, block_size=4, pad_token_id=99)
+    wide = pack_prefill_rows(chunks, starts, tables, block_size=4, pad_token_id=99, width=6, history_blocks=3)
+    assert plain.shape == (2, 2 * 3 + 2 + 1) and wide.shape == (2, 2 * 6 + 2 + 3)
+    assert wide[0, :6].tolist() == [99, 99, 99, 5, 6, 7] and wide[1, :6].tolist() == [99] * 5 + [8]
+    assert wide[0, 6:12].tolist() == [0, 0, 0, 4, 5, 6] and wide[1, 6:12].tolist() == [0] * 6
+    assert wide[:, 12:14].tolist() == [[4, 3], [0, 1]]
+    assert wide[:, 14:].tolist() == [[3, 0, 0], [0, 0, 0]]
+    for w, h in ((2, 3), (6, 0)):
+        with pytest.raises(ValueError):
+            pack_prefill_rows(chunks, starts, tables, block_size=4, pad_token_id=99, width=w, history_blocks=h)
+
+
+@pytest.mark.parametrize("sizes", [None, (8, 4, 5, 6)])
+def test_mixed_rows_split_into_the_two_packings(sizes):
+    """The mixed buffer is the chunk packing and the decode packing laid out as documented: tokens,
+    positions, chunk metadata, decode metadata (optionally at a bucket's fixed sizes)."""
+    chunks, starts, pf_tables = [[5, 6, 7], [8, 9]], [4, 0], [[3, 9, 2], [1]]
+    dec_tables, toks, pos = [[9, 4], [7], [6, 2, 1]], [11, 22, 33], [5, 2, 9]
+    kw = {} if sizes is None else dict(zip(("width", "history_blocks", "decode_rows", "decode_blocks"), sizes))
+    flat, (p, w, nb, d, mb) = pack_mixed_rows(chunks, starts, pf_tables, toks, pos, dec_tables, 4, 0, **kw)
+    pf = pack_prefill_rows(chunks, starts, pf_tables, 4, 0, width=kw.get("width"),
+                           history_blocks=kw.get("history_blocks"))
+    dc = pack_decode_rows(dec_tables, toks, pos, 4, rows=kw.get("decode_rows"), blocks=kw.get("decode_blocks"))
+    assert p == 2 and w == (3 if sizes is None else 8) and nb == pf.shape[1] - 2 * w - 2
+    assert (d, mb) == (dc.shape[0], dc.shape[1] - 4)
+    t = p * w + d
+    assert flat.shape == (2 * t + p * (2 + nb) + d * (2 + mb),)
+    assert (flat[:p * w] == pf[:, :w].ravel()).all() and (flat[p * w:t] == dc[:, 0]).all()
+    assert (flat[t:t + p * w] == pf[:, w:2 * w].ravel()).all() and (flat[t + p * w:2 * t] == dc[:, 1]).all()
+    at = 2 * t + p * (2 + nb)
+    assert (flat[2 * t:at].reshape(p, 2 + nb) == pf[:, 2 * w:]).all()
+    assert (flat[at:].reshape(d, 2 + mb) == dc[:, 2:]).all()
