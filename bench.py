@@ -105,7 +105,7 @@ def bench_decode(steps: int, warmup: int, device: torch.device):
     slots = w.slot_mapping.to(device)
     out = torch.empty((batch, wl.NUM_HEADS * wl.HEAD_DIM), dtype=torch.bfloat16, device=device)
     ws_bytes = data_plane.paged_decode_workspace_bytes(batch, block_tables.shape[1], wl.NUM_HEADS,
-                                                       wl.HEAD_DIM, wl.BLOCK_SIZE)
+                                                       wl.HEAD_DIM, wl.BLOCK_SIZE, wl.NUM_KV_HEADS)
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     keys = [w.pools[l, 0] for l in range(w.num_layers)]
     values = [w.pools[l, 1] for l in range(w.num_layers)]

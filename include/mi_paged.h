@@ -104,7 +104,7 @@ int32_t mi_gather_blocks(const void* const* key_pools, const void* const* value_
  * batch or max_blocks is 0.  No initialisation needed.
  */
 int64_t mi_paged_decode_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t num_heads,
-                                        int32_t head_dim, int32_t block_size);
+                                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size);
 
 /*
  * Kernel 3 -- paged GQA decode attention (one query token per sequence).
@@ -133,8 +133,10 @@ int64_t mi_paged_decode_workspace_bytes(int32_t batch, int32_t max_blocks, int32
  *   head) per CU with max_blocks <= 512 run a single per-sequence kernel instead, which
  *   leaves the workspace untouched; the environment variable MI_DECODE_PATH=stream or =seq
  *   forces either kernel where both apply.
- * Specialised for head_dim 128, block_size 16 and num_heads = 2 * num_kv_heads with
- * num_kv_heads in {1, 2, 4, 8}; other shapes return MI_ERR_UNSUPPORTED.
+ * Specialised for head_dim 128, block_size 16, num_kv_heads in {1, 2, 4, 8} and GQA groups
+ * num_heads / num_kv_heads in {1, 2, 4, 5, 8} (query head h reads KV head h / group, as
+ * _repeat_key_value does, src/mini_infra/model/qwen3.py:147-156); other shapes return
+ * MI_ERR_UNSUPPORTED.
  */
 int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, const void* query,
                                   int64_t query_row_stride, int64_t query_head_stride,
@@ -191,8 +193,8 @@ int32_t mi_paged_decode_attention_fused(void* out, int64_t out_row_stride, const
  *   padded_len, head_dim] (row / head / token element strides, head_dim contiguous).
  * history_blocks: [batch, max_history_blocks] int64, row stride history_stride; ids outside
  *   [0, num_blocks) read block 0.  start_lens / chunk_lens: int64 with element stride lens_stride.
- * Specialised for head_dim 128, block_size 16, num_heads = 2 * num_kv_heads, num_kv_heads in
- * {1, 2, 4, 8}; strides multiples of 8 elements, key / value token strides below 2^24 elements,
+ * Specialised for head_dim 128, block_size 16, num_kv_heads in {1, 2, 4, 8} and num_heads any
+ * multiple of num_kv_heads (query head h reads KV head h / group); strides multiples of 8 elements, key / value token strides below 2^24 elements,
  * and 16-byte aligned tensors.
  */
 int32_t mi_chunked_prefill_attention(void* out, int64_t out_row_stride, int64_t out_tok_stride, const void* query,

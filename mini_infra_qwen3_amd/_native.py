@@ -41,7 +41,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i32,
         [_c_void_p_p, _c_void_p_p, _i64, _ptr, _i64, _i32, _i32, _c_void_p_p, _c_void_p_p, _i32, _i64, _ptr],
     ),
-    "mi_paged_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32]),
+    "mi_paged_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "mi_paged_decode_attention": (
         _i32,
         [_ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64, _i32, _ptr, _i64, _i32, _i32, _i32, _i32,

@@ -13,9 +13,11 @@
 // chunk keys j with L - len_b <= j <= i.  Rows i < L - len_b (padding) get a zero output.
 //
 // Tiling for gfx950 (v_mfma_f32_16x16x32_bf16, 64-lane wavefronts):
-//  * workgroup = (row b, KV head g, 128-query tile), 8 wavefronts (one workgroup per CU at two
-//    waves per SIMD): wave w serves query head 2 g + (w >> 2) and queries [32 (w & 3), +32) of
-//    the tile, so the two GQA heads share every K/V tile staged in LDS.
+//  * workgroup = (row b, query-head pair p of KV head g, 128-query tile), 8 wavefronts (one
+//    workgroup per CU at two waves per SIMD): wave w serves query head G g + 2 p + (w >> 2) of the
+//    GQA group of G heads on KV head g and queries [32 (w & 3), +32) of the tile, so the two
+//    heads share every K/V tile staged in LDS.  A group of G heads takes ceil(G / 2) pairs; when G
+//    is odd, the second half of its last pair repeats the group's last head and writes nothing.
 //  * KV tiles of 64 keys: history tiles first (pool blocks through the block table -- the
 //    gather is fused, nothing is materialised), then chunk tiles up to the causal limit.
 //    K is staged row-major (288-byte rows), V transposed (V^T) in double-buffered LDS; the loads
@@ -40,7 +42,7 @@ namespace {
 
 constexpr int kHeadDim = 128;
 constexpr int kBlockSize = 16;
-constexpr int kGroup = 2;
+constexpr int kGroup = 2;  // query heads per workgroup (a pair of one GQA group)
 #ifndef MI_PREFILL_WAVES_PER_HEAD
 #define MI_PREFILL_WAVES_PER_HEAD 4
 #endif
@@ -99,6 +101,8 @@ struct PrefillArgs {
   const int64_t* chunk_lens;
   int64_t lens_stride;
   int32_t padded_len;
+  int32_t group;   // query heads per KV head (G)
+  int32_t pairs;   // workgroups per KV head: ceil(G / 2)
   float scale;
 };
 
@@ -140,12 +144,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   __shared__ __align__(16) uint16_t sV[2][kHeadDim * kVStride];
   extern __shared__ int s_hblk[];  // [ceil(nh / 16)] history block ids of this row (dynamic LDS)
 
-  // Workgroup -> (row b, KV head g, query tile qt).  Consecutive workgroup ids go round-robin to
+  // Workgroup -> (row b, head pair hp, query tile qt).  Consecutive workgroup ids go round-robin to
   // the 8 XCDs, each with its own L2; so that the query tiles of one (row, head) -- which stream
   // the same K/V tiles -- share an L2, id L runs on XCD L % 8 and takes the (L / 8)-th tile of that
-  // XCD's (row, head) pairs in order.  Shapes whose pair count is not a multiple of 8 keep the
+  // XCD's (row, head pair) units in order.  Shapes whose pair count is not a multiple of 8 keep the
   // plain mapping.  Within a pair the heaviest (latest) query tiles start first.
-  int b, g, qt;
+  int b, hp, qt;
   {
     const int tiles = gridDim.x;
     const int pairs = gridDim.y * gridDim.z;
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
       pair = lin / tiles;
       rank = lin % tiles;
     }
-    g = pair % gridDim.y;
+    hp = pair % gridDim.y;
     b = pair / gridDim.y;
     qt = tiles - 1 - rank;
   }
@@ -178,7 +182,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform: keeps edge-tile branches real
   const int hh = w / kWavesPerHead;
   const int qs = w % kWavesPerHead;
-  const int h = g * kGroup + hh;
+  const int g = hp / a.pairs;                    // KV head
+  const int j0 = (hp - g * a.pairs) * kGroup;    // first head of the pair within the group
+  const bool head_live = j0 + hh < a.group;      // wave-uniform: false for the spare half of an odd group
+  const int h = g * a.group + min(j0 + hh, a.group - 1);
   const int ql = lane & 15;
   const int gq = lane >> 4;
 
@@ -187,8 +194,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
     for (int c = tid; c < kQTile * kGroup * (kHeadDim / 8); c += kThreads) {
       const int qi = q0 + c / (kGroup * (kHeadDim / 8));
       const int rem = c % (kGroup * (kHeadDim / 8));
-      const int head = g * kGroup + rem / (kHeadDim / 8);
-      if (qi < L)
+      const int jj = j0 + rem / (kHeadDim / 8);
+      const int head = g * a.group + jj;
+      if (qi < L && jj < a.group)
         *reinterpret_cast<uint4*>(out_b + qi * a.out_tok + head * kHeadDim + (rem % (kHeadDim / 8)) * 8) =
             uint4{0, 0, 0, 0};
     }
@@ -457,7 +465,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
     const float lt = oacc[8][nt][0];
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int qi = qw0 + 16 * nt + ql;
-    if (qi >= L) continue;
+    if (qi >= L || !head_live) continue;
     uint16_t* orow = out_b + qi * a.out_tok + h * kHeadDim + 4 * gq;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -487,11 +495,12 @@ extern "C" int32_t mi_chunked_prefill_attention(
   if (!out || !query || !key || !value || !start_lens || !chunk_lens ||
       (max_history_blocks > 0 && (!history_blocks || !key_pool || !value_pool)))
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_chunked_prefill_attention: null pointer argument");
-  if (head_dim != kHeadDim || block_size != kBlockSize || num_kv_heads <= 0 || num_heads != kGroup * num_kv_heads)
+  if (head_dim != kHeadDim || block_size != kBlockSize || num_kv_heads <= 0 || num_heads <= 0 ||
+      num_heads % num_kv_heads != 0)
     return fail(MI_ERR_UNSUPPORTED,
-                "mi_chunked_prefill_attention: needs head_dim %d, block_size %d, num_heads = %d * num_kv_heads "
-                "(got head_dim %d, block_size %d, heads %d/%d)",
-                kHeadDim, kBlockSize, kGroup, head_dim, block_size, num_heads, num_kv_heads);
+                "mi_chunked_prefill_attention: needs head_dim %d, block_size %d, num_heads a multiple of "
+                "num_kv_heads (got head_dim %d, block_size %d, heads %d/%d)",
+                kHeadDim, kBlockSize, head_dim, block_size, num_heads, num_kv_heads);
   if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
     return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: num_kv_heads %d not in {1,2,4,8}", num_kv_heads);
   const int64_t strides[] = {out_row_stride, out_tok_stride, query_row_stride, query_head_stride, query_tok_stride,
@@ -535,13 +544,15 @@ extern "C" int32_t mi_chunked_prefill_attention(
   a.chunk_lens = chunk_lens;
   a.lens_stride = lens_stride;
   a.padded_len = padded_len;
+  a.group = num_heads / num_kv_heads;
+  a.pairs = (a.group + kGroup - 1) / kGroup;
   a.scale = scale;
 
   if (num_blocks > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: pool too large");
   if (max_history_blocks > kMaxHistoryBlocks)
     return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: history of %d blocks exceeds %d", max_history_blocks,
                 kMaxHistoryBlocks);
-  dim3 grid((padded_len + kQTile - 1) / kQTile, num_kv_heads, batch);
+  dim3 grid((padded_len + kQTile - 1) / kQTile, num_kv_heads * a.pairs, batch);
   const size_t lds = sizeof(int) * static_cast<size_t>(max_history_blocks > 0 ? max_history_blocks : 1);
   hipStream_t s = as_stream(stream);
   switch (num_kv_heads) {

@@ -13,19 +13,20 @@
 //    Every workgroup gets the same number of blocks whatever the context lengths, and the
 //    head groups of one range run side by side (adjacent workgroup ids), so the 2 KiB pool
 //    rows of a block are read by concurrent workgroups.  Wavefront w of a group serves KV
-//    head g and both query heads 2g, 2g+1 that share it (GQA group 2): every K/V byte is
-//    loaded exactly once.
+//    head g and all G query heads G g .. G g + G - 1 that share it (the GQA group; 2 for
+//    Qwen3-0.6B, kernels compiled for G in {1, 2, 4, 5, 8}): every K/V byte is loaded exactly
+//    once.
 //  * Each workgroup first turns the context lengths into a prefix sum of blocks per sequence
 //    in LDS (so a block index maps to its sequence by binary search); block ids of the next
 //    64 blocks of the range are fetched one per lane, a window ahead, and broadcast with
 //    readlane.
 //  * Inside a wavefront, lane = 16 * row + dl.  Lane dl holds dims [8 dl, 8 dl + 8) of the
-//    two query rows; row r owns tokens 4 i + r (i = 0..3) of every 16-token block.  One
+//    G queries; row r owns tokens 4 i + r (i = 0..3) of every 16-token block.  One
 //    16-byte load per lane per i brings four 256-byte (token, head) rows per instruction.
 //  * QK^T: bf16 v_dot2 on packed pairs, then a 16-lane DPP butterfly (quad_perm, half-row
 //    mirror, row mirror) leaves the full dot product in every lane of the row.
 //  * Each row keeps its own online-softmax state (running max m, sum l, fp32 accumulator
-//    of 2 heads x 8 dims), so no cross-row traffic happens inside the block loop.  The max
+//    of G heads x 8 dims), so no cross-row traffic happens inside the block loop.  The max
 //    is rescaled lazily: only when a new score exceeds the running max by more than
 //    kRescaleSlack (log2 units) -- exact, since l and the accumulator share the same m.
 //  * PV: probabilities of token pairs are packed to bf16 and v_perm regroups V so that one
@@ -52,7 +53,6 @@ namespace {
 
 constexpr int kHeadDim = 128;
 constexpr int kBlockSize = 16;
-constexpr int kGroup = 2;          // query heads per KV head
 #ifndef MI_DECODE_DEPTH
 #define MI_DECODE_DEPTH 2
 #endif
@@ -215,7 +215,116 @@ __device__ __forceinline__ int row_of(const int* s_off, int batch, int64_t x) {
   return lo;
 }
 
-template <int kKvHeads, int kWaves>
+// Softmax state of one lane row (tokens 4 i + r of every block) for the kG query heads of its KV
+// head: running max m (log2 units), sum l and the fp32 accumulator of the lane's 8 dims.
+template <int kG>
+struct RowState {
+  float m[kG], l[kG], acc[kG][8];
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+      m[h] = -INFINITY;
+      l[h] = 0.0f;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[h][d] = 0.0f;
+    }
+  }
+};
+
+// One 16-token block (first token tok_base of a context of n tokens) for lane row r: scores of
+// tokens 4 i + r against the kG queries, lazy rescale, then P V.  Only a sequence's last block
+// can reach past its context; full blocks skip the masking (uniform branch).
+template <int kG>
+__device__ __forceinline__ void attend_block(RowState<kG>& st, const uint4 (&q)[kG], const u32x4 (&kb)[4],
+                                             const u32x4 (&vb)[4], float scale, int tok_base, int n, int r) {
+  float s[kG][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int h = 0; h < kG; ++h) s[h][i] = score_log2(dpp_sum16(dot8(q[h], kb[i])), scale);
+  if (tok_base + kBlockSize > n) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool valid = tok_base + 4 * i + r < n;
+#pragma unroll
+      for (int h = 0; h < kG; ++h) s[h][i] = valid ? s[h][i] : -INFINITY;
+    }
+  }
+  float mb[kG];
+  bool grow = false;
+#pragma unroll
+  for (int h = 0; h < kG; ++h) {
+    mb[h] = fmaxf(fmaxf(s[h][0], s[h][1]), fmaxf(s[h][2], s[h][3]));
+    grow = grow || mb[h] > st.m[h] + kRescaleSlack;
+  }
+  if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // lazy rescale (wave-uniform branch)
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+      const float nm = fmaxf(st.m[h], mb[h]);
+      const float al = (nm == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(st.m[h] - nm);
+      st.m[h] = nm;
+      st.l[h] *= al;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) st.acc[h][d] *= al;
+    }
+  }
+  // exp2(-inf) = 0 covers masked tokens; a row with no valid token yet keeps m = -inf, so the
+  // reference point falls back to 0 there to avoid -inf - -inf.
+  uint32_t ph[kG][2];
+#pragma unroll
+  for (int h = 0; h < kG; ++h) {
+    const float ref = st.m[h] == -INFINITY ? 0.0f : st.m[h];
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(s[h][i] - ref);
+    st.l[h] += (p[0] + p[1]) + (p[2] + p[3]);
+    ph[h][0] = pack_p(p[0], p[1]);
+    ph[h][1] = pack_p(p[2], p[3]);
+  }
+  // P V over token pairs (0,1) and (2,3): v_perm regroups V so that one v_dot2 covers two tokens
+  // of one dim; the regrouped V serves every head of the group.
+#pragma unroll
+  for (int pr = 0; pr < 2; ++pr) {
+    const u32x4 va = vb[2 * pr];
+    const u32x4 vc = vb[2 * pr + 1];
+    const uint32_t aw[4] = {va[0], va[1], va[2], va[3]};
+    const uint32_t cw[4] = {vc[0], vc[1], vc[2], vc[3]};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t plo = __builtin_amdgcn_perm(cw[w], aw[w], 0x05040100u);  // (a.lo, c.lo)
+      const uint32_t phi = __builtin_amdgcn_perm(cw[w], aw[w], 0x07060302u);  // (a.hi, c.hi)
+#pragma unroll
+      for (int h = 0; h < kG; ++h) {
+        st.acc[h][2 * w] = fdot2(ph[h][pr], plo, st.acc[h][2 * w]);
+        st.acc[h][2 * w + 1] = fdot2(ph[h][pr], phi, st.acc[h][2 * w + 1]);
+      }
+    }
+  }
+}
+
+// Merges the four lane rows of a wavefront (log-sum-exp): afterwards every row holds, per head,
+// the wavefront's max M, sum l and accumulator.
+template <int kG>
+__device__ __forceinline__ void merge_rows(RowState<kG>& st, float (&M)[kG]) {
+#pragma unroll
+  for (int h = 0; h < kG; ++h) {
+    float mx = fmaxf(st.m[h], __shfl_xor(st.m[h], 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    M[h] = mx;
+    const float wt = (st.m[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(st.m[h] - mx);
+    st.l[h] *= wt;
+    st.l[h] += __shfl_xor(st.l[h], 16);
+    st.l[h] += __shfl_xor(st.l[h], 32);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      st.acc[h][d] *= wt;
+      st.acc[h][d] += __shfl_xor(st.acc[h][d], 16);
+      st.acc[h][d] += __shfl_xor(st.acc[h][d], 32);
+    }
+  }
+}
+
+template <int kKvHeads, int kWaves, int kG>
 // Second bound: minimum wavefronts per SIMD, so that kGroupsPerCu workgroups fit on a CU
 // (4 SIMDs per CU) and the whole grid is resident.
 __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void paged_decode_kernel(const DecodeArgs a) {
@@ -223,7 +332,7 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
   constexpr int kRowElems = kKvHeads * kHeadDim;     // elements of one pool row (token)
   constexpr int kBlockElems = kBlockSize * kRowElems;
   constexpr int kHeadGroups = kKvHeads / kWaves;
-  constexpr int kHeads = kKvHeads * kGroup;
+  constexpr int kHeads = kKvHeads * kG;
 
   extern __shared__ int s_off[];                     // [batch + 1] block prefix sums
   __shared__ int s_wave[kWaves];
@@ -287,14 +396,12 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
     const int64_t row_lo = s_off[b], row_hi = s_off[b + 1];
     const int64_t seg_end = min(hi, row_hi);
     const int n32 = static_cast<int>(context_of(a, b));  // contexts are bounded by max_blocks * 16 < 2^31
-    const uint16_t* qp = a.query + b * a.q_row + (g * kGroup) * a.q_head + 8 * dl;
-    const uint4 q0 = *reinterpret_cast<const uint4*>(qp);
-    const uint4 q1 = *reinterpret_cast<const uint4*>(qp + a.q_head);
-
-    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
-    float acc0[8], acc1[8];
+    const uint16_t* qp = a.query + b * a.q_row + (g * kG) * a.q_head + 8 * dl;
+    uint4 q[kG];
 #pragma unroll
-    for (int d = 0; d < 8; ++d) acc0[d] = acc1[d] = 0.0f;
+    for (int j = 0; j < kG; ++j) q[j] = *reinterpret_cast<const uint4*>(qp + j * a.q_head);
+    RowState<kG> st;
+    st.init();
 
     const int64_t seg_begin = x;
     for (int64_t x0 = x - (x - lo) % kDepth; x0 < seg_end; x0 += kDepth) {
@@ -303,118 +410,28 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
         const int64_t xb = x0 + s;
         if (xb < seg_begin || xb >= seg_end) continue;  // wave-uniform
         issue((s + kDepth - 1) % kDepth, xb + kDepth - 1);
-
-        // ---- scores of tokens 4 i + r of block xb, both query heads.  Only a sequence's
-        // last block can reach past its context; full blocks skip the masking (uniform branch).
-        float s0[4], s1[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s0[i] = score_log2(dpp_sum16(dot8(q0, kbuf[s][i])), scale);
-          s1[i] = score_log2(dpp_sum16(dot8(q1, kbuf[s][i])), scale);
-        }
-        const int tok_base = static_cast<int>(xb - row_lo) * kBlockSize;
-        if (tok_base + kBlockSize > n32) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool valid = tok_base + 4 * i + r < n32;
-            s0[i] = valid ? s0[i] : -INFINITY;
-            s1[i] = valid ? s1[i] : -INFINITY;
-          }
-        }
-        const float mb0 = fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3]));
-        const float mb1 = fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]));
-
-        // ---- lazy rescale (wave-uniform branch)
-        const bool grow = (mb0 > m0 + kRescaleSlack) || (mb1 > m1 + kRescaleSlack);
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-          const float n0 = fmaxf(m0, mb0), n1 = fmaxf(m1, mb1);
-          const float a0 = (n0 == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m0 - n0);
-          const float a1 = (n1 == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m1 - n1);
-          m0 = n0;
-          m1 = n1;
-          l0 *= a0;
-          l1 *= a1;
-#pragma unroll
-          for (int d = 0; d < 8; ++d) {
-            acc0[d] *= a0;
-            acc1[d] *= a1;
-          }
-        }
-        // exp2(-inf) = 0 covers masked tokens; a row with no valid token yet keeps m = -inf,
-        // so the reference point falls back to 0 there to avoid -inf - -inf.
-        const float r0 = m0 == -INFINITY ? 0.0f : m0;
-        const float r1 = m1 == -INFINITY ? 0.0f : m1;
-        float p0[4], p1[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p0[i] = __builtin_amdgcn_exp2f(s0[i] - r0);
-          p1[i] = __builtin_amdgcn_exp2f(s1[i] - r1);
-        }
-        l0 += (p0[0] + p0[1]) + (p0[2] + p0[3]);
-        l1 += (p1[0] + p1[1]) + (p1[2] + p1[3]);
-
-        // ---- P V over token pairs (0,1) and (2,3)
-#pragma unroll
-        for (int pr = 0; pr < 2; ++pr) {
-          const uint32_t ph0 = pack_p(p0[2 * pr], p0[2 * pr + 1]);
-          const uint32_t ph1 = pack_p(p1[2 * pr], p1[2 * pr + 1]);
-          const u32x4 va = vbuf[s][2 * pr];
-          const u32x4 vc = vbuf[s][2 * pr + 1];
-          const uint32_t aw[4] = {va[0], va[1], va[2], va[3]};
-          const uint32_t cw[4] = {vc[0], vc[1], vc[2], vc[3]};
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const uint32_t plo = __builtin_amdgcn_perm(cw[w], aw[w], 0x05040100u);  // (a.lo, c.lo)
-            const uint32_t phi = __builtin_amdgcn_perm(cw[w], aw[w], 0x07060302u);  // (a.hi, c.hi)
-            acc0[2 * w] = fdot2(ph0, plo, acc0[2 * w]);
-            acc0[2 * w + 1] = fdot2(ph0, phi, acc0[2 * w + 1]);
-            acc1[2 * w] = fdot2(ph1, plo, acc1[2 * w]);
-            acc1[2 * w + 1] = fdot2(ph1, phi, acc1[2 * w + 1]);
-          }
-        }
+        attend_block<kG>(st, q, kbuf[s], vbuf[s], scale, static_cast<int>(xb - row_lo) * kBlockSize, n32, r);
       }
     }
     x = seg_end;
 
-    // ---- merge the four rows (log-sum-exp)
-    float M0 = fmaxf(m0, __shfl_xor(m0, 16));
-    M0 = fmaxf(M0, __shfl_xor(M0, 32));
-    float M1 = fmaxf(m1, __shfl_xor(m1, 16));
-    M1 = fmaxf(M1, __shfl_xor(M1, 32));
-    const float w0 = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M0);
-    const float w1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - M1);
-    l0 *= w0;
-    l1 *= w1;
-    l0 += __shfl_xor(l0, 16);
-    l0 += __shfl_xor(l0, 32);
-    l1 += __shfl_xor(l1, 16);
-    l1 += __shfl_xor(l1, 32);
+    float M[kG];
+    merge_rows<kG>(st, M);
+    // Row r writes query heads g kG + j for j = r, r + 4, ... (every row has all after the merge).
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      acc0[d] *= w0;
-      acc1[d] *= w1;
-      acc0[d] += __shfl_xor(acc0[d], 16);
-      acc0[d] += __shfl_xor(acc0[d], 32);
-      acc1[d] += __shfl_xor(acc1[d], 16);
-      acc1[d] += __shfl_xor(acc1[d], 32);
-    }
-
-    // Row 0 writes query head 2g, row 1 query head 2g + 1 (every row has both after the merge).
-    const int h = g * kGroup + (r & 1);
-    float o[8];
-#pragma unroll
-    for (int d = 0; d < 8; ++d) o[d] = (r & 1) == 0 ? acc0[d] : acc1[d];
-    if (r < kGroup) {
+    for (int j = 0; j < kG; ++j) {
+      if ((j & 3) != r) continue;
+      const int h = g * kG + j;
       if (row_lo >= lo && row_hi <= hi) {  // the whole sequence is in this range
-        store_bf16x8(a.out + b * a.out_row + h * kHeadDim + 8 * dl, o, 1.0f / ((r & 1) == 0 ? l0 : l1));
+        store_bf16x8(a.out + b * a.out_row + h * kHeadDim + 8 * dl, st.acc[j], 1.0f / st.l[j]);
       } else {  // cut sequence: slot 0 if it began before this range (its first), else 1 (its last)
         const int64_t slot = (static_cast<int64_t>(stream) * 2 + (row_lo < lo ? 0 : 1)) * kHeads + h;
         float4* dst = reinterpret_cast<float4*>(a.ws_acc + slot * kHeadDim + 8 * dl);
-        dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-        dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+        dst[0] = make_float4(st.acc[j][0], st.acc[j][1], st.acc[j][2], st.acc[j][3]);
+        dst[1] = make_float4(st.acc[j][4], st.acc[j][5], st.acc[j][6], st.acc[j][7]);
         if (dl == 0) {
-          a.ws_ml[slot * 2 + 0] = (r & 1) == 0 ? M0 : M1;
-          a.ws_ml[slot * 2 + 1] = (r & 1) == 0 ? l0 : l1;
+          a.ws_ml[slot * 2 + 0] = M[j];
+          a.ws_ml[slot * 2 + 1] = st.l[j];
         }
       }
     }
@@ -445,14 +462,14 @@ constexpr int kSeqMaxBlocks = 64 * kSeqWaves;  // a lane holds one block id of i
 // barrier after the pool stores makes them visible to the workgroup's own loads of that block
 // (the slot's lines are not in the CU cache before: no other workgroup reads head g of this
 // sequence, and the cache starts every launch clean).
-template <int kKvHeads, bool kFused>
+template <int kKvHeads, int kG, bool kFused>
 __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const DecodeArgs a) {
   constexpr int kRowElems = kKvHeads * kHeadDim;
   constexpr int kBlockElems = kBlockSize * kRowElems;
   constexpr int kSeqDepth = MI_DECODE_SEQ_DEPTH;  // ring: the next kSeqDepth - 1 blocks of the wavefront in flight
-  __shared__ float s_acc[kSeqWaves][kGroup][kHeadDim];
-  __shared__ float s_ml[kSeqWaves][kGroup][2];
-  __shared__ __align__(16) uint16_t s_q[kFused ? kGroup : 1][kHeadDim];
+  __shared__ float s_acc[kSeqWaves][kG][kHeadDim];
+  __shared__ float s_ml[kSeqWaves][kG][2];
+  __shared__ __align__(16) uint16_t s_q[kFused ? kG : 1][kHeadDim];
   const int b = blockIdx.x;
   const int g = blockIdx.y;
   const int w = threadIdx.x >> 6;
@@ -460,17 +477,19 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
   const int dl = lane & 15;
   const int r = lane >> 4;
   if constexpr (kFused) {
-    static_assert(kSeqWaves > kGroup, "the fused prologue needs kGroup + 1 wavefronts");
-    if (w <= kGroup) {  // wave-uniform
-      const bool is_q = w < kGroup;
-      const uint16_t* src = is_q ? a.q_raw + b * a.q_raw_row + (g * kGroup + w) * kHeadDim
+    // Unit u < kG: query head g kG + u, normalised and rotated into LDS; unit kG: key head g,
+    // written with value head g into the sequence's new slot.  Wavefront w takes units
+    // w, w + kSeqWaves, ...
+    for (int u = w; u <= kG; u += kSeqWaves) {  // wave-uniform
+      const bool is_q = u < kG;
+      const uint16_t* src = is_q ? a.q_raw + b * a.q_raw_row + (g * kG + u) * kHeadDim
                                  : a.k_raw + b * a.k_raw_row + g * kHeadDim;
       float o0, o1;
       norm_rope_head(src, is_q ? a.q_weight : a.k_weight, a.cos + b * kHeadDim, a.sin + b * kHeadDim, a.eps, lane,
                      o0, o1);
       if (is_q) {
-        s_q[w][lane] = static_cast<uint16_t>(f32_to_bf16_bits(o0));
-        s_q[w][lane + 64] = static_cast<uint16_t>(f32_to_bf16_bits(o1));
+        s_q[u][lane] = static_cast<uint16_t>(f32_to_bf16_bits(o0));
+        s_q[u][lane + 64] = static_cast<uint16_t>(f32_to_bf16_bits(o1));
       } else {
         const int64_t slot = a.slot_mapping[b * a.slot_stride];
         if (slot >= 0 && slot < a.num_slots) {
@@ -488,9 +507,9 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
   }
   const int n = static_cast<int>(context_of(a, b));
   const int nblk = blocks_of(n);
-  uint16_t* out_b = a.out + b * a.out_row + (g * kGroup) * kHeadDim;  // query heads 2 g, 2 g + 1
+  uint16_t* out_b = a.out + b * a.out_row + (g * kG) * kHeadDim;  // query heads g kG .. g kG + kG - 1
   if (nblk == 0) {  // empty context: zero rows (uniform over the workgroup)
-    if (threadIdx.x < kGroup * 16) *reinterpret_cast<uint4*>(out_b + 8 * threadIdx.x) = uint4{0, 0, 0, 0};
+    if (threadIdx.x < kG * 16) *reinterpret_cast<uint4*>(out_b + 8 * threadIdx.x) = uint4{0, 0, 0, 0};
     return;
   }
   const float scale = a.scale;
@@ -505,20 +524,16 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
     id_lo = static_cast<uint32_t>(id);
     id_hi = static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32);
   }
-  uint4 q0, q1;
-  if constexpr (kFused) {
-    q0 = *reinterpret_cast<const uint4*>(&s_q[0][8 * dl]);
-    q1 = *reinterpret_cast<const uint4*>(&s_q[1][8 * dl]);
-  } else {
-    const uint16_t* qp = a.query + b * a.q_row + (g * kGroup) * a.q_head + 8 * dl;
-    q0 = *reinterpret_cast<const uint4*>(qp);
-    q1 = *reinterpret_cast<const uint4*>(qp + a.q_head);
-  }
-
-  float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
-  float acc0[8], acc1[8];
+  uint4 q[kG];
 #pragma unroll
-  for (int d = 0; d < 8; ++d) acc0[d] = acc1[d] = 0.0f;
+  for (int j = 0; j < kG; ++j) {
+    if constexpr (kFused)
+      q[j] = *reinterpret_cast<const uint4*>(&s_q[j][8 * dl]);
+    else
+      q[j] = *reinterpret_cast<const uint4*>(a.query + b * a.q_row + (g * kG + j) * a.q_head + 8 * dl);
+  }
+  RowState<kG> st;
+  st.init();
 
   u32x4 kbuf[kSeqDepth][4], vbuf[kSeqDepth][4];
   auto issue = [&](int slot, int i) {  // block w + kSeqWaves i, clamped to the wavefront's last
@@ -546,113 +561,36 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
         const int i = i0 + s;
         if (kSeqDepth > 1) issue((s + kSeqDepth - 1) % kSeqDepth, i + kSeqDepth - 1);
         else if (i > 0) issue(0, i);
-
-        float s0[4], s1[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          s0[t] = score_log2(dpp_sum16(dot8(q0, kbuf[s][t])), scale);
-          s1[t] = score_log2(dpp_sum16(dot8(q1, kbuf[s][t])), scale);
-        }
-        const int tok_base = (w + kSeqWaves * i) * kBlockSize;
-        if (tok_base + kBlockSize > n) {  // the sequence's last block (uniform branch)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const bool valid = tok_base + 4 * t + r < n;
-            s0[t] = valid ? s0[t] : -INFINITY;
-            s1[t] = valid ? s1[t] : -INFINITY;
-          }
-        }
-        const float mb0 = fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3]));
-        const float mb1 = fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]));
-        const bool grow = (mb0 > m0 + kRescaleSlack) || (mb1 > m1 + kRescaleSlack);
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-          const float n0 = fmaxf(m0, mb0), n1 = fmaxf(m1, mb1);
-          const float a0 = (n0 == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m0 - n0);
-          const float a1 = (n1 == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m1 - n1);
-          m0 = n0;
-          m1 = n1;
-          l0 *= a0;
-          l1 *= a1;
-#pragma unroll
-          for (int d = 0; d < 8; ++d) {
-            acc0[d] *= a0;
-            acc1[d] *= a1;
-          }
-        }
-        const float r0 = m0 == -INFINITY ? 0.0f : m0;
-        const float r1 = m1 == -INFINITY ? 0.0f : m1;
-        float p0[4], p1[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          p0[t] = __builtin_amdgcn_exp2f(s0[t] - r0);
-          p1[t] = __builtin_amdgcn_exp2f(s1[t] - r1);
-        }
-        l0 += (p0[0] + p0[1]) + (p0[2] + p0[3]);
-        l1 += (p1[0] + p1[1]) + (p1[2] + p1[3]);
-#pragma unroll
-        for (int pr = 0; pr < 2; ++pr) {
-          const uint32_t ph0 = pack_p(p0[2 * pr], p0[2 * pr + 1]);
-          const uint32_t ph1 = pack_p(p1[2 * pr], p1[2 * pr + 1]);
-          const u32x4 va = vbuf[s][2 * pr];
-          const u32x4 vc = vbuf[s][2 * pr + 1];
-          const uint32_t aw[4] = {va[0], va[1], va[2], va[3]};
-          const uint32_t cw[4] = {vc[0], vc[1], vc[2], vc[3]};
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t plo = __builtin_amdgcn_perm(cw[q], aw[q], 0x05040100u);
-            const uint32_t phi = __builtin_amdgcn_perm(cw[q], aw[q], 0x07060302u);
-            acc0[2 * q] = fdot2(ph0, plo, acc0[2 * q]);
-            acc0[2 * q + 1] = fdot2(ph0, phi, acc0[2 * q + 1]);
-            acc1[2 * q] = fdot2(ph1, plo, acc1[2 * q]);
-            acc1[2 * q + 1] = fdot2(ph1, phi, acc1[2 * q + 1]);
-          }
-        }
+        attend_block<kG>(st, q, kbuf[s], vbuf[s], scale, (w + kSeqWaves * i) * kBlockSize, n, r);
       }
     }
   }
 
   // ---- merge the four rows of the wavefront (log-sum-exp), then the wavefronts through LDS
-  float M0 = fmaxf(m0, __shfl_xor(m0, 16));
-  M0 = fmaxf(M0, __shfl_xor(M0, 32));
-  float M1 = fmaxf(m1, __shfl_xor(m1, 16));
-  M1 = fmaxf(M1, __shfl_xor(M1, 32));
-  const float w0 = (m0 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m0 - M0);
-  const float w1 = (m1 == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m1 - M1);
-  l0 *= w0;
-  l1 *= w1;
-  l0 += __shfl_xor(l0, 16);
-  l0 += __shfl_xor(l0, 32);
-  l1 += __shfl_xor(l1, 16);
-  l1 += __shfl_xor(l1, 32);
+  float M[kG];
+  merge_rows<kG>(st, M);
 #pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    acc0[d] *= w0;
-    acc1[d] *= w1;
-    acc0[d] += __shfl_xor(acc0[d], 16);
-    acc0[d] += __shfl_xor(acc0[d], 32);
-    acc1[d] += __shfl_xor(acc1[d], 16);
-    acc1[d] += __shfl_xor(acc1[d], 32);
-  }
-  if (r < kGroup) {  // row 0: query head 2 g, row 1: 2 g + 1 (every row holds both after the merge)
+  for (int j = 0; j < kG; ++j) {  // row r holds heads j = r, r + 4, ... (every row has all after the merge)
+    if ((j & 3) != r) continue;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) s_acc[w][r][8 * dl + d] = r == 0 ? acc0[d] : acc1[d];
+    for (int d = 0; d < 8; ++d) s_acc[w][j][8 * dl + d] = st.acc[j][d];
     if (dl == 0) {
-      s_ml[w][r][0] = r == 0 ? M0 : M1;
-      s_ml[w][r][1] = r == 0 ? l0 : l1;
+      s_ml[w][j][0] = M[j];
+      s_ml[w][j][1] = st.l[j];
     }
   }
   __syncthreads();
-  if (threadIdx.x < kGroup * 16) {
+  if (threadIdx.x < kG * 16) {
     const int h = threadIdx.x >> 4;
     const int dm = threadIdx.x & 15;
-    float M = -INFINITY;
-    for (int v = 0; v < kSeqWaves; ++v) M = fmaxf(M, s_ml[v][h][0]);
+    float Mx = -INFINITY;
+    for (int v = 0; v < kSeqWaves; ++v) Mx = fmaxf(Mx, s_ml[v][h][0]);
     float L = 0.0f, o[8];
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[d] = 0.0f;
     for (int v = 0; v < kSeqWaves; ++v) {
       const float mv = s_ml[v][h][0];
-      const float e = mv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv - M);
+      const float e = mv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv - Mx);
       L += e * s_ml[v][h][1];
 #pragma unroll
       for (int d = 0; d < 8; ++d) o[d] += e * s_acc[v][h][8 * dm + d];
@@ -664,11 +602,14 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
 // Finishes what the stream kernel left: sequences cut by a range boundary (merge of their
 // partials: the cut range's last-sequence slot, then the first-sequence slot of every later
 // range up to the one holding the sequence's last block) and empty contexts (zero rows).
-// grid: batch; block: max(64, heads * 16) lanes, lane (h, dm) < heads * 16 owns dims
-// [8 dm, 8 dm + 8) of head h.
+// grid: batch; block: heads * 16 lanes rounded up to whole wavefronts, lane (h, dm) < heads * 16
+// owns dims [8 dm, 8 dm + 8) of head h.
 template <int kHeads>
-__global__ __launch_bounds__(kHeads * 16 < 64 ? 64 : kHeads * 16) void paged_decode_merge_kernel(const DecodeArgs a) {
-  constexpr int kThreads = kHeads * 16 < 64 ? 64 : kHeads * 16;
+constexpr int merge_threads() { return (kHeads * 16 + 63) / 64 * 64; }
+
+template <int kHeads>
+__global__ __launch_bounds__(merge_threads<kHeads>()) void paged_decode_merge_kernel(const DecodeArgs a) {
+  constexpr int kThreads = merge_threads<kHeads>();
   extern __shared__ int s_off[];
   __shared__ int s_wave[kThreads / 64];
   const int total = scan_blocks<kThreads>(a, s_off, s_wave);
@@ -776,21 +717,21 @@ bool use_seq_path(int32_t batch, int32_t max_blocks, int32_t num_kv_heads) {
   return static_cast<int64_t>(batch) * num_kv_heads <= device_cus();
 }
 
-template <int kKvHeads, bool kFused = false>
+template <int kKvHeads, int kG, bool kFused>
 int32_t launch_decode(const DecodeArgs& a, bool seq_path, hipStream_t s) {
   constexpr int kWaves = kKvHeads < kMaxWaves ? kKvHeads : kMaxWaves;
   constexpr int kHeadGroups = kKvHeads / kWaves;
-  constexpr int kHeads = kKvHeads * kGroup;
-  constexpr int kMergeThreads = kHeads * 16 < 64 ? 64 : kHeads * 16;
+  constexpr int kHeads = kKvHeads * kG;
+  constexpr int kMergeThreads = merge_threads<kHeads>();
   const size_t lds = sizeof(int) * (static_cast<size_t>(a.batch) + 1);
   if (seq_path) {
     if (a.max_blocks > kSeqMaxBlocks) return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: table too long");
-    paged_decode_seq_kernel<kKvHeads, kFused><<<dim3(a.batch, kKvHeads), 64 * kSeqWaves, 0, s>>>(a);
+    paged_decode_seq_kernel<kKvHeads, kG, kFused><<<dim3(a.batch, kKvHeads), 64 * kSeqWaves, 0, s>>>(a);
     return check_launch("mi_paged_decode_attention(seq)");
   }
   if constexpr (kFused) return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: fused form needs the per-sequence kernel");
   if (a.max_blocks > 0) {
-    paged_decode_kernel<kKvHeads, kWaves><<<static_cast<uint32_t>(a.streams) * kHeadGroups, 64 * kWaves, lds, s>>>(a);
+    paged_decode_kernel<kKvHeads, kWaves, kG><<<static_cast<uint32_t>(a.streams) * kHeadGroups, 64 * kWaves, lds, s>>>(a);
     int32_t rc = check_launch("mi_paged_decode_attention");
     if (rc != MI_OK) return rc;
   }
@@ -798,16 +739,57 @@ int32_t launch_decode(const DecodeArgs& a, bool seq_path, hipStream_t s) {
   return check_launch("mi_paged_decode_attention(merge)");
 }
 
+// GQA groups (query heads per KV head) with compiled kernels: Qwen3 dense models use 2 (0.6B,
+// 1.7B), 4 (4B, 8B), 5 (14B) and 8 (32B); 1 is multi-head attention.
+bool group_supported(int group) { return group == 1 || group == 2 || group == 4 || group == 5 || group == 8; }
+
+template <int kG, bool kFused>
+int32_t launch_for_kv_heads(const DecodeArgs& a, int32_t num_kv_heads, bool seq_path, hipStream_t s) {
+  switch (num_kv_heads) {
+    case 1: return launch_decode<1, kG, kFused>(a, seq_path, s);
+    case 2: return launch_decode<2, kG, kFused>(a, seq_path, s);
+    case 4: return launch_decode<4, kG, kFused>(a, seq_path, s);
+    default: return launch_decode<8, kG, kFused>(a, seq_path, s);
+  }
+}
+
+template <bool kFused>
+int32_t launch_for_heads(const DecodeArgs& a, int32_t num_heads, int32_t num_kv_heads, bool seq_path, hipStream_t s) {
+  switch (num_heads / num_kv_heads) {
+    case 1: return launch_for_kv_heads<1, kFused>(a, num_kv_heads, seq_path, s);
+    case 2: return launch_for_kv_heads<2, kFused>(a, num_kv_heads, seq_path, s);
+    case 4: return launch_for_kv_heads<4, kFused>(a, num_kv_heads, seq_path, s);
+    case 5: return launch_for_kv_heads<5, kFused>(a, num_kv_heads, seq_path, s);
+    default: return launch_for_kv_heads<8, kFused>(a, num_kv_heads, seq_path, s);
+  }
+}
+
+// Shape checks shared by the entry points; returns MI_OK or the error it recorded.
+int32_t check_heads(const char* what, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size) {
+  if (head_dim != kHeadDim || block_size != kBlockSize || num_kv_heads <= 0 || num_heads <= 0 ||
+      num_heads % num_kv_heads != 0)
+    return fail(MI_ERR_UNSUPPORTED,
+                "%s: needs head_dim %d, block_size %d, num_heads a multiple of num_kv_heads "
+                "(got head_dim %d, block_size %d, heads %d/%d)",
+                what, kHeadDim, kBlockSize, head_dim, block_size, num_heads, num_kv_heads);
+  if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
+    return fail(MI_ERR_UNSUPPORTED, "%s: num_kv_heads %d not in {1,2,4,8}", what, num_kv_heads);
+  if (!group_supported(num_heads / num_kv_heads))
+    return fail(MI_ERR_UNSUPPORTED, "%s: %d query heads per KV head not in {1,2,4,5,8}", what,
+                num_heads / num_kv_heads);
+  return MI_OK;
+}
+
 }  // namespace
 }  // namespace mi
 
 extern "C" int64_t mi_paged_decode_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t num_heads,
-                                                   int32_t head_dim, int32_t block_size) {
+                                                   int32_t num_kv_heads, int32_t head_dim, int32_t block_size) {
   using namespace mi;
-  if (batch <= 0 || max_blocks <= 0 || num_heads <= 0 || head_dim <= 0 || block_size != kBlockSize ||
-      num_heads % kGroup != 0)
+  if (batch <= 0 || max_blocks <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      block_size != kBlockSize || num_heads % num_kv_heads != 0)
     return 0;
-  const int64_t streams = streams_for(batch, max_blocks, num_heads / kGroup);
+  const int64_t streams = streams_for(batch, max_blocks, num_kv_heads);
   return streams * 2 * num_heads * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
 }
 
@@ -825,13 +807,8 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
   if (batch == 0) return ok();
   if (!out || !query || !key_pool || !value_pool || !context_lens || (max_blocks > 0 && !block_tables))
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention: null pointer argument");
-  if (head_dim != kHeadDim || block_size != kBlockSize || num_kv_heads <= 0 || num_heads != kGroup * num_kv_heads)
-    return fail(MI_ERR_UNSUPPORTED,
-                "mi_paged_decode_attention: needs head_dim %d, block_size %d, num_heads = %d * num_kv_heads "
-                "(got head_dim %d, block_size %d, heads %d/%d)",
-                kHeadDim, kBlockSize, kGroup, head_dim, block_size, num_heads, num_kv_heads);
-  if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
-    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: num_kv_heads %d not in {1,2,4,8}", num_kv_heads);
+  if (const int32_t rc = check_heads("mi_paged_decode_attention", num_heads, num_kv_heads, head_dim, block_size))
+    return rc;
   if (!aligned16(out) || !aligned16(query) || !aligned16(key_pool) || !aligned16(value_pool) ||
       out_row_stride % 8 != 0 || query_row_stride % 8 != 0 || query_head_stride % 8 != 0)
     return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: query/out/pools must be 16-byte aligned");
@@ -843,7 +820,7 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
     return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention: max_blocks %d too large", max_blocks);
 
   const int32_t streams = streams_for(batch, max_blocks, num_kv_heads);
-  const int64_t need = mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size);
+  const int64_t need = mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, num_kv_heads, head_dim, block_size);
   if (max_blocks > 0 && (!workspace || workspace_bytes < need))
     return fail(MI_ERR_WORKSPACE, "mi_paged_decode_attention: workspace of %lld bytes needed, got %lld",
                 static_cast<long long>(need), static_cast<long long>(workspace_bytes));
@@ -877,13 +854,7 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
     a.scale = scale;
     a.ws_acc = ws_acc;
     a.ws_ml = ws_ml;
-    int32_t rc;
-    switch (num_kv_heads) {
-      case 1: rc = launch_decode<1>(a, seq_path, s); break;
-      case 2: rc = launch_decode<2>(a, seq_path, s); break;
-      case 4: rc = launch_decode<4>(a, seq_path, s); break;
-      default: rc = launch_decode<8>(a, seq_path, s); break;
-    }
+    const int32_t rc = launch_for_heads<false>(a, num_heads, num_kv_heads, seq_path, s);
     if (rc != MI_OK) return rc;
   }
   return ok();
@@ -904,7 +875,9 @@ extern "C" int32_t mi_paged_decode_attention_fused(
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: null pointer argument");
   if (num_blocks > INT64_MAX / kBlockSize)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: pool too large");
-  if (!use_seq_path(batch, max_blocks, num_kv_heads) || max_blocks == 0 || num_heads != kGroup * num_kv_heads) {
+  if (const int32_t rc = check_heads("mi_paged_decode_attention_fused", num_heads, num_kv_heads, head_dim, block_size))
+    return rc;
+  if (!use_seq_path(batch, max_blocks, num_kv_heads) || max_blocks == 0) {
     // Large launches: the two-launch form (the append and q rotation, then the stream kernel).
     int32_t rc = mi_qk_norm_rope(q_scratch, nullptr, nullptr, q, q_row_stride, k, k_row_stride, v, v_row_stride,
                                  q_weight, k_weight, cos, sin, batch, num_heads, num_kv_heads, head_dim, eps,
@@ -918,11 +891,6 @@ extern "C" int32_t mi_paged_decode_attention_fused(
   // One launch: the per-sequence kernel with the prologue.  Shape checks as in the two entry points.
   if (!out || !key_pool || !value_pool || !context_lens || !block_tables)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: null pointer argument");
-  if (head_dim != kHeadDim || block_size != kBlockSize)
-    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention_fused: needs head_dim %d, block_size %d", kHeadDim,
-                kBlockSize);
-  if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
-    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention_fused: num_kv_heads %d not in {1,2,4,8}", num_kv_heads);
   if (!aligned16(out) || !aligned16(key_pool) || !aligned16(value_pool) || out_row_stride % 8 != 0)
     return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention_fused: out/pools must be 16-byte aligned");
   if (block_table_stride < max_blocks || context_lens_stride <= 0 || q_row_stride < num_heads * head_dim ||
@@ -956,11 +924,5 @@ extern "C" int32_t mi_paged_decode_attention_fused(
   a.slot_stride = slot_stride;
   a.num_slots = num_blocks * kBlockSize;
   a.eps = eps;
-  hipStream_t s = as_stream(stream);
-  switch (num_kv_heads) {
-    case 1: return launch_decode<1, true>(a, true, s);
-    case 2: return launch_decode<2, true>(a, true, s);
-    case 4: return launch_decode<4, true>(a, true, s);
-    default: return launch_decode<8, true>(a, true, s);
-  }
+  return launch_for_heads<true>(a, num_heads, num_kv_heads, true, as_stream(stream));
 }

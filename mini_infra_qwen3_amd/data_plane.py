@@ -207,12 +207,15 @@ def _as_kernel_blocks(key_pool: torch.Tensor, value_pool: torch.Tensor, tables: 
     return kp, vp, (tables.unsqueeze(-1) * k + sub).reshape(tables.shape[0], tables.shape[1] * k)
 
 
-def paged_decode_workspace_bytes(batch: int, max_blocks: int, num_heads: int, head_dim: int, block_size: int) -> int:
+def paged_decode_workspace_bytes(batch: int, max_blocks: int, num_heads: int, head_dim: int, block_size: int,
+                                 num_kv_heads: int) -> int:
     """Workspace for ``paged_decode_attention`` on ``[batch, max_blocks]`` tables of a pool with
-    ``block_size``-token blocks (multiples of 16 count as 16-token sub-blocks)."""
+    ``block_size``-token blocks (multiples of 16 count as 16-token sub-blocks) and ``num_kv_heads``
+    KV heads."""
     if block_size > KERNEL_BLOCK_SIZE and block_size % KERNEL_BLOCK_SIZE == 0:
         max_blocks, block_size = max_blocks * (block_size // KERNEL_BLOCK_SIZE), KERNEL_BLOCK_SIZE
-    return int(_native.load().mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size))
+    return int(_native.load().mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, num_kv_heads, head_dim,
+                                                                        block_size))
 
 
 def paged_decode_attention(
@@ -264,7 +267,7 @@ def paged_decode_attention(
         return out
     lib = _native.load()
     stream = _stream(device)
-    need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size)
+    need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size, num_kv_heads)
     ws_ptr, ws_bytes = None, 0
     if need > 0:
         if workspace is None or workspace.numel() * workspace.element_size() < need:
@@ -343,7 +346,7 @@ def paged_decode_attention_fused(
     if batch == 0:
         return out
     q_scratch = torch.empty((batch, num_heads, head_dim), dtype=torch.bfloat16, device=device)
-    need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size)
+    need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size, num_kv_heads)
     ws_ptr, ws_bytes = None, 0
     if need > 0:
         if workspace is None or workspace.numel() * workspace.element_size() < need:

@@ -280,7 +280,7 @@ class Qwen3Model(nn.Module):
                 raise ValueError("kv_pools has a different number of layers than the model")
             need = data_plane.paged_decode_workspace_bytes(decode_rows, metadata.decode.block_tables.shape[1],
                                                           self.config.num_attention_heads, self.config.head_dim,
-                                                          pools[0][0].shape[1])
+                                                          pools[0][0].shape[1], self.config.num_key_value_heads)
             if need:
                 workspace = torch.empty(need, dtype=torch.uint8, device=device)
         elif isinstance(attn_metadata, PagedAttentionMetadata):
@@ -294,7 +294,7 @@ class Qwen3Model(nn.Module):
             pools = attn_metadata.kv_pools
             need = data_plane.paged_decode_workspace_bytes(batch, metadata.block_tables.shape[1],
                                                           self.config.num_attention_heads, self.config.head_dim,
-                                                          pools[0][0].shape[1])
+                                                          pools[0][0].shape[1], self.config.num_key_value_heads)
             if need:
                 workspace = torch.empty(need, dtype=torch.uint8, device=device)
         else:

@@ -44,15 +44,18 @@ def test_decode_workspace_size(native_lib):
     # (256 CUs x 4, over 4 head groups at 8 KV heads; 256 CUs assumed without a device), fewer
     # for launches under 16 blocks per range
     slot = 2 * 16 * 130 * 4
-    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 128, 16) == 256 * slot
-    assert native_lib.mi_paged_decode_workspace_bytes(256, 32, 16, 128, 16) == 256 * slot
-    assert native_lib.mi_paged_decode_workspace_bytes(4, 33, 16, 128, 16) == 9 * slot
-    assert native_lib.mi_paged_decode_workspace_bytes(16, 80, 16, 128, 16) == 80 * slot
-    assert native_lib.mi_paged_decode_workspace_bytes(1, 1, 16, 128, 16) == 1 * slot
-    assert native_lib.mi_paged_decode_workspace_bytes(0, 512, 16, 128, 16) == 0
-    assert native_lib.mi_paged_decode_workspace_bytes(8, 0, 16, 128, 16) == 0
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 8, 128, 16) == 256 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 32, 16, 8, 128, 16) == 256 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(4, 33, 16, 8, 128, 16) == 9 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(16, 80, 16, 8, 128, 16) == 80 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(1, 1, 16, 8, 128, 16) == 1 * slot
+    assert native_lib.mi_paged_decode_workspace_bytes(0, 512, 16, 8, 128, 16) == 0
+    assert native_lib.mi_paged_decode_workspace_bytes(8, 0, 16, 8, 128, 16) == 0
     # 2 KV heads: one head group, so ranges = 256 x 4
-    assert native_lib.mi_paged_decode_workspace_bytes(512, 512, 4, 128, 16) == 1024 * 2 * 4 * 130 * 4
+    assert native_lib.mi_paged_decode_workspace_bytes(512, 512, 4, 2, 128, 16) == 1024 * 2 * 4 * 130 * 4
+    # GQA group 4 on 8 KV heads: the ranges follow the KV heads, the slots the 32 query heads
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 32, 8, 128, 16) == 256 * 2 * 32 * 130 * 4
+    assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 3, 128, 16) == 0  # heads not a multiple
 
 
 def _ptrs(n):
@@ -94,11 +97,12 @@ def test_decode_rejects_unsupported_shapes_on_host(native_lib):
 
     assert call(dim=64) == _native.MI_ERR_UNSUPPORTED
     assert call(bs=8) == _native.MI_ERR_UNSUPPORTED
-    assert call(heads=24) == _native.MI_ERR_UNSUPPORTED
+    assert call(heads=24) == _native.MI_ERR_UNSUPPORTED  # GQA group 3: no kernel compiled for it
+    assert call(heads=20) == _native.MI_ERR_UNSUPPORTED  # not a multiple of the 8 KV heads
     assert call(heads=6, kv=3) == _native.MI_ERR_UNSUPPORTED
     assert call(max_blocks=40) == _native.MI_ERR_WORKSPACE  # no workspace
     assert b"workspace" in lib.mi_last_error()
-    need = lib.mi_paged_decode_workspace_bytes(2, 40, 16, 128, 16)
+    need = lib.mi_paged_decode_workspace_bytes(2, 40, 16, 8, 128, 16)
     assert call(max_blocks=40, ws=256, ws_bytes=need - 4) == _native.MI_ERR_WORKSPACE
 
 
@@ -120,7 +124,7 @@ def test_prefill_rejects_unsupported_shapes_on_host(native_lib):
 
     assert call(dim=64) == _native.MI_ERR_UNSUPPORTED
     assert call(bs=32) == _native.MI_ERR_UNSUPPORTED
-    assert call(heads=8) == _native.MI_ERR_UNSUPPORTED
+    assert call(heads=12) == _native.MI_ERR_UNSUPPORTED  # not a multiple of the 8 KV heads
     assert call(tok=100) == _native.MI_ERR_UNSUPPORTED  # stride not a multiple of 8 elements
     assert call(tok=1 << 24) == _native.MI_ERR_UNSUPPORTED  # key / value token stride >= 2^24 elements
     assert call(hstride=1) == _native.MI_ERR_INVALID_ARGUMENT

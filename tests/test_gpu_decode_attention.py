@@ -63,13 +63,13 @@ def test_decode_step_matches_fp64_textbook(native_lib, device):
     assert np.abs(got.numpy() - ref).max() <= TOL
 
 
-def random_case(seed, ctx, kv_heads=8, spare=8):
+def random_case(seed, ctx, kv_heads=8, spare=8, group=2):
     gen = torch.Generator().manual_seed(seed)
     num_blocks = 1 + sum(-(-n // 16) for n in ctx) + spare
     tables = workloads.permuted_tables(ctx, num_blocks, gen)
     kp = torch.randn(num_blocks, 16, kv_heads, 128, generator=gen).to(torch.bfloat16)
     vp = torch.randn(num_blocks, 16, kv_heads, 128, generator=gen).to(torch.bfloat16)
-    q = torch.randn(len(ctx), 2 * kv_heads, 128, generator=gen).to(torch.bfloat16)
+    q = torch.randn(len(ctx), group * kv_heads, 128, generator=gen).to(torch.bfloat16)
     return q, kp, vp, workloads.padded(tables), tables
 
 
@@ -115,6 +115,26 @@ def test_fewer_kv_heads(native_lib, device, kv_heads):
     got = run_kernel(q, kp, vp, bt, ctx, device)
     ref = oracle(q, kp, vp, bt, ctx)
     assert max_abs(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("kv_heads,group", [
+    (8, 4),   # Qwen3-4B / 8B: 32 query heads on 8 KV heads
+    (8, 5),   # Qwen3-14B: 40 on 8
+    (8, 8),   # Qwen3-32B: 64 on 8
+    (4, 8),   # 32 on 4
+    (8, 1),   # multi-head attention
+    (1, 4),
+])
+def test_gqa_groups(native_lib, device, kv_heads, group):
+    """Query head h reads KV head h // group (reference qwen3.py:147-156) for every compiled group,
+    with sequences cut between block ranges on the stream path."""
+    ctx = [70, 300, 5, 1, 513, 0, 33]
+    q, kp, vp, bt, _ = random_case(300 + 10 * kv_heads + group, ctx, kv_heads=kv_heads, group=group)
+    got = run_kernel(q, kp, vp, bt, ctx, device).view(len(ctx), -1)
+    ref = oracle(q, kp, vp, bt, ctx).view(len(ctx), -1)
+    live = [i for i, n in enumerate(ctx) if n > 0]
+    assert max_abs(got[live], ref[live]) <= TOL
+    assert not got[5].any()
 
 
 def test_packed_metadata_views(native_lib, device):
@@ -231,15 +251,16 @@ def two_launches(q, k, v, qw, kw, cos, sin, slots, kp, vp, tables, ctx):
     return data_plane.paged_decode_attention(q_rot, kp, vp, tables, ctx, SCALE)
 
 
-@pytest.mark.parametrize("batch,kv_heads,block_size", [(6, 8, 16), (1, 8, 16), (32, 8, 16), (40, 8, 16),
-                                                       (5, 2, 16), (7, 8, 32)])
-def test_fused_form_equals_norm_rope_then_attention(native_lib, device, batch, kv_heads, block_size):
+@pytest.mark.parametrize("batch,kv_heads,block_size,group", [
+    (6, 8, 16, 2), (1, 8, 16, 2), (32, 8, 16, 2), (40, 8, 16, 2), (5, 2, 16, 2), (7, 8, 32, 2),
+    (6, 8, 16, 4), (3, 8, 16, 5), (4, 4, 16, 8), (40, 8, 16, 4), (5, 8, 16, 1)])
+def test_fused_form_equals_norm_rope_then_attention(native_lib, device, batch, kv_heads, block_size, group):
     """mi_paged_decode_attention_fused (q/k norm + RoPE + append in the per-sequence kernel's
     prologue, or the two launches for batches past one workgroup per CU) against qk_norm_rope then
     paged_decode_attention: output and pool bit for bit, including a pad row (slot -1, context 0)
     and a context of one token (only the new one)."""
-    g = torch.Generator().manual_seed(batch * 10 + kv_heads)
-    heads = 2 * kv_heads
+    g = torch.Generator().manual_seed(batch * 10 + kv_heads + 1000 * (group - 2))
+    heads = group * kv_heads
     blocks_per = 40 * 16 // block_size
     nb = batch * blocks_per + 8
     bf = torch.bfloat16

@@ -15,7 +15,7 @@ TOL = 2e-2
 SCALE = 128 ** -0.5
 
 
-def make_case(seed, starts, lens, width=None, kv_heads=8, spare=4, value_view=False):
+def make_case(seed, starts, lens, width=None, kv_heads=8, spare=4, value_view=False, group=2):
     gen = torch.Generator().manual_seed(seed)
     width = width or max(lens)
     batch = len(lens)
@@ -24,7 +24,7 @@ def make_case(seed, starts, lens, width=None, kv_heads=8, spare=4, value_view=Fa
     tables = workloads.permuted_tables(totals, num_blocks, gen)
     kp = torch.randn(num_blocks, 16, kv_heads, 128, generator=gen).to(torch.bfloat16)
     vp = torch.randn(num_blocks, 16, kv_heads, 128, generator=gen).to(torch.bfloat16)
-    q = torch.randn(batch, 2 * kv_heads, width, 128, generator=gen).to(torch.bfloat16)
+    q = torch.randn(batch, group * kv_heads, width, 128, generator=gen).to(torch.bfloat16)
     k = torch.randn(batch, kv_heads, width, 128, generator=gen).to(torch.bfloat16)
     if value_view:  # as v_proj(...).view(B, L, H, D).transpose(1, 2) produces it
         v = torch.randn(batch, width, kv_heads, 128, generator=gen).to(torch.bfloat16).transpose(1, 2)
@@ -78,6 +78,22 @@ def test_value_as_transposed_view(native_lib, device):
 def test_fewer_kv_heads(native_lib, device, kv_heads):
     starts, lens = [20, 70], [45, 33]
     case = make_case(kv_heads, starts, lens, kv_heads=kv_heads)
+    got = run_gpu(*case, starts, lens, device)
+    check_against_oracle(got, *case, starts, lens)
+
+
+@pytest.mark.parametrize("kv_heads,group", [
+    (8, 4),   # Qwen3-4B / 8B: 32 query heads on 8 KV heads
+    (8, 5),   # Qwen3-14B: 40 on 8 (odd group: the last pair of each group is half used)
+    (8, 8),   # Qwen3-32B: 64 on 8
+    (4, 8),   # 32 on 4
+    (2, 1),   # multi-head attention
+    (4, 3),
+])
+def test_gqa_groups(native_lib, device, kv_heads, group):
+    """Query head h reads KV head h // group (reference qwen3.py:147-156) for any group size."""
+    starts, lens = [40, 0, 17], [70, 129, 5]
+    case = make_case(100 + 10 * kv_heads + group, starts, lens, kv_heads=kv_heads, group=group)
     got = run_gpu(*case, starts, lens, device)
     check_against_oracle(got, *case, starts, lens)
 

@@ -163,6 +163,54 @@ def test_paged_decode_matches_oracle_tokens_and_logits(models, bs):
                 assert_kv_close(layer, got, want.transpose(0, 1))
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(16, 4), (20, 4), (8, 8)], ids=["gqa4", "gqa5", "mha"])
+def test_other_gqa_groups_decode_like_the_oracle(heads, kv_heads):
+    """Models whose query heads share KV heads in groups other than 2 (Qwen3-4B/8B: 4, Qwen3-14B:
+    5, multi-head: 1) run the same kernels: prefill, then decode steps through the fused decode
+    kernel, give the oracle's greedy tokens and logits."""
+    cfg = Qwen3Config(vocab_size=1000, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=128)
+    model = Qwen3ForCausalLM(cfg)
+    init_random_(model, seed=3, std=0.05, untied_head_seed=99)
+    model = model.to(torch.bfloat16)
+    ref = qwen3_ref.ReferenceQwen3(cfg, {k: v.clone() for k, v in model.state_dict().items()}, "cuda:0")
+    model = model.to("cuda:0").eval()
+    prompts = prompts_of([45, 17, 3], seed=4)
+    manager = KVCacheManager(BS, num_blocks=32)
+    pool = make_pool(cfg, 32)
+    ref_pools = torch_ref.make_pools(cfg.num_hidden_layers, 32, BS, kv_heads, 128, device="cuda:0")
+    runner = PagedRunner(model)
+    for i, p in enumerate(prompts):
+        manager.allocate_slots(i, len(p))
+    tables = [manager.block_table(i) for i in range(3)]
+    lengths = [len(p) for p in prompts]
+    out = runner.run_prefill_step(prompts)
+    runner.store_prefill(pool, out.prefill_cache, tables, lengths, [0] * 3)
+    first, presents = qwen3_ref.prefill(ref, prompts)
+    qwen3_ref.store_prefill(ref_pools, presents, tables, lengths, [0] * 3, BS)
+    assert out.next_tokens == first
+    last = list(first)
+    with torch.inference_mode():
+        for _ in range(4):
+            for i in range(3):
+                assert manager.allocate_slots(i, 1)
+            tables = [manager.block_table(i) for i in range(3)]
+            ids, pos, meta = runner.prepare_decode_inputs(tables, last, lengths, BS)
+            logits = model(ids, position_ids=pos, attn_metadata=meta._replace(kv_pools=tuple(pool.kv_pools)),
+                           last_logits_only=True)[0][:, -1].float()
+            got = runner.run_decode_step(ids, pos, meta, pool)
+            want = qwen3_ref.decode_step(ref, tables, last, lengths, ref_pools, BS).float()
+            tol = LOGIT_RTOL * want.abs().max().item()
+            assert got.next_tokens == logits.argmax(-1).tolist()
+            assert (logits - want).abs().max().item() <= tol
+            # the oracle's greedy token, or one whose oracle logit ties the maximum within the logit
+            # tolerance (random weights do produce exact bf16 ties: the argmax is then arbitrary)
+            for row, token in enumerate(got.next_tokens):
+                assert token == want[row].argmax().item() or want[row, token] >= want[row].max() - tol
+            lengths = [n + 1 for n in lengths]
+            last = got.next_tokens
+
+
 def test_stale_data_in_recycled_blocks_is_masked(models):
     """test_paged_kv_cache.py:166-207: a request reusing freed, unzeroed blocks decodes exactly as
     one on a fresh pool."""
