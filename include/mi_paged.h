@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define MI_PAGED_ABI_VERSION 1
+#define MI_PAGED_ABI_VERSION 2  /* 2: mi_paged_decode_workspace_bytes takes num_kv_heads */
 
 #define MI_OK 0
 #define MI_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, bad stride  */

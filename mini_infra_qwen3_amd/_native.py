@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmi_paged.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MI_OK = 0
 MI_ERR_INVALID_ARGUMENT = -1
