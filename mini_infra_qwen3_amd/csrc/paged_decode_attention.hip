@@ -78,7 +78,22 @@ constexpr float kRescaleSlack = 8.0f;
 static_assert(kDepth >= 2 && kDepth - 1 < kWindow, "the ring looks ahead less than one id window");
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#ifndef MI_DECODE_MFMA_GROUP
+#define MI_DECODE_MFMA_GROUP 8
+#endif
+// GQA groups from this size up use the matrix-core form of the stream kernel (at most 16 heads,
+// the MFMA's column count); smaller groups keep the dot-product form.  Measured at batch 256
+// (8 KV heads, Σctx 755,887): the matrix-core form runs at 6.0-6.2 TB/s for every group, its K
+// loads being 64-byte pieces of 16 token rows; the dot-product form reads 256-byte rows and runs
+// at 6.8 / 6.7 / 6.4 / 6.3 TB/s for groups 1 / 2 / 4 / 5, but at 4.7 TB/s for 8, where its
+// per-token arithmetic outgrows the memory time.
+constexpr int kMfmaGroup = MI_DECODE_MFMA_GROUP;
 
 struct DecodeArgs {
   uint16_t* out;
@@ -324,6 +339,69 @@ __device__ __forceinline__ void merge_rows(RowState<kG>& st, float (&M)[kG]) {
   }
 }
 
+// ---- Matrix-core form (groups of kMfmaGroup..16 query heads).  Per 16-token block and wavefront:
+//  * S^T = K Q^T with four v_mfma_f32_16x16x32_bf16 over the 128 dims: A = K (lane: token
+//    lane % 16, dims 32 ks + 8 (lane / 16) .. +8, one 16-byte pool load per ks), B = Q^T (lane:
+//    head lane % 16, zero past the group), C: lane holds head lane % 16, tokens 4 (lane / 16) + i.
+//  * That C layout is the A layout of v_mfma_f32_16x16x16_bf16 (row lane % 16, k = 4 (lane / 16)
+//    + i), so the probabilities feed O = P V without moving.  V is loaded as token 4 (lane / 16) + i,
+//    dims 8 (lane % 16) .. +8; output tile t takes dim 8 j + t as its column j, so B of tile t is
+//    element t of the lane's four V pieces (two v_perm) and the lane ends up holding, for heads
+//    4 (lane / 16) + i, dims 8 (lane % 16) .. +8: one 16-byte store per head.
+//  * Softmax per head column: the running max m is shared by the column's four lanes (raised
+//    lazily, with the column max, as in the dot-product form); each lane sums its own tokens.
+struct MfmaState {
+  float m;       // running max of head lane % 16 (log2 units), equal in the four lanes of its column
+  float l;       // this lane's share of the head's sum
+  f32x4 o[8];    // tile t: O[head 4 (lane / 16) + i][dim 8 (lane % 16) + t]
+};
+
+__device__ __forceinline__ void attend_block_mfma(MfmaState& st, const bf16x8 (&qf)[4], const u32x4 (&kb)[4],
+                                                  const u32x4 (&vb)[4], float scale, int tok_base, int n,
+                                                  int lane) {
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kb[ks]), qf[ks], acc, 0, 0, 0);
+  const int tok0 = tok_base + 4 * (lane >> 4);
+  float sc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sc[i] = score_log2(acc[i], scale);
+  if (tok_base + kBlockSize > n) {  // the sequence's last block (uniform branch)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i] = tok0 + i < n ? sc[i] : -INFINITY;
+  }
+  const float mb = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+  if (__builtin_amdgcn_ballot_w64(mb > st.m + kRescaleSlack) != 0) {  // lazy rescale (wave-uniform)
+    float cm = fmaxf(mb, __shfl_xor(mb, 16));
+    cm = fmaxf(cm, __shfl_xor(cm, 32));
+    const float nm = fmaxf(st.m, cm);
+    const float al = (nm == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(st.m - nm);
+    st.m = nm;
+    st.l *= al;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // O rows are heads 4 (lane / 16) + i: lane h holds head h's factor
+      const float ai = __shfl(al, 4 * (lane >> 4) + i);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) st.o[t][i] *= ai;
+    }
+  }
+  const float ref = st.m == -INFINITY ? 0.0f : st.m;
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - ref);
+  st.l += (p[0] + p[1]) + (p[2] + p[3]);
+  const bf16x4 pa = __builtin_convertvector((f32x4){p[0], p[1], p[2], p[3]}, bf16x4);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+    const uint32_t w01 = __builtin_amdgcn_perm(vb[1][t >> 1], vb[0][t >> 1], sel);  // tokens 0, 1 at dim t
+    const uint32_t w23 = __builtin_amdgcn_perm(vb[3][t >> 1], vb[2][t >> 1], sel);  // tokens 2, 3
+    const bf16x4 vbf = __builtin_bit_cast(bf16x4, (u32x2){w01, w23});
+    st.o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vbf, st.o[t], 0, 0, 0);
+  }
+}
+
 template <int kKvHeads, int kWaves, int kG>
 // Second bound: minimum wavefronts per SIMD, so that kGroupsPerCu workgroups fit on a CU
 // (4 SIMDs per CU) and the whole grid is resident.
@@ -333,6 +411,8 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
   constexpr int kBlockElems = kBlockSize * kRowElems;
   constexpr int kHeadGroups = kKvHeads / kWaves;
   constexpr int kHeads = kKvHeads * kG;
+  constexpr bool kMfma = kG >= kMfmaGroup;
+  static_assert(kG <= 16, "at most 16 query heads per KV head");
 
   extern __shared__ int s_off[];                     // [batch + 1] block prefix sums
   __shared__ int s_wave[kWaves];
@@ -348,8 +428,13 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
   const int r = lane >> 4;
   const int g = hg * kWaves + (threadIdx.x >> 6);
   const float scale = a.scale;
-  // Lane offset (elements) of its piece of token 4 i + r inside a block.
-  const int lane_off = r * kRowElems + g * kHeadDim + 8 * dl;
+  // Lane offsets (elements) of its first K and V pieces inside a block, and the step between its
+  // four pieces.  Dot-product form: tokens 4 i + r, dims 8 dl .. +8 for both.  Matrix-core form:
+  // K token dl, dims 32 i + 8 r .. +8; V token 4 r + i, dims 8 dl .. +8.
+  const int k_off = kMfma ? dl * kRowElems + g * kHeadDim + 8 * r : r * kRowElems + g * kHeadDim + 8 * dl;
+  const int v_off = kMfma ? 4 * r * kRowElems + g * kHeadDim + 8 * dl : k_off;
+  constexpr int kKStep = kMfma ? 32 : 4 * kRowElems;
+  constexpr int kVStep = kMfma ? kRowElems : 4 * kRowElems;
 
   // Block ids of window [base, base + 64), one per lane (indices past the range repeat its
   // last block; ids outside the pool read block 0).
@@ -380,12 +465,12 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
     const uint32_t blo = __builtin_amdgcn_readlane(cur_lo, j);
     const uint32_t bhi = __builtin_amdgcn_readlane(cur_hi, j);
     const int64_t base = static_cast<int64_t>((static_cast<uint64_t>(bhi) << 32) | blo) * kBlockElems;
-    const uint16_t* kp = a.key_pool + base + lane_off;
-    const uint16_t* vp = a.value_pool + base + lane_off;
+    const uint16_t* kp = a.key_pool + base + k_off;
+    const uint16_t* vp = a.value_pool + base + v_off;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kbuf[slot][i] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(kp + i * 4 * kRowElems));
+    for (int i = 0; i < 4; ++i) kbuf[slot][i] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(kp + i * kKStep));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vbuf[slot][i] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(vp + i * 4 * kRowElems));
+    for (int i = 0; i < 4; ++i) vbuf[slot][i] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(vp + i * kVStep));
   };
 #pragma unroll
   for (int s = 0; s < kDepth - 1; ++s) issue(s, lo + s);  // ring slot of block x: (x - lo) % kDepth
@@ -396,12 +481,24 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
     const int64_t row_lo = s_off[b], row_hi = s_off[b + 1];
     const int64_t seg_end = min(hi, row_hi);
     const int n32 = static_cast<int>(context_of(a, b));  // contexts are bounded by max_blocks * 16 < 2^31
-    const uint16_t* qp = a.query + b * a.q_row + (g * kG) * a.q_head + 8 * dl;
-    uint4 q[kG];
+    const uint16_t* qp = a.query + b * a.q_row + (g * kG) * a.q_head;
+    uint4 q[kMfma ? 1 : kG];
+    bf16x8 qf[4];
+    RowState<kMfma ? 1 : kG> st;
+    MfmaState ms;
+    if constexpr (kMfma) {  // Q^T fragments: head dl (zero past the group), dims 32 ks + 8 r .. +8
 #pragma unroll
-    for (int j = 0; j < kG; ++j) q[j] = *reinterpret_cast<const uint4*>(qp + j * a.q_head);
-    RowState<kG> st;
-    st.init();
+      for (int ks = 0; ks < 4; ++ks)
+        qf[ks] = dl < kG ? *reinterpret_cast<const bf16x8*>(qp + dl * a.q_head + 32 * ks + 8 * r) : bf16x8{};
+      ms.m = -INFINITY;
+      ms.l = 0.0f;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) ms.o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    } else {
+#pragma unroll
+      for (int j = 0; j < kG; ++j) q[j] = *reinterpret_cast<const uint4*>(qp + j * a.q_head + 8 * dl);
+      st.init();
+    }
 
     const int64_t seg_begin = x;
     for (int64_t x0 = x - (x - lo) % kDepth; x0 < seg_end; x0 += kDepth) {
@@ -410,19 +507,57 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
         const int64_t xb = x0 + s;
         if (xb < seg_begin || xb >= seg_end) continue;  // wave-uniform
         issue((s + kDepth - 1) % kDepth, xb + kDepth - 1);
-        attend_block<kG>(st, q, kbuf[s], vbuf[s], scale, static_cast<int>(xb - row_lo) * kBlockSize, n32, r);
+        const int tok_base = static_cast<int>(xb - row_lo) * kBlockSize;
+        if constexpr (kMfma)
+          attend_block_mfma(ms, qf, kbuf[s], vbuf[s], scale, tok_base, n32, lane);
+        else
+          attend_block<kG>(st, q, kbuf[s], vbuf[s], scale, tok_base, n32, r);
       }
     }
     x = seg_end;
+    const bool whole = row_lo >= lo && row_hi <= hi;  // the whole sequence is in this range
 
-    float M[kG];
-    merge_rows<kG>(st, M);
+    if constexpr (kMfma) {
+      // Column sums, then each lane's heads 4 r + i (their m and sum live in lanes 4 r + i).
+      float lsum = ms.l + __shfl_xor(ms.l, 16);
+      lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = 4 * r + i;
+        const float Lj = __shfl(lsum, j);
+        const float Mj = __shfl(ms.m, j);
+        if (j >= kG) continue;
+        const int h = g * kG + j;
+        float o[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t] = ms.o[t][i];
+        if (whole) {
+          store_bf16x8(a.out + b * a.out_row + h * kHeadDim + 8 * dl, o, 1.0f / Lj);
+        } else {  // cut sequence: slot 0 if it began before this range (its first), else 1 (its last)
+          const int64_t slot = (static_cast<int64_t>(stream) * 2 + (row_lo < lo ? 0 : 1)) * kHeads + h;
+          float4* dst = reinterpret_cast<float4*>(a.ws_acc + slot * kHeadDim + 8 * dl);
+          dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+          dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+          if (dl == 0) {
+            a.ws_ml[slot * 2 + 0] = Mj;
+            a.ws_ml[slot * 2 + 1] = Lj;
+          }
+        }
+      }
+      if (x < hi) {  // next non-empty sequence (uniform)
+        while (s_off[b + 1] <= x) ++b;
+      }
+      continue;
+    }
+
+    float M[kMfma ? 1 : kG];
+    merge_rows<kMfma ? 1 : kG>(st, M);
     // Row r writes query heads g kG + j for j = r, r + 4, ... (every row has all after the merge).
 #pragma unroll
-    for (int j = 0; j < kG; ++j) {
+    for (int j = 0; j < (kMfma ? 0 : kG); ++j) {
       if ((j & 3) != r) continue;
       const int h = g * kG + j;
-      if (row_lo >= lo && row_hi <= hi) {  // the whole sequence is in this range
+      if (whole) {
         store_bf16x8(a.out + b * a.out_row + h * kHeadDim + 8 * dl, st.acc[j], 1.0f / st.l[j]);
       } else {  // cut sequence: slot 0 if it began before this range (its first), else 1 (its last)
         const int64_t slot = (static_cast<int64_t>(stream) * 2 + (row_lo < lo ? 0 : 1)) * kHeads + h;
