@@ -648,7 +648,12 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
     return;
   }
   const float scale = a.scale;
-  const int lane_off = r * kRowElems + g * kHeadDim + 8 * dl;
+  constexpr bool kMfma = kG >= kMfmaGroup;  // lane layout and per-block arithmetic as in the stream kernel
+  static_assert(kG <= 16, "at most 16 query heads per KV head");
+  const int k_off = kMfma ? dl * kRowElems + g * kHeadDim + 8 * r : r * kRowElems + g * kHeadDim + 8 * dl;
+  const int v_off = kMfma ? 4 * r * kRowElems + g * kHeadDim + 8 * dl : k_off;
+  constexpr int kKStep = kMfma ? 32 : 4 * kRowElems;
+  constexpr int kVStep = kMfma ? kRowElems : 4 * kRowElems;
   const int cnt = nblk > w ? (nblk - 1 - w) / kSeqWaves + 1 : 0;  // blocks w + kSeqWaves i, i < cnt <= 64
 
   // Lane i holds the id of block w + kSeqWaves i (ids outside the pool read block 0).
@@ -659,16 +664,34 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
     id_lo = static_cast<uint32_t>(id);
     id_hi = static_cast<uint32_t>(static_cast<uint64_t>(id) >> 32);
   }
-  uint4 q[kG];
+  uint4 q[kMfma ? 1 : kG];
+  bf16x8 qf[4];
+  RowState<kMfma ? 1 : kG> st;
+  MfmaState ms;
+  if constexpr (kMfma) {  // Q^T fragments: head dl (zero past the group), dims 32 ks + 8 r .. +8
 #pragma unroll
-  for (int j = 0; j < kG; ++j) {
-    if constexpr (kFused)
-      q[j] = *reinterpret_cast<const uint4*>(&s_q[j][8 * dl]);
-    else
-      q[j] = *reinterpret_cast<const uint4*>(a.query + b * a.q_row + (g * kG + j) * a.q_head + 8 * dl);
+    for (int ks = 0; ks < 4; ++ks) {
+      if constexpr (kFused)
+        qf[ks] = dl < kG ? *reinterpret_cast<const bf16x8*>(&s_q[dl < kG ? dl : 0][32 * ks + 8 * r]) : bf16x8{};
+      else
+        qf[ks] = dl < kG ? *reinterpret_cast<const bf16x8*>(a.query + b * a.q_row + (g * kG + dl) * a.q_head +
+                                                            32 * ks + 8 * r)
+                         : bf16x8{};
+    }
+    ms.m = -INFINITY;
+    ms.l = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ms.o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  } else {
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+      if constexpr (kFused)
+        q[j] = *reinterpret_cast<const uint4*>(&s_q[j][8 * dl]);
+      else
+        q[j] = *reinterpret_cast<const uint4*>(a.query + b * a.q_row + (g * kG + j) * a.q_head + 8 * dl);
+    }
+    st.init();
   }
-  RowState<kG> st;
-  st.init();
 
   u32x4 kbuf[kSeqDepth][4], vbuf[kSeqDepth][4];
   auto issue = [&](int slot, int i) {  // block w + kSeqWaves i, clamped to the wavefront's last
@@ -676,12 +699,12 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
     const uint32_t blo = __builtin_amdgcn_readlane(id_lo, i);
     const uint32_t bhi = __builtin_amdgcn_readlane(id_hi, i);
     const int64_t base = static_cast<int64_t>((static_cast<uint64_t>(bhi) << 32) | blo) * kBlockElems;
-    const uint16_t* kp = a.key_pool + base + lane_off;
-    const uint16_t* vp = a.value_pool + base + lane_off;
+    const uint16_t* kp = a.key_pool + base + k_off;
+    const uint16_t* vp = a.value_pool + base + v_off;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) kbuf[slot][t] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(kp + t * 4 * kRowElems));
+    for (int t = 0; t < 4; ++t) kbuf[slot][t] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(kp + t * kKStep));
 #pragma unroll
-    for (int t = 0; t < 4; ++t) vbuf[slot][t] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(vp + t * 4 * kRowElems));
+    for (int t = 0; t < 4; ++t) vbuf[slot][t] = load_vec<kNtLoads>(reinterpret_cast<const u32x4*>(vp + t * kVStep));
   };
   if (cnt > 0) {  // wave-uniform
 #pragma unroll
@@ -696,16 +719,36 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
         const int i = i0 + s;
         if (kSeqDepth > 1) issue((s + kSeqDepth - 1) % kSeqDepth, i + kSeqDepth - 1);
         else if (i > 0) issue(0, i);
-        attend_block<kG>(st, q, kbuf[s], vbuf[s], scale, (w + kSeqWaves * i) * kBlockSize, n, r);
+        if constexpr (kMfma)
+          attend_block_mfma(ms, qf, kbuf[s], vbuf[s], scale, (w + kSeqWaves * i) * kBlockSize, n, lane);
+        else
+          attend_block<kG>(st, q, kbuf[s], vbuf[s], scale, (w + kSeqWaves * i) * kBlockSize, n, r);
       }
     }
   }
 
   // ---- merge the four rows of the wavefront (log-sum-exp), then the wavefronts through LDS
-  float M[kG];
-  merge_rows<kG>(st, M);
+  if constexpr (kMfma) {  // lane: heads 4 r + i, dims 8 dl .. +8; head j's max and sum live in lane j
+    float lsum = ms.l + __shfl_xor(ms.l, 16);
+    lsum += __shfl_xor(lsum, 32);
 #pragma unroll
-  for (int j = 0; j < kG; ++j) {  // row r holds heads j = r, r + 4, ... (every row has all after the merge)
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * r + i;
+      const float Lj = __shfl(lsum, j);
+      const float Mj = __shfl(ms.m, j);
+      if (j >= kG) continue;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) s_acc[w][j][8 * dl + t] = ms.o[t][i];
+      if (dl == 0) {
+        s_ml[w][j][0] = Mj;
+        s_ml[w][j][1] = Lj;
+      }
+    }
+  }
+  float M[kMfma ? 1 : kG];
+  if constexpr (!kMfma) merge_rows<kG>(st, M);
+#pragma unroll
+  for (int j = 0; j < (kMfma ? 0 : kG); ++j) {  // row r holds heads j = r, r + 4, ... (every row has all after the merge)
     if ((j & 3) != r) continue;
 #pragma unroll
     for (int d = 0; d < 8; ++d) s_acc[w][j][8 * dl + d] = st.acc[j][d];

@@ -163,10 +163,10 @@ def test_paged_decode_matches_oracle_tokens_and_logits(models, bs):
                 assert_kv_close(layer, got, want.transpose(0, 1))
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(16, 4), (20, 4), (8, 8)], ids=["gqa4", "gqa5", "mha"])
+@pytest.mark.parametrize("heads,kv_heads", [(16, 4), (20, 4), (32, 4), (8, 8)], ids=["gqa4", "gqa5", "gqa8", "mha"])
 def test_other_gqa_groups_decode_like_the_oracle(heads, kv_heads):
     """Models whose query heads share KV heads in groups other than 2 (Qwen3-4B/8B: 4, Qwen3-14B:
-    5, multi-head: 1) run the same kernels: prefill, then decode steps through the fused decode
+    5, Qwen3-32B: 8, on the matrix-core decode form; multi-head: 1) run the same kernels: prefill, then decode steps through the fused decode
     kernel, give the oracle's greedy tokens and logits."""
     cfg = Qwen3Config(vocab_size=1000, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                       num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=128)
