@@ -85,14 +85,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #ifndef MI_DECODE_MFMA_GROUP
-#define MI_DECODE_MFMA_GROUP 8
+#define MI_DECODE_MFMA_GROUP 4
 #endif
-// GQA groups from this size up use the matrix-core form of the stream kernel (at most 16 heads,
+// GQA groups from this size up use the matrix-core form of the decode kernels (at most 16 heads,
 // the MFMA's column count); smaller groups keep the dot-product form.  Measured at batch 256
-// (8 KV heads, Σctx 755,887): the matrix-core form runs at 6.0-6.2 TB/s for every group, its K
-// loads being 64-byte pieces of 16 token rows; the dot-product form reads 256-byte rows and runs
-// at 6.8 / 6.7 / 6.4 / 6.3 TB/s for groups 1 / 2 / 4 / 5, but at 4.7 TB/s for 8, where its
-// per-token arithmetic outgrows the memory time.
+// (8 KV heads, Σctx 755,887, attention + merge), TB/s for groups 1 / 2 / 4 / 5 / 8:
+// dot-product form 6.75 / 6.67 / 6.40 / 6.27 / 4.67 (its per-token arithmetic grows with the
+// group); matrix-core form 6.75 / 6.71 / 6.56 / 6.51 / 6.35.
 constexpr int kMfmaGroup = MI_DECODE_MFMA_GROUP;
 
 struct DecodeArgs {
@@ -341,8 +340,11 @@ __device__ __forceinline__ void merge_rows(RowState<kG>& st, float (&M)[kG]) {
 
 // ---- Matrix-core form (groups of kMfmaGroup..16 query heads).  Per 16-token block and wavefront:
 //  * S^T = K Q^T with four v_mfma_f32_16x16x32_bf16 over the 128 dims: A = K (lane: token
-//    lane % 16, dims 32 ks + 8 (lane / 16) .. +8, one 16-byte pool load per ks), B = Q^T (lane:
-//    head lane % 16, zero past the group), C: lane holds head lane % 16, tokens 4 (lane / 16) + i.
+//    lane % 16, dims 32 ks + 8 (lane / 16) .. +8), B = Q^T (lane: head lane % 16, zero past the
+//    group), C: lane holds head lane % 16, tokens 4 (lane / 16) + i.  K is loaded in whole
+//    256-byte token rows, as the dot-product form loads it, and restaged into the A layout
+//    through 16 LDS rows per wavefront (A straight from the pool would read 64-byte pieces of 16
+//    rows per instruction).
 //  * That C layout is the A layout of v_mfma_f32_16x16x16_bf16 (row lane % 16, k = 4 (lane / 16)
 //    + i), so the probabilities feed O = P V without moving.  V is loaded as token 4 (lane / 16) + i,
 //    dims 8 (lane % 16) .. +8; output tile t takes dim 8 j + t as its column j, so B of tile t is
@@ -356,13 +358,28 @@ struct MfmaState {
   f32x4 o[8];    // tile t: O[head 4 (lane / 16) + i][dim 8 (lane % 16) + t]
 };
 
+constexpr int kKStageRow = kHeadDim + 8;  // LDS row (elements) of a wavefront's K staging: 272 bytes
+
+// kb: the lane's K pieces as the dot-product form loads them (token 4 i + lane / 16, dims
+// 8 (lane % 16) .. +8: whole 256-byte rows per instruction); kst: the wavefront's 16-row K staging
+// in LDS, through which they reach the MFMA A layout (token lane % 16, dims 32 ks + 8 (lane / 16)).
 __device__ __forceinline__ void attend_block_mfma(MfmaState& st, const bf16x8 (&qf)[4], const u32x4 (&kb)[4],
-                                                  const u32x4 (&vb)[4], float scale, int tok_base, int n,
-                                                  int lane) {
+                                                  const u32x4 (&vb)[4], uint16_t* kst, float scale,
+                                                  int tok_base, int n, int lane) {
+  const int dl = lane & 15, r = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(kst + (4 * i + r) * kKStageRow + 8 * dl) = kb[i];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kb[ks]), qf[ks], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(kst + dl * kKStageRow + 32 * ks + 8 * r),
+                                                  qf[ks], acc, 0, 0, 0);
+  // The next block's staging stores follow these reads in the wavefront's LDS order.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
   const int tok0 = tok_base + 4 * (lane >> 4);
   float sc[4];
 #pragma unroll
@@ -416,6 +433,7 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
 
   extern __shared__ int s_off[];                     // [batch + 1] block prefix sums
   __shared__ int s_wave[kWaves];
+  __shared__ __align__(16) uint16_t s_kst[kMfma ? kWaves : 1][kMfma ? kBlockSize * kKStageRow : 8];
   const int total = scan_blocks<kThreads>(a, s_off, s_wave);
   const int stream = blockIdx.x / kHeadGroups;
   const int hg = blockIdx.x - stream * kHeadGroups;
@@ -429,11 +447,11 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
   const int g = hg * kWaves + (threadIdx.x >> 6);
   const float scale = a.scale;
   // Lane offsets (elements) of its first K and V pieces inside a block, and the step between its
-  // four pieces.  Dot-product form: tokens 4 i + r, dims 8 dl .. +8 for both.  Matrix-core form:
-  // K token dl, dims 32 i + 8 r .. +8; V token 4 r + i, dims 8 dl .. +8.
-  const int k_off = kMfma ? dl * kRowElems + g * kHeadDim + 8 * r : r * kRowElems + g * kHeadDim + 8 * dl;
+  // four pieces.  K (both forms) and V of the dot-product form: tokens 4 i + r, dims 8 dl .. +8;
+  // V of the matrix-core form: token 4 r + i, dims 8 dl .. +8.
+  const int k_off = r * kRowElems + g * kHeadDim + 8 * dl;
   const int v_off = kMfma ? 4 * r * kRowElems + g * kHeadDim + 8 * dl : k_off;
-  constexpr int kKStep = kMfma ? 32 : 4 * kRowElems;
+  constexpr int kKStep = 4 * kRowElems;
   constexpr int kVStep = kMfma ? kRowElems : 4 * kRowElems;
 
   // Block ids of window [base, base + 64), one per lane (indices past the range repeat its
@@ -509,7 +527,7 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
         issue((s + kDepth - 1) % kDepth, xb + kDepth - 1);
         const int tok_base = static_cast<int>(xb - row_lo) * kBlockSize;
         if constexpr (kMfma)
-          attend_block_mfma(ms, qf, kbuf[s], vbuf[s], scale, tok_base, n32, lane);
+          attend_block_mfma(ms, qf, kbuf[s], vbuf[s], s_kst[threadIdx.x >> 6], scale, tok_base, n32, lane);
         else
           attend_block<kG>(st, q, kbuf[s], vbuf[s], scale, tok_base, n32, r);
       }
@@ -605,6 +623,8 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
   __shared__ float s_acc[kSeqWaves][kG][kHeadDim];
   __shared__ float s_ml[kSeqWaves][kG][2];
   __shared__ __align__(16) uint16_t s_q[kFused ? kG : 1][kHeadDim];
+  constexpr bool kMfmaForm = kG >= kMfmaGroup;
+  __shared__ __align__(16) uint16_t s_kst[kMfmaForm ? kSeqWaves : 1][kMfmaForm ? kBlockSize * kKStageRow : 8];
   const int b = blockIdx.x;
   const int g = blockIdx.y;
   const int w = threadIdx.x >> 6;
@@ -650,9 +670,9 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
   const float scale = a.scale;
   constexpr bool kMfma = kG >= kMfmaGroup;  // lane layout and per-block arithmetic as in the stream kernel
   static_assert(kG <= 16, "at most 16 query heads per KV head");
-  const int k_off = kMfma ? dl * kRowElems + g * kHeadDim + 8 * r : r * kRowElems + g * kHeadDim + 8 * dl;
+  const int k_off = r * kRowElems + g * kHeadDim + 8 * dl;
   const int v_off = kMfma ? 4 * r * kRowElems + g * kHeadDim + 8 * dl : k_off;
-  constexpr int kKStep = kMfma ? 32 : 4 * kRowElems;
+  constexpr int kKStep = 4 * kRowElems;
   constexpr int kVStep = kMfma ? kRowElems : 4 * kRowElems;
   const int cnt = nblk > w ? (nblk - 1 - w) / kSeqWaves + 1 : 0;  // blocks w + kSeqWaves i, i < cnt <= 64
 
@@ -720,7 +740,7 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
         if (kSeqDepth > 1) issue((s + kSeqDepth - 1) % kSeqDepth, i + kSeqDepth - 1);
         else if (i > 0) issue(0, i);
         if constexpr (kMfma)
-          attend_block_mfma(ms, qf, kbuf[s], vbuf[s], scale, (w + kSeqWaves * i) * kBlockSize, n, lane);
+          attend_block_mfma(ms, qf, kbuf[s], vbuf[s], s_kst[w], scale, (w + kSeqWaves * i) * kBlockSize, n, lane);
         else
           attend_block<kG>(st, q, kbuf[s], vbuf[s], scale, (w + kSeqWaves * i) * kBlockSize, n, r);
       }
