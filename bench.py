@@ -458,13 +458,55 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False) -> dict:
     return out
 
 
+def bench_decode_groups(steps: int, warmup: int, device) -> dict:
+    """Decode attention (one launch + its merge) on the batch-256 workload's first layer for the
+    GQA groups the library compiles: 8 KV heads, 8 G query heads (Qwen3-0.6B/1.7B: G = 2, 4B/8B:
+    4, 14B: 5, 32B: 8).  The K/V bytes are the same for every G; only Q and O grow."""
+    from mini_infra_qwen3_amd import data_plane, workloads as wl
+
+    w = wl.decode_at_scale(seed=0, device=device, num_layers=1)
+    tables = w.block_tables.to(device)
+    ctx = torch.tensor(w.context_lens, dtype=torch.long, device=device)
+    key_pool, value_pool = w.pools[0, 0], w.pools[0, 1]
+    kv_bytes = sum(w.context_lens) * wl.KV_BYTES_PER_TOKEN_LAYER
+    gen = torch.Generator(device=device).manual_seed(7)
+    out = {"workload": f"decode attention, batch 256, sum(ctx)={sum(w.context_lens)}, 8 KV heads, one layer",
+           "groups": {}}
+    for group in (1, 2, 4, 5, 8):
+        heads = wl.NUM_KV_HEADS * group
+        query = torch.randn((len(w.context_lens), heads, wl.HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+        res = torch.empty((len(w.context_lens), heads * wl.HEAD_DIM), dtype=torch.bfloat16, device=device)
+        ws = torch.empty(max(data_plane.paged_decode_workspace_bytes(
+            len(w.context_lens), tables.shape[1], heads, wl.HEAD_DIM, wl.BLOCK_SIZE, wl.NUM_KV_HEADS), 1),
+            dtype=torch.uint8, device=device)
+        run = lambda: data_plane.paged_decode_attention(query, key_pool, value_pool, tables, ctx, wl.SCALE,
+                                                        out=res, workspace=ws)
+        for _ in range(warmup):
+            run()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(device)
+        start.record()
+        for _ in range(steps):
+            run()
+        end.record()
+        torch.cuda.synchronize(device)
+        ms = start.elapsed_time(end) / steps
+        nbytes = kv_bytes + 2 * query.numel() * 2
+        out["groups"][str(group)] = {"us_per_launch": round(ms * 1000, 1), "bytes": nbytes,
+                                     "achieved_GBps": round(nbytes / ms / 1e6, 1),
+                                     "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                     "form": "matrix-core" if group >= 4 else "dot-product"}
+    return out
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["decode", "scatter", "gather", "prefill", "copy", "swap", "e2e", "e2e-mixed", "all"],
+    parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "gather", "prefill", "copy", "swap",
+                                           "e2e", "e2e-mixed", "all"],
                         default="all")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -486,6 +528,7 @@ def main() -> int:
         "gather": lambda: bench_gather(args.steps, args.warmup, device),
         "prefill": lambda: bench_prefill(args.steps, args.warmup, device),
         "swap": lambda: bench_swap(args.steps, args.warmup, device),
+        "decode-groups": lambda: bench_decode_groups(args.steps, args.warmup, device),
     }
     if args.only in single:  # one kernel alone (for counter runs)
         res = single[args.only]()
@@ -525,6 +568,10 @@ def main() -> int:
         torch.cuda.empty_cache()
         kernels["device_copy"] = bench_copy(5, device)
         log(f"device copy: {kernels['device_copy']['achieved_GBps']:.1f} GB/s")
+        torch.cuda.empty_cache()
+        kernels["decode_gqa_groups"] = bench_decode_groups(args.steps, 2, device)
+        log("decode by GQA group: " + ", ".join(f"{g}: {r['achieved_GBps']:.0f} GB/s"
+                                                 for g, r in kernels["decode_gqa_groups"]["groups"].items()))
         torch.cuda.empty_cache()
         kernels["kv_block_swap"] = bench_swap(max(args.steps // 4, 3), 1, device)
         sw = kernels["kv_block_swap"]
