@@ -93,6 +93,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // dot-product form 6.75 / 6.67 / 6.40 / 6.27 / 4.67 (its per-token arithmetic grows with the
 // group); matrix-core form 6.75 / 6.71 / 6.56 / 6.51 / 6.35.
 constexpr int kMfmaGroup = MI_DECODE_MFMA_GROUP;
+#ifndef MI_DECODE_SEQ_MFMA_GROUP
+#define MI_DECODE_SEQ_MFMA_GROUP 1
+#endif
+// The per-sequence kernel (small launches: latency-bound) takes the matrix-core form from this
+// group size up.  At group 2 it is the faster form at every batch it serves: 6.4 against 7.8 µs per
+// layer at batch 1, 9.5 against 11.6 at 6, 22.0 against 22.8 at 32 (contexts U[32, 1150]).
+constexpr int kSeqMfmaGroup = MI_DECODE_SEQ_MFMA_GROUP;
 
 struct DecodeArgs {
   uint16_t* out;
@@ -623,7 +630,7 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
   __shared__ float s_acc[kSeqWaves][kG][kHeadDim];
   __shared__ float s_ml[kSeqWaves][kG][2];
   __shared__ __align__(16) uint16_t s_q[kFused ? kG : 1][kHeadDim];
-  constexpr bool kMfmaForm = kG >= kMfmaGroup;
+  constexpr bool kMfmaForm = kG >= kSeqMfmaGroup;
   __shared__ __align__(16) uint16_t s_kst[kMfmaForm ? kSeqWaves : 1][kMfmaForm ? kBlockSize * kKStageRow : 8];
   const int b = blockIdx.x;
   const int g = blockIdx.y;
@@ -668,7 +675,7 @@ __global__ __launch_bounds__(64 * kSeqWaves) void paged_decode_seq_kernel(const 
     return;
   }
   const float scale = a.scale;
-  constexpr bool kMfma = kG >= kMfmaGroup;  // lane layout and per-block arithmetic as in the stream kernel
+  constexpr bool kMfma = kMfmaForm;  // lane layout and per-block arithmetic as in the stream kernel
   static_assert(kG <= 16, "at most 16 query heads per KV head");
   const int k_off = r * kRowElems + g * kHeadDim + 8 * dl;
   const int v_off = kMfma ? 4 * r * kRowElems + g * kHeadDim + 8 * dl : k_off;
