@@ -137,6 +137,23 @@ def test_gqa_groups(native_lib, device, kv_heads, group):
     assert not got[5].any()
 
 
+@pytest.mark.parametrize("group", [2, 4, 8])
+def test_rising_scores_force_rescales(native_lib, device, group):
+    """Scores that climb by ~20 natural units per block (and fall back in the last one) make every
+    block raise the running max past the lazy-rescale slack, in both kernel forms: the rescaled
+    accumulators must still match the oracle."""
+    ctx = [16 * 9 + 5, 16 * 3, 40]
+    q, kp, vp, bt, tables = random_case(500 + group, ctx, group=group)
+    q = (q.float().abs() * 0.5 + 0.5).to(torch.bfloat16)  # positive queries: scores follow the key scale
+    for table, n in zip(tables, ctx):
+        for j, blk in enumerate(table):
+            level = 0.3 + 1.2 * j if j + 1 < len(table) else 0.1  # last block: far below the max
+            kp[blk] = (kp[blk].float().abs() * level).to(torch.bfloat16)
+    got = run_kernel(q, kp, vp, bt, ctx, device)
+    ref = oracle(q, kp, vp, bt, ctx)
+    assert max_abs(got, ref) <= TOL
+
+
 def test_packed_metadata_views(native_lib, device):
     """block_tables / context_lens as strided column views of the packed decode rows."""
     w = workloads.decode_step(seed=7, batch=5)
