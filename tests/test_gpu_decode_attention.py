@@ -145,6 +145,9 @@ def test_rising_scores_force_rescales(native_lib, device, group):
     ctx = [16 * 9 + 5, 16 * 3, 40]
     q, kp, vp, bt, tables = random_case(500 + group, ctx, group=group)
     q = (q.float().abs() * 0.5 + 0.5).to(torch.bfloat16)  # positive queries: scores follow the key scale
+    # Outputs are then single V rows: halved, they stay below 4, where one bf16 ulp of rounding
+    # difference fits the absolute tolerance.
+    vp = (vp.float() * 0.5).to(torch.bfloat16)
     for table, n in zip(tables, ctx):
         for j, blk in enumerate(table):
             level = 0.3 + 1.2 * j if j + 1 < len(table) else 0.1  # last block: far below the max

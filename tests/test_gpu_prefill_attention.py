@@ -98,6 +98,27 @@ def test_gqa_groups(native_lib, device, kv_heads, group):
     check_against_oracle(got, *case, starts, lens)
 
 
+@pytest.mark.parametrize("group", [2, 5])
+def test_rising_scores_force_rescales(native_lib, device, group):
+    """Keys whose scale climbs along the history and the chunk push every 64-key tile's scores past
+    the running max by more than the lazy-rescale slack, for history tiles and causal chunk tiles."""
+    starts, lens = [200, 64], [150, 190]
+    q, k, v, kp, vp, hist = make_case(700 + group, starts, lens, group=group)
+    q = (q.float().abs() * 0.5 + 0.5).to(torch.bfloat16)  # positive queries: scores follow the key scale
+    # Rows end up dominated by single keys, so outputs are single V rows: halved, they stay below 4,
+    # where one bf16 ulp (1/64 .. 1/32) of rounding difference fits the absolute tolerance.
+    v, vp = (v.float() * 0.5).to(torch.bfloat16), (vp.float() * 0.5).to(torch.bfloat16)
+    for b, s in enumerate(starts):
+        for j in range(-(-s // 16)):
+            blk = int(hist[b, j])
+            kp[blk] = (kp[blk].float().abs() * (0.2 + 0.25 * j)).to(torch.bfloat16)
+    width = k.shape[2]
+    ramp = 0.2 + 0.06 * torch.arange(width, dtype=torch.float32)  # grows ~4x per 64 keys of the chunk
+    k = (k.float().abs() * ramp.view(1, 1, width, 1)).to(torch.bfloat16)
+    got = run_gpu(q, k, v, kp, vp, hist, starts, lens, device)
+    check_against_oracle(got, q, k, v, kp, vp, hist, starts, lens)
+
+
 def test_matches_fp64_textbook(native_lib, device):
     starts, lens = [24], [20]
     q, k, v, kp, vp, hist = make_case(11, starts, lens)
