@@ -85,13 +85,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #ifndef MI_DECODE_MFMA_GROUP
-#define MI_DECODE_MFMA_GROUP 4
+#define MI_DECODE_MFMA_GROUP 1
 #endif
-// GQA groups from this size up use the matrix-core form of the decode kernels (at most 16 heads,
-// the MFMA's column count); smaller groups keep the dot-product form.  Measured at batch 256
+// GQA groups from this size up use the matrix-core form of the stream kernel (at most 16 heads,
+// the MFMA's column count); smaller groups would use the dot-product form.  Measured at batch 256
 // (8 KV heads, Σctx 755,887, attention + merge), TB/s for groups 1 / 2 / 4 / 5 / 8:
 // dot-product form 6.75 / 6.67 / 6.40 / 6.27 / 4.67 (its per-token arithmetic grows with the
-// group); matrix-core form 6.75 / 6.71 / 6.56 / 6.51 / 6.35.
+// group); matrix-core form 6.75 / 6.71 / 6.56 / 6.51 / 6.35.  At group 2, interleaved in one
+// process (8 x 20 launches each), the matrix-core form took 461.5 µs (median) against 463.3.
 constexpr int kMfmaGroup = MI_DECODE_MFMA_GROUP;
 #ifndef MI_DECODE_SEQ_MFMA_GROUP
 #define MI_DECODE_SEQ_MFMA_GROUP 1
