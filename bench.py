@@ -494,8 +494,7 @@ def bench_decode_groups(steps: int, warmup: int, device) -> dict:
         nbytes = kv_bytes + 2 * query.numel() * 2
         out["groups"][str(group)] = {"us_per_launch": round(ms * 1000, 1), "bytes": nbytes,
                                      "achieved_GBps": round(nbytes / ms / 1e6, 1),
-                                     "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
-                                     "form": "matrix-core" if group >= 4 else "dot-product"}
+                                     "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
     return out
 
 
