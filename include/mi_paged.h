@@ -171,6 +171,30 @@ int32_t mi_paged_decode_attention_fused(void* out, int64_t out_row_stride, const
                                         void* q_scratch, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * mi_paged_decode_attention_noalloc -- mi_paged_decode_attention without a workspace argument: a
+ * variant that allocates nothing and takes no caller scratch.  It has no counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Same arguments, results and errors as mi_paged_decode_attention, bit for bit.  The partials of
+ * sequences cut between block ranges go to a fixed device array of the library,
+ * MI_PAGED_NOALLOC_SCRATCH_BYTES bytes per GPU, held from the first call on a device until the
+ * process ends.  A launch that needs more (mi_paged_decode_workspace_bytes above it; 4.3 MB at
+ * 16 query / 8 KV heads on 256 CUs) returns MI_ERR_WORKSPACE before any device call.  The array
+ * needs no clearing, but it is shared by every call on one GPU: calls that overlap on one GPU
+ * (two streams, or two threads) race on it and must be serialised by the caller.
+ */
+#define MI_PAGED_NOALLOC_SCRATCH_BYTES (8ll << 20)
+int32_t mi_paged_decode_attention_noalloc(void* out, int64_t out_row_stride, const void* query,
+                                          int64_t query_row_stride, int64_t query_head_stride,
+                                          const void* key_pool, const void* value_pool, int64_t num_blocks,
+                                          const int64_t* block_tables, int64_t block_table_stride,
+                                          int32_t max_blocks, const int64_t* context_lens,
+                                          int64_t context_lens_stride, int32_t batch, int32_t num_heads,
+                                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                                          void* stream);
+
+/*
  * Kernel 4 -- chunked-prefill attention on MFMA with the history read from the pool.
  *
  * Replaces, for one layer of PagedRunner.run_prefill_chunk_step

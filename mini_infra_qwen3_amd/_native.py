@@ -52,6 +52,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, ctypes.c_float, _ptr, _i64, _ptr, _ptr,
          _i64, _ptr, _i64, _i32, _ptr, _i64, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _ptr, _ptr, _i64, _ptr],
     ),
+    "mi_paged_decode_attention_noalloc": (
+        _i32,
+        [_ptr, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _i64, _i32, _ptr, _i64, _i32, _i32, _i32, _i32,
+         _i32, ctypes.c_float, _ptr],
+    ),
     "mi_chunked_prefill_attention": (
         _i32,
         [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _ptr, _i64,

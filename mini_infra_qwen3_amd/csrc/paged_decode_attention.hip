@@ -45,6 +45,7 @@
 //    whole XCD L2: far more costly than a launch.)
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "mi_common.h"
 
@@ -1131,4 +1132,82 @@ extern "C" int32_t mi_paged_decode_attention_fused(
   a.num_slots = num_blocks * kBlockSize;
   a.eps = eps;
   return launch_for_heads<true>(a, num_heads, num_kv_heads, true, as_stream(stream));
+}
+
+// ---- The no-allocation variant.  The stream kernel's cut-sequence partials go to `scratch`, a
+// fixed device array of this library (each GPU holds its own copy for the life of the process),
+// instead of a caller workspace.  No part of it needs clearing: a partial slot is written by its
+// range before the merge launch reads it.  Every call on one GPU shares the array, so calls that
+// overlap on one GPU (different streams, or threads) race on it.
+namespace mi {
+namespace {
+constexpr int64_t kScratchBytes = MI_PAGED_NOALLOC_SCRATCH_BYTES;  // 4.3 MB used at 16 / 8 heads on 256 CUs
+constexpr int kMaxScratchDevices = 64;
+}  // namespace
+}  // namespace mi
+
+static __device__ __align__(256) unsigned char scratch[mi::kScratchBytes];
+
+namespace mi {
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per device with that device
+// current (the array's name is only a host-side stand-in for it).
+int32_t scratch_on_current_device(void** out) {
+  static std::mutex mu;
+  static void* ptrs[kMaxScratchDevices] = {nullptr};
+  int dev = 0;
+  const hipError_t derr = hipGetDevice(&dev);
+  if (derr != hipSuccess)
+    return fail(MI_ERR_DEVICE, "mi_paged_decode_attention_noalloc: hipGetDevice: %s", hipGetErrorString(derr));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(MI_ERR_UNSUPPORTED, "mi_paged_decode_attention_noalloc: device %d beyond %d", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return fail(MI_ERR_DEVICE, "mi_paged_decode_attention_noalloc: hipGetSymbolAddress(scratch): %s",
+                  hipGetErrorString(err));
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return MI_OK;
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int32_t mi_paged_decode_attention_noalloc(void* out, int64_t out_row_stride, const void* query,
+                                                     int64_t query_row_stride, int64_t query_head_stride,
+                                                     const void* key_pool, const void* value_pool, int64_t num_blocks,
+                                                     const int64_t* block_tables, int64_t block_table_stride,
+                                                     int32_t max_blocks, const int64_t* context_lens,
+                                                     int64_t context_lens_stride, int32_t batch, int32_t num_heads,
+                                                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                                     float scale, void* stream) {
+  using namespace mi;
+  if (batch < 0 || max_blocks < 0 || num_blocks < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_noalloc: negative size");
+  if (batch == 0) return ok();
+  if (const int32_t rc = check_heads("mi_paged_decode_attention_noalloc", num_heads, num_kv_heads, head_dim,
+                                     block_size))
+    return rc;
+  // The size check comes before any device call: a launch that needs more than the fixed array
+  // is rejected without touching the GPU.
+  const int64_t need =
+      mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, num_kv_heads, head_dim, block_size);
+  if (need > kScratchBytes)
+    return fail(MI_ERR_WORKSPACE,
+                "mi_paged_decode_attention_noalloc: this launch needs %lld bytes of scratch, the fixed array "
+                "holds %lld (use mi_paged_decode_attention with a workspace)",
+                static_cast<long long>(need), static_cast<long long>(kScratchBytes));
+  void* ws = nullptr;
+  if (need > 0) {
+    if (const int32_t rc = scratch_on_current_device(&ws)) return rc;
+  }
+  return mi_paged_decode_attention(out, out_row_stride, query, query_row_stride, query_head_stride, key_pool,
+                                   value_pool, num_blocks, block_tables, block_table_stride, max_blocks, context_lens,
+                                   context_lens_stride, batch, num_heads, num_kv_heads, head_dim, block_size, scale,
+                                   ws, need > 0 ? kScratchBytes : 0, stream);
 }

@@ -58,6 +58,18 @@ def test_decode_workspace_size(native_lib):
     assert native_lib.mi_paged_decode_workspace_bytes(256, 512, 16, 3, 128, 16) == 0  # heads not a multiple
 
 
+def test_noalloc_decode_rejects_launches_beyond_its_scratch_on_host(native_lib):
+    # 2 KV heads x 8 query heads each: 1024 block ranges (256 CUs assumed without a device) x 2
+    # slots x 16 heads x 130 floats = 17 MB > the 8 MiB fixed array; rejected before any device call
+    need = native_lib.mi_paged_decode_workspace_bytes(4096, 512, 16, 2, 128, 16)
+    assert need > 8 << 20
+    rc = native_lib.mi_paged_decode_attention_noalloc(None, 0, None, 0, 0, None, None, 1, None, 512, 512, None, 1,
+                                                      4096, 16, 2, 128, 16, 1.0, None)
+    assert rc == _native.MI_ERR_WORKSPACE and b"scratch" in native_lib.mi_last_error()
+    assert native_lib.mi_paged_decode_attention_noalloc(None, 0, None, 0, 0, None, None, 1, None, 512, 0, None, 1,
+                                                        0, 16, 8, 128, 16, 1.0, None) == _native.MI_OK
+
+
 def _ptrs(n):
     return (ctypes.c_void_p * n)(*([16] * n))
 
