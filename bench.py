@@ -393,30 +393,33 @@ def bench_prefill(steps: int, warmup: int, device: torch.device) -> dict:
 
 
 # ------------------------------------------------------------------------ e2e continuous batching
-def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False) -> dict:
+def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: bool = True) -> dict:
     """Continuous batching with chunked prefill (token budget 2048, block 16, batch slots = number of
     requests) of a random-init Qwen3-0.6B (bf16, N(0, 0.02), tied embeddings): 128 requests, Poisson
     arrivals at 20 req/s, prompts U[32, 1024], 128 greedy tokens each, EOS disabled.  Output tok/s =
     output tokens x 1000 / busy_ms, busy_ms = sum over steps of (device-timed forward + host-timed
-    cache management), on the logical clock the measured step times advance.  The decode forward
-    is replayed from HIP graphs captured per padded (batch, blocks) bucket, and the prefill forward
-    of one or two chunks per padded (rows, width, history) bucket, when the backend is set up
-    (``setup_s``, outside the timed run).  ``mixed``: decode rows ride in the prefill steps (the
-    mixed batching the reference plans) instead of the reference's alternating prefill / decode,
-    with mixed steps of one or two chunks and up to 32 decode rows replayed from graphs too."""
+    cache management), on the logical clock the measured step times advance.  HIP graphs are
+    captured when the backend is set up (``setup_s``, outside the timed run).
+    ``exact`` (reference numerics, the configuration whose greedy tokens are identical to the
+    oracle's): the exact attention kernels and the reference's GEMM calls; decode forwards replay
+    a graph per batch size; prefill steps run eagerly at the chunks' own width.  ``exact=False``:
+    the bandwidth kernels and fused GEMMs, decode graphs per padded (batch, blocks) bucket and
+    prefill (and mixed) graphs per padded (rows, width) bucket.  ``mixed``: decode rows ride in
+    the prefill steps (the mixed batching the reference plans) instead of the reference's
+    alternating prefill / decode."""
     from mini_infra_qwen3_amd.core.scheduler import SchedulePhase
     from mini_infra_qwen3_amd.engine import PagedScheduleBackend, run_scheduler
     from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
     from mini_infra_qwen3_amd.workloads import serving_requests
 
-    model = Qwen3ForCausalLM(qwen3_0_6b())
+    model = Qwen3ForCausalLM(qwen3_0_6b(), exact=exact)
     init_random_(model, seed=seed, std=0.02)
     model = model.to(device=device, dtype=torch.bfloat16).eval()
 
     def run(requests):
         t0 = time.perf_counter()
-        backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True, prefill_graphs=True,
-                                       mixed_graphs=mixed)
+        backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True, prefill_graphs=not exact,
+                                       mixed_graphs=mixed and not exact)
         setup_s = time.perf_counter() - t0
         return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False,
                              mixed_batching=mixed), setup_s
@@ -429,6 +432,7 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False) -> dict:
     mixed_steps = [e for e in res.events if e.phase is SchedulePhase.MIXED]
     out = {
         "metric": "e2e output tok/s Qwen3-0.6B (continuous batching, chunked prefill 2048, paged KV)",
+        "numerics": "reference (exact sums; greedy tokens identical to the oracle)" if exact else "bandwidth kernels",
         "mixed_batching": mixed,
         "output_tok_s": round(res.throughput_tok_s, 1),
         "wall_tok_s": round(res.wall_tok_s, 1),
@@ -448,8 +452,8 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False) -> dict:
         "mixed_step_ms_mean": round(sum(e.step_ms for e in mixed_steps) / max(len(mixed_steps), 1), 3),
         "requests": len(requests),
         "arrival_rate_req_s": 20.0,
-        "decode_graphs": True,
-        "prefill_graphs": True,
+        "decode_graphs": "per batch size" if exact else "per padded (batch, blocks) bucket",
+        "prefill_graphs": not exact,
         "setup_s": round(setup_s, 2),
         "latency_ms": {k: round(v, 2) for k, v in res.latency_summary().items()},
     }
@@ -505,7 +509,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "gather", "prefill", "copy", "swap",
-                                           "e2e", "e2e-mixed", "all"],
+                                           "e2e", "e2e-mixed", "e2e-bandwidth", "all"],
                         default="all")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -534,8 +538,8 @@ def main() -> int:
         log(f"{args.only}: {json.dumps(res)}")
         print(json.dumps(res), flush=True)
         return 0
-    if args.only in ("e2e", "e2e-mixed"):
-        res = bench_e2e(device, mixed=args.only == "e2e-mixed")
+    if args.only in ("e2e", "e2e-mixed", "e2e-bandwidth"):
+        res = bench_e2e(device, mixed=args.only == "e2e-mixed", exact=args.only != "e2e-bandwidth")
         log(f"e2e: {res['output_tok_s']:.1f} output tok/s (busy), {res['wall_tok_s']:.1f} tok/s (wall)")
         print(json.dumps(res), flush=True)
         return 0
@@ -578,13 +582,15 @@ def main() -> int:
             f"{sw['unpack']['achieved_GBps']:.1f} GB/s; swap out {sw['swap_out']['achieved_GBps']:.1f} GB/s, "
             f"swap in {sw['swap_in']['achieved_GBps']:.1f} GB/s")
         torch.cuda.empty_cache()
-    e2e = e2e_mixed = None
+    e2e = e2e_mixed = e2e_bw = None
     if args.only == "all":
         e2e = bench_e2e(device)
         log(f"e2e: {e2e['output_tok_s']:.1f} output tok/s (busy), {e2e['wall_tok_s']:.1f} tok/s (wall)")
         e2e_mixed = bench_e2e(device, mixed=True)
         log(f"e2e mixed batching: {e2e_mixed['output_tok_s']:.1f} output tok/s (busy), ITL max "
             f"{e2e_mixed['latency_ms']['itl_ms_max']:.2f} ms (alternating: {e2e['latency_ms']['itl_ms_max']:.2f} ms)")
+        e2e_bw = bench_e2e(device, exact=False)
+        log(f"e2e bandwidth kernels: {e2e_bw['output_tok_s']:.1f} output tok/s (busy)")
 
     line = {
         "metric": METRIC,
@@ -614,6 +620,7 @@ def main() -> int:
         "kernels": kernels,
         "e2e": e2e,
         "e2e_mixed_batching": e2e_mixed,
+        "e2e_bandwidth_kernels": e2e_bw,
     }
     print(json.dumps(line), flush=True)
     return 0

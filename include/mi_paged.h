@@ -233,6 +233,53 @@ int32_t mi_chunked_prefill_attention(void* out, int64_t out_row_stride, int64_t 
                                      int32_t block_size, float scale, void* stream);
 
 /*
+ * Reference numerics -- attention at the reference's rounding points with exactly accumulated
+ * sums, for callers that need results independent of reduction order (a model forward that must
+ * reproduce its reference bit for bit).  Replaces the same reference code as kernels 3 and 4
+ * (src/mini_infra/model/qwen3.py:219-255 with the paged gather :257-292 and the chunk mask
+ * :438-485).  Per query row and visible key t (same visibility as kernels 3 and 4):
+ *   s_t = bf16(bf16(fp32(sum_d q_d k_td)) * scale)     (exact dot product)
+ *   m = max_t s_t,  e_t = fp32(exp(fp32(s_t - m))),  l = fp32(sum_t e_t)   (exp in fp64, exact sum)
+ *   p_t = bf16(fp32(e_t / l)),  out_d = bf16(fp32(sum_t p_t v_td))          (exact sum)
+ * i.e. the reference's bf16 scores, fp32 softmax cast to bf16 before P V, and bf16 output, with
+ * every sum exact instead of an fp32 sum in an implementation-defined order.  fp64 arithmetic,
+ * scores held in LDS: meant for latency-bound launches (decode steps, prompt-sized prefill).
+ *
+ * mi_paged_decode_attention_exact -- decode.  With q_weight == NULL, `q` holds the rotated
+ * queries ([batch, num_heads, 128], row / head strides) and k, v, k_weight, cos, sin, eps and
+ * slot_mapping are ignored: the arguments and outputs of mi_paged_decode_attention (no
+ * workspace).  With q_weight != NULL the prologue of mi_paged_decode_attention_fused runs first
+ * (q / k RMSNorm + RoPE of the raw projection rows q / k, K/V rows into their slots; the q head
+ * stride is then 128), bit-identical to mi_qk_norm_rope.  Out-of-range table ids read block 0.
+ * Any context length (contexts longer than the LDS cache recompute their scores per pass).
+ *
+ * mi_chunked_prefill_attention_exact -- chunked prefill: the arguments and layout of
+ * mi_chunked_prefill_attention.  Padding rows get zeros.
+ *
+ * Specialised for head_dim 128, block_size 16 and 1, 2, 4, 5 or 8 query heads per KV head.
+ */
+int32_t mi_paged_decode_attention_exact(void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride,
+                                        int64_t q_head_stride, const void* k, int64_t k_row_stride, const void* v,
+                                        int64_t v_row_stride, const void* q_weight, const void* k_weight,
+                                        const void* cos, const void* sin, float eps, const int64_t* slot_mapping,
+                                        int64_t slot_stride, void* key_pool, void* value_pool, int64_t num_blocks,
+                                        const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,
+                                        const int64_t* context_lens, int64_t context_lens_stride, int32_t batch,
+                                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t block_size, float scale, void* stream);
+int32_t mi_chunked_prefill_attention_exact(void* out, int64_t out_row_stride, int64_t out_tok_stride,
+                                           const void* query, int64_t query_row_stride, int64_t query_head_stride,
+                                           int64_t query_tok_stride, const void* key, int64_t key_row_stride,
+                                           int64_t key_head_stride, int64_t key_tok_stride, const void* value,
+                                           int64_t value_row_stride, int64_t value_head_stride,
+                                           int64_t value_tok_stride, const void* key_pool, const void* value_pool,
+                                           int64_t num_blocks, const int64_t* history_blocks, int64_t history_stride,
+                                           int32_t max_history_blocks, const int64_t* start_lens,
+                                           const int64_t* chunk_lens, int64_t lens_stride, int32_t batch,
+                                           int32_t padded_len, int32_t num_heads, int32_t num_kv_heads,
+                                           int32_t head_dim, int32_t block_size, float scale, void* stream);
+
+/*
  * Fused layer ops: the elementwise chains around attention in a Qwen3 decoder layer, one
  * launch each, with the reference's bf16 rounding points.  All tensors are bf16, rows of
  * contiguous elements, 16-byte aligned.
@@ -240,7 +287,9 @@ int32_t mi_chunked_prefill_attention(void* out, int64_t out_row_stride, int64_t 
  * mi_rms_norm -- RMSNorm (src/mini_infra/model/qwen3.py:55-78), optionally after the residual
  * add of Qwen3DecoderLayer.forward (:368-400):
  *   h = residual ? bf16(x + residual) : x;  residual_out = h (when residual is given)
- *   out = bf16(weight * bf16(h * rsqrt(sum(h^2) / hidden + eps)))      (fp32 inside)
+ *   out = bf16(weight * bf16(h * r)),  r = fp32(1 / sqrt(fp32(fp32(sum(h^2) / hidden) + eps)))
+ * with the sum of squares exact and the square root and division in fp64 (the reference's fp32
+ * mean, rsqrt and product, independent of the order of the sum).
  * x / residual / residual_out / out: [rows, hidden] contiguous; hidden a multiple of 8, <= 4096.
  */
 int32_t mi_rms_norm(void* out, const void* x, const void* residual, void* residual_out, const void* weight,

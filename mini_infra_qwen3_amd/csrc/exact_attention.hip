@@ -1,0 +1,894 @@
+// Attention with the reference's rounding points and exactly accumulated sums.
+//
+// The reference attends with (src/mini_infra/model/qwen3.py:219-255)
+//   scores = bf16(Q K^T) * scale          -> bf16 matmul output, then a bf16 product
+//   probs  = softmax(scores, fp32).to(bf16)
+//   out    = bf16(probs V)
+// Each of its sums (the dot products, the softmax denominator, the P V products) is an fp32 sum
+// in whatever order ATen's kernels pick, and that order differs between devices, libraries and
+// batch shapes, so the last bits of every rounding point depend on it.  The kernels here keep
+// the reference's rounding points and make every sum exact instead:
+//   s_t  = bf16(bf16(fp32(sum_d q_d k_td)) * scale)       exact dot product, rounded to fp32, bf16
+//   m    = max_t s_t
+//   e_t  = fp32(exp(fp32(s_t - m)))                       exp evaluated in fp64, rounded once
+//   l    = fp32(sum_t e_t)                                exact sum (split_add below)
+//   p_t  = bf16(fp32(e_t / l))                            division correctly rounded
+//   o_d  = bf16(fp32(sum_t p_t v_td))                     exact sum
+// over the visible keys t.  Products of two bf16 values are exact in fp64, and fp64 sums of the
+// terms met here are exact or off by far less than the final roundings can see, so the results
+// do not depend on how the work is split over lanes, wavefronts or workgroups, nor on the device:
+// the oracle computes the same definitions with torch ops and gets the same bits.  That is what
+// makes a whole model bit-identical to its oracle, and greedy decoding token-identical (a bf16
+// logit tie over a 151,936-token vocabulary is common, so any one-ulp difference anywhere in the
+// forward eventually flips a token).
+//
+// Cost: fp64 arithmetic instead of fp32 MFMA, and two passes over the keys (K for the scores,
+// then V for the output) with the scores held in LDS.  These kernels serve the model's forward,
+// where attention is latency-bound (small decode batches, prompts of a few hundred tokens); the
+// bandwidth kernels (paged_decode_attention.hip, chunked_prefill_attention.hip) keep fp32 online
+// softmax for large batches and long prompts.
+//
+// Decode (q_len 1): one workgroup of 8 wavefronts per (sequence, KV head) serves the G query
+// heads of the GQA group; wavefront w takes blocks w, w + 8, ...  Lane 16 r + d holds dims
+// [8 d, 8 d + 8) of tokens 4 i + r of a 16-token block (one 16-byte load per lane per i), the
+// layout of the bandwidth kernels.  The scores go to LDS as bf16 (exact: they are bf16 values),
+// are replaced by the probabilities once m and l are known, and are read back for P V.  A
+// context too long for the LDS cache recomputes the scores in each pass instead.
+//
+// Prefill (chunked, with history from the pool): one workgroup of 4 wavefronts per (row, KV
+// head, tile of 32 / G query positions); its 32 (query, head) rows are split 8 per wavefront.
+// Key tiles of 64 keys (history first, then the causal chunk) are staged in LDS; a lane takes one
+// key of the tile against its wavefront's 8 rows for the scores, and two output dims of those rows
+// for P V.
+#include <math.h>
+#include <mutex>
+
+#include "mi_common.h"
+
+namespace mi {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kBlockSize = 16;
+
+// ---------------------------------------------------------------- shared arithmetic ---
+// The bf16 matmul output (the exact dot product rounded to fp32, then to bf16), times the scale
+// with one more bf16 rounding (qwen3.py:243).
+__device__ __forceinline__ float exact_score(double dot, float scale) {
+  return round_bf16(round_bf16(static_cast<float>(dot)) * scale);
+}
+
+// e = fp32(exp(fp32(s - m))): the fp32 difference of two bf16 values, exponential in fp64.
+__device__ __forceinline__ float exact_exp(float s, float m) {
+  const float d = s - m;
+  return static_cast<float>(exp(static_cast<double>(d)));
+}
+
+// Order-independent sum of values in [0, 1]: x splits into h, x rounded to a multiple of 2^-32
+// ((x + 1.5 * 2^20) - 1.5 * 2^20 in fp64: the sum's ulp is 2^-32), and the remainder x - h.
+// The h parts add exactly in fp64 for up to 2^20 terms; the remainders are below 2^-33, so their
+// fp64 sum is off by ~2^-77 at most.  The total is fp32(fp64(sum h + sum lo)).
+constexpr double kSplit = 1572864.0;
+__device__ __forceinline__ void split_add(float e, double& hi, double& lo) {
+  const double x = e;
+  const double h = (x + kSplit) - kSplit;
+  hi += h;
+  lo += x - h;
+}
+
+// p = bf16(fp32(e / l)): an fp64 quotient of two fp32 values rounds to the correctly rounded
+// fp32 quotient (53 >= 2 * 24 + 2 bits).
+__device__ __forceinline__ float exact_prob(float e, float l) {
+  return round_bf16(static_cast<float>(static_cast<double>(e) / static_cast<double>(l)));
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float f) { return static_cast<uint16_t>(f32_to_bf16_bits(f)); }
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// Eight bf16 values of a 16-byte piece as doubles (exact).
+__device__ __forceinline__ void unpack8(const u32x4 v, double (&d)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t x = v[w];
+    d[2 * w] = bf16_lo(x);
+    d[2 * w + 1] = bf16_hi(x);
+  }
+}
+
+// ------------------------------------------------------------------------ decode ---
+constexpr int kDecWaves = 8;
+constexpr int kDecThreads = 64 * kDecWaves;
+constexpr int kDecCacheBytes = 128 * 1024;  // score cache (dynamic LDS) of one workgroup, at most
+
+struct ExactDecodeArgs {
+  uint16_t* out;
+  int64_t out_row;
+  const uint16_t* q;       // rotated queries [B, H, 128] (plain form) or raw q projection rows (prologue)
+  int64_t q_row, q_head;
+  const uint16_t* k_new;   // prologue: raw k / v projection rows of the new tokens
+  const uint16_t* v_new;
+  int64_t k_row, v_row;
+  const uint16_t* q_weight;
+  const uint16_t* k_weight;
+  const uint16_t* cos;     // [B, 128]
+  const uint16_t* sin;
+  float eps;
+  const int64_t* slot_mapping;
+  int64_t slot_stride;
+  int64_t num_slots;
+  uint16_t* key_pool;
+  uint16_t* value_pool;
+  int64_t num_blocks;
+  int32_t kv_heads;
+  const int64_t* block_tables;
+  int64_t bt_stride;
+  int32_t max_blocks;
+  const int64_t* context_lens;
+  int64_t ctx_stride;
+  float scale;
+  int32_t cache_tokens;    // tokens the LDS score cache holds per head (0: recompute the scores)
+};
+
+template <int kG, bool kPrologue>
+__global__ __launch_bounds__(kDecThreads) void exact_decode_kernel(const ExactDecodeArgs a) {
+  __shared__ __align__(16) float s_q[kG][kHeadDim];
+  __shared__ float s_m[kDecWaves][kG];
+  __shared__ double s_l[kDecWaves][kG][2];
+  __shared__ double s_o[kDecWaves][kHeadDim];
+  extern __shared__ uint16_t s_cache[];  // [cache_tokens][kG]: bf16 scores, then probabilities
+
+  const int b = blockIdx.x;
+  const int g = blockIdx.y;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int dl = lane & 15;
+  const int r = lane >> 4;
+  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
+
+  if constexpr (kPrologue) {
+    // Unit u < kG: query head g kG + u, normalised and rotated into LDS; unit kG: key head g,
+    // written with value head g into the sequence's new slot (the K/V append).
+    for (int u = w; u <= kG; u += kDecWaves) {
+      const bool is_q = u < kG;
+      const uint16_t* src = is_q ? a.q + b * a.q_row + (g * kG + u) * kHeadDim : a.k_new + b * a.k_row + g * kHeadDim;
+      float o0, o1;
+      norm_rope_head(src, is_q ? a.q_weight : a.k_weight, a.cos + b * kHeadDim, a.sin + b * kHeadDim, a.eps, lane,
+                     o0, o1);
+      if (is_q) {
+        s_q[u][lane] = o0;
+        s_q[u][lane + 64] = o1;
+      } else {
+        const int64_t slot = a.slot_mapping[b * a.slot_stride];
+        if (slot >= 0 && slot < a.num_slots) {
+          uint16_t* kd = a.key_pool + slot * row_elems + g * kHeadDim;
+          uint16_t* vd = a.value_pool + slot * row_elems + g * kHeadDim;
+          const uint16_t* vs = a.v_new + b * a.v_row + g * kHeadDim;
+          kd[lane] = bf16_bits(o0);
+          kd[lane + 64] = bf16_bits(o1);
+          vd[lane] = vs[lane];
+          vd[lane + 64] = vs[lane + 64];
+        }
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < kG * kHeadDim; i += kDecThreads) {
+      const int j = i / kHeadDim, d = i - j * kHeadDim;
+      s_q[j][d] = bf16_bits_to_f32(a.q[b * a.q_row + (g * kG + j) * a.q_head + d]);
+    }
+  }
+  // The barrier also orders the append before this workgroup's loads of the new token's block
+  // (no other workgroup reads KV head g of this sequence, and those lines were not read before).
+  __syncthreads();
+
+  int64_t n64 = a.context_lens[b * a.ctx_stride];
+  n64 = min(n64, static_cast<int64_t>(a.max_blocks) * kBlockSize);
+  const int n = n64 > 0 ? static_cast<int>(n64) : 0;
+  const int nblk = (n + kBlockSize - 1) / kBlockSize;
+  uint16_t* out_b = a.out + b * a.out_row + (g * kG) * kHeadDim;
+  if (nblk == 0) {  // empty context: zero rows (uniform)
+    if (threadIdx.x < kG * 16) *reinterpret_cast<uint4*>(out_b + 8 * threadIdx.x) = uint4{0, 0, 0, 0};
+    return;
+  }
+  const bool cached = n <= a.cache_tokens;  // uniform
+  const int cnt = nblk > w ? (nblk - 1 - w) / kDecWaves + 1 : 0;  // blocks w + 8 i of this wavefront
+  const float scale = a.scale;
+
+  // Lane offset inside a block: token 4 i + r (i = 0..3), dims 8 dl .. +8 of KV head g.
+  const int64_t lane_off = r * row_elems + g * kHeadDim + 8 * dl;
+  auto block_ptr = [&](const uint16_t* pool, int i) -> const uint16_t* {
+    const int blk = w + kDecWaves * i;
+    int64_t id = a.block_tables[b * a.bt_stride + blk];
+    if (id < 0 || id >= a.num_blocks) id = 0;
+    return pool + id * kBlockSize * row_elems + lane_off;
+  };
+  auto load_block = [&](const uint16_t* pool, int i, u32x4 (&buf)[4]) {
+    const uint16_t* p = block_ptr(pool, i);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) buf[t] = *reinterpret_cast<const u32x4*>(p + 4 * t * row_elems);
+  };
+  // Scores of the lane row's 4 tokens of block i against the kG queries (equal in the 16 lanes of
+  // the row after the butterfly).
+  auto block_scores = [&](const u32x4 (&kb)[4], float (&s)[4][kG]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      double kd[8];
+      unpack8(kb[t], kd);
+#pragma unroll
+      for (int j = 0; j < kG; ++j) {
+        const float4 q0 = *reinterpret_cast<const float4*>(&s_q[j][8 * dl]);
+        const float4 q1 = *reinterpret_cast<const float4*>(&s_q[j][8 * dl + 4]);
+        double acc = static_cast<double>(q0.x) * kd[0];
+        acc = fma(static_cast<double>(q0.y), kd[1], acc);
+        acc = fma(static_cast<double>(q0.z), kd[2], acc);
+        acc = fma(static_cast<double>(q0.w), kd[3], acc);
+        acc = fma(static_cast<double>(q1.x), kd[4], acc);
+        acc = fma(static_cast<double>(q1.y), kd[5], acc);
+        acc = fma(static_cast<double>(q1.z), kd[6], acc);
+        acc = fma(static_cast<double>(q1.w), kd[7], acc);
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        acc += __shfl_xor(acc, 8, 64);
+        s[t][j] = exact_score(acc, scale);
+      }
+    }
+  };
+
+  // ---- pass 1: scores, their maximum per head (and the cache)
+  float mloc[kG];
+#pragma unroll
+  for (int j = 0; j < kG; ++j) mloc[j] = -INFINITY;
+  for (int i = 0; i < cnt; ++i) {
+    u32x4 kb[4];
+    load_block(a.key_pool, i, kb);
+    float s[4][kG];
+    block_scores(kb, s);
+    const int tok0 = (w + kDecWaves * i) * kBlockSize + r;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int tok = tok0 + 4 * t;
+      if (tok < n) {
+#pragma unroll
+        for (int j = 0; j < kG; ++j) {
+          mloc[j] = fmaxf(mloc[j], s[t][j]);
+          if (cached && dl == j) s_cache[tok * kG + j] = bf16_bits(s[t][j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    const float mw = wave_max(mloc[j]);
+    if (lane == 0) s_m[w][j] = mw;
+  }
+  __syncthreads();
+  float M[kG];
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kDecWaves; ++v) mx = fmaxf(mx, s_m[v][j]);
+    M[j] = mx;
+  }
+
+  // ---- pass 2: the softmax denominators
+  double hi[kG], lo[kG];
+#pragma unroll
+  for (int j = 0; j < kG; ++j) hi[j] = lo[j] = 0.0;
+  if (cached) {
+    for (int tok = threadIdx.x; tok < n; tok += kDecThreads) {
+#pragma unroll
+      for (int j = 0; j < kG; ++j) split_add(exact_exp(bf16_bits_to_f32(s_cache[tok * kG + j]), M[j]), hi[j], lo[j]);
+    }
+  } else {
+    for (int i = 0; i < cnt; ++i) {
+      u32x4 kb[4];
+      load_block(a.key_pool, i, kb);
+      float s[4][kG];
+      block_scores(kb, s);
+      const int tok0 = (w + kDecWaves * i) * kBlockSize + r;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (tok0 + 4 * t < n) {
+#pragma unroll
+          for (int j = 0; j < kG; ++j)
+            if (dl == j) split_add(exact_exp(s[t][j], M[j]), hi[j], lo[j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    const double h = wave_sum_f64(hi[j]), l = wave_sum_f64(lo[j]);
+    if (lane == 0) {
+      s_l[w][j][0] = h;
+      s_l[w][j][1] = l;
+    }
+  }
+  __syncthreads();
+  float L[kG];
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    double h = 0.0, l = 0.0;
+#pragma unroll
+    for (int v = 0; v < kDecWaves; ++v) {
+      h += s_l[v][j][0];
+      l += s_l[v][j][1];
+    }
+    L[j] = static_cast<float>(h + l);
+  }
+  if (cached) {  // scores -> probabilities in place
+    for (int tok = threadIdx.x; tok < n; tok += kDecThreads) {
+#pragma unroll
+      for (int j = 0; j < kG; ++j) {
+        const float s = bf16_bits_to_f32(s_cache[tok * kG + j]);
+        s_cache[tok * kG + j] = bf16_bits(exact_prob(exact_exp(s, M[j]), L[j]));
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- pass 3: P V (lane: tokens 4 i + r of each block, dims 8 dl .. +8)
+  double acc[kG][8];
+#pragma unroll
+  for (int j = 0; j < kG; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0.0;
+  for (int i = 0; i < cnt; ++i) {
+    u32x4 vb[4];
+    load_block(a.value_pool, i, vb);
+    float p[4][kG];
+    const int tok0 = (w + kDecWaves * i) * kBlockSize + r;
+    if (cached) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int tok = tok0 + 4 * t;
+#pragma unroll
+        for (int j = 0; j < kG; ++j) p[t][j] = tok < n ? bf16_bits_to_f32(s_cache[tok * kG + j]) : 0.0f;
+      }
+    } else {
+      u32x4 kb[4];
+      load_block(a.key_pool, i, kb);
+      float s[4][kG];
+      block_scores(kb, s);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bool valid = tok0 + 4 * t < n;
+#pragma unroll
+        for (int j = 0; j < kG; ++j) p[t][j] = valid ? exact_prob(exact_exp(s[t][j], M[j]), L[j]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      double vd[8];
+      unpack8(vb[t], vd);
+#pragma unroll
+      for (int j = 0; j < kG; ++j) {
+        const double pj = p[t][j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] = fma(pj, vd[e], acc[j][e]);
+      }
+    }
+  }
+  // rows of the wavefront, then the wavefronts (one head at a time through LDS)
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      double x = acc[j][e];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      acc[j][e] = x;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    if (r == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_o[w][8 * dl + e] = acc[j][e];
+    }
+    __syncthreads();
+    if (threadIdx.x < kHeadDim) {
+      double o = 0.0;
+#pragma unroll
+      for (int v = 0; v < kDecWaves; ++v) o += s_o[v][threadIdx.x];
+      out_b[j * kHeadDim + threadIdx.x] = bf16_bits(static_cast<float>(o));
+    }
+    __syncthreads();
+  }
+}
+
+// ----------------------------------------------------------------------- prefill ---
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfRows = 32;               // (query, head) rows of a workgroup: 8 per wavefront
+constexpr int kPfKeys = 64;               // keys per staged tile
+constexpr int kKvRow = kHeadDim + 8;      // LDS row of a staged K or V tile (elements): 272 bytes
+constexpr int kPfQBytes = kPfRows * kHeadDim * 8;
+constexpr int kPfTileBytes = kPfKeys * kKvRow * 2;
+constexpr int kPfLdsBytes = 160 * 1024;
+constexpr int kPfMaxCacheKeys = (kPfLdsBytes - kPfQBytes - kPfTileBytes) / (kPfRows * 2) / kPfKeys * kPfKeys;
+
+struct ExactPrefillArgs {
+  uint16_t* out;
+  int64_t out_row, out_tok;
+  const uint16_t* q;
+  int64_t q_row, q_head, q_tok;
+  const uint16_t* k;
+  int64_t k_row, k_head, k_tok;
+  const uint16_t* v;
+  int64_t v_row, v_head, v_tok;
+  const uint16_t* key_pool;
+  const uint16_t* value_pool;
+  int64_t num_blocks;
+  int32_t kv_heads;
+  const int64_t* history;
+  int64_t hist_stride;
+  int32_t max_hist_blocks;
+  const int64_t* start_lens;
+  const int64_t* chunk_lens;
+  int64_t lens_stride;
+  int32_t padded_len;
+  float scale;
+  int32_t cache_keys;      // keys the LDS cache holds (>= a row's keys: cached form; else kPfKeys, recompute)
+};
+
+template <int kG>
+__global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPrefillArgs a) {
+  constexpr int kQ = kPfRows / kG;        // query positions per workgroup
+  constexpr int kRows = kQ * kG;          // rows in use (<= 32)
+  extern __shared__ __align__(16) unsigned char s_raw[];
+  double* sQ = reinterpret_cast<double*>(s_raw);                             // [32][128]
+  uint16_t* sT = reinterpret_cast<uint16_t*>(s_raw + kPfQBytes);             // [64][kKvRow]
+  uint16_t* sC = reinterpret_cast<uint16_t*>(s_raw + kPfQBytes + kPfTileBytes);  // [cache_keys][32]
+
+  const int qt = blockIdx.x;
+  const int g = blockIdx.y;
+  const int b = blockIdx.z;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int L = a.padded_len;
+  int64_t clen = a.chunk_lens[b * a.lens_stride];
+  clen = clen < 0 ? 0 : (clen > L ? L : clen);
+  const int pad = L - static_cast<int>(clen);
+  int64_t nh64 = a.start_lens[b * a.lens_stride];
+  nh64 = nh64 < 0 ? 0 : min(nh64, static_cast<int64_t>(a.max_hist_blocks) * kBlockSize);
+  const int nh = static_cast<int>(nh64);
+  const int i0 = qt * kQ;
+  const int i_last = min(i0 + kQ - 1, L - 1);
+  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
+
+  // Row rho = qi * kG + j of this workgroup: query position i0 + qi, query head g kG + j.  Wavefront
+  // w owns rows 8 w .. 8 w + 7.  Key kk (history slots first, then chunk positions pad, pad + 1, ...)
+  // is visible to a row iff kk <= kmax (= nh + i - pad; -1 for padding rows and rows past L).
+  int kmax[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int rho = 8 * w + k;
+    const int i = i0 + rho / kG;
+    kmax[k] = (rho < kRows && i < L && i >= pad) ? nh + i - pad : -1;
+  }
+  if (i_last < pad) {  // every query of the tile is padding: zero rows (uniform)
+    for (int idx = threadIdx.x; idx < kQ * kG * 16; idx += kPfThreads) {
+      const int qi = idx / (kG * 16), rest = idx - qi * kG * 16;
+      const int i = i0 + qi;
+      if (i < L)
+        *reinterpret_cast<uint4*>(a.out + b * a.out_row + i * a.out_tok + (g * kG) * kHeadDim + 8 * rest) =
+            uint4{0, 0, 0, 0};
+    }
+    return;
+  }
+  const int nkeys = nh + i_last - pad + 1;  // keys any row of the tile sees
+  const bool cached = nkeys <= a.cache_keys;  // uniform
+  const int ntiles = (nkeys + kPfKeys - 1) / kPfKeys;
+
+  // queries of the tile as doubles (padding rows and rows past L hold zeros; they are masked)
+  for (int idx = threadIdx.x; idx < kPfRows * kHeadDim; idx += kPfThreads) {
+    const int rho = idx / kHeadDim, d = idx - rho * kHeadDim;
+    const int i = i0 + rho / kG;
+    double x = 0.0;
+    if (rho < kRows && i < L)
+      x = bf16_bits_to_f32(a.q[b * a.q_row + (g * kG + rho % kG) * a.q_head + i * a.q_tok + d]);
+    sQ[rho * kHeadDim + d] = x;
+  }
+
+  // Stages K (or V) of keys [64 kt, 64 kt + 64) into sT: thread (key tid / 4, quarter tid % 4)
+  // copies four 16-byte pieces.  Keys past nkeys are zero-filled.
+  auto stage = [&](bool values, int kt) {
+    const int key = threadIdx.x >> 2, quarter = threadIdx.x & 3;
+    const int kk = kt * kPfKeys + key;
+    const uint16_t* src = nullptr;
+    if (kk < nh) {
+      int64_t id = a.history[b * a.hist_stride + kk / kBlockSize];
+      if (id < 0 || id >= a.num_blocks) id = 0;
+      src = (values ? a.value_pool : a.key_pool) + (id * kBlockSize + kk % kBlockSize) * row_elems + g * kHeadDim;
+    } else if (kk < nkeys) {
+      const int p = pad + (kk - nh);
+      src = values ? a.v + b * a.v_row + g * a.v_head + p * a.v_tok : a.k + b * a.k_row + g * a.k_head + p * a.k_tok;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int piece = quarter * 4 + c;
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (src) x = *reinterpret_cast<const u32x4*>(src + 8 * piece);
+      *reinterpret_cast<u32x4*>(sT + key * kKvRow + 8 * piece) = x;
+    }
+  };
+  // Scores of key lane of the staged tile against the wavefront's 8 rows.
+  auto tile_scores = [&](float (&s)[8]) {
+    double acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = 0.0;
+    for (int c = 0; c < kHeadDim / 8; ++c) {
+      double kd[8];
+      unpack8(*reinterpret_cast<const u32x4*>(sT + lane * kKvRow + 8 * c), kd);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const double* qr = sQ + (8 * w + k) * kHeadDim + 8 * c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[k] = fma(qr[e], kd[e], acc[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s[k] = exact_score(acc[k], a.scale);
+  };
+  auto wave_fence = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // ---- pass 1: scores and their row maxima (and the cache: sC[kk][rho], bf16)
+  float mloc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) mloc[k] = -INFINITY;
+  for (int kt = 0; kt < ntiles; ++kt) {
+    __syncthreads();  // sT is free (and sQ written, on the first tile)
+    stage(false, kt);
+    __syncthreads();
+    float s[8];
+    tile_scores(s);
+    const int kk = kt * kPfKeys + lane;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (kk <= kmax[k]) mloc[k] = fmaxf(mloc[k], s[k]);
+    }
+    if (cached && kk < nkeys) {
+      uint4 packed;
+      packed.x = static_cast<uint32_t>(bf16_bits(s[0])) | (static_cast<uint32_t>(bf16_bits(s[1])) << 16);
+      packed.y = static_cast<uint32_t>(bf16_bits(s[2])) | (static_cast<uint32_t>(bf16_bits(s[3])) << 16);
+      packed.z = static_cast<uint32_t>(bf16_bits(s[4])) | (static_cast<uint32_t>(bf16_bits(s[5])) << 16);
+      packed.w = static_cast<uint32_t>(bf16_bits(s[6])) | (static_cast<uint32_t>(bf16_bits(s[7])) << 16);
+      *reinterpret_cast<uint4*>(sC + kk * kPfRows + 8 * w) = packed;
+    }
+  }
+  float M[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) M[k] = wave_max(mloc[k]);
+
+  // ---- pass 2: denominators (a lane sums its keys kk = lane + 64 t; the wavefront reduces)
+  double hi[8], lo[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) hi[k] = lo[k] = 0.0;
+  if (cached) {
+    for (int kk = lane; kk < nkeys; kk += kPfKeys) {
+      const uint4 packed = *reinterpret_cast<const uint4*>(sC + kk * kPfRows + 8 * w);
+      const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float s = (k & 1) ? bf16_hi(words[k >> 1]) : bf16_lo(words[k >> 1]);
+        if (kk <= kmax[k]) split_add(exact_exp(s, M[k]), hi[k], lo[k]);
+      }
+    }
+  } else {
+    for (int kt = 0; kt < ntiles; ++kt) {
+      __syncthreads();
+      stage(false, kt);
+      __syncthreads();
+      float s[8];
+      tile_scores(s);
+      const int kk = kt * kPfKeys + lane;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (kk <= kmax[k]) split_add(exact_exp(s[k], M[k]), hi[k], lo[k]);
+    }
+  }
+  float Lsum[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) Lsum[k] = static_cast<float>(wave_sum_f64(hi[k]) + wave_sum_f64(lo[k]));
+  if (cached) {  // scores -> probabilities in place (this wavefront's rows, its own lanes' keys)
+    for (int kk = lane; kk < nkeys; kk += kPfKeys) {
+      uint4* cell = reinterpret_cast<uint4*>(sC + kk * kPfRows + 8 * w);
+      const uint4 packed = *cell;
+      const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
+      uint32_t outw[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float s0 = bf16_lo(words[h]), s1 = bf16_hi(words[h]);
+        const float p0 = kk <= kmax[2 * h] ? exact_prob(exact_exp(s0, M[2 * h]), Lsum[2 * h]) : 0.0f;
+        const float p1 = kk <= kmax[2 * h + 1] ? exact_prob(exact_exp(s1, M[2 * h + 1]), Lsum[2 * h + 1]) : 0.0f;
+        outw[h] = static_cast<uint32_t>(bf16_bits(p0)) | (static_cast<uint32_t>(bf16_bits(p1)) << 16);
+      }
+      *cell = uint4{outw[0], outw[1], outw[2], outw[3]};
+    }
+  }
+
+  // ---- pass 3: P V (lane: dims 2 lane, 2 lane + 1 of the wavefront's 8 rows)
+  double acc[8][2];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k][0] = acc[k][1] = 0.0;
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const uint16_t* probs;  // [64][32] bf16 probabilities of this tile's keys
+    if (cached) {
+      probs = sC + kt * kPfKeys * kPfRows;
+    } else {
+      __syncthreads();
+      stage(false, kt);
+      __syncthreads();
+      float s[8];
+      tile_scores(s);
+      const int kk = kt * kPfKeys + lane;
+      uint32_t outw[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float p0 = kk <= kmax[2 * h] ? exact_prob(exact_exp(s[2 * h], M[2 * h]), Lsum[2 * h]) : 0.0f;
+        const float p1 = kk <= kmax[2 * h + 1] ? exact_prob(exact_exp(s[2 * h + 1], M[2 * h + 1]), Lsum[2 * h + 1]) : 0.0f;
+        outw[h] = static_cast<uint32_t>(bf16_bits(p0)) | (static_cast<uint32_t>(bf16_bits(p1)) << 16);
+      }
+      *reinterpret_cast<uint4*>(sC + lane * kPfRows + 8 * w) = uint4{outw[0], outw[1], outw[2], outw[3]};
+      probs = sC;
+    }
+    wave_fence();     // this wavefront's probability stores before its reads of other lanes' keys
+    __syncthreads();  // every wavefront is done with sT
+    stage(true, kt);
+    __syncthreads();
+    const int kend = min(kPfKeys, nkeys - kt * kPfKeys);
+    for (int key = 0; key < kend; ++key) {
+      const uint4 packed = *reinterpret_cast<const uint4*>(probs + key * kPfRows + 8 * w);
+      const uint32_t pv = *reinterpret_cast<const uint32_t*>(sT + key * kKvRow + 2 * lane);
+      const double v0 = bf16_lo(pv), v1 = bf16_hi(pv);
+      const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const double p = (k & 1) ? bf16_hi(words[k >> 1]) : bf16_lo(words[k >> 1]);
+        acc[k][0] = fma(p, v0, acc[k][0]);
+        acc[k][1] = fma(p, v1, acc[k][1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int rho = 8 * w + k;
+    const int i = i0 + rho / kG;
+    if (rho >= kRows || i >= L) continue;
+    uint16_t* dst = a.out + b * a.out_row + i * a.out_tok + (g * kG + rho % kG) * kHeadDim + 2 * lane;
+    const uint32_t word = kmax[k] < 0 ? 0u
+                                      : (static_cast<uint32_t>(bf16_bits(static_cast<float>(acc[k][0]))) |
+                                         (static_cast<uint32_t>(bf16_bits(static_cast<float>(acc[k][1]))) << 16));
+    *reinterpret_cast<uint32_t*>(dst) = word;
+  }
+}
+
+// ------------------------------------------------------------------------- host ---
+bool group_ok(int g) { return g == 1 || g == 2 || g == 4 || g == 5 || g == 8; }
+
+template <typename Kernel>
+int32_t allow_lds(Kernel kernel, int bytes, const char* what) {
+  // Dynamic LDS above 64 KiB must be allowed per kernel (gfx950 has 160 KiB per workgroup).
+  const hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (err != hipSuccess) return fail(MI_ERR_DEVICE, "%s: hipFuncSetAttribute: %s", what, hipGetErrorString(err));
+  return MI_OK;
+}
+
+template <int kG, bool kPrologue>
+int32_t launch_exact_decode(const ExactDecodeArgs& a, int32_t batch, hipStream_t s) {
+  static std::once_flag once;
+  static int32_t attr_rc = MI_OK;
+  std::call_once(once, [] { attr_rc = allow_lds(exact_decode_kernel<kG, kPrologue>, kDecCacheBytes, "mi_paged_decode_attention_exact"); });
+  if (attr_rc != MI_OK) return attr_rc;
+  const size_t lds = static_cast<size_t>(a.cache_tokens) * kG * sizeof(uint16_t);
+  exact_decode_kernel<kG, kPrologue><<<dim3(batch, a.kv_heads), kDecThreads, lds, s>>>(a);
+  return check_launch("mi_paged_decode_attention_exact");
+}
+
+template <bool kPrologue>
+int32_t dispatch_exact_decode(const ExactDecodeArgs& a, int32_t batch, int group, hipStream_t s) {
+  switch (group) {
+    case 1: return launch_exact_decode<1, kPrologue>(a, batch, s);
+    case 2: return launch_exact_decode<2, kPrologue>(a, batch, s);
+    case 4: return launch_exact_decode<4, kPrologue>(a, batch, s);
+    case 5: return launch_exact_decode<5, kPrologue>(a, batch, s);
+    default: return launch_exact_decode<8, kPrologue>(a, batch, s);
+  }
+}
+
+template <int kG>
+int32_t launch_exact_prefill(const ExactPrefillArgs& a, int32_t batch, hipStream_t s) {
+  static std::once_flag once;
+  static int32_t attr_rc = MI_OK;
+  std::call_once(once, [] { attr_rc = allow_lds(exact_prefill_kernel<kG>, kPfLdsBytes, "mi_chunked_prefill_attention_exact"); });
+  if (attr_rc != MI_OK) return attr_rc;
+  constexpr int kQ = kPfRows / kG;
+  const size_t lds = static_cast<size_t>(kPfQBytes) + kPfTileBytes + static_cast<size_t>(a.cache_keys) * kPfRows * 2;
+  const dim3 grid((a.padded_len + kQ - 1) / kQ, a.kv_heads, batch);
+  exact_prefill_kernel<kG><<<grid, kPfThreads, lds, s>>>(a);
+  return check_launch("mi_chunked_prefill_attention_exact");
+}
+
+int32_t dispatch_exact_prefill(const ExactPrefillArgs& a, int32_t batch, int group, hipStream_t s) {
+  switch (group) {
+    case 1: return launch_exact_prefill<1>(a, batch, s);
+    case 2: return launch_exact_prefill<2>(a, batch, s);
+    case 4: return launch_exact_prefill<4>(a, batch, s);
+    case 5: return launch_exact_prefill<5>(a, batch, s);
+    default: return launch_exact_prefill<8>(a, batch, s);
+  }
+}
+
+int32_t check_exact_heads(const char* what, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t block_size) {
+  if (head_dim != kHeadDim || block_size != kBlockSize || num_kv_heads <= 0 || num_heads <= 0 ||
+      num_heads % num_kv_heads != 0 || !group_ok(num_heads / num_kv_heads))
+    return fail(MI_ERR_UNSUPPORTED,
+                "%s: needs head_dim %d, block_size %d and %s (got head_dim %d, block_size %d, heads %d/%d)", what,
+                kHeadDim, kBlockSize, "1, 2, 4, 5 or 8 query heads per KV head", head_dim, block_size, num_heads,
+                num_kv_heads);
+  if (num_kv_heads > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: too many KV heads", what);
+  return MI_OK;
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int32_t mi_paged_decode_attention_exact(
+    void* out, int64_t out_row_stride, const void* q, int64_t q_row_stride, int64_t q_head_stride, const void* k,
+    int64_t k_row_stride, const void* v, int64_t v_row_stride, const void* q_weight, const void* k_weight,
+    const void* cos, const void* sin, float eps, const int64_t* slot_mapping, int64_t slot_stride, void* key_pool,
+    void* value_pool, int64_t num_blocks, const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,
+    const int64_t* context_lens, int64_t context_lens_stride, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, float scale, void* stream) {
+  using namespace mi;
+  const char* what = "mi_paged_decode_attention_exact";
+  if (batch < 0 || max_blocks < 0 || num_blocks < 0) return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
+  if (batch == 0) return ok();
+  if (const int32_t rc = check_exact_heads(what, num_heads, num_kv_heads, head_dim, block_size)) return rc;
+  const bool prologue = q_weight != nullptr;
+  if (!out || !q || !key_pool || !value_pool || !context_lens || (max_blocks > 0 && !block_tables))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
+  if (prologue && (!k || !v || !k_weight || !cos || !sin || !slot_mapping))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: the prologue form needs k, v, k_weight, cos, sin and slot_mapping", what);
+  if (!aligned16(out) || out_row_stride % 8 != 0 || !aligned16(key_pool) || !aligned16(value_pool))
+    return fail(MI_ERR_UNSUPPORTED, "%s: out and pools must be 16-byte aligned", what);
+  if ((max_blocks > 0 && block_table_stride < max_blocks) || context_lens_stride <= 0 ||
+      (prologue && (q_row_stride < static_cast<int64_t>(num_heads) * head_dim ||
+                    k_row_stride < static_cast<int64_t>(num_kv_heads) * head_dim ||
+                    v_row_stride < static_cast<int64_t>(num_kv_heads) * head_dim)))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: bad stride", what);
+  if (num_blocks > INT64_MAX / (kBlockSize * static_cast<int64_t>(num_kv_heads) * head_dim))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: pool too large", what);
+  const int group = num_heads / num_kv_heads;
+  ExactDecodeArgs a{};
+  a.out = static_cast<uint16_t*>(out);
+  a.out_row = out_row_stride;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_row = q_row_stride;
+  a.q_head = prologue ? head_dim : q_head_stride;
+  a.k_new = static_cast<const uint16_t*>(k);
+  a.v_new = static_cast<const uint16_t*>(v);
+  a.k_row = k_row_stride;
+  a.v_row = v_row_stride;
+  a.q_weight = static_cast<const uint16_t*>(q_weight);
+  a.k_weight = static_cast<const uint16_t*>(k_weight);
+  a.cos = static_cast<const uint16_t*>(cos);
+  a.sin = static_cast<const uint16_t*>(sin);
+  a.eps = eps;
+  a.slot_mapping = slot_mapping;
+  a.slot_stride = slot_stride;
+  a.num_slots = num_blocks * kBlockSize;
+  a.key_pool = static_cast<uint16_t*>(key_pool);
+  a.value_pool = static_cast<uint16_t*>(value_pool);
+  a.num_blocks = num_blocks;
+  a.kv_heads = num_kv_heads;
+  a.block_tables = block_tables;
+  a.bt_stride = block_table_stride;
+  a.max_blocks = max_blocks;
+  a.context_lens = context_lens;
+  a.ctx_stride = context_lens_stride;
+  a.scale = scale;
+  const int64_t tokens = static_cast<int64_t>(max_blocks) * kBlockSize;
+  a.cache_tokens = tokens * group * static_cast<int64_t>(sizeof(uint16_t)) <= kDecCacheBytes ? static_cast<int32_t>(tokens) : 0;
+  hipStream_t s = as_stream(stream);
+  // One launch per 65535 sequences (grid y holds the KV heads, x the sequences).
+  for (int32_t b0 = 0; b0 < batch; b0 += 65535) {
+    const int32_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
+    ExactDecodeArgs c = a;
+    c.out = a.out + b0 * out_row_stride;
+    c.q = a.q + b0 * q_row_stride;
+    c.context_lens = context_lens + b0 * context_lens_stride;
+    c.block_tables = block_tables ? block_tables + b0 * block_table_stride : nullptr;
+    if (prologue) {
+      c.k_new = a.k_new + b0 * k_row_stride;
+      c.v_new = a.v_new + b0 * v_row_stride;
+      c.cos = a.cos + b0 * static_cast<int64_t>(head_dim);
+      c.sin = a.sin + b0 * static_cast<int64_t>(head_dim);
+      c.slot_mapping = slot_mapping + b0 * slot_stride;
+    }
+    const int32_t rc = prologue ? dispatch_exact_decode<true>(c, nb, group, s) : dispatch_exact_decode<false>(c, nb, group, s);
+    if (rc != MI_OK) return rc;
+  }
+  return ok();
+}
+
+extern "C" int32_t mi_chunked_prefill_attention_exact(
+    void* out, int64_t out_row_stride, int64_t out_tok_stride, const void* query, int64_t query_row_stride,
+    int64_t query_head_stride, int64_t query_tok_stride, const void* key, int64_t key_row_stride,
+    int64_t key_head_stride, int64_t key_tok_stride, const void* value, int64_t value_row_stride,
+    int64_t value_head_stride, int64_t value_tok_stride, const void* key_pool, const void* value_pool,
+    int64_t num_blocks, const int64_t* history_blocks, int64_t history_stride, int32_t max_history_blocks,
+    const int64_t* start_lens, const int64_t* chunk_lens, int64_t lens_stride, int32_t batch, int32_t padded_len,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale, void* stream) {
+  using namespace mi;
+  const char* what = "mi_chunked_prefill_attention_exact";
+  if (batch < 0 || padded_len < 0 || max_history_blocks < 0 || num_blocks < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
+  if (batch == 0 || padded_len == 0) return ok();
+  if (const int32_t rc = check_exact_heads(what, num_heads, num_kv_heads, head_dim, block_size)) return rc;
+  if (!out || !query || !key || !value || !start_lens || !chunk_lens ||
+      (max_history_blocks > 0 && (!history_blocks || !key_pool || !value_pool)))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
+  if (!aligned16(out) || !aligned16(key) || !aligned16(value) || (max_history_blocks > 0 &&
+      (!aligned16(key_pool) || !aligned16(value_pool))) || out_row_stride % 8 != 0 || out_tok_stride % 8 != 0 ||
+      key_row_stride % 8 != 0 || key_head_stride % 8 != 0 || key_tok_stride % 8 != 0 || value_row_stride % 8 != 0 ||
+      value_head_stride % 8 != 0 || value_tok_stride % 8 != 0)
+    return fail(MI_ERR_UNSUPPORTED, "%s: out / key / value / pools need 16-byte alignment and strides of 8 elements", what);
+  if (lens_stride <= 0 || (max_history_blocks > 0 && history_stride < max_history_blocks))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: bad stride", what);
+  if (batch > 65535 || num_kv_heads > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: batch above 65535", what);
+  const int group = num_heads / num_kv_heads;
+  ExactPrefillArgs a{};
+  a.out = static_cast<uint16_t*>(out);
+  a.out_row = out_row_stride;
+  a.out_tok = out_tok_stride;
+  a.q = static_cast<const uint16_t*>(query);
+  a.q_row = query_row_stride;
+  a.q_head = query_head_stride;
+  a.q_tok = query_tok_stride;
+  a.k = static_cast<const uint16_t*>(key);
+  a.k_row = key_row_stride;
+  a.k_head = key_head_stride;
+  a.k_tok = key_tok_stride;
+  a.v = static_cast<const uint16_t*>(value);
+  a.v_row = value_row_stride;
+  a.v_head = value_head_stride;
+  a.v_tok = value_tok_stride;
+  a.key_pool = static_cast<const uint16_t*>(key_pool);
+  a.value_pool = static_cast<const uint16_t*>(value_pool);
+  a.num_blocks = num_blocks;
+  a.kv_heads = num_kv_heads;
+  a.history = history_blocks;
+  a.hist_stride = history_stride;
+  a.max_hist_blocks = max_history_blocks;
+  a.start_lens = start_lens;
+  a.chunk_lens = chunk_lens;
+  a.lens_stride = lens_stride;
+  a.padded_len = padded_len;
+  a.scale = scale;
+  // Keys a row can see: its history (at most the table's) plus the chunk up to it.
+  const int64_t keys = static_cast<int64_t>(max_history_blocks) * kBlockSize + padded_len;
+  const int64_t keys_up = (keys + kPfKeys - 1) / kPfKeys * kPfKeys;
+  a.cache_keys = keys_up <= kPfMaxCacheKeys ? static_cast<int32_t>(keys_up) : kPfKeys;
+  const int32_t rc = dispatch_exact_prefill(a, batch, group, as_stream(stream));
+  return rc == MI_OK ? ok() : rc;
+}

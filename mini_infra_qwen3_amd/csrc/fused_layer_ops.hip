@@ -7,12 +7,13 @@
 // the decode K/V append of _apply_paged_kv_pool (:282-283), and the SwiGLU product of
 // Qwen3MLP.forward (:347-355).  Here each group is one launch that keeps the reference's bf16
 // rounding points:
-//   * RMSNorm:  n = bf16(x * rsqrt(sum(x^2) / N + eps)) in fp32, y = bf16(w * n);
+//   * RMSNorm:  n = bf16(x * r), y = bf16(w * n), with r = 1 / sqrt(sum(x^2) / N + eps) from an
+//     exact sum of squares (fp64) and one rounding to fp32 per step (mi_common.h, rms_inv);
 //   * residual: h = bf16(a + b);
 //   * RoPE:     y = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin));
 //   * SwiGLU:   y = bf16(bf16(silu(g)) * u), silu(g) = g / (1 + exp(-g)) in fp32.
-// The only freedom taken is the order of the fp32 sum of squares (a wave-wide tree), which can
-// move a normalised value by one bf16 ulp when it sits on a rounding boundary.
+// The one deviation from the ATen chain is that the sum of squares is exact instead of an fp32
+// sum in ATen's order, so the result does not depend on how the sum is split over lanes.
 //
 // All tensors are bf16 with rows of contiguous elements; the kernels are memory-light (a decode
 // step moves a few MB), so the point is launch count, not bandwidth.
@@ -27,12 +28,6 @@ namespace {
 constexpr int kThreads = 256;  // 4 wavefronts
 constexpr int kWave = 64;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
-
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) { return static_cast<uint16_t>(f32_to_bf16_bits(f)); }
 
@@ -45,7 +40,6 @@ struct NormArgs {
   const uint16_t* weight;
   int64_t rows;
   int32_t hidden;
-  float inv_hidden;
   float eps;
 };
 
@@ -58,7 +52,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const NormArgs a) {
   const int pieces = a.hidden / 8;
   const int64_t base = row * a.hidden;
   u32x4 h[kPieces];
-  float ss = 0.f;
+  double ss = 0.0;
 #pragma unroll
   for (int p = 0; p < kPieces; ++p) {
     const int piece = lane + p * kWave;
@@ -73,13 +67,14 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const NormArgs a) {
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float lo = bf16_lo(v[j]), hi = bf16_hi(v[j]);
-        ss += lo * lo + hi * hi;
+        const double lo = bf16_lo(v[j]), hi = bf16_hi(v[j]);
+        ss += lo * lo;
+        ss += hi * hi;
       }
       h[p] = v;
     }
   }
-  const float r = rsqrtf(wave_sum(ss) * a.inv_hidden + a.eps);
+  const float r = rms_inv(wave_sum64_f64(ss), static_cast<double>(a.hidden), a.eps);
 #pragma unroll
   for (int p = 0; p < kPieces; ++p) {
     const int piece = lane + p * kWave;
@@ -202,8 +197,7 @@ extern "C" int32_t mi_rms_norm(void* out, const void* x, const void* residual, v
   if (!aligned(out) || !aligned(x) || !aligned(residual) || !aligned(residual_out) || !aligned(weight))
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_rms_norm: pointers must be 16-byte aligned");
   NormArgs a{static_cast<uint16_t*>(out), static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(residual),
-             static_cast<uint16_t*>(residual_out), static_cast<const uint16_t*>(weight), rows, hidden,
-             1.0f / static_cast<float>(hidden), eps};
+             static_cast<uint16_t*>(residual_out), static_cast<const uint16_t*>(weight), rows, hidden, eps};
   const int64_t groups = (rows + kThreads / kWave - 1) / (kThreads / kWave);
   if (groups > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "mi_rms_norm: too many rows");
   hipStream_t s = as_stream(stream);

@@ -68,23 +68,41 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
-// ------------------------------------------------------- q/k norm + RoPE ---
-__device__ __forceinline__ float wave_sum64(float v) {
+// ------------------------------------------------------- RMSNorm, exact ---
+// The reference's RMSNorm (src/mini_infra/model/qwen3.py:67-78) is
+//   h = x.float(); y = w * (h * rsqrt(h.pow(2).mean(-1) + eps)).to(bf16)
+// whose fp32 mean depends on the order ATen sums the squares in.  Here the sum is exact (the
+// square of a bf16 value has at most 16 significant bits, so fp64 adds them without loss unless
+// the terms span more than 2^37), and so is the reciprocal square root:
+//   var = fp32(sum(h^2) / N),  t = fp32(var + eps),  r = fp32(1 / sqrt_f64(t))
+// (sqrt and division correctly rounded in fp64, then one rounding to fp32) -- a result that does
+// not depend on the reduction order or the device, which torch's on-device chain also gives
+// whenever its fp32 sum rounds the same way.
+__device__ __forceinline__ double wave_sum64_f64(double v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
   return v;
 }
 
+// r = fp32(1 / sqrt(fp32(fp32(sum_sq / n) + eps))), the division by n in fp64.
+__device__ __forceinline__ float rms_inv(double sum_sq, double n, float eps) {
+  const float var = static_cast<float>(sum_sq / n);
+  const float t = var + eps;
+  return static_cast<float>(1.0 / sqrt(static_cast<double>(t)));
+}
+
+// ------------------------------------------------------- q/k norm + RoPE ---
 // Per-head RMSNorm + RoPE of one 128-wide q or k head by one wavefront, with the reference's bf16
 // rounding points (src/mini_infra/model/qwen3.py:67-78 on the head, then _apply_rotary_embedding
-// :111-145): n = bf16(x * rsqrt(mean(x^2) + eps)), y = bf16(w * n),
+// :111-145): n = bf16(x * r) with r the exact reciprocal RMS above, y = bf16(w * n),
 // out = bf16(bf16(y * cos) + bf16(rotate_half(y) * sin)).  Lane l owns elements l and l + 64, the
 // pair rotate_half couples, so the rotation is lane-local; o0 / o1 are elements l / l + 64 (exact
 // bf16 values held in fp32).
 __device__ __forceinline__ void norm_rope_head(const uint16_t* src, const uint16_t* weight, const uint16_t* cos,
                                                const uint16_t* sin, float eps, int lane, float& o0, float& o1) {
   const float x0 = bf16_bits_to_f32(src[lane]), x1 = bf16_bits_to_f32(src[lane + 64]);
-  const float r = rsqrtf(wave_sum64(x0 * x0 + x1 * x1) * (1.0f / 128.0f) + eps);
+  const double sq = static_cast<double>(x0) * x0 + static_cast<double>(x1) * x1;
+  const float r = rms_inv(wave_sum64_f64(sq), 128.0, eps);
   const float y0 = round_bf16(bf16_bits_to_f32(weight[lane]) * round_bf16(x0 * r));
   const float y1 = round_bf16(bf16_bits_to_f32(weight[lane + 64]) * round_bf16(x1 * r));
   // element l:      y*cos - y[l+64]*sin ; element l+64: y*cos + y[l]*sin  (rotate_half = cat(-y2, y1))

@@ -227,6 +227,7 @@ def paged_decode_attention(
     scale: float,
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    exact: bool = False,
 ) -> torch.Tensor:
     """Paged GQA decode attention straight from the pool (kernel 3).
 
@@ -234,7 +235,9 @@ def paged_decode_attention(
     contiguous, block_size 16 or a multiple of it; block_tables ``[B, max_blocks]`` int64
     (null-padded); context_lens ``[B]`` int64 (includes the new token).  Returns ``out``
     ``[B, H * D]`` bf16.  ``workspace`` (optional, uint8, reused across calls) holds the
-    split-context partials; it is allocated here when missing or too small.
+    split-context partials; it is allocated here when missing or too small.  ``exact``: the
+    reference-numerics kernel (``mi_paged_decode_attention_exact``: the reference's rounding
+    points with exact sums; no workspace).
     """
     device = key_pool.device
     for name, t in (("query", query), ("key_pool", key_pool), ("value_pool", value_pool),
@@ -267,6 +270,15 @@ def paged_decode_attention(
         return out
     lib = _native.load()
     stream = _stream(device)
+    if exact:
+        rc = lib.mi_paged_decode_attention_exact(
+            out.data_ptr(), out.stride(0), query.data_ptr(), query.stride(0), query.stride(1), None, 0, None, 0, None,
+            None, None, None, 0.0, None, 0, key_pool.data_ptr(), value_pool.data_ptr(), num_blocks,
+            block_tables.data_ptr(), block_tables.stride(0) if batch > 1 else max(max_blocks, 1), max_blocks,
+            context_lens.data_ptr(), context_lens.stride(0) if batch > 1 else 1, batch, num_heads, num_kv_heads,
+            head_dim, block_size, float(scale), stream)
+        _native.check(rc, "mi_paged_decode_attention_exact")
+        return out
     need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size, num_kv_heads)
     ws_ptr, ws_bytes = None, 0
     if need > 0:
@@ -304,9 +316,11 @@ def paged_decode_attention_fused(
     scale: float,
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    exact: bool = False,
 ) -> torch.Tensor:
     """``qk_norm_rope`` (decode form: the new K/V rows go to ``slot_mapping``) followed by
-    ``paged_decode_attention``, in one launch where the per-sequence kernel serves the batch.
+    ``paged_decode_attention``, in one launch where the per-sequence kernel serves the batch
+    (with ``exact``: always one launch of the reference-numerics kernel).
 
     q ``[B, Hq * 128]``, k / v ``[B, Hkv * 128]``: the new tokens' projection rows (row views are
     fine); cos / sin ``[B, 128]``; the rest as in the two functions.  Same results, bit for bit.
@@ -345,6 +359,17 @@ def paged_decode_attention_fused(
         raise ValueError(f"out must be [B, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
     if batch == 0:
         return out
+    if exact:
+        rc = _native.load().mi_paged_decode_attention_exact(
+            out.data_ptr(), out.stride(0), q2.data_ptr(), q2.stride(0), head_dim, k2.data_ptr(), k2.stride(0),
+            v2.data_ptr(), v2.stride(0), q_weight.data_ptr(), k_weight.data_ptr(), cos2.data_ptr(), sin2.data_ptr(),
+            float(eps), slot_mapping.data_ptr(), slot_mapping.stride(0) if batch > 1 else 1, key_pool.data_ptr(),
+            value_pool.data_ptr(), num_blocks, block_tables.data_ptr(),
+            block_tables.stride(0) if batch > 1 else max(max_blocks, 1), max_blocks, context_lens.data_ptr(),
+            context_lens.stride(0) if batch > 1 else 1, batch, num_heads, num_kv_heads, head_dim, block_size,
+            float(scale), _stream(device))
+        _native.check(rc, "mi_paged_decode_attention_exact")
+        return out
     q_scratch = torch.empty((batch, num_heads, head_dim), dtype=torch.bfloat16, device=device)
     need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size, num_kv_heads)
     ws_ptr, ws_bytes = None, 0
@@ -375,8 +400,10 @@ def chunked_prefill_attention(
     chunk_lens: torch.Tensor,
     scale: float,
     out: torch.Tensor | None = None,
+    exact: bool = False,
 ) -> torch.Tensor:
-    """Chunked-prefill attention with the history read from the pool (kernel 4, MFMA).
+    """Chunked-prefill attention with the history read from the pool (kernel 4, MFMA; with
+    ``exact`` the reference-numerics kernel ``mi_chunked_prefill_attention_exact``).
 
     query ``[B, H, L, D]``; key / value ``[B, H_kv, L, D]`` (left-padded chunk, D contiguous, any
     other strides); pools ``[num_blocks, block_size, H_kv, D]``, block_size 16 or a multiple of it;
@@ -418,7 +445,8 @@ def chunked_prefill_attention(
         raise ValueError(f"out must be [B, L, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
     if batch == 0 or padded_len == 0:
         return out
-    rc = _native.load().mi_chunked_prefill_attention(
+    entry = _native.load().mi_chunked_prefill_attention_exact if exact else _native.load().mi_chunked_prefill_attention
+    rc = entry(
         out.data_ptr(), out.stride(0), out.stride(1),
         query.data_ptr(), query.stride(0), query.stride(1), query.stride(2),
         key.data_ptr(), key.stride(0), key.stride(1), key.stride(2),
@@ -429,7 +457,7 @@ def chunked_prefill_attention(
         batch, padded_len, num_heads, num_kv_heads, head_dim, block_size, float(scale),
         _stream(device),
     )
-    _native.check(rc, "mi_chunked_prefill_attention")
+    _native.check(rc, "mi_chunked_prefill_attention_exact" if exact else "mi_chunked_prefill_attention")
     return out
 
 

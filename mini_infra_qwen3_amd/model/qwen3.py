@@ -16,10 +16,21 @@ state_dict loads unchanged.  The attention differs in how it reaches K/V:
   run once over all tokens; q/k norm + RoPE and attention run in their prefill and decode forms
   on the two token ranges, writing one output buffer.
 
-Dense GEMMs (projections, MLP, lm_head) stay on PyTorch-ROCm -- q/k/v, and gate/up, each as one
-GEMM over the row-concatenated weights, the outputs split as column views; the elementwise chains around them
+Dense GEMMs (projections, MLP, lm_head) stay on PyTorch-ROCm; the elementwise chains around them
 run as fused launches of the same library (``data_plane.rms_norm`` with the residual add,
 ``qk_norm_rope`` with the decode append, ``silu_mul``), keeping the reference's bf16 rounding points.
+
+Numerics (``Qwen3ForCausalLM(config, exact=...)``):
+
+* ``exact=True`` (the default) is bit-identical to the reference op chain evaluated with exact
+  sums (``oracle.qwen3_ref.ReferenceQwen3(exact=True)``): attention runs the reference-numerics
+  kernels (the reference's rounding points, exact sums), RMSNorm sums exactly, and every GEMM is
+  the call the reference makes -- q, k, v, gate and up as separate projections, since hipBLASLt's
+  result for a row can depend on the GEMM's N and M.  Greedy decoding then reproduces the
+  reference's tokens exactly.
+* ``exact=False`` runs the bandwidth kernels (fp32 online softmax, MFMA prefill) and q/k/v and
+  gate/up each as one GEMM over row-concatenated weights (the outputs split as column views):
+  within bf16 tolerance of the reference, not bit-identical.
 """
 
 from __future__ import annotations
@@ -131,8 +142,9 @@ def _concat_weight(owner: nn.Module, linears: tuple[nn.Linear, ...]) -> torch.Te
 
 
 class Qwen3Attention(nn.Module):
-    def __init__(self, config: Qwen3Config):
+    def __init__(self, config: Qwen3Config, exact: bool = True):
         super().__init__()
+        self.exact = exact
         self.num_heads = config.num_attention_heads
         self.num_kv_heads = config.num_key_value_heads
         self.head_dim = config.head_dim
@@ -149,8 +161,11 @@ class Qwen3Attention(nn.Module):
         when decoding, the K/V append into the pool), then paged attention."""
         batch, length, _ = hidden.shape
         nq, nkv = self.num_heads * self.head_dim, self.num_kv_heads * self.head_dim
-        qkv = F.linear(hidden, _concat_weight(self, (self.q_proj, self.k_proj, self.v_proj)))
-        q, k, v = qkv[..., :nq], qkv[..., nq:nq + nkv], qkv[..., nq + nkv:]
+        if self.exact:
+            q, k, v = self.q_proj(hidden), self.k_proj(hidden), self.v_proj(hidden)
+        else:
+            qkv = F.linear(hidden, _concat_weight(self, (self.q_proj, self.k_proj, self.v_proj)))
+            q, k, v = qkv[..., :nq], qkv[..., nq:nq + nkv], qkv[..., nq + nkv:]
         key_pool, value_pool = kv_pool
         eps = self.q_norm.eps
         if isinstance(metadata, PagedMixedMetadata):
@@ -159,6 +174,7 @@ class Qwen3Attention(nn.Module):
             out = data_plane.paged_decode_attention_fused(
                 q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin, eps, metadata.slot_mapping, key_pool,
                 value_pool, metadata.block_tables, metadata.context_lens, self.scaling, workspace=workspace,
+                exact=self.exact,
             ).view(batch, 1, -1)
             present = kv_pool
         else:
@@ -171,7 +187,7 @@ class Qwen3Attention(nn.Module):
             v_rows = v_rows.view(batch, length, self.num_kv_heads, self.head_dim).transpose(1, 2)
             out = data_plane.chunked_prefill_attention(
                 q_rot, k_rot, v_rows, key_pool, value_pool, metadata.history_block_tables, metadata.start_lens,
-                metadata.chunk_lens, self.scaling,
+                metadata.chunk_lens, self.scaling, exact=self.exact,
             )
             present = (k_rot, v_rows)
         return self.o_proj(out), present
@@ -189,7 +205,7 @@ class Qwen3Attention(nn.Module):
         data_plane.paged_decode_attention_fused(q[n:], k[n:], v[n:], self.q_norm.weight, self.k_norm.weight, cos[n:],
                                                 sin[n:], eps, decode.slot_mapping, key_pool, value_pool,
                                                 decode.block_tables, decode.context_lens, self.scaling,
-                                                out=out[n:], workspace=workspace)
+                                                out=out[n:], workspace=workspace, exact=self.exact)
         k_buf, v_buf = kv_out if kv_out is not None else (None, None)
         q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q[:n], k[:n], v[:n], self.q_norm.weight, self.k_norm.weight,
                                                        cos[:n], sin[:n], eps, k_out=k_buf, v_out=v_buf)
@@ -199,28 +215,31 @@ class Qwen3Attention(nn.Module):
         prefill = metadata.prefill
         data_plane.chunked_prefill_attention(q_rot, k_rot, v_rows, key_pool, value_pool, prefill.history_block_tables,
                                              prefill.start_lens, prefill.chunk_lens, self.scaling,
-                                             out=out[:n].view(rows, width, -1))
+                                             out=out[:n].view(rows, width, -1), exact=self.exact)
         return self.o_proj(out.unsqueeze(0)), (k_rot, v_rows)
 
 
 class Qwen3MLP(nn.Module):
-    def __init__(self, config: Qwen3Config):
+    def __init__(self, config: Qwen3Config, exact: bool = True):
         super().__init__()
+        self.exact = exact
         self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.exact:
+            return self.down_proj(data_plane.silu_mul(self.gate_proj(x), self.up_proj(x)))
         inter = self.gate_proj.out_features
         gate_up = F.linear(x, _concat_weight(self, (self.gate_proj, self.up_proj)))
         return self.down_proj(data_plane.silu_mul(gate_up[..., :inter], gate_up[..., inter:]))
 
 
 class Qwen3DecoderLayer(nn.Module):
-    def __init__(self, config: Qwen3Config):
+    def __init__(self, config: Qwen3Config, exact: bool = True):
         super().__init__()
-        self.self_attn = Qwen3Attention(config)
-        self.mlp = Qwen3MLP(config)
+        self.self_attn = Qwen3Attention(config, exact)
+        self.mlp = Qwen3MLP(config, exact)
         self.input_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, config.rms_norm_eps)
 
@@ -235,12 +254,12 @@ class Qwen3DecoderLayer(nn.Module):
 
 
 class Qwen3Model(nn.Module):
-    def __init__(self, config: Qwen3Config):
+    def __init__(self, config: Qwen3Config, exact: bool = True):
         super().__init__()
         config.validate()
         self.config = config
         self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
-        self.layers = nn.ModuleList([Qwen3DecoderLayer(config) for _ in range(config.num_hidden_layers)])
+        self.layers = nn.ModuleList([Qwen3DecoderLayer(config, exact) for _ in range(config.num_hidden_layers)])
         self.norm = RMSNorm(config.hidden_size, config.rms_norm_eps)
         self.rotary_emb = RotaryEmbedding(config.head_dim, config.rope_theta)
         # Stand-in pool for prefill without history (the kernel reads no pool rows then).
@@ -335,13 +354,26 @@ class Qwen3Model(nn.Module):
 
 
 class Qwen3ForCausalLM(nn.Module):
-    def __init__(self, config: Qwen3Config):
+    def __init__(self, config: Qwen3Config, exact: bool = True):
+        """``exact``: reference numerics (bit-identical to the reference op chain with exact sums;
+        the reference's GEMM calls); ``False``: the bandwidth kernels and fused GEMMs."""
         super().__init__()
         self.config = config
-        self.model = Qwen3Model(config)
+        self.model = Qwen3Model(config, exact)
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
         if config.tie_word_embeddings:
             self.lm_head.weight = self.model.embed_tokens.weight
+
+    @property
+    def exact(self) -> bool:
+        return self.model.layers[0].self_attn.exact if len(self.model.layers) else True
+
+    def set_exact(self, exact: bool) -> "Qwen3ForCausalLM":
+        """Switches every layer between reference numerics and the bandwidth kernels (same weights)."""
+        for layer in self.model.layers:
+            layer.self_attn.exact = exact
+            layer.mlp.exact = exact
+        return self
 
     def forward(self, input_ids, attention_mask=None, position_ids=None, attn_metadata=None,
                 last_logits_only: bool = False):

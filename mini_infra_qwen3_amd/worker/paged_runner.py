@@ -13,7 +13,11 @@ Same entry points, arguments and return types as the reference's PagedRunner
   ``enable_decode_graphs`` the whole decode forward is captured once per padded (batch, blocks)
   bucket in a HIP graph: ``prepare_decode_inputs`` then packs the step (pad rows: slot -1 = no
   append, context 0 = zero output) straight into the bucket's static metadata buffer with one
-  upload, and ``run_decode_step`` replays the graph -- one launch instead of ~300;
+  upload, and ``run_decode_step`` replays the graph -- one launch instead of ~300.  A model with
+  reference numerics (``exact``) gets one graph per batch size instead (a GEMM's rows can change
+  with its M, so padding the batch would change them) and one table width (the decode kernel
+  reads only the blocks a row's context covers); prefill and mixed graphs, which pad the chunk
+  width, are for models without reference numerics;
 * ``prepare_mixed_inputs`` / ``run_mixed_step`` run prefill chunks and decode tokens in one forward
   (the mixed batching the reference plans next: src/mini_infra/core/scheduler.py:310-311).
 """
@@ -226,7 +230,11 @@ class PagedRunner(BaseModelRunner):
         another pool, run without a graph."""
         if self.device.type != "cuda":
             raise RuntimeError("decode graphs need the GPU")
-        if batch_buckets is None:
+        exact = getattr(self.model, "exact", False)
+        if exact:  # every batch size its own graph (no padded rows in the GEMMs), one table width
+            batch_buckets = range(1, max_batch + 1)
+            block_quantum = max(int(max_blocks), 1)
+        elif batch_buckets is None:
             batch_buckets = [b for b in (1, 2, 4, 8, 12, 16, 24, 32, 48, 64, 80, 96, 112, 128, 160, 192, 224, 256)
                              if b < max_batch] + [max_batch]
         self._batch_buckets = sorted(set(int(b) for b in batch_buckets if 0 < b <= max_batch))
@@ -250,6 +258,7 @@ class PagedRunner(BaseModelRunner):
         does)."""
         if self.device.type != "cuda":
             raise RuntimeError("prefill graphs need the GPU")
+        self._refuse_padded_graphs("prefill")
         top_w = -(-max_width // width_quantum) * width_quantum
         staging = self._shared_staging(max_rows * top_w, pool)
         self._prefill_pool = pool
@@ -272,6 +281,7 @@ class PagedRunner(BaseModelRunner):
         graphs, store a step's ``prefill_cache`` before the next graphed step."""
         if self.device.type != "cuda":
             raise RuntimeError("mixed graphs need the GPU")
+        self._refuse_padded_graphs("mixed")
         if decode_row_buckets is None:
             decode_row_buckets = [b for b in (1, 2, 4, 8, 16, 32, 64, 128, 256) if b < max_decode_rows]
             decode_row_buckets.append(max_decode_rows)
@@ -289,6 +299,11 @@ class PagedRunner(BaseModelRunner):
                         self.model, pool, rows, width, d, *self._mixed_tables, staging, self._mempool,
                         self.pad_token_id, self.device)
         torch.cuda.synchronize(self.device)
+
+    def _refuse_padded_graphs(self, kind: str) -> None:
+        if getattr(self.model, "exact", False):
+            raise ValueError(f"{kind} graphs pad the chunk width, which changes the GEMMs' M and with it the bits of "
+                             "their rows: a model with reference numerics (exact) runs these steps without graphs")
 
     def _mixed_bucket(self, rows: int, width: int, hist_blocks: int, decode_rows: int,
                       decode_blocks: int) -> _MixedGraph | None:

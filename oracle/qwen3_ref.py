@@ -19,8 +19,13 @@ from oracle import torch_ref
 class ReferenceQwen3:
     """The reference model as functions of its weights (``config`` needs the Qwen3Config fields)."""
 
-    def __init__(self, config, state_dict: dict[str, torch.Tensor], device: str | torch.device = "cpu"):
+    def __init__(self, config, state_dict: dict[str, torch.Tensor], device: str | torch.device = "cpu",
+                 exact: bool = False):
+        """``exact``: RMSNorm and attention with exact sums at the reference's rounding points
+        (``torch_ref.rms_norm_exact`` / ``attend_exact``) instead of ATen's fp32 sums -- the
+        numerics of the HIP model; everything else is the same op chain."""
         self.config = config
+        self.exact = exact
         self.w = {k: v.detach().to(device) for k, v in state_dict.items()}
         if "lm_head.weight" not in self.w:
             self.w["lm_head.weight"] = self.w["model.embed_tokens.weight"]
@@ -31,6 +36,8 @@ class ReferenceQwen3:
 
     # -- building blocks (qwen3.py:55-156) ---------------------------------------------------
     def _rms(self, x, weight):
+        if self.exact:
+            return torch_ref.rms_norm_exact(x, weight, self.config.rms_norm_eps)
         xf = x.float()
         normed = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.config.rms_norm_eps)
         return weight * normed.to(x.dtype)
@@ -63,10 +70,14 @@ class ReferenceQwen3:
         return F.linear(gate * F.linear(x, self.w[p + "up_proj.weight"]), self.w[p + "down_proj.weight"])
 
     # -- forward (qwen3.py:438-625) ----------------------------------------------------------
-    def forward(self, input_ids, attention_mask=None, position_ids=None, past_key_values=None, paged=None):
+    def forward(self, input_ids, attention_mask=None, position_ids=None, past_key_values=None, paged=None,
+                last_only: bool = False):
         """Returns (logits ``[B, L, V]``, presents).  ``paged``: dict(slot_mapping, block_tables,
         context_lens, kv_pools) for the decode path; otherwise ``past_key_values`` (per layer dense
-        ``[B, Hkv, past, D]``, or None) with ``attention_mask`` over ``past + L``."""
+        ``[B, Hkv, past, D]``, or None) with ``attention_mask`` over ``past + L``.  ``last_only``:
+        logits of the last position only (``[B, 1, V]``): the reference projects every position and
+        samples the last (sampler.py:9-23); projecting that row alone is the same product, and the
+        GEMM the HIP model issues."""
         c = self.config
         scaling = c.head_dim ** -0.5
         batch, length = input_ids.shape
@@ -102,9 +113,11 @@ class ReferenceQwen3:
                     k = torch.cat((past_key_values[layer][0], k), dim=2)
                     v = torch.cat((past_key_values[layer][1], v), dim=2)
                 presents.append((k, v))
-            attn = torch_ref.attend(q, k, v, bias, scaling)
+            attn = (torch_ref.attend_exact if self.exact else torch_ref.attend)(q, k, v, bias, scaling)
             h = h + F.linear(attn, self.w[p + "self_attn.o_proj.weight"])
             h = h + self._mlp(layer, self._rms(h, self.w[p + "post_attention_layernorm.weight"]))
+        if last_only:
+            h = h[:, -1:]
         h = self._rms(h, self.w["model.norm.weight"])
         return F.linear(h, self.w["lm_head.weight"]), presents
 
@@ -129,9 +142,10 @@ def prefill(model: ReferenceQwen3, prompts, pad_token_id: int = 0):
 
 
 def prefill_chunk_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, block_tables, pools, block_size,
-                         pad_token_id: int = 0):
+                         pad_token_id: int = 0, last_only: bool = False):
     """``run_prefill_chunk_step`` (paged_runner.py:32-102): gather history, mask, dense forward.
-    Returns (last-position logits ``[B, V]``, per-layer K/V of history + chunk)."""
+    Returns (last-position logits ``[B, V]``, per-layer K/V of history + chunk).  ``last_only``:
+    project only the last position (see ``ReferenceQwen3.forward``)."""
     lens = [len(c) for c in chunk_token_ids]
     width = max(lens)
     hist = [-(-s // block_size) for s in start_positions]
@@ -148,7 +162,8 @@ def prefill_chunk_logits(model: ReferenceQwen3, chunk_token_ids, start_positions
         hpos = torch.arange(max_hist * block_size, device=model.device).unsqueeze(0)
         mask = torch.cat((hpos < starts, mask), dim=1)
         past = torch_ref.gather_blocks(pools, packed[:, 2 * width + 2:])
-    logits, presents = model.forward(input_ids, attention_mask=mask, position_ids=position_ids, past_key_values=past)
+    logits, presents = model.forward(input_ids, attention_mask=mask, position_ids=position_ids, past_key_values=past,
+                                     last_only=last_only)
     return logits[:, -1], presents
 
 
@@ -178,19 +193,86 @@ def decode_step(model: ReferenceQwen3, block_tables, last_tokens, positions, poo
     return logits[:, -1]
 
 
+def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, chunk_tables, last_tokens, positions,
+                      decode_tables, pools, block_size, pad_token_id: int = 0):
+    """A mixed step -- prompt chunks and decode tokens in one forward, the batching the reference
+    plans next (src/mini_infra/core/scheduler.py:310-311) and does not define -- as the reference's
+    ops over one flattened ``[1, P L + D]`` batch: P chunks left-padded to the longest (L) as
+    ``run_prefill_chunk_step`` packs them, then one token per decoding sequence as
+    ``prepare_decode_inputs`` packs them.  Token-wise ops (embedding, norms, projections, MLP,
+    lm_head) run once over all tokens; attention runs per segment: the chunks' as a chunk step's
+    (history gathered from the pool, causal inside the chunk), the decode tokens' as a paged decode
+    step's (append, then attend over the context), neither reading the other's blocks.  Returns
+    (logits ``[P + D, V]`` of each chunk's last position then each decode token, the chunks'
+    per-layer ``(K, V)`` ``[P, Hkv, L, D]``)."""
+    c = model.config
+    dev = model.device
+    scaling = c.head_dim ** -0.5
+    rows, decode_rows = len(chunk_token_ids), len(last_tokens)
+    lens = [len(t) for t in chunk_token_ids]
+    width = max(lens)
+    n = rows * width
+    ids = torch.full((rows, width), pad_token_id, dtype=torch.long)
+    pos = torch.zeros((rows, width), dtype=torch.long)
+    for r, (toks, start) in enumerate(zip(chunk_token_ids, start_positions)):
+        ids[r, width - len(toks):] = torch.tensor(list(toks), dtype=torch.long)
+        pos[r, width - len(toks):] = torch.arange(start, start + len(toks))
+    hist = [-(-s // block_size) for s in start_positions]
+    max_hist = max(hist)
+    hist_ids = torch.zeros((rows, max_hist), dtype=torch.long)
+    for r, (t, hb) in enumerate(zip(chunk_tables, hist)):
+        hist_ids[r, :hb] = torch.tensor(list(t[:hb]), dtype=torch.long)
+    dec = torch_ref.prepare_decode_rows(decode_tables, last_tokens, positions, block_size).to(dev)
+    flat_ids = torch.cat((ids.flatten().to(dev), dec[:, 0])).unsqueeze(0)
+    flat_pos = torch.cat((pos.flatten().to(dev), dec[:, 1])).unsqueeze(0)
+    # visibility of the chunk rows (history slots < start, causal inside the chunk, no left padding)
+    allowed = torch_ref.chunk_allowed_mask(start_positions, lens, max_hist, block_size, width).to(dev)
+    chunk_bias = torch.zeros(allowed.shape, dtype=model.dtype, device=dev)
+    chunk_bias.masked_fill_(~allowed, torch.finfo(model.dtype).min)
+    dec_bias = torch_ref.paged_bias(dec[:, 4:], dec[:, 3], block_size, model.dtype)
+    attend = torch_ref.attend_exact if model.exact else torch_ref.attend
+    h = F.embedding(flat_ids, model.w["model.embed_tokens.weight"])
+    cos, sin = model._rope(flat_pos)
+    presents = []
+    for layer in range(c.num_hidden_layers):
+        p = f"model.layers.{layer}."
+        x = model._rms(h, model.w[p + "input_layernorm.weight"])
+        q, k, v = model._qkv(layer, x, cos, sin)  # [1, H, T, D]
+        qc = q[0, :, :n].reshape(-1, rows, width, c.head_dim).transpose(0, 1)
+        kc = k[0, :, :n].reshape(-1, rows, width, c.head_dim).transpose(0, 1)
+        vc = v[0, :, :n].reshape(-1, rows, width, c.head_dim).transpose(0, 1)
+        presents.append((kc, vc))
+        if max_hist:
+            (hk, hv), = torch_ref.gather_blocks([pools[layer]], hist_ids.to(dev))
+            kc, vc = torch.cat((hk, kc), dim=2), torch.cat((hv, vc), dim=2)
+        chunk_out = attend(qc.contiguous(), kc, vc, chunk_bias, scaling)  # [P, L, H D]
+        qd = q[0, :, n:].transpose(0, 1).unsqueeze(2)  # [D, H, 1, Dh]
+        kd = k[0, :, n:].transpose(0, 1).unsqueeze(2)
+        vd = v[0, :, n:].transpose(0, 1).unsqueeze(2)
+        hk, hv = torch_ref.apply_paged_kv_pool(kd, vd, pools[layer], dec[:, 2], dec[:, 4:])
+        dec_out = attend(qd.contiguous(), hk, hv, dec_bias, scaling)  # [D, 1, H D]
+        attn = torch.cat((chunk_out.reshape(n, -1), dec_out.reshape(decode_rows, -1))).unsqueeze(0)
+        h = h + F.linear(attn, model.w[p + "self_attn.o_proj.weight"])
+        h = h + model._mlp(layer, model._rms(h, model.w[p + "post_attention_layernorm.weight"]))
+    last = torch.cat((h[0, width - 1:n:width], h[0, n:])).unsqueeze(1)
+    logits = F.linear(model._rms(last, model.w["model.norm.weight"]), model.w["lm_head.weight"])
+    return logits[:, -1], presents
+
+
 class ReferenceScheduleBackend:
     """The reference's PagedScheduleBackend over this restatement
     (src/mini_infra/engine/paged_schedule_backend.py:70-128), for the continuous-batching loop.
 
     Pools live on ``model.device``.  With ``forced_tokens`` (request_idx -> token list) every step
     returns those tokens instead of its own greedy choice -- the run follows another backend's
-    sequences -- and records, per produced token, ``(request_idx, forced, own argmax, logit gap,
-    row std)`` where the gap is ``max logit - logit[forced]`` (0 when they agree) and the row std
-    is the standard deviation of the row's logits (the scale of the gap).
+    sequences; with ``watch_tokens`` it keeps its own greedy choice and only compares.  Either way
+    it records, per produced token, ``(request_idx, index, own argmax, other token, logit gap,
+    row std)`` where the gap is ``max logit - logit[other]`` (0 when they agree, or tie exactly)
+    and the row std is the standard deviation of the row's logits (the scale of the gap).
     """
 
     def __init__(self, model: ReferenceQwen3, requests, max_running_requests: int, block_size: int = 16,
-                 num_blocks: int | None = None, forced_tokens: dict | None = None):
+                 num_blocks: int | None = None, forced_tokens: dict | None = None, watch_tokens: dict | None = None):
         from mini_infra_qwen3_amd.core import KVCacheManager, required_pool_blocks
 
         c = model.config
@@ -201,18 +283,23 @@ class ReferenceScheduleBackend:
         self.pools = torch_ref.make_pools(c.num_hidden_layers, num_blocks, block_size, c.num_key_value_heads,
                                           c.head_dim, dtype=model.dtype, device=model.device)
         self.kv_cache_manager = KVCacheManager(block_size, num_blocks)
+        if forced_tokens is not None and watch_tokens is not None:
+            raise ValueError("forced_tokens and watch_tokens are exclusive")
         self.forced = forced_tokens
-        self.records: list[tuple[int, int, int, float, float]] = []
+        self.watched = forced_tokens if forced_tokens is not None else watch_tokens
+        self.records: list[tuple[int, int, int, int, float, float]] = []
 
     def _choose(self, request_ids, produced_index, logits):
         own = logits.argmax(-1).tolist()
-        if self.forced is None:
+        if self.watched is None:
             return own
         out = []
         for r, k, row, mine in zip(request_ids, produced_index, logits, own):
-            token = self.forced[r][k]
-            self.records.append((r, token, mine, float(row.max() - row[token]), float(row.std())))
-            out.append(token)
+            seq = self.watched.get(r, [])
+            other = seq[k] if k < len(seq) else -1
+            gap = float(row.max() - row[other]) if other >= 0 else float("inf")
+            self.records.append((r, k, mine, other, gap, float(row.std())))
+            out.append(other if self.forced is not None else mine)
         return out
 
     def execute_prefill(self, chunks):
@@ -222,7 +309,7 @@ class ReferenceScheduleBackend:
         starts = [ch.start for ch in chunks]
         lens = [ch.num_tokens for ch in chunks]
         logits, presents = prefill_chunk_logits(self.model, [ch.state.request.token_ids[ch.start:ch.end] for ch in chunks],
-                                                starts, tables, self.pools, self.block_size)
+                                                starts, tables, self.pools, self.block_size, last_only=True)
         store_prefill(self.pools, presents, tables, lens, starts, self.block_size)
         last = [i for i, ch in enumerate(chunks) if ch.is_last]
         tokens = self._choose([chunks[i].state.request.request_idx for i in last], [0] * len(last),
@@ -239,11 +326,24 @@ class ReferenceScheduleBackend:
         return ScheduleStepOutput(tokens, 0.0, 0.0, len(states), 0)
 
     def execute_mixed(self, states, chunks):
-        """A mixed step is, by definition, the decode step of ``states`` and the chunk step of
-        ``chunks``: disjoint requests with disjoint blocks, so neither reads what the other writes.
-        Runs both; tokens of the decode rows first, as the mixed step returns them."""
+        """A mixed step (``mixed_step_logits``): the decode rows of ``states`` and the prompt chunks of
+        ``chunks`` in one forward; tokens of the decode rows first, then those of the chunks that
+        complete their prompt."""
         from mini_infra_qwen3_amd.engine import ScheduleStepOutput
 
-        decode = self.execute_decode(states)
-        prefill = self.execute_prefill(chunks)
-        return ScheduleStepOutput(decode.next_tokens + prefill.next_tokens, 0.0, 0.0, len(states) + len(chunks), 0)
+        manager = self.kv_cache_manager
+        tables = [manager.block_table(ch.state.request.request_idx) for ch in chunks]
+        starts = [ch.start for ch in chunks]
+        lens = [ch.num_tokens for ch in chunks]
+        logits, presents = mixed_step_logits(
+            self.model, [ch.state.request.token_ids[ch.start:ch.end] for ch in chunks], starts, tables,
+            [s.generated[-1] for s in states], [s.cache_length for s in states],
+            [manager.block_table(s.request.request_idx) for s in states], self.pools, self.block_size)
+        store_prefill(self.pools, presents, tables, lens, starts, self.block_size)
+        logits = logits.float()
+        rows = len(chunks)
+        dec = self._choose([s.request.request_idx for s in states], [len(s.generated) for s in states], logits[rows:])
+        last = [i for i, ch in enumerate(chunks) if ch.is_last]
+        pf = self._choose([chunks[i].state.request.request_idx for i in last], [0] * len(last),
+                          logits[last]) if last else []
+        return ScheduleStepOutput(dec + pf, 0.0, 0.0, len(states) + len(chunks), 0)

@@ -109,6 +109,62 @@ def attend(query, key, value, attn_bias, scaling: float) -> torch.Tensor:
     return out.transpose(1, 2).contiguous().view(batch, q_len, -1)
 
 
+# ----------------------------------------------------- attention / RMSNorm, exact sums
+# The reference's rounding points (bf16 scores, fp32 softmax cast to bf16 before P V, bf16
+# output; fp32 RMSNorm) with every sum exact instead of an fp32 sum in ATen's order: the
+# definitions the HIP kernels' "exact" forms compute (csrc/exact_attention.hip,
+# csrc/mi_common.h rms_inv).  Products of bf16 values are exact in fp64; fp64 sums of the terms
+# here are exact or off far below what the final roundings see.  Pinned by tests/test_oracle.py:
+# fp64 closed forms, agreement with ``attend`` (the op-for-op restatement) within one bf16 ulp
+# per rounding point, and independence from the key order.
+
+_SPLIT = 1572864.0  # 1.5 * 2^20: (x + _SPLIT) - _SPLIT rounds |x| <= 1 to a multiple of 2^-32 in fp64
+
+
+def exact_sum(values: torch.Tensor, dim: int = -1, keepdim: bool = False) -> torch.Tensor:
+    """fp64 sum of fp32 values in [0, 1] that does not depend on the order: each value splits into
+    its multiple of 2^-32 (these add exactly for up to 2^20 terms) and a remainder below 2^-33."""
+    x = values.double()
+    hi = (x + _SPLIT) - _SPLIT
+    lo = x - hi
+    return hi.sum(dim, keepdim=keepdim) + lo.sum(dim, keepdim=keepdim)
+
+
+def rms_norm_exact(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm (src/mini_infra/model/qwen3.py:67-78) with an exact sum of squares:
+    var = fp32(sum(x^2) / N), r = fp32(1 / sqrt_f64(fp32(var + eps))), out = w * bf16(x * r)."""
+    xf = x.float()
+    var = (x.double().pow(2).sum(dim=-1, keepdim=True) / x.shape[-1]).float()
+    r = (1.0 / torch.sqrt((var + eps).double())).float()
+    return weight * (xf * r).to(x.dtype)
+
+
+def attend_exact(query, key, value, attn_bias, scaling: float) -> torch.Tensor:
+    """``attend`` (src/mini_infra/model/qwen3.py:219-255) with exact sums.  Per row and visible key t
+    (``attn_bias == 0``; the reference's finfo.min bias gives the others exactly zero weight):
+    s_t = bf16(bf16(fp32(q . k_t)) * scale), m = max s, e_t = fp32(exp_f64(fp32(s_t - m))),
+    l = fp32(exact_sum(e)), p_t = bf16(fp32(e_t / l)), out = bf16(fp32(sum_t p_t v_t)).
+    A row with no visible key (left padding) is zero; the reference's uniform average over masked
+    keys there is never read.  Returns ``[B, q, H * D]``."""
+    batch, heads, q_len, dim = query.shape
+    groups = heads // key.shape[1]
+    k = repeat_kv(key, groups).double()
+    v = repeat_kv(value, groups).double()
+    kv_len = k.shape[2]
+    allowed = (attn_bias == 0).expand(batch, 1, q_len, kv_len)
+    s = torch.matmul(query.double(), k.transpose(2, 3)).float().to(torch.bfloat16).float()
+    s = (s * torch.tensor(scaling, dtype=torch.float32, device=s.device)).to(torch.bfloat16).float()
+    s = s.masked_fill(~allowed, float("-inf"))
+    m = s.amax(dim=-1, keepdim=True)
+    none = torch.isinf(m)
+    e = torch.exp((s - torch.where(none, torch.zeros_like(m), m)).double()).float()
+    l = exact_sum(e, -1, keepdim=True).float()
+    p = (e.double() / torch.where(none, torch.ones_like(l), l).double()).float().to(torch.bfloat16)
+    out = torch.matmul(p.double(), v).float().to(query.dtype)
+    out = out.masked_fill(none, 0)
+    return out.transpose(1, 2).contiguous().view(batch, q_len, heads * dim)
+
+
 def paged_bias(block_tables: torch.Tensor, context_lens: torch.Tensor, block_size: int,
                dtype: torch.dtype) -> torch.Tensor:
     """Additive decode bias ``[B, 1, 1, max_len]``. src/mini_infra/model/qwen3.py:513-528."""
@@ -149,15 +205,17 @@ def paged_decode_step(query, key, value, kv_pool, slot_mapping, block_tables, co
     return attend(query, hist_k, hist_v, bias, scaling)
 
 
-def paged_decode_attention(query, key_pool, value_pool, block_tables, context_lens, scaling: float) -> torch.Tensor:
-    """Kernel-3 oracle (no append): gather + bias + attend.  query ``[B, H, D]`` -> ``[B, H * D]``."""
+def paged_decode_attention(query, key_pool, value_pool, block_tables, context_lens, scaling: float,
+                           exact: bool = False) -> torch.Tensor:
+    """Kernel-3 oracle (no append): gather + bias + attend (``attend_exact`` with ``exact``).
+    query ``[B, H, D]`` -> ``[B, H * D]``."""
     batch = query.shape[0]
     _, bs, heads, dim = key_pool.shape
     shape = (batch, block_tables.shape[1] * bs, heads, dim)
     hist_k = key_pool[block_tables].view(shape).transpose(1, 2)
     hist_v = value_pool[block_tables].view(shape).transpose(1, 2)
     bias = paged_bias(block_tables, context_lens, bs, query.dtype)
-    return attend(query.unsqueeze(2), hist_k, hist_v, bias, scaling).view(batch, -1)
+    return (attend_exact if exact else attend)(query.unsqueeze(2), hist_k, hist_v, bias, scaling).view(batch, -1)
 
 
 def chunk_allowed_mask(start_lens: Sequence[int], chunk_lens: Sequence[int], num_history_blocks: int,
@@ -184,7 +242,8 @@ def chunk_allowed_mask(start_lens: Sequence[int], chunk_lens: Sequence[int], num
 
 
 def chunked_prefill_attention(query, chunk_key, chunk_value, kv_pool, history_block_ids: torch.Tensor,
-                              start_lens: Sequence[int], chunk_lens: Sequence[int], scaling: float) -> torch.Tensor:
+                              start_lens: Sequence[int], chunk_lens: Sequence[int], scaling: float,
+                              exact: bool = False) -> torch.Tensor:
     """One layer of a chunked-prefill step with history -> ``[B, L, H * D]``.
 
     History gather (paged_kv_cache.py:54-72), concat with the chunk (qwen3.py:325-330), visibility
@@ -200,7 +259,7 @@ def chunked_prefill_attention(query, chunk_key, chunk_value, kv_pool, history_bl
         value = torch.cat((hist_v, chunk_value), dim=2)
     else:
         key, value = chunk_key, chunk_value
-    allowed = chunk_allowed_mask(start_lens, chunk_lens, nb, bs, query.shape[2])
-    bias = torch.zeros(allowed.shape, dtype=dtype)
+    allowed = chunk_allowed_mask(start_lens, chunk_lens, nb, bs, query.shape[2]).to(query.device)
+    bias = torch.zeros(allowed.shape, dtype=dtype, device=query.device)
     bias.masked_fill_(~allowed, torch.finfo(dtype).min)
-    return attend(query, key, value, bias, scaling)
+    return (attend_exact if exact else attend)(query, key, value, bias, scaling)

@@ -2,11 +2,13 @@
 model, same bf16 weights, in the scenarios of the reference suite (tests/unit/test_paged_kv_cache.py)
 at the Qwen3 attention shape (16 / 8 heads of 128, block 16).
 
-The oracle runs twice: on the CPU (greedy tokens must agree) and on cuda:0, where its GEMMs are the
-product's own, so that only the fused elementwise launches and attention differ: layer-0 K/V
-(upstream of any attention) must match within one bf16 ulp (the fused RMSNorm sums squares in
-another order); deeper layers carry the attention kernels' rounding differences (max-abs within
-``DEEP_ATOL``: a wrong block, slot or position moves values by O(1))."""
+The model runs reference numerics (its default: the reference's rounding points with exact sums,
+the reference's GEMM calls).  The oracle runs twice:
+* with the same numerics on cuda:0 (``ReferenceQwen3(exact=True)``), where its GEMMs are the
+  product's own: logits, greedy tokens and every stored K/V row must be bit-identical;
+* op for op on the CPU (ATen's fp32 sums): greedy tokens must agree and logits / K/V stay within
+  bf16 rounding (``LOGIT_RTOL``, ``DEEP_ATOL``: a wrong block, slot or position moves values by O(1)).
+Graph tests with padded buckets run the model's bandwidth form (``exact=False``)."""
 
 import pytest
 import torch
@@ -30,14 +32,36 @@ def small_config(layers=2):
 
 @pytest.fixture(scope="module")
 def models():
-    """(product model on cuda:0, oracle on cuda:0, oracle on cpu), identical bf16 weights, untied head."""
+    """(product model on cuda:0, oracle with the same numerics on cuda:0, op-for-op oracle on the
+    CPU), identical bf16 weights, untied head."""
     cfg = small_config()
     model = Qwen3ForCausalLM(cfg)
     init_random_(model, seed=0, std=0.05, untied_head_seed=1234)
     model = model.to(torch.bfloat16)
     weights = {k: v.clone() for k, v in model.state_dict().items()}
-    return (model.to("cuda:0").eval(), qwen3_ref.ReferenceQwen3(cfg, weights, "cuda:0"),
+    return (model.to("cuda:0").eval(), qwen3_ref.ReferenceQwen3(cfg, weights, "cuda:0", exact=True),
             qwen3_ref.ReferenceQwen3(cfg, weights))
+
+
+@pytest.fixture(scope="module")
+def fast_model(models):
+    """The same weights in the bandwidth form (fp32 online-softmax kernels, concatenated GEMMs)."""
+    model = Qwen3ForCausalLM(small_config(), exact=False)
+    init_random_(model, seed=0, std=0.05, untied_head_seed=1234)
+    model = model.to(torch.bfloat16).to("cuda:0").eval()
+    for (name, a), (_, b) in zip(model.state_dict().items(), models[0].state_dict().items()):
+        assert torch.equal(a, b), name
+    return model
+
+
+def assert_bits(got, want):
+    g, w = got.contiguous().view(torch.int16), want.contiguous().view(torch.int16)
+    assert torch.equal(g, w), f"{(g != w).sum().item()} of {g.numel()} values differ"
+
+
+def assert_kv_near(got, want):
+    """Against the op-for-op oracle on the CPU: other GEMMs and fp32 sums, values within rounding."""
+    assert (got.float().cpu() - want.float().cpu()).abs().max().item() <= DEEP_ATOL
 
 
 def assert_kv_close(layer, got, want):
@@ -101,21 +125,25 @@ def test_store_prefill_matches_oracle_and_isolates_requests(models):
     out = runner.run_prefill_step(prompts)
     runner.store_prefill(pool, out.prefill_cache, [manager.block_table(i) for i in range(2)], [37, 20], [0, 0])
     first, presents = qwen3_ref.prefill(ref, prompts)
-    assert out.next_tokens == first == qwen3_ref.prefill(ref_cpu, prompts)[0]
+    cpu_first, cpu_presents = qwen3_ref.prefill(ref_cpu, prompts)
+    assert out.next_tokens == first == cpu_first
     for i, p in enumerate(prompts):
         width = presents[0][0].shape[2]
         for layer in range(model.config.num_hidden_layers):
             k, v = request_kv(pool, layer, manager.block_table(i), len(p))
-            assert_kv_close(layer, k, presents[layer][0][i, :, width - len(p):])
-            assert_kv_close(layer, v, presents[layer][1][i, :, width - len(p):])
+            assert_bits(k, presents[layer][0][i, :, width - len(p):])
+            assert_bits(v, presents[layer][1][i, :, width - len(p):])
+            assert_kv_near(k, cpu_presents[layer][0][i, :, width - len(p):])
+            assert_kv_near(v, cpu_presents[layer][1][i, :, width - len(p):])
     for b in manager.block_table(5):
         assert not pool.kv_pools[0][0][b].any()
 
 
 @pytest.mark.parametrize("bs", [BS, 2 * BS], ids=["block16", "block32"])
 def test_paged_decode_matches_oracle_tokens_and_logits(models, bs):
-    """Mixed-length requests decoded step by step (test_paged_kv_cache.py:109-163): same greedy
-    tokens as the oracle's reference path on both devices, logits close.  A 32-token block pool
+    """Mixed-length requests decoded step by step (test_paged_kv_cache.py:109-163): logits and every
+    K/V row bit-identical to the oracle with the same numerics, greedy tokens identical to it and to
+    the op-for-op oracle on the CPU, logits within rounding of the latter.  A 32-token block pool
     runs the kernels on 16-token sub-blocks."""
     model, ref, ref_cpu = models
     cfg = model.config
@@ -149,31 +177,34 @@ def test_paged_decode_matches_oracle_tokens_and_logits(models, bs):
             got = runner.run_decode_step(ids, pos, meta, pool)  # rewrites the same rows: same inputs
             want = qwen3_ref.decode_step(ref, tables, [t[-1] for t in tokens], lengths, ref_pools, bs).float()
             want_cpu = qwen3_ref.decode_step(ref_cpu, tables, [t[-1] for t in tokens], lengths, cpu_pools, bs)
+            assert torch.equal(logits, want)
             assert got.next_tokens == logits.argmax(-1).tolist() == want.argmax(-1).tolist()
             assert got.next_tokens == want_cpu.argmax(-1).tolist()
-            assert (logits - want).abs().max().item() <= LOGIT_RTOL * want.abs().max().item()
+            assert (logits.cpu() - want_cpu.float()).abs().max().item() <= LOGIT_RTOL * want_cpu.float().abs().max().item()
             for i in range(3):
                 lengths[i] += 1
                 tokens[i].append(got.next_tokens[i])
-    for i in range(3):  # prefill- and decode-written K/V rows agree with the oracle's pools
+    for i in range(3):  # prefill- and decode-written K/V rows: the oracle's, bit for bit
         for layer in range(cfg.num_hidden_layers):
             for kv in range(2):
                 got = request_kv(pool, layer, manager.block_table(i), lengths[i])[kv]
                 want = torch.cat([ref_pools[layer][kv][b] for b in manager.block_table(i)])[:lengths[i]]
-                assert_kv_close(layer, got, want.transpose(0, 1))
+                assert_bits(got, want.transpose(0, 1))
+                want = torch.cat([cpu_pools[layer][kv][b] for b in manager.block_table(i)])[:lengths[i]]
+                assert_kv_near(got, want.transpose(0, 1))
 
 
 @pytest.mark.parametrize("heads,kv_heads", [(16, 4), (20, 4), (32, 4), (8, 8)], ids=["gqa4", "gqa5", "gqa8", "mha"])
 def test_other_gqa_groups_decode_like_the_oracle(heads, kv_heads):
     """Models whose query heads share KV heads in groups other than 2 (Qwen3-4B/8B: 4, Qwen3-14B:
-    5, Qwen3-32B: 8, on the matrix-core decode form; multi-head: 1) run the same kernels: prefill, then decode steps through the fused decode
-    kernel, give the oracle's greedy tokens and logits."""
+    5, Qwen3-32B: 8; multi-head: 1): prefill, then decode steps through the fused decode kernel,
+    give the oracle's logits bit for bit and so its greedy tokens."""
     cfg = Qwen3Config(vocab_size=1000, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
                       num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=128)
     model = Qwen3ForCausalLM(cfg)
     init_random_(model, seed=3, std=0.05, untied_head_seed=99)
     model = model.to(torch.bfloat16)
-    ref = qwen3_ref.ReferenceQwen3(cfg, {k: v.clone() for k, v in model.state_dict().items()}, "cuda:0")
+    ref = qwen3_ref.ReferenceQwen3(cfg, {k: v.clone() for k, v in model.state_dict().items()}, "cuda:0", exact=True)
     model = model.to("cuda:0").eval()
     prompts = prompts_of([45, 17, 3], seed=4)
     manager = KVCacheManager(BS, num_blocks=32)
@@ -200,13 +231,8 @@ def test_other_gqa_groups_decode_like_the_oracle(heads, kv_heads):
                            last_logits_only=True)[0][:, -1].float()
             got = runner.run_decode_step(ids, pos, meta, pool)
             want = qwen3_ref.decode_step(ref, tables, last, lengths, ref_pools, BS).float()
-            tol = LOGIT_RTOL * want.abs().max().item()
-            assert got.next_tokens == logits.argmax(-1).tolist()
-            assert (logits - want).abs().max().item() <= tol
-            # the oracle's greedy token, or one whose oracle logit ties the maximum within the logit
-            # tolerance (random weights do produce exact bf16 ties: the argmax is then arbitrary)
-            for row, token in enumerate(got.next_tokens):
-                assert token == want[row].argmax().item() or want[row, token] >= want[row].max() - tol
+            assert torch.equal(logits, want)
+            assert got.next_tokens == logits.argmax(-1).tolist() == want.argmax(-1).tolist()
             lengths = [n + 1 for n in lengths]
             last = got.next_tokens
 
@@ -282,7 +308,8 @@ def test_chunk_without_history_is_bitwise_whole_prompt_prefill(models):
 
 
 def test_chunked_prefill_matches_oracle_runner(models):
-    """One chunk step with history through both runners: same first tokens, stored K/V close."""
+    """One chunk step with history through both runners: same first tokens; stored K/V bit-identical
+    to the oracle with the same numerics, close to the op-for-op oracle's."""
     model, ref, ref_cpu = models
     cfg = model.config
     prompts = prompts_of([50, 33], seed=6)
@@ -313,19 +340,23 @@ def test_chunked_prefill_matches_oracle_runner(models):
             for kv in range(2):
                 got = request_kv(pool, layer, tables[r], len(p))[kv]
                 want = torch.cat([ref_pools[layer][kv][b] for b in tables[r]])[:len(p)].transpose(0, 1)
-                assert_kv_close(layer, got, want)
+                assert_bits(got, want)
+                want = torch.cat([cpu_pools[layer][kv][b] for b in tables[r]])[:len(p)].transpose(0, 1)
+                assert_kv_near(got, want)
 
 
 def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
     """One forward over two prompt chunks (one with history, one completing its prompt) and three
-    decoding requests equals the chunk step and the decode step run apart: same greedy tokens as
-    those and as the CPU oracle, logits close, every stored K/V row close."""
-    model, _, ref_cpu = models
+    decoding requests: logits and stored K/V bit-identical to the oracle's mixed step (the same
+    flattened batch), greedy tokens equal to the chunk step and the decode step run apart and to the
+    CPU oracle, logits close to the decode step's."""
+    model, ref, ref_cpu = models
     cfg = model.config
     runner = PagedRunner(model)
     decoders = prompts_of([45, 17, 3], seed=8)
     chunked = prompts_of([70, 20], seed=9)
     pools = [make_pool(cfg, 64), make_pool(cfg, 64)]
+    ref_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128, device="cuda:0")
     cpu_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128)
     manager = KVCacheManager(BS, num_blocks=64)
     for i, p in enumerate(decoders + chunked):
@@ -339,10 +370,11 @@ def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
         part = runner.run_prefill_chunk_step([chunked[0][:30]], [0], [tables[3]], pool)
         runner.store_prefill(pool, part.prefill_cache, [tables[3]], [30], [0])
         first = out.next_tokens
-    _, presents = qwen3_ref.prefill(ref_cpu, decoders)
-    qwen3_ref.store_prefill(cpu_pools, presents, tables[:3], [len(p) for p in decoders], [0] * 3, BS)
-    _, presents = qwen3_ref.prefill_chunk_step(ref_cpu, [chunked[0][:30]], [0], [tables[3]], cpu_pools, BS)
-    qwen3_ref.store_prefill(cpu_pools, presents, [tables[3]], [30], [0], BS)
+    for oracle, opools in ((ref, ref_pools), (ref_cpu, cpu_pools)):
+        _, presents = qwen3_ref.prefill(oracle, decoders)
+        qwen3_ref.store_prefill(opools, presents, tables[:3], [len(p) for p in decoders], [0] * 3, BS)
+        _, presents = qwen3_ref.prefill_chunk_step(oracle, [chunked[0][:30]], [0], [tables[3]], opools, BS)
+        qwen3_ref.store_prefill(opools, presents, [tables[3]], [30], [0], BS)
     chunks, starts = [chunked[0][30:], chunked[1]], [30, 0]
     lens = [len(c) for c in chunks]
     positions = [len(p) for p in decoders]
@@ -362,13 +394,18 @@ def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
                                                      pools[1])
         assert ids.shape == (1, 2 * max(lens) + 3)
         # the decode rows' append rewrites the same values when the step runs again
-        mixed_logits = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)[0][:, -1].float()
+        mixed_logits = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)[0][:, -1]
         got = runner.run_mixed_step(ids, pos, meta)
         runner.store_prefill(pools[1], got.prefill_cache, pf_tables, lens, starts)
+    want_mixed, presents = qwen3_ref.mixed_step_logits(ref, chunks, starts, pf_tables, first, positions, dec_tables,
+                                                       ref_pools, BS)
+    qwen3_ref.store_prefill(ref_pools, presents, pf_tables, lens, starts, BS)
+    assert torch.equal(mixed_logits, want_mixed)
     want_dec = qwen3_ref.decode_step(ref_cpu, dec_tables, first, positions, cpu_pools, BS)
     want_pf, _ = qwen3_ref.prefill_chunk_step(ref_cpu, chunks, starts, pf_tables, cpu_pools, BS)
     assert got.decode_next_tokens == dec_logits.argmax(-1).tolist() == want_dec.argmax(-1).tolist()
     assert got.prefill_next_tokens == apart.next_tokens == want_pf
+    mixed_logits = mixed_logits.float()
     assert (mixed_logits[2:] - dec_logits).abs().max().item() <= LOGIT_RTOL * dec_logits.abs().max().item()
     for r in range(5):
         length = positions[r] + 1 if r < 3 else len(chunked[r - 3])
@@ -378,13 +415,15 @@ def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
                 a = request_kv(pools[0], layer, table, length)[kv]
                 b = request_kv(pools[1], layer, table, length)[kv]
                 assert_kv_close(layer, b, a)
+                want = torch.cat([ref_pools[layer][kv][x] for x in table])[:length].transpose(0, 1)
+                assert_bits(b, want)
 
 
-def test_decode_graph_replays_match_eager_forward_and_touch_only_live_slots(models):
-    """Decode graphs: each replay equals an eager forward of the same padded inputs, bit for bit,
-    with eager work and syncs between replays; pad rows write nothing; batches shrink and grow
-    across buckets and contexts cross block boundaries."""
-    model = models[0]
+def test_decode_graph_replays_match_eager_forward_and_touch_only_live_slots(fast_model):
+    """Decode graphs over padded buckets (the bandwidth form): each replay equals an eager forward of
+    the same padded inputs, bit for bit, with eager work and syncs between replays; pad rows write
+    nothing; batches shrink and grow across buckets and contexts cross block boundaries."""
+    model = fast_model
     cfg = model.config
     prompts = prompts_of([30, 17, 5, 44], seed=7)
     manager = KVCacheManager(BS, num_blocks=40)
@@ -430,12 +469,63 @@ def test_decode_graph_replays_match_eager_forward_and_touch_only_live_slots(mode
     assert replays == len(schedule)
 
 
-def test_prefill_graph_replays_match_eager_forward(models):
+def test_exact_decode_graphs_per_batch_match_eager_and_oracle(models):
+    """Reference numerics: one decode graph per batch size (no padded rows) and one table width;
+    each replay bit-identical to the eager forward and to the oracle with the same numerics."""
+    model, ref, _ = models
+    cfg = model.config
+    prompts = prompts_of([30, 17, 5, 44], seed=7)
+    manager = KVCacheManager(BS, num_blocks=40)
+    pool = make_pool(cfg, 40)
+    ref_pools = torch_ref.make_pools(cfg.num_hidden_layers, 40, BS, 8, 128, device="cuda:0")
+    runner = PagedRunner(model)
+    runner.enable_decode_graphs(pool, max_batch=4, max_blocks=8)
+    assert sorted(runner._graphs) == [(b, 8) for b in (1, 2, 3, 4)]
+    for i, p in enumerate(prompts):
+        manager.allocate_slots(i, len(p))
+    tables = [manager.block_table(i) for i in range(4)]
+    out = runner.run_prefill_step(prompts)
+    runner.store_prefill(pool, out.prefill_cache, tables, [len(p) for p in prompts], [0] * 4)
+    first, presents = qwen3_ref.prefill(ref, prompts)
+    qwen3_ref.store_prefill(ref_pools, presents, tables, [len(p) for p in prompts], [0] * 4, BS)
+    assert out.next_tokens == first
+    tokens = {i: [t] for i, t in enumerate(out.next_tokens)}
+    lengths = {i: len(p) for i, p in enumerate(prompts)}
+    with torch.inference_mode():
+        for active in [[0, 1, 2, 3], [0, 1, 2], [0, 2], [2], [1, 3], [3, 1, 0]]:
+            for i in active:
+                assert manager.allocate_slots(i, 1)
+            tables = [manager.block_table(i) for i in active]
+            last, lens = [tokens[i][-1] for i in active], [lengths[i] for i in active]
+            ids, pos, meta = runner.prepare_decode_inputs(tables, last, lens, BS)
+            graph = runner._loaded[0]
+            assert graph.batch == len(active)
+            got = runner.run_decode_step(ids, pos, meta, pool)
+            want = qwen3_ref.decode_step(ref, tables, last, lens, ref_pools, BS)
+            assert torch.equal(graph.logits, want)
+            assert got.next_tokens == want.float().argmax(-1).tolist()
+            for i, t in zip(active, got.next_tokens):
+                tokens[i].append(t)
+                lengths[i] += 1
+
+
+def test_exact_models_refuse_padded_prefill_and_mixed_graphs(models):
+    model = models[0]
+    runner = PagedRunner(model)
+    pool = make_pool(model.config, 8)
+    with pytest.raises(ValueError, match="pad the chunk width"):
+        runner.enable_prefill_graphs(pool, max_rows=1, max_width=128, max_history_blocks=4)
+    with pytest.raises(ValueError, match="pad the chunk width"):
+        runner.enable_mixed_graphs(pool, max_rows=1, max_width=128, max_decode_rows=2, max_history_blocks=4,
+                                   max_decode_blocks=4)
+
+
+def test_prefill_graph_replays_match_eager_forward(fast_model, models):
     """Prefill graphs: each replay equals an eager forward of the same padded inputs, bit for bit
     (logits and the chunk K/V), with eager work and syncs between replays, across row counts, widths
     and history buckets; the tokens and stored K/V equal the eager runner's (which pads the chunk to
-    its own width, so values agree to rounding) and the CPU oracle's tokens."""
-    model, _, ref_cpu = models
+    its own width, so values agree to rounding) and the CPU oracle's tokens.  Bandwidth form."""
+    model, ref_cpu = fast_model, models[2]
     cfg = model.config
     prompts = prompts_of([150, 90, 60, 200, 300], seed=12)
     manager = KVCacheManager(BS, num_blocks=64)
@@ -484,11 +574,12 @@ def test_prefill_graph_replays_match_eager_forward(models):
                                 request_kv(pools[1], layer, tables[r], len(p))[kv])
 
 
-def test_mixed_graph_replays_match_eager_forward(models):
+def test_mixed_graph_replays_match_eager_forward(fast_model, models):
     """Mixed graphs: each replay equals an eager forward of the same padded inputs, bit for bit
     (logits and chunk K/V), across chunk-row and decode-row buckets (pad decode rows write nothing);
-    tokens equal the eager runner's unpadded mixed step and the CPU oracle's, stored K/V agree."""
-    model, _, ref_cpu = models
+    tokens equal the eager runner's unpadded mixed step and the CPU oracle's, stored K/V agree.
+    Bandwidth form."""
+    model, ref_cpu = fast_model, models[2]
     cfg = model.config
     decoders = prompts_of([45, 17, 3], seed=8)
     chunked = prompts_of([70, 20, 50], seed=9)
