@@ -86,21 +86,24 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #ifndef MI_DECODE_MFMA_GROUP
-#define MI_DECODE_MFMA_GROUP 1
+#define MI_DECODE_MFMA_GROUP 4
 #endif
 // GQA groups from this size up use the matrix-core form of the stream kernel (at most 16 heads,
-// the MFMA's column count); smaller groups would use the dot-product form.  Measured at batch 256
+// the MFMA's column count); smaller groups (Qwen3-0.6B / 1.7B's 2, multi-head 1) use the
+// dot-product form, whose v_dot2 + DPP row reduction needs no zero-padded columns.  Measured at batch 256
 // (8 KV heads, Σctx 755,887, attention + merge), TB/s for groups 1 / 2 / 4 / 5 / 8:
 // dot-product form 6.75 / 6.67 / 6.40 / 6.27 / 4.67 (its per-token arithmetic grows with the
 // group); matrix-core form 6.75 / 6.71 / 6.56 / 6.51 / 6.35.  At group 2, interleaved in one
 // process (8 x 20 launches each), the matrix-core form took 461.5 µs (median) against 463.3.
 constexpr int kMfmaGroup = MI_DECODE_MFMA_GROUP;
 #ifndef MI_DECODE_SEQ_MFMA_GROUP
-#define MI_DECODE_SEQ_MFMA_GROUP 1
+#define MI_DECODE_SEQ_MFMA_GROUP 4
 #endif
 // The per-sequence kernel (small launches: latency-bound) takes the matrix-core form from this
-// group size up.  At group 2 it is the faster form at every batch it serves: 6.4 against 7.8 µs per
-// layer at batch 1, 9.5 against 11.6 at 6, 22.0 against 22.8 at 32 (contexts U[32, 1150]).
+// group size up.  At group 2 the matrix-core form measured faster (6.4 against 7.8 µs per layer at
+// batch 1, 9.5 against 11.6 at 6, 22.0 against 22.8 at 32; contexts U[32, 1150]), but models that
+// need those latencies run the reference-numerics kernel (exact_attention.hip), so group 2 keeps
+// the dot-product form here too.
 constexpr int kSeqMfmaGroup = MI_DECODE_SEQ_MFMA_GROUP;
 
 struct DecodeArgs {

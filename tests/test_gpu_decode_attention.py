@@ -176,27 +176,30 @@ def test_zero_context_writes_zero_row(native_lib, device):
     assert not out[0].any() and out[1].ne(7.0).any()
 
 
-def test_decode_at_scale_sampled_sequences(native_lib, device):
-    """Batch 256, lognormal contexts up to 8192, about 3.2 GB of K/V per layer (one layer here).
-    Every sequence is independent, so a sample of rows is checked against the oracle on the
-    blocks it owns, and the rest through size-independent properties (finite, row norms)."""
+def test_decode_at_scale_every_row(native_lib, device):
+    """Config 3 at full size (one layer): batch 256, lognormal contexts up to 8192, about 3.2 GB of
+    K/V.  Every one of the 256 rows is checked against the oracle run on cuda:0 over the blocks its
+    sequence owns (a per-sequence gather: the reference's padded gather of all 256 rows would be
+    ~17 GB per layer): the bandwidth kernel (block ranges, most sequences cut between ranges and
+    merged) within 2e-2, the reference-numerics kernel bit for bit."""
     w = workloads.decode_at_scale(seed=0, device=device, num_layers=1)
     q, kp, vp = w.query[0], w.pools[0, 0], w.pools[0, 1]
     bt = w.block_tables.to(device)
     ctx = torch.tensor(w.context_lens, device=device)
     got = data_plane.paged_decode_attention(q, kp, vp, bt, ctx, SCALE)
-    assert torch.isfinite(got.float()).all()
-    order = sorted(range(256), key=lambda b: w.context_lens[b])
-    for b in [order[0], order[1], order[128], order[-2], order[-1]]:
+    exact = data_plane.paged_decode_attention(q, kp, vp, bt, ctx, SCALE, exact=True)
+    worst = 0.0
+    for b in range(256):
         blocks = torch.tensor(w.tables[b], device=device)
-        local_k, local_v = kp[blocks].cpu(), vp[blocks].cpu()
-        local_t = torch.arange(len(w.tables[b])).view(1, -1)
-        ref = torch_ref.paged_decode_attention(q[b:b + 1].cpu(), local_k, local_v, local_t,
-                                               torch.tensor([w.context_lens[b]]), SCALE)
-        assert max_abs(got[b:b + 1], ref) <= TOL, f"sequence {b} (context {w.context_lens[b]})"
-    # softmax weights are convex: every output element lies inside the range of V for its head
-    vmax = vp.float().abs().max().item()
-    assert got.float().abs().max().item() <= vmax + 1e-3
+        local_t = torch.arange(len(w.tables[b]), device=device).view(1, -1)
+        n = torch.tensor([w.context_lens[b]], device=device)
+        ref = torch_ref.paged_decode_attention(q[b:b + 1], kp[blocks], vp[blocks], local_t, n, SCALE)
+        err = max_abs(got[b:b + 1], ref)
+        worst = max(worst, err)
+        assert err <= TOL, f"sequence {b} (context {w.context_lens[b]}): {err}"
+        want = torch_ref.paged_decode_attention(q[b:b + 1], kp[blocks], vp[blocks], local_t, n, SCALE, exact=True)
+        assert torch.equal(exact[b:b + 1], want), f"sequence {b}: exact kernel differs from the oracle"
+    print(f"\nconfig 3, 256 rows: bandwidth kernel max-abs {worst:.3e} vs the oracle; exact kernel bit-identical")
     assert math.isclose(sum(w.context_lens) * 4096, w.kv_bytes_per_layer)
 
 
