@@ -446,6 +446,8 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
         "decode_steps": len(decode),
         "prefill_steps": len(prefill),
         "decode_step_ms_mean": round(sum(e.step_ms for e in decode) / max(len(decode), 1), 3),
+        "decode_cache_ms_mean": round(sum(e.cache_ms for e in decode) / max(len(decode), 1), 4),
+        "prefill_cache_ms_mean": round(sum(e.cache_ms for e in prefill) / max(len(prefill), 1), 4),
         "decode_batch_mean": round(sum(len(e.request_ids) for e in decode) / max(len(decode), 1), 2),
         "prefill_step_ms_mean": round(sum(e.step_ms for e in prefill) / max(len(prefill), 1), 3),
         "mixed_steps": len(mixed_steps),

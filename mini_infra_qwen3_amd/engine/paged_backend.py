@@ -5,8 +5,13 @@ Same contract and timing as the reference's PagedScheduleBackend
 
 * ``model_ms``: the runner's device-timed forward + greedy sample (StepTimer);
 * ``cache_ms``: host-timed, between device syncs: ``store_prefill`` after a prefill step, and
-  ``prepare_decode_inputs`` (pack + upload) before a decode step; a mixed step (decode rows and
-  prefill chunks in one forward, not in the reference) counts both its packing and its store.
+  the decode packing before a decode step; a mixed step (decode rows and prefill chunks in one
+  forward, not in the reference) counts both its packing and its store.
+
+The block tables live on the GPU for the whole run (``DeviceBlockTables``, a copy of the
+allocator's table matrix kept current by deltas), so a decode step uploads ``[B, 5]`` scalars and
+the entries written since the previous step instead of re-packing ``[B, 4 + max_blocks]``
+(the reference: src/mini_infra/worker/paged_runner.py:138-166).
 """
 
 from __future__ import annotations
@@ -22,6 +27,7 @@ from mini_infra_qwen3_amd.core.scheduler import PrefillChunk, RequestState
 from mini_infra_qwen3_amd.core.types import Request
 from mini_infra_qwen3_amd.device import synchronize
 from mini_infra_qwen3_amd.worker import PagedKVCachePool, PagedRunner
+from mini_infra_qwen3_amd.worker.block_tables import DeviceBlockTables
 
 
 @dataclass(frozen=True)
@@ -65,9 +71,11 @@ class PagedScheduleBackend:
                                      config.num_key_value_heads, config.head_dim,
                                      next(model.parameters()).dtype, self.device)
         self.kv_cache_manager = KVCacheManager(self.block_size, num_blocks)
+        self.tables = DeviceBlockTables(self.kv_cache_manager, min(max_running_requests, len(requests)), largest,
+                                        self.device)
         if decode_graphs:
             self.runner.enable_decode_graphs(self.pool, max_batch=min(max_running_requests, len(requests)),
-                                             max_blocks=largest)
+                                             max_blocks=largest, tables=self.tables)
         longest = max(r.prompt_len for r in requests)
         if mixed_graphs:
             self.runner.enable_mixed_graphs(
@@ -98,10 +106,9 @@ class PagedScheduleBackend:
     def execute_decode(self, states: Sequence[RequestState]) -> ScheduleStepOutput:
         synchronize(self.device)
         t0 = time.perf_counter()
-        ids, pos, meta = self.runner.prepare_decode_inputs(
-            [self.kv_cache_manager.block_table(s.request.request_idx) for s in states],
-            last_tokens=[s.generated[-1] for s in states], positions=[s.cache_length for s in states],
-            block_size=self.block_size)
+        ids, pos, meta = self.runner.prepare_decode_from_tables(
+            self.tables, [s.request.request_idx for s in states], last_tokens=[s.generated[-1] for s in states],
+            positions=[s.cache_length for s in states])
         synchronize(self.device)
         cache_ms = (time.perf_counter() - t0) * 1000.0
         out = self.runner.run_decode_step(ids, pos, meta, self.pool)

@@ -52,12 +52,16 @@ class PagedAttentionMetadata(NamedTuple):
 
     slot_mapping ``[B]``, block_tables ``[B, max_blocks]`` (null-padded), context_lens ``[B]`` (new
     token included) -- int64, possibly column views of one packed tensor; kv_pools per layer.
+    ``table_rows`` (not in the reference): when given, ``block_tables`` is a persistent
+    ``[rows, width]`` table matrix on the device and row b of the step uses its row
+    ``table_rows[b]`` (the forward gathers them once).
     """
 
     slot_mapping: torch.Tensor
     block_tables: torch.Tensor
     context_lens: torch.Tensor
     kv_pools: tuple[PastKeyValue, ...] = ()
+    table_rows: torch.Tensor | None = None
 
 
 class PagedPrefillMetadata(NamedTuple):
@@ -310,6 +314,9 @@ class Qwen3Model(nn.Module):
             if len(attn_metadata.kv_pools) != len(self.layers):
                 raise ValueError("kv_pools has a different number of layers than the model")
             metadata = attn_metadata
+            if metadata.table_rows is not None:  # this step's rows of the persistent table matrix
+                metadata = metadata._replace(block_tables=metadata.block_tables.index_select(0, metadata.table_rows),
+                                             table_rows=None)
             pools = attn_metadata.kv_pools
             need = data_plane.paged_decode_workspace_bytes(batch, metadata.block_tables.shape[1],
                                                           self.config.num_attention_heads, self.config.head_dim,

@@ -34,6 +34,7 @@ from mini_infra_qwen3_amd.data_plane import argmax_rows
 from mini_infra_qwen3_amd.device import StepTimer
 from mini_infra_qwen3_amd.model.qwen3 import PagedAttentionMetadata, PagedMixedMetadata, PagedPrefillMetadata
 from mini_infra_qwen3_amd.worker.base_runner import BaseModelRunner, PrefillOutput
+from mini_infra_qwen3_amd.worker.block_tables import DeviceBlockTables
 from mini_infra_qwen3_amd.worker.kv_cache import KVCache
 from mini_infra_qwen3_amd.worker.metadata import (pack_decode_rows, pack_mixed_rows, pack_prefill_rows,
                                                   prefill_scatter_indices)
@@ -45,13 +46,19 @@ _NULL_BLOCK_ID = 0
 
 class _DecodeGraph:
     """The decode forward of one padded bucket, captured over a static packed-metadata buffer
-    ``[batch, 4 + blocks]`` (token, position, slot, context length, block table)."""
+    ``[batch, 4 + blocks]`` (token, position, slot, context length, block table) -- or, over a
+    persistent ``DeviceBlockTables``, ``[batch, 5]`` (token, position, slot, context length, table
+    row), the block tables being gathered from the device copy inside the graph."""
 
     def __init__(self, model: torch.nn.Module, pool: PagedKVCachePool, batch: int, blocks: int,
-                 device: torch.device):
+                 device: torch.device, tables: DeviceBlockTables | None = None):
         self.batch, self.blocks = batch, blocks
-        self.static = torch.zeros((batch, 4 + blocks), dtype=torch.long, device=device)
+        self.tables = tables
+        self.static = torch.zeros((batch, 5 if tables is not None else 4 + blocks), dtype=torch.long, device=device)
         self.static[:, 2] = -1  # every row is padding until a step is loaded
+        self._staging = torch.empty(tuple(self.static.shape), dtype=torch.long, pin_memory=True)
+        self._copied = torch.cuda.Event()  # the last copy out of the staging buffer
+        self._views: dict[int, tuple] = {}
         ids, pos, meta = self.views(batch)
         meta = meta._replace(kv_pools=tuple(pool.kv_pools))
         side = torch.cuda.Stream(device)  # default priority
@@ -66,13 +73,28 @@ class _DecodeGraph:
         self.logits = logits[:, -1]
 
     def views(self, rows: int):
+        """(input_ids, position_ids, metadata) of the first ``rows`` rows (built once per row count)."""
+        cached = self._views.get(rows)
+        if cached is None:
+            cached = self._views[rows] = self._make_views(rows)
+        return cached
+
+    def _make_views(self, rows: int):
         s = self.static[:rows]
+        if self.tables is not None:
+            return s[:, 0:1], s[:, 1:2], PagedAttentionMetadata(slot_mapping=s[:, 2], block_tables=self.tables.tensor,
+                                                                context_lens=s[:, 3], table_rows=s[:, 4])
         return s[:, 0:1], s[:, 1:2], PagedAttentionMetadata(slot_mapping=s[:, 2], block_tables=s[:, 4:],
                                                             context_lens=s[:, 3])
 
     def load(self, packed: np.ndarray) -> None:
-        """Copies a step packed at the bucket's shape (``pack_decode_rows(..., rows, blocks)``)."""
-        self.static.copy_(torch.from_numpy(packed))
+        """Copies a step packed at the bucket's shape (``pack_decode_rows(..., rows, blocks)``, or the
+        ``[batch, 5]`` rows of a table-backed graph) through pinned memory (the copy is ordered before
+        the replay on the same stream; the host waits for the previous copy before reusing the buffer)."""
+        self._copied.synchronize()
+        self._staging.numpy()[...] = packed
+        self.static.copy_(self._staging, non_blocking=True)
+        self._copied.record()
 
 
 class _PrefillGraph:
@@ -199,6 +221,7 @@ class PagedRunner(BaseModelRunner):
         super().__init__(model, pad_token_id)
         self._graphs: dict[tuple[int, int], _DecodeGraph] = {}
         self._graph_pool: PagedKVCachePool | None = None
+        self._graph_tables: DeviceBlockTables | None = None
         self._batch_buckets: list[int] = []
         self._block_buckets: list[int] = []
         self._loaded: tuple[_DecodeGraph, int] | None = None
@@ -224,16 +247,21 @@ class PagedRunner(BaseModelRunner):
         return self._staging
 
     def enable_decode_graphs(self, pool: PagedKVCachePool, max_batch: int, max_blocks: int,
-                             batch_buckets: Sequence[int] | None = None, block_quantum: int = 16) -> None:
+                             batch_buckets: Sequence[int] | None = None, block_quantum: int = 16,
+                             tables: DeviceBlockTables | None = None) -> None:
         """Captures the decode forward for every (batch bucket, block bucket) up to ``max_batch``
         rows and ``max_blocks`` blocks per row, over ``pool``.  Steps outside the buckets, or on
-        another pool, run without a graph."""
+        another pool, run without a graph.  With ``tables``, the graphs read the block tables from
+        that persistent device copy (one table width) and serve ``prepare_decode_from_tables``."""
         if self.device.type != "cuda":
             raise RuntimeError("decode graphs need the GPU")
         exact = getattr(self.model, "exact", False)
-        if exact:  # every batch size its own graph (no padded rows in the GEMMs), one table width
-            batch_buckets = range(1, max_batch + 1)
+        if tables is not None:
+            max_blocks = tables.tensor.shape[1]
+        if exact or tables is not None:  # one table width
             block_quantum = max(int(max_blocks), 1)
+        if exact:  # every batch size its own graph (no padded rows in the GEMMs)
+            batch_buckets = range(1, max_batch + 1)
         elif batch_buckets is None:
             batch_buckets = [b for b in (1, 2, 4, 8, 12, 16, 24, 32, 48, 64, 80, 96, 112, 128, 160, 192, 224, 256)
                              if b < max_batch] + [max_batch]
@@ -241,10 +269,11 @@ class PagedRunner(BaseModelRunner):
         top = -(-max_blocks // block_quantum) * block_quantum
         self._block_buckets = list(range(block_quantum, top + 1, block_quantum))
         self._graph_pool = pool
+        self._graph_tables = tables
         self._graphs = {}
         for b in self._batch_buckets:
             for nb in self._block_buckets:
-                self._graphs[(b, nb)] = _DecodeGraph(self.model, pool, b, nb, self.device)
+                self._graphs[(b, nb)] = _DecodeGraph(self.model, pool, b, nb, self.device, tables)
         torch.cuda.synchronize(self.device)
 
     def enable_prefill_graphs(self, pool: PagedKVCachePool, max_rows: int, max_width: int, max_history_blocks: int,
@@ -393,7 +422,7 @@ class PagedRunner(BaseModelRunner):
         paged_runner.py:138-166).  Returns column views: input_ids / position_ids ``[B, 1]`` and the
         metadata's slot_mapping, block_tables and context_lens."""
         graph = None
-        if self._graphs and block_size == self._graph_pool.block_size:
+        if self._graphs and self._graph_tables is None and block_size == self._graph_pool.block_size:
             graph = self._bucket(len(block_tables), max((len(t) for t in block_tables), default=0))
         self._loaded = None
         if graph is not None:
@@ -406,6 +435,41 @@ class PagedRunner(BaseModelRunner):
         metadata = PagedAttentionMetadata(slot_mapping=packed[:, 2], block_tables=packed[:, 4:],
                                           context_lens=packed[:, 3])
         return packed[:, 0:1], packed[:, 1:2], metadata
+
+    def prepare_decode_from_tables(
+        self,
+        tables: DeviceBlockTables,
+        request_ids: Sequence[int],
+        last_tokens: Sequence[int],
+        positions: Sequence[int],
+    ) -> tuple[torch.Tensor, torch.Tensor, PagedAttentionMetadata]:
+        """``prepare_decode_inputs`` for requests whose block tables live in ``tables`` (and its
+        manager): brings the device copy up to date with the manager's new entries, then uploads
+        ``[B, 5]`` (token, position, slot, context length, table row) -- no table is re-packed.
+        Slots come from the manager's matrix on the host: ``table[pos // bs] * bs + pos % bs``."""
+        manager = tables.manager
+        bs = manager.block_size
+        batch = len(request_ids)
+        rows = np.fromiter((manager.row_of(r) for r in request_ids), dtype=np.int64, count=batch)
+        pos = np.asarray(positions, dtype=np.int64)
+        slots = manager.table_matrix[rows, pos // bs] * bs + pos % bs
+        packed = np.stack((np.asarray(last_tokens, dtype=np.int64), pos, slots, pos + 1, rows), axis=1)
+        tables.sync()
+        self._loaded = None
+        graph = None
+        if self._graphs and tables is self._graph_tables:
+            graph = self._bucket(batch, tables.tensor.shape[1])
+        if graph is not None:
+            full = np.zeros((graph.batch, 5), dtype=np.int64)
+            full[:, 2] = -1  # pad rows: no append, context 0 (zero output)
+            full[:batch] = packed
+            graph.load(full)
+            self._loaded = (graph, batch)
+            return graph.views(batch)
+        dev = torch.from_numpy(packed).to(self.device)
+        metadata = PagedAttentionMetadata(slot_mapping=dev[:, 2], block_tables=tables.tensor, context_lens=dev[:, 3],
+                                          table_rows=dev[:, 4])
+        return dev[:, 0:1], dev[:, 1:2], metadata
 
     def run_decode_step(
         self,

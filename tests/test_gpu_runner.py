@@ -642,3 +642,55 @@ def test_mixed_graph_replays_match_eager_forward(fast_model, models):
             for kv in range(2):
                 assert_kv_close(layer, request_kv(pools[0], layer, tables[r], length)[kv],
                                 request_kv(pools[1], layer, tables[r], length)[kv])
+
+
+def test_decode_from_persistent_device_tables_matches_the_packed_path(models):
+    """prepare_decode_from_tables (block tables kept on the GPU, updated by deltas; [B, 5] per step)
+    gives the logits of prepare_decode_inputs (the reference's [B, 4 + max_blocks] packing), bit for
+    bit, eagerly and through per-batch decode graphs, as requests grow across block boundaries,
+    finish and are replaced."""
+    from mini_infra_qwen3_amd.worker import DeviceBlockTables
+
+    model = models[0]
+    cfg = model.config
+    prompts = prompts_of([30, 17, 5, 44, 23], seed=21)
+    manager = KVCacheManager(BS, num_blocks=64)
+    pool = make_pool(cfg, 64)
+    tables = DeviceBlockTables(manager, max_rows=4, max_blocks=8, device="cuda:0")
+    graphed = PagedRunner(model)
+    graphed.enable_decode_graphs(pool, max_batch=4, max_blocks=8, tables=tables)
+    eager = PagedRunner(model)
+    for i, p in enumerate(prompts[:4]):
+        manager.allocate_slots(i, len(p))
+    out = eager.run_prefill_step(prompts[:4])
+    eager.store_prefill(pool, out.prefill_cache, [manager.block_table(i) for i in range(4)],
+                        [len(p) for p in prompts[:4]], [0] * 4)
+    tokens = {i: [t] for i, t in enumerate(out.next_tokens)}
+    lengths = {i: len(p) for i, p in enumerate(prompts)}
+    schedule = [[0, 1, 2, 3]] * 3 + [[0, 2, 3]] * 2 + [[0, 2, 3, 4]] * 4 + [[4, 2]] * 3
+    with torch.inference_mode():
+        for active in schedule:
+            if 4 in active and 4 not in tokens:  # request 1 finished: request 4 takes its row
+                manager.free(1)
+                manager.allocate_slots(4, len(prompts[4]))
+                first = eager.run_prefill_step([prompts[4]])
+                eager.store_prefill(pool, first.prefill_cache, [manager.block_table(4)], [len(prompts[4])], [0])
+                tokens[4] = list(first.next_tokens)
+            for i in active:
+                assert manager.allocate_slots(i, 1)
+            last, lens = [tokens[i][-1] for i in active], [lengths[i] for i in active]
+            ids, pos, meta = eager.prepare_decode_inputs([manager.block_table(i) for i in active], last, lens, BS)
+            want = model(ids, position_ids=pos, attn_metadata=meta._replace(kv_pools=tuple(pool.kv_pools)),
+                         last_logits_only=True)[0][:, -1]
+            ids, pos, meta = eager.prepare_decode_from_tables(tables, active, last, lens)
+            got = model(ids, position_ids=pos, attn_metadata=meta._replace(kv_pools=tuple(pool.kv_pools)),
+                        last_logits_only=True)[0][:, -1]
+            assert torch.equal(got, want)
+            ids, pos, meta = graphed.prepare_decode_from_tables(tables, active, last, lens)
+            assert graphed._loaded is not None and graphed._loaded[0].batch == len(active)
+            step = graphed.run_decode_step(ids, pos, meta, pool)
+            assert torch.equal(graphed._loaded[0].logits, want)
+            assert step.next_tokens == want.float().argmax(-1).tolist()
+            for i, t in zip(active, step.next_tokens):
+                tokens[i].append(t)
+                lengths[i] += 1
