@@ -21,6 +21,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -51,6 +52,10 @@ def cpu_model() -> str:
 
 
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+CALIB_LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "mini_infra_qwen3_amd", "libmi_calib.so")
+TRAFFIC_SOURCE = ("profiles/hbm_traffic.md: rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE (KiB per dispatch) of "
+                  "this bench's single-kernel legs, scaled by the same counters over a copy of known size "
+                  "(FETCH_SIZE x2.0, WRITE_SIZE x1.0)")
 
 
 def profiled_traffic(kernel: str) -> int | None:
@@ -150,6 +155,7 @@ def bench_decode(steps: int, warmup: int, device: torch.device):
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": profiled_traffic("paged_decode_attention"),
+            "traffic_source": TRAFFIC_SOURCE,
             "algorithmic_bytes_per_launch": attn_bytes_per_launch,
         },
         "workload": w,
@@ -170,8 +176,7 @@ def cpu_baseline_decode(w, device: torch.device, budget_s: float = 20.0) -> dict
     from mini_infra_qwen3_amd import workloads as wl
     from oracle import torch_ref
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
+    torch.set_num_threads(cpu_threads())
     total = sum(w.context_lens)
     picked, acc = [], 0
     for b, n in enumerate(w.context_lens):
@@ -213,15 +218,82 @@ def cpu_baseline_decode(w, device: torch.device, budget_s: float = 20.0) -> dict
     }
 
 
+def cpu_threads() -> int:
+    """Host threads for the CPU baselines: OMP_NUM_THREADS when set (the process's share of the
+    host), else every core."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
+
+
+def cpu_time(fn, budget_s: float, max_runs: int = 6) -> tuple[float, int]:
+    """(median seconds of the timed runs, number of timed runs): 1 warm-up, then repeats within the
+    time budget (at least one)."""
+    fn()
+    times = []
+    t_budget = time.perf_counter() + budget_s
+    while len(times) < max_runs:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_budget:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline_decode_full(w, device: torch.device, slice_size: int = 32) -> dict:
+    """The reference decode chain (oracle) over the whole batch of 256 on the host cores, one layer,
+    as summed slices of ``slice_size`` sequences (each slice gathered from its own compact pool):
+    the host-memory bound of one padded gather of all 256 rows (~17 GB) is avoided, the work is the
+    full layer's."""
+    from mini_infra_qwen3_amd import workloads as wl
+    from oracle import torch_ref
+
+    torch.set_num_threads(cpu_threads())
+    total_s, runs = 0.0, []
+    for lo in range(0, len(w.context_lens), slice_size):
+        picked = list(range(lo, min(lo + slice_size, len(w.context_lens))))
+        blocks = [blk for b in picked for blk in w.tables[b]]
+        index = torch.tensor(blocks, device=device)
+        key_pool = torch.cat([torch.zeros(1, 16, 8, 128, dtype=torch.bfloat16), w.pools[0, 0][index].cpu()])
+        value_pool = torch.cat([torch.zeros(1, 16, 8, 128, dtype=torch.bfloat16), w.pools[0, 1][index].cpu()])
+        tables, k = [], 1
+        for b in picked:
+            tables.append(list(range(k, k + len(w.tables[b]))))
+            k += len(w.tables[b])
+        bt, ctx, q = wl.padded(tables), torch.tensor([w.context_lens[b] for b in picked]), w.query[0][picked].cpu()
+        sec, n = cpu_time(lambda: torch_ref.paged_decode_attention(q, key_pool, value_pool, bt, ctx, wl.SCALE), 6.0, 3)
+        total_s += sec
+        runs.append(n)
+    nbytes = sum(w.context_lens) * wl.KV_BYTES_PER_TOKEN_LAYER
+    return {"value": nbytes / total_s / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"one layer, all 256 sequences as {len(runs)} slices of {slice_size} (sum of per-slice "
+                      f"medians after 1 warm-up, {min(runs)}-{max(runs)} timed runs each), reference torch chain "
+                      f"(gather + bias + repeat_interleave + bf16 matmul + fp32 softmax); {cpu_model()}",
+            "ms_per_layer": total_s * 1000.0, "ms_per_28_layer_step": total_s * 28000.0}
+
+
 # ------------------------------------------------------------------------------- scatter
-def bench_scatter(steps: int, warmup: int, device: torch.device) -> dict:
+def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "token",
+                  ceiling: float | None = None, cpu: bool = False) -> dict:
+    """Config 2: the 28-layer prefill store of 32 prompts U[128, 2048] (40,636 tokens) into churned
+    blocks, one launch.  ``layout`` of the source ``[B, Hkv, L, D]`` per layer: ``token`` -- the
+    memory of the HIP model's prefill K/V (``mi_qk_norm_rope`` writes ``[T, Hkv, D]`` rows, viewed
+    as ``[B, Hkv, L, D]``), so a token's 2 KiB row is contiguous; ``head`` -- the reference's
+    ``KVCache`` layout (contiguous ``[B, Hkv, L, D]``: a row is 8 pieces of 256 B, L x 256 B apart).
+    ``ceiling``: the measured read+write copy rate the achieved rate is also read against.
+    ``cpu``: time the oracle's ``write_prefill`` (the reference's index + index_copy_ chain) on the
+    host cores over 4 of the 28 layers."""
     from mini_infra_qwen3_amd import workloads as wl
     from mini_infra_qwen3_amd.worker import KVCache, PagedKVCachePool
 
     w = wl.prefill_scatter(seed=0, device=device)
+    sources = w.sources
+    if layout == "token":
+        sources = sources.transpose(-3, -2).contiguous().transpose(-3, -2)
     pool = PagedKVCachePool(wl.NUM_LAYERS, w.num_blocks, wl.BLOCK_SIZE, wl.NUM_KV_HEADS, wl.HEAD_DIM,
                             torch.bfloat16, device)
-    cache = KVCache([(w.sources[l, 0], w.sources[l, 1]) for l in range(wl.NUM_LAYERS)])
+    cache = KVCache([(sources[l, 0], sources[l, 1]) for l in range(wl.NUM_LAYERS)])
     index = torch.from_numpy(w.index).to(device)
     timer = EventTimer()
     for _ in range(warmup):
@@ -233,14 +305,38 @@ def bench_scatter(steps: int, warmup: int, device: torch.device) -> dict:
     ms = timer.mean_ms()
     moved = 2 * w.num_tokens * wl.NUM_LAYERS * wl.KV_BYTES_PER_TOKEN_LAYER  # read + write
     gbs = moved / (ms * 1e-3) / 1e9
-    del pool, cache
-    return {"workload": f"prefill scatter, 28 layers, 32 prompts U[128,2048] ({w.num_tokens} tokens), churned tables",
-            "ms_per_launch": ms, "bytes_per_launch": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
-            "traffic": profiled_traffic("reshape_and_cache")}
+    out = {"workload": f"prefill scatter, 28 layers, 32 prompts U[128,2048] ({w.num_tokens} tokens), churned tables, "
+                       f"{'token-major (the model' + chr(39) + 's K/V rows)' if layout == 'token' else 'head-major (the reference KVCache)'} source",
+           "ms_per_launch": ms, "bytes_per_launch": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
+           "frac_of_copy_ceiling": gbs / ceiling if ceiling else None,
+           "traffic": profiled_traffic("reshape_and_cache" if layout == "head" else "reshape_and_cache_token")}
+    if cpu:
+        from oracle import torch_ref
+
+        torch.set_num_threads(cpu_threads())
+        layers = 4
+        cpu_pools = [(torch.zeros(w.num_blocks, 16, 8, 128, dtype=torch.bfloat16),
+                      torch.zeros(w.num_blocks, 16, 8, 128, dtype=torch.bfloat16)) for _ in range(layers)]
+        cpu_cache = [(w.sources[l, 0].cpu(), w.sources[l, 1].cpu()) for l in range(layers)]
+        idx = torch.from_numpy(w.index)
+        sec, n = cpu_time(lambda: torch_ref.write_prefill(cpu_pools, cpu_cache, idx[0], idx[1], idx[2]), 15.0)
+        out["cpu_baseline"] = {
+            "value": 2 * w.num_tokens * layers * wl.KV_BYTES_PER_TOKEN_LAYER / sec / 1e9, "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"4 of the 28 layers, all {w.num_tokens} tokens: the reference's write_prefill (advanced-index "
+                      f"gather + index_copy_ per tensor per layer), median of {n} after 1 warm-up; {cpu_model()}"}
+        del cpu_pools, cpu_cache
+    del pool, cache, sources, w
+    torch.cuda.empty_cache()
+    return out
 
 
 # -------------------------------------------------------------------------------- gather
-def bench_gather(steps: int, warmup: int, device: torch.device) -> dict:
+def bench_gather(steps: int, warmup: int, device: torch.device, ceiling: float | None = None,
+                 cpu: bool = False) -> dict:
+    """Config 4's history gather (the reference's ``gather_blocks``), 28 layers: every chunk c of the 4
+    prompts gathers its 128 c history blocks, one launch per chunk.  ``cpu``: the oracle's
+    ``gather_blocks`` on the host cores for one of the 28 layers."""
     from mini_infra_qwen3_amd import workloads as wl
     from mini_infra_qwen3_amd.worker import PagedKVCachePool
 
@@ -268,17 +364,80 @@ def bench_gather(steps: int, warmup: int, device: torch.device) -> dict:
     ms = timer.mean_ms()
     moved = 2 * w.history_bytes_per_layer() * wl.NUM_LAYERS  # read history + write the gathered copy
     gbs = moved / (ms * 1e-3) / 1e9
+    out = {"workload": "history gather, 28 layers, 4 prompts x 16384 tokens in 2048-token chunks (7 launches)",
+           "ms_per_prompt_set": ms, "bytes": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
+           "frac_of_copy_ceiling": gbs / ceiling if ceiling else None,
+           "traffic_per_prompt_set": profiled_traffic("gather_blocks")}
+    if cpu:
+        from oracle import torch_ref
+
+        torch.set_num_threads(cpu_threads())
+        layer0 = [(pool.kv_pools[0][0].cpu(), pool.kv_pools[0][1].cpu())]
+        tabs = [t.cpu() for t in chunk_tables]
+        sec, n = cpu_time(lambda: [torch_ref.gather_blocks(layer0, t)[0][0].contiguous() for t in tabs], 15.0)
+        out["cpu_baseline"] = {
+            "value": 2 * w.history_bytes_per_layer() / sec / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"one of the 28 layers, all 7 chunk gathers of the 4 prompts: the reference's gather_blocks "
+                      f"(pool[block_ids] per tensor), median of {n} after 1 warm-up; {cpu_model()}"}
+        del layer0
     del pool
-    return {"workload": "history gather, 28 layers, 4 prompts x 16384 tokens in 2048-token chunks (7 launches)",
-            "ms_per_prompt_set": ms, "bytes": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
-            "traffic_per_prompt_set": profiled_traffic("gather_blocks")}
+    torch.cuda.empty_cache()
+    return out
 
 
 # ------------------------------------------------------------------------------ device copy
+def copy_ceiling(device: torch.device, nbytes: int = 2 << 30, reps: int = 5) -> dict:
+    """What plain streaming traffic reaches on this device: the calibration kernels of
+    libmi_calib.so (16-byte non-temporal accesses, contiguous spans per workgroup) over 2 GiB
+    buffers, for read + write (copy), read-only and write-only, best of the library's launch
+    shapes.  The read + write rate is the ceiling scatter, gather and the block records are read
+    against, the read rate the one decode attention (a read stream) is."""
+    lib = ctypes.CDLL(CALIB_LIBRARY)
+    lib.calib_stream.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                 ctypes.c_int32, ctypes.c_void_p]
+    lib.calib_stream.restype = ctypes.c_int32
+    lib.calib_groups.argtypes = [ctypes.c_int64, ctypes.c_int32]
+    lib.calib_groups.restype = ctypes.c_int64
+    lib.calib_variant.argtypes = [ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+                                  ctypes.POINTER(ctypes.c_int64)]
+    variants = lib.calib_num_variants()
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device).random_()
+    dst = torch.empty_like(src)
+    sink = torch.empty(max(lib.calib_groups(nbytes, v) for v in range(variants)), dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    result = {"workload": f"calibration streams over {nbytes >> 30} GiB buffers (libmi_calib.so)"}
+    for shape, name, moved in ((0, "read_write", 2 * nbytes), (1, "read", nbytes), (2, "write", nbytes)):
+        best = (0.0, None)
+        for v in range(variants):
+            def launch():
+                rc = lib.calib_stream(shape, dst.data_ptr(), src.data_ptr(), sink.data_ptr(), nbytes, v, stream)
+                if rc != 0:
+                    raise RuntimeError(f"calib_stream({shape}, variant {v}) failed: {rc}")
+            for _ in range(2):
+                launch()
+            timer = EventTimer()
+            for _ in range(reps):
+                timer.start()
+                launch()
+                timer.stop()
+            gbs = moved / (timer.mean_ms() * 1e-3) / 1e9
+            if gbs > best[0]:
+                t, f, sp = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+                lib.calib_variant(v, ctypes.byref(t), ctypes.byref(f), ctypes.byref(sp))
+                best = (gbs, f"{t.value} lanes, {f.value} pieces in flight, {sp.value >> 10} KiB per workgroup")
+        result[f"{name}_GBps"] = round(best[0], 1)
+        result[f"{name}_frac"] = round(best[0] / HBM_PEAK_GBS, 4)
+        result[f"{name}_shape"] = best[1]
+    del src, dst, sink
+    torch.cuda.empty_cache()
+    return result
+
+
 def bench_copy(steps: int, device: torch.device, nbytes: int = 1 << 30) -> dict:
     """torch's device-to-device copy of a 1 GiB buffer (reads and writes exactly ``nbytes`` per
-    launch): the reference point for read+write kernels, and the calibration workload of the HBM
-    traffic counters."""
+    launch; the calibration workload of the HBM traffic counters), and the calibration kernels'
+    ceilings (``copy_ceiling``)."""
     src = torch.ones(nbytes, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
     dst.copy_(src)
@@ -290,8 +449,9 @@ def bench_copy(steps: int, device: torch.device, nbytes: int = 1 << 30) -> dict:
     ms = timer.mean_ms()
     gbs = 2 * nbytes / (ms * 1e-3) / 1e9
     del src, dst
+    torch.cuda.empty_cache()
     return {"workload": "torch device copy, 1 GiB", "bytes_per_launch": 2 * nbytes, "ms_per_launch": ms,
-            "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS}
+            "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS, "ceiling": copy_ceiling(device)}
 
 
 # ------------------------------------------------------------------------ KV block swap
@@ -350,9 +510,11 @@ def bench_swap(steps: int, warmup: int, device: torch.device, num_records: int =
 
 
 # ------------------------------------------------------------------------- chunked prefill
-def bench_prefill(steps: int, warmup: int, device: torch.device) -> dict:
+def bench_prefill(steps: int, warmup: int, device: torch.device, cpu: bool = False) -> dict:
     """4 prompts x 16384 tokens, 2048-token chunks, one layer: 8 chunk steps, each one launch over the
-    4 prompts (history 2048 c read from the pool through the block table, causal inside the chunk)."""
+    4 prompts (history 2048 c read from the pool through the block table, causal inside the chunk).
+    ``cpu``: the oracle's chunked-prefill chain (gather + concat + mask + bf16 matmul + fp32
+    softmax) on the host cores for one prompt's chunk 1 (2048 history tokens)."""
     from mini_infra_qwen3_amd import data_plane, workloads as wl
 
     w = wl.chunked_prefill(seed=0)
@@ -386,13 +548,65 @@ def bench_prefill(steps: int, warmup: int, device: torch.device) -> dict:
     n = w.prompt_len
     flops = w.num_prompts * 2 * 2 * wl.NUM_HEADS * wl.HEAD_DIM * n * (n + 1) / 2  # QK^T and PV, causal pairs
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"workload": "chunked prefill attention, 4 prompts x 16384 tokens, 2048-token chunks, one layer "
-                        "(8 launches, history from the pool)",
-            "ms_per_layer": ms, "tflop_per_layer": flops / 1e12, "achieved_TFLOPs": tflops,
-            "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "frac": tflops / MFMA_BF16_PEAK_TFLOPS}
+    out = {"workload": "chunked prefill attention, 4 prompts x 16384 tokens, 2048-token chunks, one layer "
+                       "(8 launches, history from the pool)",
+           "ms_per_layer": ms, "tflop_per_layer": flops / 1e12, "achieved_TFLOPs": tflops,
+           "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "frac": tflops / MFMA_BF16_PEAK_TFLOPS}
+    if cpu:
+        from oracle import torch_ref
+
+        torch.set_num_threads(cpu_threads())
+        c = 1
+        hist = tables[:1, :c * L // wl.BLOCK_SIZE].cpu()
+        kp, vp = pools[0].cpu(), pools[1].cpu()
+        q1, k1, v1 = q[:1].cpu(), k[:1].cpu(), v[:1].cpu()
+        sec, n = cpu_time(lambda: torch_ref.chunked_prefill_attention(q1, k1, v1, (kp, vp), hist, [c * L], [L],
+                                                                      wl.SCALE), 20.0, 4)
+        chunk_flops = 2 * 2 * wl.NUM_HEADS * wl.HEAD_DIM * (L * c * L + L * (L + 1) / 2)
+        out["cpu_baseline"] = {
+            "value": chunk_flops / sec / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"one prompt's chunk {c} (2048 queries, 2048 history + causal chunk keys): the reference's "
+                      f"gather + concat + mask + attend, median of {n} after 1 warm-up; {cpu_model()}",
+            "ms_per_chunk": sec * 1000.0}
+        del kp, vp
+    del pools, q, k, v
+    torch.cuda.empty_cache()
+    return out
 
 
 # ------------------------------------------------------------------------ e2e continuous batching
+def cpu_baseline_e2e(seed: int = 0, num_requests: int = 8, max_new_tokens: int = 64) -> dict:
+    """The oracle's restatement of the reference schedule backend (the reference's torch model,
+    runner and paged pool) on the host cores: the first requests of the config-5 workload with
+    fewer output tokens, same loop, token budget and model.  Output tok/s over the loop's wall
+    time (its busy time: no idle gaps, the loop runs back to back)."""
+    from mini_infra_qwen3_amd.engine import run_scheduler
+    from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
+    from mini_infra_qwen3_amd.workloads import serving_requests
+    from oracle import qwen3_ref
+
+    torch.set_num_threads(cpu_threads())
+    cfg = qwen3_0_6b()
+    model = Qwen3ForCausalLM(cfg)
+    init_random_(model, seed=seed, std=0.02)
+    ref = qwen3_ref.ReferenceQwen3(cfg, model.to(torch.bfloat16).state_dict(), "cpu")
+    del model
+    import dataclasses
+
+    requests = [dataclasses.replace(r, max_new_tokens=max_new_tokens) for r in serving_requests(seed=seed)[:num_requests]]
+    t0 = time.perf_counter()
+    res = run_scheduler(qwen3_ref.ReferenceScheduleBackend(ref, requests, num_requests), requests,
+                        token_budget=2048, eos_token_id=-1, stop_on_eos=False)
+    wall = time.perf_counter() - t0
+    return {"value": res.num_output_tokens / wall, "unit": "output tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"first {num_requests} requests of the workload (prompts {[r.prompt_len for r in requests]}), "
+                      f"{max_new_tokens} greedy tokens each, the reference's torch model on the CPU (bf16), wall "
+                      f"time of the loop; {cpu_model()}",
+            "wall_s": wall}
+
+
+
 def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: bool = True) -> dict:
     """Continuous batching with chunked prefill (token budget 2048, block 16, batch slots = number of
     requests) of a random-init Qwen3-0.6B (bf16, N(0, 0.02), tied embeddings): 128 requests, Poisson
@@ -510,8 +724,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "gather", "prefill", "copy", "swap",
-                                           "e2e", "e2e-mixed", "e2e-bandwidth", "all"],
+    parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "scatter-head", "gather", "prefill",
+                                           "copy", "swap", "e2e", "e2e-mixed", "e2e-bandwidth", "all"],
                         default="all")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -530,6 +744,7 @@ def main() -> int:
     single = {
         "copy": lambda: bench_copy(args.steps, device),
         "scatter": lambda: bench_scatter(args.steps, args.warmup, device),
+        "scatter-head": lambda: bench_scatter(args.steps, args.warmup, device, layout="head"),
         "gather": lambda: bench_gather(args.steps, args.warmup, device),
         "prefill": lambda: bench_prefill(args.steps, args.warmup, device),
         "swap": lambda: bench_swap(args.steps, args.warmup, device),
@@ -552,8 +767,8 @@ def main() -> int:
     w = dec.pop("workload")
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_decode(w, device)
-        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+        cpu = cpu_baseline_decode_full(w, device)
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads ({cpu['ms_per_layer']:.0f} ms per layer)")
     ctx_sum = sum(w.context_lens)
     num_blocks = w.num_blocks
     del w
@@ -561,18 +776,24 @@ def main() -> int:
 
     kernels = {}
     if args.only == "all":
-        kernels["scatter"] = bench_scatter(max(args.steps // 2, 3), 2, device)
-        log(f"scatter: {kernels['scatter']['achieved_GBps']:.1f} GB/s")
-        torch.cuda.empty_cache()
-        kernels["gather"] = bench_gather(max(args.steps // 4, 3), 1, device)
-        log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s")
-        torch.cuda.empty_cache()
-        kernels["chunked_prefill"] = bench_prefill(max(args.steps // 4, 3), 3, device)
+        want_cpu = not args.no_cpu_baseline
+        kernels["device_copy"] = bench_copy(5, device)
+        ceil = kernels["device_copy"]["ceiling"]
+        log(f"device copy: {kernels['device_copy']['achieved_GBps']:.1f} GB/s; calibration streams: read+write "
+            f"{ceil['read_write_GBps']:.0f}, read {ceil['read_GBps']:.0f}, write {ceil['write_GBps']:.0f} GB/s")
+        kernels["scatter"] = bench_scatter(max(args.steps // 2, 3), 2, device, "token", ceil["read_write_GBps"],
+                                           cpu=want_cpu)
+        log(f"scatter: {kernels['scatter']['achieved_GBps']:.1f} GB/s "
+            f"({100 * kernels['scatter']['frac_of_copy_ceiling']:.1f}% of the copy ceiling)")
+        kernels["scatter_head_major_source"] = bench_scatter(max(args.steps // 2, 3), 2, device, "head",
+                                                             ceil["read_write_GBps"])
+        log(f"scatter, head-major source: {kernels['scatter_head_major_source']['achieved_GBps']:.1f} GB/s")
+        kernels["gather"] = bench_gather(max(args.steps // 4, 3), 1, device, ceil["read_write_GBps"], cpu=want_cpu)
+        log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s "
+            f"({100 * kernels['gather']['frac_of_copy_ceiling']:.1f}% of the copy ceiling)")
+        kernels["chunked_prefill"] = bench_prefill(max(args.steps // 4, 3), 3, device, cpu=want_cpu)
         log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "
             f"{kernels['chunked_prefill']['achieved_TFLOPs']:.1f} TFLOP/s")
-        torch.cuda.empty_cache()
-        kernels["device_copy"] = bench_copy(5, device)
-        log(f"device copy: {kernels['device_copy']['achieved_GBps']:.1f} GB/s")
         torch.cuda.empty_cache()
         kernels["decode_gqa_groups"] = bench_decode_groups(args.steps, 2, device)
         log("decode by GQA group: " + ", ".join(f"{g}: {r['achieved_GBps']:.0f} GB/s"
@@ -593,6 +814,9 @@ def main() -> int:
             f"{e2e_mixed['latency_ms']['itl_ms_max']:.2f} ms (alternating: {e2e['latency_ms']['itl_ms_max']:.2f} ms)")
         e2e_bw = bench_e2e(device, exact=False)
         log(f"e2e bandwidth kernels: {e2e_bw['output_tok_s']:.1f} output tok/s (busy)")
+        if not args.no_cpu_baseline:
+            e2e["cpu_baseline"] = cpu_baseline_e2e()
+            log(f"e2e cpu baseline: {e2e['cpu_baseline']['value']:.2f} output tok/s")
 
     line = {
         "metric": METRIC,
@@ -618,6 +842,7 @@ def main() -> int:
             "pct_hbm_peak": round(100 * dec["value"] / HBM_PEAK_GBS, 2),
         },
         "roofline": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec["roofline"].items()},
+        "read_ceiling_GBps": kernels.get("device_copy", {}).get("ceiling", {}).get("read_GBps"),
         "cpu_baseline": cpu,
         "kernels": kernels,
         "e2e": e2e,

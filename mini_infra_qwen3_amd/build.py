@@ -1,8 +1,10 @@
-"""Builds libmi_paged.so (the HIP kernels + C ABI) in-tree with hipcc for gfx950.
+"""Builds libmi_paged.so (the HIP kernels + C ABI) in-tree with hipcc for gfx950, and
+libmi_calib.so (HBM streaming-copy calibration kernels that bench.py reads the data-plane rates
+against; not part of the ABI).
 
 Usage: ``python -m mini_infra_qwen3_amd.build`` (also called by ``__graft_entry__.build()``).
-Every source is compiled on each call; objects go to ``_build/`` and the library next to
-this file, where ``mini_infra_qwen3_amd._native`` loads it from.
+Every source is compiled on each call; objects go to ``_build/`` and the libraries next to
+this file, where ``mini_infra_qwen3_amd._native`` (and bench.py) load them from.
 """
 
 from __future__ import annotations
@@ -16,6 +18,8 @@ from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 CSRC_DIR = PACKAGE_DIR / "csrc"
+CALIB_DIR = PACKAGE_DIR / "csrc_calib"
+CALIB_LIBRARY_PATH = PACKAGE_DIR / "libmi_calib.so"
 REPO_DIR = PACKAGE_DIR.parent
 BUILD_DIR = REPO_DIR / "_build" / "mi_paged"
 LIBRARY_PATH = PACKAGE_DIR / "libmi_paged.so"
@@ -44,8 +48,8 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def sources() -> list[Path]:
-    return sorted(CSRC_DIR.glob("*.hip"))
+def sources(directory: Path = CSRC_DIR) -> list[Path]:
+    return sorted(directory.glob("*.hip"))
 
 
 def _compile(src: Path, build_dir: Path, extra: tuple[str, ...]) -> Path:
@@ -57,27 +61,33 @@ def _compile(src: Path, build_dir: Path, extra: tuple[str, ...]) -> Path:
     return obj
 
 
-def build(verbose: bool = True, extra_flags: tuple[str, ...] = (), output: Path | None = None) -> Path:
+def build(verbose: bool = True, extra_flags: tuple[str, ...] = (), output: Path | None = None,
+          calibration: bool = True) -> Path:
     """Compiles every csrc/*.hip for gfx950 and links libmi_paged.so; returns its path.
 
     ``extra_flags`` (e.g. ``-DMI_DECODE_PART_BLOCKS=32`` to override a kernel tunable) and
-    ``output`` build a variant library elsewhere; the defaults build the in-tree library.
+    ``output`` build a variant library elsewhere; the defaults build the in-tree library, and
+    then (``calibration``) libmi_calib.so from csrc_calib/.
     """
+    if output is None and calibration:
+        _link(sources(CALIB_DIR), CALIB_LIBRARY_PATH, BUILD_DIR.with_name("mi_calib"), (), verbose)
     output = LIBRARY_PATH if output is None else Path(output)
     build_dir = BUILD_DIR if output == LIBRARY_PATH else output.parent / "_obj"
+    return _link(sources(), output, build_dir, tuple(extra_flags), verbose)
+
+
+def _link(srcs: list[Path], output: Path, build_dir: Path, extra: tuple[str, ...], verbose: bool) -> Path:
     build_dir.mkdir(parents=True, exist_ok=True)
-    srcs = sources()
     if not srcs:
-        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+        raise RuntimeError(f"no HIP sources for {output.name}")
     workers = min(len(srcs), 8)
-    extra = tuple(extra_flags)
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(lambda src: _compile(src, build_dir, extra), srcs))
     tmp = output.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"link of {LIBRARY_PATH.name} failed:\n{proc.stdout}\n{proc.stderr}")
+        raise RuntimeError(f"link of {output.name} failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, output)
     if verbose:
         print(f"built {output} from {len(srcs)} sources", flush=True)

@@ -1,0 +1,136 @@
+// HBM calibration kernels: what plain streaming traffic reaches on this device, the ceiling the
+// data-plane kernels' rates are read against (bench.py --only copy).  Not part of the paged-KV
+// C ABI: a separate library, libmi_calib.so.
+//
+// Three traffic shapes over contiguous buffers, 16-byte non-temporal accesses, each workgroup
+// streaming one contiguous span of `span` bytes with `kInFlight` pieces per lane in flight:
+//   copy  (read + write), read (loads folded into one word per workgroup), write (stores only).
+// A variant is (lanes per workgroup, pieces in flight, span); bench.py sweeps them and keeps the
+// best of each shape.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Variant {
+  int threads;
+  int in_flight;
+  int64_t span;  // bytes per workgroup
+};
+
+constexpr Variant kVariants[] = {
+    {256, 4, 64 << 10}, {512, 4, 64 << 10}, {512, 8, 128 << 10}, {1024, 4, 128 << 10},
+    {256, 8, 256 << 10}, {512, 8, 256 << 10}, {1024, 8, 512 << 10}, {512, 2, 32 << 10},
+};
+constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
+
+template <int kInFlight>
+__global__ void copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src, int64_t pieces,
+                            int64_t span_pieces) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * span_pieces;
+  const int64_t end = min(base + span_pieces, pieces);
+  const int64_t step = static_cast<int64_t>(blockDim.x) * kInFlight;
+  for (int64_t p0 = base + threadIdx.x; p0 < end; p0 += step) {
+    u32x4 v[kInFlight];
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k) {
+      const int64_t p = p0 + static_cast<int64_t>(k) * blockDim.x;
+      if (p < end) v[k] = __builtin_nontemporal_load(src + p);
+    }
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k) {
+      const int64_t p = p0 + static_cast<int64_t>(k) * blockDim.x;
+      if (p < end) __builtin_nontemporal_store(v[k], dst + p);
+    }
+  }
+}
+
+template <int kInFlight>
+__global__ void read_kernel(const u32x4* __restrict__ src, uint32_t* __restrict__ sink, int64_t pieces,
+                            int64_t span_pieces) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * span_pieces;
+  const int64_t end = min(base + span_pieces, pieces);
+  const int64_t step = static_cast<int64_t>(blockDim.x) * kInFlight;
+  uint32_t acc = 0;
+  for (int64_t p0 = base + threadIdx.x; p0 < end; p0 += step) {
+    u32x4 v[kInFlight];
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k) {
+      const int64_t p = p0 + static_cast<int64_t>(k) * blockDim.x;
+      v[k] = p < end ? __builtin_nontemporal_load(src + p) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k) acc ^= v[k][0] ^ v[k][1] ^ v[k][2] ^ v[k][3];
+  }
+  // One word per workgroup keeps the loads live: lane 0 always stores, and every other lane's store
+  // depends on its own value, so no lane's loads are dead code.
+  if (threadIdx.x == 0 || acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
+template <int kInFlight>
+__global__ void write_kernel(u32x4* __restrict__ dst, int64_t pieces, int64_t span_pieces) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * span_pieces;
+  const int64_t end = min(base + span_pieces, pieces);
+  const int64_t step = static_cast<int64_t>(blockDim.x) * kInFlight;
+  const u32x4 v = {static_cast<uint32_t>(blockIdx.x), 1u, 2u, 3u};
+  for (int64_t p0 = base + threadIdx.x; p0 < end; p0 += step) {
+#pragma unroll
+    for (int k = 0; k < kInFlight; ++k) {
+      const int64_t p = p0 + static_cast<int64_t>(k) * blockDim.x;
+      if (p < end) __builtin_nontemporal_store(v, dst + p);
+    }
+  }
+}
+
+int check_args(int64_t bytes, int32_t variant) {
+  if (bytes <= 0 || bytes % 16 != 0 || variant < 0 || variant >= kNumVariants) return -1;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int32_t calib_num_variants(void) { return kNumVariants; }
+
+extern "C" int32_t calib_variant(int32_t variant, int32_t* threads, int32_t* in_flight, int64_t* span) {
+  if (variant < 0 || variant >= kNumVariants) return -1;
+  *threads = kVariants[variant].threads;
+  *in_flight = kVariants[variant].in_flight;
+  *span = kVariants[variant].span;
+  return 0;
+}
+
+// Workgroups a launch of `bytes` takes (the read kernel's sink needs one word each).
+extern "C" int64_t calib_groups(int64_t bytes, int32_t variant) {
+  if (check_args(bytes, variant)) return -1;
+  return (bytes + kVariants[variant].span - 1) / kVariants[variant].span;
+}
+
+// shape: 0 = copy (dst <- src), 1 = read (src, sink of calib_groups words), 2 = write (dst)
+extern "C" int32_t calib_stream(int32_t shape, void* dst, const void* src, void* sink, int64_t bytes,
+                                int32_t variant, void* stream) {
+  if (check_args(bytes, variant) || shape < 0 || shape > 2) return -1;
+  if ((shape != 1 && !dst) || (shape != 2 && !src) || (shape == 1 && !sink)) return -1;
+  if ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) return -1;
+  const Variant v = kVariants[variant];
+  const int64_t pieces = bytes / 16, span_pieces = v.span / 16;
+  const int64_t groups = (pieces + span_pieces - 1) / span_pieces;
+  if (groups > 0x7fffffff) return -1;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(groups));
+  u32x4* d = static_cast<u32x4*>(dst);
+  const u32x4* r = static_cast<const u32x4*>(src);
+  uint32_t* k = static_cast<uint32_t*>(sink);
+#define CALIB_LAUNCH(N)                                                          \
+  if (shape == 0) copy_kernel<N><<<grid, v.threads, 0, s>>>(d, r, pieces, span_pieces); \
+  else if (shape == 1) read_kernel<N><<<grid, v.threads, 0, s>>>(r, k, pieces, span_pieces); \
+  else write_kernel<N><<<grid, v.threads, 0, s>>>(d, pieces, span_pieces);
+  switch (v.in_flight) {
+    case 2: CALIB_LAUNCH(2) break;
+    case 4: CALIB_LAUNCH(4) break;
+    default: CALIB_LAUNCH(8) break;
+  }
+#undef CALIB_LAUNCH
+  return hipGetLastError() == hipSuccess ? 0 : -4;
+}
