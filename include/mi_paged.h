@@ -280,6 +280,56 @@ int32_t mi_chunked_prefill_attention_exact(void* out, int64_t out_row_stride, in
                                            int32_t head_dim, int32_t block_size, float scale, void* stream);
 
 /*
+ * Kernel 4, mixed form -- the attention of a mixed chunk + decode step in one launch: the varlen
+ * attention the reference plans for mixing prefill chunks and decode tokens in one forward
+ * (src/mini_infra/core/scheduler.py:310-311, src/mini_infra/core/types.py:108), over the same
+ * rows the model's two paths would serve: chunk rows as mi_chunked_prefill_attention and decode
+ * rows as mi_paged_decode_attention plus the K/V append of mi_reshape_and_cache's decode form
+ * (reference qwen3.py:219-330, paged_kv_cache.py:97-114).
+ *
+ * A flattened token batch of T = P L + D rows, token-major ([T, H, 128] query, [T, H_kv, 128]
+ * key / value with token and head strides; out [T, H * 128] with a token stride):
+ *   tokens [0, P L): P chunk rows, each a left-padded chunk of width L (row b at token b L) with
+ *     start_lens / chunk_lens / history_blocks as in mi_chunked_prefill_attention;
+ *   tokens [P L, T): D decode rows, one token each, context_lens[b] tokens including it: the
+ *     first context_lens[b] - 1 are read from the pool through block_tables[b], the last is the
+ *     row's own key / value, which the launch also appends to pool slot slot_mapping[b] (a slot
+ *     outside the pool is skipped; context 0 marks a padding row: zero output, no append).
+ * Chunk rows give the bits of mi_chunked_prefill_attention.  Decode rows are served by the same
+ * chunk kernel (a 1-token chunk), within the same tolerance of the reference chain as kernel 3.
+ * Either part may be empty (P = 0 or L = 0, D = 0).
+ *
+ * mi_mixed_paged_attention_exact -- the same with the reference numerics of
+ * mi_chunked_prefill_attention_exact; decode rows then give the bits of
+ * mi_paged_decode_attention_exact.
+ */
+int32_t mi_mixed_paged_attention(void* out, int64_t out_tok_stride, const void* query, int64_t query_tok_stride,
+                                 int64_t query_head_stride, const void* key, int64_t key_tok_stride,
+                                 int64_t key_head_stride, const void* value, int64_t value_tok_stride,
+                                 int64_t value_head_stride, void* key_pool, void* value_pool, int64_t num_blocks,
+                                 int32_t prefill_rows, int32_t prefill_width, const int64_t* history_blocks,
+                                 int64_t history_stride, int32_t max_history_blocks, const int64_t* start_lens,
+                                 const int64_t* chunk_lens, int64_t lens_stride, int32_t decode_rows,
+                                 const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,
+                                 const int64_t* context_lens, int64_t context_lens_stride,
+                                 const int64_t* slot_mapping, int64_t slot_stride, int32_t num_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                                 void* stream);
+int32_t mi_mixed_paged_attention_exact(void* out, int64_t out_tok_stride, const void* query,
+                                       int64_t query_tok_stride, int64_t query_head_stride, const void* key,
+                                       int64_t key_tok_stride, int64_t key_head_stride, const void* value,
+                                       int64_t value_tok_stride, int64_t value_head_stride, void* key_pool,
+                                       void* value_pool, int64_t num_blocks, int32_t prefill_rows,
+                                       int32_t prefill_width, const int64_t* history_blocks, int64_t history_stride,
+                                       int32_t max_history_blocks, const int64_t* start_lens,
+                                       const int64_t* chunk_lens, int64_t lens_stride, int32_t decode_rows,
+                                       const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,
+                                       const int64_t* context_lens, int64_t context_lens_stride,
+                                       const int64_t* slot_mapping, int64_t slot_stride, int32_t num_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                                       void* stream);
+
+/*
  * Fused layer ops: the elementwise chains around attention in a Qwen3 decoder layer, one
  * launch each, with the reference's bf16 rounding points.  All tensors are bf16, rows of
  * contiguous elements, 16-byte aligned.

@@ -72,6 +72,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _ptr, _i64,
          _ptr, _i64, _i32, _ptr, _ptr, _i64, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _ptr],
     ),
+    "mi_mixed_paged_attention": (
+        _i32,
+        [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i32, _i32, _ptr, _i64,
+         _i32, _ptr, _ptr, _i64, _i32, _ptr, _i64, _i32, _ptr, _i64, _ptr, _i64, _i32, _i32, _i32, _i32,
+         ctypes.c_float, _ptr],
+    ),
+    "mi_mixed_paged_attention_exact": (
+        _i32,
+        [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i32, _i32, _ptr, _i64,
+         _i32, _ptr, _ptr, _i64, _i32, _ptr, _i64, _i32, _ptr, _i64, _ptr, _i64, _i32, _i32, _i32, _i32,
+         ctypes.c_float, _ptr],
+    ),
     "mi_rms_norm": (_i32, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i32, ctypes.c_float, _ptr]),
     "mi_qk_norm_rope": (
         _i32,

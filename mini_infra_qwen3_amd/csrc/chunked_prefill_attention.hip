@@ -35,6 +35,9 @@
 //  * Measured on MI355X, MFMA and VALU work of the same SIMD mostly add up rather than overlap,
 //    so the time per tile is about MFMA + VALU: the score roundings, exponentials and converts
 //    are the VALU share.
+#include <algorithm>
+#include <initializer_list>
+
 #include "mi_common.h"
 
 namespace mi {
@@ -91,8 +94,8 @@ struct PrefillArgs {
   int64_t k_row, k_head, k_tok;
   const uint16_t* value;
   int64_t v_row, v_head, v_tok;
-  const uint16_t* key_pool;
-  const uint16_t* value_pool;
+  uint16_t* key_pool;
+  uint16_t* value_pool;
   int64_t num_blocks;
   const int64_t* history_blocks;
   int64_t history_stride;
@@ -104,6 +107,16 @@ struct PrefillArgs {
   int32_t group;   // query heads per KV head (G)
   int32_t pairs;   // workgroups per KV head: ceil(G / 2)
   float scale;
+  int32_t tiles;   // query tiles per row: ceil(padded_len / kQTile)
+  int32_t batch;   // rows
+  int32_t groups;  // workgroups of these rows: tiles x num_kv_heads x pairs x batch
+  // Decode rows (a mixed step's single new tokens, padded_len 1): start_lens holds each row's
+  // context length including its token, so the history is the context minus one and a row with
+  // context 0 is padding; the token's K/V row is appended to pool slot slot_mapping[b] (skipped
+  // when outside the pool) by the workgroup of the first head pair of each KV head.
+  int32_t decode_rows;
+  const int64_t* slot_mapping;
+  int64_t slot_stride;
 };
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -138,11 +151,17 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint3
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
+// One launch serves up to two sets of rows (a mixed step's chunk rows and its decode rows): the
+// first a0.groups workgroups take a0, the rest a1.
 template <int kKvHeads>
-__global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kernel(const PrefillArgs a0,
+                                                                                   const PrefillArgs a1) {
   __shared__ __align__(16) uint16_t sK[2][kKTile * kKStride];
   __shared__ __align__(16) uint16_t sV[2][kHeadDim * kVStride];
   extern __shared__ int s_hblk[];  // [ceil(nh / 16)] history block ids of this row (dynamic LDS)
+
+  const bool second = static_cast<int>(blockIdx.x) >= a0.groups;  // uniform
+  const PrefillArgs a = second ? a1 : a0;
 
   // Workgroup -> (row b, head pair hp, query tile qt).  Consecutive workgroup ids go round-robin to
   // the 8 XCDs, each with its own L2; so that the query tiles of one (row, head) -- which stream
@@ -151,9 +170,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   // plain mapping.  Within a pair the heaviest (latest) query tiles start first.
   int b, hp, qt;
   {
-    const int tiles = gridDim.x;
-    const int pairs = gridDim.y * gridDim.z;
-    const int lin = blockIdx.x + tiles * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int tiles = a.tiles;
+    const int per_row = kKvHeads * a.pairs;
+    const int pairs = per_row * a.batch;
+    const int lin = static_cast<int>(blockIdx.x) - (second ? a0.groups : 0);
     int pair, rank;
     if (pairs % 8 == 0) {
       const int slot = lin >> 3;
@@ -163,16 +183,23 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
       pair = lin / tiles;
       rank = lin % tiles;
     }
-    hp = pair % gridDim.y;
-    b = pair / gridDim.y;
+    hp = pair % per_row;
+    b = pair / per_row;
     qt = tiles - 1 - rank;
   }
   const int q0 = qt * kQTile;
   const int L = a.padded_len;
-  int64_t len64 = a.chunk_lens[b * a.lens_stride];
+  int64_t len64, start64;
+  if (a.decode_rows) {
+    const int64_t ctx = a.start_lens[b * a.lens_stride];
+    len64 = ctx > 0 ? 1 : 0;
+    start64 = ctx > 0 ? ctx - 1 : 0;
+  } else {
+    len64 = a.chunk_lens[b * a.lens_stride];
+    start64 = a.start_lens[b * a.lens_stride];
+  }
   len64 = len64 < 0 ? 0 : (len64 > L ? L : len64);
   const int pad = L - static_cast<int>(len64);
-  int64_t start64 = a.start_lens[b * a.lens_stride];
   start64 = start64 < 0 ? 0 : start64;
   const int64_t hist_cap = static_cast<int64_t>(a.max_history_blocks) * kBlockSize;
   const int nh = static_cast<int>(start64 < hist_cap ? start64 : hist_cap);
@@ -188,6 +215,16 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   const int h = g * a.group + min(j0 + hh, a.group - 1);
   const int ql = lane & 15;
   const int gq = lane >> 4;
+
+  if (a.decode_rows && j0 == 0 && tid < 32 && len64 > 0) {  // append the token's K and V rows of KV head g
+    const int64_t slot = a.slot_mapping[b * a.slot_stride];
+    if (slot >= 0 && slot < a.num_blocks * kBlockSize) {
+      const int piece = (tid & 15) * 8;
+      const uint16_t* src = tid < 16 ? a.key + b * a.k_row + g * a.k_head : a.value + b * a.v_row + g * a.v_head;
+      uint16_t* dst = (tid < 16 ? a.key_pool : a.value_pool) + (slot * kKvHeads + g) * kHeadDim;
+      *reinterpret_cast<uint4*>(dst + piece) = *reinterpret_cast<const uint4*>(src + piece);
+    }
+  }
 
   uint16_t* out_b = a.out + b * a.out_row;
   if (q0 + kQTile <= pad) {  // the whole tile is padding: zero rows
@@ -480,6 +517,64 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
 }  // namespace
 }  // namespace mi
 
+namespace mi {
+namespace {
+
+// Checks shared by the entry points (sizes, head shape, strides, alignment).
+int32_t check_common(const char* name, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     int64_t num_blocks, std::initializer_list<int64_t> strides, std::initializer_list<const void*> tensors) {
+  if (head_dim != kHeadDim || block_size != kBlockSize || num_kv_heads <= 0 || num_heads <= 0 ||
+      num_heads % num_kv_heads != 0)
+    return fail(MI_ERR_UNSUPPORTED,
+                "%s: needs head_dim %d, block_size %d, num_heads a multiple of num_kv_heads (got head_dim %d, "
+                "block_size %d, heads %d/%d)",
+                name, kHeadDim, kBlockSize, head_dim, block_size, num_heads, num_kv_heads);
+  if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
+    return fail(MI_ERR_UNSUPPORTED, "%s: num_kv_heads %d not in {1,2,4,8}", name, num_kv_heads);
+  for (int64_t st : strides)
+    if (st % 8 != 0) return fail(MI_ERR_UNSUPPORTED, "%s: strides must be multiples of 8", name);
+  for (const void* t : tensors)
+    if (t && !aligned16(t)) return fail(MI_ERR_UNSUPPORTED, "%s: tensors must be 16-byte aligned", name);
+  if (num_blocks > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "%s: pool too large", name);
+  return MI_OK;
+}
+
+// Fills the row-independent fields; the caller sets the pointers and strides of its rows.
+PrefillArgs rows_args(int32_t batch, int32_t padded_len, int32_t num_heads, int32_t num_kv_heads, float scale) {
+  PrefillArgs a{};
+  a.batch = batch;
+  a.padded_len = padded_len;
+  a.group = num_heads / num_kv_heads;
+  a.pairs = (a.group + kGroup - 1) / kGroup;
+  a.scale = scale;
+  a.tiles = (padded_len + kQTile - 1) / kQTile;
+  const int64_t groups = static_cast<int64_t>(a.tiles) * num_kv_heads * a.pairs * batch;
+  a.groups = groups > 0x3fffffff ? -1 : static_cast<int32_t>(groups);
+  return a;
+}
+
+int32_t launch_rows(const char* name, const PrefillArgs& a0, const PrefillArgs& a1, int32_t num_kv_heads,
+                    int32_t max_history_blocks, void* stream) {
+  if (a0.groups < 0 || a1.groups < 0 || static_cast<int64_t>(a0.groups) + a1.groups > 0x3fffffff)
+    return fail(MI_ERR_UNSUPPORTED, "%s: too many workgroups", name);
+  if (max_history_blocks > kMaxHistoryBlocks)
+    return fail(MI_ERR_UNSUPPORTED, "%s: history of %d blocks exceeds %d", name, max_history_blocks, kMaxHistoryBlocks);
+  const int groups = a0.groups + a1.groups;
+  if (groups == 0) return ok();
+  const size_t lds = sizeof(int) * static_cast<size_t>(max_history_blocks > 0 ? max_history_blocks : 1);
+  hipStream_t s = as_stream(stream);
+  switch (num_kv_heads) {
+    case 1: chunked_prefill_kernel<1><<<groups, kThreads, lds, s>>>(a0, a1); break;
+    case 2: chunked_prefill_kernel<2><<<groups, kThreads, lds, s>>>(a0, a1); break;
+    case 4: chunked_prefill_kernel<4><<<groups, kThreads, lds, s>>>(a0, a1); break;
+    default: chunked_prefill_kernel<8><<<groups, kThreads, lds, s>>>(a0, a1); break;
+  }
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace mi
+
 extern "C" int32_t mi_chunked_prefill_attention(
     void* out, int64_t out_row_stride, int64_t out_tok_stride, const void* query, int64_t query_row_stride,
     int64_t query_head_stride, int64_t query_tok_stride, const void* key, int64_t key_row_stride,
@@ -489,36 +584,28 @@ extern "C" int32_t mi_chunked_prefill_attention(
     const int64_t* start_lens, const int64_t* chunk_lens, int64_t lens_stride, int32_t batch, int32_t padded_len,
     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale, void* stream) {
   using namespace mi;
+  const char* name = "mi_chunked_prefill_attention";
   if (batch < 0 || padded_len < 0 || max_history_blocks < 0 || num_blocks < 0)
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_chunked_prefill_attention: negative size");
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", name);
   if (batch == 0 || padded_len == 0) return ok();
   if (!out || !query || !key || !value || !start_lens || !chunk_lens ||
       (max_history_blocks > 0 && (!history_blocks || !key_pool || !value_pool)))
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_chunked_prefill_attention: null pointer argument");
-  if (head_dim != kHeadDim || block_size != kBlockSize || num_kv_heads <= 0 || num_heads <= 0 ||
-      num_heads % num_kv_heads != 0)
-    return fail(MI_ERR_UNSUPPORTED,
-                "mi_chunked_prefill_attention: needs head_dim %d, block_size %d, num_heads a multiple of "
-                "num_kv_heads (got head_dim %d, block_size %d, heads %d/%d)",
-                kHeadDim, kBlockSize, head_dim, block_size, num_heads, num_kv_heads);
-  if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
-    return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: num_kv_heads %d not in {1,2,4,8}", num_kv_heads);
-  const int64_t strides[] = {out_row_stride, out_tok_stride, query_row_stride, query_head_stride, query_tok_stride,
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", name);
+  int32_t rc = check_common(name, num_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                            {out_row_stride, out_tok_stride, query_row_stride, query_head_stride, query_tok_stride,
                              key_row_stride, key_head_stride, key_tok_stride, value_row_stride, value_head_stride,
-                             value_tok_stride};
-  for (int64_t s : strides)
-    if (s % 8 != 0) return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: strides must be multiples of 8");
-  if (!aligned16(out) || !aligned16(query) || !aligned16(key) || !aligned16(value) ||
-      (max_history_blocks > 0 && (!aligned16(key_pool) || !aligned16(value_pool))))
-    return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: tensors must be 16-byte aligned");
+                             value_tok_stride},
+                            {out, query, key, value, max_history_blocks > 0 ? key_pool : nullptr,
+                             max_history_blocks > 0 ? value_pool : nullptr});
+  if (rc != MI_OK) return rc;
   if (max_history_blocks > 0 && history_stride < max_history_blocks)
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_chunked_prefill_attention: history_stride < max_history_blocks");
-  if (lens_stride <= 0) return fail(MI_ERR_INVALID_ARGUMENT, "mi_chunked_prefill_attention: lens_stride must be > 0");
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: history_stride < max_history_blocks", name);
+  if (lens_stride <= 0) return fail(MI_ERR_INVALID_ARGUMENT, "%s: lens_stride must be > 0", name);
   if (key_tok_stride < 0 || key_tok_stride >= (1 << 24) || value_tok_stride < 0 || value_tok_stride >= (1 << 24))
-    return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: key/value token strides must be in [0, 2^24)");
-  if (batch > 65535) return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: batch > 65535");
+    return fail(MI_ERR_UNSUPPORTED, "%s: key/value token strides must be in [0, 2^24)", name);
+  if (batch > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: batch > 65535", name);
 
-  PrefillArgs a{};
+  PrefillArgs a = rows_args(batch, padded_len, num_heads, num_kv_heads, scale);
   a.out = static_cast<uint16_t*>(out);
   a.out_row = out_row_stride;
   a.out_tok = out_tok_stride;
@@ -534,8 +621,8 @@ extern "C" int32_t mi_chunked_prefill_attention(
   a.v_row = value_row_stride;
   a.v_head = value_head_stride;
   a.v_tok = value_tok_stride;
-  a.key_pool = static_cast<const uint16_t*>(key_pool);
-  a.value_pool = static_cast<const uint16_t*>(value_pool);
+  a.key_pool = static_cast<uint16_t*>(const_cast<void*>(key_pool));
+  a.value_pool = static_cast<uint16_t*>(const_cast<void*>(value_pool));
   a.num_blocks = num_blocks;
   a.history_blocks = history_blocks;
   a.history_stride = history_stride;
@@ -543,23 +630,92 @@ extern "C" int32_t mi_chunked_prefill_attention(
   a.start_lens = start_lens;
   a.chunk_lens = chunk_lens;
   a.lens_stride = lens_stride;
-  a.padded_len = padded_len;
-  a.group = num_heads / num_kv_heads;
-  a.pairs = (a.group + kGroup - 1) / kGroup;
-  a.scale = scale;
+  return launch_rows(name, a, PrefillArgs{}, num_kv_heads, max_history_blocks, stream);
+}
 
-  if (num_blocks > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: pool too large");
-  if (max_history_blocks > kMaxHistoryBlocks)
-    return fail(MI_ERR_UNSUPPORTED, "mi_chunked_prefill_attention: history of %d blocks exceeds %d", max_history_blocks,
-                kMaxHistoryBlocks);
-  dim3 grid((padded_len + kQTile - 1) / kQTile, num_kv_heads * a.pairs, batch);
-  const size_t lds = sizeof(int) * static_cast<size_t>(max_history_blocks > 0 ? max_history_blocks : 1);
-  hipStream_t s = as_stream(stream);
-  switch (num_kv_heads) {
-    case 1: chunked_prefill_kernel<1><<<grid, kThreads, lds, s>>>(a); break;
-    case 2: chunked_prefill_kernel<2><<<grid, kThreads, lds, s>>>(a); break;
-    case 4: chunked_prefill_kernel<4><<<grid, kThreads, lds, s>>>(a); break;
-    default: chunked_prefill_kernel<8><<<grid, kThreads, lds, s>>>(a); break;
+extern "C" int32_t mi_mixed_paged_attention(
+    void* out, int64_t out_tok_stride, const void* query, int64_t query_tok_stride, int64_t query_head_stride,
+    const void* key, int64_t key_tok_stride, int64_t key_head_stride, const void* value, int64_t value_tok_stride,
+    int64_t value_head_stride, void* key_pool, void* value_pool, int64_t num_blocks, int32_t prefill_rows,
+    int32_t prefill_width, const int64_t* history_blocks, int64_t history_stride, int32_t max_history_blocks,
+    const int64_t* start_lens, const int64_t* chunk_lens, int64_t lens_stride, int32_t decode_rows,
+    const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks, const int64_t* context_lens,
+    int64_t context_lens_stride, const int64_t* slot_mapping, int64_t slot_stride, int32_t num_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale, void* stream) {
+  using namespace mi;
+  const char* name = "mi_mixed_paged_attention";
+  if (prefill_rows < 0 || prefill_width < 0 || decode_rows < 0 || max_history_blocks < 0 || max_blocks < 0 ||
+      num_blocks < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", name);
+  const bool chunks = prefill_rows > 0 && prefill_width > 0;
+  if (!chunks && decode_rows == 0) return ok();
+  if (!out || !query || !key || !value || (chunks && (!start_lens || !chunk_lens)) ||
+      (chunks && max_history_blocks > 0 && !history_blocks) ||
+      (decode_rows > 0 && (!context_lens || !slot_mapping || (max_blocks > 0 && !block_tables))) ||
+      ((decode_rows > 0 || max_history_blocks > 0) && (!key_pool || !value_pool)))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", name);
+  const bool pools = decode_rows > 0 || max_history_blocks > 0;
+  int32_t rc = check_common(name, num_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                            {out_tok_stride, query_tok_stride, query_head_stride, key_tok_stride, key_head_stride,
+                             value_tok_stride, value_head_stride},
+                            {out, query, key, value, pools ? key_pool : nullptr, pools ? value_pool : nullptr});
+  if (rc != MI_OK) return rc;
+  if (chunks && max_history_blocks > 0 && history_stride < max_history_blocks)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: history_stride < max_history_blocks", name);
+  if (decode_rows > 0 && max_blocks > 0 && block_table_stride < max_blocks)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: block_table_stride < max_blocks", name);
+  if ((chunks && lens_stride <= 0) || (decode_rows > 0 && (context_lens_stride <= 0 || slot_stride <= 0)))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: lens, context_lens and slot strides must be > 0", name);
+  if (key_tok_stride < 0 || key_tok_stride >= (1 << 24) || value_tok_stride < 0 || value_tok_stride >= (1 << 24))
+    return fail(MI_ERR_UNSUPPORTED, "%s: key/value token strides must be in [0, 2^24)", name);
+  if (prefill_rows > 65535 || decode_rows > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: more than 65535 rows", name);
+
+  // Chunk rows: tokens [0, P L), row b at token b L.  Decode rows: tokens [P L, P L + D), one each.
+  const int64_t n = chunks ? static_cast<int64_t>(prefill_rows) * prefill_width : 0;
+  auto fill = [&](PrefillArgs& a, int64_t tok0, int64_t rows_tokens) {
+    a.out = static_cast<uint16_t*>(out) + tok0 * out_tok_stride;
+    a.out_row = rows_tokens * out_tok_stride;
+    a.out_tok = out_tok_stride;
+    a.query = static_cast<const uint16_t*>(query) + tok0 * query_tok_stride;
+    a.q_row = rows_tokens * query_tok_stride;
+    a.q_head = query_head_stride;
+    a.q_tok = query_tok_stride;
+    a.key = static_cast<const uint16_t*>(key) + tok0 * key_tok_stride;
+    a.k_row = rows_tokens * key_tok_stride;
+    a.k_head = key_head_stride;
+    a.k_tok = key_tok_stride;
+    a.value = static_cast<const uint16_t*>(value) + tok0 * value_tok_stride;
+    a.v_row = rows_tokens * value_tok_stride;
+    a.v_head = value_head_stride;
+    a.v_tok = value_tok_stride;
+    a.key_pool = static_cast<uint16_t*>(key_pool);
+    a.value_pool = static_cast<uint16_t*>(value_pool);
+    a.num_blocks = num_blocks;
+  };
+  PrefillArgs a0{}, a1{};
+  if (chunks) {
+    a0 = rows_args(prefill_rows, prefill_width, num_heads, num_kv_heads, scale);
+    fill(a0, 0, prefill_width);
+    a0.history_blocks = history_blocks;
+    a0.history_stride = history_stride;
+    a0.max_history_blocks = max_history_blocks;
+    a0.start_lens = start_lens;
+    a0.chunk_lens = chunk_lens;
+    a0.lens_stride = lens_stride;
   }
-  return check_launch("mi_chunked_prefill_attention");
+  if (decode_rows > 0) {
+    a1 = rows_args(decode_rows, 1, num_heads, num_kv_heads, scale);
+    fill(a1, n, 1);
+    a1.history_blocks = block_tables;
+    a1.history_stride = block_table_stride;
+    a1.max_history_blocks = max_blocks;
+    a1.start_lens = context_lens;
+    a1.chunk_lens = context_lens;
+    a1.lens_stride = context_lens_stride;
+    a1.decode_rows = 1;
+    a1.slot_mapping = slot_mapping;
+    a1.slot_stride = slot_stride;
+  }
+  return launch_rows(name, a0, a1, num_kv_heads,
+                     std::max(chunks ? max_history_blocks : 0, decode_rows > 0 ? max_blocks : 0), stream);
 }

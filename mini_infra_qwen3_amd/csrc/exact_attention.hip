@@ -40,6 +40,7 @@
 // Key tiles of 64 keys (history first, then the causal chunk) are staged in LDS; a lane takes one
 // key of the tile against its wavefront's 8 rows for the scores, and two output dims of those rows
 // for P V.
+#include <algorithm>
 #include <math.h>
 #include <mutex>
 
@@ -429,8 +430,8 @@ struct ExactPrefillArgs {
   int64_t k_row, k_head, k_tok;
   const uint16_t* v;
   int64_t v_row, v_head, v_tok;
-  const uint16_t* key_pool;
-  const uint16_t* value_pool;
+  uint16_t* key_pool;
+  uint16_t* value_pool;
   int64_t num_blocks;
   int32_t kv_heads;
   const int64_t* history;
@@ -442,10 +443,22 @@ struct ExactPrefillArgs {
   int32_t padded_len;
   float scale;
   int32_t cache_keys;      // keys the LDS cache holds (>= a row's keys: cached form; else kPfKeys, recompute)
+  int32_t tiles;           // query tiles per row
+  int32_t batch;           // rows
+  int32_t groups;          // workgroups of these rows: tiles x kv_heads x batch
+  // Decode rows (a mixed step's single new tokens, padded_len 1): start_lens holds each row's
+  // context length including its token, so the history is the context minus one and a row with
+  // context 0 is padding; the token's K/V row of each KV head is appended to pool slot
+  // slot_mapping[b] (skipped when outside the pool).
+  int32_t decode_rows;
+  const int64_t* slot_mapping;
+  int64_t slot_stride;
 };
 
+// One launch serves up to two sets of rows (a mixed step's chunk rows and its decode rows): the
+// first a0.groups workgroups take a0, the rest a1.
 template <int kG>
-__global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPrefillArgs a) {
+__global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPrefillArgs a0, const ExactPrefillArgs a1) {
   constexpr int kQ = kPfRows / kG;        // query positions per workgroup
   constexpr int kRows = kQ * kG;          // rows in use (<= 32)
   extern __shared__ __align__(16) unsigned char s_raw[];
@@ -453,16 +466,35 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   uint16_t* sT = reinterpret_cast<uint16_t*>(s_raw + kPfQBytes);             // [64][kKvRow]
   uint16_t* sC = reinterpret_cast<uint16_t*>(s_raw + kPfQBytes + kPfTileBytes);  // [cache_keys][32]
 
-  const int qt = blockIdx.x;
-  const int g = blockIdx.y;
-  const int b = blockIdx.z;
+  const bool second = static_cast<int>(blockIdx.x) >= a0.groups;  // uniform
+  const ExactPrefillArgs a = second ? a1 : a0;
+  const int lin = static_cast<int>(blockIdx.x) - (second ? a0.groups : 0);
+  const int qt = lin % a.tiles;
+  const int g = (lin / a.tiles) % a.kv_heads;
+  const int b = lin / (a.tiles * a.kv_heads);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int L = a.padded_len;
-  int64_t clen = a.chunk_lens[b * a.lens_stride];
+  int64_t clen, nh64;
+  if (a.decode_rows) {
+    const int64_t ctx = a.start_lens[b * a.lens_stride];
+    clen = ctx > 0 ? 1 : 0;
+    nh64 = ctx > 0 ? ctx - 1 : 0;
+    if (ctx > 0 && threadIdx.x < 32) {  // append the token's K and V rows of KV head g
+      const int64_t slot = a.slot_mapping[b * a.slot_stride];
+      if (slot >= 0 && slot < a.num_blocks * kBlockSize) {
+        const int piece = (threadIdx.x & 15) * 8;
+        const uint16_t* src = threadIdx.x < 16 ? a.k + b * a.k_row + g * a.k_head : a.v + b * a.v_row + g * a.v_head;
+        uint16_t* dst = (threadIdx.x < 16 ? a.key_pool : a.value_pool) + (slot * a.kv_heads + g) * kHeadDim;
+        *reinterpret_cast<uint4*>(dst + piece) = *reinterpret_cast<const uint4*>(src + piece);
+      }
+    }
+  } else {
+    clen = a.chunk_lens[b * a.lens_stride];
+    nh64 = a.start_lens[b * a.lens_stride];
+  }
   clen = clen < 0 ? 0 : (clen > L ? L : clen);
   const int pad = L - static_cast<int>(clen);
-  int64_t nh64 = a.start_lens[b * a.lens_stride];
   nh64 = nh64 < 0 ? 0 : min(nh64, static_cast<int64_t>(a.max_hist_blocks) * kBlockSize);
   const int nh = static_cast<int>(nh64);
   const int i0 = qt * kQ;
@@ -715,26 +747,46 @@ int32_t dispatch_exact_decode(const ExactDecodeArgs& a, int32_t batch, int group
 }
 
 template <int kG>
-int32_t launch_exact_prefill(const ExactPrefillArgs& a, int32_t batch, hipStream_t s) {
+int32_t launch_exact_prefill(const ExactPrefillArgs& a0, const ExactPrefillArgs& a1, const char* what, hipStream_t s) {
   static std::once_flag once;
   static int32_t attr_rc = MI_OK;
-  std::call_once(once, [] { attr_rc = allow_lds(exact_prefill_kernel<kG>, kPfLdsBytes, "mi_chunked_prefill_attention_exact"); });
+  std::call_once(once, [] { attr_rc = allow_lds(exact_prefill_kernel<kG>, kPfLdsBytes, "exact_prefill_kernel"); });
   if (attr_rc != MI_OK) return attr_rc;
-  constexpr int kQ = kPfRows / kG;
-  const size_t lds = static_cast<size_t>(kPfQBytes) + kPfTileBytes + static_cast<size_t>(a.cache_keys) * kPfRows * 2;
-  const dim3 grid((a.padded_len + kQ - 1) / kQ, a.kv_heads, batch);
-  exact_prefill_kernel<kG><<<grid, kPfThreads, lds, s>>>(a);
-  return check_launch("mi_chunked_prefill_attention_exact");
+  if (a0.groups < 0 || a1.groups < 0 || static_cast<int64_t>(a0.groups) + a1.groups > 0x3fffffff)
+    return fail(MI_ERR_UNSUPPORTED, "%s: too many workgroups", what);
+  const int groups = a0.groups + a1.groups;
+  if (groups == 0) return ok();
+  const int32_t cache_keys = std::max(a0.groups > 0 ? a0.cache_keys : 0, a1.groups > 0 ? a1.cache_keys : 0);
+  const size_t lds = static_cast<size_t>(kPfQBytes) + kPfTileBytes + static_cast<size_t>(cache_keys) * kPfRows * 2;
+  exact_prefill_kernel<kG><<<groups, kPfThreads, lds, s>>>(a0, a1);
+  return check_launch(what);
 }
 
-int32_t dispatch_exact_prefill(const ExactPrefillArgs& a, int32_t batch, int group, hipStream_t s) {
+int32_t dispatch_exact_prefill(const ExactPrefillArgs& a0, const ExactPrefillArgs& a1, int group, const char* what,
+                               hipStream_t s) {
   switch (group) {
-    case 1: return launch_exact_prefill<1>(a, batch, s);
-    case 2: return launch_exact_prefill<2>(a, batch, s);
-    case 4: return launch_exact_prefill<4>(a, batch, s);
-    case 5: return launch_exact_prefill<5>(a, batch, s);
-    default: return launch_exact_prefill<8>(a, batch, s);
+    case 1: return launch_exact_prefill<1>(a0, a1, what, s);
+    case 2: return launch_exact_prefill<2>(a0, a1, what, s);
+    case 4: return launch_exact_prefill<4>(a0, a1, what, s);
+    case 5: return launch_exact_prefill<5>(a0, a1, what, s);
+    default: return launch_exact_prefill<8>(a0, a1, what, s);
   }
+}
+
+// Row-independent fields: grid shape and the LDS score cache for rows of up to `keys` keys.
+void exact_rows(ExactPrefillArgs& a, int32_t batch, int32_t padded_len, int32_t num_heads, int32_t num_kv_heads,
+                int64_t keys, float scale) {
+  const int group = num_heads / num_kv_heads;
+  a.batch = batch;
+  a.padded_len = padded_len;
+  a.kv_heads = num_kv_heads;
+  a.scale = scale;
+  const int q_per_group = kPfRows / group;
+  a.tiles = (padded_len + q_per_group - 1) / q_per_group;
+  const int64_t groups = static_cast<int64_t>(a.tiles) * num_kv_heads * batch;
+  a.groups = groups > 0x3fffffff ? -1 : static_cast<int32_t>(groups);
+  const int64_t keys_up = (keys + kPfKeys - 1) / kPfKeys * kPfKeys;
+  a.cache_keys = keys_up <= kPfMaxCacheKeys ? static_cast<int32_t>(keys_up) : kPfKeys;
 }
 
 int32_t check_exact_heads(const char* what, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
@@ -873,22 +925,104 @@ extern "C" int32_t mi_chunked_prefill_attention_exact(
   a.v_row = value_row_stride;
   a.v_head = value_head_stride;
   a.v_tok = value_tok_stride;
-  a.key_pool = static_cast<const uint16_t*>(key_pool);
-  a.value_pool = static_cast<const uint16_t*>(value_pool);
+  a.key_pool = static_cast<uint16_t*>(const_cast<void*>(key_pool));
+  a.value_pool = static_cast<uint16_t*>(const_cast<void*>(value_pool));
   a.num_blocks = num_blocks;
-  a.kv_heads = num_kv_heads;
   a.history = history_blocks;
   a.hist_stride = history_stride;
   a.max_hist_blocks = max_history_blocks;
   a.start_lens = start_lens;
   a.chunk_lens = chunk_lens;
   a.lens_stride = lens_stride;
-  a.padded_len = padded_len;
-  a.scale = scale;
   // Keys a row can see: its history (at most the table's) plus the chunk up to it.
-  const int64_t keys = static_cast<int64_t>(max_history_blocks) * kBlockSize + padded_len;
-  const int64_t keys_up = (keys + kPfKeys - 1) / kPfKeys * kPfKeys;
-  a.cache_keys = keys_up <= kPfMaxCacheKeys ? static_cast<int32_t>(keys_up) : kPfKeys;
-  const int32_t rc = dispatch_exact_prefill(a, batch, group, as_stream(stream));
+  exact_rows(a, batch, padded_len, num_heads, num_kv_heads,
+             static_cast<int64_t>(max_history_blocks) * kBlockSize + padded_len, scale);
+  const int32_t rc = dispatch_exact_prefill(a, ExactPrefillArgs{}, group, what, as_stream(stream));
+  return rc == MI_OK ? ok() : rc;
+}
+
+extern "C" int32_t mi_mixed_paged_attention_exact(
+    void* out, int64_t out_tok_stride, const void* query, int64_t query_tok_stride, int64_t query_head_stride,
+    const void* key, int64_t key_tok_stride, int64_t key_head_stride, const void* value, int64_t value_tok_stride,
+    int64_t value_head_stride, void* key_pool, void* value_pool, int64_t num_blocks, int32_t prefill_rows,
+    int32_t prefill_width, const int64_t* history_blocks, int64_t history_stride, int32_t max_history_blocks,
+    const int64_t* start_lens, const int64_t* chunk_lens, int64_t lens_stride, int32_t decode_rows,
+    const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks, const int64_t* context_lens,
+    int64_t context_lens_stride, const int64_t* slot_mapping, int64_t slot_stride, int32_t num_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale, void* stream) {
+  using namespace mi;
+  const char* what = "mi_mixed_paged_attention_exact";
+  if (prefill_rows < 0 || prefill_width < 0 || decode_rows < 0 || max_history_blocks < 0 || max_blocks < 0 ||
+      num_blocks < 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
+  const bool chunks = prefill_rows > 0 && prefill_width > 0;
+  if (!chunks && decode_rows == 0) return ok();
+  if (const int32_t rc = check_exact_heads(what, num_heads, num_kv_heads, head_dim, block_size)) return rc;
+  const bool pools = decode_rows > 0 || max_history_blocks > 0;
+  if (!out || !query || !key || !value || (chunks && (!start_lens || !chunk_lens)) ||
+      (chunks && max_history_blocks > 0 && !history_blocks) ||
+      (decode_rows > 0 && (!context_lens || !slot_mapping || (max_blocks > 0 && !block_tables))) ||
+      (pools && (!key_pool || !value_pool)))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
+  if (!aligned16(out) || !aligned16(key) || !aligned16(value) || (pools && (!aligned16(key_pool) || !aligned16(value_pool))) ||
+      out_tok_stride % 8 != 0 || key_tok_stride % 8 != 0 || key_head_stride % 8 != 0 || value_tok_stride % 8 != 0 ||
+      value_head_stride % 8 != 0)
+    return fail(MI_ERR_UNSUPPORTED, "%s: out / key / value / pools need 16-byte alignment and strides of 8 elements", what);
+  if ((chunks && (lens_stride <= 0 || (max_history_blocks > 0 && history_stride < max_history_blocks))) ||
+      (decode_rows > 0 && (context_lens_stride <= 0 || slot_stride <= 0 ||
+                           (max_blocks > 0 && block_table_stride < max_blocks))))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: bad stride", what);
+  if (prefill_rows > 65535 || decode_rows > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: more than 65535 rows", what);
+  if (num_blocks > INT64_MAX / (kBlockSize * static_cast<int64_t>(num_kv_heads) * head_dim))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: pool too large", what);
+
+  // Chunk rows: tokens [0, P L), row b at token b L.  Decode rows: tokens [P L, P L + D), one each.
+  const int64_t n = chunks ? static_cast<int64_t>(prefill_rows) * prefill_width : 0;
+  auto fill = [&](ExactPrefillArgs& a, int64_t tok0, int64_t row_tokens) {
+    a.out = static_cast<uint16_t*>(out) + tok0 * out_tok_stride;
+    a.out_row = row_tokens * out_tok_stride;
+    a.out_tok = out_tok_stride;
+    a.q = static_cast<const uint16_t*>(query) + tok0 * query_tok_stride;
+    a.q_row = row_tokens * query_tok_stride;
+    a.q_head = query_head_stride;
+    a.q_tok = query_tok_stride;
+    a.k = static_cast<const uint16_t*>(key) + tok0 * key_tok_stride;
+    a.k_row = row_tokens * key_tok_stride;
+    a.k_head = key_head_stride;
+    a.k_tok = key_tok_stride;
+    a.v = static_cast<const uint16_t*>(value) + tok0 * value_tok_stride;
+    a.v_row = row_tokens * value_tok_stride;
+    a.v_head = value_head_stride;
+    a.v_tok = value_tok_stride;
+    a.key_pool = static_cast<uint16_t*>(key_pool);
+    a.value_pool = static_cast<uint16_t*>(value_pool);
+    a.num_blocks = num_blocks;
+  };
+  ExactPrefillArgs a0{}, a1{};
+  if (chunks) {
+    fill(a0, 0, prefill_width);
+    a0.history = history_blocks;
+    a0.hist_stride = history_stride;
+    a0.max_hist_blocks = max_history_blocks;
+    a0.start_lens = start_lens;
+    a0.chunk_lens = chunk_lens;
+    a0.lens_stride = lens_stride;
+    exact_rows(a0, prefill_rows, prefill_width, num_heads, num_kv_heads,
+               static_cast<int64_t>(max_history_blocks) * kBlockSize + prefill_width, scale);
+  }
+  if (decode_rows > 0) {
+    fill(a1, n, 1);
+    a1.history = block_tables;
+    a1.hist_stride = block_table_stride;
+    a1.max_hist_blocks = max_blocks;
+    a1.start_lens = context_lens;
+    a1.chunk_lens = context_lens;
+    a1.lens_stride = context_lens_stride;
+    a1.decode_rows = 1;
+    a1.slot_mapping = slot_mapping;
+    a1.slot_stride = slot_stride;
+    exact_rows(a1, decode_rows, 1, num_heads, num_kv_heads, static_cast<int64_t>(max_blocks) * kBlockSize + 1, scale);
+  }
+  const int32_t rc = dispatch_exact_prefill(a0, a1, num_heads / num_kv_heads, what, as_stream(stream));
   return rc == MI_OK ? ok() : rc;
 }

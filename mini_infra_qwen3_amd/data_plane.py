@@ -18,6 +18,7 @@ __all__ = [
     "argmax_rows",
     "chunked_prefill_attention",
     "gather_blocks",
+    "mixed_paged_attention",
     "pack_blocks",
     "paged_decode_attention",
     "paged_decode_attention_fused",
@@ -458,6 +459,100 @@ def chunked_prefill_attention(
         _stream(device),
     )
     _native.check(rc, "mi_chunked_prefill_attention_exact" if exact else "mi_chunked_prefill_attention")
+    return out
+
+
+def mixed_paged_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    prefill_rows: int,
+    prefill_width: int,
+    history_blocks: torch.Tensor,
+    start_lens: torch.Tensor,
+    chunk_lens: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    scale: float,
+    out: torch.Tensor | None = None,
+    exact: bool = False,
+) -> torch.Tensor:
+    """The attention of a mixed chunk + decode step in one launch (``mi_mixed_paged_attention``, or
+    ``mi_mixed_paged_attention_exact`` with ``exact``), which also appends the decode tokens' K/V.
+
+    A flattened batch of T = P L + D tokens: query ``[T, H, D]``, key / value ``[T, H_kv, D]``
+    (token-major, D contiguous; the rotated q / k of ``qk_norm_rope``).  Tokens ``[0, P L)`` are P
+    left-padded chunks of width L with ``history_blocks`` ``[P, nb]`` (nb may be 0), ``start_lens``
+    / ``chunk_lens`` ``[P]`` as in ``chunked_prefill_attention``; the last D tokens are decode rows
+    with ``block_tables`` ``[D, mb]``, ``context_lens`` ``[D]`` (tokens including the new one) and
+    ``slot_mapping`` ``[D]`` (where the new K/V go; -1: none).  Pools ``[num_blocks, block_size,
+    H_kv, D]``, block_size 16 or a multiple.  Returns ``out`` ``[T, H * D]`` bf16.
+    """
+    device = query.device
+    for name, t in (("query", query), ("key", key), ("value", value), ("key_pool", key_pool),
+                    ("value_pool", value_pool), ("history_blocks", history_blocks), ("start_lens", start_lens),
+                    ("chunk_lens", chunk_lens), ("block_tables", block_tables), ("context_lens", context_lens),
+                    ("slot_mapping", slot_mapping)):
+        _require_gpu(name, t, device)
+    for name, t, nd in (("history_blocks", history_blocks, 2), ("start_lens", start_lens, 1),
+                        ("chunk_lens", chunk_lens, 1), ("block_tables", block_tables, 2),
+                        ("context_lens", context_lens, 1), ("slot_mapping", slot_mapping, 1)):
+        _require_index(name, t, nd)
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.ndim != 3 or t.dtype != torch.bfloat16 or t.stride(2) != 1:
+            raise ValueError(f"{name} must be [T, heads, D] bf16 with D contiguous, got {tuple(t.shape)} {t.dtype}")
+    tokens, num_heads, head_dim = query.shape
+    num_blocks, block_size, num_kv_heads, _ = key_pool.shape
+    rows, width = int(prefill_rows), int(prefill_width)
+    decode_rows = int(context_lens.shape[0])
+    if rows < 0 or width < 0 or tokens != rows * width + decode_rows:
+        raise ValueError(f"{tokens} tokens are not {rows} chunk rows x {width} + {decode_rows} decode rows")
+    if key.shape != (tokens, num_kv_heads, head_dim) or value.shape != key.shape:
+        raise ValueError(f"key/value must be [{tokens}, {num_kv_heads}, {head_dim}]")
+    if key_pool.dtype != torch.bfloat16 or value_pool.shape != key_pool.shape or not key_pool.is_contiguous() \
+            or not value_pool.is_contiguous():
+        raise ValueError("pools must be contiguous bf16 with identical shapes")
+    if history_blocks.shape[0] != rows or start_lens.shape[0] != rows or chunk_lens.shape[0] != rows:
+        raise ValueError("history_blocks / start_lens / chunk_lens must have one row per chunk row")
+    if block_tables.shape[0] != decode_rows or slot_mapping.shape[0] != decode_rows:
+        raise ValueError("block_tables / slot_mapping must have one row per decode row")
+    kp, vp, history_blocks = _as_kernel_blocks(key_pool, value_pool, history_blocks)
+    _, _, block_tables = _as_kernel_blocks(key_pool, value_pool, block_tables)
+    num_blocks, block_size = kp.shape[:2]
+    if history_blocks.stride(-1) != 1:
+        history_blocks = history_blocks.contiguous()
+    if block_tables.stride(-1) != 1:
+        block_tables = block_tables.contiguous()
+    if rows > 1 and start_lens.stride(0) != chunk_lens.stride(0):
+        start_lens, chunk_lens = start_lens.contiguous(), chunk_lens.contiguous()
+    lens_stride = start_lens.stride(0) if rows > 1 else 1
+    nb, mb = history_blocks.shape[1], block_tables.shape[1]
+    if out is None:
+        out = torch.empty((tokens, num_heads * head_dim), dtype=torch.bfloat16, device=device)
+    elif out.shape != (tokens, num_heads * head_dim) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError(f"out must be [T, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
+    if tokens == 0:
+        return out
+    name = "mi_mixed_paged_attention_exact" if exact else "mi_mixed_paged_attention"
+    rc = getattr(_native.load(), name)(
+        out.data_ptr(), out.stride(0),
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key.data_ptr(), key.stride(0), key.stride(1),
+        value.data_ptr(), value.stride(0), value.stride(1),
+        kp.data_ptr(), vp.data_ptr(), num_blocks,
+        rows, width, history_blocks.data_ptr() if nb and rows else None, history_blocks.stride(0) if nb else 0,
+        nb if rows else 0, start_lens.data_ptr() if rows else None, chunk_lens.data_ptr() if rows else None,
+        lens_stride,
+        decode_rows, block_tables.data_ptr() if mb and decode_rows else None, block_tables.stride(0) if mb else 0,
+        mb if decode_rows else 0, context_lens.data_ptr() if decode_rows else None,
+        context_lens.stride(0) if decode_rows else 1, slot_mapping.data_ptr() if decode_rows else None,
+        slot_mapping.stride(0) if decode_rows else 1,
+        num_heads, num_kv_heads, head_dim, block_size, float(scale), _stream(device),
+    )
+    _native.check(rc, name)
     return out
 
 

@@ -81,7 +81,8 @@ class PagedPrefillMetadata(NamedTuple):
 class PagedMixedMetadata(NamedTuple):
     """A mixed chunk + decode step over a flattened ``[1, T]`` batch: tokens ``[0, P L)`` are
     ``prefill_rows`` (P) left-padded chunks of ``prefill_width`` (L) tokens addressed by ``prefill``;
-    the last ``T - P L`` tokens are one new token per decoding sequence, addressed by ``decode``."""
+    the last ``T - P L`` tokens are one new token per decoding sequence, addressed by ``decode``.
+    ``prefill.kv_out`` (optional) holds per-layer ``[T, H_kv, D]`` buffers for all T tokens' K/V."""
 
     prefill: PagedPrefillMetadata
     decode: PagedAttentionMetadata
@@ -197,30 +198,23 @@ class Qwen3Attention(nn.Module):
         return self.o_proj(out), present
 
     def _mixed(self, q, k, v, cos, sin, kv_pool: PastKeyValue, metadata: PagedMixedMetadata, workspace, kv_out=None):
-        """Token rows ``[0, P L)`` take the prefill path, the rest the decode path (its K/V append
-        first, so decode attention sees the new token); both attentions write one ``[T, H D]`` buffer."""
+        """One q/k norm + RoPE launch over all T tokens, then one attention launch for the chunk rows
+        (tokens ``[0, P L)``) and the decode rows (the rest), which also appends the decode tokens'
+        K/V to the pool.  ``kv_out`` (optional): ``[T, H_kv, D]`` buffers for the rotated K / V."""
         key_pool, value_pool = kv_pool
         rows, width = metadata.prefill_rows, metadata.prefill_width
         n = rows * width
-        tokens = q.shape[0]
-        eps = self.q_norm.eps
-        out = torch.empty((tokens, self.num_heads * self.head_dim), dtype=q.dtype, device=q.device)
-        decode = metadata.decode
-        data_plane.paged_decode_attention_fused(q[n:], k[n:], v[n:], self.q_norm.weight, self.k_norm.weight, cos[n:],
-                                                sin[n:], eps, decode.slot_mapping, key_pool, value_pool,
-                                                decode.block_tables, decode.context_lens, self.scaling,
-                                                out=out[n:], workspace=workspace, exact=self.exact)
         k_buf, v_buf = kv_out if kv_out is not None else (None, None)
-        q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q[:n], k[:n], v[:n], self.q_norm.weight, self.k_norm.weight,
-                                                       cos[:n], sin[:n], eps, k_out=k_buf, v_out=v_buf)
-        q_rot = q_rot.view(rows, width, self.num_heads, self.head_dim).transpose(1, 2)
-        k_rot = k_rot.view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
-        v_rows = v_rows.view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
-        prefill = metadata.prefill
-        data_plane.chunked_prefill_attention(q_rot, k_rot, v_rows, key_pool, value_pool, prefill.history_block_tables,
-                                             prefill.start_lens, prefill.chunk_lens, self.scaling,
-                                             out=out[:n].view(rows, width, -1), exact=self.exact)
-        return self.o_proj(out.unsqueeze(0)), (k_rot, v_rows)
+        q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin,
+                                                       self.q_norm.eps, k_out=k_buf, v_out=v_buf)
+        prefill, decode = metadata.prefill, metadata.decode
+        out = data_plane.mixed_paged_attention(
+            q_rot, k_rot, v_rows, key_pool, value_pool, rows, width, prefill.history_block_tables, prefill.start_lens,
+            prefill.chunk_lens, decode.block_tables, decode.context_lens, decode.slot_mapping, self.scaling,
+            exact=self.exact)
+        k_chunk = k_rot[:n].view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        v_chunk = v_rows[:n].view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        return self.o_proj(out.unsqueeze(0)), (k_chunk, v_chunk)
 
 
 class Qwen3MLP(nn.Module):

@@ -140,8 +140,8 @@ class _PrefillGraph:
 class _MixedGraph:
     """A mixed step's forward for one (chunk rows P, padded width W, decode rows D) bucket, with
     history tables NB and decode tables MB blocks wide, captured over a static buffer in the
-    ``pack_mixed_rows`` layout; chunk K/V go to the shared staging buffers.  Pad decode rows carry
-    slot -1 (no append) and context 0 (zero output)."""
+    ``pack_mixed_rows`` layout; the step's K/V (chunk and decode tokens) go to the shared staging
+    buffers.  Pad decode rows carry slot -1 (no append) and context 0 (zero output)."""
 
     def __init__(self, model: torch.nn.Module, pool: PagedKVCachePool, rows: int, width: int, decode_rows: int,
                  hist_blocks: int, decode_blocks: int, staging: torch.Tensor, mempool, pad_token_id: int,
@@ -152,9 +152,9 @@ class _MixedGraph:
         self.tokens = rows * width + decode_rows
         self.static = torch.from_numpy(self._empty()).to(device)
         ids, pos, meta = self.views()
-        n = rows * width
+        t = self.tokens
         meta = meta._replace(kv_pools=tuple(pool.kv_pools),
-                             prefill=meta.prefill._replace(kv_out=tuple((staging[l, 0, :n], staging[l, 1, :n])
+                             prefill=meta.prefill._replace(kv_out=tuple((staging[l, 0, :t], staging[l, 1, :t])
                                                                         for l in range(staging.shape[0]))))
         side = torch.cuda.Stream(device)  # default priority
         side.wait_stream(torch.cuda.current_stream(device))
@@ -316,7 +316,7 @@ class PagedRunner(BaseModelRunner):
             decode_row_buckets.append(max_decode_rows)
         self._decode_row_buckets = sorted(set(int(b) for b in decode_row_buckets if 0 < b <= max_decode_rows))
         top_w = -(-max_width // width_quantum) * width_quantum
-        staging = self._shared_staging(max_rows * top_w, pool)
+        staging = self._shared_staging(max_rows * top_w + max(self._decode_row_buckets, default=0), pool)
         self._mixed_pool = pool
         self._mixed_quantum = width_quantum
         self._mixed_tables = (max(int(max_history_blocks), 0), max(int(max_decode_blocks), 1))

@@ -144,6 +144,31 @@ def test_prefill_rejects_unsupported_shapes_on_host(native_lib):
     assert call(nb=16385, hstride=16385) == _native.MI_ERR_UNSUPPORTED  # history table beyond 64 KiB of LDS
 
 
+@pytest.mark.parametrize("exact", [False, True])
+def test_mixed_attention_rejects_bad_arguments_on_host(native_lib, exact):
+    entry = native_lib.mi_mixed_paged_attention_exact if exact else native_lib.mi_mixed_paged_attention
+
+    def call(rows=2, width=64, decode=3, heads=16, kv=8, dim=128, bs=16, nb=4, hstride=4, mb=8, bstride=8,
+             slots=16, tok=2048):
+        return entry(16, 2048, 16, tok, 128, 16, 1024, 128, 16, 1024, 128, 16, 16, 100, rows, width, 16, hstride, nb,
+                     16, 16, 1, decode, 16, bstride, mb, 16, 1, slots, 1, heads, kv, dim, bs, 0.1, None)
+
+    assert call(dim=64) == _native.MI_ERR_UNSUPPORTED
+    assert call(bs=32) == _native.MI_ERR_UNSUPPORTED
+    assert call(heads=12) == _native.MI_ERR_UNSUPPORTED  # not a multiple of the 8 KV heads
+    assert call(rows=-1) == _native.MI_ERR_INVALID_ARGUMENT
+    assert call(decode=-2) == _native.MI_ERR_INVALID_ARGUMENT
+    assert call(slots=None) == _native.MI_ERR_INVALID_ARGUMENT  # decode rows need their slots
+    assert call(hstride=3) == _native.MI_ERR_INVALID_ARGUMENT
+    assert call(bstride=7) == _native.MI_ERR_INVALID_ARGUMENT
+    assert call(rows=70000) == _native.MI_ERR_UNSUPPORTED
+    if exact:
+        assert call(heads=24) == _native.MI_ERR_UNSUPPORTED  # GQA group 3: no exact kernel for it
+    else:
+        assert call(tok=100) == _native.MI_ERR_UNSUPPORTED  # stride not a multiple of 8 elements
+    assert call(rows=0, decode=0) == _native.MI_OK  # nothing to do
+
+
 def test_argmax_rejects_bad_arguments_on_host(native_lib):
     lib = native_lib
     assert lib.mi_argmax_rows(16, 16, 4, 0, 16, None) == _native.MI_ERR_INVALID_ARGUMENT
