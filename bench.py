@@ -725,7 +725,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "scatter-head", "gather", "prefill",
-                                           "copy", "swap", "e2e", "e2e-mixed", "e2e-bandwidth", "all"],
+                                           "copy", "swap", "e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth", "all"],
                         default="all")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -755,8 +755,8 @@ def main() -> int:
         log(f"{args.only}: {json.dumps(res)}")
         print(json.dumps(res), flush=True)
         return 0
-    if args.only in ("e2e", "e2e-mixed", "e2e-bandwidth"):
-        res = bench_e2e(device, mixed=args.only == "e2e-mixed", exact=args.only != "e2e-bandwidth")
+    if args.only in ("e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth"):
+        res = bench_e2e(device, mixed=args.only.startswith("e2e-mixed"), exact=not args.only.endswith("bandwidth"))
         log(f"e2e: {res['output_tok_s']:.1f} output tok/s (busy), {res['wall_tok_s']:.1f} tok/s (wall)")
         print(json.dumps(res), flush=True)
         return 0
@@ -805,15 +805,19 @@ def main() -> int:
             f"{sw['unpack']['achieved_GBps']:.1f} GB/s; swap out {sw['swap_out']['achieved_GBps']:.1f} GB/s, "
             f"swap in {sw['swap_in']['achieved_GBps']:.1f} GB/s")
         torch.cuda.empty_cache()
-    e2e = e2e_mixed = e2e_bw = None
+    e2e = e2e_mixed = e2e_mixed_exact = e2e_bw = None
     if args.only == "all":
         e2e = bench_e2e(device)
         log(f"e2e: {e2e['output_tok_s']:.1f} output tok/s (busy), {e2e['wall_tok_s']:.1f} tok/s (wall)")
-        e2e_mixed = bench_e2e(device, mixed=True)
-        log(f"e2e mixed batching: {e2e_mixed['output_tok_s']:.1f} output tok/s (busy), ITL max "
-            f"{e2e_mixed['latency_ms']['itl_ms_max']:.2f} ms (alternating: {e2e['latency_ms']['itl_ms_max']:.2f} ms)")
         e2e_bw = bench_e2e(device, exact=False)
-        log(f"e2e bandwidth kernels: {e2e_bw['output_tok_s']:.1f} output tok/s (busy)")
+        log(f"e2e bandwidth kernels: {e2e_bw['output_tok_s']:.1f} output tok/s (busy), ITL max "
+            f"{e2e_bw['latency_ms']['itl_ms_max']:.2f} ms")
+        e2e_mixed = bench_e2e(device, mixed=True, exact=False)
+        log(f"e2e mixed batching (bandwidth kernels): {e2e_mixed['output_tok_s']:.1f} output tok/s (busy), ITL max "
+            f"{e2e_mixed['latency_ms']['itl_ms_max']:.2f} ms")
+        e2e_mixed_exact = bench_e2e(device, mixed=True)
+        log(f"e2e mixed batching (reference numerics): {e2e_mixed_exact['output_tok_s']:.1f} output tok/s (busy), "
+            f"ITL max {e2e_mixed_exact['latency_ms']['itl_ms_max']:.2f} ms")
         if not args.no_cpu_baseline:
             e2e["cpu_baseline"] = cpu_baseline_e2e()
             log(f"e2e cpu baseline: {e2e['cpu_baseline']['value']:.2f} output tok/s")
@@ -847,6 +851,7 @@ def main() -> int:
         "kernels": kernels,
         "e2e": e2e,
         "e2e_mixed_batching": e2e_mixed,
+        "e2e_mixed_batching_exact": e2e_mixed_exact,
         "e2e_bandwidth_kernels": e2e_bw,
     }
     print(json.dumps(line), flush=True)

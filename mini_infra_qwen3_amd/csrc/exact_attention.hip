@@ -117,9 +117,10 @@ struct ExactDecodeArgs {
   int64_t out_row;
   const uint16_t* q;       // rotated queries [B, H, 128] (plain form) or raw q projection rows (prologue)
   int64_t q_row, q_head;
-  const uint16_t* k_new;   // prologue: raw k / v projection rows of the new tokens
-  const uint16_t* v_new;
+  const uint16_t* k_new;   // prologue: raw k / v projection rows of the new tokens; plain form with
+  const uint16_t* v_new;   // slot_mapping: their rotated rows, KV head h at h * k_head / v_head
   int64_t k_row, v_row;
+  int64_t k_head, v_head;
   const uint16_t* q_weight;
   const uint16_t* k_weight;
   const uint16_t* cos;     // [B, 128]
@@ -141,16 +142,32 @@ struct ExactDecodeArgs {
   int32_t cache_tokens;    // tokens the LDS score cache holds per head (0: recompute the scores)
 };
 
-template <int kG, bool kPrologue>
-__global__ __launch_bounds__(kDecThreads) void exact_decode_kernel(const ExactDecodeArgs a) {
-  __shared__ __align__(16) float s_q[kG][kHeadDim];
-  __shared__ float s_m[kDecWaves][kG];
-  __shared__ double s_l[kDecWaves][kG][2];
-  __shared__ double s_o[kDecWaves][kHeadDim];
-  extern __shared__ uint16_t s_cache[];  // [cache_tokens][kG]: bf16 scores, then probabilities
+// LDS of the decode body, carved from the workgroup's dynamic LDS: queries, per-wavefront maxima,
+// denominators and outputs, then the score cache [cache_tokens][kG] (bf16 scores, then
+// probabilities).
+template <int kG, int kWaves>
+struct DecodeLds {
+  static constexpr int kQ = kG * kHeadDim * 4;
+  static constexpr int kM = kWaves * kG * 4;
+  static constexpr int kL = kWaves * kG * 2 * 8;
+  static constexpr int kO = kWaves * kHeadDim * 8;
+  static constexpr int kFixed = (kQ + kM + 7) / 8 * 8 + kL + kO;  // bytes before the cache
+};
 
-  const int b = blockIdx.x;
-  const int g = blockIdx.y;
+// Exact decode attention of sequence b, KV head g, by the workgroup's kWaves wavefronts.  kPrologue:
+// q / k RMSNorm + RoPE from the raw projection rows and the K/V append.  Plain form: rotated
+// queries; with a.slot_mapping set the rows a.k_new / a.v_new (already rotated) are appended first.
+template <int kG, bool kPrologue, int kWaves>
+__device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const int g, unsigned char* smem) {
+  constexpr int kDecWaves = kWaves;
+  constexpr int kDecThreads = 64 * kWaves;
+  using Lds = DecodeLds<kG, kWaves>;
+  auto s_q = reinterpret_cast<float (*)[kHeadDim]>(smem);
+  auto s_m = reinterpret_cast<float (*)[kG]>(smem + Lds::kQ);
+  auto s_l = reinterpret_cast<double (*)[kG][2]>(smem + (Lds::kQ + Lds::kM + 7) / 8 * 8);
+  auto s_o = reinterpret_cast<double (*)[kHeadDim]>(smem + (Lds::kQ + Lds::kM + 7) / 8 * 8 + Lds::kL);
+  uint16_t* s_cache = reinterpret_cast<uint16_t*>(smem + Lds::kFixed);
+
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int dl = lane & 15;
@@ -186,6 +203,16 @@ __global__ __launch_bounds__(kDecThreads) void exact_decode_kernel(const ExactDe
     for (int i = threadIdx.x; i < kG * kHeadDim; i += kDecThreads) {
       const int j = i / kHeadDim, d = i - j * kHeadDim;
       s_q[j][d] = bf16_bits_to_f32(a.q[b * a.q_row + (g * kG + j) * a.q_head + d]);
+    }
+    if (a.slot_mapping && threadIdx.x < 32) {  // append the token's rotated K and V rows of KV head g
+      const int64_t slot = a.slot_mapping[b * a.slot_stride];
+      const int64_t ctx = a.context_lens[b * a.ctx_stride];
+      if (ctx > 0 && slot >= 0 && slot < a.num_slots) {
+        const int piece = (threadIdx.x & 15) * 8;
+        const uint16_t* src = threadIdx.x < 16 ? a.k_new + b * a.k_row + g * a.k_head : a.v_new + b * a.v_row + g * a.v_head;
+        uint16_t* dst = (threadIdx.x < 16 ? a.key_pool : a.value_pool) + slot * row_elems + g * kHeadDim;
+        *reinterpret_cast<uint4*>(dst + piece) = *reinterpret_cast<const uint4*>(src + piece);
+      }
     }
   }
   // The barrier also orders the append before this workgroup's loads of the new token's block
@@ -410,6 +437,20 @@ __global__ __launch_bounds__(kDecThreads) void exact_decode_kernel(const ExactDe
   }
 }
 
+// The decode body called out of line from the mixed launch, so that its registers do not burden
+// the chunk rows' code of that kernel.
+template <int kG, int kWaves>
+__device__ __attribute__((noinline)) void exact_decode_rows(const ExactDecodeArgs& a, const int b, const int g,
+                                                            unsigned char* smem) {
+  exact_decode_body<kG, false, kWaves>(a, b, g, smem);
+}
+
+template <int kG, bool kPrologue>
+__global__ __launch_bounds__(kDecThreads) void exact_decode_kernel(const ExactDecodeArgs a) {
+  extern __shared__ __align__(16) unsigned char s_dec[];
+  exact_decode_body<kG, kPrologue, kDecWaves>(a, blockIdx.x, blockIdx.y, s_dec);
+}
+
 // ----------------------------------------------------------------------- prefill ---
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
@@ -446,19 +487,13 @@ struct ExactPrefillArgs {
   int32_t tiles;           // query tiles per row
   int32_t batch;           // rows
   int32_t groups;          // workgroups of these rows: tiles x kv_heads x batch
-  // Decode rows (a mixed step's single new tokens, padded_len 1): start_lens holds each row's
-  // context length including its token, so the history is the context minus one and a row with
-  // context 0 is padding; the token's K/V row of each KV head is appended to pool slot
-  // slot_mapping[b] (skipped when outside the pool).
-  int32_t decode_rows;
-  const int64_t* slot_mapping;
-  int64_t slot_stride;
 };
 
-// One launch serves up to two sets of rows (a mixed step's chunk rows and its decode rows): the
-// first a0.groups workgroups take a0, the rest a1.
+// One launch serves a mixed step: the first a.groups workgroups take the chunk rows of a, the rest
+// (one per decode row and KV head of d) run the exact decode body with this kernel's wavefronts --
+// the sums are exact, so the bits do not depend on how the keys are split.
 template <int kG>
-__global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPrefillArgs a0, const ExactPrefillArgs a1) {
+__global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPrefillArgs a, const ExactDecodeArgs d) {
   constexpr int kQ = kPfRows / kG;        // query positions per workgroup
   constexpr int kRows = kQ * kG;          // rows in use (<= 32)
   extern __shared__ __align__(16) unsigned char s_raw[];
@@ -466,33 +501,20 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   uint16_t* sT = reinterpret_cast<uint16_t*>(s_raw + kPfQBytes);             // [64][kKvRow]
   uint16_t* sC = reinterpret_cast<uint16_t*>(s_raw + kPfQBytes + kPfTileBytes);  // [cache_keys][32]
 
-  const bool second = static_cast<int>(blockIdx.x) >= a0.groups;  // uniform
-  const ExactPrefillArgs a = second ? a1 : a0;
-  const int lin = static_cast<int>(blockIdx.x) - (second ? a0.groups : 0);
+  if (static_cast<int>(blockIdx.x) >= a.groups) {  // uniform: a decode row
+    const int lin = static_cast<int>(blockIdx.x) - a.groups;
+    exact_decode_rows<kG, kPfWaves>(d, lin / d.kv_heads, lin % d.kv_heads, s_raw);
+    return;
+  }
+  const int lin = static_cast<int>(blockIdx.x);
   const int qt = lin % a.tiles;
   const int g = (lin / a.tiles) % a.kv_heads;
   const int b = lin / (a.tiles * a.kv_heads);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int L = a.padded_len;
-  int64_t clen, nh64;
-  if (a.decode_rows) {
-    const int64_t ctx = a.start_lens[b * a.lens_stride];
-    clen = ctx > 0 ? 1 : 0;
-    nh64 = ctx > 0 ? ctx - 1 : 0;
-    if (ctx > 0 && threadIdx.x < 32) {  // append the token's K and V rows of KV head g
-      const int64_t slot = a.slot_mapping[b * a.slot_stride];
-      if (slot >= 0 && slot < a.num_blocks * kBlockSize) {
-        const int piece = (threadIdx.x & 15) * 8;
-        const uint16_t* src = threadIdx.x < 16 ? a.k + b * a.k_row + g * a.k_head : a.v + b * a.v_row + g * a.v_head;
-        uint16_t* dst = (threadIdx.x < 16 ? a.key_pool : a.value_pool) + (slot * a.kv_heads + g) * kHeadDim;
-        *reinterpret_cast<uint4*>(dst + piece) = *reinterpret_cast<const uint4*>(src + piece);
-      }
-    }
-  } else {
-    clen = a.chunk_lens[b * a.lens_stride];
-    nh64 = a.start_lens[b * a.lens_stride];
-  }
+  int64_t clen = a.chunk_lens[b * a.lens_stride];
+  int64_t nh64 = a.start_lens[b * a.lens_stride];
   clen = clen < 0 ? 0 : (clen > L ? L : clen);
   const int pad = L - static_cast<int>(clen);
   nh64 = nh64 < 0 ? 0 : min(nh64, static_cast<int64_t>(a.max_hist_blocks) * kBlockSize);
@@ -558,18 +580,41 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
     }
   };
   // Scores of key lane of the staged tile against the wavefront's 8 rows.
+  // Rows of this wavefront with visible keys.  All of them except in edge tiles (padding rows,
+  // rows past L, the spare query slots of a decode row's tile), where the arithmetic of the dead
+  // rows is skipped (uniform branches; a dead row's results are never used).
+  bool all_live = true, any_live = false;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    all_live = all_live && kmax[k] >= 0;
+    any_live = any_live || kmax[k] >= 0;
+  }
   auto tile_scores = [&](float (&s)[8]) {
     double acc[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) acc[k] = 0.0;
-    for (int c = 0; c < kHeadDim / 8; ++c) {
-      double kd[8];
-      unpack8(*reinterpret_cast<const u32x4*>(sT + lane * kKvRow + 8 * c), kd);
+    if (all_live) {
+      for (int c = 0; c < kHeadDim / 8; ++c) {
+        double kd[8];
+        unpack8(*reinterpret_cast<const u32x4*>(sT + lane * kKvRow + 8 * c), kd);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const double* qr = sQ + (8 * w + k) * kHeadDim + 8 * c;
+        for (int k = 0; k < 8; ++k) {
+          const double* qr = sQ + (8 * w + k) * kHeadDim + 8 * c;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[k] = fma(qr[e], kd[e], acc[k]);
+          for (int e = 0; e < 8; ++e) acc[k] = fma(qr[e], kd[e], acc[k]);
+        }
+      }
+    } else if (any_live) {
+      for (int c = 0; c < kHeadDim / 8; ++c) {
+        double kd[8];
+        unpack8(*reinterpret_cast<const u32x4*>(sT + lane * kKvRow + 8 * c), kd);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (kmax[k] < 0) continue;
+          const double* qr = sQ + (8 * w + k) * kHeadDim + 8 * c;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[k] = fma(qr[e], kd[e], acc[k]);
+        }
       }
     }
 #pragma unroll
@@ -686,16 +731,32 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
     stage(true, kt);
     __syncthreads();
     const int kend = min(kPfKeys, nkeys - kt * kPfKeys);
-    for (int key = 0; key < kend; ++key) {
-      const uint4 packed = *reinterpret_cast<const uint4*>(probs + key * kPfRows + 8 * w);
-      const uint32_t pv = *reinterpret_cast<const uint32_t*>(sT + key * kKvRow + 2 * lane);
-      const double v0 = bf16_lo(pv), v1 = bf16_hi(pv);
-      const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
+    if (all_live) {
+      for (int key = 0; key < kend; ++key) {
+        const uint4 packed = *reinterpret_cast<const uint4*>(probs + key * kPfRows + 8 * w);
+        const uint32_t pv = *reinterpret_cast<const uint32_t*>(sT + key * kKvRow + 2 * lane);
+        const double v0 = bf16_lo(pv), v1 = bf16_hi(pv);
+        const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const double p = (k & 1) ? bf16_hi(words[k >> 1]) : bf16_lo(words[k >> 1]);
-        acc[k][0] = fma(p, v0, acc[k][0]);
-        acc[k][1] = fma(p, v1, acc[k][1]);
+        for (int k = 0; k < 8; ++k) {
+          const double p = (k & 1) ? bf16_hi(words[k >> 1]) : bf16_lo(words[k >> 1]);
+          acc[k][0] = fma(p, v0, acc[k][0]);
+          acc[k][1] = fma(p, v1, acc[k][1]);
+        }
+      }
+    } else if (any_live) {
+      for (int key = 0; key < kend; ++key) {
+        const uint4 packed = *reinterpret_cast<const uint4*>(probs + key * kPfRows + 8 * w);
+        const uint32_t pv = *reinterpret_cast<const uint32_t*>(sT + key * kKvRow + 2 * lane);
+        const double v0 = bf16_lo(pv), v1 = bf16_hi(pv);
+        const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (kmax[k] < 0) continue;
+          const double p = (k & 1) ? bf16_hi(words[k >> 1]) : bf16_lo(words[k >> 1]);
+          acc[k][0] = fma(p, v0, acc[k][0]);
+          acc[k][1] = fma(p, v1, acc[k][1]);
+        }
       }
     }
   }
@@ -728,9 +789,12 @@ template <int kG, bool kPrologue>
 int32_t launch_exact_decode(const ExactDecodeArgs& a, int32_t batch, hipStream_t s) {
   static std::once_flag once;
   static int32_t attr_rc = MI_OK;
-  std::call_once(once, [] { attr_rc = allow_lds(exact_decode_kernel<kG, kPrologue>, kDecCacheBytes, "mi_paged_decode_attention_exact"); });
+  using Lds = DecodeLds<kG, kDecWaves>;
+  std::call_once(once, [] {
+    attr_rc = allow_lds(exact_decode_kernel<kG, kPrologue>, Lds::kFixed + kDecCacheBytes, "mi_paged_decode_attention_exact");
+  });
   if (attr_rc != MI_OK) return attr_rc;
-  const size_t lds = static_cast<size_t>(a.cache_tokens) * kG * sizeof(uint16_t);
+  const size_t lds = Lds::kFixed + static_cast<size_t>(a.cache_tokens) * kG * sizeof(uint16_t);
   exact_decode_kernel<kG, kPrologue><<<dim3(batch, a.kv_heads), kDecThreads, lds, s>>>(a);
   return check_launch("mi_paged_decode_attention_exact");
 }
@@ -747,29 +811,34 @@ int32_t dispatch_exact_decode(const ExactDecodeArgs& a, int32_t batch, int group
 }
 
 template <int kG>
-int32_t launch_exact_prefill(const ExactPrefillArgs& a0, const ExactPrefillArgs& a1, const char* what, hipStream_t s) {
+int32_t launch_exact_prefill(const ExactPrefillArgs& a, const ExactDecodeArgs& d, int32_t decode_rows, const char* what,
+                             hipStream_t s) {
   static std::once_flag once;
   static int32_t attr_rc = MI_OK;
   std::call_once(once, [] { attr_rc = allow_lds(exact_prefill_kernel<kG>, kPfLdsBytes, "exact_prefill_kernel"); });
   if (attr_rc != MI_OK) return attr_rc;
-  if (a0.groups < 0 || a1.groups < 0 || static_cast<int64_t>(a0.groups) + a1.groups > 0x3fffffff)
+  const int64_t decode_groups = static_cast<int64_t>(decode_rows) * (decode_rows > 0 ? d.kv_heads : 0);
+  if (a.groups < 0 || static_cast<int64_t>(a.groups) + decode_groups > 0x3fffffff)
     return fail(MI_ERR_UNSUPPORTED, "%s: too many workgroups", what);
-  const int groups = a0.groups + a1.groups;
+  const int groups = a.groups + static_cast<int>(decode_groups);
   if (groups == 0) return ok();
-  const int32_t cache_keys = std::max(a0.groups > 0 ? a0.cache_keys : 0, a1.groups > 0 ? a1.cache_keys : 0);
-  const size_t lds = static_cast<size_t>(kPfQBytes) + kPfTileBytes + static_cast<size_t>(cache_keys) * kPfRows * 2;
-  exact_prefill_kernel<kG><<<groups, kPfThreads, lds, s>>>(a0, a1);
+  size_t lds = 0;
+  if (a.groups > 0) lds = static_cast<size_t>(kPfQBytes) + kPfTileBytes + static_cast<size_t>(a.cache_keys) * kPfRows * 2;
+  if (decode_groups > 0)
+    lds = std::max(lds, static_cast<size_t>(DecodeLds<kG, kPfWaves>::kFixed) +
+                            static_cast<size_t>(d.cache_tokens) * kG * sizeof(uint16_t));
+  exact_prefill_kernel<kG><<<groups, kPfThreads, lds, s>>>(a, d);
   return check_launch(what);
 }
 
-int32_t dispatch_exact_prefill(const ExactPrefillArgs& a0, const ExactPrefillArgs& a1, int group, const char* what,
-                               hipStream_t s) {
+int32_t dispatch_exact_prefill(const ExactPrefillArgs& a, const ExactDecodeArgs& d, int32_t decode_rows, int group,
+                               const char* what, hipStream_t s) {
   switch (group) {
-    case 1: return launch_exact_prefill<1>(a0, a1, what, s);
-    case 2: return launch_exact_prefill<2>(a0, a1, what, s);
-    case 4: return launch_exact_prefill<4>(a0, a1, what, s);
-    case 5: return launch_exact_prefill<5>(a0, a1, what, s);
-    default: return launch_exact_prefill<8>(a0, a1, what, s);
+    case 1: return launch_exact_prefill<1>(a, d, decode_rows, what, s);
+    case 2: return launch_exact_prefill<2>(a, d, decode_rows, what, s);
+    case 4: return launch_exact_prefill<4>(a, d, decode_rows, what, s);
+    case 5: return launch_exact_prefill<5>(a, d, decode_rows, what, s);
+    default: return launch_exact_prefill<8>(a, d, decode_rows, what, s);
   }
 }
 
@@ -937,7 +1006,7 @@ extern "C" int32_t mi_chunked_prefill_attention_exact(
   // Keys a row can see: its history (at most the table's) plus the chunk up to it.
   exact_rows(a, batch, padded_len, num_heads, num_kv_heads,
              static_cast<int64_t>(max_history_blocks) * kBlockSize + padded_len, scale);
-  const int32_t rc = dispatch_exact_prefill(a, ExactPrefillArgs{}, group, what, as_stream(stream));
+  const int32_t rc = dispatch_exact_prefill(a, ExactDecodeArgs{}, 0, group, what, as_stream(stream));
   return rc == MI_OK ? ok() : rc;
 }
 
@@ -998,7 +1067,7 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
     a.value_pool = static_cast<uint16_t*>(value_pool);
     a.num_blocks = num_blocks;
   };
-  ExactPrefillArgs a0{}, a1{};
+  ExactPrefillArgs a0{};
   if (chunks) {
     fill(a0, 0, prefill_width);
     a0.history = history_blocks;
@@ -1009,20 +1078,49 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
     a0.lens_stride = lens_stride;
     exact_rows(a0, prefill_rows, prefill_width, num_heads, num_kv_heads,
                static_cast<int64_t>(max_history_blocks) * kBlockSize + prefill_width, scale);
+  } else {
+    a0.kv_heads = num_kv_heads;
   }
+  // Decode rows: the exact decode body in its plain form (rotated queries), appending each row's
+  // rotated K/V first.
+  const int group = num_heads / num_kv_heads;
+  ExactDecodeArgs d{};
   if (decode_rows > 0) {
-    fill(a1, n, 1);
-    a1.history = block_tables;
-    a1.hist_stride = block_table_stride;
-    a1.max_hist_blocks = max_blocks;
-    a1.start_lens = context_lens;
-    a1.chunk_lens = context_lens;
-    a1.lens_stride = context_lens_stride;
-    a1.decode_rows = 1;
-    a1.slot_mapping = slot_mapping;
-    a1.slot_stride = slot_stride;
-    exact_rows(a1, decode_rows, 1, num_heads, num_kv_heads, static_cast<int64_t>(max_blocks) * kBlockSize + 1, scale);
+    d.out = static_cast<uint16_t*>(out) + n * out_tok_stride;
+    d.out_row = out_tok_stride;
+    d.q = static_cast<const uint16_t*>(query) + n * query_tok_stride;
+    d.q_row = query_tok_stride;
+    d.q_head = query_head_stride;
+    d.k_new = static_cast<const uint16_t*>(key) + n * key_tok_stride;
+    d.v_new = static_cast<const uint16_t*>(value) + n * value_tok_stride;
+    d.k_row = key_tok_stride;
+    d.v_row = value_tok_stride;
+    d.k_head = key_head_stride;
+    d.v_head = value_head_stride;
+    d.slot_mapping = slot_mapping;
+    d.slot_stride = slot_stride;
+    d.num_slots = num_blocks * kBlockSize;
+    d.key_pool = static_cast<uint16_t*>(key_pool);
+    d.value_pool = static_cast<uint16_t*>(value_pool);
+    d.num_blocks = num_blocks;
+    d.kv_heads = num_kv_heads;
+    d.block_tables = block_tables;
+    d.bt_stride = block_table_stride;
+    d.max_blocks = max_blocks;
+    d.context_lens = context_lens;
+    d.ctx_stride = context_lens_stride;
+    d.scale = scale;
+    const int64_t tokens = static_cast<int64_t>(max_blocks) * kBlockSize;
+    int64_t fixed = 0;
+    switch (group) {
+      case 1: fixed = DecodeLds<1, kPfWaves>::kFixed; break;
+      case 2: fixed = DecodeLds<2, kPfWaves>::kFixed; break;
+      case 4: fixed = DecodeLds<4, kPfWaves>::kFixed; break;
+      case 5: fixed = DecodeLds<5, kPfWaves>::kFixed; break;
+      default: fixed = DecodeLds<8, kPfWaves>::kFixed; break;
+    }
+    d.cache_tokens = fixed + tokens * group * 2 <= kPfLdsBytes ? static_cast<int32_t>(tokens) : 0;
   }
-  const int32_t rc = dispatch_exact_prefill(a0, a1, num_heads / num_kv_heads, what, as_stream(stream));
+  const int32_t rc = dispatch_exact_prefill(a0, d, decode_rows, group, what, as_stream(stream));
   return rc == MI_OK ? ok() : rc;
 }
