@@ -18,6 +18,13 @@
  * block used to right-pad block tables.
  *
  * Index metadata is int64, as the reference packs it on the host.
+ *
+ * Out-of-range indices, one rule for every entry point (the kernels never fault on them and never
+ * touch memory outside the pools): a block id outside [0, num_blocks) *read* through a block
+ * table or id list (attention histories, gather, pack) reads the null block 0; a *write* to a slot
+ * outside [0, num_blocks * block_size) or to a block id outside [0, num_blocks) (scatter, the
+ * decode appends, unpack) is skipped.  The reference's tensor indexing raises instead on ids >=
+ * num_blocks; the Python layer can do the same before each launch (data_plane.set_index_checks).
  */
 #ifndef MI_PAGED_H
 #define MI_PAGED_H
@@ -89,7 +96,7 @@ int32_t mi_reshape_and_cache(const void* const* key_src, const void* const* valu
  * Outputs are contiguous `[batch, num_gathered_blocks, block_bytes]`.  Whole blocks are
  * copied, including null block 0 and stale tails of recycled blocks, so the result is
  * bit-identical to the reference's advanced-index gather.  A block id outside
- * [0, num_blocks) yields a zero-filled block.
+ * [0, num_blocks) reads the null block 0.
  */
 int32_t mi_gather_blocks(const void* const* key_pools, const void* const* value_pools, int64_t num_blocks,
                          const int64_t* block_ids, int64_t block_id_stride, int32_t batch,
@@ -393,7 +400,7 @@ int32_t mi_argmax_rows(int64_t* out, const void* logits, int64_t rows, int32_t c
  * src/mini_infra/worker/paged_kv_cache.py:23-52.  Records of one call are contiguous.
  *
  * mi_pack_blocks:   records[i] = block block_ids[i] of every layer (ids out of [0, num_blocks)
- *                   give a zero record).
+ *                   read the null block 0).
  * mi_unpack_blocks: block block_ids[i] of every layer = records[i] (out-of-range ids skipped;
  *                   ids must be unique).
  * key_pools / value_pools: num_layers device pointers, each num_blocks * block_bytes.

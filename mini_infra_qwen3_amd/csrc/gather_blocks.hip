@@ -55,13 +55,7 @@ __global__ __launch_bounds__(kThreads) void gather_blocks_kernel(const GatherArg
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < a.pieces) {
-        if (valid) {
-          val[k] = load_vec<kNt>(src + p);
-        } else {
-          val[k] = V{};
-        }
-      }
+      if (p < a.pieces) val[k] = load_vec<kNt>(src + p);
     }
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {

@@ -51,8 +51,8 @@ struct RecordArgs {
   uint32_t pieces;  // block_bytes / sizeof(V)
 };
 
-// kPack: block -> record (an out-of-range block id writes a zero piece: nothing is read).
-// !kPack: record -> block (an out-of-range block id is skipped).
+// kPack: block -> record (an out-of-range block id reads the null block 0, as every read does).
+// !kPack: record -> block (an out-of-range block id is skipped, as every write is).
 template <typename V, bool kPack>
 __global__ __launch_bounds__(kThreads) void kv_records_kernel(const RecordArgs a) {
   const int64_t i = blockIdx.x;
@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kThreads) void kv_records_kernel(const RecordArgs a
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < a.pieces) val[k] = (!kPack || valid) ? load_vec<kNtLoad>(src + p) : V{};
+      if (p < a.pieces) val[k] = load_vec<kNtLoad>(src + p);
     }
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {

@@ -7,6 +7,7 @@ torch fallback, and a missing library raises ``NativeLibraryError``.
 
 from __future__ import annotations
 
+import os
 from collections.abc import Sequence
 
 import torch
@@ -26,6 +27,7 @@ __all__ = [
     "qk_norm_rope",
     "reshape_and_cache",
     "rms_norm",
+    "set_index_checks",
     "silu_mul",
     "unpack_blocks",
 ]
@@ -47,6 +49,33 @@ def _require_index(name: str, tensor: torch.Tensor, ndim: int) -> None:
 
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_INDEX_CHECKS = os.environ.get("MI_CHECK_INDICES", "") == "1"
+
+
+def set_index_checks(enabled: bool) -> bool:
+    """Turns the pre-launch index checks on or off; returns the previous setting.
+
+    On, every entry point raises ``IndexError`` -- as the reference's tensor indexing does for ids
+    >= num_blocks -- when a block id or slot it is given lies outside the pool (slot -1, the
+    "no write" marker of padding rows, is allowed), at the cost of one device reduction and host
+    synchronisation per index tensor.  Off (the default; ``MI_CHECK_INDICES=1`` in the environment
+    turns it on at import), the kernels' rule applies: reads through such ids read the null block
+    0, writes to such slots or blocks are skipped.
+    """
+    global _INDEX_CHECKS
+    previous, _INDEX_CHECKS = _INDEX_CHECKS, bool(enabled)
+    return previous
+
+
+def _check_range(name: str, ids: torch.Tensor, limit: int, allow_minus_one: bool = False) -> None:
+    if not _INDEX_CHECKS or ids.numel() == 0:
+        return
+    bad = (ids >= limit) | (ids < (-1 if allow_minus_one else 0))
+    if bool(bad.any()):
+        first = int(ids[bad].flatten()[0])
+        raise IndexError(f"{name}: index {first} is out of bounds for size {limit}")
 
 
 def reshape_and_cache(
@@ -111,6 +140,11 @@ def reshape_and_cache(
         index_stride = 1
     if num_tokens == 0:
         return
+    _check_range("slot_mapping", slot_mapping, num_blocks * block_size, allow_minus_one=True)
+    if token_rows is not None:
+        _check_range("token_rows", token_rows, k0.shape[0])
+    if token_positions is not None:
+        _check_range("token_positions", token_positions, k0.shape[2])
 
     lib = _native.load()
     rc = lib.mi_reshape_and_cache(
@@ -171,6 +205,7 @@ def gather_blocks(
                                  f"{tuple(t.shape)} {t.dtype}")
     if batch == 0 or nb == 0:
         return
+    _check_range("block_ids", block_ids, num_blocks)
     lib = _native.load()
     rc = lib.mi_gather_blocks(
         _native.pointer_array([t.data_ptr() for t in key_pools]),
@@ -258,6 +293,7 @@ def paged_decode_attention(
         raise ValueError(f"query head_dim {head_dim} != pool head_dim {pool_head_dim}")
     if block_tables.shape[0] != batch or context_lens.shape[0] != batch:
         raise ValueError("block_tables / context_lens batch differs from query batch")
+    _check_range("block_tables", block_tables, num_blocks)
     key_pool, value_pool, block_tables = _as_kernel_blocks(key_pool, value_pool, block_tables)
     num_blocks, block_size = key_pool.shape[:2]
     if block_tables.stride(1) != 1:
@@ -349,6 +385,8 @@ def paged_decode_attention_fused(
         raise ValueError("q / k / v / weights / pools have inconsistent head sizes")
     if block_tables.shape[0] != batch or context_lens.shape[0] != batch or slot_mapping.shape[0] != batch:
         raise ValueError("block_tables / context_lens / slot_mapping batch differs from the tokens'")
+    _check_range("block_tables", block_tables, key_pool.shape[0])
+    _check_range("slot_mapping", slot_mapping, key_pool.shape[0] * key_pool.shape[1], allow_minus_one=True)
     key_pool, value_pool, block_tables = _as_kernel_blocks(key_pool, value_pool, block_tables)
     num_blocks, block_size = key_pool.shape[:2]
     if block_tables.stride(1) != 1:
@@ -432,6 +470,7 @@ def chunked_prefill_attention(
         raise ValueError("pools must be contiguous bf16 with identical shapes")
     if history_blocks.shape[0] != batch or start_lens.shape[0] != batch or chunk_lens.shape[0] != batch:
         raise ValueError("history_blocks / start_lens / chunk_lens batch differs from query batch")
+    _check_range("history_blocks", history_blocks, key_pool.shape[0])
     key_pool, value_pool, history_blocks = _as_kernel_blocks(key_pool, value_pool, history_blocks)
     num_blocks, block_size = key_pool.shape[:2]
     if history_blocks.stride(1) != 1:
@@ -519,6 +558,9 @@ def mixed_paged_attention(
         raise ValueError("history_blocks / start_lens / chunk_lens must have one row per chunk row")
     if block_tables.shape[0] != decode_rows or slot_mapping.shape[0] != decode_rows:
         raise ValueError("block_tables / slot_mapping must have one row per decode row")
+    _check_range("history_blocks", history_blocks, key_pool.shape[0])
+    _check_range("block_tables", block_tables, key_pool.shape[0])
+    _check_range("slot_mapping", slot_mapping, key_pool.shape[0] * key_pool.shape[1], allow_minus_one=True)
     kp, vp, history_blocks = _as_kernel_blocks(key_pool, value_pool, history_blocks)
     _, _, block_tables = _as_kernel_blocks(key_pool, value_pool, block_tables)
     num_blocks, block_size = kp.shape[:2]
@@ -649,6 +691,7 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: to
             if not pool.is_contiguous() or pool.shape[-2:] != (num_kv_heads, head_dim):
                 raise ValueError(f"{name} must be contiguous [num_blocks, block_size, {num_kv_heads}, {head_dim}]")
         num_slots = key_pool.numel() // (num_kv_heads * head_dim)
+        _check_range("slot_mapping", slot_mapping, num_slots, allow_minus_one=True)
         rc = lib.mi_qk_norm_rope(q_out.data_ptr(), None, None, q2.data_ptr(), q2.stride(0), k2.data_ptr(),
                                  k2.stride(0), v2.data_ptr(), v2.stride(0), q_weight.data_ptr(), k_weight.data_ptr(),
                                  cos2.data_ptr(), sin2.data_ptr(), tokens, num_heads, num_kv_heads, head_dim,
@@ -718,7 +761,7 @@ def pack_blocks(key_pools: Sequence[torch.Tensor], value_pools: Sequence[torch.T
 
     Returns ``records [n, num_layers, 2, bs, H, D]`` with ``records[i, l, 0] = key_pools[l][block_ids[i]]``
     and ``records[i, l, 1] = value_pools[l][block_ids[i]]``: the wire / swap format.  block_ids:
-    ``[n]`` int64 on the pools' device; ids outside ``[0, num_blocks)`` give zero records.
+    ``[n]`` int64 on the pools' device; ids outside ``[0, num_blocks)`` read the null block 0.
     """
     pool0, device, block_bytes = _record_pools(key_pools, value_pools)
     _require_gpu("block_ids", block_ids, device)
@@ -733,6 +776,7 @@ def pack_blocks(key_pools: Sequence[torch.Tensor], value_pools: Sequence[torch.T
             raise ValueError(f"out: expected contiguous {shape} {pool0.dtype}, got {tuple(out.shape)} {out.dtype}")
     if block_ids.shape[0] == 0:
         return out
+    _check_range("block_ids", block_ids, pool0.shape[0])
     rc = _native.load().mi_pack_blocks(
         out.data_ptr(), _native.pointer_array([t.data_ptr() for t in key_pools]),
         _native.pointer_array([t.data_ptr() for t in value_pools]), pool0.shape[0], block_ids.data_ptr(),
@@ -756,6 +800,7 @@ def unpack_blocks(records: torch.Tensor, key_pools: Sequence[torch.Tensor], valu
                          f"{records.dtype}")
     if block_ids.shape[0] == 0:
         return
+    _check_range("block_ids", block_ids, pool0.shape[0])
     rc = _native.load().mi_unpack_blocks(
         _native.pointer_array([t.data_ptr() for t in key_pools]),
         _native.pointer_array([t.data_ptr() for t in value_pools]), pool0.shape[0], records.data_ptr(),

@@ -47,7 +47,8 @@ def pack_records(key_bits, value_bits, block_ids) -> np.ndarray:
 
     key_bits / value_bits: per-layer ``[num_blocks, bs, H, D]`` arrays.  Record i is block
     ``block_ids[i]`` of every layer: ``rec[i, l, 0] = key[l][id]``, ``rec[i, l, 1] = value[l][id]``;
-    an id outside ``[0, num_blocks)`` gives a zero record.  Explicit loops, one block at a time.
+    an id outside ``[0, num_blocks)`` reads the null block 0 (the library's rule for every read
+    through a block id).  Explicit loops, one block at a time.
     """
     layers = len(key_bits)
     nb = key_bits[0].shape[0]
@@ -55,7 +56,7 @@ def pack_records(key_bits, value_bits, block_ids) -> np.ndarray:
     for i, bid in enumerate(block_ids):
         bid = int(bid)
         if not 0 <= bid < nb:
-            continue
+            bid = 0
         for layer in range(layers):
             out[i, layer, 0] = key_bits[layer][bid]
             out[i, layer, 1] = value_bits[layer][bid]

@@ -52,13 +52,16 @@ def test_pack_matches_oracle(native_lib, layers, bs, heads, dim, dtype):
     assert np.array_equal(bits(records), closed_form.pack_records(keys, values, ids))
 
 
-def test_pack_of_out_of_range_ids_gives_zero_records(native_lib):
+def test_pack_of_out_of_range_ids_reads_the_null_block(native_lib):
     pool = random_pool(2, 10)
     ids = torch.tensor([3, -1, 10, 1 << 40, 9], dtype=torch.long, device=DEV)
     records = data_plane.pack_blocks([k for k, _ in pool.kv_pools], [v for _, v in pool.kv_pools], ids)
     keys, values = pool_bits(pool)
     assert np.array_equal(bits(records), closed_form.pack_records(keys, values, ids.tolist()))
-    assert not records[1:4].any()
+    zero = data_plane.pack_blocks([k for k, _ in pool.kv_pools], [v for _, v in pool.kv_pools],
+                                  torch.zeros(1, dtype=torch.long, device=DEV))
+    for i in (1, 2, 3):
+        assert torch.equal(records[i], zero[0])
 
 
 def test_unpack_matches_oracle_and_leaves_other_blocks(native_lib):
