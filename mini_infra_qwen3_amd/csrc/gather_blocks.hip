@@ -4,21 +4,26 @@
 // per layer `key_pool[block_ids]` materialised as `[batch, nb, block_size, H, D]`, for K and V of
 // every layer in one launch.  A block of one layer is contiguous in the pool (32 KiB for
 // 16 x 8 x 128 bf16) and contiguous in the output, so each workgroup streams one block with
-// 16-byte pieces: lane i of the group moves bytes [16 i, 16 i + 16) of every 4 KiB stripe,
-// all loads issued before the stores.
+// 16-byte pieces: lane i of the group moves bytes [16 i, 16 i + 16) of every 8 KiB stripe, two
+// stripes in flight, loads issued before the stores.  512 lanes x 2 pieces is the launch shape of
+// the best streaming copy measured on MI355X (bench.py's calibration kernels); it measured 2-4%
+// faster than 256 lanes x 8 pieces here.
 #include "mi_common.h"
 
 namespace mi {
 namespace {
 
 #ifndef MI_GATHER_UNROLL
-#define MI_GATHER_UNROLL 8
+#define MI_GATHER_UNROLL 2
 #endif
 #ifndef MI_GATHER_NT
 #define MI_GATHER_NT 1
 #endif
 
-constexpr int kThreads = 256;
+#ifndef MI_GATHER_THREADS
+#define MI_GATHER_THREADS 512
+#endif
+constexpr int kThreads = MI_GATHER_THREADS;
 constexpr int kUnroll = MI_GATHER_UNROLL;
 constexpr bool kNt = MI_GATHER_NT != 0;  // non-temporal pool loads and output stores
 
