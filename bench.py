@@ -781,14 +781,14 @@ def main() -> int:
         ceil = kernels["device_copy"]["ceiling"]
         log(f"device copy: {kernels['device_copy']['achieved_GBps']:.1f} GB/s; calibration streams: read+write "
             f"{ceil['read_write_GBps']:.0f}, read {ceil['read_GBps']:.0f}, write {ceil['write_GBps']:.0f} GB/s")
-        kernels["scatter"] = bench_scatter(max(args.steps // 2, 3), 2, device, "token", ceil["read_write_GBps"],
+        kernels["scatter"] = bench_scatter(max(args.steps, 10), 3, device, "token", ceil["read_write_GBps"],
                                            cpu=want_cpu)
         log(f"scatter: {kernels['scatter']['achieved_GBps']:.1f} GB/s "
             f"({100 * kernels['scatter']['frac_of_copy_ceiling']:.1f}% of the copy ceiling)")
-        kernels["scatter_head_major_source"] = bench_scatter(max(args.steps // 2, 3), 2, device, "head",
+        kernels["scatter_head_major_source"] = bench_scatter(max(args.steps, 10), 3, device, "head",
                                                              ceil["read_write_GBps"])
         log(f"scatter, head-major source: {kernels['scatter_head_major_source']['achieved_GBps']:.1f} GB/s")
-        kernels["gather"] = bench_gather(max(args.steps // 4, 3), 1, device, ceil["read_write_GBps"], cpu=want_cpu)
+        kernels["gather"] = bench_gather(max(args.steps // 2, 6), 2, device, ceil["read_write_GBps"], cpu=want_cpu)
         log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s "
             f"({100 * kernels['gather']['frac_of_copy_ceiling']:.1f}% of the copy ceiling)")
         kernels["chunked_prefill"] = bench_prefill(max(args.steps // 4, 3), 3, device, cpu=want_cpu)
