@@ -17,13 +17,16 @@
 //    element-size pieces; used by small shapes only.
 #include "mi_common.h"
 
-// Measured on MI355X (28-layer prefill store, 40k tokens): 4 tokens per workgroup with 2 loads in
-// flight per lane moves 5.75 TB/s; 32 tokens with 8 in flight moved 5.09 TB/s, 8 tokens 5.29.
+// Measured on MI355X (28-layer prefill store, 40k tokens, token-major source rows; three repetitions
+// in one process): 2 tokens per workgroup with one load per lane in flight moves 5.85-5.92 TB/s;
+// 2 tokens with 2 in flight 5.79-5.83, 4 with 2 5.57-5.75, 4 with 4 5.35-5.63, 8 with 2 or 4
+// 5.13-5.50, 16 with 4 5.22-5.51, 1 token 5.37-5.50.  Many small workgroups keep the most
+// independent 2 KiB row copies in flight.
 #ifndef MI_SCATTER_TOKENS_PER_GROUP
-#define MI_SCATTER_TOKENS_PER_GROUP 4
+#define MI_SCATTER_TOKENS_PER_GROUP 2
 #endif
 #ifndef MI_SCATTER_UNROLL
-#define MI_SCATTER_UNROLL 2
+#define MI_SCATTER_UNROLL 1
 #endif
 #ifndef MI_SCATTER_NT
 #define MI_SCATTER_NT 1
