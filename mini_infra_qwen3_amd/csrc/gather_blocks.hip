@@ -3,11 +3,13 @@
 // Behaviour of PagedKVCachePool.gather_blocks (src/mini_infra/worker/paged_kv_cache.py:54-72):
 // per layer `key_pool[block_ids]` materialised as `[batch, nb, block_size, H, D]`, for K and V of
 // every layer in one launch.  A block of one layer is contiguous in the pool (32 KiB for
-// 16 x 8 x 128 bf16) and contiguous in the output, so each workgroup streams one block with
-// 16-byte pieces: lane i of the group moves bytes [16 i, 16 i + 16) of every 8 KiB stripe, two
-// stripes in flight, loads issued before the stores.  512 lanes x 2 pieces is the launch shape of
-// the best streaming copy measured on MI355X (bench.py's calibration kernels); it measured 2-4%
-// faster than 256 lanes x 8 pieces here.
+// 16 x 8 x 128 bf16) and contiguous in the output, so four workgroups of 256 lanes stream one
+// block, a contiguous 8 KiB quarter each, with 16-byte pieces: lane i moves bytes [16 i, 16 i + 16)
+// of each 4 KiB stripe, both stripes in flight, loads issued before the stores.  Measured on
+// MI355X (config 4's history gather, three repetitions in one process): 6.15-6.18 TB/s, against
+// 5.87-5.98 for 4 KiB workgroups with one piece in flight, 5.90-6.17 for 16 KiB workgroups of 512
+// lanes, 5.68-6.01 for one 32 KiB workgroup per block (512 lanes x 2) and 5.49-5.69 for 256 lanes
+// x 8.
 #include "mi_common.h"
 
 namespace mi {
@@ -21,8 +23,12 @@ namespace {
 #endif
 
 #ifndef MI_GATHER_THREADS
-#define MI_GATHER_THREADS 512
+#define MI_GATHER_THREADS 256
 #endif
+#ifndef MI_GATHER_SPLIT
+#define MI_GATHER_SPLIT 4
+#endif
+constexpr int kSplit = MI_GATHER_SPLIT;  // workgroups per block: each copies a contiguous 1 / kSplit
 constexpr int kThreads = MI_GATHER_THREADS;
 constexpr int kUnroll = MI_GATHER_UNROLL;
 constexpr bool kNt = MI_GATHER_NT != 0;  // non-temporal pool loads and output stores
@@ -40,10 +46,12 @@ struct GatherArgs {
   uint32_t pieces;        // block_bytes / sizeof(V)
 };
 
-// grid: x = row * nb + j (one gathered block), y = layer, z = 0 for K / 1 for V.
+// grid: x = (row * nb + j) * kSplit + part (part of one gathered block), y = layer, z = 0 for K / 1
+// for V.
 template <typename V>
 __global__ __launch_bounds__(kThreads) void gather_blocks_kernel(const GatherArgs a) {
-  const uint32_t flat = blockIdx.x;
+  const uint32_t flat = blockIdx.x / kSplit;
+  const uint32_t part = blockIdx.x - flat * kSplit;
   const uint32_t row = flat / a.nb;
   const uint32_t j = flat - row * a.nb;
   const int layer = blockIdx.y;
@@ -55,17 +63,20 @@ __global__ __launch_bounds__(kThreads) void gather_blocks_kernel(const GatherArg
   V* dst = reinterpret_cast<V*>((is_value ? a.value_out[layer] : a.key_out[layer]) +
                                 static_cast<int64_t>(flat) * a.block_bytes);
 
-  for (uint32_t base = 0; base < a.pieces; base += kThreads * kUnroll) {
+  const uint32_t per_part = (a.pieces + kSplit - 1) / kSplit;
+  const uint32_t p0 = part * per_part;
+  const uint32_t p1 = min(a.pieces, p0 + per_part);
+  for (uint32_t base = p0; base < p1; base += kThreads * kUnroll) {
     V val[kUnroll];
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < a.pieces) val[k] = load_vec<kNt>(src + p);
+      if (p < p1) val[k] = load_vec<kNt>(src + p);
     }
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < a.pieces) store_vec<kNt>(dst + p, val[k]);
+      if (p < p1) store_vec<kNt>(dst + p, val[k]);
     }
   }
 }
@@ -86,7 +97,7 @@ extern "C" int32_t mi_gather_blocks(const void* const* key_pools, const void* co
   if (block_id_stride < num_gathered_blocks)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_gather_blocks: block_id_stride %lld < num_gathered_blocks %d",
                 static_cast<long long>(block_id_stride), num_gathered_blocks);
-  if (static_cast<int64_t>(batch) * num_gathered_blocks > 0x7fffffff)
+  if (static_cast<int64_t>(batch) * num_gathered_blocks * kSplit > 0x7fffffff)
     return fail(MI_ERR_UNSUPPORTED, "mi_gather_blocks: too many blocks in one call");
 
   GatherArgs a{};
@@ -116,7 +127,7 @@ extern "C" int32_t mi_gather_blocks(const void* const* key_pools, const void* co
       a.key_out[l] = static_cast<char*>(key_out[l0 + l]);
       a.value_out[l] = static_cast<char*>(value_out[l0 + l]);
     }
-    dim3 grid(static_cast<uint32_t>(batch) * num_gathered_blocks, nl, 2);
+    dim3 grid(static_cast<uint32_t>(batch) * num_gathered_blocks * kSplit, nl, 2);
     if (piece == 16)
       gather_blocks_kernel<u32x4><<<grid, kThreads, 0, s>>>(a);
     else if (piece == 4)

@@ -21,8 +21,10 @@ struct Variant {
 };
 
 constexpr Variant kVariants[] = {
-    {256, 4, 64 << 10}, {512, 4, 64 << 10}, {512, 8, 128 << 10}, {1024, 4, 128 << 10},
-    {256, 8, 256 << 10}, {512, 8, 256 << 10}, {1024, 8, 512 << 10}, {512, 2, 32 << 10},
+    {256, 1, 4 << 10},   {256, 2, 8 << 10},   {512, 1, 8 << 10},    {256, 4, 16 << 10},
+    {512, 2, 16 << 10},  {512, 2, 32 << 10},  {256, 4, 64 << 10},   {512, 4, 64 << 10},
+    {512, 8, 128 << 10}, {1024, 4, 128 << 10}, {256, 8, 256 << 10}, {512, 8, 256 << 10},
+    {1024, 8, 512 << 10},
 };
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
@@ -127,6 +129,7 @@ extern "C" int32_t calib_stream(int32_t shape, void* dst, const void* src, void*
   else if (shape == 1) read_kernel<N><<<grid, v.threads, 0, s>>>(r, k, pieces, span_pieces); \
   else write_kernel<N><<<grid, v.threads, 0, s>>>(d, pieces, span_pieces);
   switch (v.in_flight) {
+    case 1: CALIB_LAUNCH(1) break;
     case 2: CALIB_LAUNCH(2) break;
     case 4: CALIB_LAUNCH(4) break;
     default: CALIB_LAUNCH(8) break;
