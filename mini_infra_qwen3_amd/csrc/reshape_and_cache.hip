@@ -21,7 +21,9 @@
 // in one process): 2 tokens per workgroup with one load per lane in flight moves 5.85-5.92 TB/s;
 // 2 tokens with 2 in flight 5.79-5.83, 4 with 2 5.57-5.75, 4 with 4 5.35-5.63, 8 with 2 or 4
 // 5.13-5.50, 16 with 4 5.22-5.51, 1 token 5.37-5.50.  Many small workgroups keep the most
-// independent 2 KiB row copies in flight.
+// independent 2 KiB row copies in flight.  Wider workgroups holding several tokens side by side
+// (MI_SCATTER_THREADS) measured slower on another machine: 512 lanes x 2 tokens 5.43-5.44 TB/s,
+// x 4 tokens 5.84-5.92, 1024 x 4 5.40-5.57, against 6.04-6.09 for 256 x 2.
 #ifndef MI_SCATTER_TOKENS_PER_GROUP
 #define MI_SCATTER_TOKENS_PER_GROUP 2
 #endif
@@ -35,7 +37,10 @@
 namespace mi {
 namespace {
 
-constexpr int kThreads = 256;
+#ifndef MI_SCATTER_THREADS
+#define MI_SCATTER_THREADS 256
+#endif
+constexpr int kThreads = MI_SCATTER_THREADS;
 constexpr int kTokensPerGroup = MI_SCATTER_TOKENS_PER_GROUP;
 constexpr int kUnroll = MI_SCATTER_UNROLL;
 constexpr bool kNt = MI_SCATTER_NT != 0;  // non-temporal source loads and pool stores
@@ -100,8 +105,13 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_rows(const Scatter
   const char* value_src = a.value_src[layer];
   char* key_pool = a.key_pool[layer];
   char* value_pool = a.value_pool[layer];
+  // Lanes per token: all of them when a token has at least kThreads pieces, else one piece each
+  // and kThreads / per_token tokens side by side.
   const uint32_t per_token = 2u * a.chunks_per_row;
-  for (uint32_t c = threadIdx.x; c < per_token; c += kThreads) {
+  const uint32_t lanes = per_token < kThreads ? per_token : kThreads;
+  const int side = static_cast<int>(kThreads / lanes);
+  const int t_lane = static_cast<int>(threadIdx.x / lanes);
+  for (uint32_t c = threadIdx.x % lanes; c < per_token; c += lanes) {
     // Fixed piece of this lane: K or V, head h, 16-byte column j.
     const bool is_value = c >= a.chunks_per_row;
     const uint32_t w = is_value ? c - a.chunks_per_row : c;
@@ -110,16 +120,16 @@ __global__ __launch_bounds__(kThreads) void reshape_and_cache_rows(const Scatter
     const char* src = (is_value ? value_src : key_src) + h * (is_value ? a.value_head : a.key_head) + j * 16u;
     char* dst = (is_value ? value_pool : key_pool) + w * 16u;
     const int64_t* s_off = is_value ? s_value : s_key;
-    for (int t0 = 0; t0 < ntok; t0 += kUnroll) {
+    for (int t0 = t_lane; t0 < ntok; t0 += side * kUnroll) {
       u32x4 val[kUnroll];
 #pragma unroll
       for (int k = 0; k < kUnroll; ++k) {
-        const int t = t0 + k;
+        const int t = t0 + k * side;
         if (t < ntok && s_slot[t] >= 0) val[k] = load_vec<kNt>(reinterpret_cast<const u32x4*>(src + s_off[t]));
       }
 #pragma unroll
       for (int k = 0; k < kUnroll; ++k) {
-        const int t = t0 + k;
+        const int t = t0 + k * side;
         if (t < ntok && s_slot[t] >= 0) store_vec<kNt>(reinterpret_cast<u32x4*>(dst + s_slot[t] * a.row_bytes), val[k]);
       }
     }
@@ -218,7 +228,7 @@ extern "C" int32_t mi_reshape_and_cache(const void* const* key_src, const void* 
   a.chunks_per_row = a.chunks_per_head * num_kv_heads;
   if (2ull * a.chunks_per_row * kGenericTokensPerGroup >= (1ull << 31))
     return fail(MI_ERR_UNSUPPORTED, "mi_reshape_and_cache: row of %u bytes too large", a.row_bytes);
-  const bool rows_kernel = wide && (2u * a.chunks_per_row) % kThreads == 0;
+  const bool rows_kernel = wide && ((2u * a.chunks_per_row) % kThreads == 0 || kThreads % (2u * a.chunks_per_row) == 0);
   // Few tokens (a decode append) spread one per workgroup over the CUs; many tokens (a prompt)
   // go kTokensPerGroup per workgroup so each lane keeps kUnroll loads in flight.
   int64_t per_group = kGenericTokensPerGroup;
