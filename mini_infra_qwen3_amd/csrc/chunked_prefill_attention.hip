@@ -20,21 +20,22 @@
 //    is odd, the second half of its last pair repeats the group's last head and writes nothing.
 //  * KV tiles of 64 keys: history tiles first (pool blocks through the block table -- the
 //    gather is fused, nothing is materialised), then chunk tiles up to the causal limit.
-//    K is staged row-major (288-byte rows), V transposed (V^T) in double-buffered LDS; the loads
-//    of the next two tiles are in flight in registers while the current one is multiplied.
+//    K and V tiles go from memory straight into double-buffered LDS (global_load_lds_dwordx4, no
+//    registers on the way), row-major with 256-byte rows whose 16-byte chunks are XOR-swizzled by
+//    the row; tile t + 1 is in flight while tile t is multiplied.
 //  * S^T = K Q^T: A = K rows from LDS, B = Q^T from registers (loaded once), C lane layout =
 //    (query = lane % 16, keys 4 (lane / 16) + i).  Each query's softmax state lives in the
 //    lanes of its column; the row max needs two cross-lane steps, the row sum is deferred.
 //  * O^T = V^T P^T: the probabilities of a 32-key step are already in the B-operand lanes if
-//    the MFMA's k index is read as key 16 (k' / 4) + 4 (lane / 16) + k' % 4; V^T rows in LDS
-//    hold the keys in that order, so the A operand is one 16-byte read.
+//    the MFMA's k index is read as key 16 (k' / 4) + 4 (lane / 16) + k' % 4.  The A operand (V^T)
+//    comes from the row-major V tile by two transposing reads (ds_read_b64_tr_b16), 4 keys each.
 //  * Softmax and accumulation are fp32 with lazy rescaling of the running max as in the decode
 //    kernel.  Scores keep the reference's bf16 rounding points (bf16 product, then bf16 product
 //    with the scale), one packed bf16 convert per rounding: for N(0,1) inputs those roundings
 //    move logits by ~1e-2, so dropping them would leave the 2e-2 parity band.
-//  * Measured on MI355X, MFMA and VALU work of the same SIMD mostly add up rather than overlap,
-//    so the time per tile is about MFMA + VALU: the score roundings, exponentials and converts
-//    are the VALU share.
+//  * The two waves of a SIMD run in step (one workgroup barrier per tile), so per tile the
+//    matrix work, the score roundings, exponentials and converts, and the LDS operand latency
+//    largely add up.
 #include <algorithm>
 #include <initializer_list>
 
@@ -57,25 +58,10 @@ constexpr int kNt = MI_PREFILL_NT;                        // 16-query MFMA colum
 constexpr int kQPerWave = 16 * kNt;
 constexpr int kQTile = kQPerWave * kWavesPerHead;         // queries per head per workgroup
 constexpr int kWavesPerSimd = kNt == 1 ? 4 : 2;           // occupancy the register budget is set for
-#ifndef MI_PREFILL_AHEAD
-#define MI_PREFILL_AHEAD 2
-#endif
-constexpr int kAhead = MI_PREFILL_AHEAD;                  // K/V tiles in flight in registers (1 or 2)
-static_assert(kAhead == 1 || kAhead == 2, "one or two tiles ahead");
 constexpr int kKTile = 64;                 // keys per KV tile
-#ifndef MI_PREFILL_K_PAD
-#define MI_PREFILL_K_PAD 16
-#endif
-#ifndef MI_PREFILL_V_PAD
-#define MI_PREFILL_V_PAD 16
-#endif
-constexpr int kKStride = kHeadDim + MI_PREFILL_K_PAD;  // LDS row of K (elements): 288 B
-constexpr int kVStride = kKTile + MI_PREFILL_V_PAD;    // LDS row of V^T (elements): 160 B, 16-byte aligned
 constexpr int kThreads = 64 * kGroup * kWavesPerHead;    // one workgroup per CU at 4 waves per head
-constexpr int kKeysPerPass = kThreads / 16;               // K rows one pass of 16-byte pieces covers
-constexpr int kKPieces = kKTile / kKeysPerPass;           // K pieces per thread and tile
-constexpr int kVPieces = kKTile / (2 * kKeysPerPass);     // V key pairs per thread and tile
-static_assert(kKPieces * kKeysPerPass == kKTile && kVPieces * 2 * kKeysPerPass == kKTile, "tile cover");
+constexpr int kSpans = kKTile / 4;                       // 1 KiB LDS spans (4 rows of 256 B) per K or V tile
+static_assert(kSpans % (kThreads / 64) == 0, "every wave moves the same number of spans");
 constexpr int kMaxHistoryBlocks = 16384;   // history table staged in LDS: 64 KiB at most (256k tokens)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;
@@ -134,21 +120,14 @@ __device__ __forceinline__ void reference_scores(f32x4& v, float scale) {
   for (int i = 0; i < 4; ++i) v[i] = round_bf16_hi(round_bf16_hi(v[i]) * scale);
 }
 
-// Column (element) of key `key` in V^T row `dim`: rows of 32 dims are rotated by 8 keys (4 dwords)
-// per group, so that the transposing stores -- each thread writes dims 8 x .. 8 x + 7 of two keys,
-// x = lane % 16 -- spread over all banks (32 or 64 banks of 4 bytes) instead of 8 of them, while
-// the PV operand reads (8 consecutive keys of one dim) stay contiguous and conflict-free.
-__device__ __forceinline__ int vcol(int dim, int key) { return (key + 8 * (dim >> 5)) & (kKTile - 1); }
-// Position of key k of a tile in its V^T row (before the vcol rotation): the 8 keys one lane group
-// feeds to a PV MFMA (16 (k' / 4) + 4 (lane / 16) + k' % 4 within each 32-key half) sit next to
-// each other, so the A operand is one 16-byte read; key pairs (2 j, 2 j + 1) stay adjacent.
-__device__ __forceinline__ int vpos(int key) {
-  const int k = key & 31;
-  return (key & 32) + 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3);
-}
-
-__device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint32_t sel) {
-  return __builtin_amdgcn_perm(hi_src, lo_src, sel);
+// One 16-byte-per-lane load straight into LDS: lane i writes bytes [16 i, 16 i + 16) of the
+// 1 KiB span at LDS address lds (wave-uniform, passed in M0; one wait state between the M0 write
+// and the load).  Issued by inline assembly: the compiler's own form ties every later LDS read to
+// the completion of all such loads (it cannot tell the two tile buffers apart), which would wait
+// for tile t + 1 before reading tile t.  The compiler does not see these loads, so the kernel waits
+// for them itself (vmcnt(0) before each tile barrier) and sets M0 nowhere else.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds) : "memory");
 }
 
 // One launch serves up to two sets of rows (a mixed step's chunk rows and its decode rows): the
@@ -156,8 +135,9 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi_src, uint32_t lo_src, uint3
 template <int kKvHeads>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kernel(const PrefillArgs a0,
                                                                                    const PrefillArgs a1) {
-  __shared__ __align__(16) uint16_t sK[2][kKTile * kKStride];
-  __shared__ __align__(16) uint16_t sV[2][kHeadDim * kVStride];
+  // K and V tiles row-major, 256-byte rows, 16-byte chunk c of row r stored at chunk c ^ (r % 16).
+  __shared__ __align__(1024) uint16_t sK[2][kKTile * kHeadDim];
+  __shared__ __align__(1024) uint16_t sV[2][kKTile * kHeadDim];
   extern __shared__ int s_hblk[];  // [ceil(nh / 16)] history block ids of this row (dynamic LDS)
 
   const bool second = static_cast<int>(blockIdx.x) >= a0.groups;  // uniform
@@ -260,83 +240,66 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   const int c_hi = last_q / kKTile;
   const int n_tiles = n_hist_tiles + (c_hi - c_lo + 1);
 
-  // ---- tile loader.  Thread tid owns K pieces (key kKeysPerPass kk + tid / 16, dims 8 (tid % 16)
-  // .. +8), kk < kKPieces, and V key pairs (keys 2 kKeysPerPass kk + 2 (tid / 16) + {0, 1}, same
-  // dims), kk < kVPieces.  In a history tile each piece lies in pool block (its first key) / 16 of
-  // the tile -- uniform across a wavefront, whose 64 lanes span 4 consecutive keys (or pairs) of
-  // one block -- read from LDS where the workgroup staged its history table once.  Every load
-  // reads valid memory: block indices are clamped to the last history block and chunk positions
-  // to L - 1; keys past the context are masked later.
-  const int tkey = tid >> 4;
-  const int tdim = (tid & 15) * 8;
+  // ---- tile loads straight into LDS (global_load_lds_dwordx4: lane i of an instruction writes
+  // bytes [16 i, 16 i + 16) of a 1 KiB LDS span).  A tile is kSpans such spans of 4 rows for K and
+  // as many for V; wave w moves spans [kSpansPerWave w, kSpansPerWave (w + 1)) of each.  Lane i of
+  // span m fetches row 4 m + i / 16, global chunk (i % 16) ^ (row % 16), so that the chunk lands at
+  // its swizzled place: the 16 lanes of an MFMA operand read (16 rows, one logical chunk) then hit
+  // 16 different chunk positions, i.e. all banks.  In a history tile the four rows of a span lie in
+  // one pool block (uniform), read from the history table the workgroup staged in LDS; chunk rows
+  // past L - 1 read row L - 1 (their keys are masked).
   const int nhb = (nh + kBlockSize - 1) / kBlockSize;
   for (int i = tid; i < nhb; i += kThreads) {
     const int64_t x = a.history_blocks[b * a.history_stride + i];
     s_hblk[i] = (x < 0 || x >= a.num_blocks) ? 0 : static_cast<int>(x);
   }
   constexpr int64_t kBlkElems = static_cast<int64_t>(kBlockSize) * kKvHeads * kHeadDim;
-  // Per-lane parts of the load addresses (elements, 32-bit): the uniform parts -- the pool block
-  // of a history piece, the first chunk row of a pass -- are added as one scalar base per load.
-  const uint32_t k_hist_off = static_cast<uint32_t>(((tkey % kBlockSize) * kKvHeads + g) * kHeadDim + tdim);
-  const int voff = (2 * tkey) % kBlockSize;
-  const uint32_t v_hist_off0 = static_cast<uint32_t>((voff * kKvHeads + g) * kHeadDim + tdim);
-  const uint32_t v_hist_off1 = v_hist_off0 + kKvHeads * kHeadDim;
+  constexpr int kSpansPerWave = kSpans / (kThreads / 64);
+  const int drow = lane >> 4;
+  const int dchunk = lane & 15;
   const uint16_t* k_rows = a.key + b * a.k_row + g * a.k_head;
   const uint16_t* v_rows = a.value + b * a.v_row + g * a.v_head;
   const uint32_t k_tok = static_cast<uint32_t>(a.k_tok);  // < 2^24, checked by the entry point
   const uint32_t v_tok = static_cast<uint32_t>(a.v_tok);
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 #define MI_HIST_BLOCK(T, KEY) \
   __builtin_amdgcn_readfirstlane(s_hblk[min((T) * (kKTile / kBlockSize) + (KEY) / kBlockSize, max(nhb - 1, 0))])
-  // Loads of tile t, branch-free: each piece is a scalar base (pool block, or the chunk row of the
-  // pass clamped to L - 1) plus a 32-bit lane offset, selected on the uniform history/chunk test,
-  // so the compiler can count them and wait for exactly the pieces a store needs.  Chunk rows past
-  // L - 1 read row L - 1 (their keys are masked).
-  auto load_tile = [&](const int t, u32x4 (&kr)[kKPieces], u32x4 (&vr)[kVPieces][2]) {
+  auto dma_tile = [&](const int t, const int buf) {
     const bool hist = t < n_hist_tiles;
     const int key0 = (c_lo + t - n_hist_tiles) * kKTile;
 #pragma unroll
-    for (int kk = 0; kk < kKPieces; ++kk) {
-      const int row = kKeysPerPass * kk;
-      const int kc = min(key0 + row, L - 1);
-      const uint32_t chunk_off = __umul24(static_cast<uint32_t>(min(tkey, L - 1 - kc)), k_tok) + tdim;
-      const uint16_t* base = hist ? a.key_pool + static_cast<int64_t>(MI_HIST_BLOCK(t, row + tkey)) * kBlkElems
-                                  : k_rows + static_cast<int64_t>(kc) * a.k_tok;
-      const uint32_t off = hist ? k_hist_off : chunk_off;
-      kr[kk] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + 2u * off);
-    }
-#pragma unroll
-    for (int kk = 0; kk < kVPieces; ++kk) {
-      const int row = 2 * kKeysPerPass * kk;
-      const int vc = min(key0 + row, L - 1);
-      const uint16_t* base = hist ? a.value_pool + static_cast<int64_t>(MI_HIST_BLOCK(t, row + 2 * tkey)) * kBlkElems
-                                  : v_rows + static_cast<int64_t>(vc) * a.v_tok;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t chunk_off = __umul24(static_cast<uint32_t>(min(2 * tkey + e, L - 1 - vc)), v_tok) + tdim;
-        const uint32_t off = hist ? (e ? v_hist_off1 : v_hist_off0) : chunk_off;
-        vr[kk][e] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + 2u * off);
+    for (int i = 0; i < kSpansPerWave; ++i) {
+      const int m = kSpansPerWave * w + i;
+      const int r = 4 * m + drow;
+      const uint32_t c8 = static_cast<uint32_t>((dchunk ^ (r & 15)) * 8);
+      const uint16_t* ksrc;
+      const uint16_t* vsrc;
+      if (hist) {
+        const int64_t blk = MI_HIST_BLOCK(t, 4 * m);
+        const uint32_t off = static_cast<uint32_t>(((r & 15) * kKvHeads + g) * kHeadDim) + c8;
+        ksrc = a.key_pool + blk * kBlkElems + off;
+        vsrc = a.value_pool + blk * kBlkElems + off;
+      } else {
+        const uint32_t kc = static_cast<uint32_t>(min(key0 + r, L - 1));
+        ksrc = k_rows + (__umul24(kc, k_tok) + c8);
+        vsrc = v_rows + (__umul24(kc, v_tok) + c8);
       }
+      dma16(ksrc, __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(&sK[buf][m * 512])))));
+      dma16(vsrc, __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(&sV[buf][m * 512])))));
     }
   };
-
-#define MI_STORE_TILE(BUF, KR, VR)                                                                                 \
-  do {                                                                                                         \
-    const int buf_ = (BUF);                                                                                    \
-    _Pragma("unroll") for (int kk = 0; kk < kKPieces; ++kk)                                                    \
-        *reinterpret_cast<u32x4*>(&sK[buf_][(kKeysPerPass * kk + tkey) * kKStride + tdim]) = KR[kk];         \
-    _Pragma("unroll") for (int kk = 0; kk < kVPieces; ++kk) {                                                  \
-      const int key = 2 * kKeysPerPass * kk + 2 * tkey;                                                        \
-      const uint32_t x[4] = {VR[kk][0][0], VR[kk][0][1], VR[kk][0][2], VR[kk][0][3]};                  \
-      const uint32_t y[4] = {VR[kk][1][0], VR[kk][1][1], VR[kk][1][2], VR[kk][1][3]};                  \
-      _Pragma("unroll") for (int d2 = 0; d2 < 4; ++d2) {                                                       \
-        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2) * kVStride + vcol(tdim, vpos(key))]) =          \
-            perm(y[d2], x[d2], 0x05040100u);                                                                   \
-        *reinterpret_cast<uint32_t*>(&sV[buf_][(tdim + 2 * d2 + 1) * kVStride + vcol(tdim, vpos(key))]) =      \
-            perm(y[d2], x[d2], 0x07060302u);                                                                   \
-      }                                                                                                        \
-    }                                                                                                          \
-  } while (0)
+  // Per-lane LDS byte offsets of the MFMA operands.  K (A of S^T = K Q^T): row 16 mt + ql, global
+  // chunk 4 ks + gq.  V (A of O^T = V^T P^T, by transposing 8-byte reads): lane L of a 16-lane group
+  // addresses row k0 + L / 4, dims 16 dt + 4 (L % 4) .. + 3, and receives dim 16 dt + L of rows
+  // k0 .. k0 + 3; k0 = 32 ks2 + 4 gq, then + 16, gives the 8 keys in the MFMA's k order.
+  uint32_t k_off[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) k_off[ks] = ql * 256 + (((4 * ks + gq) ^ ql) & 15) * 16;
+  const int vr = 4 * gq + (ql >> 2);
+  uint32_t v_off[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) v_off[dt] = vr * 256 + (((2 * dt + ((ql >> 1) & 1)) ^ vr) & 15) * 16 + (ql & 1) * 8;
 
   // oacc[0..7]: O^T dims 16 dt + 4 gq + i; oacc[8]: the softmax row sums.  Tile 8 multiplies P^T by
   // a constant A with ones in rows 0, 4, 8, 12: its rows 0, 4, 8, 12 -- element 0 of every lane group
@@ -355,21 +318,19 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   for (int nt = 0; nt < kNt; ++nt) m_run[nt] = -INFINITY;
   const float scale = a.scale;
 
-  // With kAhead = 2, two register sets carry the K/V pieces of the next two tiles: tile t + 2 is
-  // fetched while tile t is computed, and tile t + 1 (fetched one iteration earlier) goes to LDS
-  // at its end.  With kAhead = 1 one set fetches tile t + 1 and stores it at the end of tile t.
-  u32x4 kregA[kKPieces], vregA[kVPieces][2], kregB[kKPieces], vregB[kVPieces][2];
+  // Tile t + 1 moves into the other buffer while tile t is computed; each wave waits for its own
+  // loads before the tile barrier, after which every wave's part is in place.
   __syncthreads();  // s_hblk ready
-  load_tile(0, kregA, vregA);
-  MI_STORE_TILE(0, kregA, vregA);
-  if constexpr (kAhead == 2) load_tile(min(1, n_tiles - 1), kregA, vregA);
+  dma_tile(0, 0);
+  // s_waitcnt vmcnt(0) (expcnt and lgkmcnt unconstrained) as a real instruction, so that the
+  // compiler also counts the Q fragment loads as complete and waits for nothing inside the loop.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
-  // kl / vl: registers tile t + 2 is fetched into; ks / vs: registers holding tile t + 1.
-  auto tile_step = [&](const int t, u32x4 (&kl)[kKPieces], u32x4 (&vl)[kVPieces][2], u32x4 (&ks_)[kKPieces],
-                       u32x4 (&vs_)[kVPieces][2]) {
-    const int buf = t & 1;
-    load_tile(min(t + kAhead, n_tiles - 1), kl, vl);  // past the end: re-reads the last tile
+  auto tile_step = [&](const int t, const int buf) {
+    if (t + 1 < n_tiles) dma_tile(t + 1, buf ^ 1);
+    const char* sKb = reinterpret_cast<const char*>(sK[buf]);
+    const char* sVb = reinterpret_cast<const char*>(sV[buf]);
 
     // ---- S^T = K Q^T for 64 keys x 32 queries
     f32x4 sacc[4][kNt];
@@ -381,7 +342,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[buf][(mt * 16 + ql) * kKStride + ks * 32 + gq * 8]);
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(sKb + mt * 4096 + k_off[ks]);
 #pragma unroll
         for (int nt = 0; nt < kNt; ++nt)
           sacc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[nt][ks], sacc[mt][nt], 0, 0, 0);
@@ -473,8 +434,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
     for (int ks2 = 0; ks2 < 2; ++ks2) {
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* vrow = &sV[buf][(dt * 16 + ql) * kVStride];
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vrow + vcol(dt * 16, 32 * ks2 + 8 * gq));
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) s16x4* lds_s16x4;
+        const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4)(sVb + 32 * ks2 * 256 + v_off[dt]));
+        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4)(sVb + (32 * ks2 + 16) * 256 + v_off[dt]));
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int nt = 0; nt < kNt; ++nt)
           oacc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[nt][ks2], oacc[dt][nt], 0, 0, 0);
@@ -484,16 +448,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
         oacc[8][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones_frag, pf[nt][ks2], oacc[8][nt], 0, 0, 0);
     }
 
-    MI_STORE_TILE(buf ^ 1, ks_, vs_);  // past the end: a buffer no later tile reads
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   };
-  if constexpr (kAhead == 2) {
-    for (int t = 0; t < n_tiles; t += 2) {
-      tile_step(t, kregB, vregB, kregA, vregA);
-      if (t + 1 < n_tiles) tile_step(t + 1, kregA, vregA, kregB, vregB);
-    }
-  } else {
-    for (int t = 0; t < n_tiles; ++t) tile_step(t, kregA, vregA, kregA, vregA);
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(t, 0);
+    if (t + 1 < n_tiles) tile_step(t + 1, 1);
   }
 
   // ---- normalise and write: lane holds query qw0 + 16 nt + ql, dims 16 dt + 4 gq + i
