@@ -3,13 +3,14 @@
 // Behaviour of PagedKVCachePool.gather_blocks (src/mini_infra/worker/paged_kv_cache.py:54-72):
 // per layer `key_pool[block_ids]` materialised as `[batch, nb, block_size, H, D]`, for K and V of
 // every layer in one launch.  A block of one layer is contiguous in the pool (32 KiB for
-// 16 x 8 x 128 bf16) and contiguous in the output, so four workgroups of 256 lanes stream one
-// block, a contiguous 8 KiB quarter each, with 16-byte pieces: lane i moves bytes [16 i, 16 i + 16)
-// of each 4 KiB stripe, both stripes in flight, loads issued before the stores.  Measured on
-// MI355X (config 4's history gather, three repetitions in one process): 6.15-6.18 TB/s, against
-// 5.87-5.98 for 4 KiB workgroups with one piece in flight, 5.90-6.17 for 16 KiB workgroups of 512
-// lanes, 5.68-6.01 for one 32 KiB workgroup per block (512 lanes x 2) and 5.49-5.69 for 256 lanes
-// x 8.
+// 16 x 8 x 128 bf16) and contiguous in the output, so eight workgroups of 128 lanes stream one
+// block, a contiguous 4 KiB eighth each, with 16-byte pieces: lane i moves bytes [16 i, 16 i + 16)
+// of each 2 KiB stripe, both stripes in flight, loads issued before the stores.  Measured on
+// MI355X (config 4's history gather, three repetitions in one process, against the read + write
+// copy ceiling of the same process, 6.44-6.54 TB/s): 6.47-6.53 TB/s (99-100%), against 6.25-6.31
+// for four 8 KiB workgroups of 256 lanes x 2, 6.29-6.34 for eight of 256 lanes x 1, 6.25-6.31 for
+// four of 512 x 1, 6.00-6.01 for sixteen 2 KiB workgroups of 128 x 1; earlier, 5.68-6.01 for one
+// 32 KiB workgroup per block (512 lanes x 2) and 5.49-5.69 for 256 lanes x 8.
 #include "mi_common.h"
 
 namespace mi {
@@ -23,10 +24,10 @@ namespace {
 #endif
 
 #ifndef MI_GATHER_THREADS
-#define MI_GATHER_THREADS 256
+#define MI_GATHER_THREADS 128
 #endif
 #ifndef MI_GATHER_SPLIT
-#define MI_GATHER_SPLIT 4
+#define MI_GATHER_SPLIT 8
 #endif
 constexpr int kSplit = MI_GATHER_SPLIT;  // workgroups per block: each copies a contiguous 1 / kSplit
 constexpr int kThreads = MI_GATHER_THREADS;

@@ -12,21 +12,24 @@
 // header plus the records.  mi_pack_blocks gathers blocks into records and mi_unpack_blocks
 // scatters records into (other) blocks; both are bit-exact copies.
 //
-// grid: x = record, y = layer of this launch, z = K / V.  Each workgroup moves one block_bytes
-// piece (32 KiB for 16 x 8 x 128 bf16) with 16-byte loads, all issued before the stores: 1024
-// lanes x 2 pieces cover it in one round.  Measured on 2048 random blocks of the 28-layer pool
-// (2 x 3.76 GB per launch): 5.35 TB/s pack, 5.27 TB/s unpack; 256-1024 lanes, 2-16 pieces per
-// lane and plain instead of non-temporal accesses all land within 2% (non-temporal is faster).
+// grid (one dimension): x = ((record * layers + layer) * 2 + K / V) * kSplit + part, so consecutive
+// workgroups walk a record's bytes in order.  kSplit workgroups share one block_bytes piece (32 KiB
+// for 16 x 8 x 128 bf16), a contiguous 1 / kSplit each, with 16-byte loads issued before the
+// stores.  Measured on 2048 random blocks of the 28-layer pool (2 x 3.76 GB per launch), three
+// repetitions in one process: 8 workgroups of 256 lanes x 1 piece 6.14-6.22 TB/s pack, 5.69-5.70
+// unpack; 8 x 128 x 2 6.03-6.08 / 5.60-5.63; 4 x 256 x 2 5.84-5.87 / 5.51-5.54; with the
+// (record; layer; K / V) grid instead, one 1024 x 2 workgroup per piece 5.39-5.42 / 5.28-5.29 and
+// 8 x 256 x 1 5.44-5.45 / 5.41-5.43.  Non-temporal accesses measured faster than plain ones.
 #include "mi_common.h"
 
 namespace mi {
 namespace {
 
 #ifndef MI_RECORDS_THREADS
-#define MI_RECORDS_THREADS 1024
+#define MI_RECORDS_THREADS 256
 #endif
 #ifndef MI_RECORDS_UNROLL
-#define MI_RECORDS_UNROLL 2
+#define MI_RECORDS_UNROLL 1
 #endif
 #ifndef MI_RECORDS_NT_LOAD
 #define MI_RECORDS_NT_LOAD 1
@@ -34,9 +37,13 @@ namespace {
 #ifndef MI_RECORDS_NT_STORE
 #define MI_RECORDS_NT_STORE 1
 #endif
+#ifndef MI_RECORDS_SPLIT
+#define MI_RECORDS_SPLIT 8
+#endif
 
 constexpr int kThreads = MI_RECORDS_THREADS;
 constexpr int kUnroll = MI_RECORDS_UNROLL;
+constexpr int kSplit = MI_RECORDS_SPLIT;  // workgroups per block piece, each a contiguous 1 / kSplit
 constexpr bool kNtLoad = MI_RECORDS_NT_LOAD != 0;    // non-temporal loads of the source
 constexpr bool kNtStore = MI_RECORDS_NT_STORE != 0;  // non-temporal stores of the destination
 
@@ -48,6 +55,7 @@ struct RecordArgs {
   int64_t block_bytes;
   int64_t record_bytes;
   int32_t layer0;   // first layer of this launch
+  int32_t layers;   // layers of this launch
   uint32_t pieces;  // block_bytes / sizeof(V)
 };
 
@@ -55,9 +63,11 @@ struct RecordArgs {
 // !kPack: record -> block (an out-of-range block id is skipped, as every write is).
 template <typename V, bool kPack>
 __global__ __launch_bounds__(kThreads) void kv_records_kernel(const RecordArgs a) {
-  const int64_t i = blockIdx.x;
-  const int layer = blockIdx.y;
-  const int kv = blockIdx.z;
+  const uint32_t part = blockIdx.x % kSplit;
+  const uint32_t piece_id = blockIdx.x / kSplit;
+  const int kv = piece_id & 1;
+  const int layer = (piece_id >> 1) % a.layers;
+  const int64_t i = (piece_id >> 1) / a.layers;
   const int64_t bid = a.block_ids[i];
   const bool valid = bid >= 0 && bid < a.num_blocks;
   if (!kPack && !valid) return;
@@ -65,17 +75,20 @@ __global__ __launch_bounds__(kThreads) void kv_records_kernel(const RecordArgs a
   V* rec = reinterpret_cast<V*>(a.records + i * a.record_bytes + (2 * (a.layer0 + layer) + kv) * a.block_bytes);
   const V* src = kPack ? block : rec;
   V* dst = kPack ? rec : block;
-  for (uint32_t base = 0; base < a.pieces; base += kThreads * kUnroll) {
+  const uint32_t per_part = (a.pieces + kSplit - 1) / kSplit;
+  const uint32_t p0 = part * per_part;
+  const uint32_t p1 = min(a.pieces, p0 + per_part);
+  for (uint32_t base = p0; base < p1; base += kThreads * kUnroll) {
     V val[kUnroll];
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < a.pieces) val[k] = load_vec<kNtLoad>(src + p);
+      if (p < p1) val[k] = load_vec<kNtLoad>(src + p);
     }
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < a.pieces) store_vec<kNtStore>(dst + p, val[k]);
+      if (p < p1) store_vec<kNtStore>(dst + p, val[k]);
     }
   }
 }
@@ -89,7 +102,8 @@ int32_t launch_records(const char* what, void* records, const void* const* key_p
   if (num_records == 0 || num_layers == 0 || block_bytes == 0) return ok();
   if (!records || !key_pools || !value_pools || !block_ids)
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
-  if (num_records > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "%s: too many records in one call", what);
+  if (num_records * kSplit * 2 * kMaxLayersPerLaunch > 0x7fffffff)
+    return fail(MI_ERR_UNSUPPORTED, "%s: too many records in one call", what);
   const int64_t record_bytes = 2 * static_cast<int64_t>(num_layers) * block_bytes;
 
   bool wide = block_bytes % 16 == 0 && aligned16(records);
@@ -116,7 +130,8 @@ int32_t launch_records(const char* what, void* records, const void* const* key_p
       a.pool[1][l] = const_cast<char*>(static_cast<const char*>(value_pools[l0 + l]));
     }
     a.layer0 = l0;
-    const dim3 grid(static_cast<uint32_t>(num_records), nl, 2);
+    a.layers = nl;
+    const dim3 grid(static_cast<uint32_t>(num_records * nl * 2 * kSplit), 1, 1);
     if (piece == 16)
       kv_records_kernel<u32x4, kPack><<<grid, kThreads, 0, s>>>(a);
     else if (piece == 4)

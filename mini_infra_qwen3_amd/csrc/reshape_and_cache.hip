@@ -6,7 +6,7 @@
 // per tensor per layer.
 //
 // Work mapping: a token is one destination K row and one V row of num_kv_heads * head_dim
-// elements (2 KiB each for 8 x 128 bf16), contiguous in the pool.  A workgroup of 256 lanes
+// elements (2 KiB each for 8 x 128 bf16), contiguous in the pool.  A workgroup of kThreads lanes
 // owns kTokensPerGroup consecutive tokens of one layer.
 //  * Row kernel (a token's K+V rows are a multiple of 256 16-byte pieces -- the Qwen3 shape):
 //    every lane owns fixed pieces of the row pair, so consecutive lanes move consecutive
@@ -23,12 +23,16 @@
 // 5.13-5.50, 16 with 4 5.22-5.51, 1 token 5.37-5.50.  Many small workgroups keep the most
 // independent 2 KiB row copies in flight.  Wider workgroups holding several tokens side by side
 // (MI_SCATTER_THREADS) measured slower on another machine: 512 lanes x 2 tokens 5.43-5.44 TB/s,
-// x 4 tokens 5.84-5.92, 1024 x 4 5.40-5.57, against 6.04-6.09 for 256 x 2.
+// x 4 tokens 5.84-5.92, 1024 x 4 5.40-5.57, against 6.04-6.09 for 256 x 2.  Narrower ones, three
+// repetitions against the read + write copy ceiling of the same process (6.44 TB/s): 128 lanes x 2
+// tokens with both in flight 6.14-6.21 TB/s (95-96%), 256 x 2 with one 6.05-6.17, 128 x 1 token
+// 5.93-6.09, 64 lanes 5.45-5.75; K and V rows in separate workgroups (128 x 2 with 2 in flight,
+// 128 x 4, 256 x 2) 5.48-6.14.
 #ifndef MI_SCATTER_TOKENS_PER_GROUP
 #define MI_SCATTER_TOKENS_PER_GROUP 2
 #endif
 #ifndef MI_SCATTER_UNROLL
-#define MI_SCATTER_UNROLL 1
+#define MI_SCATTER_UNROLL 2
 #endif
 #ifndef MI_SCATTER_NT
 #define MI_SCATTER_NT 1
@@ -38,7 +42,7 @@ namespace mi {
 namespace {
 
 #ifndef MI_SCATTER_THREADS
-#define MI_SCATTER_THREADS 256
+#define MI_SCATTER_THREADS 128
 #endif
 constexpr int kThreads = MI_SCATTER_THREADS;
 constexpr int kTokensPerGroup = MI_SCATTER_TOKENS_PER_GROUP;

@@ -21,10 +21,11 @@ struct Variant {
 };
 
 constexpr Variant kVariants[] = {
-    {256, 1, 4 << 10},   {256, 2, 8 << 10},   {512, 1, 8 << 10},    {256, 4, 16 << 10},
-    {512, 2, 16 << 10},  {512, 2, 32 << 10},  {256, 4, 64 << 10},   {512, 4, 64 << 10},
-    {512, 8, 128 << 10}, {1024, 4, 128 << 10}, {256, 8, 256 << 10}, {512, 8, 256 << 10},
-    {1024, 8, 512 << 10},
+    {64, 2, 2 << 10},    {64, 4, 4 << 10},    {64, 8, 8 << 10},     {128, 1, 2 << 10},
+    {128, 2, 4 << 10},   {128, 4, 8 << 10},   {128, 2, 8 << 10},    {256, 1, 4 << 10},
+    {256, 2, 8 << 10},   {512, 1, 8 << 10},   {256, 4, 16 << 10},   {512, 2, 16 << 10},
+    {512, 2, 32 << 10},  {256, 4, 64 << 10},  {512, 4, 64 << 10},   {512, 8, 128 << 10},
+    {1024, 4, 128 << 10}, {256, 8, 256 << 10}, {512, 8, 256 << 10}, {1024, 8, 512 << 10},
 };
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
