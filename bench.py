@@ -276,7 +276,7 @@ def cpu_baseline_decode_full(w, device: torch.device, slice_size: int = 32) -> d
 # ------------------------------------------------------------------------------- scatter
 def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "token",
                   ceiling: float | None = None, cpu: bool = False) -> dict:
-    """Config 2: the 28-layer prefill store of 32 prompts U[128, 2048] (40,636 tokens) into churned
+    """The 28-layer prefill store of 32 prompts U[128, 2048] (40,636 tokens) into churned
     blocks, one launch.  ``layout`` of the source ``[B, Hkv, L, D]`` per layer: ``token`` -- the
     memory of the HIP model's prefill K/V (``mi_qk_norm_rope`` writes ``[T, Hkv, D]`` rows, viewed
     as ``[B, Hkv, L, D]``), so a token's 2 KiB row is contiguous; ``head`` -- the reference's
@@ -334,7 +334,7 @@ def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "
 # -------------------------------------------------------------------------------- gather
 def bench_gather(steps: int, warmup: int, device: torch.device, ceiling: float | None = None,
                  cpu: bool = False) -> dict:
-    """Config 4's history gather (the reference's ``gather_blocks``), 28 layers: every chunk c of the 4
+    """The chunked-prefill history gather (the reference's ``gather_blocks``), 28 layers: every chunk c of the 4
     prompts gathers its 128 c history blocks, one launch per chunk.  ``cpu``: the oracle's
     ``gather_blocks`` on the host cores for one of the 28 layers."""
     from mini_infra_qwen3_amd import workloads as wl
@@ -577,7 +577,7 @@ def bench_prefill(steps: int, warmup: int, device: torch.device, cpu: bool = Fal
 # ------------------------------------------------------------------------ e2e continuous batching
 def cpu_baseline_e2e(seed: int = 0, num_requests: int = 8, max_new_tokens: int = 64) -> dict:
     """The oracle's restatement of the reference schedule backend (the reference's torch model,
-    runner and paged pool) on the host cores: the first requests of the config-5 workload with
+    runner and paged pool) on the host cores: the first requests of the continuous-batching workload with
     fewer output tokens, same loop, token budget and model.  Output tok/s over the loop's wall
     time (its busy time: no idle gaps, the loop runs back to back)."""
     from mini_infra_qwen3_amd.engine import run_scheduler

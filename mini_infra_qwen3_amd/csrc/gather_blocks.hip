@@ -6,7 +6,7 @@
 // 16 x 8 x 128 bf16) and contiguous in the output, so eight workgroups of 128 lanes stream one
 // block, a contiguous 4 KiB eighth each, with 16-byte pieces: lane i moves bytes [16 i, 16 i + 16)
 // of each 2 KiB stripe, both stripes in flight, loads issued before the stores.  Measured on
-// MI355X (config 4's history gather, three repetitions in one process, against the read + write
+// MI355X (the history gather of 4 prompts x 16384 tokens in 2048-token chunks, three repetitions in one process, against the read + write
 // copy ceiling of the same process, 6.44-6.54 TB/s): 6.47-6.53 TB/s (99-100%), against 6.25-6.31
 // for four 8 KiB workgroups of 256 lanes x 2, 6.29-6.34 for eight of 256 lanes x 1, 6.25-6.31 for
 // four of 512 x 1, 6.00-6.01 for sixteen 2 KiB workgroups of 128 x 1; earlier, 5.68-6.01 for one

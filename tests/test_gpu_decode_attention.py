@@ -177,7 +177,7 @@ def test_zero_context_writes_zero_row(native_lib, device):
 
 
 def test_decode_at_scale_every_row(native_lib, device):
-    """Config 3 at full size (one layer): batch 256, lognormal contexts up to 8192, about 3.2 GB of
+    """Decode at scale (one layer): batch 256, lognormal contexts up to 8192, about 3.2 GB of
     K/V.  Every one of the 256 rows is checked against the oracle run on cuda:0 over the blocks its
     sequence owns (a per-sequence gather: the reference's padded gather of all 256 rows would be
     ~17 GB per layer): the bandwidth kernel (block ranges, most sequences cut between ranges and
@@ -199,7 +199,7 @@ def test_decode_at_scale_every_row(native_lib, device):
         assert err <= TOL, f"sequence {b} (context {w.context_lens[b]}): {err}"
         want = torch_ref.paged_decode_attention(q[b:b + 1], kp[blocks], vp[blocks], local_t, n, SCALE, exact=True)
         assert torch.equal(exact[b:b + 1], want), f"sequence {b}: exact kernel differs from the oracle"
-    print(f"\nconfig 3, 256 rows: bandwidth kernel max-abs {worst:.3e} vs the oracle; exact kernel bit-identical")
+    print(f"\ndecode at batch 256, all rows: bandwidth kernel max-abs {worst:.3e} vs the oracle; exact kernel bit-identical")
     assert math.isclose(sum(w.context_lens) * 4096, w.kv_bytes_per_layer)
 
 

@@ -54,7 +54,7 @@ def compare(product, oracle, backend):
 
 
 @pytest.mark.timeout(900)
-def test_config5_greedy_tokens_identical_to_the_oracle():
+def test_continuous_batching_run_greedy_tokens_identical_to_the_oracle():
     """The full workload: 128 requests, Poisson arrivals at 20 req/s, prompts U[32, 1024], 128 greedy
     tokens each, token budget 2048, 128 batch slots; decode steps replay HIP graphs."""
     model, ref = build()

@@ -35,13 +35,13 @@ def decode_case(seed, batch, lo, hi, kv_heads, group, num_blocks):
 
 
 @pytest.mark.parametrize("seed,batch,lo,hi,kv_heads,group,num_blocks", [
-    (0, 8, 64, 512, 8, 2, 4096),     # config 1's shape
+    (0, 8, 64, 512, 8, 2, 4096),     # the one-layer decode step's shape (batch 8, contexts U[64, 512])
     (1, 5, 1, 40, 8, 2, 64),         # contexts of one token and partial blocks
     (2, 3, 100, 700, 4, 4, 400),
     (3, 2, 9000, 9700, 2, 8, 1300),  # past the LDS score cache: scores recomputed per pass
     (4, 4, 30, 300, 8, 5, 200),
     (5, 3, 50, 300, 8, 1, 200),
-    (6, 40, 200, 1200, 8, 2, 4000),  # a config-5 sized decode batch
+    (6, 40, 200, 1200, 8, 2, 4000),  # a decode batch of the continuous-batching run's size
 ])
 def test_exact_decode_is_bit_identical_to_the_oracle(device, seed, batch, lo, hi, kv_heads, group, num_blocks):
     q, kp, vp, bt, ctx = decode_case(seed, batch, lo, hi, kv_heads, group, num_blocks)

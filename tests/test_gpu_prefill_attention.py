@@ -162,8 +162,8 @@ def test_chunked_equals_one_shot(native_lib, device):
 
 
 @pytest.mark.timeout(600)
-def test_config4_every_chunk_of_every_prompt(native_lib, device):
-    """Config 4 at full size, one layer: 4 prompts x 16384 tokens in 8 chunks of 2048, block tables
+def test_four_16k_prompts_every_chunk_of_every_prompt(native_lib, device):
+    """Chunked prefill at full size, one layer: 4 prompts x 16384 tokens in 8 chunks of 2048, block tables
     from seeded alloc / free churn.  Each chunk step is one launch over the 4 prompts, its history
     (2048 c tokens) read from the pool, where the earlier chunks' K/V were stored.  Every real row of
     every chunk is checked against the oracle run on cuda:0 (the reference's gather + concat +
@@ -206,7 +206,7 @@ def test_config4_every_chunk_of_every_prompt(native_lib, device):
             slots = tables[b, pos // 16] * 16 + pos % 16
             kp.view(-1, 8, 128)[slots] = k[b].transpose(0, 1)
             vp.view(-1, 8, 128)[slots] = v[b].transpose(0, 1)
-    print(f"\nconfig 4, 8 chunks x 4 prompts: MFMA kernel max-abs {worst:.3e} vs the oracle; exact kernel bit-identical on chunks 0-1")
+    print(f"\nchunked prefill, 8 chunks x 4 prompts: MFMA kernel max-abs {worst:.3e} vs the oracle; exact kernel bit-identical on chunks 0-1")
 
 
 @pytest.mark.parametrize("block_size", [32, 64])
