@@ -166,6 +166,30 @@ def test_gather_out_of_range_ids_read_the_null_block(native_lib, device):
     assert torch.equal(key, want_k) and torch.equal(value, want_v)
 
 
+@pytest.mark.parametrize("layers,bs,heads,dim,dtype", [
+    (33, 16, 8, 128, torch.bfloat16),  # two launches (32 layers per launch)
+    (2, 2, 1, 6, torch.bfloat16),      # 24-byte blocks: 4-byte pieces, fewer than the workgroups per block
+    (2, 1, 1, 3, torch.bfloat16),      # 6-byte blocks: 2-byte pieces
+    (3, 3, 2, 5, torch.float32),       # 120-byte blocks: 4-byte pieces, one part each
+    (2, 16, 4, 64, torch.float32),     # 16 KiB blocks
+], ids=["33layers", "piece4", "piece2", "fp32odd", "fp32"])
+def test_gather_block_shapes(native_lib, device, layers, bs, heads, dim, dtype):
+    """Every block size the wide and narrow piece forms cover, against the closed form
+    out[b, j] = pool[ids[b, j]] (ids outside the pool read block 0)."""
+    gen = torch.Generator().manual_seed(layers * 100 + bs)
+    nb = 12
+    pool = PagedKVCachePool(layers, nb, bs, heads, dim, dtype, device)
+    cpu = torch.randn(pool.storage.shape, generator=gen).to(dtype)
+    pool.storage.copy_(cpu)
+    ids = torch.tensor([[5, 11, 0, 3], [nb + 2, 7, -1, 7]])
+    got = pool.gather_blocks(ids.to(device))
+    fixed = ids.clamp(min=0).masked_fill(ids >= nb, 0)
+    for layer, (gk, gv) in enumerate(got):
+        for kv, g in ((0, gk), (1, gv)):
+            want = cpu[layer, kv][fixed].reshape(2, 4 * bs, heads, dim).transpose(1, 2)
+            assert_bit_equal(g.cpu(), want)
+
+
 def test_gather_strided_block_ids(native_lib, device):
     """Block ids as a column slice of a packed metadata tensor (row stride != width)."""
     pool = PagedKVCachePool(1, 8, 16, 8, 128, torch.bfloat16, device)
