@@ -791,7 +791,8 @@ def main() -> int:
         kernels["gather"] = bench_gather(max(args.steps // 2, 6), 2, device, ceil["read_write_GBps"], cpu=want_cpu)
         log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s "
             f"({100 * kernels['gather']['frac_of_copy_ceiling']:.1f}% of the copy ceiling)")
-        kernels["chunked_prefill"] = bench_prefill(max(args.steps // 4, 3), 3, device, cpu=want_cpu)
+        # 20 untimed layers (~90 ms): with 3, the first timed layers of a process ran ~5% slow.
+        kernels["chunked_prefill"] = bench_prefill(max(args.steps // 2, 5), 20, device, cpu=want_cpu)
         log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "
             f"{kernels['chunked_prefill']['achieved_TFLOPs']:.1f} TFLOP/s")
         torch.cuda.empty_cache()
