@@ -96,6 +96,7 @@ struct PrefillArgs {
   int32_t tiles;   // query tiles per row: ceil(padded_len / kQTile)
   int32_t batch;   // rows
   int32_t groups;  // workgroups of these rows: tiles x num_kv_heads x pairs x batch
+  int32_t round_pairs;  // (row, head pair) units per dispatch round of one workgroup queue
   // Decode rows (a mixed step's single new tokens, padded_len 1): start_lens holds each row's
   // context length including its token, so the history is the context minus one and a row with
   // context 0 is padding; the token's K/V row is appended to pool slot slot_mapping[b] (skipped
@@ -144,25 +145,29 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   const PrefillArgs a = second ? a1 : a0;
 
   // Workgroup -> (row b, head pair hp, query tile qt).  Consecutive workgroup ids go round-robin to
-  // the 8 XCDs, each with its own L2; so that the query tiles of one (row, head) -- which stream
-  // the same K/V tiles -- share an L2, id L runs on XCD L % 8 and takes the (L / 8)-th tile of that
-  // XCD's (row, head pair) units in order.  Shapes whose pair count is not a multiple of 8 keep the
-  // plain mapping.  Within a pair the heaviest (latest) query tiles start first.
+  // the kXcds XCDs, each with its own L2, and each XCD starts its ids in order on whichever CU
+  // frees first.  When the pair count is a multiple of kXcds, id L runs on XCD L % kXcds and takes
+  // place L / kXcds in the queue of that XCD's own pairs, so the query tiles of one (row, head
+  // pair) -- which stream the same K/V tiles -- share an L2; otherwise one queue holds every pair.
+  // A queue is cut into rounds of round_pairs pairs (as many as its CUs hold with all their query
+  // tiles at once), and inside a round the tiles go heaviest (latest) first, pair by pair: the CUs
+  // that finish a round's light tiles first take the next round's heavy ones, so every CU ends up
+  // with about the same number of key tiles under the causal mask.
   int b, hp, qt;
   {
     const int tiles = a.tiles;
     const int per_row = kKvHeads * a.pairs;
     const int pairs = per_row * a.batch;
     const int lin = static_cast<int>(blockIdx.x) - (second ? a0.groups : 0);
-    int pair, rank;
-    if (pairs % 8 == 0) {
-      const int slot = lin >> 3;
-      pair = (slot / tiles) * 8 + (lin & 7);
-      rank = slot % tiles;
-    } else {
-      pair = lin / tiles;
-      rank = lin % tiles;
-    }
+    const bool by_xcd = pairs % kXcds == 0;
+    const int units = by_xcd ? pairs / kXcds : pairs;  // pairs in this queue
+    const int slot = by_xcd ? lin / kXcds : lin;       // place in this queue
+    const int round_idx = slot / (a.round_pairs * tiles);
+    const int within = slot - round_idx * a.round_pairs * tiles;
+    const int round_size = min(a.round_pairs, units - round_idx * a.round_pairs);
+    const int rank = within / round_size;
+    const int unit = round_idx * a.round_pairs + (within - rank * round_size);
+    const int pair = by_xcd ? unit * kXcds + lin % kXcds : unit;
     hp = pair % per_row;
     b = pair / per_row;
     qt = tiles - 1 - rank;
@@ -508,8 +513,16 @@ PrefillArgs rows_args(int32_t batch, int32_t padded_len, int32_t num_heads, int3
   a.pairs = (a.group + kGroup - 1) / kGroup;
   a.scale = scale;
   a.tiles = (padded_len + kQTile - 1) / kQTile;
-  const int64_t groups = static_cast<int64_t>(a.tiles) * num_kv_heads * a.pairs * batch;
+  const int64_t pairs = static_cast<int64_t>(num_kv_heads) * a.pairs * batch;
+  const int64_t groups = a.tiles * pairs;
   a.groups = groups > 0x3fffffff ? -1 : static_cast<int32_t>(groups);
+  // Dispatch rounds: the queue of one XCD (or of the whole device when the pairs do not split
+  // evenly over the XCDs) holds its CUs' worth of whole pairs per round.
+  const bool by_xcd = pairs % kXcds == 0;
+  const int64_t units = by_xcd ? pairs / kXcds : pairs;
+  const int64_t cus = by_xcd ? device_cus() / kXcds : device_cus();
+  const int64_t per_round = std::min(a.tiles > 0 ? cus / a.tiles : int64_t{1}, units);
+  a.round_pairs = static_cast<int32_t>(std::max(per_round, int64_t{1}));
   return a;
 }
 

@@ -45,6 +45,24 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Compute units of the current device (256 on MI355X), read once per device; 256 when the
+// attribute cannot be read.
+inline int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Workgroups are handed out round-robin to this many XCDs (accelerator complex dies), each with
+// its own L2: consecutive workgroup ids land on different XCDs.
+constexpr int kXcds = 8;
+
 // At most this many layers go into one launch (pointer tables travel in the
 // kernel argument segment); callers with more layers are split into chunks.
 constexpr int kMaxLayersPerLaunch = 32;

@@ -889,18 +889,6 @@ __global__ __launch_bounds__(merge_threads<kHeads>()) void paged_decode_merge_ke
   store_bf16x8(dst, acc, 1.0f / L);
 }
 
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 int head_groups_for(int32_t num_kv_heads) {
   const int waves = num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves;
   return num_kv_heads / waves;
