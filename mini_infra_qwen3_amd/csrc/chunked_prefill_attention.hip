@@ -250,9 +250,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   // as many for V; wave w moves spans [kSpansPerWave w, kSpansPerWave (w + 1)) of each.  Lane i of
   // span m fetches row 4 m + i / 16, global chunk (i % 16) ^ (row % 16), so that the chunk lands at
   // its swizzled place: the 16 lanes of an MFMA operand read (16 rows, one logical chunk) then hit
-  // 16 different chunk positions, i.e. all banks.  In a history tile the four rows of a span lie in
-  // one pool block (uniform), read from the history table the workgroup staged in LDS; chunk rows
-  // past L - 1 read row L - 1 (their keys are masked).
+  // 16 different chunk positions, i.e. all banks.  In a history tile a wave's spans lie in one pool
+  // block, whose id comes from the history table the workgroup staged in LDS; the id for tile t + 1
+  // is read while tile t - 1 is computed, so no tile waits for that read.  Chunk rows past L - 1
+  // read row L - 1 (their keys are masked).
   const int nhb = (nh + kBlockSize - 1) / kBlockSize;
   for (int i = tid; i < nhb; i += kThreads) {
     const int64_t x = a.history_blocks[b * a.history_stride + i];
@@ -267,10 +268,16 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   const uint32_t k_tok = static_cast<uint32_t>(a.k_tok);  // < 2^24, checked by the entry point
   const uint32_t v_tok = static_cast<uint32_t>(a.v_tok);
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  static_assert(kBlockSize % (4 * kSpansPerWave) == 0, "a wave's spans of a tile must lie in one pool block");
+  const int wave_blk = 4 * kSpansPerWave * w / kBlockSize;  // pool block of this wave's rows within a tile
+  const auto hist_slot = [&](const int t) { return min(t * (kKTile / kBlockSize) + wave_blk, max(nhb - 1, 0)); };
+  // LDS byte addresses of this wave's first K and V span in buffer 0 (buffer 1 follows at + kTileBytes).
+  constexpr uint32_t kTileBytes = kKTile * kHeadDim * sizeof(uint16_t);
+  const uint32_t k_lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(&sK[0][kSpansPerWave * w * 512])));
+  const uint32_t v_lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(&sV[0][kSpansPerWave * w * 512])));
 
-#define MI_HIST_BLOCK(T, KEY) \
-  __builtin_amdgcn_readfirstlane(s_hblk[min((T) * (kKTile / kBlockSize) + (KEY) / kBlockSize, max(nhb - 1, 0))])
-  auto dma_tile = [&](const int t, const int buf) {
+  // hblk: this wave's history block id for tile t (unused for chunk tiles).
+  auto dma_tile = [&](const int t, const int buf, const int hblk) {
     const bool hist = t < n_hist_tiles;
     const int key0 = (c_lo + t - n_hist_tiles) * kKTile;
 #pragma unroll
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
       const uint16_t* ksrc;
       const uint16_t* vsrc;
       if (hist) {
-        const int64_t blk = MI_HIST_BLOCK(t, 4 * m);
+        const int64_t blk = __builtin_amdgcn_readfirstlane(hblk);
         const uint32_t off = static_cast<uint32_t>(((r & 15) * kKvHeads + g) * kHeadDim) + c8;
         ksrc = a.key_pool + blk * kBlkElems + off;
         vsrc = a.value_pool + blk * kBlkElems + off;
@@ -290,8 +297,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
         ksrc = k_rows + (__umul24(kc, k_tok) + c8);
         vsrc = v_rows + (__umul24(kc, v_tok) + c8);
       }
-      dma16(ksrc, __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(&sK[buf][m * 512])))));
-      dma16(vsrc, __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(&sV[buf][m * 512])))));
+      dma16(ksrc, __builtin_amdgcn_readfirstlane(k_lds0 + buf * kTileBytes + i * 1024));
+      dma16(vsrc, __builtin_amdgcn_readfirstlane(v_lds0 + buf * kTileBytes + i * 1024));
     }
   };
   // Per-lane LDS byte offsets of the MFMA operands.  K (A of S^T = K Q^T): row 16 mt + ql, global
@@ -326,14 +333,16 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   // Tile t + 1 moves into the other buffer while tile t is computed; each wave waits for its own
   // loads before the tile barrier, after which every wave's part is in place.
   __syncthreads();  // s_hblk ready
-  dma_tile(0, 0);
+  dma_tile(0, 0, s_hblk[hist_slot(0)]);
+  int hblk_next = s_hblk[hist_slot(1)];
   // s_waitcnt vmcnt(0) (expcnt and lgkmcnt unconstrained) as a real instruction, so that the
   // compiler also counts the Q fragment loads as complete and waits for nothing inside the loop.
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
   auto tile_step = [&](const int t, const int buf) {
-    if (t + 1 < n_tiles) dma_tile(t + 1, buf ^ 1);
+    if (t + 1 < n_tiles) dma_tile(t + 1, buf ^ 1, hblk_next);
+    hblk_next = s_hblk[hist_slot(t + 2)];
     const char* sKb = reinterpret_cast<const char*>(sK[buf]);
     const char* sVb = reinterpret_cast<const char*>(sV[buf]);
 
