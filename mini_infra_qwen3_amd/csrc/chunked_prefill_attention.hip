@@ -18,6 +18,9 @@
 //    GQA group of G heads on KV head g and queries [32 (w & 3), +32) of the tile, so the two
 //    heads share every K/V tile staged in LDS.  A group of G heads takes ceil(G / 2) pairs; when G
 //    is odd, the second half of its last pair repeats the group's last head and writes nothing.
+//  * Dispatch order: the query tiles of one (row, head pair) stay on one XCD (shared L2), and each
+//    XCD's queue runs in rounds of as many whole pairs as its CUs hold, heaviest query tiles first
+//    inside a round, so the causal chunk's light and heavy tiles pair up on every CU.
 //  * KV tiles of 64 keys: history tiles first (pool blocks through the block table -- the
 //    gather is fused, nothing is materialised), then chunk tiles up to the causal limit.
 //    K and V tiles go from memory straight into double-buffered LDS (global_load_lds_dwordx4, no
