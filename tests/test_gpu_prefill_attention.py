@@ -209,6 +209,31 @@ def test_four_16k_prompts_every_chunk_of_every_prompt(native_lib, device):
     print(f"\nchunked prefill, 8 chunks x 4 prompts: MFMA kernel max-abs {worst:.3e} vs the oracle; exact kernel bit-identical on chunks 0-1")
 
 
+@pytest.mark.parametrize("kv_heads,batch,width", [
+    (8, 3, 2048),   # 24 (row, head pair) units: 3 per XCD queue, rounds of 2 and 1 (16 query tiles)
+    (8, 2, 4160),   # 33 query tiles, more than an XCD's 32 CUs: one pair per round
+    (2, 5, 8320),   # 10 units, not a multiple of the 8 XCDs: one device queue, rounds of 3, 3, 3, 1
+])
+def test_dispatch_rounds(native_lib, device, kv_heads, batch, width):
+    """Workgroup orders with a short last dispatch round, one pair per round and the single
+    device queue (on a 256-CU MI355X); every real row checked against the oracle run on cuda:0,
+    one row at a time."""
+    starts = [(700 * b) % 1500 for b in range(batch)]
+    lens = [width - 37 * b for b in range(batch)]
+    q, k, v, kp, vp, hist = make_case(200 + batch, starts, lens, width=width, kv_heads=kv_heads, spare=2)
+    got = run_gpu(q, k, v, kp, vp, hist, starts, lens, device)
+    kp, vp = kp.to(device), vp.to(device)
+    for b, n in enumerate(lens):
+        ref = torch_ref.chunked_prefill_attention(q[b:b + 1].to(device), k[b:b + 1].to(device),
+                                                  v[b:b + 1].to(device), (kp, vp), hist[b:b + 1].to(device),
+                                                  starts[b:b + 1], lens[b:b + 1], SCALE)
+        real = slice(width - n, width)
+        err = (got[b, real].float() - ref[0, real].float()).abs().max().item()
+        assert err <= TOL, f"row {b}: max-abs {err}"
+        assert not got[b, :width - n].any(), f"row {b}: padding rows must be zero"
+        del ref
+
+
 @pytest.mark.parametrize("block_size", [32, 64])
 def test_pool_blocks_of_multiples_of_16_tokens(native_lib, device, block_size):
     """History in a pool of 16 k-token blocks, read as 16-token sub-blocks."""
