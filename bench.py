@@ -389,7 +389,8 @@ def bench_gather(steps: int, warmup: int, device: torch.device, ceiling: float |
 # ------------------------------------------------------------------------------ device copy
 def copy_ceiling(device: torch.device, nbytes: int = 2 << 30, reps: int = 5) -> dict:
     """What plain streaming traffic reaches on this device: the calibration kernels of
-    libmi_calib.so (16-byte non-temporal accesses, contiguous spans per workgroup) over 2 GiB
+    libmi_calib.so (16-byte non-temporal accesses, with non-temporal or device-scope streaming
+    stores, contiguous spans per workgroup) over 2 GiB
     buffers, for read + write (copy), read-only and write-only, best of the library's launch
     shapes.  The read + write rate is the ceiling scatter, gather and the block records are read
     against, the read rate the one decode attention (a read stream) is."""
@@ -400,7 +401,7 @@ def copy_ceiling(device: torch.device, nbytes: int = 2 << 30, reps: int = 5) -> 
     lib.calib_groups.argtypes = [ctypes.c_int64, ctypes.c_int32]
     lib.calib_groups.restype = ctypes.c_int64
     lib.calib_variant.argtypes = [ctypes.c_int32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
-                                  ctypes.POINTER(ctypes.c_int64)]
+                                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32)]
     variants = lib.calib_num_variants()
     src = torch.empty(nbytes, dtype=torch.uint8, device=device).random_()
     dst = torch.empty_like(src)
@@ -423,9 +424,10 @@ def copy_ceiling(device: torch.device, nbytes: int = 2 << 30, reps: int = 5) -> 
                 timer.stop()
             gbs = moved / (timer.mean_ms() * 1e-3) / 1e9
             if gbs > best[0]:
-                t, f, sp = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
-                lib.calib_variant(v, ctypes.byref(t), ctypes.byref(f), ctypes.byref(sp))
-                best = (gbs, f"{t.value} lanes, {f.value} pieces in flight, {sp.value >> 10} KiB per workgroup")
+                t, f, sp, st = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64(), ctypes.c_int32()
+                lib.calib_variant(v, ctypes.byref(t), ctypes.byref(f), ctypes.byref(sp), ctypes.byref(st))
+                best = (gbs, f"{t.value} lanes, {f.value} pieces in flight, {sp.value >> 10} KiB per workgroup"
+                             + (", device-scope streaming stores" if st.value and shape != 1 else ""))
         result[f"{name}_GBps"] = round(best[0], 1)
         result[f"{name}_frac"] = round(best[0] / HBM_PEAK_GBS, 4)
         result[f"{name}_shape"] = best[1]

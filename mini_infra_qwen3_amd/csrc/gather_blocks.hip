@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kThreads) void gather_blocks_kernel(const GatherArg
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < p1) store_vec<kNt>(dst + p, val[k]);
+      if (p < p1) store_stream<kNt>(dst + p, val[k]);
     }
   }
 }

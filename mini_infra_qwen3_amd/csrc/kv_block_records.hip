@@ -88,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void kv_records_kernel(const RecordArgs a
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const uint32_t p = base + k * kThreads + threadIdx.x;
-      if (p < p1) store_vec<kNtStore>(dst + p, val[k]);
+      if (p < p1) store_stream<kNtStore>(dst + p, val[k]);
     }
   }
 }

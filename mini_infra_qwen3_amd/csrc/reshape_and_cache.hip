@@ -27,7 +27,10 @@
 // repetitions against the read + write copy ceiling of the same process (6.44 TB/s): 128 lanes x 2
 // tokens with both in flight 6.14-6.21 TB/s (95-96%), 256 x 2 with one 6.05-6.17, 128 x 1 token
 // 5.93-6.09, 64 lanes 5.45-5.75; K and V rows in separate workgroups (128 x 2 with 2 in flight,
-// 128 x 4, 256 x 2) 5.48-6.14.
+// 128 x 4, 256 x 2) 5.48-6.14.  Device-scope streaming stores (store_stream, which the gather and
+// the block records use) against a copy ceiling of 6.69 TB/s with the same stores: 6.07-6.22 TB/s
+// at 2 tokens per group against 6.14-6.30 with non-temporal stores; 4, 8 or 16 tokens per group
+// with either store 5.14-5.76.
 #ifndef MI_SCATTER_TOKENS_PER_GROUP
 #define MI_SCATTER_TOKENS_PER_GROUP 2
 #endif

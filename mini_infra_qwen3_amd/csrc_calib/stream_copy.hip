@@ -5,8 +5,10 @@
 // Three traffic shapes over contiguous buffers, 16-byte non-temporal accesses, each workgroup
 // streaming one contiguous span of `span` bytes with `kInFlight` pieces per lane in flight:
 //   copy  (read + write), read (loads folded into one word per workgroup), write (stores only).
-// A variant is (lanes per workgroup, pieces in flight, span); bench.py sweeps them and keeps the
-// best of each shape.
+// A variant is (lanes per workgroup, pieces in flight, span, store form); bench.py sweeps them and
+// keeps the best of each shape.  Store forms: the non-temporal store, or the same store at device
+// scope as well (nt sc1: the line goes out to memory instead of staying dirty in the XCD's L2),
+// the form the gather and the KV record copies use.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -14,22 +16,37 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+template <bool kStream>
+__device__ __forceinline__ void put(u32x4* p, const u32x4& v) {
+  if constexpr (kStream) {
+    asm volatile("global_store_dwordx4 %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+  } else {
+    __builtin_nontemporal_store(v, p);
+  }
+}
+
 struct Variant {
   int threads;
   int in_flight;
   int64_t span;  // bytes per workgroup
+  bool stream;   // device-scope non-temporal stores (nt sc1) instead of non-temporal ones
 };
 
 constexpr Variant kVariants[] = {
-    {64, 2, 2 << 10},    {64, 4, 4 << 10},    {64, 8, 8 << 10},     {128, 1, 2 << 10},
-    {128, 2, 4 << 10},   {128, 4, 8 << 10},   {128, 2, 8 << 10},    {256, 1, 4 << 10},
-    {256, 2, 8 << 10},   {512, 1, 8 << 10},   {256, 4, 16 << 10},   {512, 2, 16 << 10},
-    {512, 2, 32 << 10},  {256, 4, 64 << 10},  {512, 4, 64 << 10},   {512, 8, 128 << 10},
-    {1024, 4, 128 << 10}, {256, 8, 256 << 10}, {512, 8, 256 << 10}, {1024, 8, 512 << 10},
+    {64, 2, 2 << 10, false},     {64, 4, 4 << 10, false},     {64, 8, 8 << 10, false},
+    {128, 1, 2 << 10, false},    {128, 2, 4 << 10, false},    {128, 4, 8 << 10, false},
+    {128, 2, 8 << 10, false},    {256, 1, 4 << 10, false},    {256, 2, 8 << 10, false},
+    {512, 1, 8 << 10, false},    {256, 4, 16 << 10, false},   {512, 2, 16 << 10, false},
+    {512, 2, 32 << 10, false},   {256, 4, 64 << 10, false},   {512, 4, 64 << 10, false},
+    {512, 8, 128 << 10, false},  {1024, 4, 128 << 10, false}, {256, 8, 256 << 10, false},
+    {512, 8, 256 << 10, false},  {1024, 8, 512 << 10, false},
+    {64, 2, 2 << 10, true},      {128, 1, 2 << 10, true},     {128, 2, 4 << 10, true},
+    {256, 1, 4 << 10, true},     {256, 2, 8 << 10, true},     {512, 1, 8 << 10, true},
+    {512, 2, 16 << 10, true},
 };
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
-template <int kInFlight>
+template <int kInFlight, bool kStream>
 __global__ void copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src, int64_t pieces,
                             int64_t span_pieces) {
   const int64_t base = static_cast<int64_t>(blockIdx.x) * span_pieces;
@@ -45,7 +62,7 @@ __global__ void copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ s
 #pragma unroll
     for (int k = 0; k < kInFlight; ++k) {
       const int64_t p = p0 + static_cast<int64_t>(k) * blockDim.x;
-      if (p < end) __builtin_nontemporal_store(v[k], dst + p);
+      if (p < end) put<kStream>(dst + p, v[k]);
     }
   }
 }
@@ -72,7 +89,7 @@ __global__ void read_kernel(const u32x4* __restrict__ src, uint32_t* __restrict_
   if (threadIdx.x == 0 || acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
 }
 
-template <int kInFlight>
+template <int kInFlight, bool kStream>
 __global__ void write_kernel(u32x4* __restrict__ dst, int64_t pieces, int64_t span_pieces) {
   const int64_t base = static_cast<int64_t>(blockIdx.x) * span_pieces;
   const int64_t end = min(base + span_pieces, pieces);
@@ -82,7 +99,7 @@ __global__ void write_kernel(u32x4* __restrict__ dst, int64_t pieces, int64_t sp
 #pragma unroll
     for (int k = 0; k < kInFlight; ++k) {
       const int64_t p = p0 + static_cast<int64_t>(k) * blockDim.x;
-      if (p < end) __builtin_nontemporal_store(v, dst + p);
+      if (p < end) put<kStream>(dst + p, v);
     }
   }
 }
@@ -96,11 +113,13 @@ int check_args(int64_t bytes, int32_t variant) {
 
 extern "C" int32_t calib_num_variants(void) { return kNumVariants; }
 
-extern "C" int32_t calib_variant(int32_t variant, int32_t* threads, int32_t* in_flight, int64_t* span) {
+extern "C" int32_t calib_variant(int32_t variant, int32_t* threads, int32_t* in_flight, int64_t* span,
+                                 int32_t* stream_stores) {
   if (variant < 0 || variant >= kNumVariants) return -1;
   *threads = kVariants[variant].threads;
   *in_flight = kVariants[variant].in_flight;
   *span = kVariants[variant].span;
+  *stream_stores = kVariants[variant].stream ? 1 : 0;
   return 0;
 }
 
@@ -125,10 +144,12 @@ extern "C" int32_t calib_stream(int32_t shape, void* dst, const void* src, void*
   u32x4* d = static_cast<u32x4*>(dst);
   const u32x4* r = static_cast<const u32x4*>(src);
   uint32_t* k = static_cast<uint32_t*>(sink);
-#define CALIB_LAUNCH(N)                                                          \
-  if (shape == 0) copy_kernel<N><<<grid, v.threads, 0, s>>>(d, r, pieces, span_pieces); \
-  else if (shape == 1) read_kernel<N><<<grid, v.threads, 0, s>>>(r, k, pieces, span_pieces); \
-  else write_kernel<N><<<grid, v.threads, 0, s>>>(d, pieces, span_pieces);
+#define CALIB_LAUNCH(N)                                                                        \
+  if (shape == 0 && v.stream) copy_kernel<N, true><<<grid, v.threads, 0, s>>>(d, r, pieces, span_pieces); \
+  else if (shape == 0) copy_kernel<N, false><<<grid, v.threads, 0, s>>>(d, r, pieces, span_pieces);       \
+  else if (shape == 1) read_kernel<N><<<grid, v.threads, 0, s>>>(r, k, pieces, span_pieces);             \
+  else if (v.stream) write_kernel<N, true><<<grid, v.threads, 0, s>>>(d, pieces, span_pieces);           \
+  else write_kernel<N, false><<<grid, v.threads, 0, s>>>(d, pieces, span_pieces);
   switch (v.in_flight) {
     case 1: CALIB_LAUNCH(1) break;
     case 2: CALIB_LAUNCH(2) break;
