@@ -275,13 +275,14 @@ def cpu_baseline_decode_full(w, device: torch.device, slice_size: int = 32) -> d
 
 # ------------------------------------------------------------------------------- scatter
 def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "token",
-                  ceiling: float | None = None, cpu: bool = False) -> dict:
+                  ceiling: float | None = None, cpu: bool = False, pattern_ceiling: float | None = None) -> dict:
     """The 28-layer prefill store of 32 prompts U[128, 2048] (40,636 tokens) into churned
     blocks, one launch.  ``layout`` of the source ``[B, Hkv, L, D]`` per layer: ``token`` -- the
     memory of the HIP model's prefill K/V (``mi_qk_norm_rope`` writes ``[T, Hkv, D]`` rows, viewed
     as ``[B, Hkv, L, D]``), so a token's 2 KiB row is contiguous; ``head`` -- the reference's
     ``KVCache`` layout (contiguous ``[B, Hkv, L, D]``: a row is 8 pieces of 256 B, L x 256 B apart).
-    ``ceiling``: the measured read+write copy rate the achieved rate is also read against.
+    ``ceiling``: the measured read+write copy rate the achieved rate is also read against;
+    ``pattern_ceiling``: that of a copy whose destination 32 KiB units lie at scattered places.
     ``cpu``: time the oracle's ``write_prefill`` (the reference's index + index_copy_ chain) on the
     host cores over 4 of the 28 layers."""
     from mini_infra_qwen3_amd import workloads as wl
@@ -309,6 +310,7 @@ def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "
                        f"{'token-major (the model' + chr(39) + 's K/V rows)' if layout == 'token' else 'head-major (the reference KVCache)'} source",
            "ms_per_launch": ms, "bytes_per_launch": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
            "frac_of_copy_ceiling": gbs / ceiling if ceiling else None,
+           "frac_of_scattered_write_copy": gbs / pattern_ceiling if pattern_ceiling else None,
            "traffic": profiled_traffic("reshape_and_cache" if layout == "head" else "reshape_and_cache_token")}
     if cpu:
         from oracle import torch_ref
@@ -333,10 +335,11 @@ def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "
 
 # -------------------------------------------------------------------------------- gather
 def bench_gather(steps: int, warmup: int, device: torch.device, ceiling: float | None = None,
-                 cpu: bool = False) -> dict:
+                 cpu: bool = False, pattern_ceiling: float | None = None) -> dict:
     """The chunked-prefill history gather (the reference's ``gather_blocks``), 28 layers: every chunk c of the 4
     prompts gathers its 128 c history blocks, one launch per chunk.  ``cpu``: the oracle's
-    ``gather_blocks`` on the host cores for one of the 28 layers."""
+    ``gather_blocks`` on the host cores for one of the 28 layers.  ``ceiling`` / ``pattern_ceiling``:
+    the read+write copy rates (contiguous / from source 32 KiB units at scattered places) it is read against."""
     from mini_infra_qwen3_amd import workloads as wl
     from mini_infra_qwen3_amd.worker import PagedKVCachePool
 
@@ -367,6 +370,7 @@ def bench_gather(steps: int, warmup: int, device: torch.device, ceiling: float |
     out = {"workload": "history gather, 28 layers, 4 prompts x 16384 tokens in 2048-token chunks (7 launches)",
            "ms_per_prompt_set": ms, "bytes": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
            "frac_of_copy_ceiling": gbs / ceiling if ceiling else None,
+           "frac_of_scattered_read_copy": gbs / pattern_ceiling if pattern_ceiling else None,
            "traffic_per_prompt_set": profiled_traffic("gather_blocks")}
     if cpu:
         from oracle import torch_ref
@@ -392,8 +396,10 @@ def copy_ceiling(device: torch.device, nbytes: int = 2 << 30, reps: int = 5) -> 
     libmi_calib.so (16-byte non-temporal accesses, with non-temporal or device-scope streaming
     stores, contiguous spans per workgroup) over 2 GiB
     buffers, for read + write (copy), read-only and write-only, best of the library's launch
-    shapes.  The read + write rate is the ceiling scatter, gather and the block records are read
-    against, the read rate the one decode attention (a read stream) is."""
+    shapes, and for read + write copies whose destination (or source) 32 KiB units lie at scattered
+    places, the write (read) pattern of the scatter (gather).  The read + write rate is the ceiling
+    scatter, gather and the block records are read against, the read rate the one decode attention
+    (a read stream) is."""
     lib = ctypes.CDLL(CALIB_LIBRARY)
     lib.calib_stream.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
                                  ctypes.c_int32, ctypes.c_void_p]
@@ -408,9 +414,21 @@ def copy_ceiling(device: torch.device, nbytes: int = 2 << 30, reps: int = 5) -> 
     sink = torch.empty(max(lib.calib_groups(nbytes, v) for v in range(variants)), dtype=torch.int32, device=device)
     stream = torch.cuda.current_stream().cuda_stream
     result = {"workload": f"calibration streams over {nbytes >> 30} GiB buffers (libmi_calib.so)"}
-    for shape, name, moved in ((0, "read_write", 2 * nbytes), (1, "read", nbytes), (2, "write", nbytes)):
+    spans = []
+    for v in range(variants):
+        t, f, sp, st = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64(), ctypes.c_int32()
+        lib.calib_variant(v, ctypes.byref(t), ctypes.byref(f), ctypes.byref(sp), ctypes.byref(st))
+        spans.append(sp.value)
+    # The scattered copies move whole 32 KiB units (pool blocks) to or from scattered places, with
+    # workgroup spans of at most 32 KiB inside them.
+    for shape, name, moved, max_span in ((0, "read_write", 2 * nbytes, None), (1, "read", nbytes, None),
+                                         (2, "write", nbytes, None),
+                                         (3, "scattered_write_copy", 2 * nbytes, 32 << 10),
+                                         (4, "scattered_read_copy", 2 * nbytes, 32 << 10)):
         best = (0.0, None)
         for v in range(variants):
+            if max_span is not None and spans[v] > max_span:
+                continue
             def launch():
                 rc = lib.calib_stream(shape, dst.data_ptr(), src.data_ptr(), sink.data_ptr(), nbytes, v, stream)
                 if rc != 0:
@@ -783,16 +801,22 @@ def main() -> int:
         ceil = kernels["device_copy"]["ceiling"]
         log(f"device copy: {kernels['device_copy']['achieved_GBps']:.1f} GB/s; calibration streams: read+write "
             f"{ceil['read_write_GBps']:.0f}, read {ceil['read_GBps']:.0f}, write {ceil['write_GBps']:.0f} GB/s")
+        log(f"scattered-block copies: destination {ceil['scattered_write_copy_GBps']:.0f}, source "
+            f"{ceil['scattered_read_copy_GBps']:.0f} GB/s")
         kernels["scatter"] = bench_scatter(max(args.steps, 10), 3, device, "token", ceil["read_write_GBps"],
-                                           cpu=want_cpu)
+                                           cpu=want_cpu, pattern_ceiling=ceil["scattered_write_copy_GBps"])
         log(f"scatter: {kernels['scatter']['achieved_GBps']:.1f} GB/s "
-            f"({100 * kernels['scatter']['frac_of_copy_ceiling']:.1f}% of the copy ceiling)")
+            f"({100 * kernels['scatter']['frac_of_copy_ceiling']:.1f}% of the copy ceiling, "
+            f"{100 * kernels['scatter']['frac_of_scattered_write_copy']:.1f}% of the scattered-destination copy)")
         kernels["scatter_head_major_source"] = bench_scatter(max(args.steps, 10), 3, device, "head",
-                                                             ceil["read_write_GBps"])
+                                                             ceil["read_write_GBps"],
+                                                             pattern_ceiling=ceil["scattered_write_copy_GBps"])
         log(f"scatter, head-major source: {kernels['scatter_head_major_source']['achieved_GBps']:.1f} GB/s")
-        kernels["gather"] = bench_gather(max(args.steps // 2, 6), 2, device, ceil["read_write_GBps"], cpu=want_cpu)
+        kernels["gather"] = bench_gather(max(args.steps // 2, 6), 2, device, ceil["read_write_GBps"], cpu=want_cpu,
+                                         pattern_ceiling=ceil["scattered_read_copy_GBps"])
         log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s "
-            f"({100 * kernels['gather']['frac_of_copy_ceiling']:.1f}% of the copy ceiling)")
+            f"({100 * kernels['gather']['frac_of_copy_ceiling']:.1f}% of the copy ceiling, "
+            f"{100 * kernels['gather']['frac_of_scattered_read_copy']:.1f}% of the scattered-source copy)")
         # 20 untimed layers (~90 ms): with 3, the first timed layers of a process ran ~5% slow.
         kernels["chunked_prefill"] = bench_prefill(max(args.steps // 2, 5), 20, device, cpu=want_cpu)
         log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "

@@ -2,9 +2,10 @@
 // data-plane kernels' rates are read against (bench.py --only copy).  Not part of the paged-KV
 // C ABI: a separate library, libmi_calib.so.
 //
-// Three traffic shapes over contiguous buffers, 16-byte non-temporal accesses, each workgroup
-// streaming one contiguous span of `span` bytes with `kInFlight` pieces per lane in flight:
-//   copy  (read + write), read (loads folded into one word per workgroup), write (stores only).
+// Traffic shapes over 16-byte non-temporal accesses, each workgroup streaming one contiguous span of
+// `span` bytes with `kInFlight` pieces per lane in flight: copy (read + write), read (loads folded
+// into one word per workgroup), write (stores only), and copies whose destination or source 32 KiB
+// units lie at scattered places (the write pattern of the scatter, the read pattern of the gather).
 // A variant is (lanes per workgroup, pieces in flight, span, store form); bench.py sweeps them and
 // keeps the best of each shape.  Store forms: the non-temporal store, or the same store at device
 // scope as well (nt sc1: the line goes out to memory instead of staying dirty in the XCD's L2),
@@ -46,23 +47,32 @@ constexpr Variant kVariants[] = {
 };
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
+// permute 0: span i of the source to span i of the destination.  1 and 2 move whole 32 KiB units
+// (a pool block of one layer's K or V: 2^unit_shift spans): unit u goes to destination unit
+// (u * 0x9E3779B1) mod n (1: destination blocks at scattered places, the scatter's writes) or comes
+// from that source unit (2: the gather's reads), the spans inside a unit in order.  With n a power
+// of two (checked by the host) the odd multiplier makes it a permutation, and every span is whole.
 template <int kInFlight, bool kStream>
 __global__ void copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src, int64_t pieces,
-                            int64_t span_pieces) {
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * span_pieces;
-  const int64_t end = min(base + span_pieces, pieces);
+                            int64_t span_pieces, int32_t permute, int64_t unit_mask, int32_t unit_shift) {
+  const int64_t span = blockIdx.x;
+  const int64_t moved = ((((span >> unit_shift) * 0x9E3779B1LL) & unit_mask) << unit_shift) |
+                        (span & ((int64_t{1} << unit_shift) - 1));
+  const int64_t src_base = (permute == 2 ? moved : span) * span_pieces;
+  const int64_t dst_base = (permute == 1 ? moved : span) * span_pieces;
+  const int64_t n = min(span_pieces, pieces - span * span_pieces);
   const int64_t step = static_cast<int64_t>(blockDim.x) * kInFlight;
-  for (int64_t p0 = base + threadIdx.x; p0 < end; p0 += step) {
+  for (int64_t q0 = threadIdx.x; q0 < n; q0 += step) {
     u32x4 v[kInFlight];
 #pragma unroll
     for (int k = 0; k < kInFlight; ++k) {
-      const int64_t p = p0 + static_cast<int64_t>(k) * blockDim.x;
-      if (p < end) v[k] = __builtin_nontemporal_load(src + p);
+      const int64_t q = q0 + static_cast<int64_t>(k) * blockDim.x;
+      if (q < n) v[k] = __builtin_nontemporal_load(src + src_base + q);
     }
 #pragma unroll
     for (int k = 0; k < kInFlight; ++k) {
-      const int64_t p = p0 + static_cast<int64_t>(k) * blockDim.x;
-      if (p < end) put<kStream>(dst + p, v[k]);
+      const int64_t q = q0 + static_cast<int64_t>(k) * blockDim.x;
+      if (q < n) put<kStream>(dst + dst_base + q, v[k]);
     }
   }
 }
@@ -129,24 +139,40 @@ extern "C" int64_t calib_groups(int64_t bytes, int32_t variant) {
   return (bytes + kVariants[variant].span - 1) / kVariants[variant].span;
 }
 
-// shape: 0 = copy (dst <- src), 1 = read (src, sink of calib_groups words), 2 = write (dst)
+// shape: 0 = copy (dst <- src), 1 = read (src, sink of calib_groups words), 2 = write (dst),
+// 3 = copy to destination 32 KiB units at scattered places, 4 = copy from source 32 KiB units at
+// scattered places (3 and 4 need spans of at most 32 KiB and a power-of-two number of whole units).
 extern "C" int32_t calib_stream(int32_t shape, void* dst, const void* src, void* sink, int64_t bytes,
                                 int32_t variant, void* stream) {
-  if (check_args(bytes, variant) || shape < 0 || shape > 2) return -1;
+  if (check_args(bytes, variant) || shape < 0 || shape > 4) return -1;
   if ((shape != 1 && !dst) || (shape != 2 && !src) || (shape == 1 && !sink)) return -1;
+  const bool copies = shape == 0 || shape >= 3;
   if ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15u) return -1;
   const Variant v = kVariants[variant];
   const int64_t pieces = bytes / 16, span_pieces = v.span / 16;
   const int64_t groups = (pieces + span_pieces - 1) / span_pieces;
   if (groups > 0x7fffffff) return -1;
+  constexpr int64_t kUnitBytes = 32 << 10;
+  int32_t unit_shift = 0;
+  int64_t unit_mask = 0;
+  if (shape >= 3) {
+    if (v.span > kUnitBytes || kUnitBytes % v.span != 0 || bytes % kUnitBytes != 0) return -1;
+    const int64_t units = bytes / kUnitBytes;
+    if ((units & (units - 1)) != 0) return -1;
+    while ((int64_t{1} << unit_shift) * v.span < kUnitBytes) ++unit_shift;
+    unit_mask = units - 1;
+  }
+  const int32_t permute = shape == 3 ? 1 : (shape == 4 ? 2 : 0);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<uint32_t>(groups));
   u32x4* d = static_cast<u32x4*>(dst);
   const u32x4* r = static_cast<const u32x4*>(src);
   uint32_t* k = static_cast<uint32_t*>(sink);
-#define CALIB_LAUNCH(N)                                                                        \
-  if (shape == 0 && v.stream) copy_kernel<N, true><<<grid, v.threads, 0, s>>>(d, r, pieces, span_pieces); \
-  else if (shape == 0) copy_kernel<N, false><<<grid, v.threads, 0, s>>>(d, r, pieces, span_pieces);       \
+#define CALIB_LAUNCH(N)                                                                                 \
+  if (copies && v.stream)                                                                         \
+    copy_kernel<N, true><<<grid, v.threads, 0, s>>>(d, r, pieces, span_pieces, permute, unit_mask, unit_shift);  \
+  else if (copies)                                                                                \
+    copy_kernel<N, false><<<grid, v.threads, 0, s>>>(d, r, pieces, span_pieces, permute, unit_mask, unit_shift); \
   else if (shape == 1) read_kernel<N><<<grid, v.threads, 0, s>>>(r, k, pieces, span_pieces);             \
   else if (v.stream) write_kernel<N, true><<<grid, v.threads, 0, s>>>(d, pieces, span_pieces);           \
   else write_kernel<N, false><<<grid, v.threads, 0, s>>>(d, pieces, span_pieces);
