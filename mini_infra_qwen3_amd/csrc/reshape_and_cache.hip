@@ -30,7 +30,9 @@
 // 128 x 4, 256 x 2) 5.48-6.14.  Device-scope streaming stores (store_stream, which the gather and
 // the block records use) against a copy ceiling of 6.69 TB/s with the same stores: 6.07-6.22 TB/s
 // at 2 tokens per group against 6.14-6.30 with non-temporal stores; 4, 8 or 16 tokens per group
-// with either store 5.14-5.76.
+// with either store 5.14-5.76.  Tokens taken in slot order instead of prompt order: no change
+// (6.18-6.20 against 6.15-6.28; 99.9% of consecutive tokens already have consecutive slots).
+// Groups mapped so that each XCD takes a contiguous run of tokens: 6.06-6.15 against 6.13-6.22.
 #ifndef MI_SCATTER_TOKENS_PER_GROUP
 #define MI_SCATTER_TOKENS_PER_GROUP 2
 #endif
