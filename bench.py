@@ -8,7 +8,8 @@ algorithmic HBM bandwidth of the whole step: per layer sum(context) x 4096 B of 
 plus Q read, O written and the appended K/V rows, divided by the timed step time.
 
 Also measured in the same run (reported under ``kernels``): the 28-layer prefill scatter of
-32 prompts U[128, 2048] with churned block tables, the block-table history gather, the MFMA
+32 prompts U[128, 2048] and the block-table history gather, each on fragmented block tables (a
+free list reordered by decode-style interleaved growth) and on near-sequential ones, the MFMA
 chunked-prefill attention of 4 x 16384-token prompts in 2048-token chunks, and the KV block
 records of 2048 blocks (pack / unpack in HBM, swap to pinned host memory and back); and (under ``e2e``)
 the continuous-batching run of a random-init Qwen3-0.6B: 128 requests at 20 req/s, prompts
@@ -275,9 +276,11 @@ def cpu_baseline_decode_full(w, device: torch.device, slice_size: int = 32) -> d
 
 # ------------------------------------------------------------------------------- scatter
 def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "token",
-                  ceiling: float | None = None, cpu: bool = False, pattern_ceiling: float | None = None) -> dict:
-    """The 28-layer prefill store of 32 prompts U[128, 2048] (40,636 tokens) into churned
-    blocks, one launch.  ``layout`` of the source ``[B, Hkv, L, D]`` per layer: ``token`` -- the
+                  ceiling: float | None = None, cpu: bool = False, pattern_ceiling: float | None = None,
+                  tables: str = "fragmented") -> dict:
+    """The 28-layer prefill store of 32 prompts U[128, 2048] (40,636 tokens) into blocks from a
+    churned ``FreeKVCacheBlockQueue`` (``tables``: ``fragmented`` or ``near_sequential``, the
+    kinds of ``workloads.TABLE_KINDS``), one launch.  ``layout`` of the source ``[B, Hkv, L, D]`` per layer: ``token`` -- the
     memory of the HIP model's prefill K/V (``mi_qk_norm_rope`` writes ``[T, Hkv, D]`` rows, viewed
     as ``[B, Hkv, L, D]``), so a token's 2 KiB row is contiguous; ``head`` -- the reference's
     ``KVCache`` layout (contiguous ``[B, Hkv, L, D]``: a row is 8 pieces of 256 B, L x 256 B apart).
@@ -288,7 +291,7 @@ def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "
     from mini_infra_qwen3_amd import workloads as wl
     from mini_infra_qwen3_amd.worker import KVCache, PagedKVCachePool
 
-    w = wl.prefill_scatter(seed=0, device=device)
+    w = wl.prefill_scatter(seed=0, device=device, tables=tables)
     sources = w.sources
     if layout == "token":
         sources = sources.transpose(-3, -2).contiguous().transpose(-3, -2)
@@ -306,8 +309,10 @@ def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "
     ms = timer.mean_ms()
     moved = 2 * w.num_tokens * wl.NUM_LAYERS * wl.KV_BYTES_PER_TOKEN_LAYER  # read + write
     gbs = moved / (ms * 1e-3) / 1e9
-    out = {"workload": f"prefill scatter, 28 layers, 32 prompts U[128,2048] ({w.num_tokens} tokens), churned tables, "
-                       f"{'token-major (the model' + chr(39) + 's K/V rows)' if layout == 'token' else 'head-major (the reference KVCache)'} source",
+    source = "token-major (the model's K/V rows)" if layout == "token" else "head-major (the reference KVCache)"
+    out = {"workload": f"prefill scatter, 28 layers, 32 prompts U[128,2048] ({w.num_tokens} tokens), "
+                       f"{tables.replace('_', '-')} tables, {source} source",
+           "tables": tables, "consecutive_block_fraction": round(wl.consecutive_fraction(w.tables), 4),
            "ms_per_launch": ms, "bytes_per_launch": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
            "frac_of_copy_ceiling": gbs / ceiling if ceiling else None,
            "frac_of_scattered_write_copy": gbs / pattern_ceiling if pattern_ceiling else None,
@@ -335,15 +340,16 @@ def bench_scatter(steps: int, warmup: int, device: torch.device, layout: str = "
 
 # -------------------------------------------------------------------------------- gather
 def bench_gather(steps: int, warmup: int, device: torch.device, ceiling: float | None = None,
-                 cpu: bool = False, pattern_ceiling: float | None = None) -> dict:
+                 cpu: bool = False, pattern_ceiling: float | None = None, tables: str = "fragmented") -> dict:
     """The chunked-prefill history gather (the reference's ``gather_blocks``), 28 layers: every chunk c of the 4
-    prompts gathers its 128 c history blocks, one launch per chunk.  ``cpu``: the oracle's
+    prompts gathers its 128 c history blocks, one launch per chunk; block tables of kind ``tables``
+    (``fragmented`` or ``near_sequential``).  ``cpu``: the oracle's
     ``gather_blocks`` on the host cores for one of the 28 layers.  ``ceiling`` / ``pattern_ceiling``:
     the read+write copy rates (contiguous / from source 32 KiB units at scattered places) it is read against."""
     from mini_infra_qwen3_amd import workloads as wl
     from mini_infra_qwen3_amd.worker import PagedKVCachePool
 
-    w = wl.chunked_prefill(seed=0)
+    w = wl.chunked_prefill(seed=0, tables=tables)
     pool = PagedKVCachePool(wl.NUM_LAYERS, w.num_blocks, wl.BLOCK_SIZE, wl.NUM_KV_HEADS, wl.HEAD_DIM,
                             torch.bfloat16, device)
     pool.storage.view(torch.int16).random_(generator=torch.Generator(device=device).manual_seed(0))
@@ -367,7 +373,9 @@ def bench_gather(steps: int, warmup: int, device: torch.device, ceiling: float |
     ms = timer.mean_ms()
     moved = 2 * w.history_bytes_per_layer() * wl.NUM_LAYERS  # read history + write the gathered copy
     gbs = moved / (ms * 1e-3) / 1e9
-    out = {"workload": "history gather, 28 layers, 4 prompts x 16384 tokens in 2048-token chunks (7 launches)",
+    out = {"workload": f"history gather, 28 layers, 4 prompts x 16384 tokens in 2048-token chunks (7 launches), "
+                       f"{tables.replace('_', '-')} tables",
+           "tables": tables, "consecutive_block_fraction": round(wl.consecutive_fraction(w.tables), 4),
            "ms_per_prompt_set": ms, "bytes": moved, "achieved_GBps": gbs, "frac": gbs / HBM_PEAK_GBS,
            "frac_of_copy_ceiling": gbs / ceiling if ceiling else None,
            "frac_of_scattered_read_copy": gbs / pattern_ceiling if pattern_ceiling else None,
@@ -744,7 +752,8 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "scatter-head", "gather", "prefill",
+    parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "scatter-sequential", "scatter-head",
+                                           "gather", "gather-sequential", "prefill",
                                            "copy", "swap", "e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth", "all"],
                         default="all")
     args = parser.parse_args()
@@ -764,8 +773,10 @@ def main() -> int:
     single = {
         "copy": lambda: bench_copy(args.steps, device),
         "scatter": lambda: bench_scatter(args.steps, args.warmup, device),
+        "scatter-sequential": lambda: bench_scatter(args.steps, args.warmup, device, tables="near_sequential"),
         "scatter-head": lambda: bench_scatter(args.steps, args.warmup, device, layout="head"),
         "gather": lambda: bench_gather(args.steps, args.warmup, device),
+        "gather-sequential": lambda: bench_gather(args.steps, args.warmup, device, tables="near_sequential"),
         "prefill": lambda: bench_prefill(args.steps, args.warmup, device),
         "swap": lambda: bench_swap(args.steps, args.warmup, device),
         "decode-groups": lambda: bench_decode_groups(args.steps, args.warmup, device),
@@ -803,28 +814,32 @@ def main() -> int:
             f"{ceil['read_write_GBps']:.0f}, read {ceil['read_GBps']:.0f}, write {ceil['write_GBps']:.0f} GB/s")
         log(f"scattered-block copies: destination {ceil['scattered_write_copy_GBps']:.0f}, source "
             f"{ceil['scattered_read_copy_GBps']:.0f} GB/s")
-        kernels["scatter"] = bench_scatter(max(args.steps, 10), 3, device, "token", ceil["read_write_GBps"],
-                                           cpu=want_cpu, pattern_ceiling=ceil["scattered_write_copy_GBps"])
-        log(f"scatter: {kernels['scatter']['achieved_GBps']:.1f} GB/s "
-            f"({100 * kernels['scatter']['frac_of_copy_ceiling']:.1f}% of the copy ceiling, "
-            f"{100 * kernels['scatter']['frac_of_scattered_write_copy']:.1f}% of the scattered-destination copy)")
+        for key, kind in (("scatter", "fragmented"), ("scatter_near_sequential_tables", "near_sequential")):
+            kernels[key] = bench_scatter(max(args.steps, 10), 3, device, "token", ceil["read_write_GBps"],
+                                         cpu=want_cpu and kind == "fragmented",
+                                         pattern_ceiling=ceil["scattered_write_copy_GBps"], tables=kind)
+            r = kernels[key]
+            log(f"scatter, {kind} tables ({100 * r['consecutive_block_fraction']:.1f}% consecutive): "
+                f"{r['achieved_GBps']:.1f} GB/s ({100 * r['frac']:.1f}% of peak, "
+                f"{100 * r['frac_of_copy_ceiling']:.1f}% of the copy ceiling, "
+                f"{100 * r['frac_of_scattered_write_copy']:.1f}% of the scattered-destination copy)")
         kernels["scatter_head_major_source"] = bench_scatter(max(args.steps, 10), 3, device, "head",
                                                              ceil["read_write_GBps"],
                                                              pattern_ceiling=ceil["scattered_write_copy_GBps"])
         log(f"scatter, head-major source: {kernels['scatter_head_major_source']['achieved_GBps']:.1f} GB/s")
-        kernels["gather"] = bench_gather(max(args.steps // 2, 6), 2, device, ceil["read_write_GBps"], cpu=want_cpu,
-                                         pattern_ceiling=ceil["scattered_read_copy_GBps"])
-        log(f"gather: {kernels['gather']['achieved_GBps']:.1f} GB/s "
-            f"({100 * kernels['gather']['frac_of_copy_ceiling']:.1f}% of the copy ceiling, "
-            f"{100 * kernels['gather']['frac_of_scattered_read_copy']:.1f}% of the scattered-source copy)")
+        for key, kind in (("gather", "fragmented"), ("gather_near_sequential_tables", "near_sequential")):
+            kernels[key] = bench_gather(max(args.steps // 2, 6), 2, device, ceil["read_write_GBps"],
+                                        cpu=want_cpu and kind == "fragmented",
+                                        pattern_ceiling=ceil["scattered_read_copy_GBps"], tables=kind)
+            r = kernels[key]
+            log(f"gather, {kind} tables ({100 * r['consecutive_block_fraction']:.1f}% consecutive): "
+                f"{r['achieved_GBps']:.1f} GB/s ({100 * r['frac']:.1f}% of peak, "
+                f"{100 * r['frac_of_copy_ceiling']:.1f}% of the copy ceiling, "
+                f"{100 * r['frac_of_scattered_read_copy']:.1f}% of the scattered-source copy)")
         # 20 untimed layers (~90 ms): with 3, the first timed layers of a process ran ~5% slow.
         kernels["chunked_prefill"] = bench_prefill(max(args.steps // 2, 5), 20, device, cpu=want_cpu)
         log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "
             f"{kernels['chunked_prefill']['achieved_TFLOPs']:.1f} TFLOP/s")
-        torch.cuda.empty_cache()
-        kernels["decode_gqa_groups"] = bench_decode_groups(args.steps, 2, device)
-        log("decode by GQA group: " + ", ".join(f"{g}: {r['achieved_GBps']:.0f} GB/s"
-                                                 for g, r in kernels["decode_gqa_groups"]["groups"].items()))
         torch.cuda.empty_cache()
         kernels["kv_block_swap"] = bench_swap(max(args.steps // 4, 3), 1, device)
         sw = kernels["kv_block_swap"]

@@ -257,7 +257,8 @@ int32_t mi_chunked_prefill_attention(void* out, int64_t out_row_stride, int64_t 
  * slot_mapping are ignored: the arguments and outputs of mi_paged_decode_attention (no
  * workspace).  With q_weight != NULL the prologue of mi_paged_decode_attention_fused runs first
  * (q / k RMSNorm + RoPE of the raw projection rows q / k, K/V rows into their slots; the q head
- * stride is then 128), bit-identical to mi_qk_norm_rope.  Out-of-range table ids read block 0.
+ * stride is then 128), bit-identical to mi_qk_norm_rope; as in the mixed form's decode rows,
+ * context 0 marks a padding row, which appends nothing.  Out-of-range table ids read block 0.
  * Any context length (contexts longer than the LDS cache recompute their scores per pass).
  *
  * mi_chunked_prefill_attention_exact -- chunked prefill: the arguments and layout of

@@ -129,9 +129,10 @@ __device__ __forceinline__ void reference_scores(f32x4& v, float scale) {
 // and the load).  Issued by inline assembly: the compiler's own form ties every later LDS read to
 // the completion of all such loads (it cannot tell the two tile buffers apart), which would wait
 // for tile t + 1 before reading tile t.  The compiler does not see these loads, so the kernel waits
-// for them itself (vmcnt(0) before each tile barrier) and sets M0 nowhere else.
+// for them itself (vmcnt(0) before each tile barrier).  The LDS address goes in through an M0
+// operand constraint, so the compiler writes M0 itself and knows its value across the asm.
 __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds) : "memory");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds) : "memory");
 }
 
 // One launch serves up to two sets of rows (a mixed step's chunk rows and its decode rows): the
@@ -573,6 +574,7 @@ extern "C" int32_t mi_chunked_prefill_attention(
   if (batch < 0 || padded_len < 0 || max_history_blocks < 0 || num_blocks < 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", name);
   if (batch == 0 || padded_len == 0) return ok();
+  if (const int32_t rc = reject_empty_pool(name, num_blocks, max_history_blocks > 0)) return rc;
   if (!out || !query || !key || !value || !start_lens || !chunk_lens ||
       (max_history_blocks > 0 && (!history_blocks || !key_pool || !value_pool)))
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", name);
@@ -634,6 +636,9 @@ extern "C" int32_t mi_mixed_paged_attention(
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", name);
   const bool chunks = prefill_rows > 0 && prefill_width > 0;
   if (!chunks && decode_rows == 0) return ok();
+  if (const int32_t rc = reject_empty_pool(name, num_blocks, (chunks && max_history_blocks > 0) ||
+                                                                 (decode_rows > 0 && max_blocks > 0)))
+    return rc;
   if (!out || !query || !key || !value || (chunks && (!start_lens || !chunk_lens)) ||
       (chunks && max_history_blocks > 0 && !history_blocks) ||
       (decode_rows > 0 && (!context_lens || !slot_mapping || (max_blocks > 0 && !block_tables))) ||

@@ -187,8 +187,9 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
         s_q[u][lane] = o0;
         s_q[u][lane + 64] = o1;
       } else {
+        // Context 0 marks a padding row: no append (as in the plain and mixed forms).
         const int64_t slot = a.slot_mapping[b * a.slot_stride];
-        if (slot >= 0 && slot < a.num_slots) {
+        if (slot >= 0 && slot < a.num_slots && a.context_lens[b * a.ctx_stride] > 0) {
           uint16_t* kd = a.key_pool + slot * row_elems + g * kHeadDim;
           uint16_t* vd = a.value_pool + slot * row_elems + g * kHeadDim;
           const uint16_t* vs = a.v_new + b * a.v_row + g * kHeadDim;
@@ -884,6 +885,7 @@ extern "C" int32_t mi_paged_decode_attention_exact(
   const char* what = "mi_paged_decode_attention_exact";
   if (batch < 0 || max_blocks < 0 || num_blocks < 0) return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
   if (batch == 0) return ok();
+  if (const int32_t rc = reject_empty_pool(what, num_blocks, max_blocks > 0)) return rc;
   if (const int32_t rc = check_exact_heads(what, num_heads, num_kv_heads, head_dim, block_size)) return rc;
   const bool prologue = q_weight != nullptr;
   if (!out || !q || !key_pool || !value_pool || !context_lens || (max_blocks > 0 && !block_tables))
@@ -915,7 +917,8 @@ extern "C" int32_t mi_paged_decode_attention_exact(
   a.cos = static_cast<const uint16_t*>(cos);
   a.sin = static_cast<const uint16_t*>(sin);
   a.eps = eps;
-  a.slot_mapping = slot_mapping;
+  // The plain form appends nothing: k, v and slot_mapping are ignored without the prologue.
+  a.slot_mapping = prologue ? slot_mapping : nullptr;
   a.slot_stride = slot_stride;
   a.num_slots = num_blocks * kBlockSize;
   a.key_pool = static_cast<uint16_t*>(key_pool);
@@ -965,6 +968,7 @@ extern "C" int32_t mi_chunked_prefill_attention_exact(
   if (batch < 0 || padded_len < 0 || max_history_blocks < 0 || num_blocks < 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
   if (batch == 0 || padded_len == 0) return ok();
+  if (const int32_t rc = reject_empty_pool(what, num_blocks, max_history_blocks > 0)) return rc;
   if (const int32_t rc = check_exact_heads(what, num_heads, num_kv_heads, head_dim, block_size)) return rc;
   if (!out || !query || !key || !value || !start_lens || !chunk_lens ||
       (max_history_blocks > 0 && (!history_blocks || !key_pool || !value_pool)))
@@ -1026,6 +1030,9 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
   const bool chunks = prefill_rows > 0 && prefill_width > 0;
   if (!chunks && decode_rows == 0) return ok();
+  if (const int32_t rc = reject_empty_pool(what, num_blocks, (chunks && max_history_blocks > 0) ||
+                                                                 (decode_rows > 0 && max_blocks > 0)))
+    return rc;
   if (const int32_t rc = check_exact_heads(what, num_heads, num_kv_heads, head_dim, block_size)) return rc;
   const bool pools = decode_rows > 0 || max_history_blocks > 0;
   if (!out || !query || !key || !value || (chunks && (!start_lens || !chunk_lens)) ||

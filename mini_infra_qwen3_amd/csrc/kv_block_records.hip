@@ -46,6 +46,19 @@ constexpr int kUnroll = MI_RECORDS_UNROLL;
 constexpr int kSplit = MI_RECORDS_SPLIT;  // workgroups per block piece, each a contiguous 1 / kSplit
 constexpr bool kNtLoad = MI_RECORDS_NT_LOAD != 0;    // non-temporal loads of the source
 constexpr bool kNtStore = MI_RECORDS_NT_STORE != 0;  // non-temporal stores of the destination
+#ifndef MI_RECORDS_XCD_RUN_PACK
+#define MI_RECORDS_XCD_RUN_PACK 64
+#endif
+#ifndef MI_RECORDS_XCD_RUN_UNPACK
+#define MI_RECORDS_XCD_RUN_UNPACK 0
+#endif
+// Consecutive workgroups per XCD run (0: round-robin launch order): within each super-run of
+// kXcds * run workgroups, those on XCD i take [i run, (i + 1) run) in order.  Measured on MI355X
+// (2048 records of the Qwen3-0.6B pool, two repetitions): pack 6.27-6.33 TB/s without runs,
+// 6.23-6.28 at 16, 6.43 at 32, 6.41-6.46 at 64, 6.42-6.43 at 128 and 256; unpack 5.79 without,
+// 5.52-5.76 with runs of 16-256.
+constexpr int kXcdRunPack = MI_RECORDS_XCD_RUN_PACK;
+constexpr int kXcdRunUnpack = MI_RECORDS_XCD_RUN_UNPACK;
 
 struct RecordArgs {
   char* pool[2][kMaxLayersPerLaunch];  // [0] = key pools, [1] = value pools of this launch's layers
@@ -57,14 +70,24 @@ struct RecordArgs {
   int32_t layer0;   // first layer of this launch
   int32_t layers;   // layers of this launch
   uint32_t pieces;  // block_bytes / sizeof(V)
+  uint32_t groups;  // workgroups of this launch
 };
 
 // kPack: block -> record (an out-of-range block id reads the null block 0, as every read does).
 // !kPack: record -> block (an out-of-range block id is skipped, as every write is).
 template <typename V, bool kPack>
 __global__ __launch_bounds__(kThreads) void kv_records_kernel(const RecordArgs a) {
-  const uint32_t part = blockIdx.x % kSplit;
-  const uint32_t piece_id = blockIdx.x / kSplit;
+  constexpr int kXcdRun = kPack ? kXcdRunPack : kXcdRunUnpack;
+  uint32_t x = blockIdx.x;
+  if (kXcdRun > 0) {
+    constexpr uint32_t kSuper = static_cast<uint32_t>(kXcds) * kXcdRun;
+    if (x < a.groups / kSuper * kSuper) {
+      const uint32_t base = x / kSuper * kSuper, r = x - base;
+      x = base + (r % kXcds) * kXcdRun + r / kXcds;
+    }
+  }
+  const uint32_t part = x % kSplit;
+  const uint32_t piece_id = x / kSplit;
   const int kv = piece_id & 1;
   const int layer = (piece_id >> 1) % a.layers;
   const int64_t i = (piece_id >> 1) / a.layers;
@@ -100,6 +123,7 @@ int32_t launch_records(const char* what, void* records, const void* const* key_p
   if (num_records < 0 || num_layers < 0 || num_blocks < 0 || block_bytes < 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
   if (num_records == 0 || num_layers == 0 || block_bytes == 0) return ok();
+  if (const int32_t rc = reject_empty_pool(what, num_blocks, kPack)) return rc;
   if (!records || !key_pools || !value_pools || !block_ids)
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
   if (num_records * kSplit * 2 * kMaxLayersPerLaunch > 0x7fffffff)
@@ -131,7 +155,8 @@ int32_t launch_records(const char* what, void* records, const void* const* key_p
     }
     a.layer0 = l0;
     a.layers = nl;
-    const dim3 grid(static_cast<uint32_t>(num_records * nl * 2 * kSplit), 1, 1);
+    a.groups = static_cast<uint32_t>(num_records * nl * 2 * kSplit);
+    const dim3 grid(a.groups, 1, 1);
     if (piece == 16)
       kv_records_kernel<u32x4, kPack><<<grid, kThreads, 0, s>>>(a);
     else if (piece == 4)

@@ -46,16 +46,28 @@ __device__ __forceinline__ void store_vec(T* p, const T& v) {
 // a 2 GiB copy streams 6.69-6.71 TB/s with these stores against 6.48-6.50 with non-temporal ones;
 // the gather and the KV record copies gain 2-3%, while the scatter's 2 KiB rows at random slots
 // lose 2% and keep store_vec.  Other vector types take store_vec.
+// A VMEM store of more than 8 bytes needs a wait state before a VALU instruction may overwrite its
+// data VGPRs.  The compiler inserts it after the stores it emits, but it cannot see into this asm,
+// so the asm carries its own (s_nop 1: two wait states); without it, register reuse right after the
+// store can send the new values.
 template <bool kNt, typename T>
 __device__ __forceinline__ void store_stream(T* p, const T& v) {
   if constexpr (kNt && __is_same(T, u32x4)) {
-    asm volatile("global_store_dwordx4 %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+    asm volatile("global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
   } else {
     store_vec<kNt>(p, v);
   }
 }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// An out-of-range block id reads the null block 0, which an empty pool does not have: a call that
+// would read any block of a pool with no blocks is an invalid argument, rejected before launch.
+inline int32_t reject_empty_pool(const char* what, int64_t num_blocks, bool reads_blocks) {
+  if (num_blocks == 0 && reads_blocks)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: the pool has no blocks to read", what);
+  return MI_OK;
+}
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

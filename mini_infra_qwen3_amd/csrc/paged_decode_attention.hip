@@ -1003,6 +1003,7 @@ extern "C" int32_t mi_paged_decode_attention(void* out, int64_t out_row_stride, 
   if (batch < 0 || max_blocks < 0 || num_blocks < 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention: negative size");
   if (batch == 0) return ok();
+  if (const int32_t rc = reject_empty_pool("mi_paged_decode_attention", num_blocks, max_blocks > 0)) return rc;
   if (!out || !query || !key_pool || !value_pool || !context_lens || (max_blocks > 0 && !block_tables))
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention: null pointer argument");
   if (const int32_t rc = check_heads("mi_paged_decode_attention", num_heads, num_kv_heads, head_dim, block_size))
@@ -1069,6 +1070,7 @@ extern "C" int32_t mi_paged_decode_attention_fused(
   if (batch < 0 || max_blocks < 0 || num_blocks < 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: negative size");
   if (batch == 0) return ok();
+  if (const int32_t rc = reject_empty_pool("mi_paged_decode_attention_fused", num_blocks, max_blocks > 0)) return rc;
   if (!q || !k || !v || !q_weight || !k_weight || !cos || !sin || !slot_mapping || !q_scratch)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_fused: null pointer argument");
   if (num_blocks > INT64_MAX / kBlockSize)
@@ -1181,6 +1183,8 @@ extern "C" int32_t mi_paged_decode_attention_noalloc(void* out, int64_t out_row_
   if (batch < 0 || max_blocks < 0 || num_blocks < 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_paged_decode_attention_noalloc: negative size");
   if (batch == 0) return ok();
+  if (const int32_t rc = reject_empty_pool("mi_paged_decode_attention_noalloc", num_blocks, max_blocks > 0))
+    return rc;
   if (const int32_t rc = check_heads("mi_paged_decode_attention_noalloc", num_heads, num_kv_heads, head_dim,
                                      block_size))
     return rc;

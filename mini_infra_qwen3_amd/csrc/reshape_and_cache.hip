@@ -6,57 +6,76 @@
 // per tensor per layer.
 //
 // Work mapping: a token is one destination K row and one V row of num_kv_heads * head_dim
-// elements (2 KiB each for 8 x 128 bf16), contiguous in the pool.  A workgroup of kThreads lanes
-// owns kTokensPerGroup consecutive tokens of one layer.
-//  * Row kernel (a token's K+V rows are a multiple of 256 16-byte pieces -- the Qwen3 shape):
-//    every lane owns fixed pieces of the row pair, so consecutive lanes move consecutive
-//    16-byte pieces of one slot row and each wavefront store is a fully coalesced 1 KiB run.
-//    The group's (row, position, slot) triples are staged once through LDS (one coalesced
-//    read), then kUnroll tokens' loads are issued before their stores.
+// elements (2 KiB each for 8 x 128 bf16), contiguous in the pool.
+//  * Span kernel (16-byte aligned rows and strides -- every real shape): grid z picks K or V, and
+//    a workgroup moves the rows of kSpanTokens consecutive index entries of one layer.  Lane i of a
+//    128-lane row team moves 16-byte piece i (+ 128 k) of a token's row, so each wavefront access
+//    is one contiguous 1 KiB run of a row.  The (row, position, slot) triples are wave-uniform and
+//    read with scalar loads, all before the first data load; every data load of a lane is issued
+//    before its first store.
 //  * Generic kernel (any other row size or misaligned strides): flat piece index with
 //    element-size pieces; used by small shapes only.
+//
+// XCD runs.  Workgroups are dealt round-robin to the 8 XCDs.  Taken in index order, two tokens
+// whose rows share an aligned 4 KiB region of the source or of the pool then land on different
+// XCDs, and on MI355X that costs ~3% per side.  The prefill store always has such tokens: prompts
+// are left-padded in the source, and each prompt starts on a block boundary in the pool, so the
+// two sides' alignments differ per prompt.  The kernel therefore maps blockIdx so that each XCD
+// takes runs of kXcdRun consecutive token groups.
+//
+// Measured on MI355X (28-layer prefill store of 32 prompts U[128, 2048], 40,636 tokens, token-major
+// source rows; two repetitions in one process; read + write copy ceiling 6.64-6.72 TB/s, copy into
+// 32 KiB units at scattered places 5.63-5.76):
+//   form (lanes x tokens per workgroup, store, XCD run)   near-sequential tables   fragmented tables
+//   128 x 1, non-temporal, runs of 128                       6.56-6.58 TB/s           5.87-5.88
+//   256 x 2 (one token per row team), nt, runs of 64         6.42-6.58                5.80-5.87
+//   256 x 2, nt, runs of 128 / 256 / 32 / 16                 6.48-6.55 / 6.49 / 6.40-6.46 / 6.07-6.09
+//   256 x 2, device-scope streaming stores, runs of 64       6.36-6.37                5.82-5.84
+//   128 x 2 (two tokens per lane), streaming, no runs        6.04-6.22                5.51-5.66
+//   the earlier LDS-staged form (K and V together, 2 tokens)  6.11-6.25                5.43-5.59
+//   16 tokens (one pool block) per workgroup, 128-1024 lanes 5.34-5.87                5.19-5.48
+//   workgroups looping over token groups (grid-stride)       4.99-5.86                4.91-5.79
+// Best case for comparison (packed source, identity slots, no runs): 6.50-6.53 TB/s.  Padding the
+// index so each contiguous run starts at index = slot (mod 16) adds under 1% and is not done.
 #include "mi_common.h"
 
-// Measured on MI355X (28-layer prefill store, 40k tokens, token-major source rows; three repetitions
-// in one process): 2 tokens per workgroup with one load per lane in flight moves 5.85-5.92 TB/s;
-// 2 tokens with 2 in flight 5.79-5.83, 4 with 2 5.57-5.75, 4 with 4 5.35-5.63, 8 with 2 or 4
-// 5.13-5.50, 16 with 4 5.22-5.51, 1 token 5.37-5.50.  Many small workgroups keep the most
-// independent 2 KiB row copies in flight.  Wider workgroups holding several tokens side by side
-// (MI_SCATTER_THREADS) measured slower on another machine: 512 lanes x 2 tokens 5.43-5.44 TB/s,
-// x 4 tokens 5.84-5.92, 1024 x 4 5.40-5.57, against 6.04-6.09 for 256 x 2.  Narrower ones, three
-// repetitions against the read + write copy ceiling of the same process (6.44 TB/s): 128 lanes x 2
-// tokens with both in flight 6.14-6.21 TB/s (95-96%), 256 x 2 with one 6.05-6.17, 128 x 1 token
-// 5.93-6.09, 64 lanes 5.45-5.75; K and V rows in separate workgroups (128 x 2 with 2 in flight,
-// 128 x 4, 256 x 2) 5.48-6.14.  Device-scope streaming stores (store_stream, which the gather and
-// the block records use) against a copy ceiling of 6.69 TB/s with the same stores: 6.07-6.22 TB/s
-// at 2 tokens per group against 6.14-6.30 with non-temporal stores; 4, 8 or 16 tokens per group
-// with either store 5.14-5.76.  Tokens taken in slot order instead of prompt order: no change
-// (6.18-6.20 against 6.15-6.28; 99.9% of consecutive tokens already have consecutive slots).
-// Groups mapped so that each XCD takes a contiguous run of tokens: 6.06-6.15 against 6.13-6.22.
-// Layers interleaved in dispatch order (all layers of a token group together) instead of one
-// layer's groups after another: 5.64-5.88 against 6.16-6.23.
-#ifndef MI_SCATTER_TOKENS_PER_GROUP
-#define MI_SCATTER_TOKENS_PER_GROUP 2
-#endif
-#ifndef MI_SCATTER_UNROLL
-#define MI_SCATTER_UNROLL 2
-#endif
 #ifndef MI_SCATTER_NT
 #define MI_SCATTER_NT 1
+#endif
+#ifndef MI_SCATTER_SPAN_THREADS
+#define MI_SCATTER_SPAN_THREADS 128
+#endif
+#ifndef MI_SCATTER_SPAN_TOKENS
+#define MI_SCATTER_SPAN_TOKENS 1
+#endif
+#ifndef MI_SCATTER_SPLIT_KV
+#define MI_SCATTER_SPLIT_KV 1
+#endif
+#ifndef MI_SCATTER_STREAM
+#define MI_SCATTER_STREAM 0
+#endif
+#ifndef MI_SCATTER_XCD_RUN
+#define MI_SCATTER_XCD_RUN 128
+#endif
+#ifndef MI_SCATTER_NARROW
+#define MI_SCATTER_NARROW 1
 #endif
 
 namespace mi {
 namespace {
 
-#ifndef MI_SCATTER_THREADS
-#define MI_SCATTER_THREADS 128
-#endif
-constexpr int kThreads = MI_SCATTER_THREADS;
-constexpr int kTokensPerGroup = MI_SCATTER_TOKENS_PER_GROUP;
-constexpr int kUnroll = MI_SCATTER_UNROLL;
 constexpr bool kNt = MI_SCATTER_NT != 0;  // non-temporal source loads and pool stores
+constexpr int kGenericThreads = 128;
 constexpr int kGenericUnroll = 8;
 constexpr int kGenericTokensPerGroup = 8;
+constexpr int kRowLanes = 128;  // lanes of a row team
+constexpr int kSpanThreads = MI_SCATTER_SPAN_THREADS;
+constexpr int kSpanTokens = MI_SCATTER_SPAN_TOKENS;
+constexpr bool kSplitKv = MI_SCATTER_SPLIT_KV != 0;        // K and V rows in separate workgroups
+constexpr bool kStreamStores = MI_SCATTER_STREAM != 0;     // device-scope streaming pool stores
+constexpr int kXcdRun = MI_SCATTER_XCD_RUN;                // token groups per XCD run (0: none)
+static_assert(kSpanThreads % kRowLanes == 0 && kSpanTokens % (kSpanThreads / kRowLanes) == 0,
+              "span kernel: whole row teams, whole tokens per team");
 
 struct ScatterArgs {
   const char* key_src[kMaxLayersPerLaunch];
@@ -77,7 +96,8 @@ struct ScatterArgs {
   uint32_t head_bytes;       // bytes of one head (head_dim * elem)
   uint32_t chunks_per_head;  // head_bytes / piece
   uint32_t chunks_per_row;   // num_kv_heads * chunks_per_head
-  int32_t tokens_per_group;  // row kernel: tokens per workgroup (<= kTokensPerGroup)
+  int32_t tokens_per_group;  // span kernel: index entries per workgroup (<= kSpanTokens)
+  int64_t groups;            // token groups: ceil(num_tokens / tokens_per_group)
 };
 
 // Source byte offsets of token i for K and V; slot -1 when the token is skipped.
@@ -98,70 +118,124 @@ __device__ __forceinline__ TokenRef token_ref(const ScatterArgs& a, int64_t i) {
   return t;
 }
 
-// Row kernel: 2 * chunks_per_row (16-byte pieces per token) is a multiple of kThreads.
-__global__ __launch_bounds__(kThreads) void reshape_and_cache_rows(const ScatterArgs a) {
-  __shared__ int64_t s_key[kTokensPerGroup], s_value[kTokensPerGroup], s_slot[kTokensPerGroup];
+// kNarrow: every source and pool byte offset fits in 32 bits (checked by the host), so offsets are
+// formed with 32-bit multiplies.  kRowContig: a token's heads are adjacent in the source (the
+// model's token-major K/V rows), so piece p of the row is at byte 16 p.
+template <bool kNarrow, bool kRowContig>
+__global__ __launch_bounds__(kSpanThreads) void reshape_and_cache_span(const ScatterArgs a) {
+  constexpr int kSide = kSpanThreads / kRowLanes;  // row teams (tokens side by side)
+  constexpr int kPer = kSpanTokens / kSide;        // tokens per lane
+  constexpr int kKv = kSplitKv ? 1 : 2;
   const int layer = blockIdx.y;
-  const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * a.tokens_per_group;
-  const int ntok = static_cast<int>(min(static_cast<int64_t>(a.tokens_per_group), a.num_tokens - tok0));
-  if (static_cast<int>(threadIdx.x) < ntok) {
-    const TokenRef t = token_ref(a, tok0 + threadIdx.x);
-    s_key[threadIdx.x] = t.key_off;
-    s_value[threadIdx.x] = t.value_off;
-    s_slot[threadIdx.x] = t.slot;
-  }
-  __syncthreads();
-
-  const char* key_src = a.key_src[layer];
-  const char* value_src = a.value_src[layer];
-  char* key_pool = a.key_pool[layer];
-  char* value_pool = a.value_pool[layer];
-  // Lanes per token: all of them when a token has at least kThreads pieces, else one piece each
-  // and kThreads / per_token tokens side by side.
-  const uint32_t per_token = 2u * a.chunks_per_row;
-  const uint32_t lanes = per_token < kThreads ? per_token : kThreads;
-  const int side = static_cast<int>(kThreads / lanes);
-  const int t_lane = static_cast<int>(threadIdx.x / lanes);
-  for (uint32_t c = threadIdx.x % lanes; c < per_token; c += lanes) {
-    // Fixed piece of this lane: K or V, head h, 16-byte column j.
-    const bool is_value = c >= a.chunks_per_row;
-    const uint32_t w = is_value ? c - a.chunks_per_row : c;
-    const uint32_t h = w / a.chunks_per_head;
-    const uint32_t j = w - h * a.chunks_per_head;
-    const char* src = (is_value ? value_src : key_src) + h * (is_value ? a.value_head : a.key_head) + j * 16u;
-    char* dst = (is_value ? value_pool : key_pool) + w * 16u;
-    const int64_t* s_off = is_value ? s_value : s_key;
-    for (int t0 = t_lane; t0 < ntok; t0 += side * kUnroll) {
-      u32x4 val[kUnroll];
-#pragma unroll
-      for (int k = 0; k < kUnroll; ++k) {
-        const int t = t0 + k * side;
-        if (t < ntok && s_slot[t] >= 0) val[k] = load_vec<kNt>(reinterpret_cast<const u32x4*>(src + s_off[t]));
-      }
-#pragma unroll
-      for (int k = 0; k < kUnroll; ++k) {
-        const int t = t0 + k * side;
-        if (t < ntok && s_slot[t] >= 0) store_vec<kNt>(reinterpret_cast<u32x4*>(dst + s_slot[t] * a.row_bytes), val[k]);
-      }
+  // A row team is two whole wavefronts, so its index is wave-uniform.
+  const int team = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kRowLanes);
+  const uint32_t lane = threadIdx.x % kRowLanes;
+  int64_t g = blockIdx.x;
+  if (kXcdRun > 0) {
+    // Within each super-run of kXcds * kXcdRun groups, the workgroups that land on XCD x (every
+    // kXcds-th) take groups [x kXcdRun, (x + 1) kXcdRun) in order; the partial tail keeps identity.
+    constexpr int64_t kSuper = static_cast<int64_t>(kXcds) * kXcdRun;
+    if (g < a.groups / kSuper * kSuper) {
+      const int64_t base = g / kSuper * kSuper, r = g - base;
+      g = base + (r % kXcds) * kXcdRun + r / kXcds;
     }
+  }
+  const int64_t tok0 = g * a.tokens_per_group;
+  const int ntok = static_cast<int>(min(static_cast<int64_t>(a.tokens_per_group), a.num_tokens - tok0));
+  // All index loads first (clamped to the group's last entry so every address is valid).
+  int64_t slot[kPer], row[kPer], pos[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int64_t i = tok0 + min(team + k * kSide, ntok - 1);
+    slot[k] = a.slot_mapping[i * a.index_stride];
+    row[k] = a.token_rows ? a.token_rows[i * a.index_stride] : i;
+    pos[k] = a.token_positions ? a.token_positions[i * a.index_stride] : 0;
+  }
+  int64_t src_off[kKv][kPer], dst_off[kPer];
+  bool live[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    live[k] = team + k * kSide < ntok && static_cast<uint64_t>(slot[k]) < static_cast<uint64_t>(a.num_slots) &&
+              static_cast<uint64_t>(row[k]) < static_cast<uint64_t>(a.num_rows) &&
+              static_cast<uint64_t>(pos[k]) < static_cast<uint64_t>(a.num_positions);
+    int64_t key_off, value_off;
+    if (kNarrow) {
+      const uint32_t r = static_cast<uint32_t>(row[k]), q = static_cast<uint32_t>(pos[k]);
+      dst_off[k] = static_cast<uint32_t>(slot[k]) * a.row_bytes;
+      key_off = r * static_cast<uint32_t>(a.key_row) + q * static_cast<uint32_t>(a.key_pos);
+      value_off = r * static_cast<uint32_t>(a.value_row) + q * static_cast<uint32_t>(a.value_pos);
+    } else {
+      dst_off[k] = slot[k] * a.row_bytes;
+      key_off = row[k] * a.key_row + pos[k] * a.key_pos;
+      value_off = row[k] * a.value_row + pos[k] * a.value_pos;
+    }
+    // A skipped token still loads (offset 0 of the source, which the host guarantees is
+    // non-empty), so every lane's loads are unconditional and issue back to back; only its stores
+    // are skipped.
+    if (!live[k]) key_off = value_off = 0;
+    if (kSplitKv) {
+      src_off[0][k] = blockIdx.z ? value_off : key_off;
+    } else {
+      src_off[0][k] = key_off;
+      src_off[kKv - 1][k] = value_off;
+    }
+  }
+  const char* src_base[kKv];
+  char* dst_base[kKv];
+#pragma unroll
+  for (int kv = 0; kv < kKv; ++kv) {
+    const bool is_value = kSplitKv ? blockIdx.z != 0 : kv == 1;
+    src_base[kv] = is_value ? a.value_src[layer] : a.key_src[layer];
+    dst_base[kv] = is_value ? a.value_pool[layer] : a.key_pool[layer];
+  }
+  // Passes over the row are uniform (a lane past the row's end loads piece 0 and stores nothing),
+  // so the index triples stay in scalar registers.
+  const uint32_t passes = (a.chunks_per_row + kRowLanes - 1) / kRowLanes;
+  for (uint32_t pass = 0; pass < passes; ++pass) {
+    const uint32_t p = lane + pass * kRowLanes;
+    const bool in_row = p < a.chunks_per_row;
+    const uint32_t pc = in_row ? p : 0u;
+    const uint32_t h = kRowContig ? 0u : pc / a.chunks_per_head;
+    const uint32_t j = pc - h * a.chunks_per_head;
+    u32x4 val[kKv][kPer];
+#pragma unroll
+    for (int kv = 0; kv < kKv; ++kv) {
+      const bool is_value = kSplitKv ? blockIdx.z != 0 : kv == 1;
+      const char* src =
+          src_base[kv] + (kRowContig ? pc * 16u : h * (is_value ? a.value_head : a.key_head) + j * 16u);
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) val[kv][k] = load_vec<kNt>(reinterpret_cast<const u32x4*>(src + src_off[kv][k]));
+    }
+    if (!in_row) continue;
+#pragma unroll
+    for (int kv = 0; kv < kKv; ++kv)
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        if (!live[k]) continue;
+        u32x4* out = reinterpret_cast<u32x4*>(dst_base[kv] + p * 16u + dst_off[k]);
+        if (kStreamStores)
+          store_stream<kNt>(out, val[kv][k]);
+        else
+          store_vec<kNt>(out, val[kv][k]);
+      }
   }
 }
 
 // Generic kernel: flat piece index, any piece size V.
 template <typename V>
-__global__ __launch_bounds__(kThreads) void reshape_and_cache_generic(const ScatterArgs a) {
+__global__ __launch_bounds__(kGenericThreads) void reshape_and_cache_generic(const ScatterArgs a) {
   const int layer = blockIdx.y;
   const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * kGenericTokensPerGroup;
   const int64_t ntok = min(static_cast<int64_t>(kGenericTokensPerGroup), a.num_tokens - tok0);
   const uint32_t per_token = 2u * a.chunks_per_row;  // K row then V row
   const uint32_t n_items = static_cast<uint32_t>(ntok) * per_token;
 
-  for (uint32_t base = 0; base < n_items; base += kThreads * kGenericUnroll) {
+  for (uint32_t base = 0; base < n_items; base += kGenericThreads * kGenericUnroll) {
     V val[kGenericUnroll];
     V* dst[kGenericUnroll];
 #pragma unroll
     for (int k = 0; k < kGenericUnroll; ++k) {
-      const uint32_t f = base + k * kThreads + threadIdx.x;
+      const uint32_t f = base + k * kGenericThreads + threadIdx.x;
       dst[k] = nullptr;
       if (f < n_items) {
         const uint32_t t = f / per_token;
@@ -201,7 +275,8 @@ extern "C" int32_t mi_reshape_and_cache(const void* const* key_src, const void* 
   using namespace mi;
   if (num_tokens < 0 || num_layers < 0 || num_slots < 0 || num_src_rows < 0 || num_src_positions < 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_reshape_and_cache: negative size");
-  if (num_tokens == 0 || num_layers == 0) return ok();
+  // With no source rows or positions every token is skipped: nothing to write.
+  if (num_tokens == 0 || num_layers == 0 || num_src_rows == 0 || num_src_positions == 0) return ok();
   if (!key_src || !value_src || !key_pools || !value_pools || !slot_mapping)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_reshape_and_cache: null pointer argument");
   if (num_kv_heads <= 0 || head_dim <= 0 || (elem_bytes != 2 && elem_bytes != 4))
@@ -239,17 +314,34 @@ extern "C" int32_t mi_reshape_and_cache(const void* const* key_src, const void* 
   a.chunks_per_row = a.chunks_per_head * num_kv_heads;
   if (2ull * a.chunks_per_row * kGenericTokensPerGroup >= (1ull << 31))
     return fail(MI_ERR_UNSUPPORTED, "mi_reshape_and_cache: row of %u bytes too large", a.row_bytes);
-  const bool rows_kernel = wide && ((2u * a.chunks_per_row) % kThreads == 0 || kThreads % (2u * a.chunks_per_row) == 0);
-  // Few tokens (a decode append) spread one per workgroup over the CUs; many tokens (a prompt)
-  // go kTokensPerGroup per workgroup so each lane keeps kUnroll loads in flight.
+  const bool span_kernel = wide;
+  // Few tokens (a decode append) go one per workgroup, spread over the CUs; many tokens (a prompt)
+  // go kSpanTokens per workgroup.
   int64_t per_group = kGenericTokensPerGroup;
-  if (rows_kernel) {
+  if (span_kernel) {
     const int64_t spread = (num_tokens * num_layers + 2047) / 2048;
-    per_group = spread < 1 ? 1 : (spread > kTokensPerGroup ? kTokensPerGroup : spread);
+    per_group = spread < 1 ? 1 : (spread > kSpanTokens ? kSpanTokens : spread);
   }
   a.tokens_per_group = static_cast<int32_t>(per_group);
 
   const int64_t groups = (num_tokens + per_group - 1) / per_group;
+  a.groups = groups;
+  const bool row_contig = a.key_head == a.head_bytes && a.value_head == a.head_bytes;
+  // 32-bit offsets when every source byte a token can address and every pool byte fits (strides
+  // non-negative): the largest row and position, plus the largest head, plus one head.
+  bool narrow = MI_SCATTER_NARROW != 0;
+  for (int64_t st : strides) narrow = narrow && st >= 0 && st < (int64_t{1} << 32);
+  if (narrow) {
+    const __int128 last_key = static_cast<__int128>(num_src_rows - 1) * a.key_row +
+                              static_cast<__int128>(num_src_positions - 1) * a.key_pos +
+                              static_cast<__int128>(num_kv_heads - 1) * a.key_head + a.head_bytes;
+    const __int128 last_value = static_cast<__int128>(num_src_rows - 1) * a.value_row +
+                                static_cast<__int128>(num_src_positions - 1) * a.value_pos +
+                                static_cast<__int128>(num_kv_heads - 1) * a.value_head + a.head_bytes;
+    const __int128 pool_bytes = static_cast<__int128>(num_slots) * a.row_bytes;
+    const __int128 lim = static_cast<__int128>(1) << 32;
+    narrow = last_key <= lim && last_value <= lim && pool_bytes <= lim;
+  }
   if (groups > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "mi_reshape_and_cache: too many tokens");
   hipStream_t s = as_stream(stream);
   for (int l0 = 0; l0 < num_layers; l0 += kMaxLayersPerLaunch) {
@@ -262,15 +354,21 @@ extern "C" int32_t mi_reshape_and_cache(const void* const* key_src, const void* 
       a.key_pool[l] = static_cast<char*>(key_pools[l0 + l]);
       a.value_pool[l] = static_cast<char*>(value_pools[l0 + l]);
     }
-    dim3 grid(static_cast<uint32_t>(groups), nl);
-    if (rows_kernel)
-      reshape_and_cache_rows<<<grid, kThreads, 0, s>>>(a);
+    dim3 grid(static_cast<uint32_t>(groups), nl, span_kernel && kSplitKv ? 2 : 1);
+    if (span_kernel && narrow && row_contig)
+      reshape_and_cache_span<true, true><<<grid, kSpanThreads, 0, s>>>(a);
+    else if (span_kernel && narrow)
+      reshape_and_cache_span<true, false><<<grid, kSpanThreads, 0, s>>>(a);
+    else if (span_kernel && row_contig)
+      reshape_and_cache_span<false, true><<<grid, kSpanThreads, 0, s>>>(a);
+    else if (span_kernel)
+      reshape_and_cache_span<false, false><<<grid, kSpanThreads, 0, s>>>(a);
     else if (piece == 16)
-      reshape_and_cache_generic<u32x4><<<grid, kThreads, 0, s>>>(a);
+      reshape_and_cache_generic<u32x4><<<grid, kGenericThreads, 0, s>>>(a);
     else if (piece == 4)
-      reshape_and_cache_generic<uint32_t><<<grid, kThreads, 0, s>>>(a);
+      reshape_and_cache_generic<uint32_t><<<grid, kGenericThreads, 0, s>>>(a);
     else
-      reshape_and_cache_generic<uint16_t><<<grid, kThreads, 0, s>>>(a);
+      reshape_and_cache_generic<uint16_t><<<grid, kGenericThreads, 0, s>>>(a);
     int32_t rc = check_launch("mi_reshape_and_cache");
     if (rc != MI_OK) return rc;
   }

@@ -20,7 +20,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <bool kStream>
 __device__ __forceinline__ void put(u32x4* p, const u32x4& v) {
   if constexpr (kStream) {
-    asm volatile("global_store_dwordx4 %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+    // s_nop 1: the wait states a >8-byte store needs before a VALU write of its data VGPRs, which
+    // the compiler cannot insert after an asm store.
+    asm volatile("global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1" ::"v"(p), "v"(v) : "memory");
   } else {
     __builtin_nontemporal_store(v, p);
   }

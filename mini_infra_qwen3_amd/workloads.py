@@ -7,10 +7,13 @@ GPU path and the CPU oracle see identical inputs:
 * ``decode_step`` -- one layer: batch 8, contexts uniform in [64, 512], pool 4096 blocks,
   block tables from one random permutation of blocks 1..4095.
 * ``prefill_scatter`` -- 28 layers: 32 prompts, lengths uniform in [128, 2048], block tables
-  from ``FreeKVCacheBlockQueue`` after seeded alloc/free churn (non-contiguous blocks).
+  from ``FreeKVCacheBlockQueue`` after seeded churn: ``fragmented`` (decode-style interleaved
+  growth; under 1% of neighbouring entries consecutive) or ``near_sequential`` (a short churn at
+  the front of the pool; about 99% consecutive).
 * ``decode_at_scale`` -- 28 layers: batch 256, contexts lognormal (median 2048, sigma 1.3,
   clipped to [256, 8192]; about 90 GB of K/V), randomly permuted blocks.
-* ``chunked_prefill`` -- 4 prompts of 16384 tokens in 2048-token chunks with history.
+* ``chunked_prefill`` -- 4 prompts of 16384 tokens in 2048-token chunks with history, tables of
+  either kind.
 * ``serving_requests`` -- the continuous-batching run: 128 requests, Poisson arrivals at 20 req/s
   (exponential gaps, mean 50 ms, first arrival at 0), prompt lengths uniform in [32, 1024] with
   token ids uniform in [1000, 100000), 128 output tokens each.
@@ -68,7 +71,10 @@ def permuted_tables(lengths: list[int], num_blocks: int, gen: torch.Generator,
 
 def churned_tables(lengths: list[int], num_blocks: int, gen: torch.Generator, block_size: int = BLOCK_SIZE,
                    churn_rounds: int = 64) -> list[list[int]]:
-    """Block tables from a FreeKVCacheBlockQueue after seeded alloc/free churn of dummy requests."""
+    """Near-sequential tables: a FreeKVCacheBlockQueue after a short seeded alloc/free churn of 64
+    dummy requests, all freed again before the measured allocation.  The churn touches only the front
+    of the pool, so the allocation then runs mostly over never-used blocks: about 99% of adjacent
+    table entries are consecutive block ids."""
     queue = FreeKVCacheBlockQueue(num_blocks)
     live: list[list[int]] = []
     for _ in range(churn_rounds):
@@ -82,6 +88,38 @@ def churned_tables(lengths: list[int], num_blocks: int, gen: torch.Generator, bl
     for blocks in live:
         queue.free(blocks)
     return [queue.allocate(num_blocks_for_tokens(n, block_size)) for n in lengths]
+
+
+def fragmented_tables(lengths: list[int], num_blocks: int, gen: torch.Generator, block_size: int = BLOCK_SIZE,
+                      streams: int = 64) -> list[list[int]]:
+    """Tables from a FreeKVCacheBlockQueue whose free list was reordered the way decoding reorders it:
+    ``streams`` requests each take one block per round, in a fresh random order every round, until
+    the pool is used up; they then finish in a random order and free their blocks.  The free list
+    then interleaves the requests' blocks, so a new table's neighbouring entries are almost never
+    consecutive block ids (under 1% at the default 64 streams) and each 32 KiB block of one layer's
+    K or V lies at its own place in the pool."""
+    queue = FreeKVCacheBlockQueue(num_blocks)
+    held: list[list[int]] = [[] for _ in range(streams)]
+    while queue.num_free_blocks:
+        for s in torch.randperm(streams, generator=gen).tolist():
+            if not queue.num_free_blocks:
+                break
+            held[s].extend(queue.allocate(1))
+    for s in torch.randperm(streams, generator=gen).tolist():
+        queue.free(held[s])
+    return [queue.allocate(num_blocks_for_tokens(n, block_size)) for n in lengths]
+
+
+TABLE_KINDS = {"fragmented": fragmented_tables, "near_sequential": churned_tables}
+
+
+def consecutive_fraction(tables: list[list[int]]) -> float:
+    """Fraction of adjacent table entries that are consecutive block ids (next == previous + 1)."""
+    pairs = sum(max(len(t) - 1, 0) for t in tables)
+    if pairs == 0:
+        return 0.0
+    hits = sum(int(np.count_nonzero(np.diff(np.asarray(t, dtype=np.int64)) == 1)) for t in tables if len(t) > 1)
+    return hits / pairs
 
 
 def padded(tables: list[list[int]]) -> torch.Tensor:
@@ -173,15 +211,16 @@ class PrefillScatterWorkload:
 
 def prefill_scatter(seed: int = 0, device: torch.device | str = "cuda", num_prompts: int = 32,
                     lo: int = 128, hi: int = 2048, num_layers: int = NUM_LAYERS,
-                    num_blocks: int | None = None) -> PrefillScatterWorkload:
-    """Whole-prompt prefill scatter: prompts U[lo, hi], churned tables, sources drawn on ``device``."""
+                    num_blocks: int | None = None, tables: str = "fragmented") -> PrefillScatterWorkload:
+    """Whole-prompt prefill scatter: prompts U[lo, hi], tables of kind ``tables`` (a key of
+    ``TABLE_KINDS``), sources drawn on ``device``."""
     from mini_infra_qwen3_amd.worker.metadata import prefill_scatter_indices
 
     gen = torch.Generator().manual_seed(seed)
     lengths = uniform_lengths(num_prompts, lo, hi, gen)
     need = sum(num_blocks_for_tokens(n, BLOCK_SIZE) for n in lengths)
     num_blocks = num_blocks or 1 + need + 512
-    tables = churned_tables(lengths, num_blocks, gen)
+    tables = TABLE_KINDS[tables](lengths, num_blocks, gen)
     width = max(lengths)
     dgen = torch.Generator(device=device).manual_seed(seed + 1)
     sources = _randn_bf16((num_layers, 2, num_prompts, NUM_KV_HEADS, width, HEAD_DIM), dgen, device)
@@ -210,10 +249,11 @@ class ChunkedPrefillWorkload:
 
 
 def chunked_prefill(seed: int = 0, num_prompts: int = 4, prompt_len: int = 16384,
-                    chunk_len: int = 2048) -> ChunkedPrefillWorkload:
+                    chunk_len: int = 2048, tables: str = "fragmented") -> ChunkedPrefillWorkload:
+    """Long prompts in fixed-size chunks; block tables of kind ``tables`` (a key of ``TABLE_KINDS``)."""
     gen = torch.Generator().manual_seed(seed)
     num_blocks = 1 + num_prompts * num_blocks_for_tokens(prompt_len, BLOCK_SIZE) + 256
-    tables = churned_tables([prompt_len] * num_prompts, num_blocks, gen)
+    tables = TABLE_KINDS[tables]([prompt_len] * num_prompts, num_blocks, gen)
     return ChunkedPrefillWorkload(prompt_len, chunk_len, num_prompts, tables, num_blocks)
 
 
@@ -237,7 +277,8 @@ def serving_requests(seed: int = 0, num_requests: int = 128, rate_per_s: float =
 
 __all__ = [
     "BLOCK_SIZE", "HEAD_DIM", "KV_BYTES_PER_TOKEN_LAYER", "NUM_HEADS", "NUM_KV_HEADS", "NUM_LAYERS", "SCALE",
-    "ChunkedPrefillWorkload", "DecodeWorkload", "PrefillScatterWorkload", "chunked_prefill", "churned_tables",
+    "TABLE_KINDS", "ChunkedPrefillWorkload", "DecodeWorkload", "PrefillScatterWorkload", "chunked_prefill",
+    "churned_tables", "consecutive_fraction", "fragmented_tables",
     "decode_at_scale", "decode_step", "lognormal_lengths", "padded", "permuted_tables", "prefill_scatter",
     "serving_requests", "slots_of", "uniform_lengths",
 ]

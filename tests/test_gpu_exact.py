@@ -68,6 +68,55 @@ def test_exact_decode_empty_context_and_null_padding(device):
     assert_bits(got, want)
 
 
+def test_exact_decode_plain_form_ignores_slot_mapping(device):
+    """Without the prologue (q_weight NULL) k, v and slot_mapping are ignored: a C caller that
+    passes real slots with NULL k / v gets the plain attention and an unchanged pool."""
+    from mini_infra_qwen3_amd import _native
+
+    q, kp, vp, bt, ctx = decode_case(12, 4, 20, 60, 8, 2, 64)
+    q, kpd, vpd, bt, ctx = q.to(device), kp.to(device), vp.to(device), bt.to(device), ctx.to(device)
+    slots = (bt[:, 0] * 16 + 3).contiguous()
+    out = torch.empty(4, 16 * 128, dtype=torch.bfloat16, device=device)
+    lib = _native.load()
+    rc = lib.mi_paged_decode_attention_exact(
+        out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), q.stride(1), None, 0, None, 0, None, None, None,
+        None, 0.0, slots.data_ptr(), 1, kpd.data_ptr(), vpd.data_ptr(), kp.shape[0], bt.data_ptr(), bt.stride(0),
+        bt.shape[1], ctx.data_ptr(), 1, 4, 16, 8, 128, 16, SCALE, data_plane._stream(device))
+    _native.check(rc, "mi_paged_decode_attention_exact")
+    torch.cuda.synchronize()
+    assert_bits(kpd, kp)
+    assert_bits(vpd, vp)
+    assert_bits(out, torch_ref.paged_decode_attention(q.cpu(), kp, vp, bt.cpu(), ctx.cpu(), SCALE, exact=True))
+
+
+def test_exact_decode_prologue_padding_row_appends_nothing(device):
+    """Prologue form: a row of context 0 (a padding row) gets a zero output and appends nothing,
+    even with a slot inside the pool; the other rows append as usual."""
+    gen = torch.Generator().manual_seed(21)
+    batch, nb = 3, 32
+    kp = torch.randn(nb, 16, 8, 128, generator=gen).bfloat16()
+    vp = torch.randn(nb, 16, 8, 128, generator=gen).bfloat16()
+    q_raw = torch.randn(batch, 16 * 128, generator=gen).bfloat16()
+    k_raw = torch.randn(batch, 8 * 128, generator=gen).bfloat16()
+    v_raw = torch.randn(batch, 8 * 128, generator=gen).bfloat16()
+    weight = torch.ones(128).bfloat16()
+    cos, sin = torch.ones(batch, 128).bfloat16(), torch.zeros(batch, 128).bfloat16()
+    bt = torch.tensor([[3, 4], [5, 0], [6, 7]])
+    ctx = torch.tensor([20, 0, 17])
+    slots = torch.tensor([4 * 16 + 3, 5 * 16 + 9, 7 * 16 + 0])
+    kpd, vpd = kp.to(device), vp.to(device)
+    got = data_plane.paged_decode_attention_fused(
+        q_raw.to(device), k_raw.to(device), v_raw.to(device), weight.to(device), weight.to(device), cos.to(device),
+        sin.to(device), 1e-6, slots.to(device), kpd, vpd, bt.to(device), ctx.to(device), SCALE, exact=True)
+    torch.cuda.synchronize()
+    assert not got[1].any()
+    flat_k, flat_v = kpd.view(-1, 8, 128).cpu(), vpd.view(-1, 8, 128).cpu()
+    assert_bits(flat_k[5 * 16 + 9], kp.view(-1, 8, 128)[5 * 16 + 9])   # padding row: untouched
+    assert_bits(flat_v[5 * 16 + 9], vp.view(-1, 8, 128)[5 * 16 + 9])
+    assert_bits(flat_v[4 * 16 + 3], v_raw[0].view(8, 128))              # real rows: appended
+    assert_bits(flat_v[7 * 16 + 0], v_raw[2].view(8, 128))
+
+
 def test_exact_decode_prologue_matches_norm_rope_append_then_attend(device):
     """The prologue form (raw q / k / v rows in): q / k RMSNorm + RoPE, the K/V append at the slots,
     then attention -- output and both pools bit-identical to the oracle chain."""

@@ -105,32 +105,57 @@ def test_scatter_rejects_cpu_tensors(native_lib):
         data_plane.reshape_and_cache([pool[:1]], [pool[:1]], torch.zeros(1, dtype=torch.long), [pool], [pool])
 
 
-def test_prefill_scatter_full_size_round_trip(native_lib, device):
-    """32 prompts U[128, 2048] x 28 layers (about 8 GB moved): scatter, then gather every
-    prompt's blocks back and compare with its valid source rows bit for bit."""
-    w = workloads.prefill_scatter(seed=0, device=device)
+@pytest.mark.parametrize("tables", ["fragmented", "near_sequential"])
+def test_prefill_scatter_full_size_every_layer(native_lib, device, tables):
+    """32 prompts U[128, 2048] x 28 layers (about 9.3 GB moved), on both table kinds: every
+    written pool row of every layer equals its source row, read on the device with torch's own
+    advanced indexing (not through the product's gather), and blocks in no table stay zero."""
+    w = workloads.prefill_scatter(seed=0, device=device, tables=tables)
+    if tables == "fragmented":
+        assert workloads.consecutive_fraction(w.tables) < 0.01
     pool = PagedKVCachePool(28, w.num_blocks, 16, 8, 128, torch.bfloat16, device)
     layers = [(w.sources[l, 0], w.sources[l, 1]) for l in range(28)]
     index = torch.from_numpy(w.index).to(device)
     pool.write_prefill(KVCache(layers), index[0], index[1], index[2])
-    ids = workloads.padded(w.tables).to(device)
-    gathered = pool.gather_blocks(ids)  # [B, Hkv, nb * 16, D] per layer
-    for layer in (0, 13, 27):
-        key, value = gathered[layer]
-        for b, n in enumerate(w.lengths):
-            src_k = w.sources[layer, 0, b, :, w.padded_length - n:]
-            src_v = w.sources[layer, 1, b, :, w.padded_length - n:]
-            assert torch.equal(as_bits(key[b, :, :n]), as_bits(src_k))
-            assert torch.equal(as_bits(value[b, :, :n]), as_bits(src_v))
+    rows, positions, slots = index[0], index[1], index[2]
+    for layer in range(28):
+        for kv in range(2):
+            written = pool.kv_pools[layer][kv].view(-1, 8, 128)[slots]          # [N, Hkv, D]
+            expected = w.sources[layer, kv][rows, :, positions, :]              # [N, Hkv, D]
+            assert torch.equal(as_bits(written), as_bits(expected)), (layer, kv)
     # untouched blocks (never in any table) stay zero in every layer
     used = torch.zeros(w.num_blocks, dtype=torch.bool)
     for t in w.tables:
         used[torch.tensor(t)] = True
     free = (~used).nonzero().flatten().to(device)
     assert not pool.storage[:, :, free].any()
+    # slots of a prompt's last block past its length stay zero too
+    tails = [t[-1] * 16 + s for t, n in zip(w.tables, w.lengths) for s in range(n % 16 or 16, 16)]
+    if tails:
+        tail = torch.tensor(tails, device=device)
+        assert not pool.storage.view(28, 2, -1, 8, 128)[:, :, tail].any()
 
 
 # -------------------------------------------------------------------------------- gather
+@pytest.mark.parametrize("tables", ["fragmented", "near_sequential"])
+def test_history_gather_full_size_every_chunk(native_lib, device, tables):
+    """The history gather of 4 prompts x 16384 tokens in 2048-token chunks, 28 layers, on both
+    table kinds: chunk c gathers the first 128 c blocks of every prompt's table, and each gathered
+    layer equals torch's own advanced indexing of the pool on the device, bit for bit."""
+    w = workloads.chunked_prefill(seed=0, tables=tables)
+    pool = PagedKVCachePool(28, w.num_blocks, 16, 8, 128, torch.bfloat16, device)
+    pool.storage.view(torch.int16).random_(generator=torch.Generator(device=device).manual_seed(2))
+    for c in range(1, w.num_chunks):
+        nb = c * w.chunk_len // 16
+        ids = torch.tensor([t[:nb] for t in w.tables], dtype=torch.long, device=device)
+        got = pool.gather_blocks(ids)
+        for layer in range(28):
+            for kv in range(2):
+                want = pool.kv_pools[layer][kv][ids].view(w.num_prompts, nb * 16, 8, 128).transpose(1, 2)
+                assert torch.equal(as_bits(got[layer][kv]), as_bits(want)), (c, layer, kv)
+        del got
+
+
 def test_gather_matches_oracle_including_null_and_stale_blocks(native_lib, device):
     gen = torch.Generator().manual_seed(5)
     pool = PagedKVCachePool(4, 40, 16, 8, 128, torch.bfloat16, device)
