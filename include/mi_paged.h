@@ -35,7 +35,8 @@
 extern "C" {
 #endif
 
-#define MI_PAGED_ABI_VERSION 2  /* 2: mi_paged_decode_workspace_bytes takes num_kv_heads */
+#define MI_PAGED_ABI_VERSION 3  /* 2: mi_paged_decode_workspace_bytes takes num_kv_heads;
+                                   3: mi_paged_decode_attention_exact takes a workspace */
 
 #define MI_OK 0
 #define MI_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, bad stride  */
@@ -254,12 +255,18 @@ int32_t mi_chunked_prefill_attention(void* out, int64_t out_row_stride, int64_t 
  *
  * mi_paged_decode_attention_exact -- decode.  With q_weight == NULL, `q` holds the rotated
  * queries ([batch, num_heads, 128], row / head strides) and k, v, k_weight, cos, sin, eps and
- * slot_mapping are ignored: the arguments and outputs of mi_paged_decode_attention (no
- * workspace).  With q_weight != NULL the prologue of mi_paged_decode_attention_fused runs first
+ * slot_mapping are ignored: the arguments and outputs of mi_paged_decode_attention.  With
+ * q_weight != NULL the prologue of mi_paged_decode_attention_fused runs first
  * (q / k RMSNorm + RoPE of the raw projection rows q / k, K/V rows into their slots; the q head
  * stride is then 128), bit-identical to mi_qk_norm_rope; as in the mixed form's decode rows,
  * context 0 marks a padding row, which appends nothing.  Out-of-range table ids read block 0.
  * Any context length (contexts longer than the LDS cache recompute their scores per pass).
+ * workspace (optional, 256-byte aligned): with at least mi_paged_decode_exact_workspace_bytes(...)
+ * bytes, a batch too small to fill the GPU with one workgroup per (sequence, KV head) runs split
+ * over each sequence's blocks (three launches: scores, then the softmax statistics and P V per
+ * split, then the merge), with the same results bit for bit.  NULL, or a batch that needs no
+ * split (the size query returns 0), runs one launch; a non-NULL workspace smaller than the split
+ * needs is MI_ERR_WORKSPACE.
  *
  * mi_chunked_prefill_attention_exact -- chunked prefill: the arguments and layout of
  * mi_chunked_prefill_attention.  Padding rows get zeros.
@@ -274,7 +281,12 @@ int32_t mi_paged_decode_attention_exact(void* out, int64_t out_row_stride, const
                                         const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,
                                         const int64_t* context_lens, int64_t context_lens_stride, int32_t batch,
                                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                                        int32_t block_size, float scale, void* stream);
+                                        int32_t block_size, float scale, void* workspace, int64_t workspace_bytes,
+                                        void* stream);
+/* Workspace bytes of mi_paged_decode_attention_exact's split form for this launch shape; 0 when
+ * the launch runs unsplit.  No reference counterpart (the reference has no workspace). */
+int64_t mi_paged_decode_exact_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t num_heads,
+                                              int32_t num_kv_heads);
 int32_t mi_chunked_prefill_attention_exact(void* out, int64_t out_row_stride, int64_t out_tok_stride,
                                            const void* query, int64_t query_row_stride, int64_t query_head_stride,
                                            int64_t query_tok_stride, const void* key, int64_t key_row_stride,

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmi_paged.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MI_OK = 0
 MI_ERR_INVALID_ARGUMENT = -1
@@ -65,8 +65,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mi_paged_decode_attention_exact": (
         _i32,
         [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _ptr, _ptr, ctypes.c_float, _ptr, _i64,
-         _ptr, _ptr, _i64, _ptr, _i64, _i32, _ptr, _i64, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _ptr],
+         _ptr, _ptr, _i64, _ptr, _i64, _i32, _ptr, _i64, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _ptr, _i64,
+         _ptr],
     ),
+    "mi_paged_decode_exact_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "mi_chunked_prefill_attention_exact": (
         _i32,
         [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _ptr, _i64,

@@ -111,6 +111,16 @@ __device__ __forceinline__ void unpack8(const u32x4 v, double (&d)[8]) {
 constexpr int kDecWaves = 8;
 constexpr int kDecThreads = 64 * kDecWaves;
 constexpr int kDecCacheBytes = 128 * 1024;  // score cache (dynamic LDS) of one workgroup, at most
+#ifndef MI_EXACT_DECODE_GROUP
+#define MI_EXACT_DECODE_GROUP 2
+#endif
+// Blocks a wavefront loads before using them: MI_EXACT_DECODE_GROUP for GQA groups up to 2, one
+// block for larger groups, whose fp64 accumulators leave no registers for more (more spills to
+// scratch).
+template <int kG>
+constexpr int dec_group() {
+  return kG <= 2 ? MI_EXACT_DECODE_GROUP : 1;
+}
 
 struct ExactDecodeArgs {
   uint16_t* out;
@@ -161,6 +171,7 @@ template <int kG, bool kPrologue, int kWaves>
 __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const int g, unsigned char* smem) {
   constexpr int kDecWaves = kWaves;
   constexpr int kDecThreads = 64 * kWaves;
+  constexpr int kGrp = dec_group<kG>();
   using Lds = DecodeLds<kG, kWaves>;
   auto s_q = reinterpret_cast<float (*)[kHeadDim]>(smem);
   auto s_m = reinterpret_cast<float (*)[kG]>(smem + Lds::kQ);
@@ -235,16 +246,33 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
 
   // Lane offset inside a block: token 4 i + r (i = 0..3), dims 8 dl .. +8 of KV head g.
   const int64_t lane_off = r * row_elems + g * kHeadDim + 8 * dl;
-  auto block_ptr = [&](const uint16_t* pool, int i) -> const uint16_t* {
-    const int blk = w + kDecWaves * i;
-    int64_t id = a.block_tables[b * a.bt_stride + blk];
-    if (id < 0 || id >= a.num_blocks) id = 0;
-    return pool + id * kBlockSize * row_elems + lane_off;
+  // The wavefront's block ids (blocks w + kDecWaves i), fetched with one load, lane i holding id i
+  // (i < 64), and broadcast with readlane; ids outside the pool read block 0.  Blocks are then read
+  // kGrp at a time, all loads of a group issued before any is used, so a pass costs about one
+  // memory round trip per group instead of two per block.
+  int64_t lane_id = 0;
+  if (lane < cnt) {
+    lane_id = a.block_tables[b * a.bt_stride + w + kDecWaves * lane];
+    if (lane_id < 0 || lane_id >= a.num_blocks) lane_id = 0;
+  }
+  auto block_id = [&](int i) -> int64_t {  // i is wave-uniform
+    if (i < 64) {
+      const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(lane_id), i);
+      const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(lane_id) >> 32), i);
+      return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+    }
+    const int64_t id = a.block_tables[b * a.bt_stride + w + kDecWaves * i];
+    return id < 0 || id >= a.num_blocks ? 0 : id;
   };
-  auto load_block = [&](const uint16_t* pool, int i, u32x4 (&buf)[4]) {
-    const uint16_t* p = block_ptr(pool, i);
+  // Blocks i0 .. i0 + kGrp - 1 of the wavefront (indices past its last block reload the last
+  // one, so every load is unconditional; those are not used).
+  auto load_group = [&](const uint16_t* pool, int i0, u32x4 (&buf)[kGrp][4]) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) buf[t] = *reinterpret_cast<const u32x4*>(p + 4 * t * row_elems);
+    for (int q = 0; q < kGrp; ++q) {
+      const uint16_t* p = pool + block_id(min(i0 + q, cnt - 1)) * kBlockSize * row_elems + lane_off;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) buf[q][t] = *reinterpret_cast<const u32x4*>(p + 4 * t * row_elems);
+    }
   };
   // Scores of the lane row's 4 tokens of block i against the kG queries (equal in the 16 lanes of
   // the row after the butterfly).
@@ -278,20 +306,24 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
   float mloc[kG];
 #pragma unroll
   for (int j = 0; j < kG; ++j) mloc[j] = -INFINITY;
-  for (int i = 0; i < cnt; ++i) {
-    u32x4 kb[4];
-    load_block(a.key_pool, i, kb);
-    float s[4][kG];
-    block_scores(kb, s);
-    const int tok0 = (w + kDecWaves * i) * kBlockSize + r;
+  for (int i0 = 0; i0 < cnt; i0 += kGrp) {
+    u32x4 kb[kGrp][4];
+    load_group(a.key_pool, i0, kb);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int tok = tok0 + 4 * t;
-      if (tok < n) {
+    for (int q = 0; q < kGrp; ++q) {
+      if (i0 + q >= cnt) break;
+      float s[4][kG];
+      block_scores(kb[q], s);
+      const int tok0 = (w + kDecWaves * (i0 + q)) * kBlockSize + r;
 #pragma unroll
-        for (int j = 0; j < kG; ++j) {
-          mloc[j] = fmaxf(mloc[j], s[t][j]);
-          if (cached && dl == j) s_cache[tok * kG + j] = bf16_bits(s[t][j]);
+      for (int t = 0; t < 4; ++t) {
+        const int tok = tok0 + 4 * t;
+        if (tok < n) {
+#pragma unroll
+          for (int j = 0; j < kG; ++j) {
+            mloc[j] = fmaxf(mloc[j], s[t][j]);
+            if (cached && dl == j) s_cache[tok * kG + j] = bf16_bits(s[t][j]);
+          }
         }
       }
     }
@@ -310,6 +342,9 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
     for (int v = 0; v < kDecWaves; ++v) mx = fmaxf(mx, s_m[v][j]);
     M[j] = mx;
   }
+  // With the scores cached, pass 2 works in LDS only: the first V blocks load meanwhile.
+  u32x4 vb[kGrp][4];
+  if (cached && cnt > 0) load_group(a.value_pool, 0, vb);
 
   // ---- pass 2: the softmax denominators
   double hi[kG], lo[kG];
@@ -321,18 +356,22 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
       for (int j = 0; j < kG; ++j) split_add(exact_exp(bf16_bits_to_f32(s_cache[tok * kG + j]), M[j]), hi[j], lo[j]);
     }
   } else {
-    for (int i = 0; i < cnt; ++i) {
-      u32x4 kb[4];
-      load_block(a.key_pool, i, kb);
-      float s[4][kG];
-      block_scores(kb, s);
-      const int tok0 = (w + kDecWaves * i) * kBlockSize + r;
+    for (int i0 = 0; i0 < cnt; i0 += kGrp) {
+      u32x4 kb[kGrp][4];
+      load_group(a.key_pool, i0, kb);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (tok0 + 4 * t < n) {
+      for (int q = 0; q < kGrp; ++q) {
+        if (i0 + q >= cnt) break;
+        float s[4][kG];
+        block_scores(kb[q], s);
+        const int tok0 = (w + kDecWaves * (i0 + q)) * kBlockSize + r;
 #pragma unroll
-          for (int j = 0; j < kG; ++j)
-            if (dl == j) split_add(exact_exp(s[t][j], M[j]), hi[j], lo[j]);
+        for (int t = 0; t < 4; ++t) {
+          if (tok0 + 4 * t < n) {
+#pragma unroll
+            for (int j = 0; j < kG; ++j)
+              if (dl == j) split_add(exact_exp(s[t][j], M[j]), hi[j], lo[j]);
+          }
         }
       }
     }
@@ -374,39 +413,42 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
   for (int j = 0; j < kG; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0.0;
-  for (int i = 0; i < cnt; ++i) {
-    u32x4 vb[4];
-    load_block(a.value_pool, i, vb);
-    float p[4][kG];
-    const int tok0 = (w + kDecWaves * i) * kBlockSize + r;
-    if (cached) {
+  for (int i0 = 0; i0 < cnt; i0 += kGrp) {
+    if (!cached || i0 > 0) load_group(a.value_pool, i0, vb);
+    u32x4 kb[kGrp][4];
+    if (!cached) load_group(a.key_pool, i0, kb);
+#pragma unroll
+    for (int q = 0; q < kGrp; ++q) {
+      if (i0 + q >= cnt) break;
+      float p[4][kG];
+      const int tok0 = (w + kDecWaves * (i0 + q)) * kBlockSize + r;
+      if (cached) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int tok = tok0 + 4 * t;
+#pragma unroll
+          for (int j = 0; j < kG; ++j) p[t][j] = tok < n ? bf16_bits_to_f32(s_cache[tok * kG + j]) : 0.0f;
+        }
+      } else {
+        float s[4][kG];
+        block_scores(kb[q], s);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const bool valid = tok0 + 4 * t < n;
+#pragma unroll
+          for (int j = 0; j < kG; ++j) p[t][j] = valid ? exact_prob(exact_exp(s[t][j], M[j]), L[j]) : 0.0f;
+        }
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int tok = tok0 + 4 * t;
+        double vd[8];
+        unpack8(vb[q][t], vd);
 #pragma unroll
-        for (int j = 0; j < kG; ++j) p[t][j] = tok < n ? bf16_bits_to_f32(s_cache[tok * kG + j]) : 0.0f;
-      }
-    } else {
-      u32x4 kb[4];
-      load_block(a.key_pool, i, kb);
-      float s[4][kG];
-      block_scores(kb, s);
+        for (int j = 0; j < kG; ++j) {
+          const double pj = p[t][j];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const bool valid = tok0 + 4 * t < n;
-#pragma unroll
-        for (int j = 0; j < kG; ++j) p[t][j] = valid ? exact_prob(exact_exp(s[t][j], M[j]), L[j]) : 0.0f;
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      double vd[8];
-      unpack8(vb[t], vd);
-#pragma unroll
-      for (int j = 0; j < kG; ++j) {
-        const double pj = p[t][j];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = fma(pj, vd[e], acc[j][e]);
+          for (int e = 0; e < 8; ++e) acc[j][e] = fma(pj, vd[e], acc[j][e]);
+        }
       }
     }
   }
@@ -450,6 +492,297 @@ template <int kG, bool kPrologue>
 __global__ __launch_bounds__(kDecThreads) void exact_decode_kernel(const ExactDecodeArgs a) {
   extern __shared__ __align__(16) unsigned char s_dec[];
   exact_decode_body<kG, kPrologue, kDecWaves>(a, blockIdx.x, blockIdx.y, s_dec);
+}
+
+// ------------------------------------------------------------------ split decode ---
+// The same decode, cut over splits of each sequence's blocks so that small batches fill the GPU:
+//   kernel 1 (sequence, KV head, split): the split's scores, into the workspace (bf16 bits);
+//   kernel 2 (sequence, KV head, split): the maximum and the exact denominator over all of the
+//     sequence's scores (each split reads them all: a few thousand values), then P V over the
+//     split's own blocks as fp64 partial sums;
+//   kernel 3 (sequence, KV head): the partials summed in split order, rounded once to bf16.
+// Every sum is exact (or off by far less than the final roundings can see), so the split gives the
+// single-kernel results.  kernel 1 also runs the prologue (q rotation into LDS; the split holding
+// the sequence's last block appends the new K/V row before it reads that block).
+constexpr int kSplitWaves = 4;
+constexpr int kSplitThreads = 64 * kSplitWaves;
+constexpr int kSplitInflight = 2;  // blocks a wavefront loads before using them
+constexpr int kMaxSplits = 32;
+
+struct ExactSplitArgs {
+  ExactDecodeArgs d;
+  uint16_t* scores;   // [batch, kv_heads, ctx_cap, kG] bf16 bits
+  double* partial;    // [batch, kv_heads, splits, kG, 128]
+  int32_t ctx_cap;    // max_blocks * 16
+  int32_t splits;
+};
+
+struct SplitRange {
+  int n, nblk, lo, hi;
+};
+
+__device__ __forceinline__ SplitRange split_range(const ExactDecodeArgs& a, int b, int sp, int splits) {
+  int64_t n64 = a.context_lens[b * a.ctx_stride];
+  n64 = min(n64, static_cast<int64_t>(a.max_blocks) * kBlockSize);
+  SplitRange r;
+  r.n = n64 > 0 ? static_cast<int>(n64) : 0;
+  r.nblk = (r.n + kBlockSize - 1) / kBlockSize;
+  r.lo = static_cast<int>(static_cast<int64_t>(sp) * r.nblk / splits);
+  r.hi = static_cast<int>(static_cast<int64_t>(sp + 1) * r.nblk / splits);
+  return r;
+}
+
+template <int kG, bool kPrologue>
+__global__ __launch_bounds__(kSplitThreads) void exact_split_scores_kernel(const ExactSplitArgs sa) {
+  const ExactDecodeArgs& a = sa.d;
+  const int b = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+  const SplitRange rg = split_range(a, b, sp, sa.splits);
+  if (rg.lo >= rg.hi) return;  // uniform
+  __shared__ __align__(16) float s_q[kG][kHeadDim];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int dl = lane & 15;
+  const int r = lane >> 4;
+  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
+  if constexpr (kPrologue) {
+    // Units u < kG: query head g kG + u rotated into LDS; unit kG (split holding the last block
+    // only): key head g rotated and written with value head g into the sequence's new slot.
+    const bool appends = rg.hi == rg.nblk;
+    for (int u = w; u <= kG; u += kSplitWaves) {
+      const bool is_q = u < kG;
+      if (!is_q && !appends) continue;
+      const uint16_t* src = is_q ? a.q + b * a.q_row + (g * kG + u) * kHeadDim : a.k_new + b * a.k_row + g * kHeadDim;
+      float o0, o1;
+      norm_rope_head(src, is_q ? a.q_weight : a.k_weight, a.cos + b * kHeadDim, a.sin + b * kHeadDim, a.eps, lane,
+                     o0, o1);
+      if (is_q) {
+        s_q[u][lane] = o0;
+        s_q[u][lane + 64] = o1;
+      } else {
+        const int64_t slot = a.slot_mapping[b * a.slot_stride];
+        if (slot >= 0 && slot < a.num_slots) {  // context > 0 here: the split has blocks
+          uint16_t* kd = a.key_pool + slot * row_elems + g * kHeadDim;
+          uint16_t* vd = a.value_pool + slot * row_elems + g * kHeadDim;
+          const uint16_t* vs = a.v_new + b * a.v_row + g * kHeadDim;
+          kd[lane] = bf16_bits(o0);
+          kd[lane + 64] = bf16_bits(o1);
+          vd[lane] = vs[lane];
+          vd[lane + 64] = vs[lane + 64];
+        }
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < kG * kHeadDim; i += kSplitThreads) {
+      const int j = i / kHeadDim, d = i - j * kHeadDim;
+      s_q[j][d] = bf16_bits_to_f32(a.q[b * a.q_row + (g * kG + j) * a.q_head + d]);
+    }
+  }
+  // Orders the append before this workgroup's loads of the last block (no other workgroup reads
+  // it in this kernel).
+  __syncthreads();
+
+  const int64_t lane_off = r * row_elems + g * kHeadDim + 8 * dl;
+  uint16_t* out_scores = sa.scores + (static_cast<int64_t>(b) * a.kv_heads + g) * sa.ctx_cap * kG;
+  const int cnt = rg.hi - rg.lo > w ? (rg.hi - rg.lo - 1 - w) / kSplitWaves + 1 : 0;  // blocks lo + w + 4 i
+  for (int i0 = 0; i0 < cnt; i0 += kSplitInflight) {
+    u32x4 kb[kSplitInflight][4];
+#pragma unroll
+    for (int q = 0; q < kSplitInflight; ++q) {
+      if (i0 + q >= cnt) break;
+      const int blk = rg.lo + w + kSplitWaves * (i0 + q);
+      int64_t id = a.block_tables[b * a.bt_stride + blk];
+      if (id < 0 || id >= a.num_blocks) id = 0;
+      const uint16_t* p = a.key_pool + id * kBlockSize * row_elems + lane_off;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) kb[q][t] = *reinterpret_cast<const u32x4*>(p + 4 * t * row_elems);
+    }
+#pragma unroll
+    for (int q = 0; q < kSplitInflight; ++q) {
+      if (i0 + q >= cnt) break;
+      const int tok0 = (rg.lo + w + kSplitWaves * (i0 + q)) * kBlockSize + r;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        double kd[8];
+        unpack8(kb[q][t], kd);
+        const int tok = tok0 + 4 * t;
+#pragma unroll
+        for (int j = 0; j < kG; ++j) {
+          const float4 q0 = *reinterpret_cast<const float4*>(&s_q[j][8 * dl]);
+          const float4 q1 = *reinterpret_cast<const float4*>(&s_q[j][8 * dl + 4]);
+          double acc = static_cast<double>(q0.x) * kd[0];
+          acc = fma(static_cast<double>(q0.y), kd[1], acc);
+          acc = fma(static_cast<double>(q0.z), kd[2], acc);
+          acc = fma(static_cast<double>(q0.w), kd[3], acc);
+          acc = fma(static_cast<double>(q1.x), kd[4], acc);
+          acc = fma(static_cast<double>(q1.y), kd[5], acc);
+          acc = fma(static_cast<double>(q1.z), kd[6], acc);
+          acc = fma(static_cast<double>(q1.w), kd[7], acc);
+          acc += __shfl_xor(acc, 1, 64);
+          acc += __shfl_xor(acc, 2, 64);
+          acc += __shfl_xor(acc, 4, 64);
+          acc += __shfl_xor(acc, 8, 64);
+          if (dl == j && tok < rg.n) out_scores[tok * kG + j] = bf16_bits(exact_score(acc, a.scale));
+        }
+      }
+    }
+  }
+}
+
+template <int kG>
+__global__ __launch_bounds__(kSplitThreads) void exact_split_pv_kernel(const ExactSplitArgs sa) {
+  const ExactDecodeArgs& a = sa.d;
+  const int b = blockIdx.x, g = blockIdx.y, sp = blockIdx.z;
+  const SplitRange rg = split_range(a, b, sp, sa.splits);
+  if (rg.lo >= rg.hi) return;  // uniform
+  __shared__ float s_m[kSplitWaves][kG];
+  __shared__ double s_l[kSplitWaves][kG][2];
+  __shared__ double s_o[kSplitWaves][kHeadDim];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int dl = lane & 15;
+  const int r = lane >> 4;
+  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
+  const int64_t lane_off = r * row_elems + g * kHeadDim + 8 * dl;
+  const int cnt = rg.hi - rg.lo > w ? (rg.hi - rg.lo - 1 - w) / kSplitWaves + 1 : 0;
+  // The first V blocks go out before the softmax statistics are formed.
+  u32x4 vb[kSplitInflight][4];
+  auto load_v = [&](int i0) {
+#pragma unroll
+    for (int q = 0; q < kSplitInflight; ++q) {
+      if (i0 + q >= cnt) break;
+      const int blk = rg.lo + w + kSplitWaves * (i0 + q);
+      int64_t id = a.block_tables[b * a.bt_stride + blk];
+      if (id < 0 || id >= a.num_blocks) id = 0;
+      const uint16_t* p = a.value_pool + id * kBlockSize * row_elems + lane_off;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) vb[q][t] = *reinterpret_cast<const u32x4*>(p + 4 * t * row_elems);
+    }
+  };
+  load_v(0);
+
+  // Maximum and exact denominator over all of the sequence's scores.
+  const uint16_t* sc = sa.scores + (static_cast<int64_t>(b) * a.kv_heads + g) * sa.ctx_cap * kG;
+  float mloc[kG];
+#pragma unroll
+  for (int j = 0; j < kG; ++j) mloc[j] = -INFINITY;
+  for (int tok = threadIdx.x; tok < rg.n; tok += kSplitThreads) {
+#pragma unroll
+    for (int j = 0; j < kG; ++j) mloc[j] = fmaxf(mloc[j], bf16_bits_to_f32(sc[tok * kG + j]));
+  }
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    const float mw = wave_max(mloc[j]);
+    if (lane == 0) s_m[w][j] = mw;
+  }
+  __syncthreads();
+  float M[kG];
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kSplitWaves; ++v) mx = fmaxf(mx, s_m[v][j]);
+    M[j] = mx;
+  }
+  double hi[kG], lo[kG];
+#pragma unroll
+  for (int j = 0; j < kG; ++j) hi[j] = lo[j] = 0.0;
+  for (int tok = threadIdx.x; tok < rg.n; tok += kSplitThreads) {
+#pragma unroll
+    for (int j = 0; j < kG; ++j) split_add(exact_exp(bf16_bits_to_f32(sc[tok * kG + j]), M[j]), hi[j], lo[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    const double h = wave_sum_f64(hi[j]), l = wave_sum_f64(lo[j]);
+    if (lane == 0) {
+      s_l[w][j][0] = h;
+      s_l[w][j][1] = l;
+    }
+  }
+  __syncthreads();
+  float L[kG];
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    double h = 0.0, l = 0.0;
+#pragma unroll
+    for (int v = 0; v < kSplitWaves; ++v) {
+      h += s_l[v][j][0];
+      l += s_l[v][j][1];
+    }
+    L[j] = static_cast<float>(h + l);
+  }
+
+  // P V over the split's blocks (lane: tokens 4 i + r of each block, dims 8 dl .. +8).
+  double acc[kG][8];
+#pragma unroll
+  for (int j = 0; j < kG; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0.0;
+  for (int i0 = 0; i0 < cnt; i0 += kSplitInflight) {
+    if (i0 > 0) load_v(i0);
+#pragma unroll
+    for (int q = 0; q < kSplitInflight; ++q) {
+      if (i0 + q >= cnt) break;
+      const int tok0 = (rg.lo + w + kSplitWaves * (i0 + q)) * kBlockSize + r;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int tok = tok0 + 4 * t;
+        double vd[8];
+        unpack8(vb[q][t], vd);
+#pragma unroll
+        for (int j = 0; j < kG; ++j) {
+          const double pj = tok < rg.n ? exact_prob(exact_exp(bf16_bits_to_f32(sc[tok * kG + j]), M[j]), L[j]) : 0.0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[j][e] = fma(pj, vd[e], acc[j][e]);
+        }
+      }
+    }
+  }
+  // rows of the wavefront, then the wavefronts (one head at a time through LDS)
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      double x = acc[j][e];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      acc[j][e] = x;
+    }
+  }
+  double* part = sa.partial + ((static_cast<int64_t>(b) * a.kv_heads + g) * sa.splits + sp) * kG * kHeadDim;
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    if (r == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_o[w][8 * dl + e] = acc[j][e];
+    }
+    __syncthreads();
+    if (threadIdx.x < kHeadDim) {
+      double o = 0.0;
+#pragma unroll
+      for (int v = 0; v < kSplitWaves; ++v) o += s_o[v][threadIdx.x];
+      part[j * kHeadDim + threadIdx.x] = o;
+    }
+    __syncthreads();
+  }
+}
+
+template <int kG>
+__global__ __launch_bounds__(kHeadDim) void exact_split_merge_kernel(const ExactSplitArgs sa) {
+  const ExactDecodeArgs& a = sa.d;
+  const int b = blockIdx.x, g = blockIdx.y;
+  uint16_t* out_b = a.out + b * a.out_row + (g * kG) * kHeadDim;
+  const double* part = sa.partial + (static_cast<int64_t>(b) * a.kv_heads + g) * sa.splits * kG * kHeadDim;
+  const SplitRange rg = split_range(a, b, 0, sa.splits);
+#pragma unroll
+  for (int j = 0; j < kG; ++j) {
+    double o = 0.0;
+    for (int sp = 0; sp < sa.splits; ++sp) {
+      const int lo = static_cast<int>(static_cast<int64_t>(sp) * rg.nblk / sa.splits);
+      const int hi = static_cast<int>(static_cast<int64_t>(sp + 1) * rg.nblk / sa.splits);
+      if (lo < hi) o += part[(static_cast<int64_t>(sp) * kG + j) * kHeadDim + threadIdx.x];
+    }
+    out_b[j * kHeadDim + threadIdx.x] = bf16_bits(static_cast<float>(o));  // zero rows for empty contexts
+  }
 }
 
 // ----------------------------------------------------------------------- prefill ---
@@ -800,6 +1133,63 @@ int32_t launch_exact_decode(const ExactDecodeArgs& a, int32_t batch, hipStream_t
   return check_launch("mi_paged_decode_attention_exact");
 }
 
+template <int kG, bool kPrologue>
+int32_t launch_exact_split(const ExactSplitArgs& sa, int32_t batch, hipStream_t s) {
+  const dim3 grid(batch, sa.d.kv_heads, sa.splits);
+  exact_split_scores_kernel<kG, kPrologue><<<grid, kSplitThreads, 0, s>>>(sa);
+  if (const int32_t rc = check_launch("mi_paged_decode_attention_exact(scores)")) return rc;
+  exact_split_pv_kernel<kG><<<grid, kSplitThreads, 0, s>>>(sa);
+  if (const int32_t rc = check_launch("mi_paged_decode_attention_exact(pv)")) return rc;
+  exact_split_merge_kernel<kG><<<dim3(batch, sa.d.kv_heads), kHeadDim, 0, s>>>(sa);
+  return check_launch("mi_paged_decode_attention_exact(merge)");
+}
+
+template <bool kPrologue>
+int32_t dispatch_exact_split(const ExactSplitArgs& sa, int32_t batch, int group, hipStream_t s) {
+  switch (group) {
+    case 1: return launch_exact_split<1, kPrologue>(sa, batch, s);
+    case 2: return launch_exact_split<2, kPrologue>(sa, batch, s);
+    case 4: return launch_exact_split<4, kPrologue>(sa, batch, s);
+    case 5: return launch_exact_split<5, kPrologue>(sa, batch, s);
+    default: return launch_exact_split<8, kPrologue>(sa, batch, s);
+  }
+}
+
+// Splits of each sequence for the split decode: enough (sequence, KV head, split) workgroups for
+// two per CU, at most one per 4 table blocks (so the 4 wavefronts of a split have blocks to read)
+// and at most kMaxSplits; 1 = the single-kernel form.  Only launches of at most kMaxSplitPairs
+// (sequence, KV head) pairs split: measured on MI355X (28 layers in a HIP graph, contexts U[200,
+// 1150], GQA group 2), µs per layer single / split: batch 1 29.5 / 23.2, 4 35.9 / 25.9,
+// 9 32.6 / 35.8, 16 43.4 / 48.7, 32 44.9 / 72.9 -- three dependent launches cost more than
+// one launch's idle CUs once the batch gives a workgroup to a fifth of them.
+constexpr int64_t kMaxSplitPairs = 48;
+int32_t exact_decode_splits(int32_t batch, int32_t max_blocks, int32_t num_kv_heads) {
+  const int64_t pairs = static_cast<int64_t>(batch) * num_kv_heads;
+  if (pairs <= 0 || pairs > kMaxSplitPairs || batch > 65535) return 1;
+  int64_t splits = (2 * static_cast<int64_t>(device_cus()) + pairs - 1) / pairs;
+  splits = std::min<int64_t>(splits, kMaxSplits);
+  splits = std::min<int64_t>(splits, max_blocks / kSplitWaves);
+  return splits < 2 ? 1 : static_cast<int32_t>(splits);
+}
+
+// Workspace of the split decode: the scores [batch, kv_heads, max_blocks * 16, G] bf16, then the
+// partials [batch, kv_heads, splits, G, 128] fp64 (256-byte aligned).
+struct ExactSplitLayout {
+  int32_t splits;
+  int64_t scores_bytes, bytes;
+};
+ExactSplitLayout exact_split_layout(int32_t batch, int32_t max_blocks, int32_t num_heads, int32_t num_kv_heads) {
+  ExactSplitLayout l{1, 0, 0};
+  if (batch <= 0 || max_blocks <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return l;
+  l.splits = exact_decode_splits(batch, max_blocks, num_kv_heads);
+  if (l.splits < 2) return l;
+  const int64_t group = num_heads / num_kv_heads;
+  const int64_t pairs = static_cast<int64_t>(batch) * num_kv_heads;
+  l.scores_bytes = (pairs * max_blocks * kBlockSize * group * 2 + 255) / 256 * 256;
+  l.bytes = l.scores_bytes + pairs * l.splits * group * kHeadDim * 8;
+  return l;
+}
+
 template <bool kPrologue>
 int32_t dispatch_exact_decode(const ExactDecodeArgs& a, int32_t batch, int group, hipStream_t s) {
   switch (group) {
@@ -880,7 +1270,7 @@ extern "C" int32_t mi_paged_decode_attention_exact(
     const void* cos, const void* sin, float eps, const int64_t* slot_mapping, int64_t slot_stride, void* key_pool,
     void* value_pool, int64_t num_blocks, const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,
     const int64_t* context_lens, int64_t context_lens_stride, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
-    int32_t head_dim, int32_t block_size, float scale, void* stream) {
+    int32_t head_dim, int32_t block_size, float scale, void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace mi;
   const char* what = "mi_paged_decode_attention_exact";
   if (batch < 0 || max_blocks < 0 || num_blocks < 0) return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
@@ -934,6 +1324,28 @@ extern "C" int32_t mi_paged_decode_attention_exact(
   const int64_t tokens = static_cast<int64_t>(max_blocks) * kBlockSize;
   a.cache_tokens = tokens * group * static_cast<int64_t>(sizeof(uint16_t)) <= kDecCacheBytes ? static_cast<int32_t>(tokens) : 0;
   hipStream_t s = as_stream(stream);
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: bad workspace", what);
+  if (workspace) {  // the split form when the batch is small enough to gain from it
+    const ExactSplitLayout layout = exact_split_layout(batch, max_blocks, num_heads, num_kv_heads);
+    if (layout.splits > 1) {
+      if (workspace_bytes < layout.bytes)
+        return fail(MI_ERR_WORKSPACE, "%s: workspace of %lld bytes, the split form needs %lld", what,
+                    static_cast<long long>(workspace_bytes), static_cast<long long>(layout.bytes));
+      if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return fail(MI_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned", what);
+      ExactSplitArgs sa{};
+      sa.d = a;
+      sa.d.cache_tokens = 0;
+      sa.scores = static_cast<uint16_t*>(workspace);
+      sa.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + layout.scores_bytes);
+      sa.ctx_cap = static_cast<int32_t>(tokens);
+      sa.splits = layout.splits;
+      const int32_t rc = prologue ? dispatch_exact_split<true>(sa, batch, group, s)
+                                  : dispatch_exact_split<false>(sa, batch, group, s);
+      return rc == MI_OK ? ok() : rc;
+    }
+  }
   // One launch per 65535 sequences (grid y holds the KV heads, x the sequences).
   for (int32_t b0 = 0; b0 < batch; b0 += 65535) {
     const int32_t nb = batch - b0 < 65535 ? batch - b0 : 65535;
@@ -953,6 +1365,11 @@ extern "C" int32_t mi_paged_decode_attention_exact(
     if (rc != MI_OK) return rc;
   }
   return ok();
+}
+
+extern "C" int64_t mi_paged_decode_exact_workspace_bytes(int32_t batch, int32_t max_blocks, int32_t num_heads,
+                                                         int32_t num_kv_heads) {
+  return mi::exact_split_layout(batch, max_blocks, num_heads, num_kv_heads).bytes;
 }
 
 extern "C" int32_t mi_chunked_prefill_attention_exact(

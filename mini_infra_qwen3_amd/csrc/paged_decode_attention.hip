@@ -70,6 +70,14 @@ constexpr int kDepth = MI_DECODE_DEPTH;            // register ring depth (block
 constexpr int kMaxWaves = MI_DECODE_MAX_WAVES;     // wavefronts (KV heads) per workgroup
 constexpr bool kNtLoads = MI_DECODE_NT_LOADS != 0; // K/V stream with the non-temporal hint
 constexpr int kGroupsPerCu = MI_DECODE_GROUPS_PER_CU;
+#ifndef MI_DECODE_XCD_RUN
+#define MI_DECODE_XCD_RUN 0
+#endif
+// Consecutive stream-kernel workgroups per XCD run (0: launch order, which deals a range's head
+// groups to different XCDs).  Unlike the scatter and the gather, decode loses with runs: at batch
+// 256 (Σctx 755,887, 28 layers, three repetitions) 461-462 µs per layer without, 476.6-478.0 with
+// runs of 4, 8, 16 or 32; four KV heads per workgroup (MI_DECODE_MAX_WAVES=4) 523-526 µs.
+constexpr int kXcdRun = MI_DECODE_XCD_RUN;
 constexpr int kMaxBatchPerLaunch = 4096;           // sequences whose prefix sum one workgroup holds in LDS
 constexpr int kMinBlocksPerStream = 16;            // small launches use fewer, longer ranges
 constexpr int kWindow = 64;                        // block ids fetched per window, one per lane
@@ -447,8 +455,20 @@ __global__ __launch_bounds__(64 * kWaves, (kGroupsPerCu * kWaves + 3) / 4) void 
   __shared__ int s_wave[kWaves];
   __shared__ __align__(16) uint16_t s_kst[kMfma ? kWaves : 1][kMfma ? kBlockSize * kKStageRow : 8];
   const int total = scan_blocks<kThreads>(a, s_off, s_wave);
-  const int stream = blockIdx.x / kHeadGroups;
-  const int hg = blockIdx.x - stream * kHeadGroups;
+  int wg = blockIdx.x;
+  if (kXcdRun > 0) {
+    // Workgroups go round-robin to the XCDs: within each super-run of kXcds * kXcdRun workgroups,
+    // those on XCD i take [i kXcdRun, (i + 1) kXcdRun) in order, so the head groups of a range share
+    // an XCD; the partial tail keeps identity.
+    constexpr int kSuper = kXcds * kXcdRun;
+    const int n = a.streams * kHeadGroups;
+    if (wg < n / kSuper * kSuper) {
+      const int base = wg / kSuper * kSuper, r = wg - base;
+      wg = base + (r % kXcds) * kXcdRun + r / kXcds;
+    }
+  }
+  const int stream = wg / kHeadGroups;
+  const int hg = wg - stream * kHeadGroups;
   const int64_t lo = static_cast<int64_t>(stream) * total / a.streams;
   const int64_t hi = static_cast<int64_t>(stream + 1) * total / a.streams;
   if (lo >= hi) return;

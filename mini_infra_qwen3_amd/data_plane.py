@@ -23,6 +23,7 @@ __all__ = [
     "pack_blocks",
     "paged_decode_attention",
     "paged_decode_attention_fused",
+    "paged_decode_exact_workspace_bytes",
     "paged_decode_workspace_bytes",
     "qk_norm_rope",
     "reshape_and_cache",
@@ -254,6 +255,25 @@ def paged_decode_workspace_bytes(batch: int, max_blocks: int, num_heads: int, he
                                                                         block_size))
 
 
+def paged_decode_exact_workspace_bytes(batch: int, max_blocks: int, num_heads: int, num_kv_heads: int,
+                                       block_size: int = KERNEL_BLOCK_SIZE) -> int:
+    """Workspace of the reference-numerics decode's split form (0: the launch runs unsplit)."""
+    if block_size > KERNEL_BLOCK_SIZE and block_size % KERNEL_BLOCK_SIZE == 0:
+        max_blocks = max_blocks * (block_size // KERNEL_BLOCK_SIZE)
+    return int(_native.load().mi_paged_decode_exact_workspace_bytes(batch, max_blocks, num_heads, num_kv_heads))
+
+
+def _exact_workspace(workspace: torch.Tensor | None, need: int, device: torch.device) -> tuple[int | None, int]:
+    """(pointer, bytes) of a 256-byte aligned workspace of at least ``need`` bytes: ``workspace``
+    when it qualifies, else a new buffer (None, 0 when nothing is needed)."""
+    if need <= 0:
+        return None, 0
+    if workspace is None or workspace.numel() * workspace.element_size() < need or workspace.data_ptr() % 256:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    _require_gpu("workspace", workspace, device)
+    return workspace.data_ptr(), workspace.numel() * workspace.element_size()
+
+
 def paged_decode_attention(
     query: torch.Tensor,
     key_pool: torch.Tensor,
@@ -273,7 +293,7 @@ def paged_decode_attention(
     ``[B, H * D]`` bf16.  ``workspace`` (optional, uint8, reused across calls) holds the
     split-context partials; it is allocated here when missing or too small.  ``exact``: the
     reference-numerics kernel (``mi_paged_decode_attention_exact``: the reference's rounding
-    points with exact sums; no workspace).
+    points with exact sums), whose split form for small batches uses the workspace the same way.
     """
     device = key_pool.device
     for name, t in (("query", query), ("key_pool", key_pool), ("value_pool", value_pool),
@@ -308,12 +328,14 @@ def paged_decode_attention(
     lib = _native.load()
     stream = _stream(device)
     if exact:
+        ws_ptr, ws_bytes = _exact_workspace(
+            workspace, paged_decode_exact_workspace_bytes(batch, max_blocks, num_heads, num_kv_heads), device)
         rc = lib.mi_paged_decode_attention_exact(
             out.data_ptr(), out.stride(0), query.data_ptr(), query.stride(0), query.stride(1), None, 0, None, 0, None,
             None, None, None, 0.0, None, 0, key_pool.data_ptr(), value_pool.data_ptr(), num_blocks,
             block_tables.data_ptr(), block_tables.stride(0) if batch > 1 else max(max_blocks, 1), max_blocks,
             context_lens.data_ptr(), context_lens.stride(0) if batch > 1 else 1, batch, num_heads, num_kv_heads,
-            head_dim, block_size, float(scale), stream)
+            head_dim, block_size, float(scale), ws_ptr, ws_bytes, stream)
         _native.check(rc, "mi_paged_decode_attention_exact")
         return out
     need = paged_decode_workspace_bytes(batch, max_blocks, num_heads, head_dim, block_size, num_kv_heads)
@@ -399,6 +421,8 @@ def paged_decode_attention_fused(
     if batch == 0:
         return out
     if exact:
+        ws_ptr, ws_bytes = _exact_workspace(
+            workspace, paged_decode_exact_workspace_bytes(batch, max_blocks, num_heads, num_kv_heads), device)
         rc = _native.load().mi_paged_decode_attention_exact(
             out.data_ptr(), out.stride(0), q2.data_ptr(), q2.stride(0), head_dim, k2.data_ptr(), k2.stride(0),
             v2.data_ptr(), v2.stride(0), q_weight.data_ptr(), k_weight.data_ptr(), cos2.data_ptr(), sin2.data_ptr(),
@@ -406,7 +430,7 @@ def paged_decode_attention_fused(
             value_pool.data_ptr(), num_blocks, block_tables.data_ptr(),
             block_tables.stride(0) if batch > 1 else max(max_blocks, 1), max_blocks, context_lens.data_ptr(),
             context_lens.stride(0) if batch > 1 else 1, batch, num_heads, num_kv_heads, head_dim, block_size,
-            float(scale), _stream(device))
+            float(scale), ws_ptr, ws_bytes, _stream(device))
         _native.check(rc, "mi_paged_decode_attention_exact")
         return out
     q_scratch = torch.empty((batch, num_heads, head_dim), dtype=torch.bfloat16, device=device)

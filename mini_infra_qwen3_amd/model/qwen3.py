@@ -27,7 +27,9 @@ Numerics (``Qwen3ForCausalLM(config, exact=...)``):
   kernels (the reference's rounding points, exact sums), RMSNorm sums exactly, and every GEMM is
   the call the reference makes -- q, k, v, gate and up as separate projections, since hipBLASLt's
   result for a row can depend on the GEMM's N and M.  Greedy decoding then reproduces the
-  reference's tokens exactly.
+  reference's tokens exactly.  (Running the separate projections of one input concurrently on
+  side streams, fork and join captured in the step's HIP graph, measured slower on MI355X: decode
+  steps 3.92 ms against 3.45 in the continuous-batching run.)
 * ``exact=False`` runs the bandwidth kernels (fp32 online softmax, MFMA prefill) and q/k/v and
   gate/up each as one GEMM over row-concatenated weights (the outputs split as column views):
   within bf16 tolerance of the reference, not bit-identical.
@@ -312,9 +314,15 @@ class Qwen3Model(nn.Module):
                 metadata = metadata._replace(block_tables=metadata.block_tables.index_select(0, metadata.table_rows),
                                              table_rows=None)
             pools = attn_metadata.kv_pools
-            need = data_plane.paged_decode_workspace_bytes(batch, metadata.block_tables.shape[1],
-                                                          self.config.num_attention_heads, self.config.head_dim,
-                                                          pools[0][0].shape[1], self.config.num_key_value_heads)
+            # one buffer serves either decode form: the bandwidth kernel's split-context partials or
+            # the reference-numerics kernel's split form
+            need = max(data_plane.paged_decode_workspace_bytes(batch, metadata.block_tables.shape[1],
+                                                              self.config.num_attention_heads, self.config.head_dim,
+                                                              pools[0][0].shape[1], self.config.num_key_value_heads),
+                       data_plane.paged_decode_exact_workspace_bytes(batch, metadata.block_tables.shape[1],
+                                                                     self.config.num_attention_heads,
+                                                                     self.config.num_key_value_heads,
+                                                                     pools[0][0].shape[1]))
             if need:
                 workspace = torch.empty(need, dtype=torch.uint8, device=device)
         else:

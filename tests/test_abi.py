@@ -201,7 +201,7 @@ def test_empty_pool_is_rejected_before_any_read_on_host(native_lib):
     assert noalloc == bad
     exact = lib.mi_paged_decode_attention_exact(16, 2048, 16, 2048, 128, None, 0, None, 0, None, None, None, None,
                                                 1e-6, None, 1, 16, 16, 0, 16, 4, 4, 16, 1, 2, 16, 8, 128, 16, 0.1,
-                                                None)
+                                                None, 0, None)
     assert exact == bad
     for entry in (lib.mi_chunked_prefill_attention, lib.mi_chunked_prefill_attention_exact):
         rc = entry(16, 2048 * 4, 2048, 16, 16 * 4 * 128, 4 * 128, 128, 16, 8 * 4 * 128, 4 * 128, 128, 16,
@@ -211,3 +211,32 @@ def test_empty_pool_is_rejected_before_any_read_on_host(native_lib):
         rc = entry(16, 2048, 16, 2048, 128, 16, 1024, 128, 16, 1024, 128, 16, 16, 0, 0, 0, None, 0, 0,
                    None, None, 1, 3, 16, 8, 8, 16, 1, 16, 1, 16, 8, 128, 16, 0.1, None)
         assert rc == bad
+
+
+def test_exact_decode_split_workspace_size(native_lib):
+    # launches of at most 48 (sequence, KV head) pairs split: splits = min(ceil(2 x 256 CUs / pairs),
+    # 32, max_blocks / 4); fewer than 2 = unsplit (0)
+    lib = native_lib
+    assert lib.mi_paged_decode_exact_workspace_bytes(256, 512, 16, 8) == 0   # 2048 pairs fill the GPU
+    assert lib.mi_paged_decode_exact_workspace_bytes(9, 72, 16, 8) == 0      # 72 pairs: one launch wins
+    assert lib.mi_paged_decode_exact_workspace_bytes(4, 4, 16, 8) == 0       # one split per 4 blocks at most
+    assert lib.mi_paged_decode_exact_workspace_bytes(0, 64, 16, 8) == 0
+    # 6 sequences x 8 KV heads: 11 splits; scores 48 x 72 x 16 x 2 x 2 B (256-aligned), partials 48 x 11 x 2 x 128 x 8 B
+    scores = -(-(48 * 72 * 16 * 2 * 2) // 256) * 256
+    assert lib.mi_paged_decode_exact_workspace_bytes(6, 72, 16, 8) == scores + 48 * 11 * 2 * 128 * 8
+    # one sequence: 32 splits (capped), GQA group 4
+    assert lib.mi_paged_decode_exact_workspace_bytes(1, 200, 32, 8) == 8 * 200 * 16 * 4 * 2 + 8 * 32 * 4 * 128 * 8
+
+
+def test_exact_decode_rejects_a_short_workspace_on_host(native_lib):
+    lib = native_lib
+    need = lib.mi_paged_decode_exact_workspace_bytes(2, 64, 16, 8)
+    assert need > 0
+    rc = lib.mi_paged_decode_attention_exact(16, 2048, 16, 2048, 128, None, 0, None, 0, None, None, None, None, 1e-6,
+                                             None, 1, 16, 16, 100, 16, 64, 64, 16, 1, 2, 16, 8, 128, 16, 0.1, 256,
+                                             need - 8, None)
+    assert rc == _native.MI_ERR_WORKSPACE and b"split" in lib.mi_last_error()
+    rc = lib.mi_paged_decode_attention_exact(16, 2048, 16, 2048, 128, None, 0, None, 0, None, None, None, None, 1e-6,
+                                             None, 1, 16, 16, 100, 16, 64, 64, 16, 1, 2, 16, 8, 128, 16, 0.1, None,
+                                             64, None)
+    assert rc == _native.MI_ERR_INVALID_ARGUMENT

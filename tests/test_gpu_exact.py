@@ -81,7 +81,7 @@ def test_exact_decode_plain_form_ignores_slot_mapping(device):
     rc = lib.mi_paged_decode_attention_exact(
         out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), q.stride(1), None, 0, None, 0, None, None, None,
         None, 0.0, slots.data_ptr(), 1, kpd.data_ptr(), vpd.data_ptr(), kp.shape[0], bt.data_ptr(), bt.stride(0),
-        bt.shape[1], ctx.data_ptr(), 1, 4, 16, 8, 128, 16, SCALE, data_plane._stream(device))
+        bt.shape[1], ctx.data_ptr(), 1, 4, 16, 8, 128, 16, SCALE, None, 0, data_plane._stream(device))
     _native.check(rc, "mi_paged_decode_attention_exact")
     torch.cuda.synchronize()
     assert_bits(kpd, kp)
