@@ -152,3 +152,46 @@ def test_scheduled_paged_run_matches_serial_generation(budget, capacity, block_s
                            step_clock=lambda out: 1.0)
     for i, (p, m) in enumerate(zip(prompts, budgets)):
         assert result.tokens[i] == serial_generate(model, p, m)
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 16])
+def test_mixed_step_equals_chunk_step_plus_decode_step(block_size):
+    """The oracle's mixed step (prompt chunks and decode tokens in one flattened forward; the
+    reference defines no such step) against the reference's own two steps on the same state: a
+    chunk step over the same chunks (``prefill_chunk_logits``) and a decode step over the same
+    tokens (``decode_step``).  fp32 on the CPU: logits within rounding, the same greedy tokens, the
+    same chunk K/V and the same pools after the decode append."""
+    model = tiny_model(seed=3)
+    gen = torch.Generator().manual_seed(block_size)
+    prompt_a = torch.randint(1, 97, (10,), generator=gen).tolist()   # prefilled; decodes one token
+    prompt_b = torch.randint(1, 97, (13,), generator=gen).tolist()   # first 7 prefilled; chunk 7..12
+    prompt_c = torch.randint(1, 97, (5,), generator=gen).tolist()    # a fresh chunk
+    table_a = tables_from(11, block_size, 1)
+    table_b = tables_from(13, block_size, 1 + len(table_a))
+    table_c = tables_from(5, block_size, 1 + len(table_a) + len(table_b))
+    pools = pools_for(model, 1 + len(table_a) + len(table_b) + len(table_c), block_size)
+    _, presents = qwen3_ref.prefill_chunk_logits(model, [prompt_a, prompt_b[:7]], [0, 0], [table_a, table_b], pools,
+                                                 block_size)
+    qwen3_ref.store_prefill(pools, presents, [table_a, table_b], [10, 7], [0, 0], block_size)
+    last_a = int(torch.randint(1, 97, (1,), generator=gen))
+
+    two = [(k.clone(), v.clone()) for k, v in pools]
+    chunk_logits, chunk_presents = qwen3_ref.prefill_chunk_logits(model, [prompt_b[7:], prompt_c], [7, 0],
+                                                                  [table_b, table_c], two, block_size)
+    decode_logits = qwen3_ref.decode_step(model, [table_a], [last_a], [10], two, block_size)
+
+    one = [(k.clone(), v.clone()) for k, v in pools]
+    mixed_logits, mixed_presents = qwen3_ref.mixed_step_logits(model, [prompt_b[7:], prompt_c], [7, 0],
+                                                               [table_b, table_c], [last_a], [10], [table_a], one,
+                                                               block_size)
+    want = torch.cat((chunk_logits, decode_logits))
+    assert mixed_logits.shape == want.shape
+    torch.testing.assert_close(mixed_logits, want, rtol=1e-5, atol=1e-5)
+    assert mixed_logits.argmax(-1).tolist() == want.argmax(-1).tolist()
+    width = 6
+    for (mk, mv), (ck, cv) in zip(mixed_presents, chunk_presents):
+        torch.testing.assert_close(mk, ck[:, :, -width:], rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(mv, cv[:, :, -width:], rtol=1e-5, atol=1e-5)
+    for (ok, ov), (tk, tv) in zip(one, two):
+        torch.testing.assert_close(ok, tk, rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(ov, tv, rtol=1e-5, atol=1e-5)
