@@ -700,10 +700,61 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
         "prefill_graphs": not exact,
         "setup_s": round(setup_s, 2),
         "latency_ms": {k: round(v, 2) for k, v in res.latency_summary().items()},
+        "_tokens": res.tokens,  # per request, for the token agreement; dropped from the JSON line
     }
     del model, res
     torch.cuda.empty_cache()
     return out
+
+
+def token_agreement(reference: dict[int, list[int]], tokens: dict[int, list[int]], device: torch.device,
+                    seed: int = 0) -> dict:
+    """How many requests of a bandwidth-kernel run emit exactly the tokens of the reference-numerics
+    run (whose tokens the GPU tests show identical to the oracle's; exact equality is the
+    reference's own gate, src/mini_infra/bench/correctness.py:69-73), and for each other request its
+    first divergence: the position, and the logit margin the reference-numerics model has there
+    between its own token and the bandwidth run's, with the top-1 / top-2 margin beside it.  The
+    logits are recomputed with one reference-numerics prefill over the prompt and the common prefix
+    (the same weights); GEMM rows can round differently at another M, so a margin is a measure of
+    how close to a tie the step was, not a bit-exact replay."""
+    from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
+    from mini_infra_qwen3_amd.workloads import serving_requests
+
+    requests = serving_requests(seed=seed)
+    model = Qwen3ForCausalLM(qwen3_0_6b(), exact=True)
+    init_random_(model, seed=seed, std=0.02)
+    model = model.to(device=device, dtype=torch.bfloat16).eval()
+    identical, first, margins, top2, total_same = 0, [], [], [], 0
+    with torch.inference_mode():
+        for r in requests:
+            ref, got = reference[r.request_idx], tokens[r.request_idx]
+            total_same += sum(a == b for a, b in zip(ref, got))
+            if ref == got:
+                identical += 1
+                continue
+            d = next((i for i, (a, b) in enumerate(zip(ref, got)) if a != b), min(len(ref), len(got)))
+            first.append(d)
+            if d >= min(len(ref), len(got)):
+                continue
+            ids = torch.tensor([list(r.token_ids) + ref[:d]], dtype=torch.long, device=device)
+            logits, _ = model(ids, last_logits_only=True)
+            row = logits[0, -1].float()
+            margins.append(float(row[ref[d]] - row[got[d]]))
+            best = torch.topk(row, 2).values
+            top2.append(float(best[0] - best[1]))
+    del model
+    torch.cuda.empty_cache()
+
+    def spread(values):
+        if not values:
+            return None
+        v = sorted(values)
+        return {"min": round(v[0], 5), "median": round(v[len(v) // 2], 5), "max": round(v[-1], 5)}
+
+    return {"requests": len(requests), "identical_requests": identical,
+            "identical_tokens_frac": round(total_same / max(sum(len(t) for t in reference.values()), 1), 4),
+            "first_divergence_position": spread(first),
+            "margin_at_divergence": spread(margins), "top2_margin_at_divergence": spread(top2)}
 
 
 def bench_decode_groups(steps: int, warmup: int, device) -> dict:
@@ -754,7 +805,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "scatter-sequential", "scatter-head",
                                            "gather", "gather-sequential", "prefill",
-                                           "copy", "swap", "e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth", "all"],
+                                           "copy", "swap", "e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth",
+                                           "e2e-agreement", "all"],
                         default="all")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -788,8 +840,17 @@ def main() -> int:
         return 0
     if args.only in ("e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth"):
         res = bench_e2e(device, mixed=args.only.startswith("e2e-mixed"), exact=not args.only.endswith("bandwidth"))
+        res.pop("_tokens")
         log(f"e2e: {res['output_tok_s']:.1f} output tok/s (busy), {res['wall_tok_s']:.1f} tok/s (wall)")
         print(json.dumps(res), flush=True)
+        return 0
+    if args.only == "e2e-agreement":
+        ref = bench_e2e(device)
+        for key, mixed in (("e2e_bandwidth_kernels", False), ("e2e_mixed_batching", True)):
+            bw = bench_e2e(device, mixed=mixed, exact=False)
+            agreement = token_agreement(ref["_tokens"], bw["_tokens"], device)
+            log(f"{key}: {json.dumps(agreement)}")
+            print(json.dumps({key: agreement}), flush=True)
         return 0
     dec = bench_decode(args.steps, args.warmup, device)
     log(f"decode: {dec['ms_per_step']:.3f} ms/step, {dec['value']:.1f} GB/s; attention launch "
@@ -852,12 +913,19 @@ def main() -> int:
         e2e = bench_e2e(device)
         log(f"e2e: {e2e['output_tok_s']:.1f} output tok/s (busy), {e2e['wall_tok_s']:.1f} tok/s (wall)")
         e2e_bw = bench_e2e(device, exact=False)
+        e2e_bw["token_agreement"] = token_agreement(e2e["_tokens"], e2e_bw["_tokens"], device)
         log(f"e2e bandwidth kernels: {e2e_bw['output_tok_s']:.1f} output tok/s (busy), ITL max "
-            f"{e2e_bw['latency_ms']['itl_ms_max']:.2f} ms")
+            f"{e2e_bw['latency_ms']['itl_ms_max']:.2f} ms; {e2e_bw['token_agreement']['identical_requests']} of 128 "
+            f"requests token-identical to reference numerics")
         e2e_mixed = bench_e2e(device, mixed=True, exact=False)
+        e2e_mixed["token_agreement"] = token_agreement(e2e["_tokens"], e2e_mixed["_tokens"], device)
         log(f"e2e mixed batching (bandwidth kernels): {e2e_mixed['output_tok_s']:.1f} output tok/s (busy), ITL max "
-            f"{e2e_mixed['latency_ms']['itl_ms_max']:.2f} ms")
+            f"{e2e_mixed['latency_ms']['itl_ms_max']:.2f} ms; {e2e_mixed['token_agreement']['identical_requests']} "
+            f"of 128 requests token-identical")
         e2e_mixed_exact = bench_e2e(device, mixed=True)
+        e2e_mixed_exact["token_agreement"] = token_agreement(e2e["_tokens"], e2e_mixed_exact["_tokens"], device)
+        for r in (e2e, e2e_bw, e2e_mixed, e2e_mixed_exact):
+            r.pop("_tokens")
         log(f"e2e mixed batching (reference numerics): {e2e_mixed_exact['output_tok_s']:.1f} output tok/s (busy), "
             f"ITL max {e2e_mixed_exact['latency_ms']['itl_ms_max']:.2f} ms")
         if not args.no_cpu_baseline:
