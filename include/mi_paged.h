@@ -371,10 +371,12 @@ int32_t mi_rms_norm(void* out, const void* x, const void* residual, void* residu
  *   q_out[t, h] = rope(bf16(q_weight * bf16(norm(q[t, h]))), cos[t], sin[t])
  *   rope(x) = bf16(bf16(x * cos) + bf16(rotate_half(x) * sin)),  rotate_half(x) = cat(-x[64:], x[:64])
  * and the same for k with k_weight; v is copied unchanged.
- * Prefill form (slot_mapping == NULL): k and v go to k_out / v_out [T, Hkv, 128].
- * Decode form: they go straight to pool slot slot_mapping[t * slot_stride] of key_pool /
- * value_pool ([num_slots, Hkv, 128]) -- the reshape-and-cache append of
- * _apply_paged_kv_pool (:282-283) fused in; out-of-range slots are skipped.
+ * Rows: with k_out / v_out ([T, Hkv, 128]) each token's k and v rows go there.
+ * Slots: with slot_mapping they also go (or, without k_out / v_out, only go) straight to pool slot
+ * slot_mapping[t * slot_stride] of key_pool / value_pool ([num_slots, Hkv, 128]) -- the
+ * reshape-and-cache append of _apply_paged_kv_pool (:282-283) for a decode step, or
+ * PagedKVCachePool.write_prefill (paged_kv_cache.py:74-95) for a prefill chunk whose block table
+ * already covers it (paged_runner.py:49); out-of-range slots (-1 for left padding) are skipped.
  * q / k / v: token rows with element strides q_stride / k_stride / v_stride; cos / sin: [T, 128].
  * q_out: [T, Hq, 128].  head_dim must be 128.
  */

@@ -94,8 +94,8 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(const NormArgs a) {
 // ------------------------------------------------------------ q/k RMSNorm + RoPE (+ append)
 struct QkArgs {
   uint16_t* q_out;        // [T, Hq, 128]
-  uint16_t* k_out;        // [T, Hkv, 128] (prefill form) or null
-  uint16_t* v_out;        // [T, Hkv, 128] (prefill form) or null
+  uint16_t* k_out;        // [T, Hkv, 128] (rows form) or null
+  uint16_t* v_out;        // [T, Hkv, 128] (rows form) or null
   const uint16_t* q;      // row stride q_stride
   const uint16_t* k;
   const uint16_t* v;
@@ -104,7 +104,7 @@ struct QkArgs {
   const uint16_t* k_weight;  // [128]
   const uint16_t* cos;       // [T, 128]
   const uint16_t* sin;       // [T, 128]
-  const int64_t* slot_mapping;  // decode form: K/V rows go to pool slots; null in the prefill form
+  const int64_t* slot_mapping;  // K/V rows also (or only, without k_out) go to these pool slots; or null
   int64_t slot_stride;
   uint16_t* key_pool;        // [num_slots, Hkv, 128]
   uint16_t* value_pool;
@@ -134,22 +134,29 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(const QkArgs a) 
   const uint16_t* src = is_q ? a.q + t * a.q_stride + h * 128 : a.k + t * a.k_stride + h * 128;
   float o0, o1;
   norm_rope_head(src, is_q ? a.q_weight : a.k_weight, a.cos + t * 128, a.sin + t * 128, a.eps, lane, o0, o1);
-  uint16_t* dst;
   if (is_q) {
-    dst = a.q_out + (t * a.q_heads + h) * 128;
-  } else if (a.slot_mapping) {
-    if (slot < 0) return;
-    dst = a.key_pool + (slot * a.kv_heads + h) * 128;
-  } else {
-    dst = a.k_out + (t * a.kv_heads + h) * 128;
+    uint16_t* dst = a.q_out + (t * a.q_heads + h) * 128;
+    dst[lane] = f32_to_bf16(o0);
+    dst[lane + 64] = f32_to_bf16(o1);
+    return;
   }
-  dst[lane] = f32_to_bf16(o0);
-  dst[lane + 64] = f32_to_bf16(o1);
-  if (!is_q) {
-    const uint16_t* vs = a.v + t * a.v_stride + h * 128;
-    uint16_t* vd = a.slot_mapping ? a.value_pool + (slot * a.kv_heads + h) * 128 : a.v_out + (t * a.kv_heads + h) * 128;
-    vd[lane] = vs[lane];
-    vd[lane + 64] = vs[lane + 64];
+  const uint16_t* vs = a.v + t * a.v_stride + h * 128;
+  const uint16_t v0 = vs[lane], v1 = vs[lane + 64];
+  if (a.k_out) {  // the token's rows
+    uint16_t* kd = a.k_out + (t * a.kv_heads + h) * 128;
+    uint16_t* vd = a.v_out + (t * a.kv_heads + h) * 128;
+    kd[lane] = f32_to_bf16(o0);
+    kd[lane + 64] = f32_to_bf16(o1);
+    vd[lane] = v0;
+    vd[lane + 64] = v1;
+  }
+  if (slot >= 0) {  // and / or its pool slot
+    uint16_t* kd = a.key_pool + (slot * a.kv_heads + h) * 128;
+    uint16_t* vd = a.value_pool + (slot * a.kv_heads + h) * 128;
+    kd[lane] = f32_to_bf16(o0);
+    kd[lane + 64] = f32_to_bf16(o1);
+    vd[lane] = v0;
+    vd[lane + 64] = v1;
   }
 }
 
@@ -226,8 +233,11 @@ extern "C" int32_t mi_qk_norm_rope(void* q_out, void* k_out, void* v_out, const 
   if (num_tokens == 0) return ok();
   if (!q_out || !q || !k || !v || !q_weight || !k_weight || !cos || !sin)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_qk_norm_rope: null pointer argument");
-  if (slot_mapping ? (!key_pool || !value_pool || num_slots < 0 || slot_stride <= 0) : (!k_out || !v_out))
-    return fail(MI_ERR_INVALID_ARGUMENT, "mi_qk_norm_rope: give either slot_mapping and pools or k_out and v_out");
+  if (!k_out != !v_out) return fail(MI_ERR_INVALID_ARGUMENT, "mi_qk_norm_rope: give both k_out and v_out or neither");
+  if (!slot_mapping && !k_out)
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_qk_norm_rope: give k_out and v_out, slot_mapping and pools, or both");
+  if (slot_mapping && (!key_pool || !value_pool || num_slots < 0 || slot_stride <= 0))
+    return fail(MI_ERR_INVALID_ARGUMENT, "mi_qk_norm_rope: slot_mapping needs both pools, num_slots and a stride");
   if (q_stride < num_heads * 128 || k_stride < num_kv_heads * 128 || v_stride < num_kv_heads * 128)
     return fail(MI_ERR_INVALID_ARGUMENT, "mi_qk_norm_rope: row strides shorter than a row");
   QkArgs a{static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out),

@@ -666,16 +666,17 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: to
                  k_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float,
                  slot_mapping: torch.Tensor | None = None, key_pool: torch.Tensor | None = None,
                  value_pool: torch.Tensor | None = None, k_out: torch.Tensor | None = None,
-                 v_out: torch.Tensor | None = None):
+                 v_out: torch.Tensor | None = None, rows: bool | None = None):
     """Per-head RMSNorm + RoPE of q and k, v passed through (one launch).
 
     q ``[..., Hq * 128]``, k / v ``[..., Hkv * 128]`` over the same T tokens (row views of a
     projection are fine); cos / sin ``[T, 128]`` (any leading shape with T tokens).
-    Returns ``q_out [T, Hq, 128]`` and, in the prefill form, ``k_out`` / ``v_out [T, Hkv, 128]``;
-    with ``slot_mapping`` (decode form) k and v are written into ``key_pool`` / ``value_pool``
-    ``[num_blocks, block_size, Hkv, 128]`` at those slots and ``(q_out, None, None)`` is returned.
-    ``k_out`` / ``v_out`` (prefill form, optional): contiguous ``[T, Hkv, 128]`` buffers to write
-    instead of new ones.
+    Returns ``q_out [T, Hq, 128]`` and, with ``rows``, ``k_out`` / ``v_out [T, Hkv, 128]``; with
+    ``slot_mapping`` ``[T]`` k and v are (also) written into ``key_pool`` / ``value_pool``
+    ``[num_blocks, block_size, Hkv, 128]`` at those slots (-1: skipped).  ``rows`` defaults to
+    "no slot_mapping"; without rows ``(q_out, None, None)`` is returned (the decode form).
+    ``k_out`` / ``v_out`` (optional): contiguous ``[T, Hkv, 128]`` buffers to write instead of new
+    ones.
     """
     device = q.device
     for name, t in (("q", q), ("k", k), ("v", v), ("q_weight", q_weight), ("k_weight", k_weight),
@@ -690,7 +691,9 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: to
         raise ValueError("k / v / weights have inconsistent head sizes")
     q_out = torch.empty((tokens, num_heads, head_dim), dtype=q.dtype, device=device)
     lib = _native.load()
-    if slot_mapping is None:
+    if rows is None:
+        rows = slot_mapping is None
+    if rows:
         for name, given in (("k_out", k_out), ("v_out", v_out)):
             if given is not None:
                 _require_gpu(name, given, device)
@@ -699,6 +702,9 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: to
                     raise ValueError(f"{name} must be contiguous [{tokens}, {num_kv_heads}, {head_dim}] {q.dtype}")
         k_out = torch.empty((tokens, num_kv_heads, head_dim), dtype=q.dtype, device=device) if k_out is None else k_out
         v_out = torch.empty((tokens, num_kv_heads, head_dim), dtype=q.dtype, device=device) if v_out is None else v_out
+    else:
+        k_out = v_out = None
+    if slot_mapping is None:
         rc = lib.mi_qk_norm_rope(q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), q2.data_ptr(), q2.stride(0),
                                  k2.data_ptr(), k2.stride(0), v2.data_ptr(), v2.stride(0), q_weight.data_ptr(),
                                  k_weight.data_ptr(), cos2.data_ptr(), sin2.data_ptr(), tokens, num_heads,
@@ -716,12 +722,12 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: to
                 raise ValueError(f"{name} must be contiguous [num_blocks, block_size, {num_kv_heads}, {head_dim}]")
         num_slots = key_pool.numel() // (num_kv_heads * head_dim)
         _check_range("slot_mapping", slot_mapping, num_slots, allow_minus_one=True)
-        rc = lib.mi_qk_norm_rope(q_out.data_ptr(), None, None, q2.data_ptr(), q2.stride(0), k2.data_ptr(),
+        rc = lib.mi_qk_norm_rope(q_out.data_ptr(), k_out.data_ptr() if rows else None,
+                                 v_out.data_ptr() if rows else None, q2.data_ptr(), q2.stride(0), k2.data_ptr(),
                                  k2.stride(0), v2.data_ptr(), v2.stride(0), q_weight.data_ptr(), k_weight.data_ptr(),
                                  cos2.data_ptr(), sin2.data_ptr(), tokens, num_heads, num_kv_heads, head_dim,
                                  float(eps), slot_mapping.data_ptr(), slot_mapping.stride(0), key_pool.data_ptr(),
                                  value_pool.data_ptr(), num_slots, _stream(device))
-        k_out = v_out = None
     _native.check(rc, "mi_qk_norm_rope")
     return q_out, k_out, v_out
 

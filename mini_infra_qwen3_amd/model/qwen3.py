@@ -78,6 +78,10 @@ class PagedPrefillMetadata(NamedTuple):
     # optional per-layer (K, V) buffers, contiguous [B * L, H_kv, D], that receive the chunk's K/V
     # (the present) instead of new allocations
     kv_out: tuple[PastKeyValue, ...] = ()
+    # optional [B, L] int64: the pool slot of each padded position's token (-1: none).  The chunk's
+    # K/V rows then also go straight into the pool (the reference's later store_prefill, when the
+    # block tables already cover the chunk: src/mini_infra/worker/paged_runner.py:49,104-136)
+    slot_mapping: torch.Tensor | None = None
 
 
 class PagedMixedMetadata(NamedTuple):
@@ -186,8 +190,11 @@ class Qwen3Attention(nn.Module):
             present = kv_pool
         else:
             k_buf, v_buf = kv_out if kv_out is not None else (None, None)
-            q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin,
-                                                           eps, k_out=k_buf, v_out=v_buf)
+            slots = metadata.slot_mapping
+            q_rot, k_rot, v_rows = data_plane.qk_norm_rope(
+                q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin, eps,
+                slot_mapping=None if slots is None else slots.reshape(-1), key_pool=key_pool, value_pool=value_pool,
+                k_out=k_buf, v_out=v_buf, rows=True)
             # token-major [B, L, H, D] buffers seen as [B, H, L, D] (strided views, no copies)
             q_rot = q_rot.view(batch, length, self.num_heads, self.head_dim).transpose(1, 2)
             k_rot = k_rot.view(batch, length, self.num_kv_heads, self.head_dim).transpose(1, 2)

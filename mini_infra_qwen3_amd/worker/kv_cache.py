@@ -14,6 +14,10 @@ class KVCache:
         layers = () if past_key_values is None else past_key_values
         self.key_cache: list[torch.Tensor] = [k for k, _ in layers]
         self.value_cache: list[torch.Tensor] = [v for _, v in layers]
+        # Not in the reference: the ``[3, N]`` store index (token rows, positions, slots) of the rows
+        # the forward already wrote into the pool, or None; a store with the same index has nothing
+        # left to do.
+        self.written_index = None
 
     @property
     def past_key_values(self) -> list[tuple[torch.Tensor, torch.Tensor]]:

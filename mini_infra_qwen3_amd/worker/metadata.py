@@ -88,14 +88,17 @@ def prefill_scatter_indices(block_tables: Sequence[Sequence[int]], chunk_lens: S
 
 def pack_prefill_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions: Sequence[int],
                       block_tables: Sequence[Sequence[int]], block_size: int, pad_token_id: int,
-                      width: int | None = None, history_blocks: int | None = None) -> np.ndarray:
+                      width: int | None = None, history_blocks: int | None = None,
+                      slots: bool = False) -> np.ndarray:
     """``[B, 2 L + 2 + max_history_blocks]``: left-padded ids | positions | start, len | history table.
 
     Same row layout as the reference's chunked-prefill packing
     (src/mini_infra/worker/paged_runner.py:57-72); history blocks are the first
     ``ceil(start / block_size)`` entries of each table, null-padded.  ``width`` / ``history_blocks``
     (at least the longest chunk / history) fix the shape of a padded bucket: wider left padding
-    (pad tokens at position 0) and null-padded tables.
+    (pad tokens at position 0) and null-padded tables.  ``slots``: L more columns, the pool slot of
+    each padded position's token (``table[p // block_size] * block_size + p % block_size`` at its
+    logical position p), -1 for left padding and for tokens past the end of the table.
     """
     lens = [len(ids) for ids in chunk_token_ids]
     if not lens or min(lens) < 1:
@@ -109,8 +112,18 @@ def pack_prefill_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions:
         raise ValueError(f"chunks of {max(lens)} tokens / {max(hist)} history blocks do not fit "
                          f"width {width} / {history_blocks} blocks")
     max_hist = history_blocks
-    out = np.zeros((len(lens), 2 * width + 2 + max_hist), dtype=np.int64)
+    out = np.zeros((len(lens), 2 * width + 2 + max_hist + (width if slots else 0)), dtype=np.int64)
     out[:, :width] = pad_token_id
+    if slots:
+        base = 2 * width + 2 + max_hist
+        out[:, base:] = -1
+        for row, (n, start, table) in enumerate(zip(lens, start_positions, block_tables)):
+            logical = np.arange(start, start + n, dtype=np.int64)
+            covered = logical < len(table) * block_size
+            ids = np.asarray(table, dtype=np.int64)
+            cols = base + width - n + np.nonzero(covered)[0]
+            lc = logical[covered]
+            out[row, cols] = ids[lc // block_size] * block_size + lc % block_size
     for row, (ids, n, start, table, h) in enumerate(zip(chunk_token_ids, lens, start_positions, block_tables, hist)):
         out[row, width - n:width] = np.asarray(ids, dtype=np.int64)
         out[row, 2 * width - n:2 * width] = np.arange(start, start + n, dtype=np.int64)

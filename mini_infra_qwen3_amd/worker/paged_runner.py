@@ -99,17 +99,18 @@ class _DecodeGraph:
 
 class _PrefillGraph:
     """The chunked-prefill forward of one (rows, padded width W) bucket with history tables NB blocks
-    wide, captured over a static packed buffer ``[rows, 2 W + 2 + NB]`` in the ``pack_prefill_rows``
-    layout.  The
-    chunk K/V (the present) go to the runner's staging buffers, which every prefill graph shares, so
-    captured graphs hold no per-graph outputs beyond their logits."""
+    wide, captured over a static packed buffer ``[rows, 2 W + 2 + NB + W]`` in the
+    ``pack_prefill_rows(..., slots=True)`` layout.  The chunk K/V (the present) go to the runner's
+    staging buffers, which every prefill graph shares, so captured graphs hold no per-graph outputs
+    beyond their logits; tokens with a slot (>= 0) also go straight into the pool."""
 
     def __init__(self, model: torch.nn.Module, pool: PagedKVCachePool, rows: int, width: int, hist_blocks: int,
                  staging: torch.Tensor, mempool, pad_token_id: int, device: torch.device):
         self.rows, self.width, self.hist_blocks = rows, width, hist_blocks
         self.pad_token_id = pad_token_id
-        self.static = torch.zeros((rows, 2 * width + 2 + hist_blocks), dtype=torch.long, device=device)
+        self.static = torch.zeros((rows, 3 * width + 2 + hist_blocks), dtype=torch.long, device=device)
         self.static[:, :width] = pad_token_id  # every row is an empty chunk until a step is loaded
+        self.static[:, 2 * width + 2 + hist_blocks:] = -1
         ids, pos, meta = self.views()
         tokens = rows * width
         meta = meta._replace(kv_pools=tuple(pool.kv_pools),
@@ -128,12 +129,14 @@ class _PrefillGraph:
         self.presents = presents
 
     def views(self):
-        s, w = self.static, self.width
-        return s[:, :w], s[:, w:2 * w], PagedPrefillMetadata(history_block_tables=s[:, 2 * w + 2:],
-                                                             start_lens=s[:, 2 * w], chunk_lens=s[:, 2 * w + 1])
+        s, w, nb = self.static, self.width, self.hist_blocks
+        return s[:, :w], s[:, w:2 * w], PagedPrefillMetadata(history_block_tables=s[:, 2 * w + 2:2 * w + 2 + nb],
+                                                             start_lens=s[:, 2 * w], chunk_lens=s[:, 2 * w + 1],
+                                                             slot_mapping=s[:, 2 * w + 2 + nb:])
 
     def load(self, packed: np.ndarray) -> None:
-        """Copies a step packed at the bucket's shape (``pack_prefill_rows(..., width, history_blocks)``)."""
+        """Copies a step packed at the bucket's shape (``pack_prefill_rows(..., width, history_blocks,
+        slots=True)``)."""
         self.static.copy_(torch.from_numpy(packed))
 
 
@@ -371,28 +374,47 @@ class PagedRunner(BaseModelRunner):
         if self._prefill_graphs and pool is self._prefill_pool:
             hist = max(-(-st // pool.block_size) for st in start_positions)
             graph = self._prefill_bucket(len(chunk_token_ids), width, hist)
+        # When every table already covers its chunk (the reference's contract allows it:
+        # paged_runner.py:49), q/k norm + RoPE also writes the chunk's K/V rows into their slots and
+        # the store that follows has nothing left to do.
+        lens = [len(c) for c in chunk_token_ids]
+        direct = all(len(t) * pool.block_size >= s + n for t, s, n in zip(block_tables, start_positions, lens))
         if graph is not None:
-            graph.load(pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size,
-                                         self.pad_token_id, width=graph.width, history_blocks=graph.hist_blocks))
+            packed = pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size,
+                                       self.pad_token_id, width=graph.width, history_blocks=graph.hist_blocks,
+                                       slots=True)
+            if not direct:
+                packed[:, 2 * graph.width + 2 + graph.hist_blocks:] = -1
+            graph.load(packed)
             with StepTimer(self.device) as timer:
                 graph.graph.replay()
                 next_token = argmax_rows(graph.logits)
-            return PrefillOutput(next_token.tolist(), KVCache(graph.presents), timer.elapsed_ms)
-        packed = torch.from_numpy(pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size,
-                                                    self.pad_token_id)).to(self.device)
+            cache = KVCache(graph.presents)
+            if direct:
+                cache.written_index = prefill_scatter_indices(block_tables, lens, start_positions, graph.width,
+                                                              pool.block_size)
+            return PrefillOutput(next_token.tolist(), cache, timer.elapsed_ms)
+        packed_np = pack_prefill_rows(chunk_token_ids, start_positions, block_tables, pool.block_size,
+                                      self.pad_token_id, slots=direct)
+        nb = packed_np.shape[1] - 2 * width - 2 - (width if direct else 0)
+        packed = torch.from_numpy(packed_np).to(self.device)
         input_ids = packed[:, :width]
         position_ids = packed[:, width:2 * width]
         metadata = PagedPrefillMetadata(
-            history_block_tables=packed[:, 2 * width + 2:],
+            history_block_tables=packed[:, 2 * width + 2:2 * width + 2 + nb],
             start_lens=packed[:, 2 * width],
             chunk_lens=packed[:, 2 * width + 1],
             kv_pools=tuple(pool.kv_pools),
+            slot_mapping=packed[:, 2 * width + 2 + nb:] if direct else None,
         )
         with StepTimer(self.device) as timer:
             logits, present = self.model(input_ids, position_ids=position_ids, attn_metadata=metadata,
                                          last_logits_only=True)
             next_token, _ = greedy_sample(logits)
-        return PrefillOutput(next_token.squeeze(-1).tolist(), KVCache(present), timer.elapsed_ms)
+        cache = KVCache(present)
+        if direct:
+            cache.written_index = prefill_scatter_indices(block_tables, lens, start_positions, width, pool.block_size)
+        return PrefillOutput(next_token.squeeze(-1).tolist(), cache, timer.elapsed_ms)
 
     def store_prefill(
         self,
@@ -408,6 +430,9 @@ class PagedRunner(BaseModelRunner):
                                         pool.block_size)
         if index.shape[1] == 0:
             return
+        written = getattr(prefill_cache, "written_index", None)
+        if written is not None and written.shape == index.shape and np.array_equal(written, index):
+            return  # the forward already wrote these rows into these slots
         index_t = torch.from_numpy(index).to(self.device)
         pool.write_prefill(prefill_cache, token_rows=index_t[0], token_positions=index_t[1], slot_mapping=index_t[2])
 

@@ -520,6 +520,44 @@ def test_exact_models_refuse_padded_prefill_and_mixed_graphs(models):
                                    max_decode_blocks=4)
 
 
+@pytest.mark.parametrize("form", ["exact_eager", "bandwidth_graphs"])
+def test_prefill_direct_pool_write_matches_the_two_pass_store(models, fast_model, form):
+    """When the block tables already cover the chunk, q/k norm + RoPE writes the chunk's K/V rows
+    straight into their slots and store_prefill finds nothing left to do; the pools are then
+    bit-identical to the two-pass path (tables covering only the history during the forward, the
+    scatter afterwards).  Reference numerics eagerly, and the bandwidth form through prefill graphs."""
+    model = models[0] if form == "exact_eager" else fast_model
+    cfg = model.config
+    prompts = prompts_of([70, 45, 100], seed=21)
+    manager = KVCacheManager(BS, num_blocks=48)
+    for i, p in enumerate(prompts):
+        manager.allocate_slots(i, len(p))
+    tables = [manager.block_table(i) for i in range(3)]
+    pools = [make_pool(cfg, 48), make_pool(cfg, 48)]  # direct, two-pass
+    runners = [PagedRunner(model), PagedRunner(model)]
+    if form == "bandwidth_graphs":
+        for runner, pool in zip(runners, pools):
+            runner.enable_prefill_graphs(pool, max_rows=3, max_width=128, max_history_blocks=8)
+    steps = [([0, 1, 2], [0, 0, 0], [40, 20, 64]), ([0, 1, 2], [40, 20, 64], [70, 45, 100])]
+    with torch.inference_mode():
+        for reqs, starts, ends in steps:
+            chunks = [prompts[r][s:e] for r, s, e in zip(reqs, starts, ends)]
+            lens = [e - s for s, e in zip(starts, ends)]
+            full = [tables[r] for r in reqs]
+            history_only = [t[:-(-s // BS)] for t, s in zip(full, starts)]
+            direct = runners[0].run_prefill_chunk_step(chunks, starts, full, pools[0])
+            assert direct.prefill_cache.written_index is not None
+            runners[0].store_prefill(pools[0], direct.prefill_cache, full, lens, starts)
+            two_pass = runners[1].run_prefill_chunk_step(chunks, starts, history_only, pools[1])
+            assert two_pass.prefill_cache.written_index is None
+            runners[1].store_prefill(pools[1], two_pass.prefill_cache, full, lens, starts)
+            assert direct.next_tokens == two_pass.next_tokens
+            torch.cuda.synchronize()
+            assert_bits(pools[0].storage, pools[1].storage)
+    for r, p in enumerate(prompts):  # every token of every prompt is in place
+        assert request_kv(pools[0], 0, tables[r], len(p))[0].abs().sum() > 0
+
+
 def test_prefill_graph_replays_match_eager_forward(fast_model, models):
     """Prefill graphs: each replay equals an eager forward of the same padded inputs, bit for bit
     (logits and the chunk K/V), with eager work and syncs between replays, across row counts, widths

@@ -148,3 +148,35 @@ def test_mixed_rows_split_into_the_two_packings(sizes):
     at = 2 * t + p * (2 + nb)
     assert (flat[2 * t:at].reshape(p, 2 + nb) == pf[:, 2 * w:]).all()
     assert (flat[at:].reshape(d, 2 + mb) == dc[:, 2:]).all()
+
+
+@pytest.mark.parametrize("seed,block_size", [(0, 16), (1, 4), (2, 1)])
+def test_prefill_rows_slot_columns_match_reference_loop(seed, block_size):
+    """The optional slot columns: padded position p of row i holds the pool slot of its token
+    (the reference's per-token slot, src/mini_infra/worker/paged_runner.py:123-128), -1 on left
+    padding and past the end of the table; the other columns are the plain packing's."""
+    rng = random.Random(seed)
+    rows = 4
+    lens = [rng.randint(1, 40) for _ in range(rows)]
+    starts = [rng.randint(0, 70) for _ in range(rows)]
+    tables, next_block = [], 1
+    for s, n in zip(starts, lens):
+        need = -(-(s + n) // block_size) - (1 if rng.random() < 0.3 and n > block_size else 0)  # some too short
+        tables.append(list(range(next_block, next_block + need)))
+        next_block += need + rng.randint(0, 3)
+    ids = [[rng.randint(5, 99) for _ in range(n)] for n in lens]
+    width, hist = 48, max(-(-s // block_size) for s in starts) + 2
+    plain = pack_prefill_rows(ids, starts, tables, block_size, 0, width=width, history_blocks=hist)
+    packed = pack_prefill_rows(ids, starts, tables, block_size, 0, width=width, history_blocks=hist, slots=True)
+    assert packed.shape == (rows, plain.shape[1] + width)
+    assert np.array_equal(packed[:, :plain.shape[1]], plain)
+    slots = packed[:, plain.shape[1]:]
+    for i, (s, n, table) in enumerate(zip(starts, lens, tables)):
+        for p in range(width):
+            t = p - (width - n)
+            logical = s + t
+            if t < 0 or logical // block_size >= len(table):
+                want = -1
+            else:
+                want = table[logical // block_size] * block_size + logical % block_size
+            assert slots[i, p] == want, (i, p)
