@@ -188,7 +188,9 @@ int32_t mi_paged_decode_attention_fused(void* out, int64_t out_row_stride, const
  * sequences cut between block ranges go to a fixed device array of the library,
  * MI_PAGED_NOALLOC_SCRATCH_BYTES bytes per GPU, held from the first call on a device until the
  * process ends.  A launch that needs more (mi_paged_decode_workspace_bytes above it; 4.3 MB at
- * 16 query / 8 KV heads on 256 CUs) returns MI_ERR_WORKSPACE before any device call.  The array
+ * 16 query / 8 KV heads on 256 CUs) returns MI_ERR_WORKSPACE before any launch, copy or scratch
+ * lookup; the size check itself only queries the current device and its CU count (hipGetDevice,
+ * and hipDeviceGetAttribute once per device).  The array
  * needs no clearing, but it is shared by every call on one GPU: calls that overlap on one GPU
  * (two streams, or two threads) race on it and must be serialised by the caller.
  */
@@ -305,7 +307,7 @@ int32_t mi_chunked_prefill_attention_exact(void* out, int64_t out_row_stride, in
  * (src/mini_infra/core/scheduler.py:310-311, src/mini_infra/core/types.py:108), over the same
  * rows the model's two paths would serve: chunk rows as mi_chunked_prefill_attention and decode
  * rows as mi_paged_decode_attention plus the K/V append of mi_reshape_and_cache's decode form
- * (reference qwen3.py:219-330, paged_kv_cache.py:97-114).
+ * (reference qwen3.py:219-330, the append at qwen3.py:282-283).
  *
  * A flattened token batch of T = P L + D rows, token-major ([T, H, 128] query, [T, H_kv, 128]
  * key / value with token and head strides; out [T, H * 128] with a token stride):

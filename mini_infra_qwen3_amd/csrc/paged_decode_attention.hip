@@ -1208,8 +1208,9 @@ extern "C" int32_t mi_paged_decode_attention_noalloc(void* out, int64_t out_row_
   if (const int32_t rc = check_heads("mi_paged_decode_attention_noalloc", num_heads, num_kv_heads, head_dim,
                                      block_size))
     return rc;
-  // The size check comes before any device call: a launch that needs more than the fixed array
-  // is rejected without touching the GPU.
+  // The size check comes before any launch, copy or scratch lookup (it only queries the current
+  // device and its CU count): a launch that needs more than the fixed array is rejected before
+  // any work reaches the GPU.
   const int64_t need =
       mi_paged_decode_workspace_bytes(batch, max_blocks, num_heads, num_kv_heads, head_dim, block_size);
   if (need > kScratchBytes)
