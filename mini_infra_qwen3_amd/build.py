@@ -40,6 +40,13 @@ HIPCC_FLAGS = [
     f"-I{REPO_DIR / 'include'}",
 ]
 
+# Per-source flags.  exact_attention.hip: the fp64 MFMA accumulators of its prefill kernel in
+# ordinary VGPRs (the compiler's default puts them in AGPRs, which at 256 threads per workgroup
+# pushes the kernel to one wavefront per SIMD; in VGPRs the cached form fits four).
+SOURCE_FLAGS = {
+    "exact_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+}
+
 
 def hipcc() -> str:
     for candidate in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -54,7 +61,7 @@ def sources(directory: Path = CSRC_DIR) -> list[Path]:
 
 def _compile(src: Path, build_dir: Path, extra: tuple[str, ...]) -> Path:
     obj = build_dir / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, ()), *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stdout}\n{proc.stderr}")

@@ -22,24 +22,23 @@
 // logit tie over a 151,936-token vocabulary is common, so any one-ulp difference anywhere in the
 // forward eventually flips a token).
 //
-// Cost: fp64 arithmetic instead of fp32 MFMA, and two passes over the keys (K for the scores,
-// then V for the output) with the scores held in LDS.  These kernels serve the model's forward,
-// where attention is latency-bound (small decode batches, prompts of a few hundred tokens); the
-// bandwidth kernels (paged_decode_attention.hip, chunked_prefill_attention.hip) keep fp32 online
-// softmax for large batches and long prompts.
+// Cost: fp64 arithmetic instead of bf16 / fp32, and two or three passes over the keys (scores and
+// their maximum, the denominators, then P V), the scores cached in LDS between them.  These kernels
+// serve the model's forward, where attention is latency-bound (small decode batches, prompts of a
+// few hundred tokens); the bandwidth kernels (paged_decode_attention.hip,
+// chunked_prefill_attention.hip) keep fp32 online softmax for large batches and long prompts.
 //
 // Decode (q_len 1): one workgroup of 8 wavefronts per (sequence, KV head) serves the G query
 // heads of the GQA group; wavefront w takes blocks w, w + 8, ...  Lane 16 r + d holds dims
 // [8 d, 8 d + 8) of tokens 4 i + r of a 16-token block (one 16-byte load per lane per i), the
 // layout of the bandwidth kernels.  The scores go to LDS as bf16 (exact: they are bf16 values),
 // are replaced by the probabilities once m and l are known, and are read back for P V.  A
-// context too long for the LDS cache recomputes the scores in each pass instead.
+// context too long for the LDS cache recomputes the scores in each pass instead.  Small batches
+// split each sequence's blocks over several workgroups (three launches, merged exactly).
 //
-// Prefill (chunked, with history from the pool): one workgroup of 4 wavefronts per (row, KV
-// head, tile of 32 / G query positions); its 32 (query, head) rows are split 8 per wavefront.
-// Key tiles of 64 keys (history first, then the causal chunk) are staged in LDS; a lane takes one
-// key of the tile against its wavefront's 8 rows for the scores, and two output dims of those rows
-// for P V.
+// Prefill (chunked, with history from the pool): the dot products and P V on the fp64 matrix
+// cores, one workgroup of 4 wavefronts per 16 (query, head) columns of a (row, KV head), the
+// wavefronts splitting the keys; the layout is described at the kernel.
 #include <algorithm>
 #include <math.h>
 #include <mutex>
@@ -786,15 +785,43 @@ __global__ __launch_bounds__(kHeadDim) void exact_split_merge_kernel(const Exact
 }
 
 // ----------------------------------------------------------------------- prefill ---
+// Chunked prefill (history from the pool, then the causal chunk) on the fp64 matrix cores
+// (v_mfma_f64_16x16x4f64: D[16][16] += A[16][4] B[4][16] in fp64).  Products of bf16 values are
+// exact in fp64 and the sums are exact, so the matrix cores give the same bits as any other order.
+//
+// A workgroup takes 16 (query, head) columns of one (row, KV head): 16 / G query positions times
+// the G query heads of the group (15 columns for G = 5).  Its 4 wavefronts split the 16-key tiles
+// of the keys (wavefront w: tiles w, w + 4, ...) and merge their maxima, sums and outputs through
+// LDS, so the heaviest query tile of a chunk is spread over four SIMDs.  Per 16-key tile a
+// wavefront runs
+//   S^T = K Q^T   32 MFMAs over the 128 dims: A = K, the tile's key rho(c) = 4 (c % 4) + c / 4 in
+//                 row c; B = Q^T; the k index of MFMA t is dim 32 (lane / 16) + t, so a lane reads
+//                 64 contiguous bytes of its key and query.  D row l / 16 + 4 r holds key
+//                 rho(l / 16 + 4 r) = 4 (l / 16) + r: lane l ends up with keys 4 (l / 16) .. + 3 of
+//                 column l % 16 in its four result registers.
+//   O += P V      32 MFMAs: A = P, lane l supplying column l % 16 and key 4 (l / 16) + u (its own
+//                 register u) in MFMA u; B = V, whose column j of output tile dt is dim 8 j + dt, so
+//                 a lane reads the 16 bytes of dims 8 (l % 16) .. + 7 of each of its four keys and
+//                 writes 16 contiguous output bytes per column.
+// The passes are those of the decode body: scores and their maxima (the bf16 scores cached in
+// LDS, 8 bytes per lane and tile, when the launch's longest row fits), the exact denominators,
+// then the probabilities and P V.  Rows too long for the cache recompute S in each pass.
+//
+// Measured on one MI355X (G = 2, 8 KV heads; TFLOP/s of QK + PV as 4 x 128 flops per visible
+// (query head, key) pair; fp64 MFMA alone peaks near 46 TFLOP/s in a loop of independent
+// accumulators): one 2048-token row 487 us (35.3 TFLOP/s), two 1024-token rows 248 us, four rows of
+// ~512 tokens 182 us, 1000 history + 1024 chunk tokens 386 us.  The fp64 FMA form this replaces
+// (one lane per key, query rows broadcast from LDS, one wavefront per SIMD) took 3106 / 934 / 499 /
+// 1845 us in the same runs.
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
-constexpr int kPfRows = 32;               // (query, head) rows of a workgroup: 8 per wavefront
-constexpr int kPfKeys = 64;               // keys per staged tile
-constexpr int kKvRow = kHeadDim + 8;      // LDS row of a staged K or V tile (elements): 272 bytes
-constexpr int kPfQBytes = kPfRows * kHeadDim * 8;
-constexpr int kPfTileBytes = kPfKeys * kKvRow * 2;
+constexpr int kPfCols = 16;                                    // (query, head) columns of a workgroup
+constexpr int kPfTileKeys = 16;                                // keys of one MFMA tile
+constexpr int kPfCacheTileBytes = 64 * 8;                      // one wavefront's scores of one tile
+constexpr int kPfRedBytes = kPfWaves * kPfCols * (4 + 16);     // per-wavefront maxima and hi / lo sums
+constexpr int kPfMergeBytes = 2 * 32 * 64 * 8;                 // two wavefronts' partial outputs
 constexpr int kPfLdsBytes = 160 * 1024;
-constexpr int kPfMaxCacheKeys = (kPfLdsBytes - kPfQBytes - kPfTileBytes) / (kPfRows * 2) / kPfKeys * kPfKeys;
+constexpr int kPfMaxCacheTiles = (kPfLdsBytes - kPfRedBytes) / (kPfWaves * kPfCacheTileBytes);  // per wavefront
 
 struct ExactPrefillArgs {
   uint16_t* out;
@@ -817,35 +844,57 @@ struct ExactPrefillArgs {
   int64_t lens_stride;
   int32_t padded_len;
   float scale;
-  int32_t cache_keys;      // keys the LDS cache holds (>= a row's keys: cached form; else kPfKeys, recompute)
+  int32_t cache_tiles;     // key tiles per wavefront the LDS score cache holds (cached form)
   int32_t tiles;           // query tiles per row
   int32_t batch;           // rows
   int32_t groups;          // workgroups of these rows: tiles x kv_heads x batch
 };
 
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f64x4 mfma_f64(double a, double b, f64x4 c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// Element e of eight bf16 values held as a 16-byte piece, as a double (exact).
+__device__ __forceinline__ double bf16_at(const u32x4 v, int e) {
+  const uint32_t x = v[e >> 1];
+  return (e & 1) ? bf16_hi(x) : bf16_lo(x);
+}
+
 // One launch serves a mixed step: the first a.groups workgroups take the chunk rows of a, the rest
 // (one per decode row and KV head of d) run the exact decode body with this kernel's wavefronts --
 // the sums are exact, so the bits do not depend on how the keys are split.
-template <int kG>
+template <int kG, bool kCached, bool kDecodeRows>
 __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPrefillArgs a, const ExactDecodeArgs d) {
-  constexpr int kQ = kPfRows / kG;        // query positions per workgroup
-  constexpr int kRows = kQ * kG;          // rows in use (<= 32)
+  constexpr int kQP = kPfCols / kG;  // query positions of a workgroup
+  constexpr int kCols = kQP * kG;    // columns in use (15 for G = 5)
   extern __shared__ __align__(16) unsigned char s_raw[];
-  double* sQ = reinterpret_cast<double*>(s_raw);                             // [32][128]
-  uint16_t* sT = reinterpret_cast<uint16_t*>(s_raw + kPfQBytes);             // [64][kKvRow]
-  uint16_t* sC = reinterpret_cast<uint16_t*>(s_raw + kPfQBytes + kPfTileBytes);  // [cache_keys][32]
 
-  if (static_cast<int>(blockIdx.x) >= a.groups) {  // uniform: a decode row
-    const int lin = static_cast<int>(blockIdx.x) - a.groups;
-    exact_decode_rows<kG, kPfWaves>(d, lin / d.kv_heads, lin % d.kv_heads, s_raw);
-    return;
+  // The decode rows' call is compiled only into the launches that have them: its registers would
+  // otherwise halve the occupancy of every chunk launch.
+  if constexpr (kDecodeRows) {
+    if (static_cast<int>(blockIdx.x) >= a.groups) {  // uniform: a decode row
+      const int lin = static_cast<int>(blockIdx.x) - a.groups;
+      exact_decode_rows<kG, kPfWaves>(d, lin / d.kv_heads, lin % d.kv_heads, s_raw);
+      return;
+    }
   }
+  float* sM = reinterpret_cast<float*>(s_raw);                                    // [waves][16]
+  double* sL = reinterpret_cast<double*>(s_raw + kPfWaves * kPfCols * 4);          // [waves][16][hi, lo]
+  uint2* sC = reinterpret_cast<uint2*>(s_raw + kPfRedBytes);                      // [waves][cache_tiles][64]
+  double* sO = reinterpret_cast<double*>(s_raw + kPfRedBytes);                    // [2][32][64], after the cache
+
+  // Workgroup order: query tiles from the last (most keys) to the first across every row and KV
+  // head, the KV head fastest, so consecutive workgroups (round-robin over the XCDs) keep one KV
+  // head's keys on one XCD when there are 8 KV heads.
   const int lin = static_cast<int>(blockIdx.x);
-  const int qt = lin % a.tiles;
-  const int g = (lin / a.tiles) % a.kv_heads;
-  const int b = lin / (a.tiles * a.kv_heads);
+  const int g = lin % a.kv_heads;
+  const int b = (lin / a.kv_heads) % a.batch;
+  const int qt = a.tiles - 1 - lin / (a.kv_heads * a.batch);
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  const int q4 = lane >> 4, c = lane & 15;
   const int L = a.padded_len;
   int64_t clen = a.chunk_lens[b * a.lens_stride];
   int64_t nh64 = a.start_lens[b * a.lens_stride];
@@ -853,257 +902,183 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   const int pad = L - static_cast<int>(clen);
   nh64 = nh64 < 0 ? 0 : min(nh64, static_cast<int64_t>(a.max_hist_blocks) * kBlockSize);
   const int nh = static_cast<int>(nh64);
-  const int i0 = qt * kQ;
-  const int i_last = min(i0 + kQ - 1, L - 1);
-  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
+  const int i0 = qt * kQP;
+  const int i_last = min(i0 + kQP - 1, L - 1);
 
-  // Row rho = qi * kG + j of this workgroup: query position i0 + qi, query head g kG + j.  Wavefront
-  // w owns rows 8 w .. 8 w + 7.  Key kk (history slots first, then chunk positions pad, pad + 1, ...)
-  // is visible to a row iff kk <= kmax (= nh + i - pad; -1 for padding rows and rows past L).
-  int kmax[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int rho = 8 * w + k;
-    const int i = i0 + rho / kG;
-    kmax[k] = (rho < kRows && i < L && i >= pad) ? nh + i - pad : -1;
-  }
   if (i_last < pad) {  // every query of the tile is padding: zero rows (uniform)
-    for (int idx = threadIdx.x; idx < kQ * kG * 16; idx += kPfThreads) {
-      const int qi = idx / (kG * 16), rest = idx - qi * kG * 16;
-      const int i = i0 + qi;
-      if (i < L)
-        *reinterpret_cast<uint4*>(a.out + b * a.out_row + i * a.out_tok + (g * kG) * kHeadDim + 8 * rest) =
-            uint4{0, 0, 0, 0};
-    }
+    const int col = threadIdx.x >> 4, piece = threadIdx.x & 15;
+    const int i = i0 + col / kG;
+    if (col < kCols && i < L)
+      *reinterpret_cast<uint4*>(a.out + b * a.out_row + i * a.out_tok + (g * kG + col % kG) * kHeadDim + 8 * piece) =
+          uint4{0, 0, 0, 0};
     return;
   }
-  const int nkeys = nh + i_last - pad + 1;  // keys any row of the tile sees
-  const bool cached = nkeys <= a.cache_keys;  // uniform
-  const int ntiles = (nkeys + kPfKeys - 1) / kPfKeys;
+  const int nkeys = nh + i_last - pad + 1;  // keys any column of the tile sees
+  const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
+  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
 
-  // queries of the tile as doubles (padding rows and rows past L hold zeros; they are masked)
-  for (int idx = threadIdx.x; idx < kPfRows * kHeadDim; idx += kPfThreads) {
-    const int rho = idx / kHeadDim, d = idx - rho * kHeadDim;
-    const int i = i0 + rho / kG;
-    double x = 0.0;
-    if (rho < kRows && i < L)
-      x = bf16_bits_to_f32(a.q[b * a.q_row + (g * kG + rho % kG) * a.q_head + i * a.q_tok + d]);
-    sQ[rho * kHeadDim + d] = x;
+  // This lane's column: query position i0 + c / G, query head g G + c % G.  Key kk (history slots
+  // first, then chunk positions pad, pad + 1, ...) is visible to it iff kk <= kmax.
+  const int ci = i0 + c / kG;
+  const int kmax = (c < kCols && ci < L && ci >= pad) ? nh + ci - pad : -1;
+
+  // Q^T operand: dims 32 q4 .. + 31 of column c, as doubles (zeros for unused columns).
+  double qd[32];
+  {
+    const bool live = c < kCols && ci < L;
+    const int cq = min(ci, L - 1);  // unused columns read a real row and keep zeros
+    const uint16_t* qrow = a.q + b * a.q_row + (g * kG + c % kG) * a.q_head + static_cast<int64_t>(cq) * a.q_tok + 32 * q4;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) qd[t] = live ? static_cast<double>(bf16_bits_to_f32(qrow[t])) : 0.0;
   }
 
-  // Stages K (or V) of keys [64 kt, 64 kt + 64) into sT: thread (key tid / 4, quarter tid % 4)
-  // copies four 16-byte pieces.  Keys past nkeys are zero-filled.
-  auto stage = [&](bool values, int kt) {
-    const int key = threadIdx.x >> 2, quarter = threadIdx.x & 3;
-    const int kk = kt * kPfKeys + key;
-    const uint16_t* src = nullptr;
-    if (kk < nh) {
-      int64_t id = a.history[b * a.hist_stride + kk / kBlockSize];
+  // Row of key kk (clamped to the last key any column sees; such keys are masked or zeroed).
+  auto key_row = [&](int kk, bool values) -> const uint16_t* {
+    const int kc = min(kk, nkeys - 1);
+    if (kc < nh) {
+      int64_t id = a.history[b * a.hist_stride + kc / kBlockSize];
       if (id < 0 || id >= a.num_blocks) id = 0;
-      src = (values ? a.value_pool : a.key_pool) + (id * kBlockSize + kk % kBlockSize) * row_elems + g * kHeadDim;
-    } else if (kk < nkeys) {
-      const int p = pad + (kk - nh);
-      src = values ? a.v + b * a.v_row + g * a.v_head + p * a.v_tok : a.k + b * a.k_row + g * a.k_head + p * a.k_tok;
+      return (values ? a.value_pool : a.key_pool) + (id * kBlockSize + kc % kBlockSize) * row_elems + g * kHeadDim;
     }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int piece = quarter * 4 + c;
-      u32x4 x = {0u, 0u, 0u, 0u};
-      if (src) x = *reinterpret_cast<const u32x4*>(src + 8 * piece);
-      *reinterpret_cast<u32x4*>(sT + key * kKvRow + 8 * piece) = x;
-    }
+    const int p = pad + (kc - nh);
+    return values ? a.v + b * a.v_row + g * a.v_head + static_cast<int64_t>(p) * a.v_tok
+                  : a.k + b * a.k_row + g * a.k_head + static_cast<int64_t>(p) * a.k_tok;
   };
-  // Scores of key lane of the staged tile against the wavefront's 8 rows.
-  // Rows of this wavefront with visible keys.  All of them except in edge tiles (padding rows,
-  // rows past L, the spare query slots of a decode row's tile), where the arithmetic of the dead
-  // rows is skipped (uniform branches; a dead row's results are never used).
-  bool all_live = true, any_live = false;
+  // Scores of keys 16 kt + 4 q4 + r (r = 0..3) against column c.
+  auto tile_scores = [&](int kt, float (&sc)[4]) {
+    const u32x4* krow = reinterpret_cast<const u32x4*>(key_row(kPfTileKeys * kt + 4 * (c & 3) + (c >> 2), false) + 32 * q4);
+    u32x4 kr[4];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    all_live = all_live && kmax[k] >= 0;
-    any_live = any_live || kmax[k] >= 0;
-  }
-  auto tile_scores = [&](float (&s)[8]) {
-    double acc[8];
+    for (int x = 0; x < 4; ++x) kr[x] = krow[x];
+    f64x4 s0 = {0.0, 0.0, 0.0, 0.0}, s1 = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-    for (int k = 0; k < 8; ++k) acc[k] = 0.0;
-    if (all_live) {
-      for (int c = 0; c < kHeadDim / 8; ++c) {
-        double kd[8];
-        unpack8(*reinterpret_cast<const u32x4*>(sT + lane * kKvRow + 8 * c), kd);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const double* qr = sQ + (8 * w + k) * kHeadDim + 8 * c;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[k] = fma(qr[e], kd[e], acc[k]);
-        }
-      }
-    } else if (any_live) {
-      for (int c = 0; c < kHeadDim / 8; ++c) {
-        double kd[8];
-        unpack8(*reinterpret_cast<const u32x4*>(sT + lane * kKvRow + 8 * c), kd);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          if (kmax[k] < 0) continue;
-          const double* qr = sQ + (8 * w + k) * kHeadDim + 8 * c;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[k] = fma(qr[e], kd[e], acc[k]);
-        }
-      }
+    for (int t = 0; t < 32; t += 2) {
+      s0 = mfma_f64(bf16_at(kr[t >> 3], t & 7), qd[t], s0);
+      s1 = mfma_f64(bf16_at(kr[(t + 1) >> 3], (t + 1) & 7), qd[t + 1], s1);
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) s[k] = exact_score(acc[k], a.scale);
+    for (int r = 0; r < 4; ++r) sc[r] = exact_score(s0[r] + s1[r], a.scale);  // both halves exact
   };
-  auto wave_fence = [] {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  };
-
-  // ---- pass 1: scores and their row maxima (and the cache: sC[kk][rho], bf16)
-  float mloc[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) mloc[k] = -INFINITY;
-  for (int kt = 0; kt < ntiles; ++kt) {
-    __syncthreads();  // sT is free (and sQ written, on the first tile)
-    stage(false, kt);
-    __syncthreads();
-    float s[8];
-    tile_scores(s);
-    const int kk = kt * kPfKeys + lane;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (kk <= kmax[k]) mloc[k] = fmaxf(mloc[k], s[k]);
-    }
-    if (cached && kk < nkeys) {
-      uint4 packed;
-      packed.x = static_cast<uint32_t>(bf16_bits(s[0])) | (static_cast<uint32_t>(bf16_bits(s[1])) << 16);
-      packed.y = static_cast<uint32_t>(bf16_bits(s[2])) | (static_cast<uint32_t>(bf16_bits(s[3])) << 16);
-      packed.z = static_cast<uint32_t>(bf16_bits(s[4])) | (static_cast<uint32_t>(bf16_bits(s[5])) << 16);
-      packed.w = static_cast<uint32_t>(bf16_bits(s[6])) | (static_cast<uint32_t>(bf16_bits(s[7])) << 16);
-      *reinterpret_cast<uint4*>(sC + kk * kPfRows + 8 * w) = packed;
-    }
-  }
-  float M[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) M[k] = wave_max(mloc[k]);
-
-  // ---- pass 2: denominators (a lane sums its keys kk = lane + 64 t; the wavefront reduces)
-  double hi[8], lo[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) hi[k] = lo[k] = 0.0;
-  if (cached) {
-    for (int kk = lane; kk < nkeys; kk += kPfKeys) {
-      const uint4 packed = *reinterpret_cast<const uint4*>(sC + kk * kPfRows + 8 * w);
-      const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float s = (k & 1) ? bf16_hi(words[k >> 1]) : bf16_lo(words[k >> 1]);
-        if (kk <= kmax[k]) split_add(exact_exp(s, M[k]), hi[k], lo[k]);
-      }
-    }
-  } else {
-    for (int kt = 0; kt < ntiles; ++kt) {
-      __syncthreads();
-      stage(false, kt);
-      __syncthreads();
-      float s[8];
-      tile_scores(s);
-      const int kk = kt * kPfKeys + lane;
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (kk <= kmax[k]) split_add(exact_exp(s[k], M[k]), hi[k], lo[k]);
-    }
-  }
-  float Lsum[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) Lsum[k] = static_cast<float>(wave_sum_f64(hi[k]) + wave_sum_f64(lo[k]));
-  if (cached) {  // scores -> probabilities in place (this wavefront's rows, its own lanes' keys)
-    for (int kk = lane; kk < nkeys; kk += kPfKeys) {
-      uint4* cell = reinterpret_cast<uint4*>(sC + kk * kPfRows + 8 * w);
-      const uint4 packed = *cell;
-      const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
-      uint32_t outw[4];
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const float s0 = bf16_lo(words[h]), s1 = bf16_hi(words[h]);
-        const float p0 = kk <= kmax[2 * h] ? exact_prob(exact_exp(s0, M[2 * h]), Lsum[2 * h]) : 0.0f;
-        const float p1 = kk <= kmax[2 * h + 1] ? exact_prob(exact_exp(s1, M[2 * h + 1]), Lsum[2 * h + 1]) : 0.0f;
-        outw[h] = static_cast<uint32_t>(bf16_bits(p0)) | (static_cast<uint32_t>(bf16_bits(p1)) << 16);
-      }
-      *cell = uint4{outw[0], outw[1], outw[2], outw[3]};
-    }
-  }
-
-  // ---- pass 3: P V (lane: dims 2 lane, 2 lane + 1 of the wavefront's 8 rows)
-  double acc[8][2];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) acc[k][0] = acc[k][1] = 0.0;
-  for (int kt = 0; kt < ntiles; ++kt) {
-    const uint16_t* probs;  // [64][32] bf16 probabilities of this tile's keys
-    if (cached) {
-      probs = sC + kt * kPfKeys * kPfRows;
+  auto cache_slot = [&](int lt) -> uint2* { return sC + (static_cast<int64_t>(w) * a.cache_tiles + lt) * 64 + lane; };
+  auto tile_scores_any = [&](int kt, int lt, float (&sc)[4]) {
+    if constexpr (kCached) {
+      const uint2 x = *cache_slot(lt);
+      sc[0] = bf16_lo(x.x);
+      sc[1] = bf16_hi(x.x);
+      sc[2] = bf16_lo(x.y);
+      sc[3] = bf16_hi(x.y);
     } else {
-      __syncthreads();
-      stage(false, kt);
-      __syncthreads();
-      float s[8];
-      tile_scores(s);
-      const int kk = kt * kPfKeys + lane;
-      uint32_t outw[4];
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const float p0 = kk <= kmax[2 * h] ? exact_prob(exact_exp(s[2 * h], M[2 * h]), Lsum[2 * h]) : 0.0f;
-        const float p1 = kk <= kmax[2 * h + 1] ? exact_prob(exact_exp(s[2 * h + 1], M[2 * h + 1]), Lsum[2 * h + 1]) : 0.0f;
-        outw[h] = static_cast<uint32_t>(bf16_bits(p0)) | (static_cast<uint32_t>(bf16_bits(p1)) << 16);
-      }
-      *reinterpret_cast<uint4*>(sC + lane * kPfRows + 8 * w) = uint4{outw[0], outw[1], outw[2], outw[3]};
-      probs = sC;
+      tile_scores(kt, sc);
     }
-    wave_fence();     // this wavefront's probability stores before its reads of other lanes' keys
-    __syncthreads();  // every wavefront is done with sT
-    stage(true, kt);
-    __syncthreads();
-    const int kend = min(kPfKeys, nkeys - kt * kPfKeys);
-    if (all_live) {
-      for (int key = 0; key < kend; ++key) {
-        const uint4 packed = *reinterpret_cast<const uint4*>(probs + key * kPfRows + 8 * w);
-        const uint32_t pv = *reinterpret_cast<const uint32_t*>(sT + key * kKvRow + 2 * lane);
-        const double v0 = bf16_lo(pv), v1 = bf16_hi(pv);
-        const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
+  };
+
+  // ---- pass 1: scores and the column maxima
+  float mloc = -INFINITY;
+  for (int kt = w, lt = 0; kt < ntiles; kt += kPfWaves, ++lt) {
+    float sc[4];
+    tile_scores(kt, sc);
+    const int kb = kPfTileKeys * kt + 4 * q4;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const double p = (k & 1) ? bf16_hi(words[k >> 1]) : bf16_lo(words[k >> 1]);
-          acc[k][0] = fma(p, v0, acc[k][0]);
-          acc[k][1] = fma(p, v1, acc[k][1]);
-        }
-      }
-    } else if (any_live) {
-      for (int key = 0; key < kend; ++key) {
-        const uint4 packed = *reinterpret_cast<const uint4*>(probs + key * kPfRows + 8 * w);
-        const uint32_t pv = *reinterpret_cast<const uint32_t*>(sT + key * kKvRow + 2 * lane);
-        const double v0 = bf16_lo(pv), v1 = bf16_hi(pv);
-        const uint32_t words[4] = {packed.x, packed.y, packed.z, packed.w};
+    for (int r = 0; r < 4; ++r)
+      if (kb + r <= kmax) mloc = fmaxf(mloc, sc[r]);
+    if constexpr (kCached)
+      *cache_slot(lt) = uint2{static_cast<uint32_t>(bf16_bits(sc[0])) | (static_cast<uint32_t>(bf16_bits(sc[1])) << 16),
+                              static_cast<uint32_t>(bf16_bits(sc[2])) | (static_cast<uint32_t>(bf16_bits(sc[3])) << 16)};
+  }
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  if (q4 == 0) sM[w * kPfCols + c] = mloc;
+  __syncthreads();
+  float M = sM[c];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          if (kmax[k] < 0) continue;
-          const double p = (k & 1) ? bf16_hi(words[k >> 1]) : bf16_lo(words[k >> 1]);
-          acc[k][0] = fma(p, v0, acc[k][0]);
-          acc[k][1] = fma(p, v1, acc[k][1]);
-        }
-      }
+  for (int x = 1; x < kPfWaves; ++x) M = fmaxf(M, sM[x * kPfCols + c]);
+
+  // ---- pass 2: denominators
+  double hi = 0.0, lo = 0.0;
+  for (int kt = w, lt = 0; kt < ntiles; kt += kPfWaves, ++lt) {
+    float sc[4];
+    tile_scores_any(kt, lt, sc);
+    const int kb = kPfTileKeys * kt + 4 * q4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (kb + r <= kmax) split_add(exact_exp(sc[r], M), hi, lo);
+  }
+  hi += __shfl_xor(hi, 16, 64);
+  lo += __shfl_xor(lo, 16, 64);
+  hi += __shfl_xor(hi, 32, 64);
+  lo += __shfl_xor(lo, 32, 64);
+  if (q4 == 0) {
+    sL[(w * kPfCols + c) * 2] = hi;
+    sL[(w * kPfCols + c) * 2 + 1] = lo;
+  }
+  __syncthreads();
+  double hsum = 0.0, lsum = 0.0;
+#pragma unroll
+  for (int x = 0; x < kPfWaves; ++x) {
+    hsum += sL[(x * kPfCols + c) * 2];
+    lsum += sL[(x * kPfCols + c) * 2 + 1];
+  }
+  const float Lc = static_cast<float>(hsum + lsum);
+
+  // ---- pass 3: probabilities and P V
+  f64x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f64x4{0.0, 0.0, 0.0, 0.0};
+  for (int kt = w, lt = 0; kt < ntiles; kt += kPfWaves, ++lt) {
+    const int kb = kPfTileKeys * kt + 4 * q4;
+    u32x4 vr[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      vr[u] = *reinterpret_cast<const u32x4*>(key_row(kb + u, true) + 8 * c);
+      if (kb + u >= nkeys) vr[u] = u32x4{0u, 0u, 0u, 0u};
+    }
+    float sc[4];
+    tile_scores_any(kt, lt, sc);
+    double p[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      p[u] = kb + u <= kmax ? static_cast<double>(exact_prob(exact_exp(sc[u], M), Lc)) : 0.0;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o[dt] = mfma_f64(p[u], bf16_at(vr[u], dt), o[dt]);
     }
   }
+
+  // ---- merge the four wavefronts' partial outputs: (O0 + O2) + (O1 + O3)
+  __syncthreads();  // the cache, which the merge area overlays, is no longer read
+  if (w >= 2) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int rho = 8 * w + k;
-    const int i = i0 + rho / kG;
-    if (rho >= kRows || i >= L) continue;
-    uint16_t* dst = a.out + b * a.out_row + i * a.out_tok + (g * kG + rho % kG) * kHeadDim + 2 * lane;
-    const uint32_t word = kmax[k] < 0 ? 0u
-                                      : (static_cast<uint32_t>(bf16_bits(static_cast<float>(acc[k][0]))) |
-                                         (static_cast<uint32_t>(bf16_bits(static_cast<float>(acc[k][1]))) << 16));
-    *reinterpret_cast<uint32_t*>(dst) = word;
+    for (int e = 0; e < 32; ++e) sO[((w - 2) * 32 + e) * 64 + lane] = o[e >> 2][e & 3];
+  }
+  __syncthreads();
+  if (w < 2) {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) o[e >> 2][e & 3] += sO[(w * 32 + e) * 64 + lane];
+  }
+  __syncthreads();
+  if (w == 1) {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) sO[e * 64 + lane] = o[e >> 2][e & 3];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int col = q4 + 4 * r;
+    const int i = i0 + col / kG;
+    if (col >= kCols || i >= L) continue;
+    uint32_t word[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const double x0 = o[2 * h][r] + sO[((2 * h) * 4 + r) * 64 + lane];
+      const double x1 = o[2 * h + 1][r] + sO[((2 * h + 1) * 4 + r) * 64 + lane];
+      word[h] = i < pad ? 0u
+                        : static_cast<uint32_t>(bf16_bits(static_cast<float>(x0))) |
+                              (static_cast<uint32_t>(bf16_bits(static_cast<float>(x1))) << 16);
+    }
+    *reinterpret_cast<uint4*>(a.out + b * a.out_row + static_cast<int64_t>(i) * a.out_tok +
+                              (g * kG + col % kG) * kHeadDim + 8 * c) = uint4{word[0], word[1], word[2], word[3]};
   }
 }
 
@@ -1201,12 +1176,14 @@ int32_t dispatch_exact_decode(const ExactDecodeArgs& a, int32_t batch, int group
   }
 }
 
-template <int kG>
+template <int kG, bool kCached, bool kDecodeRows>
 int32_t launch_exact_prefill(const ExactPrefillArgs& a, const ExactDecodeArgs& d, int32_t decode_rows, const char* what,
                              hipStream_t s) {
   static std::once_flag once;
   static int32_t attr_rc = MI_OK;
-  std::call_once(once, [] { attr_rc = allow_lds(exact_prefill_kernel<kG>, kPfLdsBytes, "exact_prefill_kernel"); });
+  std::call_once(once, [] {
+    attr_rc = allow_lds(exact_prefill_kernel<kG, kCached, kDecodeRows>, kPfLdsBytes, "exact_prefill_kernel");
+  });
   if (attr_rc != MI_OK) return attr_rc;
   const int64_t decode_groups = static_cast<int64_t>(decode_rows) * (decode_rows > 0 ? d.kv_heads : 0);
   if (a.groups < 0 || static_cast<int64_t>(a.groups) + decode_groups > 0x3fffffff)
@@ -1214,26 +1191,40 @@ int32_t launch_exact_prefill(const ExactPrefillArgs& a, const ExactDecodeArgs& d
   const int groups = a.groups + static_cast<int>(decode_groups);
   if (groups == 0) return ok();
   size_t lds = 0;
-  if (a.groups > 0) lds = static_cast<size_t>(kPfQBytes) + kPfTileBytes + static_cast<size_t>(a.cache_keys) * kPfRows * 2;
+  if (a.groups > 0)
+    lds = static_cast<size_t>(kPfRedBytes) +
+          std::max(static_cast<size_t>(kPfMergeBytes),
+                   kCached ? static_cast<size_t>(a.cache_tiles) * kPfWaves * kPfCacheTileBytes : size_t{0});
   if (decode_groups > 0)
     lds = std::max(lds, static_cast<size_t>(DecodeLds<kG, kPfWaves>::kFixed) +
                             static_cast<size_t>(d.cache_tokens) * kG * sizeof(uint16_t));
-  exact_prefill_kernel<kG><<<groups, kPfThreads, lds, s>>>(a, d);
+  exact_prefill_kernel<kG, kCached, kDecodeRows><<<groups, kPfThreads, lds, s>>>(a, d);
   return check_launch(what);
+}
+
+template <int kG>
+int32_t launch_exact_prefill_form(const ExactPrefillArgs& a, const ExactDecodeArgs& d, int32_t decode_rows,
+                                  const char* what, hipStream_t s) {
+  if (decode_rows > 0)
+    return a.cache_tiles > 0 ? launch_exact_prefill<kG, true, true>(a, d, decode_rows, what, s)
+                             : launch_exact_prefill<kG, false, true>(a, d, decode_rows, what, s);
+  return a.cache_tiles > 0 ? launch_exact_prefill<kG, true, false>(a, d, decode_rows, what, s)
+                           : launch_exact_prefill<kG, false, false>(a, d, decode_rows, what, s);
 }
 
 int32_t dispatch_exact_prefill(const ExactPrefillArgs& a, const ExactDecodeArgs& d, int32_t decode_rows, int group,
                                const char* what, hipStream_t s) {
   switch (group) {
-    case 1: return launch_exact_prefill<1>(a, d, decode_rows, what, s);
-    case 2: return launch_exact_prefill<2>(a, d, decode_rows, what, s);
-    case 4: return launch_exact_prefill<4>(a, d, decode_rows, what, s);
-    case 5: return launch_exact_prefill<5>(a, d, decode_rows, what, s);
-    default: return launch_exact_prefill<8>(a, d, decode_rows, what, s);
+    case 1: return launch_exact_prefill_form<1>(a, d, decode_rows, what, s);
+    case 2: return launch_exact_prefill_form<2>(a, d, decode_rows, what, s);
+    case 4: return launch_exact_prefill_form<4>(a, d, decode_rows, what, s);
+    case 5: return launch_exact_prefill_form<5>(a, d, decode_rows, what, s);
+    default: return launch_exact_prefill_form<8>(a, d, decode_rows, what, s);
   }
 }
 
-// Row-independent fields: grid shape and the LDS score cache for rows of up to `keys` keys.
+// Row-independent fields: grid shape and the LDS score cache for rows of up to `keys` keys (the
+// cached form when each wavefront's share of them fits, else the recomputing form).
 void exact_rows(ExactPrefillArgs& a, int32_t batch, int32_t padded_len, int32_t num_heads, int32_t num_kv_heads,
                 int64_t keys, float scale) {
   const int group = num_heads / num_kv_heads;
@@ -1241,12 +1232,13 @@ void exact_rows(ExactPrefillArgs& a, int32_t batch, int32_t padded_len, int32_t 
   a.padded_len = padded_len;
   a.kv_heads = num_kv_heads;
   a.scale = scale;
-  const int q_per_group = kPfRows / group;
+  const int q_per_group = kPfCols / group;
   a.tiles = (padded_len + q_per_group - 1) / q_per_group;
   const int64_t groups = static_cast<int64_t>(a.tiles) * num_kv_heads * batch;
   a.groups = groups > 0x3fffffff ? -1 : static_cast<int32_t>(groups);
-  const int64_t keys_up = (keys + kPfKeys - 1) / kPfKeys * kPfKeys;
-  a.cache_keys = keys_up <= kPfMaxCacheKeys ? static_cast<int32_t>(keys_up) : kPfKeys;
+  const int64_t key_tiles = (keys + kPfTileKeys - 1) / kPfTileKeys;
+  const int64_t per_wave = (key_tiles + kPfWaves - 1) / kPfWaves;
+  a.cache_tiles = per_wave <= kPfMaxCacheTiles ? static_cast<int32_t>(per_wave) : 0;
 }
 
 int32_t check_exact_heads(const char* what, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
