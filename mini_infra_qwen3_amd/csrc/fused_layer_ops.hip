@@ -160,6 +160,81 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(const QkArgs a) 
   }
 }
 
+// Vector form, for 16-byte aligned rows: 16 lanes per (token, head), lane j holding elements
+// [8 j, 8 j + 8) (16-byte loads and stores), a wavefront four heads of one token.  The sum of
+// squares is exact in fp64 in any order, so the 16-lane reduction gives the scalar form's bits;
+// rotate_half pairs lane j with lane j ^ 8.
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_vec_kernel(const QkArgs a) {
+  const int heads = a.q_heads + a.kv_heads;
+  const int quads = (heads + 3) / 4;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
+  if (wave >= a.tokens * quads) return;  // uniform per wavefront
+  const int lane = threadIdx.x % kWave;
+  const int j = lane & 15;
+  const int64_t t = wave / quads;
+  const int head_raw = static_cast<int>(wave % quads) * 4 + (lane >> 4);
+  const bool live = head_raw < heads;  // uniform per 16-lane group
+  const int head = live ? head_raw : heads - 1;
+  const bool is_q = head < a.q_heads;
+  const int h = is_q ? head : head - a.q_heads;
+  const uint16_t* src = (is_q ? a.q + t * a.q_stride : a.k + t * a.k_stride) + h * 128 + 8 * j;
+  const u32x4 x = *reinterpret_cast<const u32x4*>(src);
+  const u32x4 w = *reinterpret_cast<const u32x4*>((is_q ? a.q_weight : a.k_weight) + 8 * j);
+  const u32x4 cs = *reinterpret_cast<const u32x4*>(a.cos + t * 128 + 8 * j);
+  const u32x4 sn = *reinterpret_cast<const u32x4*>(a.sin + t * 128 + 8 * j);
+  float xf[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    xf[2 * e] = bf16_lo(x[e]);
+    xf[2 * e + 1] = bf16_hi(x[e]);
+  }
+  double sq = 0.0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sq += static_cast<double>(xf[e]) * xf[e];
+#pragma unroll
+  for (int m = 1; m <= 8; m <<= 1) sq += __shfl_xor(sq, m, 64);
+  const float r = rms_inv(sq, 128.0, a.eps);
+  float y[8];
+  u32x4 yb;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[2 * e] = round_bf16(bf16_lo(w[e]) * round_bf16(xf[2 * e] * r));
+    y[2 * e + 1] = round_bf16(bf16_hi(w[e]) * round_bf16(xf[2 * e + 1] * r));
+    yb[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
+  }
+  u32x4 pb;  // the rotate_half partner's normalised values (elements 64 apart)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) pb[e] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(yb[e]), 8, 64));
+  const float sign = j < 8 ? -1.0f : 1.0f;  // element e < 64: y cos - y[e + 64] sin; else y cos + y[e - 64] sin
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float o0 = round_bf16(round_bf16(y[2 * e] * bf16_lo(cs[e])) + round_bf16(sign * bf16_lo(pb[e]) * bf16_lo(sn[e])));
+    const float o1 =
+        round_bf16(round_bf16(y[2 * e + 1] * bf16_hi(cs[e])) + round_bf16(sign * bf16_hi(pb[e]) * bf16_hi(sn[e])));
+    o[e] = pack_bf16x2(o0, o1);
+  }
+  if (!live) return;
+  if (is_q) {
+    *reinterpret_cast<u32x4*>(a.q_out + (t * a.q_heads + h) * 128 + 8 * j) = o;
+    return;
+  }
+  int64_t slot = -1;
+  if (a.slot_mapping) {
+    slot = a.slot_mapping[t * a.slot_stride];
+    if (slot < 0 || slot >= a.num_slots) slot = -1;
+  }
+  const u32x4 v = *reinterpret_cast<const u32x4*>(a.v + t * a.v_stride + h * 128 + 8 * j);
+  if (a.k_out) {  // the token's rows
+    *reinterpret_cast<u32x4*>(a.k_out + (t * a.kv_heads + h) * 128 + 8 * j) = o;
+    *reinterpret_cast<u32x4*>(a.v_out + (t * a.kv_heads + h) * 128 + 8 * j) = v;
+  }
+  if (slot >= 0) {  // and / or its pool slot
+    *reinterpret_cast<u32x4*>(a.key_pool + (slot * a.kv_heads + h) * 128 + 8 * j) = o;
+    *reinterpret_cast<u32x4*>(a.value_pool + (slot * a.kv_heads + h) * 128 + 8 * j) = v;
+  }
+}
+
 // ------------------------------------------------------------------------------ SwiGLU
 struct SiluArgs {
   uint16_t* out;
@@ -246,10 +321,18 @@ extern "C" int32_t mi_qk_norm_rope(void* q_out, void* k_out, void* v_out, const 
            static_cast<const uint16_t*>(k_weight), static_cast<const uint16_t*>(cos),
            static_cast<const uint16_t*>(sin), slot_mapping, slot_stride, static_cast<uint16_t*>(key_pool),
            static_cast<uint16_t*>(value_pool), num_slots, num_tokens, num_heads, num_kv_heads, eps};
-  const int64_t units = num_tokens * (num_heads + num_kv_heads);
-  const int64_t groups = (units + kThreads / kWave - 1) / (kThreads / kWave);
+  // 16-byte rows everywhere: the vector form (four heads per wavefront); else one head per wavefront.
+  const bool vec = aligned16(q_out) && aligned16(q) && aligned16(k) && aligned16(v) && aligned(k_out) &&
+                   aligned(v_out) && aligned(key_pool) && aligned(value_pool) && aligned16(q_weight) &&
+                   aligned16(k_weight) && aligned16(cos) && aligned16(sin) && q_stride % 8 == 0 &&
+                   k_stride % 8 == 0 && v_stride % 8 == 0;
+  const int64_t per_token = vec ? (num_heads + num_kv_heads + 3) / 4 : num_heads + num_kv_heads;
+  const int64_t groups = (num_tokens * per_token + kThreads / kWave - 1) / (kThreads / kWave);
   if (groups > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "mi_qk_norm_rope: too many tokens");
-  qk_norm_rope_kernel<<<static_cast<uint32_t>(groups), kThreads, 0, as_stream(stream)>>>(a);
+  if (vec)
+    qk_norm_rope_vec_kernel<<<static_cast<uint32_t>(groups), kThreads, 0, as_stream(stream)>>>(a);
+  else
+    qk_norm_rope_kernel<<<static_cast<uint32_t>(groups), kThreads, 0, as_stream(stream)>>>(a);
   return check_launch("mi_qk_norm_rope");
 }
 

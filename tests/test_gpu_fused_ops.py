@@ -95,6 +95,29 @@ def test_qk_norm_rope_decode_form_appends_into_pool_slots():
     assert torch.equal(kflat[untouched], k0[untouched]) and torch.equal(vflat[untouched], v0[untouched])
 
 
+def test_qk_norm_rope_vector_and_scalar_forms_are_bit_identical():
+    """16-byte aligned rows take the vector form (16 lanes per head), others one head per
+    wavefront: the same bits, rows and pool slots alike (the sum of squares is exact in fp64)."""
+    T, H, G, nb, bs = 300, 16, 8, 24, 16
+    qk = randn(T, H * 128 + G * 128 + 1, seed=30)
+    q_odd, k_odd = qk[:, 1:H * 128 + 1], qk[:, H * 128 + 1:]   # 2-byte offset: the scalar form
+    v = randn(T, G * 128, seed=31)
+    qw, kw = randn(128, seed=32, scale=0.1) + 1, randn(128, seed=33, scale=0.1) + 1
+    cos, sin = randn(T, 128, seed=34), randn(T, 128, seed=35)
+    slots = torch.randperm(nb * bs, device=DEV)[:T]
+    slots[::7] = -1
+    outs = []
+    for q, k in ((q_odd, k_odd), (q_odd.contiguous(), k_odd.contiguous())):
+        kp, vp = torch.zeros(nb, bs, G, 128, dtype=torch.bfloat16, device=DEV), \
+            torch.zeros(nb, bs, G, 128, dtype=torch.bfloat16, device=DEV)
+        q_out, k_out, v_out = data_plane.qk_norm_rope(q, k, v, qw, kw, cos, sin, EPS, slot_mapping=slots,
+                                                      key_pool=kp, value_pool=vp, rows=True)
+        outs.append((q_out, k_out, v_out, kp, vp))
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(outs[1][2].view(T, -1), v)
+
+
 def test_silu_mul_and_strided_views():
     gu = randn(7, 3, 2 * 3072, seed=18, scale=3.0)
     gate, up = gu[..., :3072], gu[..., 3072:]
