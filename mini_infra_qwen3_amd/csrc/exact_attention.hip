@@ -84,16 +84,12 @@ __device__ __forceinline__ float exact_prob(float e, float l) {
 
 __device__ __forceinline__ uint16_t bf16_bits(float f) { return static_cast<uint16_t>(f32_to_bf16_bits(f)); }
 
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  return xmax32(xmax16(v));
 }
 
 // Eight bf16 values of a 16-byte piece as doubles (exact).
@@ -292,11 +288,7 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
         acc = fma(static_cast<double>(q1.y), kd[5], acc);
         acc = fma(static_cast<double>(q1.z), kd[6], acc);
         acc = fma(static_cast<double>(q1.w), kd[7], acc);
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        acc += __shfl_xor(acc, 4, 64);
-        acc += __shfl_xor(acc, 8, 64);
-        s[t][j] = exact_score(acc, scale);
+        s[t][j] = exact_score(dpp_sum16_f64(acc), scale);
       }
     }
   };
@@ -377,7 +369,7 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
   }
 #pragma unroll
   for (int j = 0; j < kG; ++j) {
-    const double h = wave_sum_f64(hi[j]), l = wave_sum_f64(lo[j]);
+    const double h = wave_sum64_f64(hi[j]), l = wave_sum64_f64(lo[j]);
     if (lane == 0) {
       s_l[w][j][0] = h;
       s_l[w][j][1] = l;
@@ -457,8 +449,7 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       double x = acc[j][e];
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
+      x = xsum32_f64(xsum16_f64(x));
       acc[j][e] = x;
     }
   }
@@ -616,10 +607,7 @@ __global__ __launch_bounds__(kSplitThreads) void exact_split_scores_kernel(const
           acc = fma(static_cast<double>(q1.y), kd[5], acc);
           acc = fma(static_cast<double>(q1.z), kd[6], acc);
           acc = fma(static_cast<double>(q1.w), kd[7], acc);
-          acc += __shfl_xor(acc, 1, 64);
-          acc += __shfl_xor(acc, 2, 64);
-          acc += __shfl_xor(acc, 4, 64);
-          acc += __shfl_xor(acc, 8, 64);
+          acc = dpp_sum16_f64(acc);
           if (dl == j && tok < rg.n) out_scores[tok * kG + j] = bf16_bits(exact_score(acc, a.scale));
         }
       }
@@ -691,7 +679,7 @@ __global__ __launch_bounds__(kSplitThreads) void exact_split_pv_kernel(const Exa
   }
 #pragma unroll
   for (int j = 0; j < kG; ++j) {
-    const double h = wave_sum_f64(hi[j]), l = wave_sum_f64(lo[j]);
+    const double h = wave_sum64_f64(hi[j]), l = wave_sum64_f64(lo[j]);
     if (lane == 0) {
       s_l[w][j][0] = h;
       s_l[w][j][1] = l;
@@ -742,8 +730,7 @@ __global__ __launch_bounds__(kSplitThreads) void exact_split_pv_kernel(const Exa
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       double x = acc[j][e];
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
+      x = xsum32_f64(xsum16_f64(x));
       acc[j][e] = x;
     }
   }
@@ -985,8 +972,7 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
       *cache_slot(lt) = uint2{static_cast<uint32_t>(bf16_bits(sc[0])) | (static_cast<uint32_t>(bf16_bits(sc[1])) << 16),
                               static_cast<uint32_t>(bf16_bits(sc[2])) | (static_cast<uint32_t>(bf16_bits(sc[3])) << 16)};
   }
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  mloc = xmax32(xmax16(mloc));
   if (q4 == 0) sM[w * kPfCols + c] = mloc;
   __syncthreads();
   float M = sM[c];
@@ -1003,10 +989,8 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
     for (int r = 0; r < 4; ++r)
       if (kb + r <= kmax) split_add(exact_exp(sc[r], M), hi, lo);
   }
-  hi += __shfl_xor(hi, 16, 64);
-  lo += __shfl_xor(lo, 16, 64);
-  hi += __shfl_xor(hi, 32, 64);
-  lo += __shfl_xor(lo, 32, 64);
+  hi = xsum32_f64(xsum16_f64(hi));
+  lo = xsum32_f64(xsum16_f64(lo));
   if (q4 == 0) {
     sL[(w * kPfCols + c) * 2] = hi;
     sL[(w * kPfCols + c) * 2 + 1] = lo;

@@ -112,6 +112,58 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
+// Cross-lane steps without LDS permutes: a 16-lane DPP butterfly within each row (xor 1, xor 2,
+// 8-lane mirror, 16-lane mirror; on the two halves of a double), then v_permlane16_swap /
+// v_permlane32_swap across rows (a swap returns the lane's own value and its partner's, so their
+// sum is x + x[lane ^ 16] or x + x[lane ^ 32] in every lane).  Every lane of the wavefront must be
+// active.  The sums met here are exact (or, for the remainders of the exact kernels' split sums,
+// far below what the roundings see), so the order gives the bits of any other.
+template <int kCtrl>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const uint64_t u = __double_as_longlong(x);
+  const uint32_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), kCtrl, 0xf, 0xf, false));
+  const uint32_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)), kCtrl, 0xf, 0xf, false));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
+}
+__device__ __forceinline__ double join_f64(uint32_t hi, uint32_t lo) {
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+__device__ __forceinline__ double dpp_sum16_f64(double x) {
+  x += dpp_f64<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_f64<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_f64<0x141>(x);  // row_half_mirror
+  x += dpp_f64<0x140>(x);  // row_mirror
+  return x;
+}
+__device__ __forceinline__ double xsum16_f64(double x) {  // x + x[lane ^ 16]
+  const uint64_t u = __double_as_longlong(x);
+  const auto lo = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(u), static_cast<uint32_t>(u), false, false);
+  const auto hi =
+      __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(u >> 32), static_cast<uint32_t>(u >> 32), false, false);
+  return join_f64(hi[0], lo[0]) + join_f64(hi[1], lo[1]);
+}
+__device__ __forceinline__ double xsum32_f64(double x) {  // x + x[lane ^ 32]
+  const uint64_t u = __double_as_longlong(x);
+  const auto lo = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(u), static_cast<uint32_t>(u), false, false);
+  const auto hi =
+      __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(u >> 32), static_cast<uint32_t>(u >> 32), false, false);
+  return join_f64(hi[0], lo[0]) + join_f64(hi[1], lo[1]);
+}
+__device__ __forceinline__ float xmax16(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xmax32(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
 // ------------------------------------------------------- RMSNorm, exact ---
 // The reference's RMSNorm (src/mini_infra/model/qwen3.py:67-78) is
 //   h = x.float(); y = w * (h * rsqrt(h.pow(2).mean(-1) + eps)).to(bf16)
@@ -122,11 +174,7 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as
 // (sqrt and division correctly rounded in fp64, then one rounding to fp32) -- a result that does
 // not depend on the reduction order or the device, which torch's on-device chain also gives
 // whenever its fp32 sum rounds the same way.
-__device__ __forceinline__ double wave_sum64_f64(double v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
+__device__ __forceinline__ double wave_sum64_f64(double v) { return xsum32_f64(xsum16_f64(dpp_sum16_f64(v))); }
 
 // r = fp32(1 / sqrt(fp32(fp32(sum_sq / n) + eps))), the division by n in fp64.
 __device__ __forceinline__ float rms_inv(double sum_sq, double n, float eps) {
