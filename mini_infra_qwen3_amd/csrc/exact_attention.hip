@@ -1118,9 +1118,9 @@ int32_t dispatch_exact_split(const ExactSplitArgs& sa, int32_t batch, int group,
 // two per CU, at most one per 4 table blocks (so the 4 wavefronts of a split have blocks to read)
 // and at most kMaxSplits; 1 = the single-kernel form.  Only launches of at most kMaxSplitPairs
 // (sequence, KV head) pairs split: measured on MI355X (28 layers in a HIP graph, contexts U[200,
-// 1150], GQA group 2), µs per layer single / split: batch 1 29.5 / 23.2, 4 35.9 / 25.9,
-// 9 32.6 / 35.8, 16 43.4 / 48.7, 32 44.9 / 72.9 -- three dependent launches cost more than
-// one launch's idle CUs once the batch gives a workgroup to a fifth of them.
+// 1150], GQA group 2), µs per layer single / split: batch 1 24.4 / 21.2, 4 30.4 / 24.5,
+// 9 27.8 / 33.6, 16 36.2 / 45.8, 24 36.5 / 59.6, 32 38.0 / 67.6 -- three dependent launches cost
+// more than one launch's idle CUs once the batch gives a workgroup to a fifth of them.
 constexpr int64_t kMaxSplitPairs = 48;
 int32_t exact_decode_splits(int32_t batch, int32_t max_blocks, int32_t num_kv_heads) {
   const int64_t pairs = static_cast<int64_t>(batch) * num_kv_heads;
