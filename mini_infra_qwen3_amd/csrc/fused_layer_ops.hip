@@ -160,10 +160,11 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(const QkArgs a) 
   }
 }
 
-// Vector form, for 16-byte aligned rows: 16 lanes per (token, head), lane j holding elements
-// [8 j, 8 j + 8) (16-byte loads and stores), a wavefront four heads of one token.  The sum of
-// squares is exact in fp64 in any order, so the 16-lane reduction gives the scalar form's bits;
-// rotate_half pairs lane j with lane j ^ 8.
+// Vector form, for 16-byte aligned rows: 16 lanes (one DPP row) per (token, head), lane j holding
+// elements [8 j, 8 j + 8) (16-byte loads and stores), a wavefront four heads of one token.  The sum
+// of squares is exact in fp64 in any order, so the 16-lane reduction gives the scalar form's bits;
+// rotate_half pairs lane j with lane j ^ 8 (a rotation of the row by 8).  Every lane of a wavefront
+// that starts runs the cross-lane steps.
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_vec_kernel(const QkArgs a) {
   const int heads = a.q_heads + a.kv_heads;
   const int quads = (heads + 3) / 4;
@@ -191,9 +192,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_vec_kernel(const QkArgs
   double sq = 0.0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) sq += static_cast<double>(xf[e]) * xf[e];
-#pragma unroll
-  for (int m = 1; m <= 8; m <<= 1) sq += __shfl_xor(sq, m, 64);
-  const float r = rms_inv(sq, 128.0, a.eps);
+  const float r = rms_inv(dpp_sum16_f64(sq), 128.0, a.eps);
   float y[8];
   u32x4 yb;
 #pragma unroll
@@ -202,9 +201,10 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_vec_kernel(const QkArgs
     y[2 * e + 1] = round_bf16(bf16_hi(w[e]) * round_bf16(xf[2 * e + 1] * r));
     yb[e] = pack_bf16x2(y[2 * e], y[2 * e + 1]);
   }
-  u32x4 pb;  // the rotate_half partner's normalised values (elements 64 apart)
+  u32x4 pb;  // the rotate_half partner's normalised values (elements 64 apart): DPP row_ror:8 = lane ^ 8
 #pragma unroll
-  for (int e = 0; e < 4; ++e) pb[e] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(yb[e]), 8, 64));
+  for (int e = 0; e < 4; ++e)
+    pb[e] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(yb[e]), 0x128, 0xf, 0xf, false));
   const float sign = j < 8 ? -1.0f : 1.0f;  // element e < 64: y cos - y[e + 64] sin; else y cos + y[e - 64] sin
   u32x4 o;
 #pragma unroll
