@@ -105,13 +105,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // process (8 x 20 launches each), the matrix-core form took 461.5 µs (median) against 463.3.
 constexpr int kMfmaGroup = MI_DECODE_MFMA_GROUP;
 #ifndef MI_DECODE_SEQ_MFMA_GROUP
-#define MI_DECODE_SEQ_MFMA_GROUP 4
+#define MI_DECODE_SEQ_MFMA_GROUP 2
 #endif
 // The per-sequence kernel (small launches: latency-bound) takes the matrix-core form from this
 // group size up.  At group 2 the matrix-core form measured faster (6.4 against 7.8 µs per layer at
-// batch 1, 9.5 against 11.6 at 6, 22.0 against 22.8 at 32; contexts U[32, 1150]), but models that
-// need those latencies run the reference-numerics kernel (exact_attention.hip), so group 2 keeps
-// the dot-product form here too.
+// batch 1, 9.5 against 11.6 at 6, 22.0 against 22.8 at 32; contexts U[32, 1150]); in the
+// bandwidth-kernel e2e runs of config 5 (two repetitions each, one machine) the decode step went
+// from 2.144-2.145 to 2.104-2.121 ms alternating and from 2.127-2.136 to 2.114-2.118 ms mixed.
 constexpr int kSeqMfmaGroup = MI_DECODE_SEQ_MFMA_GROUP;
 
 struct DecodeArgs {
