@@ -33,6 +33,7 @@ import torch
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor datasheet
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
+MFMA_FP64_PEAK_TFLOPS = 78.6    # MI355X dense fp64 matrix peak
 PCIE_PEAK_GBS = 64.0  # MI355X host link, PCIe 5.0 x16, one direction
 METRIC = "paged decode-attn HBM GB/s (% peak) at B=256; e2e output tok/s Qwen3-0.6B"
 
@@ -602,6 +603,45 @@ def bench_prefill(steps: int, warmup: int, device: torch.device, cpu: bool = Fal
     return out
 
 
+def bench_exact_prefill(steps: int, warmup: int, device: torch.device) -> dict:
+    """Reference-numerics chunked prefill attention (the model's default: exact sums, fp64 matrix
+    cores) on the heaviest chunk step the e2e workload makes: two 1024-token prompts (the longest it
+    draws) in one 2048-token budget, no history, 16 query / 8 KV heads, one layer."""
+    from mini_infra_qwen3_amd import data_plane, workloads as wl
+
+    rows, n = 2, 1024
+    gen = torch.Generator(device=device).manual_seed(4)
+    q = torch.randn((rows, wl.NUM_HEADS, n, wl.HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn((rows, wl.NUM_KV_HEADS, n, wl.HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn((rows, wl.NUM_KV_HEADS, n, wl.HEAD_DIM), generator=gen, device=device).to(torch.bfloat16)
+    pools = torch.zeros((2, 1, wl.BLOCK_SIZE, wl.NUM_KV_HEADS, wl.HEAD_DIM), dtype=torch.bfloat16, device=device)
+    hist = torch.zeros((rows, 0), dtype=torch.long, device=device)
+    starts = torch.zeros((rows,), dtype=torch.long, device=device)
+    lens = torch.full((rows,), n, dtype=torch.long, device=device)
+    out = torch.empty((rows, n, wl.NUM_HEADS * wl.HEAD_DIM), dtype=torch.bfloat16, device=device)
+
+    def layer():
+        data_plane.chunked_prefill_attention(q, k, v, pools[0], pools[1], hist, starts, lens, wl.SCALE, out=out,
+                                             exact=True)
+
+    timer = EventTimer()
+    for _ in range(warmup):
+        layer()
+    for _ in range(steps):
+        timer.start()
+        layer()
+        timer.stop()
+    ms = timer.mean_ms()
+    flops = rows * 2 * 2 * wl.NUM_HEADS * wl.HEAD_DIM * n * (n + 1) / 2  # QK^T and PV, causal pairs
+    tflops = flops / (ms * 1e-3) / 1e12
+    del q, k, v, pools, out
+    torch.cuda.empty_cache()
+    return {"workload": "reference-numerics chunked prefill attention (exact sums, fp64 matrix cores), 2 prompts x "
+                        "1024 tokens in one chunk, no history, one layer",
+            "ms_per_layer": ms, "tflop_per_layer": flops / 1e12, "achieved_TFLOPs": tflops,
+            "peak_TFLOPs": MFMA_FP64_PEAK_TFLOPS, "frac": tflops / MFMA_FP64_PEAK_TFLOPS, "dtype": "f64"}
+
+
 # ------------------------------------------------------------------------ e2e continuous batching
 def cpu_baseline_e2e(seed: int = 0, num_requests: int = 8, max_new_tokens: int = 64) -> dict:
     """The oracle's restatement of the reference schedule backend (the reference's torch model,
@@ -804,7 +844,7 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "scatter-sequential", "scatter-head",
-                                           "gather", "gather-sequential", "prefill",
+                                           "gather", "gather-sequential", "prefill", "exact-prefill",
                                            "copy", "swap", "e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth",
                                            "e2e-agreement", "all"],
                         default="all")
@@ -830,6 +870,7 @@ def main() -> int:
         "gather": lambda: bench_gather(args.steps, args.warmup, device),
         "gather-sequential": lambda: bench_gather(args.steps, args.warmup, device, tables="near_sequential"),
         "prefill": lambda: bench_prefill(args.steps, args.warmup, device),
+        "exact-prefill": lambda: bench_exact_prefill(args.steps, args.warmup, device),
         "swap": lambda: bench_swap(args.steps, args.warmup, device),
         "decode-groups": lambda: bench_decode_groups(args.steps, args.warmup, device),
     }
@@ -901,6 +942,9 @@ def main() -> int:
         kernels["chunked_prefill"] = bench_prefill(max(args.steps // 2, 5), 20, device, cpu=want_cpu)
         log(f"chunked prefill: {kernels['chunked_prefill']['ms_per_layer']:.2f} ms/layer, "
             f"{kernels['chunked_prefill']['achieved_TFLOPs']:.1f} TFLOP/s")
+        kernels["exact_prefill"] = bench_exact_prefill(max(args.steps // 2, 5), 3, device)
+        log(f"exact prefill: {kernels['exact_prefill']['ms_per_layer'] * 1000:.0f} us/layer, "
+            f"{kernels['exact_prefill']['achieved_TFLOPs']:.1f} TFLOP/s fp64")
         torch.cuda.empty_cache()
         kernels["kv_block_swap"] = bench_swap(max(args.steps // 4, 3), 1, device)
         sw = kernels["kv_block_swap"]

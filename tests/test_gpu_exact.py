@@ -183,6 +183,7 @@ def prefill_case(seed, starts, lens, kv_heads, group):
     (5, [30, 0], [100, 77], 5, 8),
     (6, [200], [90], 8, 2),
     (7, [70], [33], 1, 4),
+    (9, [40, 0], [300, 45], 4, 8),          # Qwen3-4B / 8B's group: 4 query positions per workgroup
     (8, [5000], [700], 2, 8),               # 5.7k keys: past the LDS score cache, recomputed per pass
 ])
 def test_exact_prefill_is_bit_identical_to_the_oracle(device, seed, starts, lens, group, kv_heads):
