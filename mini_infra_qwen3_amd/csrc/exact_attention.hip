@@ -796,10 +796,11 @@ __global__ __launch_bounds__(kHeadDim) void exact_split_merge_kernel(const Exact
 //
 // Measured on one MI355X (G = 2, 8 KV heads; TFLOP/s of QK + PV as 4 x 128 flops per visible
 // (query head, key) pair; fp64 MFMA alone peaks near 46 TFLOP/s in a loop of independent
-// accumulators): one 2048-token row 487 us (35.3 TFLOP/s), two 1024-token rows 248 us, four rows of
-// ~512 tokens 182 us, 1000 history + 1024 chunk tokens 386 us.  The fp64 FMA form this replaces
+// accumulators): one 2048-token row 471-476 us (36.1-36.5 TFLOP/s), two 1024-token rows 235-236 us,
+// four rows of ~512 tokens 168 us, 1000 history + 1024 chunk tokens 374-378 us, with the queries
+// read by 16-byte loads (2-byte loads: 484 / 249 / 184 / 387 us).  The fp64 FMA form this replaces
 // (one lane per key, query rows broadcast from LDS, one wavefront per SIMD) took 3106 / 934 / 499 /
-// 1845 us in the same runs.
+// 1845 us.  A timing copy without the cross-wavefront merge of the outputs ran about 1% faster.
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfCols = 16;                                    // (query, head) columns of a workgroup
@@ -835,6 +836,7 @@ struct ExactPrefillArgs {
   int32_t tiles;           // query tiles per row
   int32_t batch;           // rows
   int32_t groups;          // workgroups of these rows: tiles x kv_heads x batch
+  int32_t q_vec;           // query rows 16-byte aligned (pointer and strides): 16-byte loads
 };
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
@@ -915,8 +917,16 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
     const bool live = c < kCols && ci < L;
     const int cq = min(ci, L - 1);  // unused columns read a real row and keep zeros
     const uint16_t* qrow = a.q + b * a.q_row + (g * kG + c % kG) * a.q_head + static_cast<int64_t>(cq) * a.q_tok + 32 * q4;
+    if (a.q_vec) {  // uniform
+      u32x4 qv[4];
 #pragma unroll
-    for (int t = 0; t < 32; ++t) qd[t] = live ? static_cast<double>(bf16_bits_to_f32(qrow[t])) : 0.0;
+      for (int x = 0; x < 4; ++x) qv[x] = reinterpret_cast<const u32x4*>(qrow)[x];
+#pragma unroll
+      for (int t = 0; t < 32; ++t) qd[t] = live ? bf16_at(qv[t >> 3], t & 7) : 0.0;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 32; ++t) qd[t] = live ? static_cast<double>(bf16_bits_to_f32(qrow[t])) : 0.0;
+    }
   }
 
   // Row of key kk (clamped to the last key any column sees; such keys are masked or zeroed).
@@ -1400,6 +1410,7 @@ extern "C" int32_t mi_chunked_prefill_attention_exact(
   a.start_lens = start_lens;
   a.chunk_lens = chunk_lens;
   a.lens_stride = lens_stride;
+  a.q_vec = aligned16(query) && query_row_stride % 8 == 0 && query_head_stride % 8 == 0 && query_tok_stride % 8 == 0;
   // Keys a row can see: its history (at most the table's) plus the chunk up to it.
   exact_rows(a, batch, padded_len, num_heads, num_kv_heads,
              static_cast<int64_t>(max_history_blocks) * kBlockSize + padded_len, scale);
@@ -1470,6 +1481,7 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
   ExactPrefillArgs a0{};
   if (chunks) {
     fill(a0, 0, prefill_width);
+    a0.q_vec = aligned16(query) && query_tok_stride % 8 == 0 && query_head_stride % 8 == 0;
     a0.history = history_blocks;
     a0.hist_stride = history_stride;
     a0.max_hist_blocks = max_history_blocks;
