@@ -206,6 +206,21 @@ def test_exact_prefill_is_bit_identical_to_the_oracle(device, seed, starts, lens
         assert not got[b, :width - n].any()
 
 
+def test_exact_prefill_query_load_forms_are_bit_identical(device):
+    """Aligned query rows take 16-byte loads, others 2-byte loads: the same bits."""
+    starts, lens = [60, 0], [150, 97]
+    q, k, v, kp, vp, hist = prefill_case(11, starts, lens, 8, 2)
+    args = [t.to(device) for t in (q, k, v, kp, vp, hist)]
+    B, H, L, D = q.shape
+    odd = torch.empty((B, H, L, D + 1), dtype=q.dtype, device=device)
+    q_odd = odd[..., 1:]                                   # 2-byte offset, token stride D + 1
+    q_odd.copy_(args[0])
+    st, ln = torch.tensor(starts, device=device), torch.tensor(lens, device=device)
+    aligned = data_plane.chunked_prefill_attention(*args, st, ln, SCALE, exact=True)
+    unaligned = data_plane.chunked_prefill_attention(q_odd, *args[1:], st, ln, SCALE, exact=True)
+    assert_bits(unaligned.cpu(), aligned.cpu())
+
+
 def test_exact_rms_norm_is_bit_identical_to_the_oracle(device):
     gen = torch.Generator().manual_seed(0)
     x = (torch.randn(3000, 1024, generator=gen) * 3).bfloat16()
