@@ -322,8 +322,8 @@ int32_t mi_chunked_prefill_attention_exact(void* out, int64_t out_row_stride, in
  * Either part may be empty (P = 0 or L = 0, D = 0).
  *
  * mi_mixed_paged_attention_exact -- the same with the reference numerics of
- * mi_chunked_prefill_attention_exact; decode rows then give the bits of
- * mi_paged_decode_attention_exact.
+ * mi_chunked_prefill_attention_exact (decode rows as one-token chunks there too, their sums exact);
+ * decode rows then give the bits of mi_paged_decode_attention_exact.
  */
 int32_t mi_mixed_paged_attention(void* out, int64_t out_tok_stride, const void* query, int64_t query_tok_stride,
                                  int64_t query_head_stride, const void* key, int64_t key_tok_stride,

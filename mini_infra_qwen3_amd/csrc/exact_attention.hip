@@ -470,14 +470,6 @@ __device__ void exact_decode_body(const ExactDecodeArgs& a, const int b, const i
   }
 }
 
-// The decode body called out of line from the mixed launch, so that its registers do not burden
-// the chunk rows' code of that kernel.
-template <int kG, int kWaves>
-__device__ __attribute__((noinline)) void exact_decode_rows(const ExactDecodeArgs& a, const int b, const int g,
-                                                            unsigned char* smem) {
-  exact_decode_body<kG, false, kWaves>(a, b, g, smem);
-}
-
 template <int kG, bool kPrologue>
 __global__ __launch_bounds__(kDecThreads) void exact_decode_kernel(const ExactDecodeArgs a) {
   extern __shared__ __align__(16) unsigned char s_dec[];
@@ -837,6 +829,13 @@ struct ExactPrefillArgs {
   int32_t batch;           // rows
   int32_t groups;          // workgroups of these rows: tiles x kv_heads x batch
   int32_t q_vec;           // query rows 16-byte aligned (pointer and strides): 16-byte loads
+  // Decode rows (a mixed step's single new tokens, padded_len 1): start_lens holds each row's
+  // context length including its token, so the history is the context minus one and the chunk key
+  // is the token itself; a row with context 0 is padding.  The token's K/V row of each KV head is
+  // also appended to pool slot slot_mapping[b] (skipped when outside the pool).
+  int32_t decode_rows;
+  const int64_t* slot_mapping;
+  int64_t slot_stride;
 };
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
@@ -851,24 +850,17 @@ __device__ __forceinline__ double bf16_at(const u32x4 v, int e) {
   return (e & 1) ? bf16_hi(x) : bf16_lo(x);
 }
 
-// One launch serves a mixed step: the first a.groups workgroups take the chunk rows of a, the rest
-// (one per decode row and KV head of d) run the exact decode body with this kernel's wavefronts --
-// the sums are exact, so the bits do not depend on how the keys are split.
-template <int kG, bool kCached, bool kDecodeRows>
-__global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPrefillArgs a, const ExactDecodeArgs d) {
+// One launch serves a mixed step: the first a1.groups workgroups take the decode rows of a1 as
+// one-token chunks (history: the context but the token; each as heavy as the chunk's heaviest
+// query tiles, so dispatched first), the rest the chunk rows of a0 -- the sums are exact, so the
+// decode rows get the bits of the exact decode body.
+template <int kG, bool kCached>
+__global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPrefillArgs a0, const ExactPrefillArgs a1) {
   constexpr int kQP = kPfCols / kG;  // query positions of a workgroup
   constexpr int kCols = kQP * kG;    // columns in use (15 for G = 5)
   extern __shared__ __align__(16) unsigned char s_raw[];
-
-  // The decode rows' call is compiled only into the launches that have them: its registers would
-  // otherwise halve the occupancy of every chunk launch.
-  if constexpr (kDecodeRows) {
-    if (static_cast<int>(blockIdx.x) >= a.groups) {  // uniform: a decode row
-      const int lin = static_cast<int>(blockIdx.x) - a.groups;
-      exact_decode_rows<kG, kPfWaves>(d, lin / d.kv_heads, lin % d.kv_heads, s_raw);
-      return;
-    }
-  }
+  const bool decode = static_cast<int>(blockIdx.x) < a1.groups;  // uniform
+  const ExactPrefillArgs a = decode ? a1 : a0;
   float* sM = reinterpret_cast<float*>(s_raw);                                    // [waves][16]
   double* sL = reinterpret_cast<double*>(s_raw + kPfWaves * kPfCols * 4);          // [waves][16][hi, lo]
   uint2* sC = reinterpret_cast<uint2*>(s_raw + kPfRedBytes);                      // [waves][cache_tiles][64]
@@ -877,7 +869,7 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   // Workgroup order: query tiles from the last (most keys) to the first across every row and KV
   // head, the KV head fastest, so consecutive workgroups (round-robin over the XCDs) keep one KV
   // head's keys on one XCD when there are 8 KV heads.
-  const int lin = static_cast<int>(blockIdx.x);
+  const int lin = static_cast<int>(blockIdx.x) - (decode ? 0 : a1.groups);
   const int g = lin % a.kv_heads;
   const int b = (lin / a.kv_heads) % a.batch;
   const int qt = a.tiles - 1 - lin / (a.kv_heads * a.batch);
@@ -885,14 +877,32 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   const int lane = threadIdx.x & 63;
   const int q4 = lane >> 4, c = lane & 15;
   const int L = a.padded_len;
-  int64_t clen = a.chunk_lens[b * a.lens_stride];
-  int64_t nh64 = a.start_lens[b * a.lens_stride];
+  int64_t clen, nh64;
+  if (a.decode_rows) {
+    const int64_t ctx = a.start_lens[b * a.lens_stride];
+    clen = ctx > 0 ? 1 : 0;
+    nh64 = ctx - 1;
+  } else {
+    clen = a.chunk_lens[b * a.lens_stride];
+    nh64 = a.start_lens[b * a.lens_stride];
+  }
   clen = clen < 0 ? 0 : (clen > L ? L : clen);
   const int pad = L - static_cast<int>(clen);
   nh64 = nh64 < 0 ? 0 : min(nh64, static_cast<int64_t>(a.max_hist_blocks) * kBlockSize);
   const int nh = static_cast<int>(nh64);
   const int i0 = qt * kQP;
   const int i_last = min(i0 + kQP - 1, L - 1);
+  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
+
+  if (a.decode_rows && clen > 0 && threadIdx.x < 32) {  // append the token's K and V rows of KV head g
+    const int64_t slot = a.slot_mapping[b * a.slot_stride];
+    if (slot >= 0 && slot < a.num_blocks * kBlockSize) {
+      const int piece = (threadIdx.x & 15) * 8;
+      const uint16_t* src = threadIdx.x < 16 ? a.k + b * a.k_row + g * a.k_head : a.v + b * a.v_row + g * a.v_head;
+      uint16_t* dst = (threadIdx.x < 16 ? a.key_pool : a.value_pool) + slot * row_elems + g * kHeadDim;
+      *reinterpret_cast<uint4*>(dst + piece) = *reinterpret_cast<const uint4*>(src + piece);
+    }
+  }
 
   if (i_last < pad) {  // every query of the tile is padding: zero rows (uniform)
     const int col = threadIdx.x >> 4, piece = threadIdx.x & 15;
@@ -904,7 +914,6 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   }
   const int nkeys = nh + i_last - pad + 1;  // keys any column of the tile sees
   const int ntiles = (nkeys + kPfTileKeys - 1) / kPfTileKeys;
-  const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
 
   // This lane's column: query position i0 + c / G, query head g G + c % G.  Key kk (history slots
   // first, then chunk positions pad, pad + 1, ...) is visible to it iff kk <= kmax.
@@ -1170,50 +1179,35 @@ int32_t dispatch_exact_decode(const ExactDecodeArgs& a, int32_t batch, int group
   }
 }
 
-template <int kG, bool kCached, bool kDecodeRows>
-int32_t launch_exact_prefill(const ExactPrefillArgs& a, const ExactDecodeArgs& d, int32_t decode_rows, const char* what,
-                             hipStream_t s) {
+template <int kG, bool kCached>
+int32_t launch_exact_prefill(const ExactPrefillArgs& a0, const ExactPrefillArgs& a1, const char* what, hipStream_t s) {
   static std::once_flag once;
   static int32_t attr_rc = MI_OK;
-  std::call_once(once, [] {
-    attr_rc = allow_lds(exact_prefill_kernel<kG, kCached, kDecodeRows>, kPfLdsBytes, "exact_prefill_kernel");
-  });
+  std::call_once(once, [] { attr_rc = allow_lds(exact_prefill_kernel<kG, kCached>, kPfLdsBytes, "exact_prefill_kernel"); });
   if (attr_rc != MI_OK) return attr_rc;
-  const int64_t decode_groups = static_cast<int64_t>(decode_rows) * (decode_rows > 0 ? d.kv_heads : 0);
-  if (a.groups < 0 || static_cast<int64_t>(a.groups) + decode_groups > 0x3fffffff)
+  if (a0.groups < 0 || a1.groups < 0 || static_cast<int64_t>(a0.groups) + a1.groups > 0x3fffffff)
     return fail(MI_ERR_UNSUPPORTED, "%s: too many workgroups", what);
-  const int groups = a.groups + static_cast<int>(decode_groups);
+  const int groups = a0.groups + a1.groups;
   if (groups == 0) return ok();
-  size_t lds = 0;
-  if (a.groups > 0)
-    lds = static_cast<size_t>(kPfRedBytes) +
-          std::max(static_cast<size_t>(kPfMergeBytes),
-                   kCached ? static_cast<size_t>(a.cache_tiles) * kPfWaves * kPfCacheTileBytes : size_t{0});
-  if (decode_groups > 0)
-    lds = std::max(lds, static_cast<size_t>(DecodeLds<kG, kPfWaves>::kFixed) +
-                            static_cast<size_t>(d.cache_tokens) * kG * sizeof(uint16_t));
-  exact_prefill_kernel<kG, kCached, kDecodeRows><<<groups, kPfThreads, lds, s>>>(a, d);
+  const size_t lds = static_cast<size_t>(kPfRedBytes) +
+                     std::max(static_cast<size_t>(kPfMergeBytes),
+                              kCached ? static_cast<size_t>(a0.cache_tiles) * kPfWaves * kPfCacheTileBytes : size_t{0});
+  exact_prefill_kernel<kG, kCached><<<groups, kPfThreads, lds, s>>>(a0, a1);
   return check_launch(what);
 }
 
-template <int kG>
-int32_t launch_exact_prefill_form(const ExactPrefillArgs& a, const ExactDecodeArgs& d, int32_t decode_rows,
-                                  const char* what, hipStream_t s) {
-  if (decode_rows > 0)
-    return a.cache_tiles > 0 ? launch_exact_prefill<kG, true, true>(a, d, decode_rows, what, s)
-                             : launch_exact_prefill<kG, false, true>(a, d, decode_rows, what, s);
-  return a.cache_tiles > 0 ? launch_exact_prefill<kG, true, false>(a, d, decode_rows, what, s)
-                           : launch_exact_prefill<kG, false, false>(a, d, decode_rows, what, s);
-}
-
-int32_t dispatch_exact_prefill(const ExactPrefillArgs& a, const ExactDecodeArgs& d, int32_t decode_rows, int group,
-                               const char* what, hipStream_t s) {
+// Both row sets share one score-cache size (the larger of the two; the recomputing form when
+// either set's rows are too long for the cache).
+int32_t dispatch_exact_prefill(ExactPrefillArgs a0, ExactPrefillArgs a1, int group, const char* what, hipStream_t s) {
+  const bool cached = (a0.groups == 0 || a0.cache_tiles > 0) && (a1.groups == 0 || a1.cache_tiles > 0);
+  const int32_t tiles = cached ? std::max(a0.groups > 0 ? a0.cache_tiles : 0, a1.groups > 0 ? a1.cache_tiles : 0) : 0;
+  a0.cache_tiles = a1.cache_tiles = tiles;
   switch (group) {
-    case 1: return launch_exact_prefill_form<1>(a, d, decode_rows, what, s);
-    case 2: return launch_exact_prefill_form<2>(a, d, decode_rows, what, s);
-    case 4: return launch_exact_prefill_form<4>(a, d, decode_rows, what, s);
-    case 5: return launch_exact_prefill_form<5>(a, d, decode_rows, what, s);
-    default: return launch_exact_prefill_form<8>(a, d, decode_rows, what, s);
+    case 1: return cached ? launch_exact_prefill<1, true>(a0, a1, what, s) : launch_exact_prefill<1, false>(a0, a1, what, s);
+    case 2: return cached ? launch_exact_prefill<2, true>(a0, a1, what, s) : launch_exact_prefill<2, false>(a0, a1, what, s);
+    case 4: return cached ? launch_exact_prefill<4, true>(a0, a1, what, s) : launch_exact_prefill<4, false>(a0, a1, what, s);
+    case 5: return cached ? launch_exact_prefill<5, true>(a0, a1, what, s) : launch_exact_prefill<5, false>(a0, a1, what, s);
+    default: return cached ? launch_exact_prefill<8, true>(a0, a1, what, s) : launch_exact_prefill<8, false>(a0, a1, what, s);
   }
 }
 
@@ -1414,7 +1408,7 @@ extern "C" int32_t mi_chunked_prefill_attention_exact(
   // Keys a row can see: its history (at most the table's) plus the chunk up to it.
   exact_rows(a, batch, padded_len, num_heads, num_kv_heads,
              static_cast<int64_t>(max_history_blocks) * kBlockSize + padded_len, scale);
-  const int32_t rc = dispatch_exact_prefill(a, ExactDecodeArgs{}, 0, group, what, as_stream(stream));
+  const int32_t rc = dispatch_exact_prefill(a, ExactPrefillArgs{}, group, what, as_stream(stream));
   return rc == MI_OK ? ok() : rc;
 }
 
@@ -1493,46 +1487,24 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
   } else {
     a0.kv_heads = num_kv_heads;
   }
-  // Decode rows: the exact decode body in its plain form (rotated queries), appending each row's
-  // rotated K/V first.
+  // Decode rows: one-token chunks at tokens [P L, P L + D) whose history is the context minus the
+  // token (the block table), appending each row's rotated K/V to its slot.
   const int group = num_heads / num_kv_heads;
-  ExactDecodeArgs d{};
+  ExactPrefillArgs a1{};
   if (decode_rows > 0) {
-    d.out = static_cast<uint16_t*>(out) + n * out_tok_stride;
-    d.out_row = out_tok_stride;
-    d.q = static_cast<const uint16_t*>(query) + n * query_tok_stride;
-    d.q_row = query_tok_stride;
-    d.q_head = query_head_stride;
-    d.k_new = static_cast<const uint16_t*>(key) + n * key_tok_stride;
-    d.v_new = static_cast<const uint16_t*>(value) + n * value_tok_stride;
-    d.k_row = key_tok_stride;
-    d.v_row = value_tok_stride;
-    d.k_head = key_head_stride;
-    d.v_head = value_head_stride;
-    d.slot_mapping = slot_mapping;
-    d.slot_stride = slot_stride;
-    d.num_slots = num_blocks * kBlockSize;
-    d.key_pool = static_cast<uint16_t*>(key_pool);
-    d.value_pool = static_cast<uint16_t*>(value_pool);
-    d.num_blocks = num_blocks;
-    d.kv_heads = num_kv_heads;
-    d.block_tables = block_tables;
-    d.bt_stride = block_table_stride;
-    d.max_blocks = max_blocks;
-    d.context_lens = context_lens;
-    d.ctx_stride = context_lens_stride;
-    d.scale = scale;
-    const int64_t tokens = static_cast<int64_t>(max_blocks) * kBlockSize;
-    int64_t fixed = 0;
-    switch (group) {
-      case 1: fixed = DecodeLds<1, kPfWaves>::kFixed; break;
-      case 2: fixed = DecodeLds<2, kPfWaves>::kFixed; break;
-      case 4: fixed = DecodeLds<4, kPfWaves>::kFixed; break;
-      case 5: fixed = DecodeLds<5, kPfWaves>::kFixed; break;
-      default: fixed = DecodeLds<8, kPfWaves>::kFixed; break;
-    }
-    d.cache_tokens = fixed + tokens * group * 2 <= kPfLdsBytes ? static_cast<int32_t>(tokens) : 0;
+    fill(a1, n, 1);
+    a1.q_vec = aligned16(query) && query_tok_stride % 8 == 0 && query_head_stride % 8 == 0;
+    a1.history = block_tables;
+    a1.hist_stride = block_table_stride;
+    a1.max_hist_blocks = max_blocks;
+    a1.start_lens = context_lens;
+    a1.chunk_lens = context_lens;
+    a1.lens_stride = context_lens_stride;
+    a1.decode_rows = 1;
+    a1.slot_mapping = slot_mapping;
+    a1.slot_stride = slot_stride;
+    exact_rows(a1, decode_rows, 1, num_heads, num_kv_heads, static_cast<int64_t>(max_blocks) * kBlockSize + 1, scale);
   }
-  const int32_t rc = dispatch_exact_prefill(a0, d, decode_rows, group, what, as_stream(stream));
+  const int32_t rc = dispatch_exact_prefill(a0, a1, group, what, as_stream(stream));
   return rc == MI_OK ? ok() : rc;
 }
