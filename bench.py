@@ -684,7 +684,9 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
     captured when the backend is set up (``setup_s``, outside the timed run).
     ``exact`` (reference numerics, the configuration whose greedy tokens are identical to the
     oracle's): the exact attention kernels and the reference's GEMM calls; decode forwards replay
-    a graph per batch size; prefill steps run eagerly at the chunks' own width.  ``exact=False``:
+    a graph per batch size; prefill steps run eagerly at the chunks' own width; mixed steps run at
+    their padded shape (width to a multiple of 128, decode rows to a power of two), replayed from
+    a graph per shape.  ``exact=False``:
     the bandwidth kernels and fused GEMMs, decode graphs per padded (batch, blocks) bucket and
     prefill (and mixed) graphs per padded (rows, width) bucket.  ``mixed``: decode rows ride in
     the prefill steps (the mixed batching the reference plans) instead of the reference's
@@ -701,7 +703,7 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
     def run(requests):
         t0 = time.perf_counter()
         backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True, prefill_graphs=not exact,
-                                       mixed_graphs=mixed and not exact)
+                                       mixed_graphs=mixed)
         setup_s = time.perf_counter() - t0
         return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False,
                              mixed_batching=mixed), setup_s
@@ -738,6 +740,7 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
         "arrival_rate_req_s": 20.0,
         "decode_graphs": "per batch size" if exact else "per padded (batch, blocks) bucket",
         "prefill_graphs": not exact,
+        "mixed_graphs": mixed,
         "setup_s": round(setup_s, 2),
         "latency_ms": {k: round(v, 2) for k, v in res.latency_summary().items()},
         "_tokens": res.tokens,  # per request, for the token agreement; dropped from the JSON line

@@ -54,8 +54,9 @@ class PagedScheduleBackend:
         ``prefill_graphs``: likewise the chunked-prefill forward of up to ``prefill_graph_rows`` chunks,
         for widths up to the longest prompt and histories up to its blocks.  ``mixed_graphs``: the
         mixed-step forward of up to ``mixed_graph_rows`` chunks with up to ``mixed_graph_decode_rows``
-        decode rows.  A model with reference numerics (``exact``) takes decode graphs per batch size
-        and no prefill or mixed graphs (they pad the chunk width: ValueError)."""
+        decode rows.  A model with reference numerics (``exact``) takes decode graphs per batch size,
+        mixed graphs at the padded shapes it runs every mixed step at (``padded_mixed_shape``) and
+        no prefill graphs (they pad the chunk width: ValueError)."""
         self.model = model
         self.device = next(model.parameters()).device
         self.block_size = paged_cache_config.block_size

@@ -136,6 +136,22 @@ def pack_prefill_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions:
     return out
 
 
+MIXED_WIDTH_QUANTUM = 128  # chunk width step of a padded mixed step
+
+
+def padded_mixed_shape(width: int, decode_rows: int, quantum: int = MIXED_WIDTH_QUANTUM) -> tuple[int, int]:
+    """The (chunk width, decode rows) a mixed step with reference numerics runs at: the longest
+    chunk rounded up to a multiple of ``quantum``, the decode rows up to a power of two (none stays
+    none).  The reference plans mixed steps but does not define them
+    (src/mini_infra/core/scheduler.py:310-311); their GEMMs run over all P L + D rows, and a GEMM's
+    rows can round differently at another M.  With L and D on these steps every step shape is one of
+    a few buckets, each of which a HIP graph replays with the same GEMM calls, and so the same bits,
+    as the eager forward of that shape."""
+    if width <= 0 or decode_rows < 0 or quantum <= 0:
+        raise ValueError(f"bad mixed step shape: width {width}, decode rows {decode_rows}, quantum {quantum}")
+    return -(-width // quantum) * quantum, (1 << (decode_rows - 1).bit_length()) if decode_rows else 0
+
+
 def pack_mixed_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions: Sequence[int],
                     prefill_tables: Sequence[Sequence[int]], last_tokens: Sequence[int], positions: Sequence[int],
                     decode_tables: Sequence[Sequence[int]], block_size: int, pad_token_id: int,
@@ -162,4 +178,5 @@ def pack_mixed_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions: S
     return flat, (rows, width, nb, decode.shape[0], decode.shape[1] - 4)
 
 
-__all__ = ["pack_decode_rows", "pack_mixed_rows", "pack_prefill_rows", "padded_tables", "prefill_scatter_indices"]
+__all__ = ["MIXED_WIDTH_QUANTUM", "pack_decode_rows", "pack_mixed_rows", "pack_prefill_rows", "padded_mixed_shape",
+           "padded_tables", "prefill_scatter_indices"]

@@ -16,8 +16,9 @@ Same entry points, arguments and return types as the reference's PagedRunner
   upload, and ``run_decode_step`` replays the graph -- one launch instead of ~300.  A model with
   reference numerics (``exact``) gets one graph per batch size instead (a GEMM's rows can change
   with its M, so padding the batch would change them) and one table width (the decode kernel
-  reads only the blocks a row's context covers); prefill and mixed graphs, which pad the chunk
-  width, are for models without reference numerics;
+  reads only the blocks a row's context covers); prefill graphs, which pad the chunk width, are
+  for models without reference numerics.  Such a model runs every mixed step at a padded shape
+  (``padded_mixed_shape``), so mixed graphs serve it as well;
 * ``prepare_mixed_inputs`` / ``run_mixed_step`` run prefill chunks and decode tokens in one forward
   (the mixed batching the reference plans next: src/mini_infra/core/scheduler.py:310-311).
 """
@@ -36,8 +37,8 @@ from mini_infra_qwen3_amd.model.qwen3 import PagedAttentionMetadata, PagedMixedM
 from mini_infra_qwen3_amd.worker.base_runner import BaseModelRunner, PrefillOutput
 from mini_infra_qwen3_amd.worker.block_tables import DeviceBlockTables
 from mini_infra_qwen3_amd.worker.kv_cache import KVCache
-from mini_infra_qwen3_amd.worker.metadata import (pack_decode_rows, pack_mixed_rows, pack_prefill_rows,
-                                                  prefill_scatter_indices)
+from mini_infra_qwen3_amd.worker.metadata import (MIXED_WIDTH_QUANTUM, pack_decode_rows, pack_mixed_rows,
+                                                  pack_prefill_rows, padded_mixed_shape, prefill_scatter_indices)
 from mini_infra_qwen3_amd.worker.paged_kv_cache import PagedKVCachePool
 from mini_infra_qwen3_amd.worker.sampler import greedy_sample
 
@@ -234,6 +235,7 @@ class PagedRunner(BaseModelRunner):
         self._mixed_graphs: dict[tuple[int, int, int], _MixedGraph] = {}
         self._mixed_pool: PagedKVCachePool | None = None
         self._mixed_loaded: tuple[_MixedGraph, int] | None = None
+        self._mixed_eager: tuple[int, int] | None = None  # (slot buffer address, live decode rows)
         self._decode_row_buckets: list[int] = []
         self._staging: torch.Tensor | None = None
         self._mempool = None
@@ -304,19 +306,29 @@ class PagedRunner(BaseModelRunner):
         torch.cuda.synchronize(self.device)
 
     def enable_mixed_graphs(self, pool: PagedKVCachePool, max_rows: int, max_width: int, max_decode_rows: int,
-                            max_history_blocks: int, max_decode_blocks: int, width_quantum: int = 128,
+                            max_history_blocks: int, max_decode_blocks: int, width_quantum: int = MIXED_WIDTH_QUANTUM,
                             decode_row_buckets: Sequence[int] | None = None) -> None:
         """Captures the mixed-step forward for 1..``max_rows`` chunk rows, padded widths in multiples of
         ``width_quantum`` up to ``max_width`` and decode-row buckets up to ``max_decode_rows`` (pad
         rows append nothing), with history / decode tables ``max_history_blocks`` /
         ``max_decode_blocks`` wide, over ``pool``.  Other steps run without a graph; as with prefill
-        graphs, store a step's ``prefill_cache`` before the next graphed step."""
+        graphs, store a step's ``prefill_cache`` before the next graphed step.  A model with
+        reference numerics runs every mixed step at ``padded_mixed_shape`` (graphed or not), so its
+        buckets are exactly those shapes: width quantum ``MIXED_WIDTH_QUANTUM`` and power-of-two
+        decode rows."""
         if self.device.type != "cuda":
             raise RuntimeError("mixed graphs need the GPU")
-        self._refuse_padded_graphs("mixed")
+        exact = getattr(self.model, "exact", False)
         if decode_row_buckets is None:
             decode_row_buckets = [b for b in (1, 2, 4, 8, 16, 32, 64, 128, 256) if b < max_decode_rows]
-            decode_row_buckets.append(max_decode_rows)
+            if not exact:
+                decode_row_buckets.append(max_decode_rows)
+            elif max_decode_rows & (max_decode_rows - 1) == 0:
+                decode_row_buckets.append(max_decode_rows)
+        if exact and (width_quantum != MIXED_WIDTH_QUANTUM or
+                      any(int(b) & (int(b) - 1) for b in decode_row_buckets if int(b) > 0)):
+            raise ValueError(f"a model with reference numerics runs mixed steps at width multiples of "
+                             f"{MIXED_WIDTH_QUANTUM} and power-of-two decode rows; its graphs must use those buckets")
         self._decode_row_buckets = sorted(set(int(b) for b in decode_row_buckets if 0 < b <= max_decode_rows))
         top_w = -(-max_width // width_quantum) * width_quantum
         staging = self._shared_staging(max_rows * top_w + max(self._decode_row_buckets, default=0), pool)
@@ -530,31 +542,41 @@ class PagedRunner(BaseModelRunner):
     ) -> tuple[torch.Tensor, torch.Tensor, PagedMixedMetadata]:
         """Packs a mixed step -- chunk rows as ``run_prefill_chunk_step`` takes them, decode rows as
         ``prepare_decode_inputs`` does -- into one int64 buffer with one upload.  Returns input_ids /
-        position_ids ``[1, P L + D]`` and the metadata, all views of that buffer."""
+        position_ids ``[1, P L + D]`` and the metadata, all views of that buffer.  With reference
+        numerics L and D are ``padded_mixed_shape`` of the longest chunk and the decode rows (pad rows
+        append nothing and attend to nothing), whether a graph replays the step or not; otherwise L
+        is the longest chunk and D the decode rows, unless a graph bucket pads them."""
         self._mixed_loaded = None
+        self._mixed_eager = None
+        live = len(decode_block_tables)
+        width = max(len(c) for c in chunk_token_ids)
+        exact = getattr(self.model, "exact", False)
+        pad_width, pad_rows = padded_mixed_shape(width, live) if exact else (None, None)
         if self._mixed_graphs and pool is self._mixed_pool:
-            width = max(len(c) for c in chunk_token_ids)
             hist = max(-(-st // pool.block_size) for st in start_positions)
-            graph = self._mixed_bucket(len(chunk_token_ids), width, hist, len(decode_block_tables),
+            graph = self._mixed_bucket(len(chunk_token_ids), width, hist, live,
                                        max((len(t) for t in decode_block_tables), default=0))
+            if graph is not None and exact and (graph.width, graph.decode_rows) != (pad_width, pad_rows):
+                graph = None  # not this step's shape (the eager forward below runs it)
             if graph is not None:
                 flat, _ = pack_mixed_rows(chunk_token_ids, start_positions, prefill_block_tables, last_tokens, positions,
                                           decode_block_tables, pool.block_size, self.pad_token_id, width=graph.width,
                                           history_blocks=graph.hist_blocks, decode_rows=graph.decode_rows,
                                           decode_blocks=graph.decode_blocks)
                 graph.load(flat)
-                self._mixed_loaded = (graph, len(decode_block_tables))
+                self._mixed_loaded = (graph, live)
                 ids, pos, meta = graph.views()
                 return ids, pos, meta._replace(kv_pools=tuple(pool.kv_pools))
         flat, (rows, width, nb, decode_rows, mb) = pack_mixed_rows(
             chunk_token_ids, start_positions, prefill_block_tables, last_tokens, positions, decode_block_tables,
-            pool.block_size, self.pad_token_id)
+            pool.block_size, self.pad_token_id, width=pad_width, decode_rows=pad_rows)
         packed = torch.from_numpy(flat).to(self.device)
         tokens = rows * width + decode_rows
         at = 2 * tokens
         chunk = packed[at:at + rows * (2 + nb)].view(rows, 2 + nb)
         at += rows * (2 + nb)
         dec = packed[at:].view(decode_rows, 2 + mb)
+        self._mixed_eager = (dec.data_ptr(), live)
         pools = tuple(pool.kv_pools)
         metadata = PagedMixedMetadata(
             prefill=PagedPrefillMetadata(history_block_tables=chunk[:, 2:], start_lens=chunk[:, 0],
@@ -584,7 +606,11 @@ class PagedRunner(BaseModelRunner):
             next_token, _ = greedy_sample(logits)
         tokens = next_token.squeeze(-1).tolist()
         rows = metadata.prefill_rows
-        return MixedStepOutput(tokens[:rows], tokens[rows:], KVCache(present), timer.elapsed_ms)
+        live = len(tokens) - rows
+        eager = self._mixed_eager
+        if eager is not None and metadata.decode.slot_mapping.data_ptr() == eager[0]:
+            live = eager[1]  # inputs from prepare_mixed_inputs, padded to the step's shape
+        return MixedStepOutput(tokens[:rows], tokens[rows:rows + live], KVCache(present), timer.elapsed_ms)
 
 
 __all__ = ["MixedStepOutput", "PagedDecodeOutput", "PagedRunner"]

@@ -194,7 +194,8 @@ def decode_step(model: ReferenceQwen3, block_tables, last_tokens, positions, poo
 
 
 def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, chunk_tables, last_tokens, positions,
-                      decode_tables, pools, block_size, pad_token_id: int = 0):
+                      decode_tables, pools, block_size, pad_token_id: int = 0, width: int | None = None,
+                      decode_rows: int | None = None):
     """A mixed step -- prompt chunks and decode tokens in one forward, the batching the reference
     plans next (src/mini_infra/core/scheduler.py:310-311) and does not define -- as the reference's
     ops over one flattened ``[1, P L + D]`` batch: P chunks left-padded to the longest (L) as
@@ -204,13 +205,21 @@ def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, c
     (history gathered from the pool, causal inside the chunk), the decode tokens' as a paged decode
     step's (append, then attend over the context), neither reading the other's blocks.  Returns
     (logits ``[P + D, V]`` of each chunk's last position then each decode token, the chunks'
-    per-layer ``(K, V)`` ``[P, Hkv, L, D]``)."""
+    per-layer ``(K, V)`` ``[P, Hkv, L, D]``).
+
+    ``width`` / ``decode_rows`` (at least the longest chunk / the decode tokens) pad L and D: pad
+    decode rows (token ``pad_token_id``, position 0) append nothing, attend to nothing (zero
+    output) and return no logits; every op still runs over all P L + D rows, so each GEMM has the
+    padded M."""
     c = model.config
     dev = model.device
     scaling = c.head_dim ** -0.5
-    rows, decode_rows = len(chunk_token_ids), len(last_tokens)
+    rows, live = len(chunk_token_ids), len(last_tokens)
     lens = [len(t) for t in chunk_token_ids]
-    width = max(lens)
+    width = max(lens) if width is None else width
+    decode_rows = live if decode_rows is None else decode_rows
+    if width < max(lens) or decode_rows < live:
+        raise ValueError(f"width {width} / decode_rows {decode_rows} below the step's {max(lens)} / {live}")
     n = rows * width
     ids = torch.full((rows, width), pad_token_id, dtype=torch.long)
     pos = torch.zeros((rows, width), dtype=torch.long)
@@ -223,8 +232,9 @@ def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, c
     for r, (t, hb) in enumerate(zip(chunk_tables, hist)):
         hist_ids[r, :hb] = torch.tensor(list(t[:hb]), dtype=torch.long)
     dec = torch_ref.prepare_decode_rows(decode_tables, last_tokens, positions, block_size).to(dev)
-    flat_ids = torch.cat((ids.flatten().to(dev), dec[:, 0])).unsqueeze(0)
-    flat_pos = torch.cat((pos.flatten().to(dev), dec[:, 1])).unsqueeze(0)
+    pad = torch.zeros(decode_rows - live, dtype=torch.long, device=dev)
+    flat_ids = torch.cat((ids.flatten().to(dev), dec[:, 0], pad + pad_token_id)).unsqueeze(0)
+    flat_pos = torch.cat((pos.flatten().to(dev), dec[:, 1], pad)).unsqueeze(0)
     # visibility of the chunk rows (history slots < start, causal inside the chunk, no left padding)
     allowed = torch_ref.chunk_allowed_mask(start_positions, lens, max_hist, block_size, width).to(dev)
     chunk_bias = torch.zeros(allowed.shape, dtype=model.dtype, device=dev)
@@ -246,17 +256,18 @@ def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, c
             (hk, hv), = torch_ref.gather_blocks([pools[layer]], hist_ids.to(dev))
             kc, vc = torch.cat((hk, kc), dim=2), torch.cat((hv, vc), dim=2)
         chunk_out = attend(qc.contiguous(), kc, vc, chunk_bias, scaling)  # [P, L, H D]
-        qd = q[0, :, n:].transpose(0, 1).unsqueeze(2)  # [D, H, 1, Dh]
-        kd = k[0, :, n:].transpose(0, 1).unsqueeze(2)
-        vd = v[0, :, n:].transpose(0, 1).unsqueeze(2)
+        qd = q[0, :, n:n + live].transpose(0, 1).unsqueeze(2)  # [D, H, 1, Dh]
+        kd = k[0, :, n:n + live].transpose(0, 1).unsqueeze(2)
+        vd = v[0, :, n:n + live].transpose(0, 1).unsqueeze(2)
         hk, hv = torch_ref.apply_paged_kv_pool(kd, vd, pools[layer], dec[:, 2], dec[:, 4:])
         dec_out = attend(qd.contiguous(), hk, hv, dec_bias, scaling)  # [D, 1, H D]
-        attn = torch.cat((chunk_out.reshape(n, -1), dec_out.reshape(decode_rows, -1))).unsqueeze(0)
+        pad_out = torch.zeros((decode_rows - live, chunk_out.shape[-1]), dtype=chunk_out.dtype, device=dev)
+        attn = torch.cat((chunk_out.reshape(n, -1), dec_out.reshape(live, -1), pad_out)).unsqueeze(0)
         h = h + F.linear(attn, model.w[p + "self_attn.o_proj.weight"])
         h = h + model._mlp(layer, model._rms(h, model.w[p + "post_attention_layernorm.weight"]))
     last = torch.cat((h[0, width - 1:n:width], h[0, n:])).unsqueeze(1)
     logits = F.linear(model._rms(last, model.w["model.norm.weight"]), model.w["lm_head.weight"])
-    return logits[:, -1], presents
+    return logits[:rows + live, -1], presents
 
 
 class ReferenceScheduleBackend:
@@ -335,10 +346,17 @@ class ReferenceScheduleBackend:
         tables = [manager.block_table(ch.state.request.request_idx) for ch in chunks]
         starts = [ch.start for ch in chunks]
         lens = [ch.num_tokens for ch in chunks]
+        # With exact numerics a mixed step runs at a padded shape -- the longest chunk rounded up to
+        # a multiple of 128, the decode rows to a power of two -- which fixes each GEMM's M.
+        width = decode_rows = None
+        if self.model.exact:
+            width = -(-max(lens) // 128) * 128
+            decode_rows = 1 << (len(states) - 1).bit_length() if states else 0
         logits, presents = mixed_step_logits(
             self.model, [ch.state.request.token_ids[ch.start:ch.end] for ch in chunks], starts, tables,
             [s.generated[-1] for s in states], [s.cache_length for s in states],
-            [manager.block_table(s.request.request_idx) for s in states], self.pools, self.block_size)
+            [manager.block_table(s.request.request_idx) for s in states], self.pools, self.block_size,
+            width=width, decode_rows=decode_rows)
         store_prefill(self.pools, presents, tables, lens, starts, self.block_size)
         logits = logits.float()
         rows = len(chunks)

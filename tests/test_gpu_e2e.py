@@ -79,12 +79,13 @@ def test_greedy_tokens_identical_on_chunked_slices(untied_head_seed, mixed):
     """24 requests with prompts up to 700 tokens and 48 outputs under a 256-token budget, so that
     prompts are chunked over several steps with history.  ``context_dependent_model``: an untied
     N(0, 1) head (output that depends on the whole context, as the reference's diverse test model:
-    tests/unit/conftest.py:13-25).  ``mixed_batching``: decode rows and prompt chunks share steps
-    (the oracle runs a mixed step as one forward over the same flattened batch)."""
+    tests/unit/conftest.py:13-25).  ``mixed_batching``: decode rows and prompt chunks share steps,
+    replayed from mixed graphs where a bucket fits (the oracle runs a mixed step as one forward over
+    the same flattened batch, padded to the same shape)."""
     model, ref = build(untied_head_seed)
     requests = serving_requests(seed=1, num_requests=24, min_prompt=32, max_prompt=700, max_new_tokens=48)
     mrr, budget = 8, 256
-    backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=True)
+    backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=True, mixed_graphs=mixed)
     product = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
                             stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed)
     chunk_steps = product.num_steps(SchedulePhase.PREFILL) + product.num_steps(SchedulePhase.MIXED)

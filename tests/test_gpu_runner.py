@@ -348,8 +348,9 @@ def test_chunked_prefill_matches_oracle_runner(models):
 def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
     """One forward over two prompt chunks (one with history, one completing its prompt) and three
     decoding requests: logits and stored K/V bit-identical to the oracle's mixed step (the same
-    flattened batch), greedy tokens equal to the chunk step and the decode step run apart and to the
-    CPU oracle, logits close to the decode step's."""
+    flattened batch, padded to width 128 and 4 decode rows as reference numerics run every mixed
+    step), greedy tokens equal to the chunk step and the decode step run apart and to the CPU
+    oracle, logits close to the decode step's."""
     model, ref, ref_cpu = models
     cfg = model.config
     runner = PagedRunner(model)
@@ -392,13 +393,13 @@ def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
         # mixed (pool 1)
         ids, pos, meta = runner.prepare_mixed_inputs(chunks, starts, pf_tables, first, positions, dec_tables,
                                                      pools[1])
-        assert ids.shape == (1, 2 * max(lens) + 3)
+        assert ids.shape == (1, 2 * 128 + 4)
         # the decode rows' append rewrites the same values when the step runs again
-        mixed_logits = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)[0][:, -1]
+        mixed_logits = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)[0][:5, -1]
         got = runner.run_mixed_step(ids, pos, meta)
         runner.store_prefill(pools[1], got.prefill_cache, pf_tables, lens, starts)
     want_mixed, presents = qwen3_ref.mixed_step_logits(ref, chunks, starts, pf_tables, first, positions, dec_tables,
-                                                       ref_pools, BS)
+                                                       ref_pools, BS, width=128, decode_rows=4)
     qwen3_ref.store_prefill(ref_pools, presents, pf_tables, lens, starts, BS)
     assert torch.equal(mixed_logits, want_mixed)
     want_dec = qwen3_ref.decode_step(ref_cpu, dec_tables, first, positions, cpu_pools, BS)
@@ -509,15 +510,106 @@ def test_exact_decode_graphs_per_batch_match_eager_and_oracle(models):
                 lengths[i] += 1
 
 
-def test_exact_models_refuse_padded_prefill_and_mixed_graphs(models):
+def test_exact_models_refuse_prefill_graphs_and_other_mixed_shapes(models):
+    """Reference numerics: no prefill graphs (they pad the chunk width), and mixed graphs only at the
+    shapes every mixed step runs at (width multiples of 128, power-of-two decode rows)."""
     model = models[0]
     runner = PagedRunner(model)
     pool = make_pool(model.config, 8)
     with pytest.raises(ValueError, match="pad the chunk width"):
         runner.enable_prefill_graphs(pool, max_rows=1, max_width=128, max_history_blocks=4)
-    with pytest.raises(ValueError, match="pad the chunk width"):
+    with pytest.raises(ValueError, match="power-of-two decode rows"):
+        runner.enable_mixed_graphs(pool, max_rows=1, max_width=128, max_decode_rows=3, max_history_blocks=4,
+                                   max_decode_blocks=4, decode_row_buckets=[3])
+    with pytest.raises(ValueError, match="power-of-two decode rows"):
         runner.enable_mixed_graphs(pool, max_rows=1, max_width=128, max_decode_rows=2, max_history_blocks=4,
-                                   max_decode_blocks=4)
+                                   max_decode_blocks=4, width_quantum=64)
+    assert not runner._mixed_graphs
+
+
+def test_exact_mixed_graph_replays_match_eager_runner_and_oracle(models):
+    """Reference numerics run every mixed step at its padded shape (width to a multiple of 128,
+    decode rows to a power of two), graphed or not: graph replays equal an eager forward of the
+    same inputs, and the logits of both equal the GPU oracle's mixed step at that shape, bit for
+    bit, with eager work and syncs between replays and one bucket replayed twice; steps outside the
+    buckets (three chunk rows, a chunk wider than the buckets) run eagerly at the same padded shape.
+    Tokens of the graphed and the eager runner are equal and the pools bit-identical to the
+    oracle's."""
+    model, ref, _ = models
+    cfg = model.config
+    decoders = prompts_of([45, 17, 3], seed=8)
+    chunked = prompts_of([70, 20, 50, 33, 12, 9, 40, 130], seed=9)
+    pools = [make_pool(cfg, 64), make_pool(cfg, 64)]  # graphed, eager
+    ref_pools = torch_ref.make_pools(cfg.num_hidden_layers, 64, BS, 8, 128, device="cuda:0")
+    manager = KVCacheManager(BS, num_blocks=64)
+    graphed, eager_runner = PagedRunner(model), PagedRunner(model)
+    graphed.enable_mixed_graphs(pools[0], max_rows=2, max_width=128, max_decode_rows=4, max_history_blocks=8,
+                                max_decode_blocks=8)
+    assert sorted(graphed._mixed_graphs) == [(r, 128, d) for r in (1, 2) for d in (1, 2, 4)]
+    n_req = len(decoders) + len(chunked)
+    for i, p in enumerate(decoders + chunked):
+        manager.allocate_slots(i, len(p))
+    tables = [manager.block_table(i) for i in range(n_req)]
+    with torch.inference_mode():
+        for pool, runner in zip(pools, (graphed, eager_runner)):
+            out = runner.run_prefill_step(decoders)
+            runner.store_prefill(pool, out.prefill_cache, tables[:3], [len(p) for p in decoders], [0] * 3)
+    _, presents = qwen3_ref.prefill(ref, decoders)
+    qwen3_ref.store_prefill(ref_pools, presents, tables[:3], [len(p) for p in decoders], [0] * 3, BS)
+    last, positions = list(out.next_tokens), [len(p) for p in decoders]
+    # (chunks as (chunked request, start, end), decoding requests, replayed from a graph)
+    steps = [([(0, 0, 30)], [0, 1, 2], True), ([(0, 30, 70), (1, 0, 20)], [0, 1, 2], True),
+             ([(2, 0, 50)], [0, 2], True), ([(3, 0, 33), (4, 0, 12), (5, 0, 9)], [0, 1], False),
+             ([(6, 0, 40)], [0, 1, 2], True), ([(7, 0, 130)], [1], False)]
+    replays = 0
+    with torch.inference_mode():
+        for chunks, dec, graphed_step in steps:
+            for i in dec:
+                assert manager.allocate_slots(i, 1)
+            dec_tables = [manager.block_table(i) for i in dec]
+            chunk_ids = [chunked[c][a:b] for c, a, b in chunks]
+            starts, lens = [a for _, a, _ in chunks], [b - a for _, a, b in chunks]
+            pf_tables = [tables[3 + c] for c, _, _ in chunks]
+            width, dec_rows = -(-max(lens) // 128) * 128, 1 << (len(dec) - 1).bit_length()
+            live = len(chunks) + len(dec)
+            results = []
+            for pool, runner in zip(pools, (graphed, eager_runner)):
+                ids, pos, meta = runner.prepare_mixed_inputs(chunk_ids, starts, pf_tables, [last[i] for i in dec],
+                                                             [positions[i] for i in dec], dec_tables, pool)
+                assert ids.shape == (1, len(chunks) * width + dec_rows)
+                replayed = runner is graphed and runner._mixed_loaded is not None
+                assert replayed == (graphed_step and runner is graphed)
+                eager, eager_present = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
+                torch.cuda.synchronize()
+                got = runner.run_mixed_step(ids, pos, meta)
+                if replayed:
+                    replays += 1
+                    graph = runner._mixed_loaded[0]
+                    assert torch.equal(graph.logits, eager[:, -1]), f"replay {replays} differs from the eager forward"
+                    for (k, v), (ek, ev) in zip(got.prefill_cache, eager_present):
+                        assert torch.equal(k, ek) and torch.equal(v, ev)
+                runner.store_prefill(pool, got.prefill_cache, pf_tables, lens, starts)
+                results.append((got, eager[:live, -1].clone()))
+            want, presents = qwen3_ref.mixed_step_logits(ref, chunk_ids, starts, pf_tables, [last[i] for i in dec],
+                                                         [positions[i] for i in dec], dec_tables, ref_pools, BS,
+                                                         width=width, decode_rows=dec_rows)
+            qwen3_ref.store_prefill(ref_pools, presents, pf_tables, lens, starts, BS)
+            for got, logits in results:
+                assert torch.equal(logits, want)
+                assert got.decode_next_tokens == want[len(chunks):].float().argmax(-1).tolist()
+                assert got.prefill_next_tokens == want[:len(chunks)].float().argmax(-1).tolist()
+            for i, t in zip(dec, results[0][0].decode_next_tokens):
+                last[i], positions[i] = t, positions[i] + 1
+    assert replays == 4
+    torch.cuda.synchronize()
+    assert_bits(pools[0].storage, pools[1].storage)
+    for r in range(n_req):
+        length = positions[r] if r < 3 else len(chunked[r - 3])
+        table = manager.block_table(r)
+        for layer in range(cfg.num_hidden_layers):
+            for kv in range(2):
+                want = torch.cat([ref_pools[layer][kv][x] for x in table])[:length].transpose(0, 1)
+                assert_bits(request_kv(pools[0], layer, table, length)[kv], want)
 
 
 @pytest.mark.parametrize("form", ["exact_eager", "bandwidth_graphs"])

@@ -11,6 +11,7 @@ from mini_infra_qwen3_amd.worker.metadata import (
     pack_decode_rows,
     pack_mixed_rows,
     pack_prefill_rows,
+    padded_mixed_shape,
     padded_tables,
     prefill_scatter_indices,
 )
@@ -148,6 +149,19 @@ def test_mixed_rows_split_into_the_two_packings(sizes):
     at = 2 * t + p * (2 + nb)
     assert (flat[2 * t:at].reshape(p, 2 + nb) == pf[:, 2 * w:]).all()
     assert (flat[at:].reshape(d, 2 + mb) == dc[:, 2:]).all()
+
+
+def test_padded_mixed_shape_known_answers():
+    """Width up to the next multiple of 128 (or the quantum given), decode rows up to the next power
+    of two, no decode rows stays none; nonsense shapes raise."""
+    cases = {(1, 0): (128, 0), (128, 1): (128, 1), (129, 2): (256, 2), (983, 3): (1024, 4), (1024, 8): (1024, 8),
+             (1025, 9): (1152, 16), (39, 13): (128, 16), (2048, 33): (2048, 64)}
+    for (width, rows), want in cases.items():
+        assert padded_mixed_shape(width, rows) == want
+    assert padded_mixed_shape(70, 5, quantum=64) == (128, 8)
+    for bad in ((0, 1), (5, -1), (5, 1, 0)):
+        with pytest.raises(ValueError):
+            padded_mixed_shape(*bad)
 
 
 @pytest.mark.parametrize("seed,block_size", [(0, 16), (1, 4), (2, 1)])
