@@ -179,6 +179,40 @@ def test_loop_invariants_and_metric(budget, capacity):
     assert result.makespan_ms > result.busy_ms
 
 
+def test_loop_freezes_the_collector_only_while_it_runs():
+    """The loop keeps the objects that exist when it starts out of cyclic collections while it runs
+    and restores the collector afterwards, also when a step raises; with the collector disabled it
+    leaves it alone."""
+    import gc
+
+    seen = []
+
+    class Probe(FakeBackend):
+        def execute_decode(self, states):
+            seen.append((gc.isenabled(), gc.get_freeze_count() > 0))
+            return super().execute_decode(states)
+
+    class Failing(FakeBackend):
+        def execute_prefill(self, chunks):
+            raise RuntimeError("step failed")
+
+    requests = [Request(i, tuple(range(1, 6)), 3, 0.0) for i in range(3)]
+    assert gc.get_freeze_count() == 0
+    run_scheduler(Probe(), requests, token_budget=16, max_running_requests=3)
+    assert seen and all(enabled and frozen for enabled, frozen in seen)
+    assert gc.isenabled() and gc.get_freeze_count() == 0
+    with pytest.raises(RuntimeError, match="step failed"):
+        run_scheduler(Failing(), requests, token_budget=16, max_running_requests=3)
+    assert gc.isenabled() and gc.get_freeze_count() == 0
+    seen.clear()
+    gc.disable()
+    try:
+        run_scheduler(Probe(), requests, token_budget=16, max_running_requests=3)
+    finally:
+        gc.enable()
+    assert seen and not any(frozen for _, frozen in seen)
+
+
 def test_step_clock_makes_the_schedule_timing_independent():
     requests = [Request(i, tuple(range(1, 9 + 3 * i)), 4, 10.0 * i) for i in range(6)]
     a, b = FakeBackend(), FakeBackend()
