@@ -703,7 +703,7 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
     def run(requests):
         t0 = time.perf_counter()
         backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True, prefill_graphs=not exact,
-                                       mixed_graphs=mixed)
+                                       mixed_graphs=mixed, mixed_graph_tokens=2048)
         setup_s = time.perf_counter() - t0
         return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False,
                              mixed_batching=mixed), setup_s

@@ -35,8 +35,9 @@
 extern "C" {
 #endif
 
-#define MI_PAGED_ABI_VERSION 3  /* 2: mi_paged_decode_workspace_bytes takes num_kv_heads;
-                                   3: mi_paged_decode_attention_exact takes a workspace */
+#define MI_PAGED_ABI_VERSION 4  /* 2: mi_paged_decode_workspace_bytes takes num_kv_heads;
+                                   3: mi_paged_decode_attention_exact takes a workspace;
+                                   4: mi_mixed_paged_attention[_exact] take ragged chunk rows */
 
 #define MI_OK 0
 #define MI_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative size, bad stride  */
@@ -309,11 +310,16 @@ int32_t mi_chunked_prefill_attention_exact(void* out, int64_t out_row_stride, in
  * rows as mi_paged_decode_attention plus the K/V append of mi_reshape_and_cache's decode form
  * (reference qwen3.py:219-330, the append at qwen3.py:282-283).
  *
- * A flattened token batch of T = P L + D rows, token-major ([T, H, 128] query, [T, H_kv, 128]
+ * A flattened token batch of T = C + D rows, token-major ([T, H, 128] query, [T, H_kv, 128]
  * key / value with token and head strides; out [T, H * 128] with a token stride):
- *   tokens [0, P L): P chunk rows, each a left-padded chunk of width L (row b at token b L) with
- *     start_lens / chunk_lens / history_blocks as in mi_chunked_prefill_attention;
- *   tokens [P L, T): D decode rows, one token each, context_lens[b] tokens including it: the
+ *   tokens [0, C): P chunk rows with start_lens / chunk_lens / history_blocks as in
+ *     mi_chunked_prefill_attention, each seen as a left-padded chunk of width L (L at least every
+ *     chunk_lens[b]: the attention's tiling).  With chunk_first NULL, C = P L and row b is tokens
+ *     [b L, b L + L) (padding included; padding rows get zero output).  With chunk_first (ragged
+ *     rows, device [P]), C = chunk_tokens and row b's chunk_lens[b] real tokens are tokens
+ *     chunk_first[b] .. chunk_first[b] + chunk_lens[b] - 1 (first clamped to [0, C - chunk_lens[b]]):
+ *     no padding is stored, read or written, so C can be the sum of the lengths;
+ *   tokens [C, T): D decode rows, one token each, context_lens[b] tokens including it: the
  *     first context_lens[b] - 1 are read from the pool through block_tables[b], the last is the
  *     row's own key / value, which the launch also appends to pool slot slot_mapping[b] (a slot
  *     outside the pool is skipped; context 0 marks a padding row: zero output, no append).
@@ -329,7 +335,8 @@ int32_t mi_mixed_paged_attention(void* out, int64_t out_tok_stride, const void* 
                                  int64_t query_head_stride, const void* key, int64_t key_tok_stride,
                                  int64_t key_head_stride, const void* value, int64_t value_tok_stride,
                                  int64_t value_head_stride, void* key_pool, void* value_pool, int64_t num_blocks,
-                                 int32_t prefill_rows, int32_t prefill_width, const int64_t* history_blocks,
+                                 int32_t prefill_rows, int32_t prefill_width, int64_t chunk_tokens,
+                                 const int64_t* chunk_first, const int64_t* history_blocks,
                                  int64_t history_stride, int32_t max_history_blocks, const int64_t* start_lens,
                                  const int64_t* chunk_lens, int64_t lens_stride, int32_t decode_rows,
                                  const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,
@@ -342,7 +349,8 @@ int32_t mi_mixed_paged_attention_exact(void* out, int64_t out_tok_stride, const 
                                        int64_t key_tok_stride, int64_t key_head_stride, const void* value,
                                        int64_t value_tok_stride, int64_t value_head_stride, void* key_pool,
                                        void* value_pool, int64_t num_blocks, int32_t prefill_rows,
-                                       int32_t prefill_width, const int64_t* history_blocks, int64_t history_stride,
+                                       int32_t prefill_width, int64_t chunk_tokens, const int64_t* chunk_first,
+                                       const int64_t* history_blocks, int64_t history_stride,
                                        int32_t max_history_blocks, const int64_t* start_lens,
                                        const int64_t* chunk_lens, int64_t lens_stride, int32_t decode_rows,
                                        const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks,

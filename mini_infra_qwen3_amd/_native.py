@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be imported before the library; see module docstring)
 
 LIBRARY_PATH = Path(__file__).resolve().with_name("libmi_paged.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MI_OK = 0
 MI_ERR_INVALID_ARGUMENT = -1
@@ -76,14 +76,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "mi_mixed_paged_attention": (
         _i32,
-        [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i32, _i32, _ptr, _i64,
-         _i32, _ptr, _ptr, _i64, _i32, _ptr, _i64, _i32, _ptr, _i64, _ptr, _i64, _i32, _i32, _i32, _i32,
+        [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i32, _i32, _i64, _ptr,
+         _ptr, _i64, _i32, _ptr, _ptr, _i64, _i32, _ptr, _i64, _i32, _ptr, _i64, _ptr, _i64, _i32, _i32, _i32, _i32,
          ctypes.c_float, _ptr],
     ),
     "mi_mixed_paged_attention_exact": (
         _i32,
-        [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i32, _i32, _ptr, _i64,
-         _i32, _ptr, _ptr, _i64, _i32, _ptr, _i64, _i32, _ptr, _i64, _ptr, _i64, _i32, _i32, _i32, _i32,
+        [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i32, _i32, _i64, _ptr,
+         _ptr, _i64, _i32, _ptr, _ptr, _i64, _i32, _ptr, _i64, _i32, _ptr, _i64, _ptr, _i64, _i32, _i32, _i32, _i32,
          ctypes.c_float, _ptr],
     ),
     "mi_rms_norm": (_i32, [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i32, ctypes.c_float, _ptr]),

@@ -107,6 +107,12 @@ struct PrefillArgs {
   int32_t decode_rows;
   const int64_t* slot_mapping;
   int64_t slot_stride;
+  // Ragged chunk rows (a mixed step's chunks packed back to back): when set, the len_b real tokens
+  // of row b are flat tokens row_first[b] .. row_first[b] + len_b - 1 of query / key / value / out
+  // (the token strides apply, the row strides are unused; row_first[b] is clamped to
+  // [0, row_tokens - len_b]), and padding positions are neither read nor written.
+  const int64_t* row_first;
+  int64_t row_tokens;
 };
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -190,6 +196,20 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   len64 = len64 < 0 ? 0 : (len64 > L ? L : len64);
   const int pad = L - static_cast<int>(len64);
   start64 = start64 < 0 ? 0 : start64;
+  // Element offset of padded position rpad of row b (its first stored token): position i >= rpad
+  // of a tensor with row / token strides (r, t) is at base + (i - rpad) t.
+  const bool ragged = a.row_first != nullptr;  // uniform
+  if (ragged && len64 == 0) return;             // an empty ragged row stores nothing
+  int64_t first = 0;
+  if (ragged) {
+    first = a.row_first[b];
+    first = first < 0 ? 0 : (first > a.row_tokens - len64 ? a.row_tokens - len64 : first);
+  }
+  const int rpad = ragged ? pad : 0;
+  const int64_t q_base = ragged ? first * a.q_tok : b * a.q_row;
+  const int64_t k_base = ragged ? first * a.k_tok : b * a.k_row;
+  const int64_t v_base = ragged ? first * a.v_tok : b * a.v_row;
+  const int64_t o_base = ragged ? first * a.out_tok : b * a.out_row;
   const int64_t hist_cap = static_cast<int64_t>(a.max_history_blocks) * kBlockSize;
   const int nh = static_cast<int>(start64 < hist_cap ? start64 : hist_cap);
 
@@ -215,8 +235,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
     }
   }
 
-  uint16_t* out_b = a.out + b * a.out_row;
-  if (q0 + kQTile <= pad) {  // the whole tile is padding: zero rows
+  uint16_t* out_b = a.out + o_base;  // padded position rpad
+  if (q0 + kQTile <= pad) {  // the whole tile is padding: zero rows (a ragged row stores none)
+    if (ragged) return;
     for (int c = tid; c < kQTile * kGroup * (kHeadDim / 8); c += kThreads) {
       const int qi = q0 + c / (kGroup * (kHeadDim / 8));
       const int rem = c % (kGroup * (kHeadDim / 8));
@@ -238,7 +259,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       uint4 v = uint4{0, 0, 0, 0};
-      if (qi < L) v = *reinterpret_cast<const uint4*>(a.query + b * a.q_row + h * a.q_head + qi * a.q_tok + ks * 32 + gq * 8);
+      if (qi < L && qi >= rpad)
+        v = *reinterpret_cast<const uint4*>(a.query + q_base + h * a.q_head + (qi - rpad) * a.q_tok + ks * 32 + gq * 8);
       qf[nt][ks] = __builtin_bit_cast(bf16x8, v);
     }
   }
@@ -257,7 +279,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   // 16 different chunk positions, i.e. all banks.  In a history tile a wave's spans lie in one pool
   // block, whose id comes from the history table the workgroup staged in LDS; the id for tile t + 1
   // is read while tile t - 1 is computed, so no tile waits for that read.  Chunk rows past L - 1
-  // read row L - 1 (their keys are masked).
+  // read row L - 1, and a ragged row's padding rows its first stored row (their keys are masked).
   const int nhb = (nh + kBlockSize - 1) / kBlockSize;
   for (int i = tid; i < nhb; i += kThreads) {
     const int64_t x = a.history_blocks[b * a.history_stride + i];
@@ -267,8 +289,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
   constexpr int kSpansPerWave = kSpans / (kThreads / 64);
   const int drow = lane >> 4;
   const int dchunk = lane & 15;
-  const uint16_t* k_rows = a.key + b * a.k_row + g * a.k_head;
-  const uint16_t* v_rows = a.value + b * a.v_row + g * a.v_head;
+  const uint16_t* k_rows = a.key + k_base + g * a.k_head;  // padded position rpad
+  const uint16_t* v_rows = a.value + v_base + g * a.v_head;
   const uint32_t k_tok = static_cast<uint32_t>(a.k_tok);  // < 2^24, checked by the entry point
   const uint32_t v_tok = static_cast<uint32_t>(a.v_tok);
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -297,7 +319,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
         ksrc = a.key_pool + blk * kBlkElems + off;
         vsrc = a.value_pool + blk * kBlkElems + off;
       } else {
-        const uint32_t kc = static_cast<uint32_t>(min(key0 + r, L - 1));
+        const uint32_t kc = static_cast<uint32_t>(min(max(key0 + r, rpad), L - 1) - rpad);
         ksrc = k_rows + (__umul24(kc, k_tok) + c8);
         vsrc = v_rows + (__umul24(kc, v_tok) + c8);
       }
@@ -480,8 +502,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void chunked_prefill_kerne
     const float lt = oacc[8][nt][0];
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int qi = qw0 + 16 * nt + ql;
-    if (qi >= L || !head_live) continue;
-    uint16_t* orow = out_b + qi * a.out_tok + h * kHeadDim + 4 * gq;
+    if (qi >= L || qi < rpad || !head_live) continue;
+    uint16_t* orow = out_b + (qi - rpad) * a.out_tok + h * kHeadDim + 4 * gq;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       uint2 v;
@@ -624,15 +646,16 @@ extern "C" int32_t mi_mixed_paged_attention(
     void* out, int64_t out_tok_stride, const void* query, int64_t query_tok_stride, int64_t query_head_stride,
     const void* key, int64_t key_tok_stride, int64_t key_head_stride, const void* value, int64_t value_tok_stride,
     int64_t value_head_stride, void* key_pool, void* value_pool, int64_t num_blocks, int32_t prefill_rows,
-    int32_t prefill_width, const int64_t* history_blocks, int64_t history_stride, int32_t max_history_blocks,
-    const int64_t* start_lens, const int64_t* chunk_lens, int64_t lens_stride, int32_t decode_rows,
-    const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks, const int64_t* context_lens,
-    int64_t context_lens_stride, const int64_t* slot_mapping, int64_t slot_stride, int32_t num_heads,
-    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale, void* stream) {
+    int32_t prefill_width, int64_t chunk_tokens, const int64_t* chunk_first, const int64_t* history_blocks,
+    int64_t history_stride, int32_t max_history_blocks, const int64_t* start_lens, const int64_t* chunk_lens,
+    int64_t lens_stride, int32_t decode_rows, const int64_t* block_tables, int64_t block_table_stride,
+    int32_t max_blocks, const int64_t* context_lens, int64_t context_lens_stride, const int64_t* slot_mapping,
+    int64_t slot_stride, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+    void* stream) {
   using namespace mi;
   const char* name = "mi_mixed_paged_attention";
   if (prefill_rows < 0 || prefill_width < 0 || decode_rows < 0 || max_history_blocks < 0 || max_blocks < 0 ||
-      num_blocks < 0)
+      num_blocks < 0 || (chunk_first && chunk_tokens < 0))
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", name);
   const bool chunks = prefill_rows > 0 && prefill_width > 0;
   if (!chunks && decode_rows == 0) return ok();
@@ -660,8 +683,9 @@ extern "C" int32_t mi_mixed_paged_attention(
     return fail(MI_ERR_UNSUPPORTED, "%s: key/value token strides must be in [0, 2^24)", name);
   if (prefill_rows > 65535 || decode_rows > 65535) return fail(MI_ERR_UNSUPPORTED, "%s: more than 65535 rows", name);
 
-  // Chunk rows: tokens [0, P L), row b at token b L.  Decode rows: tokens [P L, P L + D), one each.
-  const int64_t n = chunks ? static_cast<int64_t>(prefill_rows) * prefill_width : 0;
+  // Chunk rows: tokens [0, P L), row b at token b L, or with chunk_first the ragged rows of tokens
+  // [0, chunk_tokens).  Decode rows: the D tokens after them, one each.
+  const int64_t n = chunk_first ? chunk_tokens : (chunks ? static_cast<int64_t>(prefill_rows) * prefill_width : 0);
   auto fill = [&](PrefillArgs& a, int64_t tok0, int64_t rows_tokens) {
     a.out = static_cast<uint16_t*>(out) + tok0 * out_tok_stride;
     a.out_row = rows_tokens * out_tok_stride;
@@ -692,6 +716,8 @@ extern "C" int32_t mi_mixed_paged_attention(
     a0.start_lens = start_lens;
     a0.chunk_lens = chunk_lens;
     a0.lens_stride = lens_stride;
+    a0.row_first = chunk_first;
+    a0.row_tokens = chunk_tokens;
   }
   if (decode_rows > 0) {
     a1 = rows_args(decode_rows, 1, num_heads, num_kv_heads, scale);

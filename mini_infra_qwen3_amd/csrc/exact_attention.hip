@@ -836,6 +836,12 @@ struct ExactPrefillArgs {
   int32_t decode_rows;
   const int64_t* slot_mapping;
   int64_t slot_stride;
+  // Ragged chunk rows (a mixed step's chunks packed back to back): when set, the clen real tokens
+  // of row b are flat tokens row_first[b] .. row_first[b] + clen - 1 of q / k / v / out (the token
+  // strides apply, the row strides are unused; row_first[b] is clamped to [0, row_tokens - clen]),
+  // and padding positions are neither read nor written.
+  const int64_t* row_first;
+  int64_t row_tokens;
 };
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
@@ -893,6 +899,20 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   const int i0 = qt * kQP;
   const int i_last = min(i0 + kQP - 1, L - 1);
   const int64_t row_elems = static_cast<int64_t>(a.kv_heads) * kHeadDim;
+  // Element offset of padded position rpad of row b (its first stored token): position i >= rpad
+  // of a tensor with row / token strides (r, t) is at base + (i - rpad) t.
+  const bool ragged = a.row_first != nullptr;  // uniform
+  if (ragged && clen == 0) return;              // an empty ragged row stores nothing
+  int64_t first = 0;
+  if (ragged) {
+    first = a.row_first[b];
+    first = first < 0 ? 0 : (first > a.row_tokens - clen ? a.row_tokens - clen : first);
+  }
+  const int rpad = ragged ? pad : 0;
+  const int64_t q_base = ragged ? first * a.q_tok : b * a.q_row;
+  const int64_t k_base = ragged ? first * a.k_tok : b * a.k_row;
+  const int64_t v_base = ragged ? first * a.v_tok : b * a.v_row;
+  const int64_t o_base = ragged ? first * a.out_tok : b * a.out_row;
 
   if (a.decode_rows && clen > 0 && threadIdx.x < 32) {  // append the token's K and V rows of KV head g
     const int64_t slot = a.slot_mapping[b * a.slot_stride];
@@ -904,7 +924,8 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
     }
   }
 
-  if (i_last < pad) {  // every query of the tile is padding: zero rows (uniform)
+  if (i_last < pad) {  // every query of the tile is padding: zero rows (uniform; a ragged row stores none)
+    if (ragged) return;
     const int col = threadIdx.x >> 4, piece = threadIdx.x & 15;
     const int i = i0 + col / kG;
     if (col < kCols && i < L)
@@ -924,8 +945,8 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   double qd[32];
   {
     const bool live = c < kCols && ci < L;
-    const int cq = min(ci, L - 1);  // unused columns read a real row and keep zeros
-    const uint16_t* qrow = a.q + b * a.q_row + (g * kG + c % kG) * a.q_head + static_cast<int64_t>(cq) * a.q_tok + 32 * q4;
+    const int cq = max(min(ci, L - 1), rpad);  // unused columns read a stored row and keep zeros
+    const uint16_t* qrow = a.q + q_base + (g * kG + c % kG) * a.q_head + static_cast<int64_t>(cq - rpad) * a.q_tok + 32 * q4;
     if (a.q_vec) {  // uniform
       u32x4 qv[4];
 #pragma unroll
@@ -946,9 +967,9 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
       if (id < 0 || id >= a.num_blocks) id = 0;
       return (values ? a.value_pool : a.key_pool) + (id * kBlockSize + kc % kBlockSize) * row_elems + g * kHeadDim;
     }
-    const int p = pad + (kc - nh);
-    return values ? a.v + b * a.v_row + g * a.v_head + static_cast<int64_t>(p) * a.v_tok
-                  : a.k + b * a.k_row + g * a.k_head + static_cast<int64_t>(p) * a.k_tok;
+    const int p = pad + (kc - nh) - rpad;  // from the row's first stored position
+    return values ? a.v + v_base + g * a.v_head + static_cast<int64_t>(p) * a.v_tok
+                  : a.k + k_base + g * a.k_head + static_cast<int64_t>(p) * a.k_tok;
   };
   // Scores of keys 16 kt + 4 q4 + r (r = 0..3) against column c.
   auto tile_scores = [&](int kt, float (&sc)[4]) {
@@ -1070,7 +1091,7 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
   for (int r = 0; r < 4; ++r) {
     const int col = q4 + 4 * r;
     const int i = i0 + col / kG;
-    if (col >= kCols || i >= L) continue;
+    if (col >= kCols || i >= L || i < rpad) continue;
     uint32_t word[4];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -1080,7 +1101,7 @@ __global__ __launch_bounds__(kPfThreads) void exact_prefill_kernel(const ExactPr
                         : static_cast<uint32_t>(bf16_bits(static_cast<float>(x0))) |
                               (static_cast<uint32_t>(bf16_bits(static_cast<float>(x1))) << 16);
     }
-    *reinterpret_cast<uint4*>(a.out + b * a.out_row + static_cast<int64_t>(i) * a.out_tok +
+    *reinterpret_cast<uint4*>(a.out + o_base + static_cast<int64_t>(i - rpad) * a.out_tok +
                               (g * kG + col % kG) * kHeadDim + 8 * c) = uint4{word[0], word[1], word[2], word[3]};
   }
 }
@@ -1416,15 +1437,16 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
     void* out, int64_t out_tok_stride, const void* query, int64_t query_tok_stride, int64_t query_head_stride,
     const void* key, int64_t key_tok_stride, int64_t key_head_stride, const void* value, int64_t value_tok_stride,
     int64_t value_head_stride, void* key_pool, void* value_pool, int64_t num_blocks, int32_t prefill_rows,
-    int32_t prefill_width, const int64_t* history_blocks, int64_t history_stride, int32_t max_history_blocks,
-    const int64_t* start_lens, const int64_t* chunk_lens, int64_t lens_stride, int32_t decode_rows,
-    const int64_t* block_tables, int64_t block_table_stride, int32_t max_blocks, const int64_t* context_lens,
-    int64_t context_lens_stride, const int64_t* slot_mapping, int64_t slot_stride, int32_t num_heads,
-    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale, void* stream) {
+    int32_t prefill_width, int64_t chunk_tokens, const int64_t* chunk_first, const int64_t* history_blocks,
+    int64_t history_stride, int32_t max_history_blocks, const int64_t* start_lens, const int64_t* chunk_lens,
+    int64_t lens_stride, int32_t decode_rows, const int64_t* block_tables, int64_t block_table_stride,
+    int32_t max_blocks, const int64_t* context_lens, int64_t context_lens_stride, const int64_t* slot_mapping,
+    int64_t slot_stride, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+    void* stream) {
   using namespace mi;
   const char* what = "mi_mixed_paged_attention_exact";
   if (prefill_rows < 0 || prefill_width < 0 || decode_rows < 0 || max_history_blocks < 0 || max_blocks < 0 ||
-      num_blocks < 0)
+      num_blocks < 0 || (chunk_first && chunk_tokens < 0))
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
   const bool chunks = prefill_rows > 0 && prefill_width > 0;
   if (!chunks && decode_rows == 0) return ok();
@@ -1450,8 +1472,9 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
   if (num_blocks > INT64_MAX / (kBlockSize * static_cast<int64_t>(num_kv_heads) * head_dim))
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: pool too large", what);
 
-  // Chunk rows: tokens [0, P L), row b at token b L.  Decode rows: tokens [P L, P L + D), one each.
-  const int64_t n = chunks ? static_cast<int64_t>(prefill_rows) * prefill_width : 0;
+  // Chunk rows: tokens [0, P L), row b at token b L, or with chunk_first the ragged rows of tokens
+  // [0, chunk_tokens).  Decode rows: the D tokens after them, one each.
+  const int64_t n = chunk_first ? chunk_tokens : (chunks ? static_cast<int64_t>(prefill_rows) * prefill_width : 0);
   auto fill = [&](ExactPrefillArgs& a, int64_t tok0, int64_t row_tokens) {
     a.out = static_cast<uint16_t*>(out) + tok0 * out_tok_stride;
     a.out_row = row_tokens * out_tok_stride;
@@ -1482,13 +1505,15 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
     a0.start_lens = start_lens;
     a0.chunk_lens = chunk_lens;
     a0.lens_stride = lens_stride;
+    a0.row_first = chunk_first;
+    a0.row_tokens = chunk_tokens;
     exact_rows(a0, prefill_rows, prefill_width, num_heads, num_kv_heads,
                static_cast<int64_t>(max_history_blocks) * kBlockSize + prefill_width, scale);
   } else {
     a0.kv_heads = num_kv_heads;
   }
-  // Decode rows: one-token chunks at tokens [P L, P L + D) whose history is the context minus the
-  // token (the block table), appending each row's rotated K/V to its slot.
+  // Decode rows: one-token chunks at the D tokens after the chunk rows, whose history is the
+  // context minus the token (the block table), appending each row's rotated K/V to its slot.
   const int group = num_heads / num_kv_heads;
   ExactPrefillArgs a1{};
   if (decode_rows > 0) {

@@ -542,14 +542,21 @@ def mixed_paged_attention(
     scale: float,
     out: torch.Tensor | None = None,
     exact: bool = False,
+    chunk_first: torch.Tensor | None = None,
+    chunk_tokens: int | None = None,
 ) -> torch.Tensor:
     """The attention of a mixed chunk + decode step in one launch (``mi_mixed_paged_attention``, or
     ``mi_mixed_paged_attention_exact`` with ``exact``), which also appends the decode tokens' K/V.
 
-    A flattened batch of T = P L + D tokens: query ``[T, H, D]``, key / value ``[T, H_kv, D]``
-    (token-major, D contiguous; the rotated q / k of ``qk_norm_rope``).  Tokens ``[0, P L)`` are P
-    left-padded chunks of width L with ``history_blocks`` ``[P, nb]`` (nb may be 0), ``start_lens``
-    / ``chunk_lens`` ``[P]`` as in ``chunked_prefill_attention``; the last D tokens are decode rows
+    A flattened batch of T = C + D tokens: query ``[T, H, D]``, key / value ``[T, H_kv, D]``
+    (token-major, D contiguous; the rotated q / k of ``qk_norm_rope``).  Tokens ``[0, C)`` are P
+    chunk rows with ``history_blocks`` ``[P, nb]`` (nb may be 0), ``start_lens`` / ``chunk_lens``
+    ``[P]`` as in ``chunked_prefill_attention``, each seen as a left-padded chunk of width L (at least
+    every chunk length).  Without ``chunk_first``, C = P L and row b is tokens ``[b L, b L + L)``;
+    with ``chunk_first`` ``[P]`` (ragged rows) C = ``chunk_tokens`` and row b's real tokens start at
+    token ``chunk_first[b]``, with no padding stored (the launch writes no row for a token outside
+    the rows; an ``out`` allocated here starts zeroed, so such tokens get zero rows).  The last D
+    tokens are decode rows
     with ``block_tables`` ``[D, mb]``, ``context_lens`` ``[D]`` (tokens including the new one) and
     ``slot_mapping`` ``[D]`` (where the new K/V go; -1: none).  Pools ``[num_blocks, block_size,
     H_kv, D]``, block_size 16 or a multiple.  Returns ``out`` ``[T, H * D]`` bf16.
@@ -571,8 +578,18 @@ def mixed_paged_attention(
     num_blocks, block_size, num_kv_heads, _ = key_pool.shape
     rows, width = int(prefill_rows), int(prefill_width)
     decode_rows = int(context_lens.shape[0])
-    if rows < 0 or width < 0 or tokens != rows * width + decode_rows:
-        raise ValueError(f"{tokens} tokens are not {rows} chunk rows x {width} + {decode_rows} decode rows")
+    if chunk_first is None:
+        if rows < 0 or width < 0 or tokens != rows * width + decode_rows:
+            raise ValueError(f"{tokens} tokens are not {rows} chunk rows x {width} + {decode_rows} decode rows")
+        chunk_tokens = rows * width
+    else:
+        _require_gpu("chunk_first", chunk_first, device)
+        _require_index("chunk_first", chunk_first, 1)
+        if chunk_tokens is None or rows < 0 or width < 0 or chunk_first.shape[0] != rows or \
+                tokens != int(chunk_tokens) + decode_rows:
+            raise ValueError(f"{tokens} tokens are not {chunk_tokens} ragged chunk tokens of {rows} rows + "
+                             f"{decode_rows} decode rows")
+        chunk_first = chunk_first.contiguous()
     if key.shape != (tokens, num_kv_heads, head_dim) or value.shape != key.shape:
         raise ValueError(f"key/value must be [{tokens}, {num_kv_heads}, {head_dim}]")
     if key_pool.dtype != torch.bfloat16 or value_pool.shape != key_pool.shape or not key_pool.is_contiguous() \
@@ -597,7 +614,8 @@ def mixed_paged_attention(
     lens_stride = start_lens.stride(0) if rows > 1 else 1
     nb, mb = history_blocks.shape[1], block_tables.shape[1]
     if out is None:
-        out = torch.empty((tokens, num_heads * head_dim), dtype=torch.bfloat16, device=device)
+        alloc = torch.zeros if chunk_first is not None else torch.empty
+        out = alloc((tokens, num_heads * head_dim), dtype=torch.bfloat16, device=device)
     elif out.shape != (tokens, num_heads * head_dim) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
         raise ValueError(f"out must be [T, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
     if tokens == 0:
@@ -609,7 +627,8 @@ def mixed_paged_attention(
         key.data_ptr(), key.stride(0), key.stride(1),
         value.data_ptr(), value.stride(0), value.stride(1),
         kp.data_ptr(), vp.data_ptr(), num_blocks,
-        rows, width, history_blocks.data_ptr() if nb and rows else None, history_blocks.stride(0) if nb else 0,
+        rows, width, int(chunk_tokens), chunk_first.data_ptr() if chunk_first is not None and rows else None,
+        history_blocks.data_ptr() if nb and rows else None, history_blocks.stride(0) if nb else 0,
         nb if rows else 0, start_lens.data_ptr() if rows else None, chunk_lens.data_ptr() if rows else None,
         lens_stride,
         decode_rows, block_tables.data_ptr() if mb and decode_rows else None, block_tables.stride(0) if mb else 0,

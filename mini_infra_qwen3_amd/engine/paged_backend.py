@@ -48,12 +48,14 @@ class PagedScheduleBackend:
     def __init__(self, model: torch.nn.Module, requests: Sequence[Request], max_running_requests: int,
                  paged_cache_config: PagedCacheConfig = PagedCacheConfig(), pad_token_id: int = 0,
                  decode_graphs: bool = False, prefill_graphs: bool = False, prefill_graph_rows: int = 4,
-                 mixed_graphs: bool = False, mixed_graph_rows: int = 2, mixed_graph_decode_rows: int = 32):
+                 mixed_graphs: bool = False, mixed_graph_rows: int = 3, mixed_graph_decode_rows: int = 32,
+                 mixed_graph_tokens: int | None = None):
         """``decode_graphs``: capture the decode forward in HIP graphs for every padded (batch, blocks)
         bucket this run can reach, before the run (as serving engines do at start-up).
         ``prefill_graphs``: likewise the chunked-prefill forward of up to ``prefill_graph_rows`` chunks,
         for widths up to the longest prompt and histories up to its blocks.  ``mixed_graphs``: the
-        mixed-step forward of up to ``mixed_graph_rows`` chunks with up to ``mixed_graph_decode_rows``
+        mixed-step forward of up to ``mixed_graph_rows`` chunks (at most ``mixed_graph_tokens`` chunk
+        tokens in all: the scheduler's token budget, or no cap) with up to ``mixed_graph_decode_rows``
         decode rows.  A model with reference numerics (``exact``) takes decode graphs per batch size,
         mixed graphs at the padded shapes it runs every mixed step at (``padded_mixed_shape``) and
         no prefill graphs (they pad the chunk width: ValueError)."""
@@ -81,6 +83,7 @@ class PagedScheduleBackend:
         if mixed_graphs:
             self.runner.enable_mixed_graphs(
                 self.pool, max_rows=min(mixed_graph_rows, max_running_requests), max_width=longest,
+                max_chunk_tokens=mixed_graph_tokens,
                 max_decode_rows=min(mixed_graph_decode_rows, max_running_requests, len(requests)),
                 max_history_blocks=num_blocks_for_tokens(longest, self.block_size), max_decode_blocks=largest)
         if prefill_graphs:

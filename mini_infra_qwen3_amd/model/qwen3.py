@@ -85,16 +85,27 @@ class PagedPrefillMetadata(NamedTuple):
 
 
 class PagedMixedMetadata(NamedTuple):
-    """A mixed chunk + decode step over a flattened ``[1, T]`` batch: tokens ``[0, P L)`` are
-    ``prefill_rows`` (P) left-padded chunks of ``prefill_width`` (L) tokens addressed by ``prefill``;
-    the last ``T - P L`` tokens are one new token per decoding sequence, addressed by ``decode``.
-    ``prefill.kv_out`` (optional) holds per-layer ``[T, H_kv, D]`` buffers for all T tokens' K/V."""
+    """A mixed chunk + decode step over a flattened ``[1, T]`` batch, T = C + D: tokens ``[0, C)``
+    are the ``prefill_rows`` (P) chunk rows addressed by ``prefill``, the last D tokens one new token
+    per decoding sequence, addressed by ``decode``.  With ``chunk_first`` (``[P]``, ragged rows) row
+    b's tokens are tokens ``chunk_first[b]`` .. of ``[0, chunk_tokens)`` (pad tokens may follow the
+    rows), and the attention sees each row left-padded to ``prefill_width`` (at least every chunk
+    length).  Without it, C = P L with L = ``prefill_width``: row b is tokens ``[b L, b L + L)``,
+    left-padded.  ``prefill.kv_out`` (optional) holds per-layer ``[T, H_kv, D]`` buffers for all T
+    tokens' K/V."""
 
     prefill: PagedPrefillMetadata
     decode: PagedAttentionMetadata
     prefill_rows: int
     prefill_width: int
     kv_pools: tuple[PastKeyValue, ...] = ()
+    chunk_first: torch.Tensor | None = None
+    chunk_tokens: int = 0
+
+    @property
+    def chunk_span(self) -> int:
+        """C: the tokens of the chunk rows (ragged or padded)."""
+        return self.chunk_tokens if self.chunk_first is not None else self.prefill_rows * self.prefill_width
 
 
 class RMSNorm(nn.Module):
@@ -208,11 +219,13 @@ class Qwen3Attention(nn.Module):
 
     def _mixed(self, q, k, v, cos, sin, kv_pool: PastKeyValue, metadata: PagedMixedMetadata, workspace, kv_out=None):
         """One q/k norm + RoPE launch over all T tokens, then one attention launch for the chunk rows
-        (tokens ``[0, P L)``) and the decode rows (the rest), which also appends the decode tokens'
-        K/V to the pool.  ``kv_out`` (optional): ``[T, H_kv, D]`` buffers for the rotated K / V."""
+        (tokens ``[0, C)``) and the decode rows (the rest), which also appends the decode tokens'
+        K/V to the pool.  ``kv_out`` (optional): ``[T, H_kv, D]`` buffers for the rotated K / V.  The
+        chunk K/V come back as ``[P, H_kv, L, D]`` rows, or for ragged rows as one ``[1, H_kv, C, D]``
+        row."""
         key_pool, value_pool = kv_pool
         rows, width = metadata.prefill_rows, metadata.prefill_width
-        n = rows * width
+        n = metadata.chunk_span
         k_buf, v_buf = kv_out if kv_out is not None else (None, None)
         q_rot, k_rot, v_rows = data_plane.qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin,
                                                        self.q_norm.eps, k_out=k_buf, v_out=v_buf)
@@ -220,9 +233,10 @@ class Qwen3Attention(nn.Module):
         out = data_plane.mixed_paged_attention(
             q_rot, k_rot, v_rows, key_pool, value_pool, rows, width, prefill.history_block_tables, prefill.start_lens,
             prefill.chunk_lens, decode.block_tables, decode.context_lens, decode.slot_mapping, self.scaling,
-            exact=self.exact)
-        k_chunk = k_rot[:n].view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
-        v_chunk = v_rows[:n].view(rows, width, self.num_kv_heads, self.head_dim).transpose(1, 2)
+            exact=self.exact, chunk_first=metadata.chunk_first, chunk_tokens=n)
+        per_row = (1, n) if metadata.chunk_first is not None else (rows, width)
+        k_chunk = k_rot[:n].view(*per_row, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        v_chunk = v_rows[:n].view(*per_row, self.num_kv_heads, self.head_dim).transpose(1, 2)
         return self.o_proj(out.unsqueeze(0)), (k_chunk, v_chunk)
 
 
@@ -296,10 +310,10 @@ class Qwen3Model(nn.Module):
         if isinstance(attn_metadata, PagedMixedMetadata):
             metadata = attn_metadata
             pools = metadata.kv_pools
-            rows, width = metadata.prefill_rows, metadata.prefill_width
+            rows = metadata.prefill_rows
             decode_rows = metadata.decode.slot_mapping.shape[0]
-            if batch != 1 or length != rows * width + decode_rows or rows < 1 or decode_rows < 1:
-                raise ValueError(f"mixed step takes input_ids [1, P * L + D] with P, D >= 1, got {tuple(input_ids.shape)}")
+            if batch != 1 or length != metadata.chunk_span + decode_rows or rows < 1 or decode_rows < 1:
+                raise ValueError(f"mixed step takes input_ids [1, C + D] with P, D >= 1, got {tuple(input_ids.shape)}")
             if position_ids is None:
                 raise ValueError("a mixed step needs position_ids")
             if len(pools) != len(self.layers):
@@ -361,9 +375,18 @@ class Qwen3Model(nn.Module):
             hidden, residual, present = layer(hidden, residual, cos, sin, kv_pool, metadata, workspace, kv_out)
             presents.append(present)
         if last_only and isinstance(metadata, PagedMixedMetadata):
-            width, n = metadata.prefill_width, metadata.prefill_rows * metadata.prefill_width
-            hidden = torch.cat((hidden[0, width - 1:n:width], hidden[0, n:])).unsqueeze(1)
-            residual = torch.cat((residual[0, width - 1:n:width], residual[0, n:])).unsqueeze(1)
+            n = metadata.chunk_span
+            if metadata.chunk_first is not None:  # each ragged row's last token
+                # clamped like the attention clamps a row's first token: a row of length 0 (the
+                # zero-filled buffer a mixed graph is captured over) reads token 0, and no sampler
+                # reads its logit
+                last = (metadata.chunk_first + metadata.prefill.chunk_lens - 1).clamp(0, max(n - 1, 0))
+                hidden = torch.cat((hidden[0].index_select(0, last), hidden[0, n:])).unsqueeze(1)
+                residual = torch.cat((residual[0].index_select(0, last), residual[0, n:])).unsqueeze(1)
+            else:
+                width = metadata.prefill_width
+                hidden = torch.cat((hidden[0, width - 1:n:width], hidden[0, n:])).unsqueeze(1)
+                residual = torch.cat((residual[0, width - 1:n:width], residual[0, n:])).unsqueeze(1)
         elif last_only:  # the norm is row-wise: only the position the sampler reads
             hidden, residual = hidden[:, -1:, :], residual[:, -1:, :]
         return self.norm(hidden, residual)[0], presents

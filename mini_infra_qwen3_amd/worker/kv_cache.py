@@ -18,6 +18,9 @@ class KVCache:
         # the forward already wrote into the pool, or None; a store with the same index has nothing
         # left to do.
         self.written_index = None
+        # Not in the reference: for the chunk K/V of a mixed step with ragged rows (one cached row of
+        # all the step's chunk tokens), the first token of each chunk row; None otherwise.
+        self.ragged_first = None
 
     @property
     def past_key_values(self) -> list[tuple[torch.Tensor, torch.Tensor]]:

@@ -60,11 +60,14 @@ def pack_decode_rows(block_tables: Sequence[Sequence[int]], last_tokens: Sequenc
 
 
 def prefill_scatter_indices(block_tables: Sequence[Sequence[int]], chunk_lens: Sequence[int],
-                            start_positions: Sequence[int], padded_length: int, block_size: int) -> np.ndarray:
+                            start_positions: Sequence[int], padded_length: int, block_size: int,
+                            row_first: Sequence[int] | None = None) -> np.ndarray:
     """``[3, N]`` (token_rows, token_positions, slots) of the valid chunk tokens, row-major.
 
     Token t of row i sits at padded position ``padded_length - chunk_lens[i] + t`` and goes to
     logical position ``start_positions[i] + t`` (src/mini_infra/worker/paged_runner.py:118-128).
+    With ``row_first`` (ragged rows, all in one cached row): token t of row i sits at position
+    ``row_first[i] + t`` of row 0.
     """
     lens = np.asarray(chunk_lens, dtype=np.int64)
     starts = np.asarray(start_positions, dtype=np.int64)
@@ -80,9 +83,13 @@ def prefill_scatter_indices(block_tables: Sequence[Sequence[int]], chunk_lens: S
     covered = np.array([len(t) for t in block_tables], dtype=np.int64)
     if np.any(logical // block_size >= covered[rows]):
         raise ValueError("a block table does not cover its chunk")
-    out[0] = rows
-    out[1] = padded_length - np.repeat(lens, lens) + offsets
     out[2] = tables[rows, logical // block_size] * block_size + logical % block_size
+    if row_first is None:
+        out[0] = rows
+        out[1] = padded_length - np.repeat(lens, lens) + offsets
+    else:
+        out[0] = 0
+        out[1] = np.repeat(np.asarray(row_first, dtype=np.int64), lens) + offsets
     return out
 
 
@@ -139,43 +146,65 @@ def pack_prefill_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions:
 MIXED_WIDTH_QUANTUM = 128  # chunk width step of a padded mixed step
 
 
-def padded_mixed_shape(width: int, decode_rows: int, quantum: int = MIXED_WIDTH_QUANTUM) -> tuple[int, int]:
-    """The (chunk width, decode rows) a mixed step with reference numerics runs at: the longest
-    chunk rounded up to a multiple of ``quantum``, the decode rows up to a power of two (none stays
-    none).  The reference plans mixed steps but does not define them
-    (src/mini_infra/core/scheduler.py:310-311); their GEMMs run over all P L + D rows, and a GEMM's
-    rows can round differently at another M.  With L and D on these steps every step shape is one of
+def padded_mixed_shape(chunk_tokens: int, decode_rows: int, quantum: int = MIXED_WIDTH_QUANTUM) -> tuple[int, int]:
+    """The (chunk tokens, decode rows) a mixed step with reference numerics runs at: its chunks'
+    tokens rounded up to a multiple of ``quantum``, the decode rows up to a power of two (none
+    stays none).  The reference plans mixed steps but does not define them
+    (src/mini_infra/core/scheduler.py:310-311); their GEMMs run over all C + D rows, and a GEMM's
+    rows can round differently at another M.  With C and D on these steps every step shape is one of
     a few buckets, each of which a HIP graph replays with the same GEMM calls, and so the same bits,
     as the eager forward of that shape."""
-    if width <= 0 or decode_rows < 0 or quantum <= 0:
-        raise ValueError(f"bad mixed step shape: width {width}, decode rows {decode_rows}, quantum {quantum}")
-    return -(-width // quantum) * quantum, (1 << (decode_rows - 1).bit_length()) if decode_rows else 0
+    if chunk_tokens <= 0 or decode_rows < 0 or quantum <= 0:
+        raise ValueError(f"bad mixed step shape: {chunk_tokens} chunk tokens, decode rows {decode_rows}, "
+                         f"quantum {quantum}")
+    return -(-chunk_tokens // quantum) * quantum, (1 << (decode_rows - 1).bit_length()) if decode_rows else 0
 
 
 def pack_mixed_rows(chunk_token_ids: Sequence[Sequence[int]], start_positions: Sequence[int],
                     prefill_tables: Sequence[Sequence[int]], last_tokens: Sequence[int], positions: Sequence[int],
                     decode_tables: Sequence[Sequence[int]], block_size: int, pad_token_id: int,
-                    width: int | None = None, history_blocks: int | None = None, decode_rows: int | None = None,
+                    chunk_tokens: int | None = None, history_blocks: int | None = None,
+                    decode_rows: int | None = None,
                     decode_blocks: int | None = None) -> tuple[np.ndarray, tuple[int, int, int, int, int]]:
     """One int64 buffer for a mixed chunk + decode step, uploaded at once.
 
-    Layout (T = P L + D): tokens ``[T]`` | positions ``[T]`` | per chunk row (start, length,
-    history table) ``[P, 2 + nb]`` | per decode row (slot, context length, block table)
-    ``[D, 2 + mb]``.  The first P L tokens / positions are the chunks left-padded to L, row-major,
-    as ``pack_prefill_rows`` lays them out; the last D are the decode tokens of ``pack_decode_rows``.
-    The optional sizes fix L, nb, D and mb for a padded bucket (see the two packers).
-    Returns the buffer and (P, L, nb, D, mb).
+    Layout (T = C + D): tokens ``[T]`` | positions ``[T]`` | per chunk row (start, length, first
+    token, history table) ``[P, 3 + nb]`` | per decode row (slot, context length, block table)
+    ``[D, 2 + mb]``.  The first C tokens are the chunks back to back (ragged rows: row b's tokens
+    from token ``first``, at logical positions start ..), then pad tokens (position 0) up to C; the
+    last D are the decode tokens of ``pack_decode_rows``.  History tables are the first
+    ``ceil(start / block_size)`` entries of each table, null-padded, as ``pack_prefill_rows`` takes
+    them.  The optional sizes fix C, nb, D and mb for a padded bucket.  Returns the buffer and
+    (P, C, nb, D, mb).
     """
-    prefill = pack_prefill_rows(chunk_token_ids, start_positions, prefill_tables, block_size, pad_token_id,
-                                width=width, history_blocks=history_blocks)
+    lens = [len(ids) for ids in chunk_token_ids]
+    if not lens or min(lens) < 1:
+        raise ValueError("every chunk must hold at least one token")
+    hist = [-(-s // block_size) for s in start_positions]
+    total = sum(lens)
+    chunk_tokens = total if chunk_tokens is None else chunk_tokens
+    nb = max(hist) if history_blocks is None else history_blocks
+    if chunk_tokens < total or nb < max(hist):
+        raise ValueError(f"{total} chunk tokens / {max(hist)} history blocks do not fit {chunk_tokens} / {nb}")
     decode = pack_decode_rows(decode_tables, last_tokens, positions, block_size, rows=decode_rows,
                               blocks=decode_blocks)
-    rows = prefill.shape[0]
-    width = max(len(ids) for ids in chunk_token_ids) if width is None else width
-    nb = prefill.shape[1] - 2 * width - 2
-    flat = np.concatenate([prefill[:, :width].ravel(), decode[:, 0], prefill[:, width:2 * width].ravel(), decode[:, 1],
-                           prefill[:, 2 * width:].ravel(), decode[:, 2:].ravel()])
-    return flat, (rows, width, nb, decode.shape[0], decode.shape[1] - 4)
+    rows = len(lens)
+    ids = np.full(chunk_tokens, pad_token_id, dtype=np.int64)
+    pos = np.zeros(chunk_tokens, dtype=np.int64)
+    meta = np.zeros((rows, 3 + nb), dtype=np.int64)
+    first = 0
+    for row, (toks, n, start, table, h) in enumerate(zip(chunk_token_ids, lens, start_positions, prefill_tables,
+                                                         hist)):
+        ids[first:first + n] = np.asarray(toks, dtype=np.int64)
+        pos[first:first + n] = np.arange(start, start + n, dtype=np.int64)
+        meta[row, :3] = (start, n, first)
+        if h:
+            if len(table) < h:
+                raise ValueError("a block table does not cover its history")
+            meta[row, 3:3 + h] = np.asarray(table[:h], dtype=np.int64)
+        first += n
+    flat = np.concatenate([ids, decode[:, 0], pos, decode[:, 1], meta.ravel(), decode[:, 2:].ravel()])
+    return flat, (rows, chunk_tokens, nb, decode.shape[0], decode.shape[1] - 4)
 
 
 __all__ = ["MIXED_WIDTH_QUANTUM", "pack_decode_rows", "pack_mixed_rows", "pack_prefill_rows", "padded_mixed_shape",

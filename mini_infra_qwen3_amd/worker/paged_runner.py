@@ -142,18 +142,20 @@ class _PrefillGraph:
 
 
 class _MixedGraph:
-    """A mixed step's forward for one (chunk rows P, padded width W, decode rows D) bucket, with
+    """A mixed step's forward for one (chunk rows P, chunk tokens C, decode rows D) bucket, with
     history tables NB and decode tables MB blocks wide, captured over a static buffer in the
-    ``pack_mixed_rows`` layout; the step's K/V (chunk and decode tokens) go to the shared staging
-    buffers.  Pad decode rows carry slot -1 (no append) and context 0 (zero output)."""
+    ``pack_mixed_rows`` layout (ragged chunk rows); the attention sees each chunk row left-padded
+    to ``width``, the longest chunk the graph serves (query tiles wholly in a row's padding exit at
+    once).  The step's K/V (chunk and decode tokens) go to the shared staging buffers.  Pad decode
+    rows carry slot -1 (no append) and context 0 (zero output); pad chunk tokens belong to no row."""
 
-    def __init__(self, model: torch.nn.Module, pool: PagedKVCachePool, rows: int, width: int, decode_rows: int,
-                 hist_blocks: int, decode_blocks: int, staging: torch.Tensor, mempool, pad_token_id: int,
-                 device: torch.device):
-        self.rows, self.width, self.decode_rows = rows, width, decode_rows
+    def __init__(self, model: torch.nn.Module, pool: PagedKVCachePool, rows: int, chunk_tokens: int, width: int,
+                 decode_rows: int, hist_blocks: int, decode_blocks: int, staging: torch.Tensor, mempool,
+                 pad_token_id: int, device: torch.device):
+        self.rows, self.chunk_tokens, self.width, self.decode_rows = rows, chunk_tokens, width, decode_rows
         self.hist_blocks, self.decode_blocks = hist_blocks, decode_blocks
         self.pad_token_id = pad_token_id
-        self.tokens = rows * width + decode_rows
+        self.tokens = chunk_tokens + decode_rows
         self.static = torch.from_numpy(self._empty()).to(device)
         ids, pos, meta = self.views()
         t = self.tokens
@@ -174,25 +176,25 @@ class _MixedGraph:
         self.static_slots_ptr = self.views()[2].decode.slot_mapping.data_ptr()
 
     def _empty(self) -> np.ndarray:
-        t, n = self.tokens, self.rows * self.width
-        full = np.zeros(2 * t + self.rows * (2 + self.hist_blocks) + self.decode_rows * (2 + self.decode_blocks),
+        t = self.tokens
+        full = np.zeros(2 * t + self.rows * (3 + self.hist_blocks) + self.decode_rows * (2 + self.decode_blocks),
                         dtype=np.int64)
-        full[:n] = self.pad_token_id
-        full[n:t] = self.pad_token_id
-        dec = full[2 * t + self.rows * (2 + self.hist_blocks):].reshape(self.decode_rows, 2 + self.decode_blocks)
+        full[:t] = self.pad_token_id  # chunk rows of length 0: nothing to attend or store
+        dec = full[2 * t + self.rows * (3 + self.hist_blocks):].reshape(self.decode_rows, 2 + self.decode_blocks)
         dec[:, 0] = -1
         return full
 
     def views(self):
         s, t = self.static, self.tokens
-        at = 2 * t + self.rows * (2 + self.hist_blocks)
-        chunk = s[2 * t:at].view(self.rows, 2 + self.hist_blocks)
+        at = 2 * t + self.rows * (3 + self.hist_blocks)
+        chunk = s[2 * t:at].view(self.rows, 3 + self.hist_blocks)
         dec = s[at:].view(self.decode_rows, 2 + self.decode_blocks)
         meta = PagedMixedMetadata(
-            prefill=PagedPrefillMetadata(history_block_tables=chunk[:, 2:], start_lens=chunk[:, 0],
+            prefill=PagedPrefillMetadata(history_block_tables=chunk[:, 3:], start_lens=chunk[:, 0],
                                          chunk_lens=chunk[:, 1]),
             decode=PagedAttentionMetadata(slot_mapping=dec[:, 0], block_tables=dec[:, 2:], context_lens=dec[:, 1]),
-            prefill_rows=self.rows, prefill_width=self.width)
+            prefill_rows=self.rows, prefill_width=self.width, chunk_first=chunk[:, 2],
+            chunk_tokens=self.chunk_tokens)
         return s[:t].view(1, t), s[t:2 * t].view(1, t), meta
 
     def load(self, flat: np.ndarray) -> None:
@@ -236,6 +238,8 @@ class PagedRunner(BaseModelRunner):
         self._mixed_pool: PagedKVCachePool | None = None
         self._mixed_loaded: tuple[_MixedGraph, int] | None = None
         self._mixed_eager: tuple[int, int] | None = None  # (slot buffer address, live decode rows)
+        self._mixed_first: list[int] = []  # first token of each chunk row of the last prepared mixed step
+        self._mixed_width = 0
         self._decode_row_buckets: list[int] = []
         self._staging: torch.Tensor | None = None
         self._mempool = None
@@ -307,15 +311,18 @@ class PagedRunner(BaseModelRunner):
 
     def enable_mixed_graphs(self, pool: PagedKVCachePool, max_rows: int, max_width: int, max_decode_rows: int,
                             max_history_blocks: int, max_decode_blocks: int, width_quantum: int = MIXED_WIDTH_QUANTUM,
-                            decode_row_buckets: Sequence[int] | None = None) -> None:
-        """Captures the mixed-step forward for 1..``max_rows`` chunk rows, padded widths in multiples of
-        ``width_quantum`` up to ``max_width`` and decode-row buckets up to ``max_decode_rows`` (pad
-        rows append nothing), with history / decode tables ``max_history_blocks`` /
-        ``max_decode_blocks`` wide, over ``pool``.  Other steps run without a graph; as with prefill
-        graphs, store a step's ``prefill_cache`` before the next graphed step.  A model with
-        reference numerics runs every mixed step at ``padded_mixed_shape`` (graphed or not), so its
-        buckets are exactly those shapes: width quantum ``MIXED_WIDTH_QUANTUM`` and power-of-two
-        decode rows."""
+                            decode_row_buckets: Sequence[int] | None = None,
+                            max_chunk_tokens: int | None = None) -> None:
+        """Captures the mixed-step forward for 1..``max_rows`` chunk rows of at most ``max_width``
+        tokens each, chunk tokens (ragged rows, back to back) in multiples of ``width_quantum`` up to
+        the rows times ``max_width`` (capped at ``max_chunk_tokens``) rounded up, and decode-row
+        buckets up to
+        ``max_decode_rows`` (pad rows append nothing), with history / decode tables
+        ``max_history_blocks`` / ``max_decode_blocks`` wide, over ``pool``.  Other steps run without a
+        graph; as with prefill graphs, store a step's ``prefill_cache`` before the next graphed step.
+        A model with reference numerics runs every mixed step at ``padded_mixed_shape`` (graphed or
+        not), so its buckets are exactly those shapes: chunk-token quantum ``MIXED_WIDTH_QUANTUM`` and
+        power-of-two decode rows."""
         if self.device.type != "cuda":
             raise RuntimeError("mixed graphs need the GPU")
         exact = getattr(self.model, "exact", False)
@@ -327,21 +334,26 @@ class PagedRunner(BaseModelRunner):
                 decode_row_buckets.append(max_decode_rows)
         if exact and (width_quantum != MIXED_WIDTH_QUANTUM or
                       any(int(b) & (int(b) - 1) for b in decode_row_buckets if int(b) > 0)):
-            raise ValueError(f"a model with reference numerics runs mixed steps at width multiples of "
+            raise ValueError(f"a model with reference numerics runs mixed steps at chunk-token multiples of "
                              f"{MIXED_WIDTH_QUANTUM} and power-of-two decode rows; its graphs must use those buckets")
         self._decode_row_buckets = sorted(set(int(b) for b in decode_row_buckets if 0 < b <= max_decode_rows))
-        top_w = -(-max_width // width_quantum) * width_quantum
-        staging = self._shared_staging(max_rows * top_w + max(self._decode_row_buckets, default=0), pool)
+        def top(rows: int) -> int:
+            tokens = rows * max_width if max_chunk_tokens is None else min(rows * max_width, max_chunk_tokens)
+            return -(-tokens // width_quantum) * width_quantum
+
+        top_c = top(max_rows)
+        staging = self._shared_staging(top_c + max(self._decode_row_buckets, default=0), pool)
         self._mixed_pool = pool
         self._mixed_quantum = width_quantum
+        self._mixed_width = int(max_width)
         self._mixed_tables = (max(int(max_history_blocks), 0), max(int(max_decode_blocks), 1))
         self._mixed_graphs = {}
         for rows in range(1, max_rows + 1):
-            for width in range(width_quantum, top_w + 1, width_quantum):
+            for c in range(width_quantum, top(rows) + 1, width_quantum):
                 for d in self._decode_row_buckets:
-                    self._mixed_graphs[(rows, width, d)] = _MixedGraph(
-                        self.model, pool, rows, width, d, *self._mixed_tables, staging, self._mempool,
-                        self.pad_token_id, self.device)
+                    self._mixed_graphs[(rows, c, d)] = _MixedGraph(
+                        self.model, pool, rows, c, self._mixed_width, d, *self._mixed_tables, staging,
+                        self._mempool, self.pad_token_id, self.device)
         torch.cuda.synchronize(self.device)
 
     def _refuse_padded_graphs(self, kind: str) -> None:
@@ -349,13 +361,14 @@ class PagedRunner(BaseModelRunner):
             raise ValueError(f"{kind} graphs pad the chunk width, which changes the GEMMs' M and with it the bits of "
                              "their rows: a model with reference numerics (exact) runs these steps without graphs")
 
-    def _mixed_bucket(self, rows: int, width: int, hist_blocks: int, decode_rows: int,
+    def _mixed_bucket(self, rows: int, width: int, chunk_tokens: int, hist_blocks: int, decode_rows: int,
                       decode_blocks: int) -> _MixedGraph | None:
-        if not self._mixed_graphs or hist_blocks > self._mixed_tables[0] or decode_blocks > self._mixed_tables[1]:
+        if not self._mixed_graphs or hist_blocks > self._mixed_tables[0] or decode_blocks > self._mixed_tables[1] \
+                or width > self._mixed_width:
             return None
         d = next((b for b in self._decode_row_buckets if b >= decode_rows), None)
-        w = -(-width // self._mixed_quantum) * self._mixed_quantum
-        return None if d is None else self._mixed_graphs.get((rows, w, d))
+        c = -(-chunk_tokens // self._mixed_quantum) * self._mixed_quantum
+        return None if d is None else self._mixed_graphs.get((rows, c, d))
 
     def _prefill_bucket(self, rows: int, width: int, blocks: int) -> _PrefillGraph | None:
         if blocks > self._hist_blocks:
@@ -439,7 +452,7 @@ class PagedRunner(BaseModelRunner):
         """Writes each row's last ``chunk_lens[i]`` cached tokens to logical positions
         ``start_positions[i]..`` of its block table (reference paged_runner.py:104-136); no sync."""
         index = prefill_scatter_indices(block_tables, chunk_lens, start_positions, prefill_cache.length,
-                                        pool.block_size)
+                                        pool.block_size, row_first=getattr(prefill_cache, "ragged_first", None))
         if index.shape[1] == 0:
             return
         written = getattr(prefill_cache, "written_index", None)
@@ -549,41 +562,44 @@ class PagedRunner(BaseModelRunner):
         self._mixed_loaded = None
         self._mixed_eager = None
         live = len(decode_block_tables)
-        width = max(len(c) for c in chunk_token_ids)
+        lens = [len(c) for c in chunk_token_ids]
+        width, total = max(lens), sum(lens)
+        self._mixed_first = [int(x) for x in np.cumsum([0] + lens[:-1])]
         exact = getattr(self.model, "exact", False)
-        pad_width, pad_rows = padded_mixed_shape(width, live) if exact else (None, None)
+        pad_chunk, pad_rows = padded_mixed_shape(total, live) if exact else (None, None)
         if self._mixed_graphs and pool is self._mixed_pool:
             hist = max(-(-st // pool.block_size) for st in start_positions)
-            graph = self._mixed_bucket(len(chunk_token_ids), width, hist, live,
+            graph = self._mixed_bucket(len(chunk_token_ids), width, total, hist, live,
                                        max((len(t) for t in decode_block_tables), default=0))
-            if graph is not None and exact and (graph.width, graph.decode_rows) != (pad_width, pad_rows):
+            if graph is not None and exact and (graph.chunk_tokens, graph.decode_rows) != (pad_chunk, pad_rows):
                 graph = None  # not this step's shape (the eager forward below runs it)
             if graph is not None:
                 flat, _ = pack_mixed_rows(chunk_token_ids, start_positions, prefill_block_tables, last_tokens, positions,
-                                          decode_block_tables, pool.block_size, self.pad_token_id, width=graph.width,
-                                          history_blocks=graph.hist_blocks, decode_rows=graph.decode_rows,
-                                          decode_blocks=graph.decode_blocks)
+                                          decode_block_tables, pool.block_size, self.pad_token_id,
+                                          chunk_tokens=graph.chunk_tokens, history_blocks=graph.hist_blocks,
+                                          decode_rows=graph.decode_rows, decode_blocks=graph.decode_blocks)
                 graph.load(flat)
                 self._mixed_loaded = (graph, live)
                 ids, pos, meta = graph.views()
                 return ids, pos, meta._replace(kv_pools=tuple(pool.kv_pools))
-        flat, (rows, width, nb, decode_rows, mb) = pack_mixed_rows(
+        flat, (rows, chunk_tokens, nb, decode_rows, mb) = pack_mixed_rows(
             chunk_token_ids, start_positions, prefill_block_tables, last_tokens, positions, decode_block_tables,
-            pool.block_size, self.pad_token_id, width=pad_width, decode_rows=pad_rows)
+            pool.block_size, self.pad_token_id, chunk_tokens=pad_chunk, decode_rows=pad_rows)
         packed = torch.from_numpy(flat).to(self.device)
-        tokens = rows * width + decode_rows
+        tokens = chunk_tokens + decode_rows
         at = 2 * tokens
-        chunk = packed[at:at + rows * (2 + nb)].view(rows, 2 + nb)
-        at += rows * (2 + nb)
+        chunk = packed[at:at + rows * (3 + nb)].view(rows, 3 + nb)
+        at += rows * (3 + nb)
         dec = packed[at:].view(decode_rows, 2 + mb)
         self._mixed_eager = (dec.data_ptr(), live)
         pools = tuple(pool.kv_pools)
         metadata = PagedMixedMetadata(
-            prefill=PagedPrefillMetadata(history_block_tables=chunk[:, 2:], start_lens=chunk[:, 0],
+            prefill=PagedPrefillMetadata(history_block_tables=chunk[:, 3:], start_lens=chunk[:, 0],
                                          chunk_lens=chunk[:, 1], kv_pools=pools),
             decode=PagedAttentionMetadata(slot_mapping=dec[:, 0], block_tables=dec[:, 2:], context_lens=dec[:, 1],
                                           kv_pools=pools),
-            prefill_rows=rows, prefill_width=width, kv_pools=pools)
+            prefill_rows=rows, prefill_width=width, kv_pools=pools, chunk_first=chunk[:, 2],
+            chunk_tokens=chunk_tokens)
         return packed[:tokens].view(1, tokens), packed[tokens:2 * tokens].view(1, tokens), metadata
 
     def run_mixed_step(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
@@ -598,8 +614,8 @@ class PagedRunner(BaseModelRunner):
                 graph.graph.replay()
                 next_token = argmax_rows(graph.logits)
             tokens = next_token.tolist()
-            return MixedStepOutput(tokens[:graph.rows], tokens[graph.rows:graph.rows + live], KVCache(graph.presents),
-                                   timer.elapsed_ms)
+            return MixedStepOutput(tokens[:graph.rows], tokens[graph.rows:graph.rows + live],
+                                   self._ragged_cache(graph.presents), timer.elapsed_ms)
         with StepTimer(self.device) as timer:
             logits, present = self.model(input_ids, position_ids=position_ids, attn_metadata=metadata,
                                          last_logits_only=True)
@@ -610,7 +626,15 @@ class PagedRunner(BaseModelRunner):
         eager = self._mixed_eager
         if eager is not None and metadata.decode.slot_mapping.data_ptr() == eager[0]:
             live = eager[1]  # inputs from prepare_mixed_inputs, padded to the step's shape
-        return MixedStepOutput(tokens[:rows], tokens[rows:rows + live], KVCache(present), timer.elapsed_ms)
+        cache = self._ragged_cache(present) if metadata.chunk_first is not None else KVCache(present)
+        return MixedStepOutput(tokens[:rows], tokens[rows:rows + live], cache, timer.elapsed_ms)
+
+    def _ragged_cache(self, present) -> KVCache:
+        """The chunk K/V of a ragged mixed step (one cached row of all chunk tokens), with the first
+        token of each chunk row for ``store_prefill``."""
+        cache = KVCache(present)
+        cache.ragged_first = self._mixed_first
+        return cache
 
 
 __all__ = ["MixedStepOutput", "PagedDecodeOutput", "PagedRunner"]

@@ -194,38 +194,43 @@ def decode_step(model: ReferenceQwen3, block_tables, last_tokens, positions, poo
 
 
 def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, chunk_tables, last_tokens, positions,
-                      decode_tables, pools, block_size, pad_token_id: int = 0, width: int | None = None,
+                      decode_tables, pools, block_size, pad_token_id: int = 0, chunk_tokens: int | None = None,
                       decode_rows: int | None = None):
     """A mixed step -- prompt chunks and decode tokens in one forward, the batching the reference
     plans next (src/mini_infra/core/scheduler.py:310-311) and does not define -- as the reference's
-    ops over one flattened ``[1, P L + D]`` batch: P chunks left-padded to the longest (L) as
-    ``run_prefill_chunk_step`` packs them, then one token per decoding sequence as
-    ``prepare_decode_inputs`` packs them.  Token-wise ops (embedding, norms, projections, MLP,
-    lm_head) run once over all tokens; attention runs per segment: the chunks' as a chunk step's
-    (history gathered from the pool, causal inside the chunk), the decode tokens' as a paged decode
-    step's (append, then attend over the context), neither reading the other's blocks.  Returns
-    (logits ``[P + D, V]`` of each chunk's last position then each decode token, the chunks'
-    per-layer ``(K, V)`` ``[P, Hkv, L, D]``).
+    ops over one flattened ``[1, C + D]`` batch: the P chunks' tokens back to back (ragged rows, no
+    padding between them), then one token per decoding sequence as ``prepare_decode_inputs`` packs
+    them.  Token-wise ops (embedding, norms, projections, MLP, lm_head) run once over all tokens;
+    attention runs per segment: each chunk's as a chunk step's (history gathered from the pool,
+    causal inside the chunk; the rows are laid out left-padded to the longest chunk L for it, the
+    padding masked), the decode tokens' as a paged decode step's (append, then attend over the
+    context), neither reading the other's blocks.  Returns (logits ``[P + D, V]`` of each chunk's
+    last token then each decode token, the chunks' per-layer ``(K, V)`` ``[P, Hkv, L, D]``,
+    left-padded as ``prefill_chunk_logits`` returns them).
 
-    ``width`` / ``decode_rows`` (at least the longest chunk / the decode tokens) pad L and D: pad
-    decode rows (token ``pad_token_id``, position 0) append nothing, attend to nothing (zero
-    output) and return no logits; every op still runs over all P L + D rows, so each GEMM has the
-    padded M."""
+    ``chunk_tokens`` / ``decode_rows`` (at least the chunks' tokens / the decode tokens) pad C and D:
+    pad chunk tokens (token ``pad_token_id``, position 0) belong to no row; pad decode rows append
+    nothing, attend to nothing (zero output) and return no logits; every op still runs over all
+    C + D rows, so each GEMM has the padded M."""
     c = model.config
     dev = model.device
     scaling = c.head_dim ** -0.5
     rows, live = len(chunk_token_ids), len(last_tokens)
     lens = [len(t) for t in chunk_token_ids]
-    width = max(lens) if width is None else width
+    width, total = max(lens), sum(lens)
+    n = total if chunk_tokens is None else chunk_tokens
     decode_rows = live if decode_rows is None else decode_rows
-    if width < max(lens) or decode_rows < live:
-        raise ValueError(f"width {width} / decode_rows {decode_rows} below the step's {max(lens)} / {live}")
-    n = rows * width
-    ids = torch.full((rows, width), pad_token_id, dtype=torch.long)
-    pos = torch.zeros((rows, width), dtype=torch.long)
-    for r, (toks, start) in enumerate(zip(chunk_token_ids, start_positions)):
-        ids[r, width - len(toks):] = torch.tensor(list(toks), dtype=torch.long)
-        pos[r, width - len(toks):] = torch.arange(start, start + len(toks))
+    if n < total or decode_rows < live:
+        raise ValueError(f"chunk_tokens {n} / decode_rows {decode_rows} below the step's {total} / {live}")
+    first = [sum(lens[:r]) for r in range(rows)]
+    ids = torch.full((n,), pad_token_id, dtype=torch.long)
+    pos = torch.zeros((n,), dtype=torch.long)
+    for toks, start, f in zip(chunk_token_ids, start_positions, first):
+        ids[f:f + len(toks)] = torch.tensor(list(toks), dtype=torch.long)
+        pos[f:f + len(toks)] = torch.arange(start, start + len(toks))
+    # padded layout of the chunk rows: row r, position width - len + t <-> ragged token first[r] + t
+    pad_rows = torch.tensor([r for r, l in enumerate(lens) for _ in range(l)], dtype=torch.long, device=dev)
+    pad_cols = torch.tensor([width - l + t for l in lens for t in range(l)], dtype=torch.long, device=dev)
     hist = [-(-s // block_size) for s in start_positions]
     max_hist = max(hist)
     hist_ids = torch.zeros((rows, max_hist), dtype=torch.long)
@@ -233,14 +238,20 @@ def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, c
         hist_ids[r, :hb] = torch.tensor(list(t[:hb]), dtype=torch.long)
     dec = torch_ref.prepare_decode_rows(decode_tables, last_tokens, positions, block_size).to(dev)
     pad = torch.zeros(decode_rows - live, dtype=torch.long, device=dev)
-    flat_ids = torch.cat((ids.flatten().to(dev), dec[:, 0], pad + pad_token_id)).unsqueeze(0)
-    flat_pos = torch.cat((pos.flatten().to(dev), dec[:, 1], pad)).unsqueeze(0)
+    flat_ids = torch.cat((ids.to(dev), dec[:, 0], pad + pad_token_id)).unsqueeze(0)
+    flat_pos = torch.cat((pos.to(dev), dec[:, 1], pad)).unsqueeze(0)
     # visibility of the chunk rows (history slots < start, causal inside the chunk, no left padding)
     allowed = torch_ref.chunk_allowed_mask(start_positions, lens, max_hist, block_size, width).to(dev)
     chunk_bias = torch.zeros(allowed.shape, dtype=model.dtype, device=dev)
     chunk_bias.masked_fill_(~allowed, torch.finfo(model.dtype).min)
     dec_bias = torch_ref.paged_bias(dec[:, 4:], dec[:, 3], block_size, model.dtype)
     attend = torch_ref.attend_exact if model.exact else torch_ref.attend
+
+    def padded(x):  # [H, total, Dh] ragged -> [P, H, L, Dh] left-padded (zeros in the padding)
+        out = torch.zeros((rows, width, x.shape[0], x.shape[2]), dtype=x.dtype, device=dev)
+        out[pad_rows, pad_cols] = x.transpose(0, 1)
+        return out.transpose(1, 2)
+
     h = F.embedding(flat_ids, model.w["model.embed_tokens.weight"])
     cos, sin = model._rope(flat_pos)
     presents = []
@@ -248,9 +259,7 @@ def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, c
         p = f"model.layers.{layer}."
         x = model._rms(h, model.w[p + "input_layernorm.weight"])
         q, k, v = model._qkv(layer, x, cos, sin)  # [1, H, T, D]
-        qc = q[0, :, :n].reshape(-1, rows, width, c.head_dim).transpose(0, 1)
-        kc = k[0, :, :n].reshape(-1, rows, width, c.head_dim).transpose(0, 1)
-        vc = v[0, :, :n].reshape(-1, rows, width, c.head_dim).transpose(0, 1)
+        qc, kc, vc = padded(q[0, :, :total]), padded(k[0, :, :total]), padded(v[0, :, :total])
         presents.append((kc, vc))
         if max_hist:
             (hk, hv), = torch_ref.gather_blocks([pools[layer]], hist_ids.to(dev))
@@ -261,11 +270,13 @@ def mixed_step_logits(model: ReferenceQwen3, chunk_token_ids, start_positions, c
         vd = v[0, :, n:n + live].transpose(0, 1).unsqueeze(2)
         hk, hv = torch_ref.apply_paged_kv_pool(kd, vd, pools[layer], dec[:, 2], dec[:, 4:])
         dec_out = attend(qd.contiguous(), hk, hv, dec_bias, scaling)  # [D, 1, H D]
-        pad_out = torch.zeros((decode_rows - live, chunk_out.shape[-1]), dtype=chunk_out.dtype, device=dev)
-        attn = torch.cat((chunk_out.reshape(n, -1), dec_out.reshape(live, -1), pad_out)).unsqueeze(0)
+        zeros = torch.zeros((n - total + decode_rows - live, chunk_out.shape[-1]), dtype=chunk_out.dtype, device=dev)
+        attn = torch.cat((chunk_out[pad_rows, pad_cols], zeros[:n - total], dec_out.reshape(live, -1),
+                          zeros[n - total:])).unsqueeze(0)
         h = h + F.linear(attn, model.w[p + "self_attn.o_proj.weight"])
         h = h + model._mlp(layer, model._rms(h, model.w[p + "post_attention_layernorm.weight"]))
-    last = torch.cat((h[0, width - 1:n:width], h[0, n:])).unsqueeze(1)
+    ends = torch.tensor([f + l - 1 for f, l in zip(first, lens)], dtype=torch.long, device=dev)
+    last = torch.cat((h[0].index_select(0, ends), h[0, n:])).unsqueeze(1)
     logits = F.linear(model._rms(last, model.w["model.norm.weight"]), model.w["lm_head.weight"])
     return logits[:rows + live, -1], presents
 
@@ -346,17 +357,17 @@ class ReferenceScheduleBackend:
         tables = [manager.block_table(ch.state.request.request_idx) for ch in chunks]
         starts = [ch.start for ch in chunks]
         lens = [ch.num_tokens for ch in chunks]
-        # With exact numerics a mixed step runs at a padded shape -- the longest chunk rounded up to
+        # With exact numerics a mixed step runs at a padded shape -- the chunks' tokens rounded up to
         # a multiple of 128, the decode rows to a power of two -- which fixes each GEMM's M.
-        width = decode_rows = None
+        chunk_tokens = decode_rows = None
         if self.model.exact:
-            width = -(-max(lens) // 128) * 128
+            chunk_tokens = -(-sum(lens) // 128) * 128
             decode_rows = 1 << (len(states) - 1).bit_length() if states else 0
         logits, presents = mixed_step_logits(
             self.model, [ch.state.request.token_ids[ch.start:ch.end] for ch in chunks], starts, tables,
             [s.generated[-1] for s in states], [s.cache_length for s in states],
             [manager.block_table(s.request.request_idx) for s in states], self.pools, self.block_size,
-            width=width, decode_rows=decode_rows)
+            chunk_tokens=chunk_tokens, decode_rows=decode_rows)
         store_prefill(self.pools, presents, tables, lens, starts, self.block_size)
         logits = logits.float()
         rows = len(chunks)

@@ -155,9 +155,10 @@ def test_mixed_attention_rejects_bad_arguments_on_host(native_lib, exact):
     entry = native_lib.mi_mixed_paged_attention_exact if exact else native_lib.mi_mixed_paged_attention
 
     def call(rows=2, width=64, decode=3, heads=16, kv=8, dim=128, bs=16, nb=4, hstride=4, mb=8, bstride=8,
-             slots=16, tok=2048):
-        return entry(16, 2048, 16, tok, 128, 16, 1024, 128, 16, 1024, 128, 16, 16, 100, rows, width, 16, hstride, nb,
-                     16, 16, 1, decode, 16, bstride, mb, 16, 1, slots, 1, heads, kv, dim, bs, 0.1, None)
+             slots=16, tok=2048, chunk_tokens=0, chunk_first=None):
+        return entry(16, 2048, 16, tok, 128, 16, 1024, 128, 16, 1024, 128, 16, 16, 100, rows, width, chunk_tokens,
+                     chunk_first, 16, hstride, nb, 16, 16, 1, decode, 16, bstride, mb, 16, 1, slots, 1, heads, kv,
+                     dim, bs, 0.1, None)
 
     assert call(dim=64) == _native.MI_ERR_UNSUPPORTED
     assert call(bs=32) == _native.MI_ERR_UNSUPPORTED
@@ -173,6 +174,7 @@ def test_mixed_attention_rejects_bad_arguments_on_host(native_lib, exact):
     else:
         assert call(tok=100) == _native.MI_ERR_UNSUPPORTED  # stride not a multiple of 8 elements
     assert call(rows=0, decode=0) == _native.MI_OK  # nothing to do
+    assert call(chunk_tokens=-1, chunk_first=16) == _native.MI_ERR_INVALID_ARGUMENT  # ragged rows, negative size
 
 
 def test_argmax_rejects_bad_arguments_on_host(native_lib):
@@ -208,7 +210,7 @@ def test_empty_pool_is_rejected_before_any_read_on_host(native_lib):
                    8 * 4 * 128, 4 * 128, 128, 16, 16, 0, 16, 2, 2, 16, 16, 1, 2, 4, 16, 8, 128, 16, 0.1, None)
         assert rc == bad
     for entry in (lib.mi_mixed_paged_attention, lib.mi_mixed_paged_attention_exact):
-        rc = entry(16, 2048, 16, 2048, 128, 16, 1024, 128, 16, 1024, 128, 16, 16, 0, 0, 0, None, 0, 0,
+        rc = entry(16, 2048, 16, 2048, 128, 16, 1024, 128, 16, 1024, 128, 16, 16, 0, 0, 0, 0, None, None, 0, 0,
                    None, None, 1, 3, 16, 8, 8, 16, 1, 16, 1, 16, 8, 128, 16, 0.1, None)
         assert rc == bad
 

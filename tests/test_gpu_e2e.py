@@ -85,7 +85,8 @@ def test_greedy_tokens_identical_on_chunked_slices(untied_head_seed, mixed):
     model, ref = build(untied_head_seed)
     requests = serving_requests(seed=1, num_requests=24, min_prompt=32, max_prompt=700, max_new_tokens=48)
     mrr, budget = 8, 256
-    backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=True, mixed_graphs=mixed)
+    backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=True, mixed_graphs=mixed,
+                                   mixed_graph_tokens=budget)
     product = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
                             stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed)
     chunk_steps = product.num_steps(SchedulePhase.PREFILL) + product.num_steps(SchedulePhase.MIXED)

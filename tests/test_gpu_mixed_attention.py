@@ -187,6 +187,46 @@ def test_mixed_exact_is_bit_identical_to_the_exact_kernels(native_lib, device, s
     assert (out[n:].float() - ref.float()).abs().max().item() <= 4e-3
 
 
+def ragged_of(case, tail=3):
+    """The case with its chunk rows packed back to back (each row's real tokens, no padding) and
+    ``tail`` pad tokens after them, then the decode tokens: (q, k, v, chunk_first, chunk_tokens)."""
+    rows, width = case["rows"], case["width"]
+    n = rows * width
+    keep = [b * width + i for b, l in enumerate(case["lens"].tolist()) for i in range(width - l, width)]
+    first = torch.tensor([0] + list(torch.cumsum(case["lens"], 0)[:-1].tolist()), dtype=torch.long)[:rows]
+    gen = torch.Generator().manual_seed(99)
+    parts = []
+    for name in ("q", "k", "v"):
+        t = case[name]
+        pad = torch.randn((tail,) + tuple(t.shape[1:]), generator=gen).to(t.dtype)
+        parts.append(torch.cat((t[keep], pad, t[n:])))
+    return parts[0], parts[1], parts[2], first, len(keep) + tail, keep
+
+
+@pytest.mark.parametrize("exact", [False, True])
+@pytest.mark.parametrize("starts,lens,width,contexts", [c for c in CASES if c[0]])
+def test_mixed_ragged_rows_give_the_padded_rows_bits(native_lib, device, exact, starts, lens, width, contexts):
+    """Ragged chunk rows (chunk_first / chunk_tokens: each row's real tokens packed back to back, pad
+    tokens after them) give, bit for bit, the outputs of the same rows left-padded to the width, the
+    same decode rows and the same pool appends; no padding position and no pad token is written."""
+    case = make_case(17, starts, lens, width, contexts)
+    want, want_kp, want_vp = run_mixed(case, device, exact=exact)
+    q, k, v, first, chunk_tokens, keep = ragged_of(case)
+    c = {key: (val.to(device) if torch.is_tensor(val) else val) for key, val in case.items()}
+    kp, vp = c["kp"].clone(), c["vp"].clone()
+    sentinel = torch.full((q.shape[0], q.shape[1] * 128), -7.5, dtype=torch.bfloat16, device=device)
+    out = sentinel.clone()
+    data_plane.mixed_paged_attention(q.to(device), k.to(device), v.to(device), kp, vp, c["rows"], c["width"],
+                                     c["hist"], c["starts"], c["lens"], c["dec"], c["ctx"], c["slots"], SCALE,
+                                     out=out, exact=exact, chunk_first=first.to(device), chunk_tokens=chunk_tokens)
+    torch.cuda.synchronize()
+    n, m = case["rows"] * case["width"], len(keep)
+    assert torch.equal(out[:m], want[keep])
+    assert torch.equal(out[m:chunk_tokens], sentinel[m:chunk_tokens])  # pad tokens: nothing written
+    assert torch.equal(out[chunk_tokens:], want[n:])                   # decode rows
+    assert torch.equal(kp, want_kp) and torch.equal(vp, want_vp)
+
+
 def test_mixed_rejects_bad_shapes(native_lib, device):
     case = make_case(3, [0], [10], 10, [5])
     c = {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in case.items()}

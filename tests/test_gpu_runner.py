@@ -348,9 +348,9 @@ def test_chunked_prefill_matches_oracle_runner(models):
 def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
     """One forward over two prompt chunks (one with history, one completing its prompt) and three
     decoding requests: logits and stored K/V bit-identical to the oracle's mixed step (the same
-    flattened batch, padded to width 128 and 4 decode rows as reference numerics run every mixed
-    step), greedy tokens equal to the chunk step and the decode step run apart and to the CPU
-    oracle, logits close to the decode step's."""
+    flattened batch: ragged chunk rows padded to 128 chunk tokens and 4 decode rows, as reference
+    numerics run every mixed step), greedy tokens equal to the chunk step and the decode step run
+    apart and to the CPU oracle, logits close to the decode step's."""
     model, ref, ref_cpu = models
     cfg = model.config
     runner = PagedRunner(model)
@@ -393,13 +393,13 @@ def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
         # mixed (pool 1)
         ids, pos, meta = runner.prepare_mixed_inputs(chunks, starts, pf_tables, first, positions, dec_tables,
                                                      pools[1])
-        assert ids.shape == (1, 2 * 128 + 4)
+        assert ids.shape == (1, 128 + 4)
         # the decode rows' append rewrites the same values when the step runs again
         mixed_logits = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)[0][:5, -1]
         got = runner.run_mixed_step(ids, pos, meta)
         runner.store_prefill(pools[1], got.prefill_cache, pf_tables, lens, starts)
     want_mixed, presents = qwen3_ref.mixed_step_logits(ref, chunks, starts, pf_tables, first, positions, dec_tables,
-                                                       ref_pools, BS, width=128, decode_rows=4)
+                                                       ref_pools, BS, chunk_tokens=128, decode_rows=4)
     qwen3_ref.store_prefill(ref_pools, presents, pf_tables, lens, starts, BS)
     assert torch.equal(mixed_logits, want_mixed)
     want_dec = qwen3_ref.decode_step(ref_cpu, dec_tables, first, positions, cpu_pools, BS)
@@ -528,11 +528,12 @@ def test_exact_models_refuse_prefill_graphs_and_other_mixed_shapes(models):
 
 
 def test_exact_mixed_graph_replays_match_eager_runner_and_oracle(models):
-    """Reference numerics run every mixed step at its padded shape (width to a multiple of 128,
-    decode rows to a power of two), graphed or not: graph replays equal an eager forward of the
-    same inputs, and the logits of both equal the GPU oracle's mixed step at that shape, bit for
-    bit, with eager work and syncs between replays and one bucket replayed twice; steps outside the
-    buckets (three chunk rows, a chunk wider than the buckets) run eagerly at the same padded shape.
+    """Reference numerics run every mixed step at its padded shape (ragged chunk rows, their tokens
+    rounded up to a multiple of 128, decode rows to a power of two), graphed or not: graph replays
+    equal an eager forward of the same inputs, and the logits of both equal the GPU oracle's mixed
+    step at that shape, bit for bit, with eager work and syncs between replays and one bucket
+    replayed twice; steps outside the buckets (three chunk rows, a chunk longer than the graphs
+    serve) run eagerly at the same padded shape.
     Tokens of the graphed and the eager runner are equal and the pools bit-identical to the
     oracle's."""
     model, ref, _ = models
@@ -545,7 +546,8 @@ def test_exact_mixed_graph_replays_match_eager_runner_and_oracle(models):
     graphed, eager_runner = PagedRunner(model), PagedRunner(model)
     graphed.enable_mixed_graphs(pools[0], max_rows=2, max_width=128, max_decode_rows=4, max_history_blocks=8,
                                 max_decode_blocks=8)
-    assert sorted(graphed._mixed_graphs) == [(r, 128, d) for r in (1, 2) for d in (1, 2, 4)]
+    assert sorted(graphed._mixed_graphs) == sorted([(1, 128, d) for d in (1, 2, 4)] +
+                                                   [(2, c, d) for c in (128, 256) for d in (1, 2, 4)])
     n_req = len(decoders) + len(chunked)
     for i, p in enumerate(decoders + chunked):
         manager.allocate_slots(i, len(p))
@@ -570,13 +572,13 @@ def test_exact_mixed_graph_replays_match_eager_runner_and_oracle(models):
             chunk_ids = [chunked[c][a:b] for c, a, b in chunks]
             starts, lens = [a for _, a, _ in chunks], [b - a for _, a, b in chunks]
             pf_tables = [tables[3 + c] for c, _, _ in chunks]
-            width, dec_rows = -(-max(lens) // 128) * 128, 1 << (len(dec) - 1).bit_length()
+            chunk_tokens, dec_rows = -(-sum(lens) // 128) * 128, 1 << (len(dec) - 1).bit_length()
             live = len(chunks) + len(dec)
             results = []
             for pool, runner in zip(pools, (graphed, eager_runner)):
                 ids, pos, meta = runner.prepare_mixed_inputs(chunk_ids, starts, pf_tables, [last[i] for i in dec],
                                                              [positions[i] for i in dec], dec_tables, pool)
-                assert ids.shape == (1, len(chunks) * width + dec_rows)
+                assert ids.shape == (1, chunk_tokens + dec_rows)
                 replayed = runner is graphed and runner._mixed_loaded is not None
                 assert replayed == (graphed_step and runner is graphed)
                 eager, eager_present = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)
@@ -592,7 +594,7 @@ def test_exact_mixed_graph_replays_match_eager_runner_and_oracle(models):
                 results.append((got, eager[:live, -1].clone()))
             want, presents = qwen3_ref.mixed_step_logits(ref, chunk_ids, starts, pf_tables, [last[i] for i in dec],
                                                          [positions[i] for i in dec], dec_tables, ref_pools, BS,
-                                                         width=width, decode_rows=dec_rows)
+                                                         chunk_tokens=chunk_tokens, decode_rows=dec_rows)
             qwen3_ref.store_prefill(ref_pools, presents, pf_tables, lens, starts, BS)
             for got, logits in results:
                 assert torch.equal(logits, want)
@@ -719,7 +721,7 @@ def test_mixed_graph_replays_match_eager_forward(fast_model, models):
     graphed, eager_runner = PagedRunner(model), PagedRunner(model)
     graphed.enable_mixed_graphs(pools[0], max_rows=2, max_width=128, max_decode_rows=4, max_history_blocks=8,
                                 max_decode_blocks=8, decode_row_buckets=[2, 4])
-    assert len(graphed._mixed_graphs) == 2 * 1 * 2
+    assert len(graphed._mixed_graphs) == (1 + 2) * 2  # chunk tokens 128 (one row), 128 / 256 (two); 2 decode buckets
     for i, p in enumerate(decoders + chunked):
         manager.allocate_slots(i, len(p))
     tables = [manager.block_table(i) for i in range(6)]

@@ -129,31 +129,50 @@ def test_prefill_rows_widened_to_a_bucket():
             pack_prefill_rows(chunks, starts, tables, block_size=4, pad_token_id=99, width=w, history_blocks=h)
 
 
-@pytest.mark.parametrize("sizes", [None, (8, 4, 5, 6)])
-def test_mixed_rows_split_into_the_two_packings(sizes):
-    """The mixed buffer is the chunk packing and the decode packing laid out as documented: tokens,
-    positions, chunk metadata, decode metadata (optionally at a bucket's fixed sizes)."""
+@pytest.mark.parametrize("sizes", [None, (9, 4, 5, 6)])
+def test_mixed_rows_ragged_layout(sizes):
+    """The mixed buffer: chunk tokens back to back (then pad tokens up to C), decode tokens, their
+    positions, per chunk row (start, length, first token, history table), and the decode rows of
+    ``pack_decode_rows`` (optionally at a bucket's fixed sizes)."""
     chunks, starts, pf_tables = [[5, 6, 7], [8, 9]], [4, 0], [[3, 9, 2], [1]]
     dec_tables, toks, pos = [[9, 4], [7], [6, 2, 1]], [11, 22, 33], [5, 2, 9]
-    kw = {} if sizes is None else dict(zip(("width", "history_blocks", "decode_rows", "decode_blocks"), sizes))
-    flat, (p, w, nb, d, mb) = pack_mixed_rows(chunks, starts, pf_tables, toks, pos, dec_tables, 4, 0, **kw)
-    pf = pack_prefill_rows(chunks, starts, pf_tables, 4, 0, width=kw.get("width"),
-                           history_blocks=kw.get("history_blocks"))
+    kw = {} if sizes is None else dict(zip(("chunk_tokens", "history_blocks", "decode_rows", "decode_blocks"), sizes))
+    flat, (p, c, nb, d, mb) = pack_mixed_rows(chunks, starts, pf_tables, toks, pos, dec_tables, 4, 99, **kw)
     dc = pack_decode_rows(dec_tables, toks, pos, 4, rows=kw.get("decode_rows"), blocks=kw.get("decode_blocks"))
-    assert p == 2 and w == (3 if sizes is None else 8) and nb == pf.shape[1] - 2 * w - 2
+    assert (p, c, nb) == ((2, 5, 1) if sizes is None else (2, 9, 4))
     assert (d, mb) == (dc.shape[0], dc.shape[1] - 4)
-    t = p * w + d
-    assert flat.shape == (2 * t + p * (2 + nb) + d * (2 + mb),)
-    assert (flat[:p * w] == pf[:, :w].ravel()).all() and (flat[p * w:t] == dc[:, 0]).all()
-    assert (flat[t:t + p * w] == pf[:, w:2 * w].ravel()).all() and (flat[t + p * w:2 * t] == dc[:, 1]).all()
-    at = 2 * t + p * (2 + nb)
-    assert (flat[2 * t:at].reshape(p, 2 + nb) == pf[:, 2 * w:]).all()
-    assert (flat[at:].reshape(d, 2 + mb) == dc[:, 2:]).all()
+    t = c + d
+    assert flat.shape == (2 * t + p * (3 + nb) + d * (2 + mb),)
+    assert flat[:c].tolist() == [5, 6, 7, 8, 9] + [99] * (c - 5)
+    assert (flat[c:t] == dc[:, 0]).all()
+    assert flat[t:t + c].tolist() == [4, 5, 6, 0, 1] + [0] * (c - 5)
+    assert (flat[t + c:2 * t] == dc[:, 1]).all()
+    meta = flat[2 * t:2 * t + p * (3 + nb)].reshape(p, 3 + nb)
+    assert meta[:, :3].tolist() == [[4, 3, 0], [0, 2, 3]]
+    assert meta[0, 3:].tolist() == [3] + [0] * (nb - 1)  # ceil(4 / 4) = 1 history block
+    assert meta[1, 3:].tolist() == [0] * nb
+    assert (flat[2 * t + p * (3 + nb):].reshape(d, 2 + mb) == dc[:, 2:]).all()
+    with pytest.raises(ValueError):
+        pack_mixed_rows(chunks, starts, pf_tables, toks, pos, dec_tables, 4, 99, chunk_tokens=4)
+    with pytest.raises(ValueError):
+        pack_mixed_rows([[5], []], [0, 0], [[1], [2]], toks, pos, dec_tables, 4, 99)
+
+
+def test_ragged_scatter_indices_follow_the_rows_first_tokens():
+    """With row_first, token t of row i is position row_first[i] + t of the one cached row; the
+    slots are the plain index's."""
+    tables, lens, starts = [[3, 9, 2], [1, 5]], [3, 4], [4, 2]
+    plain = prefill_scatter_indices(tables, lens, starts, 6, 4)
+    ragged = prefill_scatter_indices(tables, lens, starts, 99, 4, row_first=[0, 3])
+    assert (ragged[2] == plain[2]).all()
+    assert ragged[0].tolist() == [0] * 7
+    assert ragged[1].tolist() == [0, 1, 2, 3, 4, 5, 6]
+    assert plain[1].tolist() == [3, 4, 5, 2, 3, 4, 5]
 
 
 def test_padded_mixed_shape_known_answers():
-    """Width up to the next multiple of 128 (or the quantum given), decode rows up to the next power
-    of two, no decode rows stays none; nonsense shapes raise."""
+    """Chunk tokens up to the next multiple of 128 (or the quantum given), decode rows up to the next
+    power of two, no decode rows stays none; nonsense shapes raise."""
     cases = {(1, 0): (128, 0), (128, 1): (128, 1), (129, 2): (256, 2), (983, 3): (1024, 4), (1024, 8): (1024, 8),
              (1025, 9): (1152, 16), (39, 13): (128, 16), (2048, 33): (2048, 64)}
     for (width, rows), want in cases.items():

@@ -190,18 +190,20 @@ def test_mixed_step_equals_chunk_step_plus_decode_step(block_size):
     assert mixed_logits.argmax(-1).tolist() == want.argmax(-1).tolist()
     width = 6
     for (mk, mv), (ck, cv) in zip(mixed_presents, chunk_presents):
-        torch.testing.assert_close(mk, ck[:, :, -width:], rtol=1e-5, atol=1e-5)
-        torch.testing.assert_close(mv, cv[:, :, -width:], rtol=1e-5, atol=1e-5)
+        assert mk.shape[2] == width
+        for row, n in enumerate((6, 5)):  # real tokens (the chunk step also caches its pad tokens' K/V)
+            torch.testing.assert_close(mk[row, :, -n:], ck[row, :, -n:], rtol=1e-5, atol=1e-5)
+            torch.testing.assert_close(mv[row, :, -n:], cv[row, :, -n:], rtol=1e-5, atol=1e-5)
     for (ok, ov), (tk, tv) in zip(one, two):
         torch.testing.assert_close(ok, tk, rtol=1e-5, atol=1e-5)
         torch.testing.assert_close(ov, tv, rtol=1e-5, atol=1e-5)
 
 
 def test_padded_mixed_step_equals_the_unpadded_one():
-    """The oracle's mixed step at a padded shape (wider chunk rows, pad decode rows: the shape a
-    mixed step with reference numerics runs at) against the unpadded step on the same state: the
-    same logits for the real rows (within fp32 rounding on the CPU: only the GEMMs' M differs),
-    the chunk K/V right-aligned in the wider rows, pad decode rows writing nothing to the pools."""
+    """The oracle's mixed step at a padded shape (pad chunk tokens after the ragged rows, pad decode
+    rows: the shape a mixed step with reference numerics runs at) against the unpadded step on the
+    same state: the same logits for the real rows (within fp32 rounding on the CPU: only the
+    GEMMs' M differs), the same chunk K/V, pad decode rows writing nothing to the pools."""
     block_size = 4
     model = tiny_model(seed=5)
     gen = torch.Generator().manual_seed(11)
@@ -219,17 +221,18 @@ def test_padded_mixed_step_equals_the_unpadded_one():
     plain_pools = [(k.clone(), v.clone()) for k, v in pools]
     padded_pools = [(k.clone(), v.clone()) for k, v in pools]
     plain, plain_kv = qwen3_ref.mixed_step_logits(model, *args, plain_pools, block_size)
-    padded, padded_kv = qwen3_ref.mixed_step_logits(model, *args, padded_pools, block_size, width=16, decode_rows=4)
+    padded, padded_kv = qwen3_ref.mixed_step_logits(model, *args, padded_pools, block_size, chunk_tokens=16,
+                                                    decode_rows=4)
     assert padded.shape == plain.shape == (3, model.config.vocab_size)
     torch.testing.assert_close(padded, plain, rtol=1e-5, atol=1e-5)
     assert padded.argmax(-1).tolist() == plain.argmax(-1).tolist()
     for (pk, pv), (k, v) in zip(padded_kv, plain_kv):
-        assert pk.shape[2] == 16 and k.shape[2] == 6
-        for row, n in enumerate((6, 5)):  # real tokens only: a pad query's output depends on the width
-            torch.testing.assert_close(pk[row, :, -n:], k[row, :, -n:], rtol=1e-5, atol=1e-5)
-            torch.testing.assert_close(pv[row, :, -n:], v[row, :, -n:], rtol=1e-5, atol=1e-5)
+        assert pk.shape == k.shape and k.shape[2] == 6
+        torch.testing.assert_close(pk, k, rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(pv, v, rtol=1e-5, atol=1e-5)
     for (pk, pv), (k, v) in zip(padded_pools, plain_pools):
         torch.testing.assert_close(pk, k, rtol=1e-5, atol=1e-5)
         torch.testing.assert_close(pv, v, rtol=1e-5, atol=1e-5)
     with pytest.raises(ValueError, match="below the step"):
-        qwen3_ref.mixed_step_logits(model, *args, [(k.clone(), v.clone()) for k, v in pools], block_size, width=4)
+        qwen3_ref.mixed_step_logits(model, *args, [(k.clone(), v.clone()) for k, v in pools], block_size,
+                                    chunk_tokens=10)
