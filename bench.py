@@ -13,7 +13,8 @@ free list reordered by decode-style interleaved growth) and on near-sequential o
 chunked-prefill attention of 4 x 16384-token prompts in 2048-token chunks, and the KV block
 records of 2048 blocks (pack / unpack in HBM, swap to pinned host memory and back); and (under ``e2e``)
 the continuous-batching run of a random-init Qwen3-0.6B: 128 requests at 20 req/s, prompts
-U[32, 1024], 128 output tokens, chunked prefill with a 2048-token budget.  The CPU baseline times the reference's torch
+U[32, 1024], 128 output tokens, chunked prefill with a 2048-token budget (with mixed batching also
+once with at most 1024 prompt tokens per mixed step).  The CPU baseline times the reference's torch
 decode chain (the oracle) on the host cores on a bounded sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only decode]
@@ -34,6 +35,7 @@ import torch
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor datasheet
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix peak
 MFMA_FP64_PEAK_TFLOPS = 78.6    # MI355X dense fp64 matrix peak
+MIXED_CHUNK_CAP = 1024  # prompt tokens per mixed step in the capped mixed-batching run
 PCIE_PEAK_GBS = 64.0  # MI355X host link, PCIe 5.0 x16, one direction
 METRIC = "paged decode-attn HBM GB/s (% peak) at B=256; e2e output tok/s Qwen3-0.6B"
 
@@ -675,7 +677,8 @@ def cpu_baseline_e2e(seed: int = 0, num_requests: int = 8, max_new_tokens: int =
 
 
 
-def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: bool = True) -> dict:
+def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: bool = True,
+              mixed_chunk_tokens: int | None = None) -> dict:
     """Continuous batching with chunked prefill (token budget 2048, block 16, batch slots = number of
     requests) of a random-init Qwen3-0.6B (bf16, N(0, 0.02), tied embeddings): 128 requests, Poisson
     arrivals at 20 req/s, prompts U[32, 1024], 128 greedy tokens each, EOS disabled.  Output tok/s =
@@ -690,7 +693,8 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
     the bandwidth kernels and fused GEMMs, decode graphs per padded (batch, blocks) bucket and
     prefill (and mixed) graphs per padded (rows, width) bucket.  ``mixed``: decode rows ride in
     the prefill steps (the mixed batching the reference plans) instead of the reference's
-    alternating prefill / decode."""
+    alternating prefill / decode; ``mixed_chunk_tokens`` caps the prompt tokens of such a step
+    (prefill-only steps keep the 2048-token budget), which bounds the decoding requests' gaps."""
     from mini_infra_qwen3_amd.core.scheduler import SchedulePhase
     from mini_infra_qwen3_amd.engine import PagedScheduleBackend, run_scheduler
     from mini_infra_qwen3_amd.model import Qwen3ForCausalLM, init_random_, qwen3_0_6b
@@ -703,10 +707,10 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
     def run(requests):
         t0 = time.perf_counter()
         backend = PagedScheduleBackend(model, requests, len(requests), decode_graphs=True, prefill_graphs=not exact,
-                                       mixed_graphs=mixed, mixed_graph_tokens=2048)
+                                       mixed_graphs=mixed, mixed_graph_tokens=mixed_chunk_tokens or 2048)
         setup_s = time.perf_counter() - t0
         return run_scheduler(backend, requests, token_budget=2048, eos_token_id=-1, stop_on_eos=False,
-                             mixed_batching=mixed), setup_s
+                             mixed_batching=mixed, mixed_chunk_tokens=mixed_chunk_tokens), setup_s
 
     run(serving_requests(seed=seed + 1, num_requests=8, max_new_tokens=8))  # warm-up: kernels, GEMM choices
     requests = serving_requests(seed=seed)
@@ -718,6 +722,7 @@ def bench_e2e(device: torch.device, seed: int = 0, mixed: bool = False, exact: b
         "metric": "e2e output tok/s Qwen3-0.6B (continuous batching, chunked prefill 2048, paged KV)",
         "numerics": "reference (exact sums; greedy tokens identical to the oracle)" if exact else "bandwidth kernels",
         "mixed_batching": mixed,
+        "mixed_chunk_tokens": mixed_chunk_tokens,
         "output_tok_s": round(res.throughput_tok_s, 1),
         "wall_tok_s": round(res.wall_tok_s, 1),
         "busy_ms": round(res.busy_ms, 1),
@@ -849,7 +854,7 @@ def main() -> int:
     parser.add_argument("--only", choices=["decode", "decode-groups", "scatter", "scatter-sequential", "scatter-head",
                                            "gather", "gather-sequential", "prefill", "exact-prefill",
                                            "copy", "swap", "e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth",
-                                           "e2e-agreement", "all"],
+                                           "e2e-mixed-capped", "e2e-agreement", "all"],
                         default="all")
     args = parser.parse_args()
     if args.gpus != 1:
@@ -882,8 +887,9 @@ def main() -> int:
         log(f"{args.only}: {json.dumps(res)}")
         print(json.dumps(res), flush=True)
         return 0
-    if args.only in ("e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth"):
-        res = bench_e2e(device, mixed=args.only.startswith("e2e-mixed"), exact=not args.only.endswith("bandwidth"))
+    if args.only in ("e2e", "e2e-mixed", "e2e-bandwidth", "e2e-mixed-bandwidth", "e2e-mixed-capped"):
+        res = bench_e2e(device, mixed=args.only.startswith("e2e-mixed"), exact=not args.only.endswith("bandwidth"),
+                        mixed_chunk_tokens=MIXED_CHUNK_CAP if args.only == "e2e-mixed-capped" else None)
         res.pop("_tokens")
         log(f"e2e: {res['output_tok_s']:.1f} output tok/s (busy), {res['wall_tok_s']:.1f} tok/s (wall)")
         print(json.dumps(res), flush=True)
@@ -955,7 +961,7 @@ def main() -> int:
             f"{sw['unpack']['achieved_GBps']:.1f} GB/s; swap out {sw['swap_out']['achieved_GBps']:.1f} GB/s, "
             f"swap in {sw['swap_in']['achieved_GBps']:.1f} GB/s")
         torch.cuda.empty_cache()
-    e2e = e2e_mixed = e2e_mixed_exact = e2e_bw = None
+    e2e = e2e_mixed = e2e_mixed_exact = e2e_mixed_capped = e2e_bw = None
     if args.only == "all":
         e2e = bench_e2e(device)
         log(f"e2e: {e2e['output_tok_s']:.1f} output tok/s (busy), {e2e['wall_tok_s']:.1f} tok/s (wall)")
@@ -971,10 +977,15 @@ def main() -> int:
             f"of 128 requests token-identical")
         e2e_mixed_exact = bench_e2e(device, mixed=True)
         e2e_mixed_exact["token_agreement"] = token_agreement(e2e["_tokens"], e2e_mixed_exact["_tokens"], device)
-        for r in (e2e, e2e_bw, e2e_mixed, e2e_mixed_exact):
-            r.pop("_tokens")
         log(f"e2e mixed batching (reference numerics): {e2e_mixed_exact['output_tok_s']:.1f} output tok/s (busy), "
             f"ITL max {e2e_mixed_exact['latency_ms']['itl_ms_max']:.2f} ms")
+        e2e_mixed_capped = bench_e2e(device, mixed=True, mixed_chunk_tokens=MIXED_CHUNK_CAP)
+        for r in (e2e, e2e_bw, e2e_mixed, e2e_mixed_exact, e2e_mixed_capped):
+            r.pop("_tokens")
+        log(f"e2e mixed batching (reference numerics, at most {MIXED_CHUNK_CAP} prompt tokens per mixed step): "
+            f"{e2e_mixed_capped['output_tok_s']:.1f} output tok/s (busy), ITL max "
+            f"{e2e_mixed_capped['latency_ms']['itl_ms_max']:.2f} ms, TTFT p95 "
+            f"{e2e_mixed_capped['latency_ms']['ttft_ms_p95']:.2f} ms")
         if not args.no_cpu_baseline:
             e2e["cpu_baseline"] = cpu_baseline_e2e()
             log(f"e2e cpu baseline: {e2e['cpu_baseline']['value']:.2f} output tok/s")
@@ -1009,6 +1020,7 @@ def main() -> int:
         "e2e": e2e,
         "e2e_mixed_batching": e2e_mixed,
         "e2e_mixed_batching_exact": e2e_mixed_exact,
+        "e2e_mixed_batching_exact_chunk_cap": e2e_mixed_capped,
         "e2e_bandwidth_kernels": e2e_bw,
     }
     print(json.dumps(line), flush=True)

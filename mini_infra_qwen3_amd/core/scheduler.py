@@ -17,6 +17,9 @@ src/mini_infra/core/request.py:52-110):
 all requests whose prompt is cached and spends what is left of the token budget (one token per
 decoding request) on prefill chunks, split as above, in one MIXED step; a step with only one kind
 of work is a plain DECODE or PREFILL step.  There is no decode protection: decoding never waits.
+``mixed_chunk_tokens`` caps the prompt tokens of a MIXED step below that remainder (stall-free
+batching as in Sarathi-Serve: a smaller chunk bounds the step's time and so the inter-token gap of
+every decoding request, at the cost of more steps per prompt); PREFILL steps keep the full budget.
 
 Pure CPU logic: no tensors, no device.
 """
@@ -140,18 +143,23 @@ class IterationScheduler:
     """Continuous batching with chunked prefill over a paged KV cache.
 
     ``token_budget``: padded prompt tokens per PREFILL step (hard cap); ``max_running_requests``:
-    batch slots; ``kv_cache_manager``: the block allocator this scheduler allocates and frees with.
+    batch slots; ``kv_cache_manager``: the block allocator this scheduler allocates and frees with;
+    ``mixed_chunk_tokens`` (with ``mixed``): at most this many prompt tokens in a MIXED step.
     """
 
     def __init__(self, token_budget: int, max_running_requests: int, kv_cache_manager: KVCacheManager,
-                 mixed: bool = False):
+                 mixed: bool = False, mixed_chunk_tokens: int | None = None):
         if max_running_requests < 1:
             raise ValueError("max_running_requests must be positive")
         if token_budget < max_running_requests:
             raise ValueError("token_budget must be at least max_running_requests (every running prefill "
                              "advances by at least one token per step)")
+        if mixed_chunk_tokens is not None and (not mixed or mixed_chunk_tokens < max_running_requests):
+            raise ValueError("mixed_chunk_tokens needs mixed batching and at least max_running_requests tokens "
+                             "(every prefill in a mixed step advances by at least one token)")
         self.token_budget = token_budget
         self.mixed = mixed
+        self.mixed_chunk_tokens = mixed_chunk_tokens
         self.max_running_requests = max_running_requests
         self.kv_cache_manager = kv_cache_manager
         self.waiting: deque[RequestState] = deque()
@@ -199,8 +207,12 @@ class IterationScheduler:
     def _decide(self) -> SchedulerOutput | None:
         decoding = self._decoding()
         if self.mixed:
-            # token_budget >= max_running_requests, so every chunk still gets at least one token
-            chunks = self._plan_chunks(self.token_budget - len(decoding))
+            # token_budget >= max_running_requests, so every chunk still gets at least one token;
+            # so does mixed_chunk_tokens (>= max_running_requests), which caps only MIXED steps
+            budget = self.token_budget - len(decoding)
+            if decoding and self.mixed_chunk_tokens is not None:
+                budget = min(budget, self.mixed_chunk_tokens)
+            chunks = self._plan_chunks(budget)
             if chunks and decoding:
                 padded = len(chunks) * max(c.num_tokens for c in chunks)
                 return SchedulerOutput(SchedulePhase.MIXED, decoding + tuple(c.state for c in chunks),

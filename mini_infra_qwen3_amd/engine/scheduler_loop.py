@@ -138,12 +138,13 @@ def run_scheduler(backend, requests: Sequence[Request], token_budget: int = 2048
                   max_running_requests: int | None = None, eos_token_id: int | None = None,
                   stop_on_eos: bool = True,
                   step_clock: Callable[[SchedulerOutput], float] | None = None,
-                  mixed_batching: bool = False) -> ScheduleResult:
+                  mixed_batching: bool = False, mixed_chunk_tokens: int | None = None) -> ScheduleResult:
     """Runs ``requests`` to completion on ``backend`` (``execute_prefill`` / ``execute_decode`` and a
     ``kv_cache_manager``) with continuous batching and chunked prefill under ``token_budget``.
 
     ``max_running_requests`` defaults to the number of requests (reference scheduler_loop.py:162-163).
-    ``mixed_batching`` runs decode rows and prefill chunks in the same step (``execute_mixed``).
+    ``mixed_batching`` runs decode rows and prefill chunks in the same step (``execute_mixed``), with
+    at most ``mixed_chunk_tokens`` prompt tokens in such a step when given.
 
     While the loop runs, the objects that exist when it starts (model, pool, graphs) are frozen out
     of Python's cyclic garbage collector (``gc.freeze``, undone on return): a full collection over
@@ -157,7 +158,8 @@ def run_scheduler(backend, requests: Sequence[Request], token_budget: int = 2048
     states = [RequestState(r) for r in requests]
     arrivals = ArrivalQueue(states)
     clock_ms = min(r.arrival_ms for r in requests)
-    scheduler = IterationScheduler(token_budget, mrr, backend.kv_cache_manager, mixed=mixed_batching)
+    scheduler = IterationScheduler(token_budget, mrr, backend.kv_cache_manager, mixed=mixed_batching,
+                                   mixed_chunk_tokens=mixed_chunk_tokens)
     device = getattr(backend, "device", torch.device("cpu"))
     freeze = gc.isenabled()
     if freeze:

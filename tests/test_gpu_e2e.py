@@ -73,27 +73,33 @@ def test_continuous_batching_run_greedy_tokens_identical_to_the_oracle():
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("untied_head_seed,mixed", [(1234, False), (None, True)],
-                         ids=["context_dependent_model", "mixed_batching"])
-def test_greedy_tokens_identical_on_chunked_slices(untied_head_seed, mixed):
+@pytest.mark.parametrize("untied_head_seed,mixed,chunk_cap", [(1234, False, None), (None, True, None), (None, True, 96)],
+                         ids=["context_dependent_model", "mixed_batching", "mixed_batching_chunk_cap"])
+def test_greedy_tokens_identical_on_chunked_slices(untied_head_seed, mixed, chunk_cap):
     """24 requests with prompts up to 700 tokens and 48 outputs under a 256-token budget, so that
     prompts are chunked over several steps with history.  ``context_dependent_model``: an untied
     N(0, 1) head (output that depends on the whole context, as the reference's diverse test model:
     tests/unit/conftest.py:13-25).  ``mixed_batching``: decode rows and prompt chunks share steps,
     replayed from mixed graphs where a bucket fits (the oracle runs a mixed step as one forward over
-    the same flattened batch, padded to the same shape)."""
+    the same flattened batch, padded to the same shape).  ``mixed_batching_chunk_cap``: at most 96
+    prompt tokens in a mixed step (prefill-only steps keep the budget)."""
     model, ref = build(untied_head_seed)
     requests = serving_requests(seed=1, num_requests=24, min_prompt=32, max_prompt=700, max_new_tokens=48)
     mrr, budget = 8, 256
     backend = PagedScheduleBackend(model, requests, mrr, decode_graphs=True, mixed_graphs=mixed,
-                                   mixed_graph_tokens=budget)
+                                   mixed_graph_tokens=chunk_cap or budget)
     product = run_scheduler(backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
-                            stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed)
+                            stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed,
+                            mixed_chunk_tokens=chunk_cap)
     chunk_steps = product.num_steps(SchedulePhase.PREFILL) + product.num_steps(SchedulePhase.MIXED)
     assert chunk_steps > len(requests)  # prompts were chunked
     assert (product.num_steps(SchedulePhase.MIXED) > 0) == mixed
+    if chunk_cap:
+        assert max(sum(b - a for a, b in e.chunk_spans) for e in product.events
+                   if e.phase is SchedulePhase.MIXED) <= chunk_cap
     oracle_backend = qwen3_ref.ReferenceScheduleBackend(ref, requests, mrr, watch_tokens=product.tokens)
     oracle = run_scheduler(oracle_backend, requests, token_budget=budget, max_running_requests=mrr, eos_token_id=-1,
-                           stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed)
+                           stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed,
+                           mixed_chunk_tokens=chunk_cap)
     diverged = compare(product, oracle, oracle_backend)
     assert not diverged, diverged

@@ -17,8 +17,9 @@ def states_with(prompt_lens, max_new=4):
     return [RequestState(Request(i, tuple(range(1, n + 1)), max_new)) for i, n in enumerate(prompt_lens)]
 
 
-def scheduler(token_budget, capacity, manager=None, mixed=False):
-    return IterationScheduler(token_budget, capacity, manager or KVCacheManager(4, 1000), mixed=mixed)
+def scheduler(token_budget, capacity, manager=None, mixed=False, mixed_chunk_tokens=None):
+    return IterationScheduler(token_budget, capacity, manager or KVCacheManager(4, 1000), mixed=mixed,
+                              mixed_chunk_tokens=mixed_chunk_tokens)
 
 
 def ranges(out):
@@ -252,6 +253,26 @@ def test_mixed_update_takes_decode_tokens_first():
         s.update_from_output(s.schedule(2.0), [1], 2.0)
 
 
+def test_mixed_chunk_cap_bounds_mixed_steps_only():
+    """``mixed_chunk_tokens``: a MIXED step carries at most that many prompt tokens; a PREFILL step
+    (nothing decoding) keeps the whole budget."""
+    s = scheduler(16, 4, mixed=True, mixed_chunk_tokens=4)
+    s.add_requests(states_with([2, 20], max_new=10))
+    first = step(s, 0.0)
+    assert first.phase is PREFILL and ranges(first) == [(0, 0, 2), (1, 0, 8)]
+    for clock, want in ((1.0, (1, 8, 12)), (2.0, (1, 12, 16)), (3.0, (1, 16, 20))):
+        out = step(s, clock)
+        assert out.phase is MIXED and ranges(out) == [want] and out.num_scheduled_tokens == 5
+    assert step(s, 4.0).phase is DECODE
+    uncapped = scheduler(16, 4, mixed=True)
+    uncapped.add_requests(states_with([2, 20], max_new=10))
+    step(uncapped, 0.0)
+    assert ranges(step(uncapped, 1.0)) == [(1, 8, 20)]
+    for kwargs in ({"mixed": False, "mixed_chunk_tokens": 8}, {"mixed": True, "mixed_chunk_tokens": 3}):
+        with pytest.raises(ValueError):
+            scheduler(16, 4, **kwargs)
+
+
 @pytest.mark.parametrize("budget,capacity", [(8, 2), (16, 4), (64, 8)])
 def test_mixed_loop_generates_the_same_tokens(budget, capacity):
     lens, outs = [13, 4, 9, 2, 16, 30, 7], [5, 7, 3, 6, 4, 2, 9]
@@ -281,6 +302,13 @@ def test_mixed_loop_generates_the_same_tokens(budget, capacity):
     assert max(len(e.request_ids) for e in mixed.events) <= capacity
     assert backend.kv_cache_manager.num_used_blocks == 0
     assert sorted(i for e in mixed.events for i in e.finished_request_ids) == list(range(7))
+    # a chunk cap in mixed steps changes the steps, not the tokens
+    capped = run_scheduler(FakeBackend(), requests, token_budget=budget, max_running_requests=capacity,
+                           mixed_batching=True, mixed_chunk_tokens=capacity)
+    assert capped.tokens == plain.tokens
+    mixed_chunks = [sum(b - a for a, b in e.chunk_spans) for e in capped.events if e.phase is MIXED]
+    assert mixed_chunks and max(mixed_chunks) <= capacity
+    assert len(capped.events) >= len(mixed.events)
 
 
 def test_percentile_is_nearest_rank():
