@@ -318,7 +318,9 @@ int32_t mi_chunked_prefill_attention_exact(void* out, int64_t out_row_stride, in
  *     [b L, b L + L) (padding included; padding rows get zero output).  With chunk_first (ragged
  *     rows, device [P]), C = chunk_tokens and row b's chunk_lens[b] real tokens are tokens
  *     chunk_first[b] .. chunk_first[b] + chunk_lens[b] - 1 (first clamped to [0, C - chunk_lens[b]]):
- *     no padding is stored, read or written, so C can be the sum of the lengths;
+ *     no padding is stored or read, so C can be the sum of the lengths, and each token of [0, C)
+ *     that no row covers (a padded step's tail) gets a zero row (a small launch before the
+ *     attention's);
  *   tokens [C, T): D decode rows, one token each, context_lens[b] tokens including it: the
  *     first context_lens[b] - 1 are read from the pool through block_tables[b], the last is the
  *     row's own key / value, which the launch also appends to pool slot slot_mapping[b] (a slot

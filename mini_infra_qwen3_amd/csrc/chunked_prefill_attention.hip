@@ -580,7 +580,44 @@ int32_t launch_rows(const char* name, const PrefillArgs& a0, const PrefillArgs& 
   return check_launch(name);
 }
 
+// One workgroup per token t of [0, row_tokens): every thread checks its share of the rows, and the
+// workgroup writes a zero row unless one of them covers t.
+constexpr int kZeroThreads = 256;
+__global__ __launch_bounds__(kZeroThreads) void zero_uncovered_kernel(uint16_t* out, int64_t out_tok, int32_t row_elems,
+                                                                       const int64_t* first, const int64_t* lens,
+                                                                       int64_t lens_stride, int32_t rows, int32_t width,
+                                                                       int64_t row_tokens, int32_t vec) {
+  const int64_t t = blockIdx.x;
+  int covered = 0;
+  for (int b = threadIdx.x; b < rows; b += kZeroThreads) {
+    int64_t len = lens[b * lens_stride];
+    len = len < 0 ? 0 : (len > width ? width : len);
+    int64_t f = first[b];
+    f = f < 0 ? 0 : (f > row_tokens - len ? row_tokens - len : f);
+    covered |= t >= f && t < f + len;
+  }
+  if (__syncthreads_or(covered)) return;
+  uint16_t* row = out + t * out_tok;
+  if (vec) {
+    for (int i = threadIdx.x; i < row_elems / 8; i += kZeroThreads) reinterpret_cast<uint4*>(row)[i] = uint4{0, 0, 0, 0};
+  } else {
+    for (int i = threadIdx.x; i < row_elems; i += kZeroThreads) row[i] = 0;
+  }
+}
+
 }  // namespace
+
+int32_t zero_uncovered_tokens(const char* what, void* out, int64_t out_tok_stride, int32_t row_elems,
+                              const int64_t* first, const int64_t* lens, int64_t lens_stride, int32_t rows,
+                              int32_t width, int64_t row_tokens, void* stream) {
+  if (row_tokens <= 0) return MI_OK;
+  if (row_tokens > 0x7fffffff) return fail(MI_ERR_UNSUPPORTED, "%s: more than 2^31 - 1 chunk tokens", what);
+  const int32_t vec = aligned16(out) && out_tok_stride % 8 == 0 && row_elems % 8 == 0;
+  zero_uncovered_kernel<<<static_cast<unsigned>(row_tokens), kZeroThreads, 0, as_stream(stream)>>>(
+      static_cast<uint16_t*>(out), out_tok_stride, row_elems, first, lens, lens_stride, rows, width, row_tokens, vec);
+  return check_launch(what);
+}
+
 }  // namespace mi
 
 extern "C" int32_t mi_chunked_prefill_attention(
@@ -658,7 +695,8 @@ extern "C" int32_t mi_mixed_paged_attention(
       num_blocks < 0 || (chunk_first && chunk_tokens < 0))
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", name);
   const bool chunks = prefill_rows > 0 && prefill_width > 0;
-  if (!chunks && decode_rows == 0) return ok();
+  const bool ragged = chunk_first && chunk_tokens > 0;  // writes a zero row for every uncovered token
+  if (!chunks && decode_rows == 0 && !ragged) return ok();
   if (const int32_t rc = reject_empty_pool(name, num_blocks, (chunks && max_history_blocks > 0) ||
                                                                  (decode_rows > 0 && max_blocks > 0)))
     return rc;
@@ -731,6 +769,11 @@ extern "C" int32_t mi_mixed_paged_attention(
     a1.decode_rows = 1;
     a1.slot_mapping = slot_mapping;
     a1.slot_stride = slot_stride;
+  }
+  if (ragged) {
+    rc = zero_uncovered_tokens(name, out, out_tok_stride, num_heads * head_dim, chunk_first, chunk_lens, lens_stride,
+                               chunks ? prefill_rows : 0, prefill_width, chunk_tokens, stream);
+    if (rc != MI_OK) return rc;
   }
   return launch_rows(name, a0, a1, num_kv_heads,
                      std::max(chunks ? max_history_blocks : 0, decode_rows > 0 ? max_blocks : 0), stream);

@@ -1449,7 +1449,8 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
       num_blocks < 0 || (chunk_first && chunk_tokens < 0))
     return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative size", what);
   const bool chunks = prefill_rows > 0 && prefill_width > 0;
-  if (!chunks && decode_rows == 0) return ok();
+  const bool ragged = chunk_first && chunk_tokens > 0;  // writes a zero row for every uncovered token
+  if (!chunks && decode_rows == 0 && !ragged) return ok();
   if (const int32_t rc = reject_empty_pool(what, num_blocks, (chunks && max_history_blocks > 0) ||
                                                                  (decode_rows > 0 && max_blocks > 0)))
     return rc;
@@ -1529,6 +1530,12 @@ extern "C" int32_t mi_mixed_paged_attention_exact(
     a1.slot_mapping = slot_mapping;
     a1.slot_stride = slot_stride;
     exact_rows(a1, decode_rows, 1, num_heads, num_kv_heads, static_cast<int64_t>(max_blocks) * kBlockSize + 1, scale);
+  }
+  if (ragged) {
+    if (const int32_t rc = zero_uncovered_tokens(what, out, out_tok_stride, num_heads * head_dim, chunk_first, chunk_lens,
+                                                 lens_stride, chunks ? prefill_rows : 0, prefill_width, chunk_tokens,
+                                                 stream))
+      return rc;
   }
   const int32_t rc = dispatch_exact_prefill(a0, a1, group, what, as_stream(stream));
   return rc == MI_OK ? ok() : rc;

@@ -17,6 +17,14 @@ int32_t ok();
 // Checks hipGetLastError() after a launch; MI_ERR_DEVICE with the HIP message.
 int32_t check_launch(const char* what);
 
+// Zeroes the out rows of the tokens of [0, row_tokens) that no ragged chunk row of a mixed step
+// covers (row b covers tokens first[b] .. first[b] + len_b - 1, with len_b = lens[b lens_stride]
+// clamped to [0, width] and first[b] to [0, row_tokens - len_b], as the attention kernels clamp
+// them); row_elems bf16 values per token, token stride out_tok_stride.  One launch on `stream`.
+int32_t zero_uncovered_tokens(const char* what, void* out, int64_t out_tok_stride, int32_t row_elems,
+                              const int64_t* first, const int64_t* lens, int64_t lens_stride, int32_t rows,
+                              int32_t width, int64_t row_tokens, void* stream);
+
 // 16-byte vector used by the streaming copies (a native vector type, so the
 // non-temporal builtins accept it).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

@@ -554,9 +554,8 @@ def mixed_paged_attention(
     ``[P]`` as in ``chunked_prefill_attention``, each seen as a left-padded chunk of width L (at least
     every chunk length).  Without ``chunk_first``, C = P L and row b is tokens ``[b L, b L + L)``;
     with ``chunk_first`` ``[P]`` (ragged rows) C = ``chunk_tokens`` and row b's real tokens start at
-    token ``chunk_first[b]``, with no padding stored (the launch writes no row for a token outside
-    the rows; an ``out`` allocated here starts zeroed, so such tokens get zero rows).  The last D
-    tokens are decode rows
+    token ``chunk_first[b]``, with no padding stored (a token that no row covers gets a zero row;
+    at least one row when ``chunk_tokens`` > 0).  The last D tokens are decode rows
     with ``block_tables`` ``[D, mb]``, ``context_lens`` ``[D]`` (tokens including the new one) and
     ``slot_mapping`` ``[D]`` (where the new K/V go; -1: none).  Pools ``[num_blocks, block_size,
     H_kv, D]``, block_size 16 or a multiple.  Returns ``out`` ``[T, H * D]`` bf16.
@@ -586,7 +585,7 @@ def mixed_paged_attention(
         _require_gpu("chunk_first", chunk_first, device)
         _require_index("chunk_first", chunk_first, 1)
         if chunk_tokens is None or rows < 0 or width < 0 or chunk_first.shape[0] != rows or \
-                tokens != int(chunk_tokens) + decode_rows:
+                tokens != int(chunk_tokens) + decode_rows or (rows == 0 and int(chunk_tokens) > 0):
             raise ValueError(f"{tokens} tokens are not {chunk_tokens} ragged chunk tokens of {rows} rows + "
                              f"{decode_rows} decode rows")
         chunk_first = chunk_first.contiguous()
@@ -614,8 +613,7 @@ def mixed_paged_attention(
     lens_stride = start_lens.stride(0) if rows > 1 else 1
     nb, mb = history_blocks.shape[1], block_tables.shape[1]
     if out is None:
-        alloc = torch.zeros if chunk_first is not None else torch.empty
-        out = alloc((tokens, num_heads * head_dim), dtype=torch.bfloat16, device=device)
+        out = torch.empty((tokens, num_heads * head_dim), dtype=torch.bfloat16, device=device)
     elif out.shape != (tokens, num_heads * head_dim) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
         raise ValueError(f"out must be [T, H * D] bf16 with unit inner stride, got {tuple(out.shape)}")
     if tokens == 0:

@@ -187,43 +187,55 @@ def test_mixed_exact_is_bit_identical_to_the_exact_kernels(native_lib, device, s
     assert (out[n:].float() - ref.float()).abs().max().item() <= 4e-3
 
 
-def ragged_of(case, tail=3):
-    """The case with its chunk rows packed back to back (each row's real tokens, no padding) and
-    ``tail`` pad tokens after them, then the decode tokens: (q, k, v, chunk_first, chunk_tokens)."""
+def ragged_of(case, tail=3, gap=0):
+    """The case with its chunk rows packed in order (each row's real tokens, no padding), ``gap`` pad
+    tokens before each row and ``tail`` after the last, then the decode tokens: (q, k, v,
+    chunk_first, chunk_tokens, keep, real) -- ``keep[j]`` is the padded-layout token of ragged
+    token ``real[j]``; every other ragged chunk token is a pad token."""
     rows, width = case["rows"], case["width"]
     n = rows * width
-    keep = [b * width + i for b, l in enumerate(case["lens"].tolist()) for i in range(width - l, width)]
-    first = torch.tensor([0] + list(torch.cumsum(case["lens"], 0)[:-1].tolist()), dtype=torch.long)[:rows]
+    order, first = [], []  # padded-layout token of each ragged chunk token, -1 for a pad token
+    for b, l in enumerate(case["lens"].tolist()):
+        order += [-1] * gap
+        first.append(len(order))
+        order += [b * width + i for i in range(width - l, width)]
+    order += [-1] * tail
+    idx = torch.tensor([i if i >= 0 else n + j for j, i in enumerate(order)], dtype=torch.long)
     gen = torch.Generator().manual_seed(99)
     parts = []
     for name in ("q", "k", "v"):
         t = case[name]
-        pad = torch.randn((tail,) + tuple(t.shape[1:]), generator=gen).to(t.dtype)
-        parts.append(torch.cat((t[keep], pad, t[n:])))
-    return parts[0], parts[1], parts[2], first, len(keep) + tail, keep
+        pads = torch.randn((len(order),) + tuple(t.shape[1:]), generator=gen).to(t.dtype)
+        parts.append(torch.cat((torch.cat((t[:n], pads))[idx], t[n:])))
+    real = [j for j, i in enumerate(order) if i >= 0]
+    keep = [i for i in order if i >= 0]
+    return parts[0], parts[1], parts[2], torch.tensor(first, dtype=torch.long), len(order), keep, real
 
 
 @pytest.mark.parametrize("exact", [False, True])
 @pytest.mark.parametrize("starts,lens,width,contexts", [c for c in CASES if c[0]])
-def test_mixed_ragged_rows_give_the_padded_rows_bits(native_lib, device, exact, starts, lens, width, contexts):
-    """Ragged chunk rows (chunk_first / chunk_tokens: each row's real tokens packed back to back, pad
-    tokens after them) give, bit for bit, the outputs of the same rows left-padded to the width, the
-    same decode rows and the same pool appends; no padding position and no pad token is written."""
+@pytest.mark.parametrize("tail,gap", [(3, 0), (0, 0), (5, 2)])
+def test_mixed_ragged_rows_give_the_padded_rows_bits(native_lib, device, exact, starts, lens, width, contexts, tail,
+                                                      gap):
+    """Ragged chunk rows (chunk_first / chunk_tokens: each row's real tokens packed in order, pad
+    tokens before the rows and after them) give, bit for bit, the outputs of the same rows
+    left-padded to the width, the same decode rows and the same pool appends; every pad token gets
+    a zero row (over a sentinel-filled ``out``)."""
     case = make_case(17, starts, lens, width, contexts)
     want, want_kp, want_vp = run_mixed(case, device, exact=exact)
-    q, k, v, first, chunk_tokens, keep = ragged_of(case)
+    q, k, v, first, chunk_tokens, keep, real = ragged_of(case, tail, gap)
     c = {key: (val.to(device) if torch.is_tensor(val) else val) for key, val in case.items()}
     kp, vp = c["kp"].clone(), c["vp"].clone()
-    sentinel = torch.full((q.shape[0], q.shape[1] * 128), -7.5, dtype=torch.bfloat16, device=device)
-    out = sentinel.clone()
+    out = torch.full((q.shape[0], q.shape[1] * 128), -7.5, dtype=torch.bfloat16, device=device)
     data_plane.mixed_paged_attention(q.to(device), k.to(device), v.to(device), kp, vp, c["rows"], c["width"],
                                      c["hist"], c["starts"], c["lens"], c["dec"], c["ctx"], c["slots"], SCALE,
                                      out=out, exact=exact, chunk_first=first.to(device), chunk_tokens=chunk_tokens)
     torch.cuda.synchronize()
-    n, m = case["rows"] * case["width"], len(keep)
-    assert torch.equal(out[:m], want[keep])
-    assert torch.equal(out[m:chunk_tokens], sentinel[m:chunk_tokens])  # pad tokens: nothing written
-    assert torch.equal(out[chunk_tokens:], want[n:])                   # decode rows
+    n = case["rows"] * case["width"]
+    pad = sorted(set(range(chunk_tokens)) - set(real))
+    assert torch.equal(out[real], want[keep])
+    assert len(pad) == tail + gap * case["rows"] and not out[pad].any()  # pad tokens: zero rows
+    assert torch.equal(out[chunk_tokens:], want[n:])                       # decode rows
     assert torch.equal(kp, want_kp) and torch.equal(vp, want_vp)
 
 
@@ -236,3 +248,7 @@ def test_mixed_rejects_bad_shapes(native_lib, device):
     with pytest.raises(ValueError):  # one slot per decode row
         data_plane.mixed_paged_attention(c["q"], c["k"], c["v"], c["kp"], c["vp"], 1, 10, c["hist"], c["starts"],
                                          c["lens"], c["dec"], c["ctx"], c["slots"][:0], SCALE)
+    with pytest.raises(ValueError):  # ragged chunk tokens but no chunk row
+        data_plane.mixed_paged_attention(c["q"], c["k"], c["v"], c["kp"], c["vp"], 0, 10, c["hist"][:0],
+                                         c["starts"][:0], c["lens"][:0], c["dec"], c["ctx"], c["slots"], SCALE,
+                                         chunk_first=c["starts"][:0], chunk_tokens=10)
