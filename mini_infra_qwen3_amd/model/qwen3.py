@@ -92,7 +92,9 @@ class PagedMixedMetadata(NamedTuple):
     rows), and the attention sees each row left-padded to ``prefill_width`` (at least every chunk
     length).  Without it, C = P L with L = ``prefill_width``: row b is tokens ``[b L, b L + L)``,
     left-padded.  ``prefill.kv_out`` (optional) holds per-layer ``[T, H_kv, D]`` buffers for all T
-    tokens' K/V."""
+    tokens' K/V.  Host-side facts of the step for its caller (the forward ignores them):
+    ``live_decode_rows``, how many of the D decode rows are real (the rest pad; None: all), and
+    ``chunk_first_host``, ``chunk_first`` as host integers."""
 
     prefill: PagedPrefillMetadata
     decode: PagedAttentionMetadata
@@ -101,6 +103,8 @@ class PagedMixedMetadata(NamedTuple):
     kv_pools: tuple[PastKeyValue, ...] = ()
     chunk_first: torch.Tensor | None = None
     chunk_tokens: int = 0
+    live_decode_rows: int | None = None
+    chunk_first_host: tuple[int, ...] | None = None
 
     @property
     def chunk_span(self) -> int:

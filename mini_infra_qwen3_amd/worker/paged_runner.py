@@ -237,8 +237,6 @@ class PagedRunner(BaseModelRunner):
         self._mixed_graphs: dict[tuple[int, int, int], _MixedGraph] = {}
         self._mixed_pool: PagedKVCachePool | None = None
         self._mixed_loaded: tuple[_MixedGraph, int] | None = None
-        self._mixed_eager: tuple[int, int] | None = None  # (slot buffer address, live decode rows)
-        self._mixed_first: list[int] = []  # first token of each chunk row of the last prepared mixed step
         self._mixed_width = 0
         self._decode_row_buckets: list[int] = []
         self._staging: torch.Tensor | None = None
@@ -555,16 +553,18 @@ class PagedRunner(BaseModelRunner):
     ) -> tuple[torch.Tensor, torch.Tensor, PagedMixedMetadata]:
         """Packs a mixed step -- chunk rows as ``run_prefill_chunk_step`` takes them, decode rows as
         ``prepare_decode_inputs`` does -- into one int64 buffer with one upload.  Returns input_ids /
-        position_ids ``[1, P L + D]`` and the metadata, all views of that buffer.  With reference
-        numerics L and D are ``padded_mixed_shape`` of the longest chunk and the decode rows (pad rows
-        append nothing and attend to nothing), whether a graph replays the step or not; otherwise L
-        is the longest chunk and D the decode rows, unless a graph bucket pads them."""
+        position_ids ``[1, C + D]`` and the metadata, all views of that buffer: the chunks' C tokens
+        back to back (ragged rows, row b from token ``chunk_first[b]``), then the D decode tokens.
+        With reference numerics (C, D) is ``padded_mixed_shape`` of the chunk tokens and the decode
+        rows (pad tokens belong to no row, pad decode rows append nothing and attend to nothing),
+        whether a graph replays the step or not; otherwise C is the chunk tokens and D the decode
+        rows, unless a graph bucket pads them.  The metadata carries the live decode rows and the
+        rows' first tokens on the host."""
         self._mixed_loaded = None
-        self._mixed_eager = None
         live = len(decode_block_tables)
         lens = [len(c) for c in chunk_token_ids]
         width, total = max(lens), sum(lens)
-        self._mixed_first = [int(x) for x in np.cumsum([0] + lens[:-1])]
+        host = {"live_decode_rows": live, "chunk_first_host": tuple(int(x) for x in np.cumsum([0] + lens[:-1]))}
         exact = getattr(self.model, "exact", False)
         pad_chunk, pad_rows = padded_mixed_shape(total, live) if exact else (None, None)
         if self._mixed_graphs and pool is self._mixed_pool:
@@ -581,7 +581,7 @@ class PagedRunner(BaseModelRunner):
                 graph.load(flat)
                 self._mixed_loaded = (graph, live)
                 ids, pos, meta = graph.views()
-                return ids, pos, meta._replace(kv_pools=tuple(pool.kv_pools))
+                return ids, pos, meta._replace(kv_pools=tuple(pool.kv_pools), **host)
         flat, (rows, chunk_tokens, nb, decode_rows, mb) = pack_mixed_rows(
             chunk_token_ids, start_positions, prefill_block_tables, last_tokens, positions, decode_block_tables,
             pool.block_size, self.pad_token_id, chunk_tokens=pad_chunk, decode_rows=pad_rows)
@@ -591,7 +591,6 @@ class PagedRunner(BaseModelRunner):
         chunk = packed[at:at + rows * (3 + nb)].view(rows, 3 + nb)
         at += rows * (3 + nb)
         dec = packed[at:].view(decode_rows, 2 + mb)
-        self._mixed_eager = (dec.data_ptr(), live)
         pools = tuple(pool.kv_pools)
         metadata = PagedMixedMetadata(
             prefill=PagedPrefillMetadata(history_block_tables=chunk[:, 3:], start_lens=chunk[:, 0],
@@ -599,14 +598,15 @@ class PagedRunner(BaseModelRunner):
             decode=PagedAttentionMetadata(slot_mapping=dec[:, 0], block_tables=dec[:, 2:], context_lens=dec[:, 1],
                                           kv_pools=pools),
             prefill_rows=rows, prefill_width=width, kv_pools=pools, chunk_first=chunk[:, 2],
-            chunk_tokens=chunk_tokens)
+            chunk_tokens=chunk_tokens, **host)
         return packed[:tokens].view(1, tokens), packed[tokens:2 * tokens].view(1, tokens), metadata
 
     def run_mixed_step(self, input_ids: torch.Tensor, position_ids: torch.Tensor,
                        metadata: PagedMixedMetadata) -> MixedStepOutput:
         """One forward over the chunks and the decode tokens: the decode rows' K/V go into the pool,
-        the chunks' K/V come back as ``prefill_cache``; greedy tokens of both.  Inputs that
-        ``prepare_mixed_inputs`` loaded into a captured bucket replay its graph."""
+        the chunks' K/V come back as ``prefill_cache``; greedy tokens of both (of the live decode
+        rows only, ``metadata.live_decode_rows``).  Inputs that ``prepare_mixed_inputs`` loaded
+        into a captured bucket replay its graph."""
         loaded = self._mixed_loaded
         if loaded is not None and metadata.decode.slot_mapping.data_ptr() == loaded[0].static_slots_ptr:
             graph, live = loaded
@@ -615,25 +615,28 @@ class PagedRunner(BaseModelRunner):
                 next_token = argmax_rows(graph.logits)
             tokens = next_token.tolist()
             return MixedStepOutput(tokens[:graph.rows], tokens[graph.rows:graph.rows + live],
-                                   self._ragged_cache(graph.presents), timer.elapsed_ms)
+                                   self._ragged_cache(graph.presents, metadata), timer.elapsed_ms)
         with StepTimer(self.device) as timer:
             logits, present = self.model(input_ids, position_ids=position_ids, attn_metadata=metadata,
                                          last_logits_only=True)
             next_token, _ = greedy_sample(logits)
         tokens = next_token.squeeze(-1).tolist()
         rows = metadata.prefill_rows
-        live = len(tokens) - rows
-        eager = self._mixed_eager
-        if eager is not None and metadata.decode.slot_mapping.data_ptr() == eager[0]:
-            live = eager[1]  # inputs from prepare_mixed_inputs, padded to the step's shape
-        cache = self._ragged_cache(present) if metadata.chunk_first is not None else KVCache(present)
+        live = len(tokens) - rows if metadata.live_decode_rows is None else metadata.live_decode_rows
+        cache = self._ragged_cache(present, metadata) if metadata.chunk_first is not None else KVCache(present)
         return MixedStepOutput(tokens[:rows], tokens[rows:rows + live], cache, timer.elapsed_ms)
 
-    def _ragged_cache(self, present) -> KVCache:
+    @staticmethod
+    def _ragged_cache(present, metadata: PagedMixedMetadata) -> KVCache:
         """The chunk K/V of a ragged mixed step (one cached row of all chunk tokens), with the first
-        token of each chunk row for ``store_prefill``."""
+        token of each chunk row for ``store_prefill``: the metadata's host copy, else its device
+        rows clamped as the attention kernels clamp them (to [0, C - len])."""
         cache = KVCache(present)
-        cache.ragged_first = self._mixed_first
+        first = metadata.chunk_first_host
+        if first is None:
+            lens = metadata.prefill.chunk_lens.clamp(0, metadata.prefill_width)
+            first = tuple(torch.minimum(metadata.chunk_first.clamp(min=0), metadata.chunk_span - lens).tolist())
+        cache.ragged_first = list(first)
         return cache
 
 

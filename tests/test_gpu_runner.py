@@ -394,9 +394,17 @@ def test_mixed_step_matches_separate_chunk_and_decode_steps(models):
         ids, pos, meta = runner.prepare_mixed_inputs(chunks, starts, pf_tables, first, positions, dec_tables,
                                                      pools[1])
         assert ids.shape == (1, 128 + 4)
+        assert meta.live_decode_rows == 3 and meta.chunk_first_host == (0, lens[0])
         # the decode rows' append rewrites the same values when the step runs again
         mixed_logits = model(ids, position_ids=pos, attn_metadata=meta, last_logits_only=True)[0][:5, -1]
+        # another step prepared before this one runs leaves this one's rows and live decode rows alone
+        runner.prepare_mixed_inputs(chunks[::-1], starts[::-1], pf_tables[::-1], first[:2], positions[:2],
+                                    dec_tables[:2], pools[1])
         got = runner.run_mixed_step(ids, pos, meta)
+        assert got.prefill_cache.ragged_first == [0, lens[0]] and len(got.decode_next_tokens) == 3
+        # metadata without the host copy: the same first tokens from its device rows
+        assert PagedRunner._ragged_cache(got.prefill_cache.past_key_values,
+                                         meta._replace(chunk_first_host=None)).ragged_first == [0, lens[0]]
         runner.store_prefill(pools[1], got.prefill_cache, pf_tables, lens, starts)
     want_mixed, presents = qwen3_ref.mixed_step_logits(ref, chunks, starts, pf_tables, first, positions, dec_tables,
                                                        ref_pools, BS, chunk_tokens=128, decode_rows=4)
