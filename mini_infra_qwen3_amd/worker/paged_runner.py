@@ -21,6 +21,10 @@ Same entry points, arguments and return types as the reference's PagedRunner
   (``padded_mixed_shape``), so mixed graphs serve it as well;
 * ``prepare_mixed_inputs`` / ``run_mixed_step`` run prefill chunks and decode tokens in one forward
   (the mixed batching the reference plans next: src/mini_infra/core/scheduler.py:310-311).
+
+A graph bucket's static buffers hold one prepared step, so with graphs each ``prepare_*`` call is
+followed by its ``run_*`` call before the next ``prepare_*`` of the same kind (as the reference's
+loop calls them); eager steps carry everything in the tensors and metadata they return.
 """
 
 from __future__ import annotations
