@@ -318,8 +318,7 @@ class PagedRunner(BaseModelRunner):
         """Captures the mixed-step forward for 1..``max_rows`` chunk rows of at most ``max_width``
         tokens each, chunk tokens (ragged rows, back to back) in multiples of ``width_quantum`` up to
         the rows times ``max_width`` (capped at ``max_chunk_tokens``) rounded up, and decode-row
-        buckets up to
-        ``max_decode_rows`` (pad rows append nothing), with history / decode tables
+        buckets up to ``max_decode_rows`` (pad rows append nothing), with history / decode tables
         ``max_history_blocks`` / ``max_decode_blocks`` wide, over ``pool``.  Other steps run without a
         graph; as with prefill graphs, store a step's ``prefill_cache`` before the next graphed step.
         A model with reference numerics runs every mixed step at ``padded_mixed_shape`` (graphed or
