@@ -239,6 +239,36 @@ def test_mixed_ragged_rows_give_the_padded_rows_bits(native_lib, device, exact, 
     assert torch.equal(kp, want_kp) and torch.equal(vp, want_vp)
 
 
+@pytest.mark.parametrize("exact", [False, True])
+def test_ragged_tokens_without_chunk_rows_get_zero_rows_through_the_c_abi(native_lib, device, exact):
+    """Ragged chunk tokens with no chunk row (``chunk_first`` set, P = 0, C = 5): the entry point
+    writes zero rows for all C tokens and serves the decode rows after them with the bits (and pool
+    appends) of the same rows without chunk tokens.  Called through the C ABI: the Python wrapper
+    refuses this form."""
+    case = make_case(5, [], [], 0, [9, 100, 16, 0])
+    want, want_kp, want_vp = run_mixed(case, device, exact=exact)
+    chunk_tokens = 5
+    gen = torch.Generator().manual_seed(3)
+    c = {key: (val.to(device) if torch.is_tensor(val) else val) for key, val in case.items()}
+    q, k, v = (torch.cat((torch.randn((chunk_tokens,) + tuple(c[n].shape[1:]), generator=gen).to(torch.bfloat16)
+                          .to(device), c[n])) for n in ("q", "k", "v"))
+    kp, vp = c["kp"].clone(), c["vp"].clone()
+    out = torch.full((q.shape[0], q.shape[1] * 128), -7.5, dtype=torch.bfloat16, device=device)
+    first = torch.zeros(1, dtype=torch.long, device=device)  # never read: no chunk row
+    entry = native_lib.mi_mixed_paged_attention_exact if exact else native_lib.mi_mixed_paged_attention
+    rc = entry(out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0),
+               k.stride(1), v.data_ptr(), v.stride(0), v.stride(1), kp.data_ptr(), vp.data_ptr(), kp.shape[0],
+               0, 0, chunk_tokens, first.data_ptr(), None, 0, 0, None, None, 1,
+               c["ctx"].shape[0], c["dec"].data_ptr(), c["dec"].stride(0), c["dec"].shape[1], c["ctx"].data_ptr(), 1,
+               c["slots"].data_ptr(), 1, q.shape[1], k.shape[1], 128, 16, SCALE,
+               torch.cuda.current_stream(device).cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, native_lib.mi_last_error()
+    assert not out[:chunk_tokens].any()
+    assert torch.equal(out[chunk_tokens:], want)
+    assert torch.equal(kp, want_kp) and torch.equal(vp, want_vp)
+
+
 def test_mixed_rejects_bad_shapes(native_lib, device):
     case = make_case(3, [0], [10], 10, [5])
     c = {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in case.items()}
