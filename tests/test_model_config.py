@@ -45,3 +45,25 @@ def test_config_rejects_indivisible_heads():
     with pytest.raises(ValueError):
         Qwen3Config(vocab_size=10, hidden_size=16, intermediate_size=16, num_hidden_layers=1,
                     num_attention_heads=3, num_key_value_heads=2, head_dim=8).validate()
+
+
+def test_set_exact_switches_every_layer_and_fused_weights_follow_the_linears():
+    """``set_exact`` flips both numerics flags of every layer; the bandwidth form's concatenated
+    q/k/v weight is cached and rebuilt when a projection's weight changes in place."""
+    from mini_infra_qwen3_amd.model.qwen3 import _concat_weight
+
+    model = Qwen3ForCausalLM(tiny())
+    assert model.exact
+    assert model.set_exact(False) is model and not model.exact
+    assert all(not layer.self_attn.exact and not layer.mlp.exact for layer in model.model.layers)
+    attn = model.model.layers[0].self_attn
+    linears = (attn.q_proj, attn.k_proj, attn.v_proj)
+    fused = _concat_weight(attn, linears)
+    assert _concat_weight(attn, linears) is fused
+    assert torch.equal(fused, torch.cat([l.weight for l in linears]))
+    with torch.no_grad():
+        attn.k_proj.weight.add_(1.0)
+    rebuilt = _concat_weight(attn, linears)
+    nq = attn.q_proj.out_features
+    assert rebuilt is not fused and torch.equal(rebuilt[nq:nq + attn.k_proj.out_features], attn.k_proj.weight)
+    assert model.set_exact(True).exact
