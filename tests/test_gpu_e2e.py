@@ -54,19 +54,29 @@ def compare(product, oracle, backend):
 
 
 @pytest.mark.timeout(900)
-def test_continuous_batching_run_greedy_tokens_identical_to_the_oracle():
+@pytest.mark.parametrize("mixed,chunk_cap", [(False, None), (True, None), (True, 1024)],
+                         ids=["alternating", "mixed_batching", "mixed_batching_chunk_cap"])
+def test_continuous_batching_run_greedy_tokens_identical_to_the_oracle(mixed, chunk_cap):
     """The full workload: 128 requests, Poisson arrivals at 20 req/s, prompts U[32, 1024], 128 greedy
-    tokens each, token budget 2048, 128 batch slots; decode steps replay HIP graphs."""
+    tokens each, token budget 2048, 128 batch slots; decode steps replay HIP graphs.  The mixed runs
+    (the bench's reference-numerics mixed legs) replay mixed graphs at the padded step shapes, the
+    last with at most 1024 prompt tokens per mixed step."""
     model, ref = build()
     requests = serving_requests(seed=0)
     assert len(requests) == 128 and all(r.max_new_tokens == 128 for r in requests)
-    backend = PagedScheduleBackend(model, requests, 128, decode_graphs=True)
+    backend = PagedScheduleBackend(model, requests, 128, decode_graphs=True, mixed_graphs=mixed,
+                                   mixed_graph_tokens=chunk_cap or 2048)
     product = run_scheduler(backend, requests, token_budget=2048, max_running_requests=128, eos_token_id=-1,
-                            stop_on_eos=False, step_clock=step_clock)
-    assert product.num_steps(SchedulePhase.PREFILL) > 100 and product.num_steps(SchedulePhase.DECODE) > 1000
+                            stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed,
+                            mixed_chunk_tokens=chunk_cap)
+    if mixed:
+        assert product.num_steps(SchedulePhase.MIXED) > 100 and product.num_steps(SchedulePhase.DECODE) > 1000
+    else:
+        assert product.num_steps(SchedulePhase.PREFILL) > 100 and product.num_steps(SchedulePhase.DECODE) > 1000
     oracle_backend = qwen3_ref.ReferenceScheduleBackend(ref, requests, 128, watch_tokens=product.tokens)
     oracle = run_scheduler(oracle_backend, requests, token_budget=2048, max_running_requests=128, eos_token_id=-1,
-                           stop_on_eos=False, step_clock=step_clock)
+                           stop_on_eos=False, step_clock=step_clock, mixed_batching=mixed,
+                           mixed_chunk_tokens=chunk_cap)
     assert len(oracle_backend.records) == 128 * 128
     diverged = compare(product, oracle, oracle_backend)
     assert not diverged, diverged
