@@ -40,8 +40,6 @@ from pathlib import Path
 
 import torch
 
-from mini_infra_qwen3_amd import data_plane
-
 RECORD_MAGIC = b"MIKVBLK1"
 FORMAT_VERSION = 1
 _HEADER = struct.Struct("<8sIIIIIIIIQQII")

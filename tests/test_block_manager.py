@@ -178,8 +178,6 @@ def test_device_block_tables_follow_the_allocator_by_deltas():
     each sync, uploading only the entries written since the previous one."""
     import random
 
-    import torch
-
     from mini_infra_qwen3_amd.worker.block_tables import DeviceBlockTables
 
     rng = random.Random(5)
