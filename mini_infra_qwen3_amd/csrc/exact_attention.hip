@@ -787,8 +787,9 @@ __global__ __launch_bounds__(kHeadDim) void exact_split_merge_kernel(const Exact
 // then the probabilities and P V.  Rows too long for the cache recompute S in each pass.
 //
 // Measured on one MI355X (G = 2, 8 KV heads; TFLOP/s of QK + PV as 4 x 128 flops per visible
-// (query head, key) pair; fp64 MFMA alone peaks near 46 TFLOP/s in a loop of independent
-// accumulators): one 2048-token row 471-476 us (36.1-36.5 TFLOP/s), two 1024-token rows 235-236 us,
+// (query head, key) pair; v_mfma_f64_16x16x4f64 alone peaks near 46 TFLOP/s in a loop of
+// independent accumulators, v_mfma_f64_4x4x4f64 near 72, but forms on the latter ran no faster:
+// the fp64 exponentials, divisions and operand conversions bound this kernel): one 2048-token row 471-476 us (36.1-36.5 TFLOP/s), two 1024-token rows 235-236 us,
 // four rows of ~512 tokens 168 us, 1000 history + 1024 chunk tokens 374-378 us, with the queries
 // read by 16-byte loads (2-byte loads: 484 / 249 / 184 / 387 us).  The fp64 FMA form this replaces
 // (one lane per key, query rows broadcast from LDS, one wavefront per SIMD) took 3106 / 934 / 499 /
